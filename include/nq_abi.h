@@ -1,0 +1,204 @@
+/*
+ * nq_abi.h -- C ABI of the MI355X-native serving hot path for Qwen3-TTS.
+ *
+ * Every entry point:
+ *   - takes device pointers, element strides and sizes, plus a hipStream_t
+ *     passed as `void *` (0 = the null stream);
+ *   - never allocates, never synchronises, and is safe to record into a
+ *     hipGraph (no memset/memcpy nodes are issued);
+ *   - returns 0 on success or a negative NQ_ERR_* code; nq_status_string()
+ *     names it.  Argument errors are detected on the host before any launch.
+ *
+ * Tensor layouts use element strides (not bytes).  "bf16" buffers hold
+ * bfloat16 bit patterns (uint16_t).  Reference citations name the file and
+ * line of nari-labs/nari-qwen3-tts (src/nari_qwen3_tts/...) whose behaviour
+ * the entry point replaces.
+ */
+#ifndef NQ_ABI_H
+#define NQ_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NQ_ABI_VERSION 1
+
+enum nq_status {
+    NQ_OK = 0,
+    NQ_ERR_INVALID_ARGUMENT = -1, /* shape / contract violation -> ValueError */
+    NQ_ERR_UNSUPPORTED = -2,      /* dtype / size outside the kernels' range -> TypeError */
+    NQ_ERR_LAUNCH = -3,           /* HIP launch or runtime failure -> RuntimeError */
+    NQ_ERR_CAPACITY = -4          /* too few free KV pages -> KVAllocationError */
+};
+
+/* dtype codes for logits and activations */
+enum nq_dtype { NQ_F32 = 0, NQ_BF16 = 1 };
+
+int nq_abi_version(void);
+const char *nq_status_string(int status);
+
+/*
+ * Ragged KV metadata on the GPU.
+ * Replaces PagedTalkerKV._metadata (executor/talker_kv.py:403-483) together
+ * with the page choice of PagedKVAllocator.reserve (executor/cache.py:135-184):
+ * new pages are the lowest free pages, taken in row order.
+ *
+ * Real rows r < n_rows: prior sequence length seq_len[r], position_start
+ * pos_start[r], advance[r] >= 1 new tokens, prior_pages[r] pages already listed
+ * in page_table[table_row[r] * table_stride + 0 .. prior_pages[r]).  New pages
+ * are read from free_pages[0 ..) (sorted ascending) and appended to the same
+ * page_table row.  Rows n_rows .. capture_rows-1 are padding rows that use
+ * scratch_pages[row].  Outputs (device):
+ *   qo_indptr[capture_rows+1] (only when prefill != 0; may be NULL otherwise),
+ *   kv_indptr[capture_rows+1], kv_indices[kv_indices_capacity],
+ *   last_page_len[capture_rows], position_ids / write_pages / write_offsets
+ *   [token_capacity] (int64).
+ * status[0] receives NQ_OK or NQ_ERR_CAPACITY, status[1] the number of free
+ * pages consumed.  grid_blocks = 0 picks a default launch width.
+ */
+int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start, const int32_t *advance,
+                   const int32_t *prior_pages, const int32_t *table_row, int n_rows,
+                   int capture_rows, int token_capacity, int page_size, int prefill,
+                   int32_t *page_table, int64_t table_stride, const int32_t *free_pages,
+                   int n_free, const int32_t *scratch_pages, int n_scratch,
+                   int32_t *qo_indptr, int32_t *kv_indptr, int32_t *kv_indices,
+                   int64_t kv_indices_capacity, int32_t *last_page_len, int64_t *position_ids,
+                   int64_t *write_pages, int64_t *write_offsets, int32_t *status,
+                   int grid_blocks, void *stream);
+
+/*
+ * Work decomposition for nq_paged_attention, computed on the GPU from the
+ * ragged metadata.  Replaces the host-side plan() of the FlashInfer wrappers
+ * (executor/talker_kv.py:175-223 prefill, :259-303 decode).
+ * qo_indptr may be NULL (pure decode: row r owns query r).  Each query token
+ * gets its causal key range (bottom-right aligned: query i of a row with
+ * qo_len queries sees keys < kv_len - qo_len + i + 1) split into chunks whose
+ * size the plan picks on the GPU from the total work.  Writes into
+ * `workspace` (size from nq_attention_workspace_bytes for the same maxima) and
+ * clears the merge counters it holds.  max_pages bounds the pages of all rows
+ * together.
+ */
+int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pages, int page_size,
+                                     int num_qo_heads, int num_kv_heads, int head_dim);
+int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                      const int32_t *last_page_len, int n_rows, int max_query_tokens,
+                      int max_pages, int page_size, int num_qo_heads, int num_kv_heads,
+                      int head_dim, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Paged GQA attention for mixed decode (qo_len == 1) and causal prefill
+ * (qo_len > 1, bottom-right aligned) rows over one layer of the paged cache.
+ * Replaces BatchDecodeWithPagedKVCacheWrapper.run / BatchPrefillWith-
+ * PagedKVCacheWrapper.run as used by executor/talker_kv.py:225-226,305-306.
+ * q: bf16 [tokens, num_qo_heads, head_dim] with strides (q_s0, q_s1, 1).
+ * cache: bf16 layer view; element (page, kind, slot, kv_head, d) at
+ *   page*c_page + kind*c_kind + slot*c_slot + kv_head*c_head + d
+ *   (kind 0 = K, 1 = V; the reference layout is [pages, 2, ps, Hkv, D]).
+ * out: bf16 [tokens, num_qo_heads, head_dim] with strides (o_s0, o_s1, 1).
+ * The plan in `workspace` must come from nq_attention_plan for the same
+ * metadata and the same (max_query_tokens, max_pages).  status (device int32, may be NULL) is set to NQ_ERR_INVALID_
+ * ARGUMENT when a page id outside [0, num_pages) is met (that page is skipped).
+ */
+int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
+                       int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
+                       int num_pages, const int32_t *kv_indptr, const int32_t *kv_indices,
+                       int page_size, int num_qo_heads, int num_kv_heads, int head_dim,
+                       float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
+                       int max_query_tokens, int max_pages, void *workspace,
+                       int64_t workspace_bytes, int32_t *status, void *stream);
+
+/*
+ * Code-predictor short-cache attention: one query per row over the first
+ * valid_length positions of a dense per-row cache.
+ * Replaces decode_attn_nhd_short_cache (model/kernels.py:408-520).
+ * Element (row, kind, pos, kv_head, d) of the cache sits at
+ *   row*c_row + kind*c_kind + pos*c_pos + kv_head*c_head + d.
+ */
+int nq_cp_short_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
+                          int64_t c_row, int64_t c_kind, int64_t c_pos, int64_t c_head,
+                          int rows, int valid_length, int num_qo_heads, int num_kv_heads,
+                          int head_dim, float sm_scale, uint16_t *out, int64_t o_s0,
+                          int64_t o_s1, void *stream);
+
+/*
+ * Fused per-head RMSNorm + rotate-half RoPE of q and k (in place), with K and
+ * V written into the cache.
+ * Replaces paired_qk_norm_rope_paged_cache_ (model/kernels.py:15-160) and,
+ * with write_pages == NULL, paired_qk_norm_rope_dense_cache_ (model/kernels.py:
+ * 163-248, 335-405): the destination "page" is then the token index and the
+ * slot is the constant `cache_position`.  With cache == NULL nothing is
+ * written (paired_qk_norm_rope_, model/kernels.py:275-332).
+ * round_to_input != 0 rounds the normalised values to bf16 before RoPE
+ * (model/kernels.py:65-67).  positions: int64 with stride pos_stride.
+ */
+int nq_qk_norm_rope_kv_write(uint16_t *q, int64_t q_s0, int64_t q_s1, uint16_t *k,
+                             int64_t k_s0, int64_t k_s1, const uint16_t *v, int64_t v_s0,
+                             int64_t v_s1, const uint16_t *q_weight, const uint16_t *k_weight,
+                             const int64_t *positions, int64_t pos_stride, int tokens,
+                             int num_qo_heads, int num_kv_heads, int head_dim, float eps,
+                             float rope_theta, int round_to_input, uint16_t *cache,
+                             int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
+                             const int64_t *write_pages, const int64_t *write_offsets,
+                             int cache_position, void *stream);
+
+/*
+ * Fused sampler with caller-supplied uniforms, one row per workgroup:
+ * optional logit masks, repetition penalty on seen ids (x>0 ? x/r : x*r),
+ * division by temperature, top-k (value desc, id asc), top-p nucleus and an
+ * inverse-CDF draw from uniforms[row] in [0,1).  Rows with temperature == 0
+ * take the argmax of the penalised logits (lowest id on ties).
+ * Replaces sample_talker_cuda_graph (executor/sampling.py:156-198),
+ * sample_logits_cuda_graph (:201-239), the fused code-predictor kernel
+ * (:242-336) and the penalty/greedy rules of sample_logits_stateless
+ * (model/sampling.py:55-65,127-225); the seen-mask update of
+ * TalkerExecutor._sample (executor/talker.py:373) when update_seen != 0, and
+ * the logit masks of TalkerExecutor.forward_logits (executor/talker.py:
+ * 173-183, 240-243) when mask_from < vocab.
+ * logits: dtype NQ_F32 or NQ_BF16, [rows, vocab] with row stride logits_s0.
+ * seen: uint8/bool [rows, vocab] (row stride seen_s0) or NULL.
+ * top_k: int32 (<= 0 means the whole vocabulary).  Masks: ids >= mask_from
+ * except eos_id become -inf; eos_id becomes -inf where suppress_eos[row] != 0
+ * (suppress_eos may be NULL).  tokens: int64 [rows].  vocab <= 8192.
+ */
+int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows, int vocab,
+              const float *temperature, const int32_t *top_k, const float *top_p,
+              const float *repetition_penalty, uint8_t *seen, int64_t seen_s0,
+              const float *uniforms, int mask_from, int eos_id, const uint8_t *suppress_eos,
+              int update_seen, int64_t *tokens, void *stream);
+
+/*
+ * Uniform draws in [0,1) from (seed, offset) counters with Philox-4x32-10
+ * (Salmon et al., SC'11): key = seed, counter = (offset, 0); u = (x0 >> 8) * 2^-24.
+ * Stands in for the stateless (seed, offset) draws of the reference
+ * (executor/sampling.py:183-195,281; contract/rng.py:32-43).
+ */
+int nq_uniforms_from_counter(const int64_t *seed, int64_t seed_stride, const int64_t *offset,
+                             int64_t offset_stride, int rows, float *uniforms, void *stream);
+
+/*
+ * Residual add + RMSNorm in place: residual += hidden; hidden = rmsnorm(residual).
+ * Replaces flashinfer.norm.fused_add_rmsnorm as called by qwen3_tts_add_rmsnorm
+ * (model/layers.py:43-79).  bf16 [rows, width], contiguous rows.
+ */
+int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16_t *weight, int rows,
+                   int width, float eps, void *stream);
+
+/*
+ * out = rmsnorm(x) (model/layers.py:82-115).  bf16 [rows, width]; out may alias x.
+ */
+int nq_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out, int rows, int width,
+               float eps, void *stream);
+
+/*
+ * out[r, j] = silu(gate_up[r, j]) * gate_up[r, width + j]
+ * (qwen3_tts_silu_and_mul, model/layers.py:28-40).  bf16, contiguous rows.
+ */
+int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int width, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQ_ABI_H */

@@ -1,0 +1,62 @@
+// Shared device helpers for the CDNA4 (gfx950) kernels of the hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nq_abi.h"
+
+#define NQ_CHECK_ARG(cond)                                                                     \
+    do {                                                                                       \
+        if (!(cond)) return NQ_ERR_INVALID_ARGUMENT;                                           \
+    } while (0)
+
+#define NQ_LAUNCH_STATUS() ((hipGetLastError() == hipSuccess) ? NQ_OK : NQ_ERR_LAUNCH)
+
+namespace nq {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16, quiet NaN preserved (matches torch).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// Unpack 8 bf16 held in a 128-bit vector into floats.
+__device__ __forceinline__ void unpack8(const uint4 &p, float (&x)[8]) {
+    x[0] = __uint_as_float(p.x << 16);
+    x[1] = __uint_as_float(p.x & 0xffff0000u);
+    x[2] = __uint_as_float(p.y << 16);
+    x[3] = __uint_as_float(p.y & 0xffff0000u);
+    x[4] = __uint_as_float(p.z << 16);
+    x[5] = __uint_as_float(p.z & 0xffff0000u);
+    x[6] = __uint_as_float(p.w << 16);
+    x[7] = __uint_as_float(p.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+template <int Width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = 1; m < Width; m <<= 1) v += __shfl_xor(v, m, kWave);
+    return v;
+}
+
+template <int Width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int m = 1; m < Width; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+    return v;
+}
+
+}  // namespace nq

@@ -1,0 +1,166 @@
+// Row-wise residual-add + RMSNorm, RMSNorm and SwiGLU pointwise kernels of the
+// talker decode step (model/layers.py:28-115), bf16 in and out, fp32 math.
+// One workgroup per row; each thread keeps its 8-element slices in registers
+// between the sum-of-squares reduction and the scaled store, so a row is read
+// and written exactly once.
+#include "nq_common.h"
+
+namespace nq {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kMaxVec = 4;  // width <= 256 * 8 * 4 = 8192
+
+__device__ float norm_block_sum(float v, float *tmp) {
+    v = group_sum<kWave>(v);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane == 0) tmp[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / kWave; ++w) s += tmp[w];
+    __syncthreads();
+    return s;
+}
+
+__global__ void __launch_bounds__(kNormThreads)
+add_rmsnorm_kernel(uint16_t *__restrict__ hidden, uint16_t *__restrict__ residual,
+                   const uint16_t *__restrict__ weight, int width, float eps) {
+    __shared__ float tmp[kNormThreads / kWave];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
+    const int nvec = width / 8;
+    float x[kMaxVec][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
+            float a[8], b[8];
+            unpack8(*reinterpret_cast<const uint4 *>(hidden + base + vi * 8), a);
+            unpack8(*reinterpret_cast<const uint4 *>(residual + base + vi * 8), b);
+            uint4 packed;
+            uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                pw[e / 2] = pack2_bf16(a[e] + b[e], a[e + 1] + b[e + 1]);
+            }
+            *reinterpret_cast<uint4 *>(residual + base + vi * 8) = packed;
+            unpack8(packed, x[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+        }
+    }
+    const float inv = rsqrtf(norm_block_sum(ss, tmp) / static_cast<float>(width) + eps);
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
+            float w[8];
+            unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w);
+            uint4 packed;
+            uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                pw[e / 2] = pack2_bf16(x[i][e] * inv * w[e], x[i][e + 1] * inv * w[e + 1]);
+            *reinterpret_cast<uint4 *>(hidden + base + vi * 8) = packed;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kNormThreads)
+rmsnorm_kernel(const uint16_t *__restrict__ xin, const uint16_t *__restrict__ weight,
+               uint16_t *__restrict__ out, int width, float eps) {
+    __shared__ float tmp[kNormThreads / kWave];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
+    const int nvec = width / 8;
+    float x[kMaxVec][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
+            unpack8(*reinterpret_cast<const uint4 *>(xin + base + vi * 8), x[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+        }
+    }
+    const float inv = rsqrtf(norm_block_sum(ss, tmp) / static_cast<float>(width) + eps);
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
+            float w[8];
+            unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w);
+            uint4 packed;
+            uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                pw[e / 2] = pack2_bf16(x[i][e] * inv * w[e], x[i][e + 1] * inv * w[e + 1]);
+            *reinterpret_cast<uint4 *>(out + base + vi * 8) = packed;
+        }
+    }
+}
+
+__global__ void silu_mul_kernel(const uint16_t *__restrict__ gate_up, uint16_t *__restrict__ out,
+                                int rows, int width) {
+    const int nvec = width / 8;
+    const int64_t total = static_cast<int64_t>(rows) * nvec;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t r = i / nvec;
+        const int64_t v = i - r * nvec;
+        float g[8], u[8];
+        unpack8(*reinterpret_cast<const uint4 *>(gate_up + r * 2 * width + v * 8), g);
+        unpack8(*reinterpret_cast<const uint4 *>(gate_up + r * 2 * width + width + v * 8), u);
+        uint4 packed;
+        uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float a = g[e] / (1.0f + expf(-g[e])) * u[e];
+            const float b = g[e + 1] / (1.0f + expf(-g[e + 1])) * u[e + 1];
+            pw[e / 2] = pack2_bf16(a, b);
+        }
+        *reinterpret_cast<uint4 *>(out + r * width + v * 8) = packed;
+    }
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace nq
+
+extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16_t *weight,
+                              int rows, int width, float eps, void *stream) {
+    NQ_CHECK_ARG(hidden && residual && weight && rows >= 0 && width >= 8);
+    if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
+    if (!nq::al16(hidden) || !nq::al16(residual) || !nq::al16(weight)) return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    hipLaunchKernelGGL(nq::add_rmsnorm_kernel, dim3(rows), dim3(nq::kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), hidden, residual, weight, width, eps);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out, int rows,
+                          int width, float eps, void *stream) {
+    NQ_CHECK_ARG(x && weight && out && rows >= 0 && width >= 8);
+    if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
+    if (!nq::al16(x) || !nq::al16(weight) || !nq::al16(out)) return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    hipLaunchKernelGGL(nq::rmsnorm_kernel, dim3(rows), dim3(nq::kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), x, weight, out, width, eps);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int width,
+                           void *stream) {
+    NQ_CHECK_ARG(gate_up && out && rows >= 0 && width >= 8);
+    if (width % 8) return NQ_ERR_UNSUPPORTED;
+    if (!nq::al16(gate_up) || !nq::al16(out)) return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    const int64_t total = static_cast<int64_t>(rows) * (width / 8);
+    int64_t grid = (total + 255) / 256;
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(nq::silu_mul_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), gate_up, out, rows, width);
+    return NQ_LAUNCH_STATUS();
+}

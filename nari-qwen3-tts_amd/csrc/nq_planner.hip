@@ -1,0 +1,229 @@
+// GPU construction of the ragged paged-KV metadata of one capture bucket.
+//
+// Restates PagedTalkerKV._metadata (executor/talker_kv.py:403-483) and the
+// page choice of PagedKVAllocator.reserve (executor/cache.py:135-184) as
+// integer kernels.  Every workgroup scans the (few) row descriptors into LDS
+// redundantly, so no inter-workgroup synchronisation is needed; the
+// O(pages + tokens) output fill is then spread grid-stride over the launch.
+#include "nq_common.h"
+
+namespace nq {
+namespace {
+
+constexpr int kPlanThreads = 1024;  // also the largest capture bucket supported
+
+// Block-wide exclusive scan of one int per thread.  Returns the exclusive
+// prefix; *total receives the block sum.  `tmp` holds >= kPlanThreads/64 ints.
+__device__ int block_exclusive_scan(int v, int *tmp, int *total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        int o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) tmp[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        const int nw = blockDim.x / kWave;
+        int w = lane < nw ? tmp[lane] : 0;
+        int wi = w;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            int o = __shfl_up(wi, d, kWave);
+            if (lane >= d) wi += o;
+        }
+        if (lane < nw) tmp[lane] = wi - w;  // exclusive wave offsets
+        if (lane == nw - 1) tmp[kWave] = wi;
+    }
+    __syncthreads();
+    const int res = tmp[wave] + incl - v;
+    *total = tmp[kWave];
+    __syncthreads();
+    return res;
+}
+
+// Largest r in [0, n) with off[r] <= x (off non-decreasing, off[0] == 0).
+__device__ __forceinline__ int find_row(const int *off, int n, int x) {
+    int lo = 0, hi = n;  // invariant: off[lo] <= x, answer in [lo, hi)
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= x) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+__global__ void __launch_bounds__(kPlanThreads)
+plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restrict__ pos_start,
+                   const int32_t *__restrict__ advance, const int32_t *__restrict__ prior_pages,
+                   const int32_t *__restrict__ table_row, int n_rows, int capture_rows,
+                   int token_capacity, int page_size, int prefill, int32_t *__restrict__ page_table,
+                   int64_t table_stride, const int32_t *__restrict__ free_pages, int n_free,
+                   const int32_t *__restrict__ scratch_pages, int32_t *__restrict__ qo_indptr,
+                   int32_t *__restrict__ kv_indptr, int32_t *__restrict__ kv_indices,
+                   int64_t kv_indices_capacity, int32_t *__restrict__ last_page_len,
+                   int64_t *__restrict__ position_ids, int64_t *__restrict__ write_pages,
+                   int64_t *__restrict__ write_offsets, int32_t *__restrict__ status) {
+    __shared__ int s_page_off[kPlanThreads];
+    __shared__ int s_tok_off[kPlanThreads];
+    __shared__ int s_miss_off[kPlanThreads];
+    __shared__ int s_tmp[kWave + 1];
+
+    const int r = threadIdx.x;
+    int npages = 0, ntok = 0, miss = 0, adv_real = 0, bad = 0;
+    if (r < n_rows) {
+        const int total = seq_len[r] + advance[r];
+        const int needed = (total + page_size - 1) / page_size;
+        miss = needed - prior_pages[r];
+        if (miss < 0 || advance[r] < 1) bad = 1;
+        npages = needed;
+        ntok = advance[r];
+        adv_real = advance[r];
+    } else if (r < capture_rows) {
+        npages = 1;
+        ntok = prefill ? 0 : 1;
+    }
+    int total_pages, total_tok, total_miss, sum_adv, any_bad;
+    const int page_off = block_exclusive_scan(npages, s_tmp, &total_pages);
+    const int tok_off = block_exclusive_scan(ntok, s_tmp, &total_tok);
+    const int miss_off = block_exclusive_scan(miss > 0 ? miss : 0, s_tmp, &total_miss);
+    block_exclusive_scan(adv_real, s_tmp, &sum_adv);
+    block_exclusive_scan(bad, s_tmp, &any_bad);
+    s_page_off[r] = page_off;
+    s_tok_off[r] = tok_off;
+    s_miss_off[r] = miss_off;
+    __syncthreads();
+
+    int err = NQ_OK;
+    if (any_bad || total_pages > kv_indices_capacity || total_tok > token_capacity)
+        err = NQ_ERR_INVALID_ARGUMENT;
+    else if (total_miss > n_free)
+        err = NQ_ERR_CAPACITY;
+    if (blockIdx.x == 0 && r == 0) {
+        status[0] = err;
+        status[1] = err == NQ_OK ? total_miss : 0;
+    }
+    if (err != NQ_OK) return;
+
+    if (blockIdx.x == 0 && r < capture_rows) {
+        kv_indptr[r + 1] = page_off + npages;
+        if (r == 0) kv_indptr[0] = 0;
+        if (r < n_rows) {
+            const int total = seq_len[r] + advance[r];
+            const int rem = total % page_size;
+            last_page_len[r] = rem ? rem : page_size;
+        } else {
+            last_page_len[r] = 1;
+        }
+        if (prefill) {
+            // padding rows add no queries
+            qo_indptr[r + 1] = (r < n_rows) ? tok_off + ntok : sum_adv;
+            if (r == 0) qo_indptr[0] = 0;
+        }
+    }
+
+    const int64_t gstride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+
+    // Page list: prior pages, then the row's slice of the sorted free list.
+    for (int64_t j = gid; j < total_pages; j += gstride) {
+        const int row = find_row(s_page_off, capture_rows, static_cast<int>(j));
+        const int i = static_cast<int>(j) - s_page_off[row];
+        int page;
+        if (row < n_rows) {
+            const int prior = prior_pages[row];
+            int32_t *trow = page_table + static_cast<int64_t>(table_row[row]) * table_stride;
+            if (i < prior) {
+                page = trow[i];
+            } else {
+                page = free_pages[s_miss_off[row] + (i - prior)];
+                trow[i] = page;  // proposed pages; harmless if the publication is discarded
+            }
+        } else {
+            page = scratch_pages[row];
+        }
+        kv_indices[j] = page;
+    }
+
+    // Per-token write slots and positions.
+    for (int64_t t = gid; t < token_capacity; t += gstride) {
+        int64_t wpage, woff, pos;
+        if (t < total_tok) {
+            const int row = find_row(s_tok_off, capture_rows, static_cast<int>(t));
+            const int o = static_cast<int>(t) - s_tok_off[row];
+            if (row < n_rows) {
+                const int abs_pos = seq_len[row] + o;
+                const int pidx = abs_pos / page_size;
+                const int prior = prior_pages[row];
+                if (pidx < prior)
+                    wpage = page_table[static_cast<int64_t>(table_row[row]) * table_stride + pidx];
+                else
+                    wpage = free_pages[s_miss_off[row] + (pidx - prior)];
+                woff = abs_pos % page_size;
+                pos = static_cast<int64_t>(pos_start[row]) + o;
+            } else {  // decode padding row: scratch slot 0 of its own page
+                wpage = scratch_pages[row];
+                woff = 0;
+                pos = 0;
+            }
+        } else {  // padding tokens walk the scratch slots after the real tokens
+            const int64_t slot = t - sum_adv;
+            wpage = scratch_pages[slot / page_size];
+            woff = slot % page_size;
+            pos = 0;
+        }
+        position_ids[t] = pos;
+        write_pages[t] = wpage;
+        write_offsets[t] = woff;
+    }
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start,
+                              const int32_t *advance, const int32_t *prior_pages,
+                              const int32_t *table_row, int n_rows, int capture_rows,
+                              int token_capacity, int page_size, int prefill,
+                              int32_t *page_table, int64_t table_stride,
+                              const int32_t *free_pages, int n_free,
+                              const int32_t *scratch_pages, int n_scratch,
+                              int32_t *qo_indptr, int32_t *kv_indptr, int32_t *kv_indices,
+                              int64_t kv_indices_capacity, int32_t *last_page_len,
+                              int64_t *position_ids, int64_t *write_pages,
+                              int64_t *write_offsets, int32_t *status, int grid_blocks,
+                              void *stream) {
+    NQ_CHECK_ARG(n_rows >= 1 && n_rows <= capture_rows);
+    if (capture_rows > nq::kPlanThreads) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(page_size >= 1 && token_capacity >= 1 && n_free >= 0);
+    // Scratch capacity rule of PagedTalkerKV._validate_scratch_capacity (talker_kv.py:397-401).
+    NQ_CHECK_ARG(capture_rows <= n_scratch);
+    NQ_CHECK_ARG(static_cast<int64_t>(token_capacity) <= static_cast<int64_t>(n_scratch) * page_size);
+    NQ_CHECK_ARG(seq_len && pos_start && advance && prior_pages && table_row && page_table);
+    NQ_CHECK_ARG(scratch_pages && kv_indptr && kv_indices && last_page_len && status);
+    NQ_CHECK_ARG(position_ids && write_pages && write_offsets && table_stride >= 1);
+    NQ_CHECK_ARG(!prefill || qo_indptr);
+    NQ_CHECK_ARG(n_free == 0 || free_pages);
+    int grid = grid_blocks > 0 ? grid_blocks : 8;
+    hipLaunchKernelGGL(nq::plan_ragged_kernel, dim3(grid), dim3(nq::kPlanThreads), 0,
+                       static_cast<hipStream_t>(stream), seq_len, pos_start, advance,
+                       prior_pages, table_row, n_rows, capture_rows, token_capacity, page_size,
+                       prefill, page_table, table_stride, free_pages, n_free, scratch_pages,
+                       qo_indptr, kv_indptr, kv_indices, kv_indices_capacity, last_page_len,
+                       position_ids, write_pages, write_offsets, status);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_abi_version(void) { return NQ_ABI_VERSION; }
+
+extern "C" const char *nq_status_string(int status) {
+    switch (status) {
+        case NQ_OK: return "ok";
+        case NQ_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case NQ_ERR_UNSUPPORTED: return "unsupported dtype or size";
+        case NQ_ERR_LAUNCH: return "HIP launch failure";
+        case NQ_ERR_CAPACITY: return "not enough free KV pages";
+        default: return "unknown status";
+    }
+}

@@ -1,0 +1,401 @@
+// Fused sampler: logit masks, repetition penalty, temperature, top-k, top-p
+// and an inverse-CDF draw from a caller-supplied uniform, one workgroup per
+// row; plus Philox-4x32-10 uniforms from (seed, offset) counters.
+//
+// Arithmetic contract (restated exactly by the numpy oracle, so token ids are
+// bit-identical; this translation unit is built with -ffp-contract=off):
+//   x_i   = logit_i (fp32; bf16 widened exactly); masked ids -> -inf
+//           (executor/talker.py:173-183, 240-243)
+//   x_i   = seen_i ? (x_i > 0 ? x_i / r : x_i * r) : x_i   (model/sampling.py:55-65)
+//   T == 0: token = argmax_i x_i, lowest id on ties         (model/sampling.py:183-187)
+//   s_i   = x_i / T                                         (model/sampling.py:218,
+//                                                            executor/sampling.py:267)
+//   order : by (s desc, id asc) on the IEEE bit pattern (sortable key), top
+//           k_eff = (k > 0 ? min(k, V) : V) ranks           (executor/sampling.py:172-177,268)
+//   w_r   = nq_exp(s_r - s_0)                               (executor/sampling.py:272)
+//   cum   = segmented wave scan: lane L of 64 owns ranks [L*E, L*E+E), E = ceil(k/64);
+//           sequential inclusive sums inside a lane, Kogge-Stone inclusive scan
+//           of the lane totals, cum_r = excl_L + local_r
+//   keep  = longest rank prefix with (cum_r - w_r) < min(p,1) * cum_{k-1}
+//                                                           (executor/sampling.py:275-277)
+//   token = id of the first kept rank with cum_r >= u * cum_{last kept}
+//           (the last kept rank if none)                    (executor/sampling.py:282-288)
+// nq_exp is Cody-Waite range reduction (ln 2 split as in Cephes' expf) with a
+// degree-7 Taylor polynomial in Horner form; inputs below -87 give 0.
+#include "nq_common.h"
+
+namespace nq {
+namespace {
+
+constexpr int kSampThreads = 256;
+constexpr int kMaxVocab = 4096;
+constexpr uint32_t kLog2eBits = 0x3fb8aa3bu;   // 1.44269504f
+constexpr uint32_t kLn2HiBits = 0x3f318000u;   // 0.693359375f
+constexpr uint32_t kLn2LoBits = 0xb95e8083u;   // -2.12194440e-4f
+constexpr uint32_t kExpLowBits = 0xc2ae0000u;  // -87.0f
+
+__device__ __forceinline__ float fbits(uint32_t b) { return __uint_as_float(b); }
+
+__device__ float nq_exp(float x) {
+    if (!(x > fbits(kExpLowBits))) return 0.0f;
+    const float t = x * fbits(kLog2eBits);
+    const float n = floorf(t + 0.5f);
+    float r = x - n * fbits(kLn2HiBits);
+    r = r - n * fbits(kLn2LoBits);
+    float p = 1.0f / 5040.0f;
+    p = p * r + 1.0f / 720.0f;
+    p = p * r + 1.0f / 120.0f;
+    p = p * r + 1.0f / 24.0f;
+    p = p * r + 1.0f / 6.0f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    const int ni = static_cast<int>(n);
+    return p * __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
+}
+
+__device__ __forceinline__ uint32_t sort_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t composite(float f, int id) {
+    return (static_cast<uint64_t>(sort_key(f)) << 32) | (0xffffffffu - static_cast<uint32_t>(id));
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, kWave);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, kWave);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ int samp_block_scan(int v, int *tmp, int *total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        int o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) tmp[wave] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int w = 0; w < kSampThreads / kWave; ++w) {
+            const int x = tmp[w];
+            tmp[w] = acc;
+            acc += x;
+        }
+        tmp[kWave] = acc;
+    }
+    __syncthreads();
+    const int res = tmp[wave] + incl - v;
+    *total = tmp[kWave];
+    __syncthreads();
+    return res;
+}
+
+template <typename InT>
+__device__ __forceinline__ float load_logit(const InT *p);
+template <>
+__device__ __forceinline__ float load_logit<float>(const float *p) { return *p; }
+template <>
+__device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *p) { return bf16_to_f32(*p); }
+
+template <typename InT>
+__global__ void __launch_bounds__(kSampThreads)
+sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
+              const float *__restrict__ temperature, const int32_t *__restrict__ top_k,
+              const float *__restrict__ top_p, const float *__restrict__ penalty,
+              uint8_t *__restrict__ seen, int64_t seen_s0, const float *__restrict__ uniforms,
+              int mask_from, int eos_id, const uint8_t *__restrict__ suppress_eos,
+              int update_seen, int64_t *__restrict__ tokens) {
+    __shared__ float s_val[kMaxVocab];
+    __shared__ uint64_t s_sort[kMaxVocab];
+    __shared__ uint32_t s_hist[256];
+    __shared__ int s_tmp[kWave + 1];
+    __shared__ int s_bin, s_above;
+    __shared__ uint64_t s_red[kSampThreads / kWave];
+
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const InT *lrow = logits + row * logits_s0;
+    const float T = temperature[row];
+    const float r = penalty ? penalty[row] : 1.0f;
+    const bool greedy = T == 0.0f;
+    const bool sup_eos = suppress_eos && suppress_eos[row];
+    uint8_t *srow = seen ? seen + row * seen_s0 : nullptr;
+
+    // 1. masks, penalty, temperature into LDS.
+    for (int id = tid; id < vocab; id += kSampThreads) {
+        float x = load_logit<InT>(lrow + id);
+        if ((id >= mask_from && id != eos_id) || (id == eos_id && sup_eos)) x = -INFINITY;
+        if (srow && srow[id]) x = x > 0.0f ? x / r : x * r;
+        s_val[id] = greedy ? x : x / T;
+    }
+    __syncthreads();
+
+    int token;
+    if (greedy) {
+        uint64_t best = 0;
+        for (int id = tid; id < vocab; id += kSampThreads) {
+            const uint64_t c = composite(s_val[id], id);
+            best = c > best ? c : best;
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const uint64_t o = shfl_xor_u64(best, m);
+            best = o > best ? o : best;
+        }
+        if (lane == 0) s_red[wave] = best;
+        __syncthreads();
+        best = s_red[0];
+        for (int w = 1; w < kSampThreads / kWave; ++w) best = s_red[w] > best ? s_red[w] : best;
+        token = static_cast<int>(0xffffffffu - static_cast<uint32_t>(best));
+    } else {
+        const int kq = top_k[row];
+        const int k_eff = (kq > 0 && kq < vocab) ? kq : vocab;
+        float p = top_p[row];
+        p = p < 1.0f ? p : 1.0f;
+
+        // 2. radix select of the k_eff-th largest sortable key.
+        uint32_t prefix = 0, pmask = 0;
+        int remaining = k_eff;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            s_hist[tid] = 0;
+            __syncthreads();
+            for (int id = tid; id < vocab; id += kSampThreads) {
+                const uint32_t key = sort_key(s_val[id]);
+                if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            const int bin = 255 - tid;
+            const int v = static_cast<int>(s_hist[bin]);
+            int tot;
+            const int above = samp_block_scan(v, s_tmp, &tot);  // count in bins > bin
+            if (above < remaining && remaining <= above + v) {
+                s_bin = bin;
+                s_above = above;
+            }
+            __syncthreads();
+            prefix |= static_cast<uint32_t>(s_bin) << shift;
+            pmask |= 255u << shift;
+            remaining -= s_above;
+            __syncthreads();
+        }
+        const uint32_t thr = prefix;
+        const int need_eq = remaining;
+
+        // 3. compact the selected ids in id order.
+        const int per = (vocab + kSampThreads - 1) / kSampThreads;
+        const int lo_id = tid * per;
+        const int hi_id = min(vocab, lo_id + per);
+        int n_eq = 0;
+        for (int id = lo_id; id < hi_id; ++id) n_eq += sort_key(s_val[id]) == thr;
+        int tot;
+        const int eq_base = samp_block_scan(n_eq, s_tmp, &tot);
+        int n_sel = 0, eq_seen = 0;
+        for (int id = lo_id; id < hi_id; ++id) {
+            const uint32_t key = sort_key(s_val[id]);
+            const bool eq = key == thr;
+            n_sel += (key > thr) || (eq && eq_base + eq_seen < need_eq);
+            eq_seen += eq;
+        }
+        const int sel_base = samp_block_scan(n_sel, s_tmp, &tot);
+        {
+            int at = sel_base;
+            eq_seen = 0;
+            for (int id = lo_id; id < hi_id; ++id) {
+                const float f = s_val[id];
+                const uint32_t key = sort_key(f);
+                const bool eq = key == thr;
+                if ((key > thr) || (eq && eq_base + eq_seen < need_eq)) s_sort[at++] = composite(f, id);
+                eq_seen += eq;
+            }
+        }
+        __syncthreads();
+
+        // 4. sort the k_eff selected entries by (value desc, id asc).
+        if (k_eff <= kWave) {
+            if (wave == 0) {
+                uint64_t key = lane < k_eff ? s_sort[lane] : 0ull;
+#pragma unroll
+                for (int kk = 2; kk <= kWave; kk <<= 1) {
+#pragma unroll
+                    for (int j = kk >> 1; j > 0; j >>= 1) {
+                        const uint64_t other = shfl_xor_u64(key, j);
+                        const bool lower = (lane & j) == 0;
+                        const bool asc = (lane & kk) == 0;
+                        const bool take_max = lower == asc;
+                        key = take_max ? (key > other ? key : other) : (key < other ? key : other);
+                    }
+                }
+                if (lane < k_eff) s_sort[lane] = key;
+            }
+        } else {
+            int n2 = 1;
+            while (n2 < k_eff) n2 <<= 1;
+            for (int i = k_eff + tid; i < n2; i += kSampThreads) s_sort[i] = 0ull;
+            __syncthreads();
+            for (int kk = 2; kk <= n2; kk <<= 1) {
+                for (int j = kk >> 1; j > 0; j >>= 1) {
+                    for (int idx = tid; idx < n2 / 2; idx += kSampThreads) {
+                        const int i = 2 * j * (idx / j) + (idx % j);
+                        const int pr = i + j;
+                        const bool asc = (i & kk) == 0;
+                        const uint64_t a = s_sort[i], b = s_sort[pr];
+                        const bool swap = asc ? (a < b) : (a > b);
+                        if (swap) {
+                            s_sort[i] = b;
+                            s_sort[pr] = a;
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+        }
+        __syncthreads();
+
+        // 5. weights (rank order), stored as (w bits << 32 | id).
+        const float v0 = s_val[static_cast<int>(0xffffffffu - static_cast<uint32_t>(s_sort[0]))];
+        __syncthreads();
+        for (int rr = tid; rr < k_eff; rr += kSampThreads) {
+            const int id = static_cast<int>(0xffffffffu - static_cast<uint32_t>(s_sort[rr]));
+            const float w = nq_exp(s_val[id] - v0);
+            s_sort[rr] = (static_cast<uint64_t>(__float_as_uint(w)) << 32) | static_cast<uint32_t>(id);
+        }
+        __syncthreads();
+
+        // 6. segmented wave scan, nucleus and draw (wave 0).
+        if (wave == 0) {
+            const int E = (k_eff + kWave - 1) / kWave;
+            const int r0 = lane * E;
+            const int r1 = min(k_eff, r0 + E);
+            float loc = 0.0f;
+            for (int rr = r0; rr < r1; ++rr) {
+                loc = loc + __uint_as_float(static_cast<uint32_t>(s_sort[rr] >> 32));
+                s_val[rr] = loc;  // local inclusive sums, rank-indexed (ids are no longer needed)
+            }
+            float S = loc;
+#pragma unroll
+            for (int d = 1; d < kWave; d <<= 1) {
+                const float o = __shfl_up(S, d, kWave);
+                if (lane >= d) S = S + o;
+            }
+            float excl = __shfl_up(S, 1, kWave);
+            if (lane == 0) excl = 0.0f;
+            for (int rr = r0; rr < r1; ++rr) s_val[rr] = excl + s_val[rr];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float total = s_val[k_eff - 1];
+            const float pt = p * total;
+            const int E = (k_eff + kWave - 1) / kWave;
+            const int r0 = lane * E;
+            const int r1 = min(k_eff, r0 + E);
+            int first_drop = k_eff;
+            for (int rr = r0; rr < r1; ++rr) {
+                const float w = __uint_as_float(static_cast<uint32_t>(s_sort[rr] >> 32));
+                if (!((s_val[rr] - w) < pt)) { first_drop = rr; break; }
+            }
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) first_drop = min(first_drop, __shfl_xor(first_drop, m, kWave));
+            const int kept = first_drop > 0 ? first_drop : 1;
+            const float mass = s_val[kept - 1];
+            const float um = uniforms[row] * mass;
+            int pick = kept - 1;
+            for (int rr = r0; rr < min(r1, kept); ++rr)
+                if (s_val[rr] >= um) { pick = rr; break; }
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) pick = min(pick, __shfl_xor(pick, m, kWave));
+            if (v0 == -INFINITY) pick = 0;
+            if (lane == 0) s_bin = static_cast<int>(static_cast<uint32_t>(s_sort[pick]));
+        }
+        __syncthreads();
+        token = s_bin;
+    }
+    if (tid == 0) {
+        tokens[row] = token;
+        if (update_seen && srow) srow[token] = 1;
+    }
+}
+
+// Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds, key bumped by
+// the Weyl constants.  Returns the first output word.
+__device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                                 uint32_t k0, uint32_t k1) {
+    constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+    constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+        const uint64_t p0 = static_cast<uint64_t>(M0) * c0;
+        const uint64_t p1 = static_cast<uint64_t>(M1) * c2;
+        const uint32_t hi0 = static_cast<uint32_t>(p0 >> 32), lo0 = static_cast<uint32_t>(p0);
+        const uint32_t hi1 = static_cast<uint32_t>(p1 >> 32), lo1 = static_cast<uint32_t>(p1);
+        const uint32_t n0 = hi1 ^ c1 ^ k0;
+        const uint32_t n1 = lo1;
+        const uint32_t n2 = hi0 ^ c3 ^ k1;
+        const uint32_t n3 = lo0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += W0;
+        k1 += W1;
+    }
+    return c0;
+}
+
+__global__ void uniforms_kernel(const int64_t *__restrict__ seed, int64_t seed_stride,
+                                const int64_t *__restrict__ offset, int64_t offset_stride, int rows,
+                                float *__restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    const uint64_t s = static_cast<uint64_t>(seed[i * seed_stride]);
+    const uint64_t o = static_cast<uint64_t>(offset[i * offset_stride]);
+    const uint32_t x = philox_first(static_cast<uint32_t>(o), static_cast<uint32_t>(o >> 32), 0u, 0u,
+                                    static_cast<uint32_t>(s), static_cast<uint32_t>(s >> 32));
+    out[i] = static_cast<float>(x >> 8) * (1.0f / 16777216.0f);
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows,
+                         int vocab, const float *temperature, const int32_t *top_k,
+                         const float *top_p, const float *repetition_penalty, uint8_t *seen,
+                         int64_t seen_s0, const float *uniforms, int mask_from, int eos_id,
+                         const uint8_t *suppress_eos, int update_seen, int64_t *tokens,
+                         void *stream) {
+    NQ_CHECK_ARG(logits && temperature && top_k && top_p && uniforms && tokens);
+    NQ_CHECK_ARG(rows >= 0 && vocab >= 1);
+    NQ_CHECK_ARG(!update_seen || seen);
+    if (vocab > nq::kMaxVocab) return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (logits_dtype == NQ_F32) {
+        hipLaunchKernelGGL(nq::sample_kernel<float>, dim3(rows), dim3(nq::kSampThreads), 0, s,
+                           static_cast<const float *>(logits), logits_s0, vocab, temperature,
+                           top_k, top_p, repetition_penalty, seen, seen_s0, uniforms, mask_from,
+                           eos_id, suppress_eos, update_seen, tokens);
+    } else if (logits_dtype == NQ_BF16) {
+        hipLaunchKernelGGL(nq::sample_kernel<uint16_t>, dim3(rows), dim3(nq::kSampThreads), 0, s,
+                           static_cast<const uint16_t *>(logits), logits_s0, vocab, temperature,
+                           top_k, top_p, repetition_penalty, seen, seen_s0, uniforms, mask_from,
+                           eos_id, suppress_eos, update_seen, tokens);
+    } else {
+        return NQ_ERR_UNSUPPORTED;
+    }
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_uniforms_from_counter(const int64_t *seed, int64_t seed_stride,
+                                        const int64_t *offset, int64_t offset_stride, int rows,
+                                        float *uniforms, void *stream) {
+    NQ_CHECK_ARG(seed && offset && uniforms && rows >= 0);
+    if (rows == 0) return NQ_OK;
+    hipLaunchKernelGGL(nq::uniforms_kernel, dim3((rows + 255) / 256), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), seed, seed_stride, offset, offset_stride,
+                       rows, uniforms);
+    return NQ_LAUNCH_STATUS();
+}

@@ -1,0 +1,19 @@
+"""Exception types with the reference's names and meaning.
+
+KVAllocationError / StaleKVPublicationError mirror executor/cache.py:11-16,
+SlotBusyError mirrors executor/cuda_graph.py:102-103.
+"""
+
+from __future__ import annotations
+
+
+class KVAllocationError(RuntimeError):
+    pass
+
+
+class StaleKVPublicationError(RuntimeError):
+    pass
+
+
+class SlotBusyError(RuntimeError):
+    pass

@@ -1,0 +1,166 @@
+"""One talker decode step on the GPU: the unit the serving metric counts.
+
+Follows the reference step (executor/talker.py:231-262, 341-374 and
+model/components.py:29-90): decode embedding = step embed + projected text
+embedding, then per layer input norm, packed QKV projection, fused
+qk-norm/RoPE/paged KV write + paged attention (TalkerAttentionContext.attend),
+o-proj, fused residual add + RMSNorm, SwiGLU MLP and the next fused add-norm;
+the codec head; the fused sampler (logit masks, repetition penalty over the
+seen mask, temperature, top-k, top-p, draw) with the seen-mask update.
+
+GEMMs go through torch (hipBLASLt) in bf16; everything else is the HIP
+library.  Weights are random (N(0, 0.02), norm weights 1) because no
+checkpoint is available; shapes follow the Qwen3-TTS 1.7B talker.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from types import SimpleNamespace
+
+import torch
+import torch.nn.functional as F
+
+from .layers import qwen3_tts_add_rmsnorm, qwen3_tts_rmsnorm, qwen3_tts_silu_and_mul
+from .sampling import sample_with_uniforms, uniforms_from_counter
+
+
+@dataclass(frozen=True)
+class TalkerConfig:
+    num_layers: int = 28
+    hidden: int = 2048
+    num_qo_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 6144
+    vocab: int = 3072
+    text_vocab: int = 4096
+    codec_vocab: int = 2048  # ids >= this are suppressed except EOS (executor/talker.py:173-183)
+    eos_id: int = 2150
+    rms_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.num_qo_heads + 2 * self.num_kv_heads) * self.head_dim
+
+
+class TalkerWeights:
+    """Random-init talker parameters in bf16 on one device."""
+
+    def __init__(self, config: TalkerConfig, device: torch.device, seed: int = 0, std: float = 0.02) -> None:
+        self.config = config
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        c = config
+        bf = dict(dtype=torch.bfloat16, device=device)
+
+        def randn(*shape):
+            return (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
+
+        self.layers = []
+        for _ in range(c.num_layers):
+            self.layers.append(
+                SimpleNamespace(
+                    input_norm=torch.ones(c.hidden, **bf),
+                    qkv=randn(c.qkv_width, c.hidden),
+                    o=randn(c.hidden, c.num_qo_heads * c.head_dim),
+                    post_norm=torch.ones(c.hidden, **bf),
+                    gate_up=randn(2 * c.intermediate, c.hidden),
+                    down=randn(c.hidden, c.intermediate),
+                    attention=SimpleNamespace(
+                        q_norm=SimpleNamespace(weight=torch.ones(c.head_dim, **bf), variance_epsilon=c.rms_eps),
+                        k_norm=SimpleNamespace(weight=torch.ones(c.head_dim, **bf), variance_epsilon=c.rms_eps),
+                        rope_theta=c.rope_theta,
+                    ),
+                )
+            )
+        self.final_norm = torch.ones(c.hidden, **bf)
+        self.codec_head = randn(c.vocab, c.hidden)
+        self.text_embedding = randn(c.text_vocab, c.hidden)
+
+    def weight_bytes(self) -> int:
+        total = self.final_norm.numel() + self.codec_head.numel()
+        for layer in self.layers:
+            total += sum(t.numel() for t in (layer.input_norm, layer.qkv, layer.o, layer.post_norm, layer.gate_up, layer.down))
+            total += layer.attention.q_norm.weight.numel() + layer.attention.k_norm.weight.numel()
+        return 2 * total
+
+
+class TalkerDecodeStep:
+    """Static buffers and the forward of one decode bucket (``rows`` physical rows)."""
+
+    def __init__(self, weights: TalkerWeights, context, rows: int, *, use_counter_rng: bool = False) -> None:
+        c = weights.config
+        self.w = weights
+        self.context = context
+        self.rows = rows
+        dev = weights.codec_head.device
+        self.device = dev
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.step_embed = torch.zeros(rows, c.hidden, **bf)
+        self.text_ids = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.temperature = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.top_k = torch.ones(rows, dtype=torch.int32, device=dev)
+        self.top_p = torch.ones(rows, dtype=torch.float32, device=dev)
+        self.penalty = torch.ones(rows, dtype=torch.float32, device=dev)
+        self.seen = torch.zeros(rows, c.vocab, dtype=torch.bool, device=dev)
+        self.suppress_eos = torch.zeros(rows, dtype=torch.bool, device=dev)
+        self.uniforms = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.seed = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.offsets = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.use_counter_rng = use_counter_rng
+        # work buffers
+        self.residual = torch.zeros(rows, c.hidden, **bf)
+        self.hidden = torch.zeros(rows, c.hidden, **bf)
+        self.qkv = torch.zeros(rows, c.qkv_width, **bf)
+        self.gate_up = torch.zeros(rows, 2 * c.intermediate, **bf)
+        self.act = torch.zeros(rows, c.intermediate, **bf)
+        self.logits = torch.zeros(rows, c.vocab, **bf)
+        self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
+
+    def forward(self) -> torch.Tensor:
+        c = self.w.config
+        ctx = self.context
+        n = self.rows
+        # materialize_decode (executor/talker.py:256-262)
+        torch.add(self.step_embed, F.embedding(self.text_ids, self.w.text_embedding), out=self.residual)
+        qwen3_tts_rmsnorm(self.residual, self.w.layers[0].input_norm, c.rms_eps, out=self.hidden)
+        q_w = c.num_qo_heads * c.head_dim
+        kv_w = c.num_kv_heads * c.head_dim
+        for index, layer in enumerate(self.w.layers):
+            ctx.select_layer(index)
+            torch.matmul(self.hidden, layer.qkv.t(), out=self.qkv)
+            q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
+            k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
+            v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
+            attended = ctx.attend(layer.attention, q, k, v)
+            torch.matmul(attended.view(n, q_w), layer.o.t(), out=self.hidden)
+            qwen3_tts_add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
+            torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
+            qwen3_tts_silu_and_mul(self.gate_up, out=self.act)
+            torch.matmul(self.act, layer.down.t(), out=self.hidden)
+            nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
+            qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
+        ctx.advance_sequence_lengths()
+        torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
+        if self.use_counter_rng:
+            uniforms_from_counter(self.seed, self.offsets, out=self.uniforms)
+        sample_with_uniforms(
+            self.logits,
+            self.temperature,
+            self.top_k,
+            self.top_p,
+            self.uniforms,
+            repetition_penalty=self.penalty,
+            seen_token_mask=self.seen,
+            mask_from=c.codec_vocab,
+            eos_id=c.eos_id,
+            suppress_eos=self.suppress_eos,
+            update_seen=True,
+            out=self.tokens,
+        )
+        return self.tokens
+
+
+__all__ = ["TalkerConfig", "TalkerDecodeStep", "TalkerWeights"]

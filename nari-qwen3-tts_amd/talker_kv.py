@@ -1,0 +1,533 @@
+"""Paged talker KV with GPU-built metadata and HIP attention bindings.
+
+Drop-in for the reference's ``PagedTalkerKV`` and its FlashInfer bindings
+(executor/talker_kv.py:15-570): the same constructor, the TalkerKVBackend
+methods (create_prefill/create_decode, prepare_prefill/prepare_decode,
+prepare_capture/finish_capture, abort, add_request/remove_request/state) and
+the TalkerAttentionContext protocol (metadata, plan, select_layer, attend,
+advance_sequence_lengths).  What moves to the GPU:
+
+- ``_metadata`` (talker_kv.py:403-483): the host keeps page ownership (the
+  allocator) and stages O(rows) scalars; ``nq_plan_ragged`` writes
+  qo/kv indptr, the page list, last-page lengths, positions and write slots
+  straight into the binding's static buffers, reading prior pages from a
+  device page table and new pages from a device copy of the sorted free list.
+- ``plan`` (talker_kv.py:175-223, 259-303): ``nq_attention_plan`` splits the
+  keys of every query into chunks on the GPU; there is no plan signature to
+  reuse because planning is one small kernel.
+- ``attend`` (talker_kv.py:104-129): ``nq_qk_norm_rope_kv_write`` then
+  ``nq_paged_attention``.
+
+Storage keeps the reference layout ``[layers, pages, 2, page_size, Hkv, D]``
+(talker_kv.py:336-340), bf16.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .cache import PagedKVAllocator, PendingKVPublication, RequestKVState
+
+
+@dataclass(frozen=True, slots=True)
+class TalkerAttentionMetadata:
+    qo_indptr: torch.Tensor | None
+    paged_kv_indptr: torch.Tensor
+    paged_kv_indices: torch.Tensor
+    paged_kv_last_page_len: torch.Tensor
+    position_ids: torch.Tensor
+    write_pages: torch.Tensor
+    write_offsets: torch.Tensor
+    padding_pages: tuple[int, ...]
+    reuse_attention_plan: bool = True
+
+
+class _MetadataBuffers:
+    """Static device buffers one planner launch writes into."""
+
+    def __init__(self, *, rows: int, tokens: int, index_capacity: int, prefill: bool, device) -> None:
+        i32 = dict(dtype=torch.int32, device=device)
+        i64 = dict(dtype=torch.long, device=device)
+        self.qo_indptr = torch.zeros(rows + 1, **i32) if prefill else None
+        self.kv_indptr = torch.zeros(rows + 1, **i32)
+        self.kv_indices = torch.zeros(index_capacity, **i32)
+        self.last_page_len = torch.ones(rows, **i32)
+        self.position_ids = torch.zeros(tokens, **i64)
+        self.write_pages = torch.zeros(tokens, **i64)
+        self.write_offsets = torch.zeros(tokens, **i64)
+        self.status = torch.zeros(2, **i32)
+
+
+class _HipBindingBase:
+    """One captured slot's attention context (TalkerAttentionContext)."""
+
+    prefill = False
+
+    def __init__(
+        self,
+        *,
+        storage: torch.Tensor,
+        capture_batch_size: int,
+        token_capacity: int,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        total_pages: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        **_: object,
+    ) -> None:
+        self.storage = storage
+        self.capture_batch_size = capture_batch_size
+        self.token_capacity = token_capacity
+        self.num_qo_heads = num_qo_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.total_pages = total_pages
+        self.device = device
+        self.dtype = dtype
+        # Padding rows may repeat scratch pages, hence + rows (talker_kv.py:147-153).
+        self.index_capacity = total_pages + capture_batch_size
+        self.buffers = _MetadataBuffers(
+            rows=capture_batch_size,
+            tokens=token_capacity,
+            index_capacity=self.index_capacity,
+            prefill=self.prefill,
+            device=device,
+        )
+        lib = _lib.load()
+        nbytes = lib.nq_attention_workspace_bytes(
+            token_capacity, self.index_capacity, page_size, num_qo_heads, num_kv_heads, head_dim
+        )
+        _lib.check(min(int(nbytes), 0), "nq_attention_workspace_bytes")
+        self.workspace = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        self.attention_status = torch.zeros(1, dtype=torch.int32, device=device)
+        self.output = torch.zeros((token_capacity, num_qo_heads, head_dim), dtype=dtype, device=device)
+        self.position_ids = self.buffers.position_ids
+        self.write_pages = self.buffers.write_pages
+        self.write_offsets = self.buffers.write_offsets
+        self.metadata: TalkerAttentionMetadata | None = None
+        self._layer_index = 0
+
+    # -- planning ---------------------------------------------------------
+    def _stage(self, metadata: TalkerAttentionMetadata) -> None:
+        """Copy metadata produced elsewhere into the static buffers."""
+
+        b = self.buffers
+        if metadata.paged_kv_indptr.data_ptr() == b.kv_indptr.data_ptr():
+            return
+        if metadata.position_ids.shape != b.position_ids.shape:
+            raise ValueError("Talker position metadata does not match the captured token capacity")
+        if metadata.paged_kv_indices.numel() > b.kv_indices.numel():
+            raise ValueError("Talker page metadata exceeds its captured buffer")
+        b.kv_indptr.copy_(metadata.paged_kv_indptr, non_blocking=True)
+        b.kv_indices[: metadata.paged_kv_indices.numel()].copy_(metadata.paged_kv_indices, non_blocking=True)
+        b.last_page_len.copy_(metadata.paged_kv_last_page_len, non_blocking=True)
+        b.position_ids.copy_(metadata.position_ids, non_blocking=True)
+        b.write_pages.copy_(metadata.write_pages, non_blocking=True)
+        b.write_offsets.copy_(metadata.write_offsets, non_blocking=True)
+        if b.qo_indptr is not None:
+            b.qo_indptr.copy_(metadata.qo_indptr, non_blocking=True)
+
+    def plan(self, metadata: TalkerAttentionMetadata) -> None:
+        if self.prefill and metadata.qo_indptr is None:
+            raise ValueError("Talker prefill requires packed query metadata")
+        if not self.prefill and metadata.qo_indptr is not None:
+            raise ValueError("Talker decode cannot contain packed query metadata")
+        self._stage(metadata)
+        b = self.buffers
+        _lib.call(
+            "nq_attention_plan",
+            _lib.ptr(b.qo_indptr),
+            _lib.ptr(b.kv_indptr),
+            _lib.ptr(b.last_page_len),
+            self.capture_batch_size,
+            self.token_capacity,
+            self.index_capacity,
+            self.page_size,
+            self.num_qo_heads,
+            self.num_kv_heads,
+            self.head_dim,
+            _lib.ptr(self.workspace),
+            self.workspace.numel(),
+            _lib.stream(self.device),
+        )
+        self.metadata = metadata
+
+    def select_layer(self, index: int) -> None:
+        if not 0 <= index < self.storage.shape[0]:
+            raise IndexError("Talker layer index exceeds paged KV storage")
+        self._layer_index = index
+
+    # -- attention ----------------------------------------------------------
+    def attend(self, attention: object, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+        tokens, hq, d = query.shape
+        if tokens != self.token_capacity or hq != self.num_qo_heads or d != self.head_dim:
+            raise ValueError("Talker query shape does not match the captured binding")
+        if key.shape != value.shape or key.shape != (tokens, self.num_kv_heads, d):
+            raise ValueError("Qwen3-TTS QKV shapes are incompatible")
+        if not (query.dtype == key.dtype == value.dtype == self.storage.dtype == torch.bfloat16):
+            raise TypeError("paired QKV paged staging requires bf16 q, k, v and cache")
+        if any(t.stride(-1) != 1 for t in (query, key, value)):
+            raise ValueError("QKV and paged cache must be contiguous per head")
+        qw, kw = attention.q_norm.weight, attention.k_norm.weight
+        if qw.dtype != torch.bfloat16 or kw.dtype != torch.bfloat16:
+            raise TypeError("QK norm weights must be bf16")
+        layer = self.storage[self._layer_index]
+        b = self.buffers
+        stream = _lib.stream(self.device)
+        _lib.call(
+            "nq_qk_norm_rope_kv_write",
+            query.data_ptr(), query.stride(0), query.stride(1),
+            key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1),
+            qw.data_ptr(), kw.data_ptr(),
+            b.position_ids.data_ptr(), 1, tokens, hq, self.num_kv_heads, d,
+            float(attention.q_norm.variance_epsilon), float(attention.rope_theta), 1,
+            layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
+            b.write_pages.data_ptr(), b.write_offsets.data_ptr(), 0, stream,
+        )
+        out = self.output
+        _lib.call(
+            "nq_paged_attention",
+            query.data_ptr(), query.stride(0), query.stride(1),
+            layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
+            layer.shape[0], b.kv_indptr.data_ptr(), b.kv_indices.data_ptr(),
+            self.page_size, hq, self.num_kv_heads, d, float(d) ** -0.5,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            self.token_capacity, self.index_capacity, self.workspace.data_ptr(), self.workspace.numel(),
+            self.attention_status.data_ptr(), stream,
+        )
+        return out
+
+    @staticmethod
+    def advance_sequence_lengths() -> None:
+        # The Engine owns committed lengths; replay only proposes a publication.
+        return None
+
+
+class HipPrefillBinding(_HipBindingBase):
+    prefill = True
+
+
+class HipDecodeBinding(_HipBindingBase):
+    prefill = False
+
+
+class _Staging:
+    """Ring of pinned host rows -> device rows for the planner's inputs."""
+
+    FIELDS = 5  # seq_len, pos_start, advance, prior_pages, table_row
+
+    def __init__(self, rows: int, device, depth: int = 4) -> None:
+        self.rows = rows
+        self.host = [torch.zeros((self.FIELDS, rows), dtype=torch.int32, pin_memory=True) for _ in range(depth)]
+        self.dev = [torch.zeros((self.FIELDS, rows), dtype=torch.int32, device=device) for _ in range(depth)]
+        self.events = [None] * depth
+        self.next = 0
+
+    def stage(self, values: list[list[int]]):
+        i = self.next
+        self.next = (i + 1) % len(self.host)
+        if self.events[i] is not None:
+            self.events[i].synchronize()
+        host = self.host[i]
+        n = len(values[0])
+        host[:, :n] = torch.tensor(values, dtype=torch.int32)
+        self.dev[i][:, :n].copy_(host[:, :n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events[i] = ev
+        return self.dev[i]
+
+
+class PagedTalkerKV:
+    """Request state, device page tables and one HIP binding per captured slot."""
+
+    def __init__(
+        self,
+        *,
+        num_layers: int,
+        num_kv_heads: int,
+        num_qo_heads: int,
+        head_dim: int,
+        total_pages: int,
+        page_size: int,
+        scratch_page_count: int,
+        workspace_bytes: int,
+        device: torch.device,
+        dtype: torch.dtype,
+        binding_factory=None,
+    ) -> None:
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("PagedTalkerKV runs on the GPU only (HIP kernels, no CPU path)")
+        if dtype != torch.bfloat16:
+            raise TypeError("paged talker KV stores bf16")
+        if page_size < 1 or page_size & (page_size - 1):
+            raise ValueError("page_size must be a power of two")
+        _lib.load()
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.num_qo_heads = num_qo_heads
+        self.head_dim = head_dim
+        self.total_pages = total_pages
+        self.page_size = page_size
+        self.workspace_bytes = workspace_bytes
+        self.device = device
+        self.dtype = dtype
+        self.storage = torch.zeros(
+            (num_layers, total_pages, 2, page_size, num_kv_heads, head_dim), dtype=dtype, device=device
+        )
+        self.allocator = PagedKVAllocator(total_pages=total_pages, page_size=page_size)
+        self._scratch_pages = self.allocator.claim_scratch_pages(scratch_page_count)
+        self._scratch_dev = torch.tensor(self._scratch_pages, dtype=torch.int32, device=device)
+        self._binding_factory = binding_factory
+        self._next_capture = 0
+        self._capture_requests: dict[int, tuple[str, ...]] = {}
+        # Device page table: one row of page ids per live request.
+        self._max_pages_per_request = total_pages
+        self._table = torch.zeros((64, self._max_pages_per_request), dtype=torch.int32, device=device)
+        self._table_row: dict[str, int] = {}
+        self._free_rows: list[int] = list(range(63, -1, -1))
+        # Device copy of the sorted free list and how much of its front is consumed.
+        self._free_dev = torch.zeros(max(total_pages, 1), dtype=torch.int32, device=device)
+        self._free_host = torch.zeros(max(total_pages, 1), dtype=torch.int32, pin_memory=True)
+        self._free_upload_event: torch.cuda.Event | None = None
+        self._free_epoch = -1
+        self._free_count = 0
+        self._free_head = 0
+        self._staging: _Staging | None = None
+
+    # -- request lifecycle ----------------------------------------------------
+    def add_request(self, request_id: str) -> None:
+        self.allocator.add_request(request_id)
+        if not self._free_rows:
+            old = self._table
+            grown = torch.zeros((old.shape[0] * 2, old.shape[1]), dtype=torch.int32, device=self.device)
+            grown[: old.shape[0]].copy_(old)
+            self._table = grown
+            self._free_rows = list(range(grown.shape[0] - 1, old.shape[0] - 1, -1))
+        self._table_row[request_id] = self._free_rows.pop()
+
+    def remove_request(self, request_id: str) -> None:
+        self.allocator.remove_request(request_id)
+        self._free_rows.append(self._table_row.pop(request_id))
+
+    def state(self, request_id: str) -> RequestKVState:
+        return self.allocator.state(request_id)
+
+    def adopt_request(self, request_id: str, pages, sequence_length: int, position_start: int | None = None) -> None:
+        """Give a live request committed KV on ``pages`` (benchmark and test setup)."""
+
+        pages = tuple(int(p) for p in pages)
+        self.allocator.adopt(
+            request_id, pages, sequence_length, sequence_length if position_start is None else position_start
+        )
+        row = self._table_row[request_id]
+        if pages:
+            self._table[row, : len(pages)].copy_(torch.tensor(pages, dtype=torch.int32))
+
+    # -- bindings -----------------------------------------------------------
+    def _binding(self, key, slot: int):
+        prefill = hasattr(key, "token_capacity")
+        factory = self._binding_factory or (HipPrefillBinding if prefill else HipDecodeBinding)
+        arguments = dict(
+            storage=self.storage,
+            capture_batch_size=key.capture_batch_size,
+            token_capacity=key.token_capacity if prefill else key.capture_batch_size,
+            num_qo_heads=self.num_qo_heads,
+            num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim,
+            page_size=self.page_size,
+            total_pages=self.total_pages,
+            device=self.device,
+            dtype=self.dtype,
+        )
+        if self._binding_factory is not None:
+            arguments.update(slot=slot, metadata=None)
+        return factory(**arguments)
+
+    def create_prefill(self, key, *, slot: int):
+        return self._binding(key, slot)
+
+    def create_decode(self, key, *, slot: int):
+        return self._binding(key, slot)
+
+    @staticmethod
+    def _set_metadata(context: object, metadata: TalkerAttentionMetadata) -> None:
+        if isinstance(context, dict):
+            context["metadata"] = metadata
+        else:
+            context.plan(metadata)
+
+    def _validate_scratch_capacity(self, *, capture_rows: int, token_capacity: int) -> None:
+        if capture_rows > len(self._scratch_pages):
+            raise ValueError("Talker CUDA Graph rows exceed executor-private scratch pages")
+        if token_capacity > len(self._scratch_pages) * self.page_size:
+            raise ValueError("Talker token capacity exceeds executor-private scratch slots")
+
+    def _sync_free_list(self) -> None:
+        if self.allocator.free_list_epoch == self._free_epoch:
+            return
+        free = self.allocator.free_list()
+        if self._free_upload_event is not None:
+            self._free_upload_event.synchronize()
+        n = len(free)
+        if n:
+            self._free_host[:n] = torch.tensor(free, dtype=torch.int32)
+            self._free_dev[:n].copy_(self._free_host[:n], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            self._free_upload_event = ev
+        self._free_epoch = self.allocator.free_list_epoch
+        self._free_count = n
+        self._free_head = 0
+
+    def _metadata(
+        self,
+        *,
+        request_ids: tuple[str, ...],
+        advances: tuple[int, ...],
+        capture_rows: int,
+        token_capacity: int,
+        prefill: bool,
+        context: object,
+        reuse_attention_plan: bool = True,
+    ) -> tuple[tuple[PendingKVPublication, ...], TalkerAttentionMetadata]:
+        self._validate_scratch_capacity(capture_rows=capture_rows, token_capacity=token_capacity)
+        if len(request_ids) > capture_rows:
+            raise ValueError("Talker request rows do not fit the capture")
+        if sum(advances) + (0 if prefill else capture_rows - len(request_ids)) > token_capacity:
+            raise ValueError("Talker KV metadata exceeds the captured token capacity")
+        self._sync_free_list()
+        priors = [self.state(rid) for rid in request_ids]
+        reservation = self.allocator.reserve(request_ids, advances)
+        publications = reservation.publications
+        try:
+            if isinstance(context, _HipBindingBase):
+                buffers = context.buffers
+            else:
+                buffers = _MetadataBuffers(
+                    rows=capture_rows,
+                    tokens=token_capacity,
+                    index_capacity=self.total_pages + capture_rows,
+                    prefill=prefill,
+                    device=self.device,
+                )
+            if self._staging is None or self._staging.rows < capture_rows:
+                self._staging = _Staging(max(capture_rows, 64), self.device)
+            rows = self._staging.stage(
+                [
+                    [p.sequence_length for p in priors],
+                    [p.position_start for p in priors],
+                    list(advances),
+                    [len(p.page_indices) for p in priors],
+                    [self._table_row[rid] for rid in request_ids],
+                ]
+            )
+            free_view = self._free_dev[self._free_head :]
+            _lib.call(
+                "nq_plan_ragged",
+                rows[0].data_ptr(), rows[1].data_ptr(), rows[2].data_ptr(), rows[3].data_ptr(),
+                rows[4].data_ptr(), len(request_ids), capture_rows, token_capacity, self.page_size,
+                int(prefill), self._table.data_ptr(), self._table.stride(0),
+                free_view.data_ptr(), self._free_count - self._free_head,
+                self._scratch_dev.data_ptr(), len(self._scratch_pages),
+                _lib.ptr(buffers.qo_indptr), buffers.kv_indptr.data_ptr(), buffers.kv_indices.data_ptr(),
+                buffers.kv_indices.numel(), buffers.last_page_len.data_ptr(),
+                buffers.position_ids.data_ptr(), buffers.write_pages.data_ptr(),
+                buffers.write_offsets.data_ptr(), buffers.status.data_ptr(), 0, _lib.stream(self.device),
+            )
+            self._free_head += reservation.pages_taken
+            total_pages = sum(len(p.page_indices) for p in publications) + (capture_rows - len(request_ids))
+            metadata = TalkerAttentionMetadata(
+                qo_indptr=buffers.qo_indptr,
+                paged_kv_indptr=buffers.kv_indptr,
+                paged_kv_indices=buffers.kv_indices[:total_pages],
+                paged_kv_last_page_len=buffers.last_page_len,
+                position_ids=buffers.position_ids,
+                write_pages=buffers.write_pages,
+                write_offsets=buffers.write_offsets,
+                padding_pages=self._scratch_pages,
+                reuse_attention_plan=reuse_attention_plan,
+            )
+            return publications, metadata
+        except Exception:
+            self.abort(publications)
+            raise
+
+    def prepare_prefill(self, context, key, request_ids, sequence_lengths):
+        if len(request_ids) != len(sequence_lengths) or len(request_ids) > key.capture_batch_size:
+            raise ValueError("Talker prefill request rows do not fit the capture")
+        if sum(sequence_lengths) > key.token_capacity:
+            raise ValueError("Talker prefill tokens exceed the capture")
+        publications, metadata = self._metadata(
+            request_ids=tuple(request_ids),
+            advances=tuple(sequence_lengths),
+            capture_rows=key.capture_batch_size,
+            token_capacity=key.token_capacity,
+            prefill=True,
+            context=context,
+        )
+        try:
+            self._set_metadata(context, metadata)
+        except Exception:
+            self.abort(publications)
+            raise
+        return publications
+
+    def prepare_decode(self, context, key, request_ids, *, reuse_attention_plan: bool = True):
+        if not request_ids or len(request_ids) > key.capture_batch_size:
+            raise ValueError("Talker decode request rows do not fit the capture")
+        publications, metadata = self._metadata(
+            request_ids=tuple(request_ids),
+            advances=(1,) * len(request_ids),
+            capture_rows=key.capture_batch_size,
+            token_capacity=key.capture_batch_size,
+            prefill=False,
+            context=context,
+            reuse_attention_plan=reuse_attention_plan,
+        )
+        try:
+            self._set_metadata(context, metadata)
+        except Exception:
+            self.abort(publications)
+            raise
+        return publications
+
+    def prepare_capture(self, context, key):
+        capture_id = self._next_capture
+        self._next_capture += 1
+        request_ids = tuple(f"__hip_capture_{capture_id}_{row}__" for row in range(key.capture_batch_size))
+        for rid in request_ids:
+            self.add_request(rid)
+        self._capture_requests[id(context)] = request_ids
+        if not hasattr(key, "token_capacity"):
+            return self.prepare_decode(context, key, request_ids)
+        base, extra = divmod(key.token_capacity, key.capture_batch_size)
+        lengths = tuple(base + (1 if row < extra else 0) for row in range(key.capture_batch_size))
+        return self.prepare_prefill(context, key, request_ids, lengths)
+
+    def finish_capture(self, context, publications) -> None:
+        self.abort(publications)
+        for rid in self._capture_requests.pop(id(context), ()):
+            self.remove_request(rid)
+
+    @staticmethod
+    def abort(publications) -> None:
+        for publication in publications:
+            publication.discard()
+
+
+__all__ = [
+    "HipDecodeBinding",
+    "HipPrefillBinding",
+    "PagedTalkerKV",
+    "TalkerAttentionMetadata",
+]

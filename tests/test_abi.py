@@ -1,0 +1,65 @@
+"""The C-ABI library loads and exports every entry point include/nq_abi.h declares (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nq_abi.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(nq_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_and_binding_agree(nq):
+    from nari_qwen3_tts_amd import _lib
+
+    assert _declared() == set(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(nq):
+    from nari_qwen3_tts_amd import _lib
+
+    if not _lib.LIBRARY_PATH.exists():
+        pytest.fail("libnq_hip.so is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(_lib.LIBRARY_PATH))
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_host_side_metadata_queries_need_no_gpu(nq):
+    from nari_qwen3_tts_amd import _lib
+
+    lib = _lib.load()
+    assert lib.nq_abi_version() == 1
+    assert _lib.status_string(-4) == "not enough free KV pages"
+    assert lib.nq_attention_workspace_bytes(64, 32832, 16, 16, 8, 128) > 0
+    assert lib.nq_attention_workspace_bytes(0, 1, 16, 16, 8, 128) == -1
+
+
+def test_argument_errors_are_caught_on_the_host(nq):
+    """Invalid shapes return NQ_ERR_* before anything is launched."""
+
+    from nari_qwen3_tts_amd import _lib
+
+    lib = _lib.load()
+    # capture rows above the single-workgroup limit
+    assert lib.nq_plan_ragged(*([None] * 5), 1, 2048, 1, 16, 0, None, 1, None, 0, None, 2048, None, None, None, 0,
+                              None, None, None, None, None, 0, None) == -2
+    # vocabulary above the sampler's LDS budget
+    assert lib.nq_sample(1, 0, 8192, 1, 8192, 1, 1, 1, None, None, 0, 1, 8192, -1, None, 0, 1, None) == -2
+    with pytest.raises(TypeError):
+        _lib.check(-2, "x")
+    with pytest.raises(ValueError):
+        _lib.check(-1, "x")
+    from nari_qwen3_tts_amd.errors import KVAllocationError
+
+    with pytest.raises(KVAllocationError):
+        _lib.check(-4, "x")

@@ -1,0 +1,94 @@
+"""HIP q/k RoPE, norm and SwiGLU kernels vs the oracle and torch fp32 references."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import to_np
+from oracle import norms as o_norms
+from oracle import qk_rope as o_rope
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("d,round_to_input", [(128, True), (64, False), (64, True)])
+def test_qk_norm_rope_dense_cache_and_no_cache(nq, device, d, round_to_input):
+    from nari_qwen3_tts_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(d)
+    rows, hq, hkv = 37, 16, 8
+    qkv = torch.randn(rows, (hq + 2 * hkv) * d, generator=g, device=device).to(torch.bfloat16)
+    q = qkv[:, : hq * d].view(rows, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(rows, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(rows, hkv, d)
+    qw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, 4096, (rows, 16), generator=g, device=device)
+    q0, k0, v0 = to_np(q), to_np(k), to_np(v)
+    col = pos[:, 5]
+    if round_to_input:
+        kernels.paired_qk_norm_rope_(q, k, qw, kw, col, 1e-6, 1e6)
+    else:
+        cache = torch.zeros(rows, 2, 16, hkv, d, dtype=torch.bfloat16, device=device)
+        kernels.paired_qk_norm_rope_dense_cache_(q, k, v, qw, kw, col, 1e-6, 1e6, cache[:, 0], cache[:, 1], 5)
+    torch.cuda.synchronize()
+    p = to_np(col)
+    np.testing.assert_allclose(to_np(q), o_rope.norm_rope(q0, to_np(qw), p, 1e-6, 1e6, round_to_input), atol=2e-2, rtol=1e-2)
+    np.testing.assert_allclose(to_np(k), o_rope.norm_rope(k0, to_np(kw), p, 1e-6, 1e6, round_to_input), atol=2e-2, rtol=1e-2)
+    if not round_to_input:
+        np.testing.assert_array_equal(to_np(cache[:, 0, 5]), to_np(k))
+        np.testing.assert_array_equal(to_np(cache[:, 1, 5]), v0)
+        assert torch.count_nonzero(cache[:, :, :5]) == 0 and torch.count_nonzero(cache[:, :, 6:]) == 0
+
+
+def test_paged_cache_variant_writes_pages(nq, device):
+    from nari_qwen3_tts_amd import kernels
+
+    g = torch.Generator(device=device)
+    g.manual_seed(3)
+    rows, hq, hkv, d, pages, ps = 20, 16, 8, 128, 64, 16
+    q = torch.randn(rows, hq, d, generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn(rows, hkv, d, generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn(rows, hkv, d, generator=g, device=device).to(torch.bfloat16)
+    w = torch.ones(d, dtype=torch.bfloat16, device=device)
+    layer = torch.zeros(pages, 2, ps, hkv, d, dtype=torch.bfloat16, device=device)
+    wp = torch.randperm(pages, generator=g, device=device)[:rows]
+    wo = torch.randint(0, ps, (rows,), generator=g, device=device)
+    pos = torch.zeros(rows, dtype=torch.long, device=device)  # position 0: identity rotation
+    q0, k0, v0 = to_np(q), to_np(k), to_np(v)
+    kernels.paired_qk_norm_rope_paged_cache_(q, k, v, w, w, pos, 1e-6, 1e6, layer, wp, wo)
+    torch.cuda.synchronize()
+    want_k = o_rope.norm_rope(k0, np.ones(d, np.float32), np.zeros(rows), 1e-6, 1e6, True)
+    np.testing.assert_allclose(to_np(k), want_k, atol=1e-2, rtol=1e-2)
+    want = o_rope.paged_write(np.zeros(layer.shape, np.float32), to_np(k), v0, to_np(wp), to_np(wo))
+    np.testing.assert_array_equal(to_np(layer), want)
+
+
+def test_add_rmsnorm_rmsnorm_silu(nq, device):
+    from nari_qwen3_tts_amd.layers import qwen3_tts_add_rmsnorm, qwen3_tts_rmsnorm, qwen3_tts_silu_and_mul
+
+    g = torch.Generator(device=device)
+    g.manual_seed(0)
+    rows, width = 64, 2048
+    hidden = torch.randn(rows, width, generator=g, device=device).to(torch.bfloat16)
+    residual = torch.randn(rows, width, generator=g, device=device).to(torch.bfloat16)
+    weight = (torch.rand(width, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    h0, r0 = to_np(hidden), to_np(residual)
+    qwen3_tts_add_rmsnorm(hidden, residual, weight, 1e-6)
+    want_h, want_r = o_norms.add_rmsnorm(h0, r0, to_np(weight), 1e-6)
+    np.testing.assert_array_equal(to_np(residual), want_r)
+    np.testing.assert_allclose(to_np(hidden), want_h, atol=2e-2, rtol=1e-2)
+    # torch fp32 reference of RMSNorm (model/layers.py:110-115)
+    x = torch.randn(rows, width, generator=g, device=device).to(torch.bfloat16)
+    out = qwen3_tts_rmsnorm(x, weight, 1e-6)
+    xf = x.float()
+    ref = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + 1e-6) * weight.float()).to(torch.bfloat16)
+    assert (out.float() - ref.float()).abs().max().item() <= 2e-2
+    gu = torch.randn(rows, 2 * 6144, generator=g, device=device).to(torch.bfloat16)
+    act = qwen3_tts_silu_and_mul(gu)
+    gf, uf = gu.float().chunk(2, dim=-1)
+    ref = torch.nn.functional.silu(gf) * uf
+    assert (act.float() - ref).abs().max().item() <= 3e-2
