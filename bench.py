@@ -1,0 +1,295 @@
+"""Talker decode-step benchmark on one MI355X (batch 64, 28 layers, paged KV).
+
+Workload (the serving metric's configuration): random-init Qwen3-style talker,
+28 layers, hidden 2048, 16 query / 8 KV heads of dim 128, SwiGLU 6144, vocab
+3072, bf16; 64 decode rows with prior KV lengths U[64, 2048]; page size 16;
+every page of every sequence drawn from a random permutation of a 32768-page
+pool filled with N(0,1) bf16 K/V.  One step = GPU metadata planning for the
+64 rows (ragged page table + attention plan) + one hipGraph replay of the
+forward (28 x [norm, QKV GEMM, q/k norm+RoPE+paged KV write, paged attention,
+o-proj, add-norm, SwiGLU MLP, add-norm], codec head, Philox uniforms, fused
+sampler with masks / repetition penalty / top-k 50 / top-p 0.95 / T 0.9 and
+seen-mask update) + publishing the KV of the new token.  Sequences grow by one
+token per step.
+
+Prints one JSON line: tok/s over the timed steps, the paged-attention kernel's
+achieved HBM bandwidth against the 8 TB/s peak (``roofline``), and the CPU
+oracle on a bounded sample of the same step (``cpu_baseline``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+ROWS = 64
+PAGE_SIZE = 16
+POOL_PAGES = 32768
+KV_LO, KV_HI = 64, 2048
+SEED = 1002
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class DecodeKey:
+    def __init__(self, capture_batch_size: int) -> None:
+        self.capture_batch_size = capture_batch_size
+
+
+def build_workload(torch, np):
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
+    from nari_qwen3_tts_amd.talker import TalkerConfig, TalkerDecodeStep, TalkerWeights
+    from nari_qwen3_tts_amd.talker_kv import PagedTalkerKV
+
+    dev = torch.device("cuda:0")
+    cfg = TalkerConfig()
+    t0 = time.perf_counter()
+    kv = PagedTalkerKV(
+        num_layers=cfg.num_layers, num_kv_heads=cfg.num_kv_heads, num_qo_heads=cfg.num_qo_heads,
+        head_dim=cfg.head_dim, total_pages=POOL_PAGES, page_size=PAGE_SIZE, scratch_page_count=ROWS,
+        workspace_bytes=0, device=dev, dtype=torch.bfloat16,
+    )
+    g = torch.Generator(device=dev)
+    g.manual_seed(SEED)
+    for layer in range(cfg.num_layers):
+        kv.storage[layer].normal_(generator=g)
+    weights = TalkerWeights(cfg, dev, seed=SEED)
+    key = DecodeKey(ROWS)
+    ctx = kv.create_decode(key, slot=0)
+    step = TalkerDecodeStep(weights, ctx, ROWS, use_counter_rng=True)
+    # Sampling state: the reference defaults T 0.9, top-k 50, top-p 0.95, penalty 1.05 over a 64-token history.
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(SEED)
+    step.temperature.fill_(0.9)
+    step.top_k.fill_(50)
+    step.top_p.fill_(0.95)
+    step.penalty.fill_(1.05)
+    step.seed.copy_(torch.arange(ROWS, dtype=torch.long) * 7919 + 17)
+    step.offsets.copy_(torch.arange(ROWS, dtype=torch.long) * 0 + 512)
+    hist = torch.randint(0, cfg.codec_vocab, (ROWS, 64), generator=gen)
+    seen = torch.zeros(ROWS, cfg.vocab, dtype=torch.bool)
+    seen.scatter_(1, hist, True)
+    step.seen.copy_(seen)
+    step.step_embed.copy_((torch.randn(ROWS, cfg.hidden, generator=gen) * 0.5).to(torch.bfloat16))
+    step.text_ids.copy_(torch.randint(0, cfg.text_vocab, (ROWS,), generator=gen))
+
+    # Capture with executor-private requests (PagedTalkerKV.prepare_capture), as the reference does.
+    publications = kv.prepare_capture(ctx, key)
+    driver = HipGraphCaptureDriver(device=dev)
+    call = driver.capture(step.forward)
+    kv.finish_capture(ctx, publications)
+
+    rng = np.random.default_rng(SEED)
+    lengths = rng.integers(KV_LO, KV_HI + 1, size=ROWS)
+    pool = rng.permutation(np.asarray(kv.allocator.free_list()))
+    rids, at = [], 0
+    for i, n in enumerate(lengths):
+        rid = f"req{i}"
+        kv.add_request(rid)
+        need = -(-int(n) // PAGE_SIZE)
+        kv.adopt_request(rid, pool[at : at + need], int(n))
+        at += need
+        rids.append(rid)
+    torch.cuda.synchronize()
+    log(f"setup {time.perf_counter() - t0:.1f}s; weights {weights.weight_bytes() / 1e9:.3f} GB")
+    return dict(cfg=cfg, kv=kv, ctx=ctx, step=step, call=call, rids=tuple(rids), key=key, weights=weights)
+
+
+def run_step(w):
+    pubs = w["kv"].prepare_decode(w["ctx"], w["key"], w["rids"])
+    w["call"].replay()
+    w["step"].offsets.add_(512)
+    for p in pubs:
+        p.publish()
+
+
+def kv_tokens(w) -> int:
+    return sum(w["kv"].state(r).sequence_length for r in w["rids"])
+
+
+def attention_probe(torch, w, replays: int = 20):
+    """Average duration of the paged-attention kernel: a graph of its 28 layer launches, timed with events."""
+
+    kv, ctx, cfg = w["kv"], w["ctx"], w["cfg"]
+    pubs = kv.prepare_decode(ctx, w["key"], w["rids"])  # metadata for one more token per row
+    q = torch.randn(ROWS, cfg.num_qo_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
+    def launches():
+        for layer_index in range(cfg.num_layers):
+            ctx.run_attention(q, layer_index)
+
+    from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
+
+    call = HipGraphCaptureDriver(device=q.device).capture(launches)
+    tokens_per_launch = sum(kv.state(r).sequence_length + 1 for r in w["rids"])
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    call.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        call.replay()
+    end.record(stream)
+    end.synchronize()
+    avg_ms = start.elapsed_time(end) / (replays * cfg.num_layers)
+    kv.abort(pubs)
+    status = int(ctx.attention_status.item())
+    if status != 0:
+        raise RuntimeError(f"attention status {status}")
+    bytes_per_launch = tokens_per_launch * cfg.num_kv_heads * cfg.head_dim * 2 * 2  # K and V, bf16
+    return avg_ms, bytes_per_launch, tokens_per_launch
+
+
+def cpu_baseline(torch, np, w, budget_s: float = 12.0):
+    """The oracle decode step on the host cores: as many of the 28 layers as fit the budget, scaled to 28."""
+
+    from oracle import bf16 as o_bf16
+    from oracle import planner as o_plan
+    from oracle import talker as o_talker
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # noqa: BLE001 - threadpoolctl is optional
+        cores = 1
+    kv, cfg, step, wts = w["kv"], w["cfg"], w["step"], w["weights"]
+    states = [kv.state(r) for r in w["rids"]]
+    # compact copy of the pages the rows own (+ one new page per row if needed)
+    alloc = o_plan.Allocator(POOL_PAGES, PAGE_SIZE)
+    alloc.free = list(kv.allocator.free_list())
+    rows, pages_used = [], []
+    for s in states:
+        need = -(-(s.sequence_length + 1) // PAGE_SIZE)
+        pages = list(s.page_indices) + alloc.free[: need - len(s.page_indices)]
+        del alloc.free[: need - len(s.page_indices)]
+        rows.append((s.sequence_length, s.position_start, pages))
+        pages_used.extend(pages)
+    remap = {p: i for i, p in enumerate(pages_used)}
+    scratch = list(range(len(pages_used), len(pages_used) + ROWS))
+    meta = o_plan.metadata([(a, b, [remap[p] for p in pg]) for a, b, pg in rows], [1] * ROWS, capture_rows=ROWS,
+                           token_capacity=ROWS, prefill=False, page_size=PAGE_SIZE, scratch_pages=scratch)
+    idx = torch.tensor(pages_used, dtype=torch.long, device="cuda")
+
+    def host(t):
+        return o_bf16.from_bits(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+
+    residual = o_bf16.round_f32(host(step.step_embed) + host(wts.text_embedding[step.text_ids]))
+    cfgd = dict(num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
+                rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta)
+    done = 0
+    elapsed = 0.0
+    for li in range(cfg.num_layers):
+        L = wts.layers[li]
+        layer_np = dict(input_norm=host(L.input_norm), qkv=host(L.qkv), o=host(L.o), post_norm=host(L.post_norm),
+                        gate_up=host(L.gate_up), down=host(L.down), q_norm=host(L.attention.q_norm.weight),
+                        k_norm=host(L.attention.k_norm.weight))
+        nxt = host(wts.final_norm) if li + 1 == cfg.num_layers else host(wts.layers[li + 1].input_norm)
+        cache = np.zeros((1, len(pages_used) + ROWS, 2, PAGE_SIZE, cfg.num_kv_heads, cfg.head_dim), dtype=np.float32)
+        cache[0, : len(pages_used)] = host(kv.storage[li].index_select(0, idx))
+        t0 = time.perf_counter()
+        _, residual = o_talker.decode_layers([layer_np], cfgd, residual, cache, meta, range(0, 1), final_norm=nxt)
+        elapsed += time.perf_counter() - t0
+        done += 1
+        if elapsed >= budget_s:
+            break
+    step_s = elapsed / done * cfg.num_layers
+    return dict(value=ROWS / step_s, unit="tok/s", cores=int(cores), kind="port",
+                sample=f"oracle decode step (numpy) over {done} of {cfg.num_layers} layers for {ROWS} rows, "
+                       f"{elapsed:.1f}s, scaled to {cfg.num_layers} layers")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the serving path shards by independent request rows with no "
+              "per-step exchange, and this build has no multi-GPU leg (use --gpus 1).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    w = build_workload(torch, np)
+    for _ in range(args.warmup):
+        run_step(w)
+    torch.cuda.synchronize()
+    kv_before = kv_tokens(w)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_step(w)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kv_after = kv_tokens(w)
+    ms = elapsed * 1000.0 / args.steps
+    tok_s = ROWS * args.steps / elapsed
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step, {tok_s:.0f} tok/s")
+
+    avg_ms, bytes_per_launch, tokens_per_launch = attention_probe(torch, w)
+    achieved = bytes_per_launch / (avg_ms / 1e3) / 1e9
+    log(f"paged attention: {avg_ms * 1e3:.1f} us/launch over {tokens_per_launch} KV tokens -> {achieved:.0f} GB/s")
+    cfg = w["cfg"]
+    mean_kv = (kv_before + kv_after) / 2 / ROWS + 1
+    step_bytes = (ROWS * mean_kv * cfg.num_kv_heads * cfg.head_dim * 4 * cfg.num_layers + w["weights"].weight_bytes())
+
+    result = {
+        "metric": "talker decode-step tok/s at batch 64 (+ paged-attn HBM GB/s vs peak)",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, N(0,1) KV pool, random page permutation)",
+        "config": {
+            "workload": "talker decode step: 28 layers, hidden 2048, 16q/8kv heads x 128, SwiGLU 6144, vocab 3072, "
+                        "batch 64, KV lens U[64,2048], page size 16, 32768-page permuted pool",
+            "global_batch": ROWS,
+            "seq_len": f"U[{KV_LO},{KV_HI}] prior KV",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "nq_paged_attention: paged_stream_kernel<128,2> + merge_stream_kernel<128,2>",
+            "bytes_per_launch": bytes_per_launch,
+            "us_per_launch": round(avg_ms * 1e3, 2),
+        },
+        "step_roofline": {
+            "algorithmic_bytes": int(step_bytes),
+            "achieved_GBps": round(step_bytes / (ms / 1e3) / 1e9, 1),
+            "frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, np, w)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

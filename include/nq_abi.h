@@ -72,20 +72,23 @@ int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start, const int32
  * Work decomposition for nq_paged_attention, computed on the GPU from the
  * ragged metadata.  Replaces the host-side plan() of the FlashInfer wrappers
  * (executor/talker_kv.py:175-223 prefill, :259-303 decode).
- * qo_indptr may be NULL (pure decode: row r owns query r).  Each query token
- * gets its causal key range (bottom-right aligned: query i of a row with
- * qo_len queries sees keys < kv_len - qo_len + i + 1) split into chunks whose
- * size the plan picks on the GPU from the total work.  Writes into
- * `workspace` (size from nq_attention_workspace_bytes for the same maxima) and
- * clears the merge counters it holds.  max_pages bounds the pages of all rows
- * together.
+ * qo_indptr may be NULL (pure decode: row r owns query r).  Rows with one
+ * query become 16-token key blocks (page id resolved from kv_indices) that
+ * the attention launch splits evenly over its waves; rows with several
+ * queries get, per query, its causal key range (bottom-right aligned: query i
+ * of a row with qo_len queries sees keys < kv_len - qo_len + i + 1) split
+ * into chunks whose size the plan picks on the GPU from the total work.
+ * Writes into `workspace` (size from nq_attention_workspace_bytes for the same
+ * maxima).  max_pages bounds the pages of all rows together (the length of
+ * kv_indices).
  */
 int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pages, int page_size,
                                      int num_qo_heads, int num_kv_heads, int head_dim);
 int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
-                      const int32_t *last_page_len, int n_rows, int max_query_tokens,
-                      int max_pages, int page_size, int num_qo_heads, int num_kv_heads,
-                      int head_dim, void *workspace, int64_t workspace_bytes, void *stream);
+                      const int32_t *last_page_len, const int32_t *kv_indices, int n_rows,
+                      int max_query_tokens, int max_pages, int page_size, int num_qo_heads,
+                      int num_kv_heads, int head_dim, void *workspace, int64_t workspace_bytes,
+                      void *stream);
 
 /*
  * Paged GQA attention for mixed decode (qo_len == 1) and causal prefill
@@ -98,16 +101,17 @@ int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
  *   (kind 0 = K, 1 = V; the reference layout is [pages, 2, ps, Hkv, D]).
  * out: bf16 [tokens, num_qo_heads, head_dim] with strides (o_s0, o_s1, 1).
  * The plan in `workspace` must come from nq_attention_plan for the same
- * metadata and the same (max_query_tokens, max_pages).  status (device int32, may be NULL) is set to NQ_ERR_INVALID_
+ * metadata and the same (max_query_tokens, max_pages).  prefill_rows = 0
+ * promises the plan holds no row with more than one query (the chunked
+ * prefill kernels are then not launched).  status (device int32, may be NULL) is set to NQ_ERR_INVALID_
  * ARGUMENT when a page id outside [0, num_pages) is met (that page is skipped).
  */
 int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
                        int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
-                       int num_pages, const int32_t *kv_indptr, const int32_t *kv_indices,
-                       int page_size, int num_qo_heads, int num_kv_heads, int head_dim,
-                       float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
-                       int max_query_tokens, int max_pages, void *workspace,
-                       int64_t workspace_bytes, int32_t *status, void *stream);
+                       int num_pages, const int32_t *kv_indices, int page_size, int num_qo_heads,
+                       int num_kv_heads, int head_dim, float sm_scale, uint16_t *out, int64_t o_s0,
+                       int64_t o_s1, int max_query_tokens, int max_pages, int prefill_rows,
+                       void *workspace, int64_t workspace_bytes, int32_t *status, void *stream);
 
 /*
  * Code-predictor short-cache attention: one query per row over the first

@@ -1,14 +1,26 @@
 // Paged GQA attention over the talker's paged KV cache, and the code
 // predictor's dense short-cache attention.
 //
-// Work unit: one (query token, key chunk, kv head) item per workgroup of 4
-// waves.  Each wave streams 16-token blocks of K and V straight from HBM with
-// 128-bit loads (D/8 lanes cover one 256-byte K or V row, so one load
-// instruction moves 1 KiB of a page), keeps an online softmax per lane group
-// and, at the end of the chunk, the waves combine through LDS.  Items of the
-// same query are merged by the workgroup that finishes last (an arrival
-// counter per (query, kv head), reset by that workgroup), so a step needs one
-// launch per layer and no separate reduction kernel.
+// Decode rows (one query) use a stream decomposition: the plan lists every
+// 16-token key block of every decode row (page id, first slot, token count,
+// row and query) and the (kv head, block) units are split into equal
+// contiguous spans, one span per wave.  A wave fetches its span's block
+// descriptors with one coalesced load, then streams K and V with 128-bit loads
+// (D/8 lanes cover one 256-byte row, so one load instruction moves 1 KiB).
+// Every kv head's block list is cut into the same spans and wave i takes span
+// i / Hkv of head i % Hkv, so the waves of one span read the head slices of
+// the same pages at the same time (whole 2 KiB token rows per page).  Register
+// use stays at 128 so four waves per SIMD are resident and the launch's 4096
+// waves cover the chip in one round.  A wave
+// keeps one online softmax per (query, kv head) it touches and writes either
+// the final output (when it saw all of that row's keys) or an fp32 partial;
+// a second launch merges the partials, so no device-wide fence is needed
+// inside the streaming kernel and every wave moves the same number of bytes
+// whatever the length mix of the batch.
+//
+// Causal prefill rows (several queries) are split per query into key chunks
+// of 64..1024 tokens and run by a workgroup-per-chunk kernel with the same
+// inner loop and its own merge.
 //
 // Semantics follow FlashInfer's paged decode/prefill as bound in
 // executor/talker_kv.py:140-306 (scale 1/sqrt(D), fp32 softmax and
@@ -22,41 +34,65 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kWaves = kAttnThreads / kWave;
-constexpr int kBlockTok = 16;        // tokens per wave iteration
-constexpr int kTargetItems = 8192;   // preferred upper bound on chunk items per launch
-constexpr int kPpcCandidates = 14;   // pages per chunk in {1, 2, ..., 8192}
-constexpr int kPlanThreads = 1024;   // rows per plan launch (largest bucket)
+constexpr int kBlockTok = 16;          // tokens per key block
+constexpr int kStreamWaves = 4096;     // upper bound on stream workers per launch
+constexpr bool kStreamDoubleBuffer = false;
+constexpr int kMinBlocksPerWave = 4;   // smaller spans would make merging dominate
+constexpr int kTargetItems = 8192;     // preferred upper bound on prefill chunk items
 constexpr int kMinChunkTokens = 64;
+constexpr int kMaxChunkTokens = 1024;  // also the LDS page-id capacity (page size >= 1)
+constexpr int kPlanThreads = 1024;     // rows per plan launch (largest bucket)
+constexpr int kPlanGrid = 8;
 
-enum MetaSlot { kMetaChunks = 0, kMetaPpc = 1, kMetaStatus = 2, kMetaQueries = 3 };
+enum MetaSlot {
+    kMetaChunks = 0, kMetaChunkTok = 1, kMetaStatus = 2, kMetaQueries = 3,
+    kMetaDecRows = 4, kMetaBlocks = 5
+};
+
+// Prefill chunk descriptor.
+struct alignas(16) ChunkDesc {
+    int query;       // query token index (row of q / out)
+    int page_start;  // index into kv_indices of the chunk's first page
+    int tok_begin;   // first key position of the chunk
+    int tok_end;     // one past its last key position
+    int n_chunks;    // chunks of this query
+    int first_chunk; // index of the query's first chunk
+    int pad0, pad1;
+};
+
+// Decode block descriptor (int4): {page (a kv_indices offset when the page
+// size is below 16), first slot | token count << 24, decode row, query}.
+// Decode row descriptor (int4): {row, query, first block, block count}.
 
 struct PlanLayout {
-    int64_t meta, chunk_indptr, q_row, q_kvlen, counters, part_ml, part_o, total;
-    int64_t max_chunks;
+    int64_t meta, chunk_indptr, desc, part_ml, part_o;
+    int64_t dec_rows, blocks, spart_ml, spart_o, total;
+    int64_t max_chunks, max_blocks, max_slots;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-__host__ __device__ inline int64_t chunk_capacity(int T, int max_pages, int Hkv) {
-    return 2 * static_cast<int64_t>(T) + kTargetItems / Hkv + max_pages / 64 + 64;
-}
-
-__host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int Hq, int Hkv, int D) {
+__host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page_size, int Hq, int Hkv,
+                                                  int D) {
     PlanLayout L;
-    L.max_chunks = chunk_capacity(T, max_pages, Hkv);
+    const int G = Hq / Hkv;
+    L.max_chunks = 2 * static_cast<int64_t>(T) + kTargetItems / Hkv +
+                   static_cast<int64_t>(max_pages) * page_size / kMaxChunkTokens + 64;
+    L.max_blocks = static_cast<int64_t>(max_pages) * (page_size > kBlockTok ? page_size / kBlockTok : 1) + T;
+    L.max_slots = kStreamWaves + static_cast<int64_t>(Hkv) * T;
     int64_t off = 0;
     L.meta = off;         off = align256(off + 8 * 4);
     L.chunk_indptr = off; off = align256(off + (static_cast<int64_t>(T) + 1) * 4);
-    L.q_row = off;        off = align256(off + static_cast<int64_t>(T) * 4);
-    L.q_kvlen = off;      off = align256(off + static_cast<int64_t>(T) * 4);
-    L.counters = off;     off = align256(off + static_cast<int64_t>(T) * Hkv * 4);
+    L.desc = off;         off = align256(off + L.max_chunks * static_cast<int64_t>(sizeof(ChunkDesc)));
     L.part_ml = off;      off = align256(off + L.max_chunks * Hq * 2 * 4);
     L.part_o = off;       off = align256(off + L.max_chunks * Hq * D * 4);
+    L.dec_rows = off;     off = align256(off + static_cast<int64_t>(T) * 16);
+    L.blocks = off;       off = align256(off + L.max_blocks * 16);
+    L.spart_ml = off;     off = align256(off + L.max_slots * G * 2 * 4);
+    L.spart_o = off;      off = align256(off + L.max_slots * G * D * 4);
     L.total = off;
     return L;
 }
-
-__device__ __forceinline__ int ilog2_exact(int x) { return 31 - __clz(x); }
 
 __device__ int plan_block_scan(int v, int *tmp, int *total) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -88,224 +124,282 @@ __device__ int plan_block_scan(int v, int *tmp, int *total) {
     return res;
 }
 
-// One workgroup: per query token its row, causal key count and chunk range.
+// Largest r in [0, n) with off[r] <= x (off non-decreasing, off[0] == 0).
+__device__ __forceinline__ int find_le(const int *off, int n, int x) {
+    int lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= x) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// Every workgroup scans the rows into LDS; workgroup 0 writes the per-row and
+// prefill-chunk tables, all workgroups fill the decode block table.
 __global__ void __launch_bounds__(kPlanThreads)
 attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__restrict__ kv_indptr,
-                      const int32_t *__restrict__ last_page_len, int n_rows, int max_queries,
-                      int page_size, int num_kv_heads, int64_t max_chunks, char *__restrict__ ws,
+                      const int32_t *__restrict__ last_page_len,
+                      const int32_t *__restrict__ kv_indices, int n_rows, int max_queries,
+                      int index_limit, int page_size, int num_kv_heads, char *__restrict__ ws,
                       PlanLayout L) {
     __shared__ int s_qo[kPlanThreads + 1];
     __shared__ int s_kvlen[kPlanThreads];
-    __shared__ unsigned long long s_cand[kPpcCandidates];
+    __shared__ int s_base[kPlanThreads];
+    __shared__ int s_boff[kPlanThreads];
+    __shared__ int s_dec[kPlanThreads];
+    __shared__ unsigned long long s_cand[8];
     __shared__ int s_tmp[kWave + 1];
 
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
     int32_t *chunk_indptr = reinterpret_cast<int32_t *>(ws + L.chunk_indptr);
-    int32_t *q_row = reinterpret_cast<int32_t *>(ws + L.q_row);
-    int32_t *q_kvlen = reinterpret_cast<int32_t *>(ws + L.q_kvlen);
-    int32_t *counters = reinterpret_cast<int32_t *>(ws + L.counters);
+    ChunkDesc *desc = reinterpret_cast<ChunkDesc *>(ws + L.desc);
+    int4 *dec_rows = reinterpret_cast<int4 *>(ws + L.dec_rows);
+    int4 *blocks = reinterpret_cast<int4 *>(ws + L.blocks);
 
     const int tid = threadIdx.x;
+    const bool lead = blockIdx.x == 0;
+    int ps_log2 = 0;
+    while ((1 << ps_log2) < page_size) ++ps_log2;
     if (tid < n_rows) {
         const int np = kv_indptr[tid + 1] - kv_indptr[tid];
         int last = last_page_len[tid];
         last = last < 1 ? 1 : (last > page_size ? page_size : last);  // keys stay inside the row's pages
         s_kvlen[tid] = np > 0 ? (np - 1) * page_size + last : 0;
+        s_base[tid] = kv_indptr[tid];
         s_qo[tid] = qo_indptr ? qo_indptr[tid] : tid;
     }
     if (tid == 0) s_qo[n_rows] = qo_indptr ? qo_indptr[n_rows] : n_rows;
-    if (tid < kPpcCandidates) s_cand[tid] = 0;
+    if (tid < 8) s_cand[tid] = 0;
     __syncthreads();
     const int T = s_qo[n_rows];
-    if (T < 0 || T > max_queries) {
-        if (tid == 0) {
+    auto fail = [&](int code) {
+        if (lead && tid == 0) {
             meta[kMetaChunks] = 0;
-            meta[kMetaPpc] = 1;
-            meta[kMetaStatus] = NQ_ERR_INVALID_ARGUMENT;
+            meta[kMetaChunkTok] = kMinChunkTokens;
+            meta[kMetaStatus] = code;
             meta[kMetaQueries] = 0;
+            meta[kMetaDecRows] = 0;
+            meta[kMetaBlocks] = 0;
         }
+    };
+    if (T < 0 || T > max_queries) {
+        fail(NQ_ERR_INVALID_ARGUMENT);
         return;
     }
 
-    // Causal pages of query q.
-    auto query_pages = [&](int q, int *row_out, int *kvlen_out) {
-        int lo = 0, hi = n_rows;
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (s_qo[mid] <= q) lo = mid; else hi = mid;
+    // Decode rows and their key blocks.
+    int is_dec = 0, nblk = 0;
+    if (tid < n_rows && s_qo[tid + 1] - s_qo[tid] == 1) {
+        is_dec = 1;
+        nblk = (s_kvlen[tid] + kBlockTok - 1) / kBlockTok;
+        nblk = nblk < 1 ? 1 : nblk;
+    }
+    int n_dec, n_blocks;
+    const int dec_idx = plan_block_scan(is_dec, s_tmp, &n_dec);
+    const int boff = plan_block_scan(nblk, s_tmp, &n_blocks);
+    s_dec[tid] = dec_idx;
+    s_boff[tid] = boff;
+    __syncthreads();
+    if (n_blocks > L.max_blocks) {
+        fail(NQ_ERR_CAPACITY);
+        return;
+    }
+    if (lead && is_dec) dec_rows[dec_idx] = make_int4(tid, s_qo[tid], boff, nblk);
+
+    const int gstride = gridDim.x * blockDim.x;
+    for (int b = blockIdx.x * blockDim.x + tid; b < n_blocks; b += gstride) {
+        const int r = find_le(s_boff, n_rows, b);
+        const int tok0 = (b - s_boff[r]) * kBlockTok;
+        int ntok = s_kvlen[r] - tok0;
+        ntok = ntok < 0 ? 0 : (ntok > kBlockTok ? kBlockTok : ntok);
+        int page, slot0;
+        if (page_size >= kBlockTok) {
+            const int at = s_base[r] + (tok0 >> ps_log2);
+            page = (ntok > 0 && at < index_limit) ? kv_indices[at] : -1;
+            slot0 = tok0 & (page_size - 1);
+        } else {
+            page = s_base[r] + (tok0 >> ps_log2);  // kv_indices offset; pages looked up per token
+            slot0 = 0;
         }
+        blocks[b] = make_int4(page, slot0 | (ntok << 24), s_dec[r], s_qo[r]);
+    }
+    if (!lead) return;
+
+    // Prefill queries: key chunks per query.
+    auto query_keys = [&](int q, int *row_out) {
+        const int lo = find_le(s_qo, n_rows, q);
         const int qo_len = s_qo[lo + 1] - s_qo[lo];
         int kvlen = s_kvlen[lo] - qo_len + (q - s_qo[lo]) + 1;
         kvlen = kvlen < 0 ? 0 : (kvlen > s_kvlen[lo] ? s_kvlen[lo] : kvlen);
         *row_out = lo;
-        *kvlen_out = kvlen;
-        return (kvlen + page_size - 1) / page_size;
+        return qo_len > 1 ? kvlen : -1;  // -1: a decode query, served by the stream kernel
     };
-
-    // Pass 1: chunk totals for every candidate chunk size.
-    unsigned long long cand[kPpcCandidates];
+    const int n_cand = 5;  // 64 .. 1024 tokens
+    unsigned long long cand[n_cand];
 #pragma unroll
-    for (int c = 0; c < kPpcCandidates; ++c) cand[c] = 0;
+    for (int c = 0; c < n_cand; ++c) cand[c] = 0;
     for (int q = tid; q < T; q += blockDim.x) {
-        int row, kvlen;
-        const int pages = query_pages(q, &row, &kvlen);
+        int row;
+        const int kvlen = query_keys(q, &row);
+        if (kvlen < 0) continue;
 #pragma unroll
-        for (int c = 0; c < kPpcCandidates; ++c) {
-            const int n = (pages + (1 << c) - 1) >> c;
+        for (int c = 0; c < n_cand; ++c) {
+            int ct = kMinChunkTokens << c;
+            ct = ct < page_size ? page_size : ct;
+            const int n = (kvlen + ct - 1) / ct;
             cand[c] += n > 0 ? n : 1;
         }
     }
 #pragma unroll
-    for (int c = 0; c < kPpcCandidates; ++c) atomicAdd(&s_cand[c], cand[c]);
+    for (int c = 0; c < n_cand; ++c) atomicAdd(&s_cand[c], cand[c]);
     __syncthreads();
-
-    const int min_tokens = kMinChunkTokens > page_size ? kMinChunkTokens : page_size;
-    int ppc_log = 0;
-    while ((page_size << ppc_log) < min_tokens && ppc_log < kPpcCandidates - 1) ++ppc_log;
     int chosen = -1;
-    for (int c = ppc_log; c < kPpcCandidates; ++c)
+    for (int c = 0; c < n_cand; ++c)
         if (s_cand[c] * num_kv_heads <= kTargetItems) { chosen = c; break; }
     if (chosen < 0)
-        for (int c = ppc_log; c < kPpcCandidates; ++c)
-            if (s_cand[c] <= static_cast<unsigned long long>(max_chunks)) { chosen = c; break; }
+        for (int c = 0; c < n_cand; ++c)
+            if (s_cand[c] <= static_cast<unsigned long long>(L.max_chunks)) { chosen = c; break; }
     if (chosen < 0) {
-        if (tid == 0) {
-            meta[kMetaChunks] = 0;
-            meta[kMetaPpc] = 1;
-            meta[kMetaStatus] = NQ_ERR_CAPACITY;
-            meta[kMetaQueries] = 0;
-        }
+        fail(NQ_ERR_CAPACITY);
         return;
     }
+    int chunk_tok = kMinChunkTokens << chosen;
+    chunk_tok = chunk_tok < page_size ? page_size : chunk_tok;
+    const int chunk_pages = chunk_tok / page_size;
 
-    // Pass 2: chunk prefix per query.
     int carry = 0;
     for (int base = 0; base < T; base += blockDim.x) {
         const int q = base + tid;
-        int n = 0, row = 0, kvlen = 0;
+        int n = 0, row = 0, kvlen = -1;
         if (q < T) {
-            const int pages = query_pages(q, &row, &kvlen);
-            n = (pages + (1 << chosen) - 1) >> chosen;
-            if (n < 1) n = 1;
+            kvlen = query_keys(q, &row);
+            if (kvlen >= 0) {
+                n = (kvlen + chunk_tok - 1) / chunk_tok;
+                if (n < 1) n = 1;
+            }
         }
         int total;
         const int excl = plan_block_scan(n, s_tmp, &total);
         if (q < T) {
-            chunk_indptr[q] = carry + excl;
-            q_row[q] = row;
-            q_kvlen[q] = kvlen;
+            const int c0 = carry + excl;
+            chunk_indptr[q] = c0;
+            for (int k = 0; k < n; ++k) {
+                ChunkDesc d;
+                d.query = q;
+                d.page_start = s_base[row] + k * chunk_pages;
+                d.tok_begin = k * chunk_tok;
+                d.tok_end = min(kvlen, (k + 1) * chunk_tok);
+                d.n_chunks = n;
+                d.first_chunk = c0;
+                d.pad0 = d.pad1 = 0;
+                desc[c0 + k] = d;
+            }
         }
         carry += total;
     }
-    for (int i = tid; i < T * num_kv_heads; i += blockDim.x) counters[i] = 0;
     if (tid == 0) {
         chunk_indptr[T] = carry;
         meta[kMetaChunks] = carry;
-        meta[kMetaPpc] = 1 << chosen;
-        meta[kMetaStatus] = NQ_OK;
+        meta[kMetaChunkTok] = chunk_tok;
         meta[kMetaQueries] = T;
+        meta[kMetaDecRows] = n_dec;
+        meta[kMetaBlocks] = n_blocks;
+        meta[kMetaStatus] = NQ_OK;
     }
 }
 
-// Where the keys of one work item live.
-struct PagedSource {
-    const int32_t *kv_indices;
-    int page_base;
-    int ps_log2;
-    int num_pages;
-    __device__ __forceinline__ int page_of(int tok) const {
-        return kv_indices[page_base + (tok >> ps_log2)];
-    }
-    __device__ __forceinline__ int slot_of(int tok) const { return tok & ((1 << ps_log2) - 1); }
+// ---------------------------------------------------------------------------
+// Shared lane layout: D/8 lanes hold one 256/128-byte K or V row (8 bf16 each),
+// so a wave covers TPL = 64/(D/8) tokens per 128-bit load instruction.
+
+template <int D, int G>
+struct Lanes {
+    static constexpr int LPT = D / 8;
+    static constexpr int TPL = kWave / LPT;
+    static constexpr int NL = kBlockTok / TPL;  // loads per 16-token block per K or V
 };
 
-struct DenseSource {
-    int row;
-    __device__ __forceinline__ int page_of(int) const { return row; }
-    __device__ __forceinline__ int slot_of(int tok) const { return tok; }
-};
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-struct Smem {
-    float m[kWaves][8];
-    float l[kWaves][8];
-    float acc[kWaves][8][128];
-    int flag;
-};
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b),
+                                           c, false);
+}
 
-// Attend one query token (G consecutive query heads of kv head h) to the keys
-// [tok_begin, tok_end).  Leaves the combined (m, l, acc) of the workgroup for
-// output element t = j*D + d in *m_out/*l_out/*o_out of the calling thread
-// (threads t < G*D; larger G*D handled by the caller's loop).
-template <int D, int G, typename Src>
-__device__ __forceinline__ void attend_chunk(const uint16_t *__restrict__ qptr, int64_t q_s1,
-                                             const uint16_t *__restrict__ cache, int64_t c_page,
-                                             int64_t c_kind, int64_t c_slot, int64_t c_head,
-                                             int h, int tok_begin, int tok_end, int page_limit,
-                                             float scale_log2, const Src &src, Smem &sm,
-                                             int32_t *status) {
-    constexpr int LPT = D / 8;            // lanes per 256/128-byte row
-    constexpr int TPL = kWave / LPT;      // tokens per load instruction
-    constexpr int NL = kBlockTok / TPL;   // loads per block per K or V
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int g = lane / LPT;
-    const int sub = lane % LPT;
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2_t v;
+    v.x = static_cast<__bf16>(lo);
+    v.y = static_cast<__bf16>(hi);
+    return __builtin_bit_cast(uint32_t, v);
+}
 
-    float qv[G][8];
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-        const uint4 p = *reinterpret_cast<const uint4 *>(qptr + (h * G + j) * q_s1 + sub * 8);
-        unpack8(p, qv[j]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qv[j][e] *= scale_log2;
-    }
+__device__ __forceinline__ uint32_t word(const uint4 &v, int w) {
+    return w == 0 ? v.x : (w == 1 ? v.y : (w == 2 ? v.z : v.w));
+}
+
+// Online softmax of G query heads over 16-token blocks.  q stays in bf16 and
+// both products run on v_dot2_f32_bf16 with fp32 accumulation: q.k as four
+// dot2 per 8 elements, and P.V pairs two tokens per dot2 (the weights are
+// rounded to bf16 for the product and for the normaliser alike, as a bf16
+// tensor-core P.V would).
+template <int D, int G>
+struct SoftmaxState {
+    uint32_t qb[G][4];
+    float scale;
     float m[G], l[G], acc[G][8];
+
+    __device__ __forceinline__ void reset() {
 #pragma unroll
-    for (int j = 0; j < G; ++j) {
-        m[j] = -INFINITY;
-        l[j] = 0.f;
+        for (int j = 0; j < G; ++j) {
+            m[j] = -INFINITY;
+            l[j] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+            for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+        }
     }
 
-    const uint16_t *head_base = cache + h * c_head + sub * 8;
-    const int ntok = tok_end - tok_begin;
-    const int nblk = ntok > 0 ? (ntok + kBlockTok - 1) / kBlockTok : 0;
-    bool bad_page = false;
-    for (int b = wave; b < nblk; b += kWaves) {
-        const int tb = tok_begin + b * kBlockTok;
-        uint4 kr[NL], vr[NL];
-        bool valid[NL];
+    __device__ __forceinline__ void load_q(const uint16_t *qptr, int64_t q_s1, int h, int sub,
+                                           float scale_log2) {
+        scale = scale_log2;
 #pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int tok = tb + i * TPL + g;
-            valid[i] = tok < tok_end;
-            kr[i] = make_uint4(0, 0, 0, 0);
-            vr[i] = make_uint4(0, 0, 0, 0);
-            if (valid[i]) {
-                const int page = src.page_of(tok);
-                if (static_cast<unsigned>(page) < static_cast<unsigned>(page_limit)) {
-                    const uint16_t *p = head_base + page * c_page + src.slot_of(tok) * c_slot;
-                    kr[i] = *reinterpret_cast<const uint4 *>(p);
-                    vr[i] = *reinterpret_cast<const uint4 *>(p + c_kind);
-                } else {
-                    valid[i] = false;
-                    bad_page = true;
-                }
-            }
+        for (int j = 0; j < G; ++j) {
+            const uint4 p = *reinterpret_cast<const uint4 *>(qptr + (h * G + j) * q_s1 + sub * 8);
+            qb[j][0] = p.x;
+            qb[j][1] = p.y;
+            qb[j][2] = p.z;
+            qb[j][3] = p.w;
         }
+    }
+
+    // One 16-token block already in registers.
+    __device__ __forceinline__ void consume(const uint4 (&kr)[Lanes<D, G>::NL],
+                                            const uint4 (&vr)[Lanes<D, G>::NL],
+                                            const bool (&valid)[Lanes<D, G>::NL]) {
+        constexpr int NL = Lanes<D, G>::NL;
+        constexpr int LPT = Lanes<D, G>::LPT;
+        static_assert(NL % 2 == 0, "tokens are paired for P.V");
         float s[NL][G];
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            float kf[8];
-            unpack8(kr[i], kf);
 #pragma unroll
             for (int j = 0; j < G; ++j) {
-                float part = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) part += qv[j][e] * kf[e];
-                part = group_sum<LPT>(part);
+                float part = dot2_bf16(qb[j][0], kr[i].x, 0.f);
+                part = dot2_bf16(qb[j][1], kr[i].y, part);
+                part = dot2_bf16(qb[j][2], kr[i].z, part);
+                part = dot2_bf16(qb[j][3], kr[i].w, part);
+                part = group_sum<LPT>(part) * scale;
                 s[i][j] = valid[i] ? part : -INFINITY;
+            }
+        }
+        // V words of token pairs (2u, 2u+1) interleaved: (v_a[e], v_b[e]).
+        uint32_t vlo[NL / 2][4], vhi[NL / 2][4];
+#pragma unroll
+        for (int u = 0; u < NL / 2; ++u) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t a = word(vr[2 * u], w), b = word(vr[2 * u + 1], w);
+                vlo[u][w] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                vhi[u][w] = __builtin_amdgcn_perm(b, a, 0x07060302u);
             }
         }
 #pragma unroll
@@ -317,59 +411,399 @@ __device__ __forceinline__ void attend_chunk(const uint16_t *__restrict__ qptr, 
             if (mn == -INFINITY) continue;
             const float alpha = exp2f(m[j] - mn);
             m[j] = mn;
-            l[j] *= alpha;
+            float lsum = 0.f;
+            uint32_t pp[NL / 2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
+            for (int u = 0; u < NL / 2; ++u) {
+                pp[u] = pack_bf16x2(exp2f(s[2 * u][j] - mn), exp2f(s[2 * u + 1][j] - mn));
+                lsum += __uint_as_float(pp[u] << 16) + __uint_as_float(pp[u] & 0xffff0000u);
+            }
+            l[j] = l[j] * alpha + lsum;
 #pragma unroll
-            for (int i = 0; i < NL; ++i) {
-                const float p = exp2f(s[i][j] - mn);
-                l[j] += p;
-                float vf[8];
-                unpack8(vr[i], vf);
+            for (int w = 0; w < 4; ++w) {
+                float a0 = acc[j][2 * w] * alpha, a1 = acc[j][2 * w + 1] * alpha;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[j][e] += p * vf[e];
+                for (int u = 0; u < NL / 2; ++u) {
+                    a0 = dot2_bf16(pp[u], vlo[u][w], a0);
+                    a1 = dot2_bf16(pp[u], vhi[u][w], a1);
+                }
+                acc[j][2 * w] = a0;
+                acc[j][2 * w + 1] = a1;
             }
         }
     }
-    if (bad_page && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
 
-    // Combine the lane groups of the wave (lanes sub, sub+LPT, ...).
+    // Fold the lane groups of the wave together (result valid in every lane).
+    __device__ __forceinline__ void combine_lane_groups() {
+        constexpr int LPT = Lanes<D, G>::LPT;
 #pragma unroll
-    for (int mask = LPT; mask < kWave; mask <<= 1) {
+        for (int mask = LPT; mask < kWave; mask <<= 1) {
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const float mo = __shfl_xor(m[j], mask, kWave);
-            const float lo = __shfl_xor(l[j], mask, kWave);
-            const float mn = fmaxf(m[j], mo);
-            const float a = m[j] == -INFINITY ? 0.f : exp2f(m[j] - mn);
-            const float bsc = mo == -INFINITY ? 0.f : exp2f(mo - mn);
-            l[j] = l[j] * a + lo * bsc;
+            for (int j = 0; j < G; ++j) {
+                const float mo = __shfl_xor(m[j], mask, kWave);
+                const float lo = __shfl_xor(l[j], mask, kWave);
+                const float mn = fmaxf(m[j], mo);
+                const float a = m[j] == -INFINITY ? 0.f : exp2f(m[j] - mn);
+                const float bsc = mo == -INFINITY ? 0.f : exp2f(mo - mn);
+                l[j] = l[j] * a + lo * bsc;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float ao = __shfl_xor(acc[j][e], mask, kWave);
-                acc[j][e] = acc[j][e] * a + ao * bsc;
+                for (int e = 0; e < 8; ++e) {
+                    const float ao = __shfl_xor(acc[j][e], mask, kWave);
+                    acc[j][e] = acc[j][e] * a + ao * bsc;
+                }
+                m[j] = mn;
             }
-            m[j] = mn;
         }
     }
+};
+
+// ---------------------------------------------------------------------------
+// Stream kernel for decode rows.
+
+// Loads of one 16-token block, straight-line: tokens past the block's count
+// or on an invalid page read slot 0 of a valid page and are masked, so all
+// 2*NL loads are in flight together.  kSmallPages (page size < 16) looks each
+// token's page up in kv_indices first.
+template <int D, int G, bool kSmallPages>
+__device__ __forceinline__ void stream_issue(const int4 &dsc, int h, const uint16_t *__restrict__ cache,
+                                             int64_t c_page, int64_t c_kind, int64_t c_slot,
+                                             int64_t c_head, int num_pages, int ps_log2,
+                                             const int32_t *__restrict__ kv_indices, int index_limit,
+                                             int g, int sub, uint4 (&kr)[Lanes<D, G>::NL],
+                                             uint4 (&vr)[Lanes<D, G>::NL],
+                                             bool (&valid)[Lanes<D, G>::NL], bool *bad) {
+    constexpr int NL = Lanes<D, G>::NL;
+    constexpr int TPL = Lanes<D, G>::TPL;
+    const int ntok = static_cast<int>(static_cast<unsigned>(dsc.y) >> 24);
+    const int slot0 = dsc.y & 0xffffff;
+    const uint16_t *head_base = cache + h * c_head + sub * 8;
+    int page[NL], slot[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int t = i * TPL + g;
+        if constexpr (kSmallPages) {
+            const int at = dsc.x + (t >> ps_log2);
+            page[i] = (t < ntok && at < index_limit) ? kv_indices[at] : 0;
+            slot[i] = t & ((1 << ps_log2) - 1);
+        } else {
+            page[i] = dsc.x;
+            slot[i] = slot0 + t;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int t = i * TPL + g;
+        const bool page_ok = static_cast<unsigned>(page[i]) < static_cast<unsigned>(num_pages);
+        const bool in_block = t < ntok;
+        if (in_block && !page_ok) *bad = true;
+        valid[i] = in_block && page_ok;
+        const int64_t off = static_cast<int64_t>(page_ok ? page[i] : 0) * c_page +
+                            static_cast<int64_t>(valid[i] ? slot[i] : 0) * c_slot;
+        kr[i] = *reinterpret_cast<const uint4 *>(head_base + off);
+        vr[i] = *reinterpret_cast<const uint4 *>(head_base + off + c_kind);
+    }
+}
+
+__device__ __forceinline__ int4 shfl_int4(const int4 &v, int src) {
+    return make_int4(__shfl(v.x, src, kWave), __shfl(v.y, src, kWave), __shfl(v.z, src, kWave),
+                     __shfl(v.w, src, kWave));
+}
+
+__host__ __device__ __forceinline__ int span_start(int s, int n_blocks, int n_spans) {
+    return static_cast<int>(static_cast<int64_t>(s) * n_blocks / n_spans);
+}
+
+// Spans per kv head: every head's block list is cut at the same places, so the
+// Hkv waves of one span read the Hkv head slices of the same pages together.
+__host__ __device__ __forceinline__ int stream_spans(int n_blocks, int span_cap) {
+    int S = n_blocks / kMinBlocksPerWave;
+    return S < 1 ? 1 : (S > span_cap ? span_cap : S);
+}
+
+// Span holding block b (largest s with span_start(s) <= b).
+__device__ __forceinline__ int span_of(int b, int n_blocks, int n_spans) {
+    int s = static_cast<int>(static_cast<int64_t>(b) * n_spans / n_blocks);
+    while (s + 1 < n_spans && span_start(s + 1, n_blocks, n_spans) <= b) ++s;
+    while (s > 0 && span_start(s, n_blocks, n_spans) > b) --s;
+    return s;
+}
+
+template <int D, int G, bool kSmallPages>
+__device__ __forceinline__ void
+stream_body(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
+            const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
+            int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
+            int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
+            int64_t o_s0, int64_t o_s1, char *__restrict__ ws, const PlanLayout &L, int32_t *status) {
+    using LN = Lanes<D, G>;
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && status) atomicExch(status, meta[kMetaStatus]);
+        return;
+    }
+    const int n_dec = meta[kMetaDecRows];
+    const int NBT = meta[kMetaBlocks];
+    const int S = stream_spans(NBT, gridDim.x * kWaves / num_kv_heads);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = blockIdx.x * kWaves + threadIdx.x / kWave;
+    if (NBT == 0 || wid >= S * num_kv_heads) return;  // whole waves leave; no barriers below
+    const int h_span = wid % num_kv_heads;
+    const int span = wid / num_kv_heads;
+    const int s0 = span_start(span, NBT, S);
+    const int s1 = span_start(span + 1, NBT, S);
+    const int4 *blocks = reinterpret_cast<const int4 *>(ws + L.blocks);
+    const int4 *dec_rows = reinterpret_cast<const int4 *>(ws + L.dec_rows);
+    float *part_ml = reinterpret_cast<float *>(ws + L.spart_ml);
+    float *part_o = reinterpret_cast<float *>(ws + L.spart_o);
+    const int g = lane / LN::LPT;
+    const int sub = lane % LN::LPT;
+
+    // Block descriptors of the span, 64 at a time, one per lane; (h, b) walk
+    // the span without divisions.
+    int win = s0;
+    int4 dwin = make_int4(-1, 0, 0, 0);
+    if (s0 + lane < s1) dwin = blocks[s0 + lane];
+
+    SoftmaxState<D, G> st;
+    st.reset();
+    int cur_pair = -1, cur_query = 0, cur_h = 0, pair_lo = 0, pair_hi = 0;
+    bool bad = false;
+
+    const int h_cur = h_span;
+    bool done = false;
+    // Flush the finished (row, kv head) on a row change or at the span end:
+    // final output if this wave saw all of its blocks, else an fp32 partial.
+    auto enter = [&](int w, const int4 &dsc) {
+        const int pair = w < s1 ? dsc.z : -2;  // decode row; the head is fixed per wave
+        if (pair == cur_pair) return;
+        if (cur_pair >= 0) {
+            st.combine_lane_groups();
+            if (g == 0) {
+                if (pair_lo >= s0 && pair_hi <= s1) {
+#pragma unroll
+                    for (int j = 0; j < G; ++j) {
+                        const float inv = st.l[j] > 0.f ? 1.0f / st.l[j] : 0.f;
+                        uint4 o;
+                        o.x = pack2_bf16(st.acc[j][0] * inv, st.acc[j][1] * inv);
+                        o.y = pack2_bf16(st.acc[j][2] * inv, st.acc[j][3] * inv);
+                        o.z = pack2_bf16(st.acc[j][4] * inv, st.acc[j][5] * inv);
+                        o.w = pack2_bf16(st.acc[j][6] * inv, st.acc[j][7] * inv);
+                        *reinterpret_cast<uint4 *>(out + cur_query * o_s0 + (cur_h * G + j) * o_s1 + sub * 8) = o;
+                    }
+                } else {
+                    const int64_t slot = static_cast<int64_t>(span + cur_pair) * num_kv_heads + cur_h;
+#pragma unroll
+                    for (int j = 0; j < G; ++j) {
+                        float *po = part_o + (slot * G + j) * D + sub * 8;
+                        *reinterpret_cast<float4 *>(po) =
+                            make_float4(st.acc[j][0], st.acc[j][1], st.acc[j][2], st.acc[j][3]);
+                        *reinterpret_cast<float4 *>(po + 4) =
+                            make_float4(st.acc[j][4], st.acc[j][5], st.acc[j][6], st.acc[j][7]);
+                        if (sub == 0) {
+                            part_ml[(slot * G + j) * 2] = st.m[j];
+                            part_ml[(slot * G + j) * 2 + 1] = st.l[j];
+                        }
+                    }
+                }
+            }
+        }
+        if (w == s1) {
+            done = true;
+            return;
+        }
+        cur_pair = pair;
+        cur_query = dsc.w;
+        cur_h = h_cur;
+        const int4 dr = dec_rows[dsc.z];
+        pair_lo = dr.z;
+        pair_hi = pair_lo + dr.w;
+        st.reset();
+        st.load_q(q + cur_query * q_s0, q_s1, h_cur, sub, scale_log2);
+    };
+    auto desc_of = [&](int w) {
+        if (w - win >= kWave) {
+            win += kWave;
+            dwin = win + lane < s1 ? blocks[win + lane] : make_int4(-1, 0, 0, 0);
+        }
+        return shfl_int4(dwin, w - win);
+    };
+    if constexpr (!kStreamDoubleBuffer) {
+        uint4 kc[LN::NL], vc[LN::NL];
+        bool okc[LN::NL];
+        for (int w = s0;; ++w) {
+            const int4 dc = w < s1 ? desc_of(w) : make_int4(-1, 0, 0, 0);
+            enter(w, dc);
+            if (done) break;
+            stream_issue<D, G, kSmallPages>(dc, h_cur, cache, c_page, c_kind, c_slot, c_head, num_pages,
+                                            ps_log2, kv_indices, index_limit, g, sub, kc, vc, okc, &bad);
+            st.consume(kc, vc, okc);
+        }
+        if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+        return;
+    }
+    // Two register buffers alternate: while one block is consumed the loads of
+    // the next are in flight.
+    uint4 ka[LN::NL], va[LN::NL], kb[LN::NL], vb[LN::NL];
+    bool oka[LN::NL], okb[LN::NL];
+    int4 da = desc_of(s0), db = make_int4(-1, 0, 0, 0);
+    stream_issue<D, G, kSmallPages>(da, h_cur, cache, c_page, c_kind, c_slot, c_head, num_pages, ps_log2,
+                                    kv_indices, index_limit, g, sub, ka, va, oka, &bad);
+    for (int w = s0;; w += 2) {
+        if (w + 1 < s1) {
+            db = desc_of(w + 1);
+            stream_issue<D, G, kSmallPages>(db, h_cur, cache, c_page, c_kind, c_slot, c_head, num_pages,
+                                            ps_log2, kv_indices, index_limit, g, sub, kb, vb, okb, &bad);
+        }
+        enter(w, da);
+        if (done) break;
+        st.consume(ka, va, oka);
+        if (w + 2 < s1) {
+            da = desc_of(w + 2);
+            stream_issue<D, G, kSmallPages>(da, h_cur, cache, c_page, c_kind, c_slot, c_head, num_pages,
+                                            ps_log2, kv_indices, index_limit, g, sub, ka, va, oka, &bad);
+        }
+        enter(w + 1, db);
+        if (done) break;
+        st.consume(kb, vb, okb);
+    }
+    if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+}
+
+#define NQ_STREAM_ARGS                                                                            \
+    const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1, const uint16_t *__restrict__ cache, \
+        int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,             \
+        const int32_t *__restrict__ kv_indices, int index_limit, int num_kv_heads, int ps_log2,     \
+        float scale_log2, uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1,                   \
+        char *__restrict__ ws, PlanLayout L, int32_t *status
+#define NQ_STREAM_PASS                                                                             \
+    q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit,      \
+        num_kv_heads, ps_log2, scale_log2, out, o_s0, o_s1, ws, L, status
+
+// Up to two query heads per kv head the state fits 128 VGPRs: four waves per
+// SIMD stay resident, so the 4096 waves of a launch run in a single round.
+template <int D, int G, bool kSmallPages>
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+paged_stream_kernel_occ4(NQ_STREAM_ARGS) {
+    stream_body<D, G, kSmallPages>(NQ_STREAM_PASS);
+}
+
+template <int D, int G, bool kSmallPages>
+__global__ void __launch_bounds__(kAttnThreads) paged_stream_kernel(NQ_STREAM_ARGS) {
+    stream_body<D, G, kSmallPages>(NQ_STREAM_PASS);
+}
+
+// Merge the stream partials of each (decode row, kv head) pair that more than
+// one wave touched: one workgroup per pair, one thread per output element.
+template <int D, int G>
+__global__ void __launch_bounds__(kAttnThreads)
+merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads, int worker_cap,
+                    uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1) {
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) return;
+    const int n_dec = meta[kMetaDecRows];
+    const int NBT = meta[kMetaBlocks];
+    if (NBT == 0) return;
+    const int S = stream_spans(NBT, worker_cap / num_kv_heads);
+    const int4 *dec_rows = reinterpret_cast<const int4 *>(ws + L.dec_rows);
+    const float *part_ml = reinterpret_cast<const float *>(ws + L.spart_ml);
+    const float *part_o = reinterpret_cast<const float *>(ws + L.spart_o);
+    const int n_pairs = n_dec * num_kv_heads;
+    for (int p = blockIdx.x; p < n_pairs; p += gridDim.x) {
+        const int h = p / n_dec, j = p - h * n_dec;
+        const int4 dr = dec_rows[j];
+        const int i0 = span_of(dr.z, NBT, S);
+        const int i1 = span_of(dr.z + dr.w - 1, NBT, S);
+        if (i0 == i1) continue;  // one wave saw the whole row and wrote it
+        for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
+            const int jj = t / D, d = t % D;
+            float mx = -INFINITY;
+            for (int i = i0; i <= i1; ++i)
+                mx = fmaxf(mx, part_ml[((static_cast<int64_t>(i + j) * num_kv_heads + h) * G + jj) * 2]);
+            float ls = 0.f, os = 0.f;
+            if (mx != -INFINITY) {
+#pragma unroll 4
+                for (int i = i0; i <= i1; ++i) {
+                    const int64_t slot = static_cast<int64_t>(i + j) * num_kv_heads + h;
+                    const float mk = part_ml[(slot * G + jj) * 2];
+                    const float sc = mk == -INFINITY ? 0.f : exp2f(mk - mx);
+                    ls += part_ml[(slot * G + jj) * 2 + 1] * sc;
+                    os += part_o[(slot * G + jj) * D + d] * sc;
+                }
+            }
+            out[dr.y * o_s0 + (h * G + jj) * o_s1 + d] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Chunk kernel for causal prefill queries and the dense short-cache kernel:
+// a workgroup per (query, chunk, kv head); waves split the chunk's blocks.
+
+struct Smem {
+    float m[kWaves][8];
+    float l[kWaves][8];
+    float acc[kWaves][8][128];
+    int pages[kMaxChunkTokens];
+};
+
+// Attend G query heads of kv head h to `ntok` keys; key position `rel` lives in
+// page page_of(rel) at slot slot_of(rel).  Leaves per-wave states in `sm`.
+template <int D, int G, typename PageOf, typename SlotOf>
+__device__ __forceinline__ void attend_chunk(const uint16_t *__restrict__ qptr, int64_t q_s1,
+                                             const uint16_t *__restrict__ cache, int64_t c_page,
+                                             int64_t c_kind, int64_t c_slot, int64_t c_head, int h,
+                                             int ntok, int page_limit, float scale_log2,
+                                             PageOf page_of, SlotOf slot_of, Smem &sm, bool *bad) {
+    using LN = Lanes<D, G>;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int g = lane / LN::LPT;
+    const int sub = lane % LN::LPT;
+    SoftmaxState<D, G> st;
+    st.reset();
+    st.load_q(qptr, q_s1, h, sub, scale_log2);
+    const uint16_t *head_base = cache + h * c_head + sub * 8;
+    const int nblk = ntok > 0 ? (ntok + kBlockTok - 1) / kBlockTok : 0;
+    for (int b = wave; b < nblk; b += kWaves) {
+        uint4 kr[LN::NL], vr[LN::NL];
+        bool valid[LN::NL];
+        int page[LN::NL];
+#pragma unroll
+        for (int i = 0; i < LN::NL; ++i) {
+            const int rel = b * kBlockTok + i * LN::TPL + g;
+            page[i] = rel < ntok ? page_of(rel) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < LN::NL; ++i) {
+            const int rel = b * kBlockTok + i * LN::TPL + g;
+            const bool page_ok = static_cast<unsigned>(page[i]) < static_cast<unsigned>(page_limit);
+            const bool in_range = rel < ntok;
+            if (in_range && !page_ok) *bad = true;
+            valid[i] = in_range && page_ok;
+            const int64_t off = static_cast<int64_t>(page_ok ? page[i] : 0) * c_page +
+                                static_cast<int64_t>(valid[i] ? slot_of(rel) : 0) * c_slot;
+            kr[i] = *reinterpret_cast<const uint4 *>(head_base + off);
+            vr[i] = *reinterpret_cast<const uint4 *>(head_base + off + c_kind);
+        }
+        st.consume(kr, vr, valid);
+    }
+    st.combine_lane_groups();
     if (g == 0) {
 #pragma unroll
         for (int j = 0; j < G; ++j) {
             if (sub == 0) {
-                sm.m[wave][j] = m[j];
-                sm.l[wave][j] = l[j];
+                sm.m[wave][j] = st.m[j];
+                sm.l[wave][j] = st.l[j];
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sm.acc[wave][j][sub * 8 + e] = acc[j][e];
+            for (int e = 0; e < 8; ++e) sm.acc[wave][j][sub * 8 + e] = st.acc[j][e];
         }
     }
     __syncthreads();
 }
 
-// Combine the per-wave states in shared memory for output element t = j*D+d.
 template <int D>
-__device__ __forceinline__ void wave_combine(const Smem &sm, int t, float *M, float *Lsum,
-                                             float *O) {
+__device__ __forceinline__ void wave_combine(const Smem &sm, int t, float *M, float *Lsum, float *O) {
     const int j = t / D, d = t % D;
     float mx = -INFINITY;
 #pragma unroll
@@ -391,95 +825,94 @@ __device__ __forceinline__ void wave_combine(const Smem &sm, int t, float *M, fl
 
 template <int D, int G>
 __global__ void __launch_bounds__(kAttnThreads)
-paged_decode_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
-                    const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind,
-                    int64_t c_slot, int64_t c_head, int num_pages,
-                    const int32_t *__restrict__ kv_indptr, const int32_t *__restrict__ kv_indices,
-                    int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
-                    int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L,
-                    int32_t *status) {
+paged_chunk_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
+                   const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind,
+                   int64_t c_slot, int64_t c_head, int num_pages,
+                   const int32_t *__restrict__ kv_indices, int index_limit, int num_kv_heads,
+                   int ps_log2, float scale_log2, uint16_t *__restrict__ out, int64_t o_s0,
+                   int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
     __shared__ Smem sm;
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
-    const int32_t *chunk_indptr = reinterpret_cast<const int32_t *>(ws + L.chunk_indptr);
-    const int32_t *q_row = reinterpret_cast<const int32_t *>(ws + L.q_row);
-    const int32_t *q_kvlen = reinterpret_cast<const int32_t *>(ws + L.q_kvlen);
-    int32_t *counters = reinterpret_cast<int32_t *>(ws + L.counters);
+    const ChunkDesc *desc = reinterpret_cast<const ChunkDesc *>(ws + L.desc);
     float *part_ml = reinterpret_cast<float *>(ws + L.part_ml);
     float *part_o = reinterpret_cast<float *>(ws + L.part_o);
     if (meta[kMetaStatus] != NQ_OK) return;
     const int n_chunks = meta[kMetaChunks];
-    const int T = meta[kMetaQueries];
-    const int chunk_tok = meta[kMetaPpc] << ps_log2;
     const int Hq = num_kv_heads * G;
     const int64_t n_items = static_cast<int64_t>(n_chunks) * num_kv_heads;
-
+    const int ps = 1 << ps_log2;
+    bool bad = false;
     for (int64_t w = blockIdx.x; w < n_items; w += gridDim.x) {
         const int c = static_cast<int>(w / num_kv_heads);
         const int h = static_cast<int>(w - static_cast<int64_t>(c) * num_kv_heads);
-        int lo = 0, hi = T;  // query owning chunk c
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (chunk_indptr[mid] <= c) lo = mid; else hi = mid;
+        const ChunkDesc d = desc[c];
+        const int ntok = d.tok_end - d.tok_begin;
+        const int npg = (ntok + ps - 1) >> ps_log2;
+        for (int t = threadIdx.x; t < npg; t += kAttnThreads) {
+            const int at = d.page_start + t;
+            sm.pages[t] = at < index_limit ? kv_indices[at] : -1;
         }
-        const int qi = lo;
-        const int c0 = chunk_indptr[qi];
-        const int nk = chunk_indptr[qi + 1] - c0;
-        const int row = q_row[qi];
-        const int kvlen = q_kvlen[qi];
-        const int tok_begin = (c - c0) * chunk_tok;
-        const int tok_end = min(kvlen, tok_begin + chunk_tok);
-        PagedSource src{kv_indices, kv_indptr[row], ps_log2, num_pages};
-        attend_chunk<D, G>(q + qi * q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, h,
-                           tok_begin, tok_end, num_pages, scale_log2, src, sm, status);
-        if (nk == 1) {
-            for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
-                float M, Ls, O;
-                wave_combine<D>(sm, t, &M, &Ls, &O);
-                const int j = t / D, d = t % D;
-                out[qi * o_s0 + (h * G + j) * o_s1 + d] = f32_to_bf16(Ls > 0.f ? O / Ls : 0.f);
-            }
-        } else {
-            for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
-                float M, Ls, O;
-                wave_combine<D>(sm, t, &M, &Ls, &O);
-                const int j = t / D, d = t % D;
+        __syncthreads();
+        attend_chunk<D, G>(
+            q + d.query * q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, h, ntok, num_pages,
+            scale_log2, [&](int rel) { return sm.pages[rel >> ps_log2]; },
+            [&](int rel) { return rel & (ps - 1); }, sm, &bad);
+        for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
+            float M, Ls, O;
+            wave_combine<D>(sm, t, &M, &Ls, &O);
+            const int j = t / D, dd = t % D;
+            if (d.n_chunks == 1) {
+                out[d.query * o_s0 + (h * G + j) * o_s1 + dd] = f32_to_bf16(Ls > 0.f ? O / Ls : 0.f);
+            } else {
                 const int64_t hh = static_cast<int64_t>(c) * Hq + h * G + j;
-                part_o[hh * D + d] = O;
-                if (d == 0) {
+                part_o[hh * D + dd] = O;
+                if (dd == 0) {
                     part_ml[hh * 2] = M;
                     part_ml[hh * 2 + 1] = Ls;
                 }
             }
-            __threadfence();
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                const int prev = atomicAdd(&counters[qi * num_kv_heads + h], 1);
-                sm.flag = (prev == nk - 1);
-            }
-            __syncthreads();
-            if (sm.flag) {
-                __threadfence();
-                for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
-                    const int j = t / D, d = t % D;
-                    float mx = -INFINITY;
-                    for (int k = 0; k < nk; ++k)
-                        mx = fmaxf(mx, part_ml[(static_cast<int64_t>(c0 + k) * Hq + h * G + j) * 2]);
-                    float ls = 0.f, os = 0.f;
-                    if (mx != -INFINITY) {
-                        for (int k = 0; k < nk; ++k) {
-                            const int64_t hh = static_cast<int64_t>(c0 + k) * Hq + h * G + j;
-                            const float mk = part_ml[hh * 2];
-                            const float sc = mk == -INFINITY ? 0.f : exp2f(mk - mx);
-                            ls += part_ml[hh * 2 + 1] * sc;
-                            os += part_o[hh * D + d] * sc;
-                        }
-                    }
-                    out[qi * o_s0 + (h * G + j) * o_s1 + d] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
-                }
-                if (threadIdx.x == 0) atomicExch(&counters[qi * num_kv_heads + h], 0);
-            }
         }
         __syncthreads();
+    }
+    if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+}
+
+template <int D, int G>
+__global__ void __launch_bounds__(kAttnThreads)
+merge_chunks_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads,
+                    uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1) {
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) return;
+    const int T = meta[kMetaQueries];
+    const int32_t *chunk_indptr = reinterpret_cast<const int32_t *>(ws + L.chunk_indptr);
+    const float *part_ml = reinterpret_cast<const float *>(ws + L.part_ml);
+    const float *part_o = reinterpret_cast<const float *>(ws + L.part_o);
+    const int Hq = num_kv_heads * G;
+    const int64_t n_items = static_cast<int64_t>(T) * num_kv_heads;
+    for (int64_t w = blockIdx.x; w < n_items; w += gridDim.x) {
+        const int qi = static_cast<int>(w / num_kv_heads);
+        const int h = static_cast<int>(w - static_cast<int64_t>(qi) * num_kv_heads);
+        const int c0 = chunk_indptr[qi];
+        const int nk = chunk_indptr[qi + 1] - c0;
+        if (nk <= 1) continue;
+        for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
+            const int j = t / D, dd = t % D;
+            float mx = -INFINITY;
+            for (int k = 0; k < nk; ++k)
+                mx = fmaxf(mx, part_ml[(static_cast<int64_t>(c0 + k) * Hq + h * G + j) * 2]);
+            float ls = 0.f, os = 0.f;
+            if (mx != -INFINITY) {
+#pragma unroll 4
+                for (int k = 0; k < nk; ++k) {
+                    const int64_t hh = static_cast<int64_t>(c0 + k) * Hq + h * G + j;
+                    const float mk = part_ml[hh * 2];
+                    const float sc = mk == -INFINITY ? 0.f : exp2f(mk - mx);
+                    ls += part_ml[hh * 2 + 1] * sc;
+                    os += part_o[hh * D + dd] * sc;
+                }
+            }
+            out[qi * o_s0 + (h * G + j) * o_s1 + dd] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
+        }
     }
 }
 
@@ -491,12 +924,13 @@ dense_short_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                    uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1) {
     __shared__ Smem sm;
     const int64_t n_items = static_cast<int64_t>(rows) * num_kv_heads;
+    bool bad = false;
     for (int64_t w = blockIdx.x; w < n_items; w += gridDim.x) {
         const int row = static_cast<int>(w / num_kv_heads);
         const int h = static_cast<int>(w - static_cast<int64_t>(row) * num_kv_heads);
-        DenseSource src{row};
-        attend_chunk<D, G>(q + row * q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head, h, 0,
-                           valid_length, rows, scale_log2, src, sm, nullptr);
+        attend_chunk<D, G>(
+            q + row * q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head, h, valid_length, rows,
+            scale_log2, [&](int) { return row; }, [&](int rel) { return rel; }, sm, &bad);
         for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
             float M, Ls, O;
             wave_combine<D>(sm, t, &M, &Ls, &O);
@@ -512,15 +946,40 @@ constexpr float kLog2e = 1.4426950408889634f;
 template <int D, int G>
 int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
                  int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,
-                 const int32_t *kv_indptr, const int32_t *kv_indices, int Hkv, int ps_log2,
-                 float scale, uint16_t *out, int64_t o_s0, int64_t o_s1, char *ws,
-                 const PlanLayout &L, int32_t *status, hipStream_t stream) {
-    int64_t items = L.max_chunks * Hkv;
-    int grid = static_cast<int>(items < 4096 ? items : 4096);
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((paged_decode_kernel<D, G>), dim3(grid), dim3(kAttnThreads), 0, stream, q,
-                       q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indptr,
-                       kv_indices, Hkv, ps_log2, scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+                 const int32_t *kv_indices, int index_limit, int Hkv, int ps_log2, float scale,
+                 uint16_t *out, int64_t o_s0, int64_t o_s1, char *ws, const PlanLayout &L,
+                 int max_queries, int prefill_rows, int32_t *status, hipStream_t stream) {
+    const int sgrid = kStreamWaves / kWaves;
+#define NQ_LAUNCH_STREAM(KERNEL, SMALL)                                                          \
+    hipLaunchKernelGGL((KERNEL<D, G, SMALL>), dim3(sgrid), dim3(kAttnThreads), 0, stream, q, q_s0, \
+                       q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,         \
+                       index_limit, Hkv, ps_log2, scale * kLog2e, out, o_s0, o_s1, ws, L, status)
+    const bool small_pages = ps_log2 < 4;
+    if constexpr (G <= 2) {
+        if (small_pages) NQ_LAUNCH_STREAM(paged_stream_kernel_occ4, true);
+        else NQ_LAUNCH_STREAM(paged_stream_kernel_occ4, false);
+    } else {
+        if (small_pages) NQ_LAUNCH_STREAM(paged_stream_kernel, true);
+        else NQ_LAUNCH_STREAM(paged_stream_kernel, false);
+    }
+#undef NQ_LAUNCH_STREAM
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    const int64_t pairs = static_cast<int64_t>(max_queries) * Hkv;
+    const int mgrid = static_cast<int>(pairs < 2048 ? pairs : 2048);
+    hipLaunchKernelGGL((merge_stream_kernel<D, G>), dim3(mgrid), dim3(kAttnThreads), 0, stream, ws,
+                       L, Hkv, sgrid * kWaves, out, o_s0, o_s1);
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    if (!prefill_rows) return NQ_OK;
+    const int64_t items = L.max_chunks * Hkv;
+    const int grid = static_cast<int>(items < 8192 ? items : 8192);
+    hipLaunchKernelGGL((paged_chunk_kernel<D, G>), dim3(grid), dim3(kAttnThreads), 0, stream, q,
+                       q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,
+                       index_limit, Hkv, ps_log2, scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    const int64_t merges = static_cast<int64_t>(max_queries) * Hkv;
+    const int cgrid = static_cast<int>(merges < 4096 ? merges : 4096);
+    hipLaunchKernelGGL((merge_chunks_kernel<D, G>), dim3(cgrid), dim3(kAttnThreads), 0, stream, ws,
+                       L, Hkv, out, o_s0, o_s1);
     return NQ_LAUNCH_STATUS();
 }
 
@@ -549,26 +1008,27 @@ extern "C" int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pa
     if (max_query_tokens < 1 || max_pages < 1 || page_size < 1 || num_kv_heads < 1 ||
         num_qo_heads < num_kv_heads || head_dim < 8)
         return NQ_ERR_INVALID_ARGUMENT;
-    return nq::plan_layout(max_query_tokens, max_pages, num_qo_heads, num_kv_heads, head_dim).total;
+    return nq::plan_layout(max_query_tokens, max_pages, page_size, num_qo_heads, num_kv_heads, head_dim)
+        .total;
 }
 
 extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
-                                 const int32_t *last_page_len, int n_rows, int max_query_tokens,
-                                 int max_pages, int page_size, int num_qo_heads, int num_kv_heads,
-                                 int head_dim, void *workspace, int64_t workspace_bytes,
-                                 void *stream) {
+                                 const int32_t *last_page_len, const int32_t *kv_indices,
+                                 int n_rows, int max_query_tokens, int max_pages, int page_size,
+                                 int num_qo_heads, int num_kv_heads, int head_dim, void *workspace,
+                                 int64_t workspace_bytes, void *stream) {
     NQ_CHECK_ARG(n_rows >= 1 && max_query_tokens >= 1 && max_pages >= 1);
     if (n_rows > nq::kPlanThreads) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0);
     NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
-    NQ_CHECK_ARG(kv_indptr && last_page_len && workspace);
+    NQ_CHECK_ARG(kv_indptr && last_page_len && kv_indices && workspace);
     NQ_CHECK_ARG(qo_indptr || n_rows <= max_query_tokens);
     const PlanLayout L =
-        nq::plan_layout(max_query_tokens, max_pages, num_qo_heads, num_kv_heads, head_dim);
+        nq::plan_layout(max_query_tokens, max_pages, page_size, num_qo_heads, num_kv_heads, head_dim);
     NQ_CHECK_ARG(workspace_bytes >= L.total);
-    hipLaunchKernelGGL(nq::attention_plan_kernel, dim3(1), dim3(nq::kPlanThreads), 0,
+    hipLaunchKernelGGL(nq::attention_plan_kernel, dim3(nq::kPlanGrid), dim3(nq::kPlanThreads), 0,
                        static_cast<hipStream_t>(stream), qo_indptr, kv_indptr, last_page_len,
-                       n_rows, max_query_tokens, page_size, num_kv_heads, L.max_chunks,
+                       kv_indices, n_rows, max_query_tokens, max_pages, page_size, num_kv_heads,
                        static_cast<char *>(workspace), L);
     return NQ_LAUNCH_STATUS();
 }
@@ -576,19 +1036,19 @@ extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_ind
 extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,
                                   const uint16_t *cache, int64_t c_page, int64_t c_kind,
                                   int64_t c_slot, int64_t c_head, int num_pages,
-                                  const int32_t *kv_indptr, const int32_t *kv_indices,
-                                  int page_size, int num_qo_heads, int num_kv_heads, int head_dim,
-                                  float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
-                                  int max_query_tokens, int max_pages, void *workspace,
-                                  int64_t workspace_bytes, int32_t *status, void *stream) {
-    NQ_CHECK_ARG(q && cache && kv_indptr && kv_indices && out && workspace);
+                                  const int32_t *kv_indices, int page_size, int num_qo_heads,
+                                  int num_kv_heads, int head_dim, float sm_scale, uint16_t *out,
+                                  int64_t o_s0, int64_t o_s1, int max_query_tokens, int max_pages,
+                                  int prefill_rows, void *workspace, int64_t workspace_bytes,
+                                  int32_t *status, void *stream) {
+    NQ_CHECK_ARG(q && cache && kv_indices && out && workspace);
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1);
     NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
     NQ_CHECK_ARG(max_query_tokens >= 1 && max_pages >= 1);
     if (!nq::aligned16(q) || !nq::aligned16(cache) || !nq::aligned16(out)) return NQ_ERR_UNSUPPORTED;
-    if ((q_s0 | q_s1 | c_page | c_kind | c_slot | c_head) & 7) return NQ_ERR_UNSUPPORTED;
+    if ((q_s0 | q_s1 | c_page | c_kind | c_slot | c_head | o_s0 | o_s1) & 7) return NQ_ERR_UNSUPPORTED;
     const PlanLayout L =
-        nq::plan_layout(max_query_tokens, max_pages, num_qo_heads, num_kv_heads, head_dim);
+        nq::plan_layout(max_query_tokens, max_pages, page_size, num_qo_heads, num_kv_heads, head_dim);
     NQ_CHECK_ARG(workspace_bytes >= L.total);
     int ps_log2 = 0;
     while ((1 << ps_log2) < page_size) ++ps_log2;
@@ -598,8 +1058,9 @@ extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,
 #define NQ_PAGED(DD, GG)                                                                          \
     if (head_dim == DD && G == GG)                                                                \
         return nq::launch_paged<DD, GG>(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head,     \
-                                        num_pages, kv_indptr, kv_indices, num_kv_heads, ps_log2,  \
-                                        sm_scale, out, o_s0, o_s1, ws, L, status, s);
+                                        num_pages, kv_indices, max_pages, num_kv_heads, ps_log2,  \
+                                        sm_scale, out, o_s0, o_s1, ws, L, max_query_tokens,       \
+                                        prefill_rows, status, s);
     NQ_PAGED(128, 1) NQ_PAGED(128, 2) NQ_PAGED(128, 4) NQ_PAGED(128, 8)
     NQ_PAGED(64, 1) NQ_PAGED(64, 2) NQ_PAGED(64, 4) NQ_PAGED(64, 8)
 #undef NQ_PAGED

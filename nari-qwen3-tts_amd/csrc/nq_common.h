@@ -45,10 +45,30 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
     return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
 }
 
+// DPP lane permutations (gfx9 encodings): quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror (reverse 8 lanes), row_mirror (reverse 16 lanes).
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of Width lanes, result in every lane of the group.
+// Widths up to 16 stay inside a DPP row (one VALU op per step); wider groups
+// fall back to cross-row shuffles.
 template <int Width>
 __device__ __forceinline__ float group_sum(float v) {
+    static_assert(Width >= 1 && Width <= kWave && (Width & (Width - 1)) == 0, "power of two");
+    if constexpr (Width >= 2) v += dpp_f32<kDppQuadXor1>(v);
+    if constexpr (Width >= 4) v += dpp_f32<kDppQuadXor2>(v);
+    if constexpr (Width >= 8) v += dpp_f32<kDppHalfMirror>(v);
+    if constexpr (Width >= 16) v += dpp_f32<kDppMirror>(v);
 #pragma unroll
-    for (int m = 1; m < Width; m <<= 1) v += __shfl_xor(v, m, kWave);
+    for (int m = 16; m < Width; m <<= 1) v += __shfl_xor(v, m, kWave);
     return v;
 }
 

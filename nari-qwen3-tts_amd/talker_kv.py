@@ -146,6 +146,7 @@ class _HipBindingBase:
             _lib.ptr(b.qo_indptr),
             _lib.ptr(b.kv_indptr),
             _lib.ptr(b.last_page_len),
+            _lib.ptr(b.kv_indices),
             self.capture_batch_size,
             self.token_capacity,
             self.index_capacity,
@@ -192,16 +193,23 @@ class _HipBindingBase:
             layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
             b.write_pages.data_ptr(), b.write_offsets.data_ptr(), 0, stream,
         )
+        return self.run_attention(query, self._layer_index, stream)
+
+    def run_attention(self, query: torch.Tensor, layer_index: int, stream: int | None = None) -> torch.Tensor:
+        """Paged attention of ``query`` over one layer with the planned metadata (no q/k transform)."""
+
+        layer = self.storage[layer_index]
         out = self.output
         _lib.call(
             "nq_paged_attention",
             query.data_ptr(), query.stride(0), query.stride(1),
             layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
-            layer.shape[0], b.kv_indptr.data_ptr(), b.kv_indices.data_ptr(),
-            self.page_size, hq, self.num_kv_heads, d, float(d) ** -0.5,
+            layer.shape[0], self.buffers.kv_indices.data_ptr(),
+            self.page_size, self.num_qo_heads, self.num_kv_heads, self.head_dim, float(self.head_dim) ** -0.5,
             out.data_ptr(), out.stride(0), out.stride(1),
-            self.token_capacity, self.index_capacity, self.workspace.data_ptr(), self.workspace.numel(),
-            self.attention_status.data_ptr(), stream,
+            self.token_capacity, self.index_capacity, int(self.prefill), self.workspace.data_ptr(),
+            self.workspace.numel(), self.attention_status.data_ptr(),
+            _lib.stream(self.device) if stream is None else stream,
         )
         return out
 

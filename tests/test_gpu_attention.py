@@ -15,17 +15,7 @@ MAX_ABS, MEAN_ABS = 2e-2, 2e-3
 
 
 def _run(nq, ctx, q, layer_index=0):
-    from nari_qwen3_tts_amd import _lib
-
-    layer = ctx.storage[layer_index]
-    out = ctx.output
-    _lib.call(
-        "nq_paged_attention", q.data_ptr(), q.stride(0), q.stride(1), layer.data_ptr(), layer.stride(0),
-        layer.stride(1), layer.stride(2), layer.stride(3), layer.shape[0], ctx.buffers.kv_indptr.data_ptr(),
-        ctx.buffers.kv_indices.data_ptr(), ctx.page_size, ctx.num_qo_heads, ctx.num_kv_heads, ctx.head_dim,
-        ctx.head_dim ** -0.5, out.data_ptr(), out.stride(0), out.stride(1), ctx.token_capacity, ctx.index_capacity,
-        ctx.workspace.data_ptr(), ctx.workspace.numel(), ctx.attention_status.data_ptr(), _lib.stream(q.device),
-    )
+    out = ctx.run_attention(q, layer_index)
     torch.cuda.synchronize()
     assert int(ctx.attention_status.item()) == 0
     return out
@@ -113,7 +103,7 @@ def test_mixed_prefill_and_decode_rows(nq, device):
     """Reduced cfg3: causal prefill chunks (bottom-right) and decode rows in one launch."""
 
     rng = np.random.default_rng(1003)
-    kv = make_kv(nq, device, pages=8192, ps=16, scratch=64)
+    kv = make_kv(nq, device, pages=8192, ps=16, scratch=128)
     g = torch.Generator(device=device)
     g.manual_seed(1003)
     kv.storage.copy_(torch.randn(kv.storage.shape, generator=g, device=device).to(torch.bfloat16))

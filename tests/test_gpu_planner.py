@@ -106,13 +106,14 @@ def test_scratch_capacity_errors_of_reference(nq, device):
 def test_pool_exhaustion_raises_before_launch(nq, device):
     from nari_qwen3_tts_amd.errors import KVAllocationError
 
-    kv = make_kv(nq, device, layers=1, hq=4, hkv=2, d=64, pages=6, ps=4, scratch=2)
+    kv = make_kv(nq, device, layers=1, hq=4, hkv=2, d=64, pages=10, ps=4, scratch=5)
     kv.add_request("a")
     kv.add_request("b")
-    key = PrefillKey(2, 32)
+    key = PrefillKey(2, 18)
     with pytest.raises(KVAllocationError):
-        kv.prepare_prefill(kv.create_prefill(key, slot=0), key, ("a", "b"), (1, 16))
-    assert kv.allocator.free_pages == 4
+        kv.prepare_prefill(kv.create_prefill(key, slot=0), key, ("a", "b"), (1, 17))
+    assert kv.allocator.free_pages == 5
+    assert kv.state("a").sequence_length == 0
 
 
 @pytest.mark.parametrize(
@@ -148,7 +149,7 @@ def test_mixed_prefill_and_decode_rows_match_oracle(nq, device):
     """cfg3 shape: 16 prefill chunks (prior U[0,512], advance U[32,256]) + 112 decode rows."""
 
     rng = np.random.default_rng(1003)
-    kv = make_kv(nq, device, pages=32768, ps=16, scratch=200)
+    kv = make_kv(nq, device, pages=32768, ps=16, scratch=300)
     pre_prior = rng.integers(0, 513, size=16)
     pre_adv = rng.integers(32, 257, size=16)
     dec_prior = rng.integers(64, 2049, size=112)
