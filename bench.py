@@ -35,6 +35,9 @@ PAGE_SIZE = 16
 POOL_PAGES = 32768
 KV_LO, KV_HI = 64, 2048
 SEED = 1002
+# HBM bytes one attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE counter passes
+# in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device copy: x2.0 and x1.0).
+ATTENTION_TRAFFIC_BYTES = 251_622_400
 
 
 def log(*a):
@@ -152,8 +155,9 @@ def attention_probe(torch, w, replays: int = 20):
     return avg_ms, bytes_per_launch, tokens_per_launch
 
 
-def cpu_baseline(torch, np, w, budget_s: float = 12.0):
-    """The oracle decode step on the host cores: as many of the 28 layers as fit the budget, scaled to 28."""
+def cpu_baseline(torch, np, w, budget_s: float = 10.0):
+    """The oracle decode step on the host cores: all 28 layers, repeated (up to three passes) until the
+    budget is spent, reported per 28-layer step."""
 
     from oracle import bf16 as o_bf16
     from oracle import planner as o_plan
@@ -191,7 +195,8 @@ def cpu_baseline(torch, np, w, budget_s: float = 12.0):
                 rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta)
     done = 0
     elapsed = 0.0
-    for li in range(cfg.num_layers):
+    for step_layer in range(3 * cfg.num_layers):
+        li = step_layer % cfg.num_layers
         L = wts.layers[li]
         layer_np = dict(input_norm=host(L.input_norm), qkv=host(L.qkv), o=host(L.o), post_norm=host(L.post_norm),
                         gate_up=host(L.gate_up), down=host(L.down), q_norm=host(L.attention.q_norm.weight),
@@ -203,12 +208,28 @@ def cpu_baseline(torch, np, w, budget_s: float = 12.0):
         _, residual = o_talker.decode_layers([layer_np], cfgd, residual, cache, meta, range(0, 1), final_norm=nxt)
         elapsed += time.perf_counter() - t0
         done += 1
-        if elapsed >= budget_s:
+        if elapsed >= budget_s and done >= cfg.num_layers:
             break
     step_s = elapsed / done * cfg.num_layers
     return dict(value=ROWS / step_s, unit="tok/s", cores=int(cores), kind="port",
-                sample=f"oracle decode step (numpy) over {done} of {cfg.num_layers} layers for {ROWS} rows, "
-                       f"{elapsed:.1f}s, scaled to {cfg.num_layers} layers")
+                sample=f"oracle decode step (numpy): {done} layer passes ({cfg.num_layers} layers per step) for {ROWS} "
+                       f"rows in {elapsed:.1f}s, scaled to one {cfg.num_layers}-layer step")
+
+
+def copy_calibration(torch, mib: int, reps: int = 4) -> None:
+    """Plain device-to-device copies of a known size: the yardstick that scales the
+    FETCH_SIZE / WRITE_SIZE hardware counters to bytes (each copy reads and writes ``mib`` MiB)."""
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / reps * 1e6
+    log(f"copy calibration: {reps} x {mib} MiB device copies, {us:.1f} us each ({2 * n / us / 1e3:.0f} GB/s r+w)")
 
 
 def main() -> int:
@@ -217,6 +238,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the serving path shards by independent request rows with no "
@@ -226,6 +249,8 @@ def main() -> int:
     import numpy as np
     import torch
 
+    if args.calibrate_copy_mib:
+        copy_calibration(torch, args.calibrate_copy_mib)
     w = build_workload(torch, np)
     for _ in range(args.warmup):
         run_step(w)
@@ -274,7 +299,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": ATTENTION_TRAFFIC_BYTES,
             "kernel": "nq_paged_attention: paged_stream_kernel<128,2> + merge_stream_kernel<128,2>",
             "bytes_per_launch": bytes_per_launch,
             "us_per_launch": round(avg_ms * 1e3, 2),
