@@ -201,6 +201,37 @@ int nq_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out, int row
  */
 int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int width, void *stream);
 
+/*
+ * Skinny projection Y[M, N] = X[M, K] . W[N, K]^T in bf16 with fp32
+ * accumulation for M <= 128 activation rows (decode buckets), with the
+ * consumer of the projection fused in.  Replaces the nn.Linear projections of
+ * the talker layer run by torch/hipBLASLt (model/layers.py:195-270: packed
+ * QKV, o_proj, gate_up, down; the codec head, executor/talker.py:231-262)
+ * and, through `epilogue`, the kernel that follows each of them:
+ *   NQ_EPI_NONE        out = bf16(Y)
+ *   NQ_EPI_ADD_RMSNORM residual = bf16(residual + bf16(Y));
+ *                      out = rmsnorm(residual) * norm_weight  (the fused
+ *                      add-RMSNorm of model/layers.py:43-79; N <= 8192)
+ *   NQ_EPI_SILU_MUL    out[M, N/2] = silu(bf16(Y[:, :N/2])) * bf16(Y[:, N/2:])
+ *                      (qwen3_tts_silu_and_mul, model/layers.py:28-40)
+ *   NQ_EPI_PARTIALS    Y is left as S = nq_linear_splits(M, N, K) fp32 planes
+ *                      [S, M, N] at the start of `workspace` (for a consumer
+ *                      that sums them itself).
+ * K is cut into S slices whose fp32 partial planes are always summed in
+ * slice order, so the result is deterministic and the same for every
+ * epilogue.  Requires N % 64 == 0 and K % 512 == 0 (K % 256 when M > 64):
+ * otherwise NQ_ERR_UNSUPPORTED (nq_linear_splits returns -1).  Row strides in
+ * elements; x, w, out, residual, norm_weight 16-byte aligned.
+ * nq_linear_workspace_bytes gives the workspace size (0 = none needed).
+ */
+enum nq_epilogue { NQ_EPI_NONE = 0, NQ_EPI_ADD_RMSNORM = 1, NQ_EPI_SILU_MUL = 2, NQ_EPI_PARTIALS = 3 };
+int nq_linear_splits(int M, int N, int K);
+int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue);
+int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
+              int epilogue, uint16_t *out, int64_t o_s0, uint16_t *residual,
+              const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
+              void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,10 @@ NQ_ERR_LAUNCH = -3
 NQ_ERR_CAPACITY = -4
 NQ_F32 = 0
 NQ_BF16 = 1
+NQ_EPI_NONE = 0
+NQ_EPI_ADD_RMSNORM = 1
+NQ_EPI_SILU_MUL = 2
+NQ_EPI_PARTIALS = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -48,8 +52,15 @@ _SIGNATURES: dict[str, list] = {
     "nq_add_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "nq_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "nq_silu_mul": [_P, _P, _I, _I, _P],
+    "nq_linear_splits": [_I, _I, _I],
+    "nq_linear_workspace_bytes": [_I, _I, _I, _I],
+    "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _L, _P],
 }
-_RESTYPES = {"nq_status_string": ctypes.c_char_p, "nq_attention_workspace_bytes": ctypes.c_int64}
+_RESTYPES = {
+    "nq_status_string": ctypes.c_char_p,
+    "nq_attention_workspace_bytes": ctypes.c_int64,
+    "nq_linear_workspace_bytes": ctypes.c_int64,
+}
 
 EXPORTED = tuple(_SIGNATURES)
 

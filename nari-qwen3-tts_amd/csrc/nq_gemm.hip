@@ -1,0 +1,260 @@
+// Skinny bf16 GEMM for the decode step: Y[M, N] = X[M, K] . W[N, K]^T with
+// M <= 128 activation rows and a weight matrix W that is read from HBM exactly
+// once.  Replaces the torch/hipBLASLt projections of the talker layer
+// (model/layers.py:195-270 QKV / o / gate_up / down, the codec head).
+//
+// At decode sizes the projection is a weight stream: 64 rows x 2 flops per
+// weight byte is far below the MFMA ridge, so the design maximises bytes in
+// flight rather than reuse.  A workgroup (4 waves) owns a K slice of KS
+// columns and a band of 64 * NTW output columns.  Each wave issues every
+// 128-bit load of its 16 * NTW weight rows over the slice at once (one-shot:
+// KS / 32 * NTW loads per lane), while the workgroup stages the matching
+// X[:, slice] block in LDS.  Then each wave runs the v_mfma_f32_16x16x32_bf16
+// chain with W as the A operand (16 output columns x 32 k) and X^T from LDS as
+// the B operand (32 k x 16 rows), so a lane ends with four consecutive output
+// columns of one row.  Slices of one band write fp32 partials [S, M, N] that a
+// second kernel reduces in a fixed order (deterministic, no atomics); with a
+// single slice the bf16 result is written directly.
+#include "nq_common.h"
+#include "nq_internal.h"
+
+namespace nq {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kGemmWaves = kGemmThreads / kWave;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &v) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &v, sizeof(r));
+    return r;
+}
+
+// LDS row pitch of the staged X block: KS bf16 + 8 bf16 of padding, so the
+// 16 rows one B-operand read touches start on distinct 4-bank groups.
+template <int KS>
+constexpr int x_pitch() {
+    return KS + 8;
+}
+
+template <int KS>
+__device__ __forceinline__ void gemm_load_w(uint4 (&wr)[KS / 32], const uint16_t *__restrict__ w, int64_t w_s0,
+                                            int n_row, int k0, int kq) {
+    const uint16_t *row = w + static_cast<int64_t>(n_row) * w_s0 + k0 + kq * 8;
+#pragma unroll
+    for (int j = 0; j < KS / 32; ++j) wr[j] = *reinterpret_cast<const uint4 *>(row + j * 32);
+}
+
+// MFMA chain of one 16-column tile over the staged slice, then its store:
+// the lane holds Y[m*16 + r16][col + kq*4 + 0..3].
+template <int MT, int KS>
+__device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint16_t *xs, int r16, int kq, int M,
+                                          int N, int col, int slice, uint16_t *__restrict__ out, int64_t o_s0,
+                                          float *__restrict__ part) {
+    floatx4_t acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KS / 32; ++j) {
+        const bf16x8_t a = as_bf16x8(wr[j]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const bf16x8_t bx =
+                as_bf16x8(*reinterpret_cast<const uint4 *>(xs + (m * 16 + r16) * x_pitch<KS>() + j * 32 + kq * 8));
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bx, acc[m], 0, 0, 0);
+        }
+        // bound how far the scheduler hoists LDS reads (register pressure)
+        if (j % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    }
+    col += kq * 4;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int row = m * 16 + r16;
+        if (row >= M) continue;
+        if (part) {
+            float *p = part + (static_cast<int64_t>(slice) * M + row) * N + col;
+            *reinterpret_cast<float4 *>(p) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+        } else {
+            uint2 o;
+            o.x = pack2_bf16(acc[m][0], acc[m][1]);
+            o.y = pack2_bf16(acc[m][2], acc[m][3]);
+            *reinterpret_cast<uint2 *>(out + row * o_s0 + col) = o;
+        }
+    }
+}
+
+// Workgroup (bx, by): K slice by, 64-column bands bx*nb .. bx*nb + nb - 1.
+// The X slice is staged once; wave w computes columns band*64 + w*16 + 0..15
+// of each band while the next band's weights are already in flight.
+template <int MT, int KS>
+__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w,
+            int64_t w_s0, int N, int nb, uint16_t *__restrict__ out, int64_t o_s0,
+            float *__restrict__ part) {
+    constexpr int kSteps = KS / 32;
+    constexpr int kRows = 16 * MT;
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kRows * x_pitch<KS>()];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;  // which 8-wide k group of the 32-k step
+    const int band0 = blockIdx.x * nb;
+    const int k0 = blockIdx.y * KS;
+
+    // 1. X[:, k0 : k0 + KS] into registers (rows >= M are zero): issued first,
+    // so that waiting for them does not wait for the weights
+    constexpr int kVecPerRow = KS / 8;
+    constexpr int kXVec = kRows * kVecPerRow / kGemmThreads;
+    static_assert(kRows * kVecPerRow % kGemmThreads == 0, "X block splits evenly over the threads");
+    uint4 xr[kXVec];
+#pragma unroll
+    for (int q = 0; q < kXVec; ++q) {
+        const int i = threadIdx.x + q * kGemmThreads;
+        const int row = i / kVecPerRow, col = i % kVecPerRow;
+        xr[q] = row < M ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + k0 + col * 8) : make_uint4(0, 0, 0, 0);
+    }
+
+    // 2. the first band's weights, all in flight together
+    uint4 wa[kSteps], wb[kSteps];
+    gemm_load_w<KS>(wa, w, w_s0, band0 * 64 + wave * 16 + r16, k0, kq);
+    // keep every weight load ahead of the wait for the X block
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int q = 0; q < kXVec; ++q) {
+        const int i = threadIdx.x + q * kGemmThreads;
+        const int row = i / kVecPerRow, col = i % kVecPerRow;
+        *reinterpret_cast<uint4 *>(xs + row * x_pitch<KS>() + col * 8) = xr[q];
+    }
+    __syncthreads();
+
+    // 3. bands in pairs: the loads of one buffer fly while the other is used
+    for (int b = 0; b < nb; b += 2) {
+        const int col_a = (band0 + b) * 64 + wave * 16;
+        if (b + 1 < nb) gemm_load_w<KS>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
+        gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part);
+        if (b + 1 >= nb) break;
+        if (b + 2 < nb) gemm_load_w<KS>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
+        gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part);
+    }
+}
+
+// Y = bf16(sum over slices of part), eight columns per thread, slices added
+// in index order (the same order the fused epilogues use).
+__global__ void __launch_bounds__(kGemmThreads)
+gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t *__restrict__ out,
+                   int64_t o_s0) {
+    const int64_t total = static_cast<int64_t>(M) * N / 8;
+    const int64_t plane = static_cast<int64_t>(M) * N;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kGemmThreads) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * kGemmThreads) {
+        float v[8];
+        sum_partials8(part + i * 8, S, plane, v);
+        const int64_t e = i * 8;
+        const int row = static_cast<int>(e / N), col = static_cast<int>(e % N);
+        uint4 o;
+        o.x = pack2_bf16(v[0], v[1]);
+        o.y = pack2_bf16(v[2], v[3]);
+        o.z = pack2_bf16(v[4], v[5]);
+        o.w = pack2_bf16(v[6], v[7]);
+        *reinterpret_cast<uint4 *>(out + row * o_s0 + col) = o;
+    }
+}
+
+// K slice per workgroup: 512 columns of K (256 when the X block has 128 rows,
+// which keeps the staged block inside 64 KiB of LDS).  Every slice is one
+// fp32 partial plane.
+int slice_of(int M) { return M > 64 ? 256 : 512; }
+
+// Bands per workgroup: the largest divisor of the band count that still
+// leaves at least one workgroup per CU; more bands per workgroup share one
+// staged X slice.
+int bands_per_wg(int bands, int splits) {
+    constexpr int kTargetWgs = 256;
+    int best = 1;
+    for (int nb = 2; nb <= 8; ++nb)
+        if (bands % nb == 0 && (bands / nb) * splits >= kTargetWgs) best = nb;
+    return best;
+}
+
+template <int MT, int KS>
+void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
+                 uint16_t *out, int64_t o_s0, float *part, hipStream_t st) {
+    const int bands = N / 64, S = K / KS;
+    const int nb = bands_per_wg(bands, S);
+    dim3 grid(bands / nb, S);
+    hipLaunchKernelGGL((gemm_kernel<MT, KS>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N, nb, out,
+                       o_s0, part);
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_linear_splits(int M, int N, int K) {
+    if (M <= 0 || M > 128 || N <= 0 || N % 64 != 0 || K <= 0 || K % slice_of(M) != 0) return -1;
+    return K / slice_of(M);
+}
+
+extern "C" int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue) {
+    const int S = nq_linear_splits(M, N, K);
+    if (S < 0 || epilogue < NQ_EPI_NONE || epilogue > NQ_EPI_PARTIALS) return -1;
+    if (S == 1 && epilogue == NQ_EPI_NONE) return 0;
+    return static_cast<int64_t>(S) * M * N * 4;
+}
+
+extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
+                         int epilogue, uint16_t *out, int64_t o_s0, uint16_t *residual,
+                         const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
+                         void *stream) {
+    NQ_CHECK_ARG(x && w && M > 0 && N > 0 && K > 0);
+    NQ_CHECK_ARG(epilogue >= NQ_EPI_NONE && epilogue <= NQ_EPI_PARTIALS);
+    const int S = nq_linear_splits(M, N, K);
+    if (S < 0) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 8 == 0 && w_s0 % 8 == 0);
+    NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0);
+    const int out_width = epilogue == NQ_EPI_SILU_MUL ? N / 2 : N;
+    if (epilogue != NQ_EPI_PARTIALS) {
+        NQ_CHECK_ARG(out && o_s0 >= out_width && o_s0 % 8 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0);
+    }
+    if (epilogue == NQ_EPI_ADD_RMSNORM) {
+        NQ_CHECK_ARG(residual && norm_weight);
+        NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(norm_weight)) % 16 == 0);
+        if (N > 8192) return NQ_ERR_UNSUPPORTED;
+    }
+    if (epilogue == NQ_EPI_SILU_MUL) NQ_CHECK_ARG(N % 16 == 0);
+    const int64_t need = nq_linear_workspace_bytes(M, N, K, epilogue);
+    NQ_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need &&
+                               reinterpret_cast<uintptr_t>(workspace) % 16 == 0));
+    float *part = need ? static_cast<float *>(workspace) : nullptr;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    switch (mt) {
+        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
+        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
+        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
+        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
+    }
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    switch (epilogue) {
+        case NQ_EPI_NONE:
+            if (S > 1) {
+                const int64_t vec = static_cast<int64_t>(M) * N / 8;
+                int blocks = static_cast<int>((vec + kGemmThreads - 1) / kGemmThreads);
+                hipLaunchKernelGGL(gemm_reduce_kernel, dim3(blocks > 2048 ? 2048 : blocks), dim3(kGemmThreads), 0,
+                                   st, part, S, M, N, out, o_s0);
+            }
+            return NQ_LAUNCH_STATUS();
+        case NQ_EPI_ADD_RMSNORM:
+            return launch_add_rmsnorm_partials(part, S, M, N, out, o_s0, residual, norm_weight, eps, st);
+        case NQ_EPI_SILU_MUL:
+            return launch_silu_mul_partials(part, S, M, N / 2, out, o_s0, st);
+        default:
+            return NQ_OK;  // partials stay in the workspace for the caller's consumer
+    }
+}

@@ -4,6 +4,7 @@
 // between the sum-of-squares reduction and the scaled store, so a row is read
 // and written exactly once.
 #include "nq_common.h"
+#include "nq_internal.h"
 
 namespace nq {
 namespace {
@@ -23,28 +24,59 @@ __device__ float norm_block_sum(float v, float *tmp) {
     return s;
 }
 
+// Source of the "hidden" operand: a bf16 tensor, or the fp32 split-K partial
+// planes of a projection, summed in plane order and rounded to bf16 (exactly
+// the value the bf16 projection output would hold).
+struct Bf16Src {
+    const uint16_t *p;
+    int64_t s0;
+    __device__ __forceinline__ void load8(int64_t row, int col, float (&x)[8]) const {
+        unpack8(*reinterpret_cast<const uint4 *>(p + row * s0 + col), x);
+    }
+};
+
+struct PartialSrc {
+    const float *p;
+    int S;
+    int64_t plane;  // elements per partial plane
+    int64_t s0;     // row stride of a plane
+    __device__ __forceinline__ void load8(int64_t row, int col, float (&x)[8]) const {
+        sum_partials8(p + row * s0 + col, S, plane, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16(x[e]));
+    }
+};
+
+template <typename Src>
 __global__ void __launch_bounds__(kNormThreads)
-add_rmsnorm_kernel(uint16_t *__restrict__ hidden, uint16_t *__restrict__ residual,
-                   const uint16_t *__restrict__ weight, int width, float eps) {
+add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
+                   uint16_t *__restrict__ residual, const uint16_t *__restrict__ weight, int width,
+                   float eps) {
     __shared__ float tmp[kNormThreads / kWave];
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * width;
+    const int64_t row = blockIdx.x;
     const int nvec = width / 8;
-    float x[kMaxVec][8];
+    float x[kMaxVec][8], w[kMaxVec][8];
     float ss = 0.f;
+    // every load of the row first (hidden, residual, weight), then the math
+    float a[kMaxVec][8], b[kMaxVec][8];
 #pragma unroll
     for (int i = 0; i < kMaxVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
-            float a[8], b[8];
-            unpack8(*reinterpret_cast<const uint4 *>(hidden + base + vi * 8), a);
-            unpack8(*reinterpret_cast<const uint4 *>(residual + base + vi * 8), b);
+            hidden.load8(row, vi * 8, a[i]);
+            unpack8(*reinterpret_cast<const uint4 *>(residual + row * width + vi * 8), b[i]);
+            unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
             uint4 packed;
             uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                pw[e / 2] = pack2_bf16(a[e] + b[e], a[e + 1] + b[e + 1]);
-            }
-            *reinterpret_cast<uint4 *>(residual + base + vi * 8) = packed;
+            for (int e = 0; e < 8; e += 2) pw[e / 2] = pack2_bf16(a[i][e] + b[i][e], a[i][e + 1] + b[i][e + 1]);
+            *reinterpret_cast<uint4 *>(residual + row * width + vi * 8) = packed;
             unpack8(packed, x[i]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
@@ -55,14 +87,12 @@ add_rmsnorm_kernel(uint16_t *__restrict__ hidden, uint16_t *__restrict__ residua
     for (int i = 0; i < kMaxVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
-            float w[8];
-            unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w);
             uint4 packed;
             uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
 #pragma unroll
             for (int e = 0; e < 8; e += 2)
-                pw[e / 2] = pack2_bf16(x[i][e] * inv * w[e], x[i][e + 1] * inv * w[e + 1]);
-            *reinterpret_cast<uint4 *>(hidden + base + vi * 8) = packed;
+                pw[e / 2] = pack2_bf16(x[i][e] * inv * w[i][e], x[i][e + 1] * inv * w[i][e + 1]);
+            *reinterpret_cast<uint4 *>(hidden_out + row * ho_s0 + vi * 8) = packed;
         }
     }
 }
@@ -101,17 +131,18 @@ rmsnorm_kernel(const uint16_t *__restrict__ xin, const uint16_t *__restrict__ we
     }
 }
 
-__global__ void silu_mul_kernel(const uint16_t *__restrict__ gate_up, uint16_t *__restrict__ out,
-                                int rows, int width) {
+template <typename Src>
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(Src gate_up, uint16_t *__restrict__ out, int64_t o_s0, int rows, int width) {
     const int nvec = width / 8;
     const int64_t total = static_cast<int64_t>(rows) * nvec;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t r = i / nvec;
-        const int64_t v = i - r * nvec;
+        const int v = static_cast<int>(i - r * nvec);
         float g[8], u[8];
-        unpack8(*reinterpret_cast<const uint4 *>(gate_up + r * 2 * width + v * 8), g);
-        unpack8(*reinterpret_cast<const uint4 *>(gate_up + r * 2 * width + width + v * 8), u);
+        gate_up.load8(r, v * 8, g);
+        gate_up.load8(r, width + v * 8, u);
         uint4 packed;
         uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
 #pragma unroll
@@ -120,13 +151,38 @@ __global__ void silu_mul_kernel(const uint16_t *__restrict__ gate_up, uint16_t *
             const float b = g[e + 1] / (1.0f + expf(-g[e + 1])) * u[e + 1];
             pw[e / 2] = pack2_bf16(a, b);
         }
-        *reinterpret_cast<uint4 *>(out + r * width + v * 8) = packed;
+        *reinterpret_cast<uint4 *>(out + r * o_s0 + v * 8) = packed;
     }
+}
+
+int silu_grid(int rows, int width) {
+    const int64_t total = static_cast<int64_t>(rows) * (width / 8);
+    int64_t grid = (total + 255) / 256;
+    return static_cast<int>(grid > 4096 ? 4096 : grid);
 }
 
 bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
+
+int launch_add_rmsnorm_partials(const float *part, int S, int rows, int width, uint16_t *hidden_out,
+                                int64_t ho_s0, uint16_t *residual, const uint16_t *weight, float eps,
+                                hipStream_t st) {
+    if (width % 8 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
+    const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
+    hipLaunchKernelGGL(add_rmsnorm_kernel<PartialSrc>, dim3(rows), dim3(kNormThreads), 0, st, src, hidden_out,
+                       ho_s0, residual, weight, width, eps);
+    return NQ_LAUNCH_STATUS();
+}
+
+int launch_silu_mul_partials(const float *part, int S, int rows, int width, uint16_t *out, int64_t o_s0,
+                             hipStream_t st) {
+    const PartialSrc src{part, S, static_cast<int64_t>(rows) * 2 * width, 2 * width};
+    hipLaunchKernelGGL(silu_mul_kernel<PartialSrc>, dim3(silu_grid(rows, width)), dim3(256), 0, st, src, out,
+                       o_s0, rows, width);
+    return NQ_LAUNCH_STATUS();
+}
+
 }  // namespace nq
 
 extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16_t *weight,
@@ -135,8 +191,10 @@ extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16
     if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
     if (!nq::al16(hidden) || !nq::al16(residual) || !nq::al16(weight)) return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
-    hipLaunchKernelGGL(nq::add_rmsnorm_kernel, dim3(rows), dim3(nq::kNormThreads), 0,
-                       static_cast<hipStream_t>(stream), hidden, residual, weight, width, eps);
+    const nq::Bf16Src src{hidden, width};
+    hipLaunchKernelGGL(nq::add_rmsnorm_kernel<nq::Bf16Src>, dim3(rows), dim3(nq::kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), src, hidden, static_cast<int64_t>(width), residual,
+                       weight, width, eps);
     return NQ_LAUNCH_STATUS();
 }
 
@@ -157,10 +215,8 @@ extern "C" int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int
     if (width % 8) return NQ_ERR_UNSUPPORTED;
     if (!nq::al16(gate_up) || !nq::al16(out)) return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
-    const int64_t total = static_cast<int64_t>(rows) * (width / 8);
-    int64_t grid = (total + 255) / 256;
-    if (grid > 4096) grid = 4096;
-    hipLaunchKernelGGL(nq::silu_mul_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), gate_up, out, rows, width);
+    const nq::Bf16Src src{gate_up, 2 * static_cast<int64_t>(width)};
+    hipLaunchKernelGGL(nq::silu_mul_kernel<nq::Bf16Src>, dim3(nq::silu_grid(rows, width)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), src, out, static_cast<int64_t>(width), rows, width);
     return NQ_LAUNCH_STATUS();
 }

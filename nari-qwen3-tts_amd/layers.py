@@ -1,8 +1,10 @@
-"""Norm and SwiGLU entry points with the reference's call shapes.
+"""Norm, SwiGLU and projection entry points with the reference's call shapes.
 
 ``qwen3_tts_add_rmsnorm`` / ``qwen3_tts_rmsnorm`` / ``qwen3_tts_silu_and_mul``
 mirror model/layers.py:28-100: the fused add-norm updates both inputs in
 place (residual <- residual + hidden, hidden <- rmsnorm(residual)).
+``linear`` is the bias-free nn.Linear of model/layers.py:195-270 for decode
+row counts (<= 128), computed by the skinny HIP GEMM.
 """
 
 from __future__ import annotations
@@ -61,4 +63,75 @@ def qwen3_tts_silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = Non
     return out
 
 
-__all__ = ["qwen3_tts_add_rmsnorm", "qwen3_tts_rmsnorm", "qwen3_tts_silu_and_mul"]
+def linear_workspace_bytes(rows: int, out_features: int, in_features: int, epilogue: int = _lib.NQ_EPI_NONE) -> int:
+    """fp32 split-K scratch the projection needs (0 when none); raises for shapes it does not cover."""
+
+    n = int(_lib.load().nq_linear_workspace_bytes(int(rows), int(out_features), int(in_features), int(epilogue)))
+    if n < 0:
+        raise TypeError(f"no HIP projection for rows={rows}, out={out_features}, in={in_features}")
+    return n
+
+
+def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None, eps=0.0, workspace=None):
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("linear needs bf16 activations and weights")
+    if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("linear needs 2-D tensors with unit inner stride")
+    rows, k = x.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError("weight in_features must match x")
+    _lib.require_device(x, weight)
+    need = linear_workspace_bytes(rows, n, k, epilogue)
+    out = torch.empty((rows, out_width), dtype=x.dtype, device=x.device) if out is None else out
+    if out.shape != (rows, out_width) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError(f"out must be bf16 [{rows}, {out_width}] with unit inner stride")
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.call(
+        "nq_linear", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k, int(epilogue),
+        out.data_ptr(), out.stride(0), _lib.ptr(residual), _lib.ptr(norm_weight), float(eps),
+        _lib.ptr(workspace) if need else None, workspace.numel() * workspace.element_size() if need else 0,
+        _lib.stream(x.device),
+    )
+    return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x @ weight.T for bf16 x [rows, in] (row stride free) and weight [out, in]."""
+
+    return _linear(x, weight, _lib.NQ_EPI_NONE, out, weight.shape[0], workspace=workspace)
+
+
+def linear_add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
+                       eps: float, out: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The projection followed by the fused add-RMSNorm: residual += x @ weight.T (bf16);
+    out = rmsnorm(residual) * norm_weight."""
+
+    for t, name in ((residual, "residual"), (norm_weight, "norm weight")):
+        _check(t, name)
+    if residual.shape != (x.shape[0], weight.shape[0]) or norm_weight.shape != (weight.shape[0],):
+        raise ValueError("residual / norm weight must match the projection output")
+    return _linear(x, weight, _lib.NQ_EPI_ADD_RMSNORM, out, weight.shape[0], residual, norm_weight, eps, workspace)
+
+
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU input: y = x @ weight.T with weight [2 * I, in] (gate rows, then up rows);
+    out = silu(y[:, :I]) * y[:, I:]."""
+
+    if weight.shape[0] % 2:
+        raise ValueError("gate_up weight needs an even number of rows")
+    return _linear(x, weight, _lib.NQ_EPI_SILU_MUL, out, weight.shape[0] // 2, workspace=workspace)
+
+
+__all__ = [
+    "linear",
+    "linear_add_rmsnorm",
+    "linear_silu_mul",
+    "linear_workspace_bytes",
+    "qwen3_tts_add_rmsnorm",
+    "qwen3_tts_rmsnorm",
+    "qwen3_tts_silu_and_mul",
+]

@@ -8,8 +8,10 @@ o-proj, fused residual add + RMSNorm, SwiGLU MLP and the next fused add-norm;
 the codec head; the fused sampler (logit masks, repetition penalty over the
 seen mask, temperature, top-k, top-p, draw) with the seen-mask update.
 
-GEMMs go through torch (hipBLASLt) in bf16; everything else is the HIP
-library.  Weights are random (N(0, 0.02), norm weights 1) because no
+The projections run on the HIP library's skinny GEMM with the following
+kernel fused in (o_proj and down with the residual add-RMSNorm, gate_up with
+SiLU-mul) whenever the bucket has at most 128 rows; larger buckets use
+torch.matmul.  Weights are random (N(0, 0.02), norm weights 1) because no
 checkpoint is available; shapes follow the Qwen3-TTS 1.7B talker.
 """
 
@@ -21,7 +23,16 @@ from types import SimpleNamespace
 import torch
 import torch.nn.functional as F
 
-from .layers import qwen3_tts_add_rmsnorm, qwen3_tts_rmsnorm, qwen3_tts_silu_and_mul
+from . import _lib
+from .layers import (
+    linear,
+    linear_add_rmsnorm,
+    linear_silu_mul,
+    linear_workspace_bytes,
+    qwen3_tts_add_rmsnorm,
+    qwen3_tts_rmsnorm,
+    qwen3_tts_silu_and_mul,
+)
 from .sampling import sample_with_uniforms, uniforms_from_counter
 
 
@@ -118,6 +129,19 @@ class TalkerDecodeStep:
         self.act = torch.zeros(rows, c.intermediate, **bf)
         self.logits = torch.zeros(rows, c.vocab, **bf)
         self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
+        q_w = c.num_qo_heads * c.head_dim
+        projections = (
+            (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
+            (c.hidden, q_w, _lib.NQ_EPI_ADD_RMSNORM),
+            (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
+            (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
+            (c.vocab, c.hidden, _lib.NQ_EPI_NONE),
+        )
+        self.use_hip_linear = all(_lib.load().nq_linear_splits(rows, n, k) > 0 for n, k, _ in projections)
+        self.linear_workspace = None
+        if self.use_hip_linear:
+            need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in projections)
+            self.linear_workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
 
     def forward(self) -> torch.Tensor:
         c = self.w.config
@@ -128,22 +152,34 @@ class TalkerDecodeStep:
         qwen3_tts_rmsnorm(self.residual, self.w.layers[0].input_norm, c.rms_eps, out=self.hidden)
         q_w = c.num_qo_heads * c.head_dim
         kv_w = c.num_kv_heads * c.head_dim
+        ws = self.linear_workspace
         for index, layer in enumerate(self.w.layers):
             ctx.select_layer(index)
-            torch.matmul(self.hidden, layer.qkv.t(), out=self.qkv)
+            nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
+            if self.use_hip_linear:
+                linear(self.hidden, layer.qkv, out=self.qkv, workspace=ws)
+            else:
+                torch.matmul(self.hidden, layer.qkv.t(), out=self.qkv)
             q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
             k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
             v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
-            attended = ctx.attend(layer.attention, q, k, v)
-            torch.matmul(attended.view(n, q_w), layer.o.t(), out=self.hidden)
-            qwen3_tts_add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
-            torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
-            qwen3_tts_silu_and_mul(self.gate_up, out=self.act)
-            torch.matmul(self.act, layer.down.t(), out=self.hidden)
-            nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
-            qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
+            attended = ctx.attend(layer.attention, q, k, v).view(n, q_w)
+            if self.use_hip_linear:
+                linear_add_rmsnorm(attended, layer.o, self.residual, layer.post_norm, c.rms_eps, self.hidden, ws)
+                linear_silu_mul(self.hidden, layer.gate_up, out=self.act, workspace=ws)
+                linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
+            else:
+                torch.matmul(attended, layer.o.t(), out=self.hidden)
+                qwen3_tts_add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
+                torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
+                qwen3_tts_silu_and_mul(self.gate_up, out=self.act)
+                torch.matmul(self.act, layer.down.t(), out=self.hidden)
+                qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
         ctx.advance_sequence_lengths()
-        torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
+        if self.use_hip_linear:
+            linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
+        else:
+            torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
         if self.use_counter_rng:
             uniforms_from_counter(self.seed, self.offsets, out=self.uniforms)
         sample_with_uniforms(

@@ -1,0 +1,139 @@
+"""Skinny HIP projection (nq_linear) vs a torch fp32 reference of the same product, and its fused
+epilogues vs the unfused kernels (bit-exact: the split-K planes are summed in one fixed order)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+# talker decode shapes (packed QKV, o_proj, gate_up, down, codec head), the
+# code-predictor shapes at 128 rows, and ragged / single-slice edge cases
+SHAPES = [
+    (64, 4096, 2048),
+    (64, 2048, 2048),
+    (64, 12288, 2048),
+    (64, 2048, 6144),
+    (64, 3072, 2048),
+    (128, 4096, 1024),
+    (128, 1024, 2048),
+    (1, 64, 512),
+    (37, 192, 1024),
+    (16, 128, 512),
+    (100, 320, 768),
+]
+
+
+def _reference(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return x.float() @ w.float().t()
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_matches_fp32_reference(nq, device, m, n, k):
+    from nari_qwen3_tts_amd.layers import linear
+
+    g = torch.Generator(device=device)
+    g.manual_seed(m * 7 + n + k)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    y = linear(x, w)
+    torch.cuda.synchronize()
+    ref = _reference(x, w)
+    err = (y.float() - ref).abs()
+    # fp32 accumulation in another order, then one bf16 rounding of the result
+    bound = 8e-3 * ref.abs() + 2e-3
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3g}"
+
+
+def test_linear_strided_rows_and_determinism(nq, device):
+    from nari_qwen3_tts_amd.layers import linear
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    m, n, k = 64, 2048, 2048
+    xbuf = torch.randn(m, k + 64, generator=g, device=device).to(torch.bfloat16)
+    x = xbuf[:, 32 : 32 + k]  # row stride k + 64, 64-byte offset
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    obuf = torch.full((m, n + 128), 7.0, dtype=torch.bfloat16, device=device)
+    out = obuf[:, :n]
+    linear(x, w, out=out)
+    first = out.clone()
+    linear(x, w, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(first, out), "split-K reduction must be deterministic"
+    assert bool((obuf[:, n:] == 7.0).all()), "columns past N must stay untouched"
+    ref = _reference(x, w)
+    assert bool(((out.float() - ref).abs() <= 8e-3 * ref.abs() + 2e-3).all())
+
+
+def test_linear_rejects_unsupported_shapes(nq, device):
+    from nari_qwen3_tts_amd.layers import linear
+
+    x = torch.zeros(8, 500, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(64, 500, dtype=torch.bfloat16, device=device)
+    with pytest.raises(TypeError):
+        linear(x, w)
+    with pytest.raises(TypeError):
+        linear(torch.zeros(200, 512, dtype=torch.bfloat16, device=device),
+               torch.zeros(64, 512, dtype=torch.bfloat16, device=device))
+
+
+@pytest.mark.parametrize("m", [64, 37, 128])
+def test_fused_add_rmsnorm_equals_unfused(nq, device, m):
+    from nari_qwen3_tts_amd.layers import linear, linear_add_rmsnorm, qwen3_tts_add_rmsnorm
+
+    g = torch.Generator(device=device)
+    g.manual_seed(11 + m)
+    k, n = (6144, 2048) if m != 128 else (1024, 1024)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    res = torch.randn(m, n, generator=g, device=device).to(torch.bfloat16)
+    nw = (torch.rand(n, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    # unfused: projection, then the add-RMSNorm kernel
+    y = linear(x, w)
+    res_a = res.clone()
+    qwen3_tts_add_rmsnorm(y, res_a, nw, 1e-6)
+    # fused
+    res_b = res.clone()
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+    linear_add_rmsnorm(x, w, res_b, nw, 1e-6, out)
+    torch.cuda.synchronize()
+    assert torch.equal(res_a, res_b)
+    assert torch.equal(y, out)
+
+
+@pytest.mark.parametrize("m", [64, 5])
+def test_fused_silu_mul_equals_unfused(nq, device, m):
+    from nari_qwen3_tts_amd.layers import linear, linear_silu_mul, qwen3_tts_silu_and_mul
+
+    g = torch.Generator(device=device)
+    g.manual_seed(21 + m)
+    k, inter = 2048, 6144
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(2 * inter, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    want = qwen3_tts_silu_and_mul(linear(x, w))
+    got = linear_silu_mul(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(want, got)
+
+
+def test_partials_epilogue_sums_to_the_projection(nq, device):
+    from nari_qwen3_tts_amd import _lib
+    from nari_qwen3_tts_amd.layers import linear, linear_workspace_bytes
+
+    g = torch.Generator(device=device)
+    g.manual_seed(31)
+    m, n, k = 64, 4096, 2048
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    splits = int(_lib.load().nq_linear_splits(m, n, k))
+    ws = torch.empty(linear_workspace_bytes(m, n, k, _lib.NQ_EPI_PARTIALS), dtype=torch.uint8, device=device)
+    _lib.call("nq_linear", x.data_ptr(), k, w.data_ptr(), k, m, n, k, _lib.NQ_EPI_PARTIALS, None, 0, None, None,
+              0.0, ws.data_ptr(), ws.numel(), _lib.stream(device))
+    planes = ws.view(torch.float32)[: splits * m * n].view(splits, m, n)
+    total = planes[0].clone()
+    for s in range(1, splits):
+        total += planes[s]
+    torch.cuda.synchronize()
+    assert torch.equal(total.to(torch.bfloat16), linear(x, w))
