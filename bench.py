@@ -232,25 +232,7 @@ def copy_calibration(torch, mib: int, reps: int = 4) -> None:
     log(f"copy calibration: {reps} x {mib} MiB device copies, {us:.1f} us each ({2 * n / us / 1e3:.0f} GB/s r+w)")
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
-                    help="first run plain device copies of this many MiB (counter calibration)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: the serving path shards by independent request rows with no "
-              "per-step exchange, and this build has no multi-GPU leg (use --gpus 1).", file=sys.stderr)
-        return 2
-
-    import numpy as np
-    import torch
-
-    if args.calibrate_copy_mib:
-        copy_calibration(torch, args.calibrate_copy_mib)
+def talker_decode(args, torch, np) -> dict:
     w = build_workload(torch, np)
     for _ in range(args.warmup):
         run_step(w)
@@ -312,6 +294,153 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, np, w)
+    return result
+
+
+CP_ROWS = 128
+CP_SEED = 1004
+
+
+def code_predictor(args, torch, np) -> dict:
+    """Code-predictor frame batch: 128 frames, 5 layers (hidden 1024, 16/8 heads of 64, SwiGLU 3072),
+    15 sequential codebook groups over a 2048 vocab, top-k 50 / T 0.9, one hipGraph replay per batch."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.code_predictor import CodePredictorConfig, CodePredictorFrame, CodePredictorWeights
+    from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
+
+    dev = torch.device("cuda:0")
+    cfg = CodePredictorConfig()
+    weights = CodePredictorWeights(cfg, dev, seed=CP_SEED)
+    frame = CodePredictorFrame(weights, CP_ROWS, use_counter_rng=True)
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(CP_SEED)
+    frame.layer0_token.copy_(torch.randint(0, cfg.talker_vocab, (CP_ROWS,), generator=gen))
+    frame.past_hidden.copy_(torch.randn(CP_ROWS, cfg.talker_hidden, generator=gen).to(torch.bfloat16))
+    frame.temperature.fill_(0.9)
+    frame.top_k.fill_(50)
+    frame.top_p.fill_(1.0)
+    frame.seed.copy_(torch.randint(0, 1 << 40, (CP_ROWS,), generator=gen))
+    frame.offsets.copy_(torch.arange(CP_ROWS * 15).view(CP_ROWS, 15))
+    call = HipGraphCaptureDriver(device=dev).capture(frame.forward)
+    for _ in range(args.warmup):
+        call.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        call.replay()
+    end.record(stream)
+    end.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    c = cfg
+    frame_bytes = (weights.weight_bytes_per_pass() * c.num_code_groups
+                   + weights.lm_head.numel() * 2 + weights.proj_w.numel() * 2)
+    achieved = frame_bytes / (ms / 1e3) / 1e9
+    log(f"code predictor: {ms:.3f} ms per {CP_ROWS}-frame batch, {frame_bytes / 1e9:.3f} GB -> {achieved:.0f} GB/s")
+    result = {
+        "metric": "code-predictor frames/s (128 frames x 15 codebook steps per batch)",
+        "value": round(CP_ROWS * args.steps / elapsed, 1),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random layer-0 tokens and talker states)",
+        "config": {
+            "workload": "code-predictor frame: 128 rows, 5 layers, hidden 1024, 16q/8kv heads x 64, SwiGLU 3072, "
+                        "vocab 2048, 15 groups, top-k 50, T 0.9, hipGraph replay",
+            "global_batch": CP_ROWS,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "whole frame graph (weights of 16 passes + 15 heads per replay)",
+            "bytes_per_launch": int(frame_bytes),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = code_predictor_cpu_baseline(torch, np, weights, frame)
+    return result
+
+
+def code_predictor_cpu_baseline(torch, np, weights, frame, budget_s: float = 10.0) -> dict:
+    """The oracle frame (numpy) on the host cores over as many rows as fit the budget, per frame."""
+
+    from oracle import bf16 as o_bf16
+    from oracle import code_predictor as o_cp
+
+    def host(t):
+        t = t.detach().cpu()
+        if t.dtype == torch.bfloat16:
+            return o_bf16.from_bits(t.contiguous().view(torch.int16).numpy().view(np.uint16))
+        return t.numpy()
+
+    c = weights.config
+    hw = dict(layers=[{k: host(v) for k, v in vars(L).items()} for L in weights.layers],
+              final_norm=host(weights.final_norm), lm_head=host(weights.lm_head), proj_w=host(weights.proj_w),
+              proj_b=host(weights.proj_b), layer0_embedding=host(weights.layer0_embedding),
+              codec_embedding=host(weights.codec_embedding), projected_layer0=host(weights.projected_layer0),
+              projected_residual=host(weights.projected_residual))
+    hcfg = dict(num_qo_heads=c.num_qo_heads, num_kv_heads=c.num_kv_heads, head_dim=c.head_dim, rms_eps=c.rms_eps,
+                rope_theta=c.rope_theta, num_code_groups=c.num_code_groups)
+    tokens = host(frame.tokens)
+    rows, done, elapsed = 16, 0, 0.0
+    while elapsed < budget_s and done < CP_ROWS:
+        sl = slice(done, done + rows)
+        t0 = time.perf_counter()
+        o_cp.whole_frame(hw, hcfg, host(frame.layer0_token)[sl], host(frame.past_hidden)[sl], tokens[:, sl])
+        elapsed += time.perf_counter() - t0
+        done += rows
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # noqa: BLE001 - threadpoolctl is optional
+        cores = 1
+    return dict(value=done / elapsed, unit="frames/s", cores=int(cores), kind="port",
+                sample=f"oracle frame (numpy, teacher-forced) for {done} of {CP_ROWS} rows in {elapsed:.1f}s")
+
+
+WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="talker-decode",
+                    help="talker-decode is the serving metric; the others measure the neighbouring hot-path rows")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run plain device copies of this many MiB (counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the serving path shards by independent request rows with no "
+              "per-step exchange, and this build has no multi-GPU leg (use --gpus 1).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    if args.calibrate_copy_mib:
+        copy_calibration(torch, args.calibrate_copy_mib)
+    result = WORKLOADS[args.workload](args, torch, np)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -208,7 +208,8 @@ int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int width, voi
  * the talker layer run by torch/hipBLASLt (model/layers.py:195-270: packed
  * QKV, o_proj, gate_up, down; the codec head, executor/talker.py:231-262)
  * and, through `epilogue`, the kernel that follows each of them:
- *   NQ_EPI_NONE        out = bf16(Y)
+ *   NQ_EPI_NONE        out = bf16(Y + bias) (bias [N] bf16 or NULL: the
+ *                      biased nn.Linear, one rounding like a GEMM epilogue)
  *   NQ_EPI_ADD_RMSNORM residual = bf16(residual + bf16(Y));
  *                      out = rmsnorm(residual) * norm_weight  (the fused
  *                      add-RMSNorm of model/layers.py:43-79; N <= 8192)
@@ -228,7 +229,7 @@ enum nq_epilogue { NQ_EPI_NONE = 0, NQ_EPI_ADD_RMSNORM = 1, NQ_EPI_SILU_MUL = 2,
 int nq_linear_splits(int M, int N, int K);
 int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue);
 int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
-              int epilogue, uint16_t *out, int64_t o_s0, uint16_t *residual,
+              int epilogue, const uint16_t *bias, uint16_t *out, int64_t o_s0, uint16_t *residual,
               const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
               void *stream);
 

@@ -54,7 +54,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_silu_mul": [_P, _P, _I, _I, _P],
     "nq_linear_splits": [_I, _I, _I],
     "nq_linear_workspace_bytes": [_I, _I, _I, _I],
-    "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _L, _P],
+    "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P, _F, _P, _L, _P],
 }
 _RESTYPES = {
     "nq_status_string": ctypes.c_char_p,

@@ -1,0 +1,204 @@
+"""Code-predictor frame loop on the GPU: one hipGraph-capturable pass that turns
+each row's layer-0 codec token and talker hidden state into the 16-code frame.
+
+Mirrors ``CodePredictorExecutor.whole_frame`` (executor/code_predictor.py:
+159-235) and ``Qwen3TTSCodePredictor.forward_depth_unrolled`` on its fused
+branch (model/components.py:254-356):
+
+- pass 0 runs the small->MTP projection of ``past_hidden`` through the layers
+  at cache position 0 (only the K/V it writes matter);
+- codec_sum starts as the layer-0 embedding of the layer-0 token, the first
+  input is the projected layer-0 embedding of that token;
+- for group g = 1..15: the layers at cache position g with the final norm,
+  logits = hidden @ lm_head[g-1]^T, one sampled token per row, codec_sum +=
+  codec_embedding[g-1][token], next input = projected codec embedding.
+
+Each layer is: RMSNorm (first layer; later ones come out of the previous
+epilogue), packed QKV projection, q/k RMSNorm + RoPE with the K/V write into
+the dense 16-slot cache (no bf16 rounding before the rotation,
+model/kernels.py:335-405), short-cache attention over the valid positions,
+o_proj with the residual add + post-attention RMSNorm fused, gate_up with
+SiLU-mul fused, down with the residual add + next RMSNorm fused.  The residual
+adds are the reference's plain bf16 ``residual + projection`` followed by the
+norm (components.py:331-346), which is what the fused epilogue computes.
+
+Sampling takes uniforms ([15, rows], one per row and group); with
+``use_counter_rng`` they are derived on the device from (seed, offsets[:, g-1])
+by Philox-4x32-10 like the reference's counter-addressed draws.  Rows with
+temperature 0 take the argmax (the reference maps them to top-1,
+executor/code_predictor.py:149-162, which selects the same token).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from types import SimpleNamespace
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .kernels import decode_attn_nhd_short_cache, paired_qk_norm_rope_dense_cache_
+from .layers import linear, linear_add_rmsnorm, linear_silu_mul, linear_workspace_bytes, qwen3_tts_rmsnorm
+from .sampling import sample_with_uniforms, uniforms_from_counter
+
+
+@dataclass(frozen=True)
+class CodePredictorConfig:
+    num_layers: int = 5
+    hidden: int = 1024
+    num_qo_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 64
+    intermediate: int = 3072
+    vocab: int = 2048
+    talker_hidden: int = 2048
+    talker_vocab: int = 3072
+    num_code_groups: int = 16
+    rms_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.num_qo_heads + 2 * self.num_kv_heads) * self.head_dim
+
+
+class CodePredictorWeights:
+    """Random-init code-predictor parameters (bf16) plus the tables the executor derives once:
+    ``projected_layer0`` = projection(layer-0 embedding) and ``projected_residual[g]`` =
+    projection(codec_embedding[g]) for g < 14 (executor/code_predictor.py:72-88)."""
+
+    def __init__(self, config: CodePredictorConfig, device: torch.device, seed: int = 0, std: float = 0.02) -> None:
+        self.config = c = config
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        bf = dict(dtype=torch.bfloat16, device=device)
+
+        def randn(*shape, scale=std):
+            return (torch.randn(*shape, generator=g, device=device) * scale).to(torch.bfloat16)
+
+        self.layers = [
+            SimpleNamespace(
+                input_norm=torch.ones(c.hidden, **bf),
+                qkv=randn(c.qkv_width, c.hidden),
+                o=randn(c.hidden, c.num_qo_heads * c.head_dim),
+                post_norm=torch.ones(c.hidden, **bf),
+                gate_up=randn(2 * c.intermediate, c.hidden),
+                down=randn(c.hidden, c.intermediate),
+                q_norm=torch.ones(c.head_dim, **bf),
+                k_norm=torch.ones(c.head_dim, **bf),
+            )
+            for _ in range(c.num_layers)
+        ]
+        self.final_norm = torch.ones(c.hidden, **bf)
+        groups = c.num_code_groups - 1
+        self.lm_head = randn(groups, c.vocab, c.hidden)
+        self.proj_w = randn(c.hidden, c.talker_hidden)
+        self.proj_b = randn(c.hidden)
+        self.layer0_embedding = randn(c.talker_vocab, c.talker_hidden, scale=1.0)
+        self.codec_embedding = randn(groups, c.vocab, c.talker_hidden, scale=1.0)
+        # derived once, as the executor does (torch GEMM with bias; not on the per-frame path)
+        self.projected_layer0 = F.linear(self.layer0_embedding, self.proj_w, self.proj_b).contiguous()
+        self.projected_residual = torch.stack(
+            [F.linear(self.codec_embedding[i], self.proj_w, self.proj_b) for i in range(groups - 1)]
+        ).contiguous()
+
+    def weight_bytes_per_pass(self) -> int:
+        c = self.config
+        per_layer = c.qkv_width * c.hidden + c.hidden * c.num_qo_heads * c.head_dim + 3 * c.intermediate * c.hidden
+        return 2 * per_layer * c.num_layers
+
+
+class CodePredictorFrame:
+    """Static buffers for ``rows`` physical rows and the whole-frame forward."""
+
+    def __init__(self, weights: CodePredictorWeights, rows: int, *, use_counter_rng: bool = False) -> None:
+        c = weights.config
+        if not 1 <= rows <= 128:
+            raise ValueError("the code-predictor frame runs 1..128 rows")
+        self.w = weights
+        self.rows = rows
+        self.use_counter_rng = use_counter_rng
+        dev = weights.lm_head.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        groups = c.num_code_groups
+        # inputs
+        self.layer0_token = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.past_hidden = torch.zeros(rows, c.talker_hidden, **bf)
+        self.temperature = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.top_k = torch.ones(rows, dtype=torch.int32, device=dev)
+        self.top_p = torch.ones(rows, dtype=torch.float32, device=dev)
+        self.seed = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.offsets = torch.zeros(rows, groups - 1, dtype=torch.long, device=dev)
+        self.uniforms = torch.zeros(groups - 1, rows, dtype=torch.float32, device=dev)
+        self.position_ids = torch.arange(groups, dtype=torch.long, device=dev).unsqueeze(0).repeat(rows, 1)
+        # outputs
+        self.frames = torch.zeros(rows, groups, dtype=torch.long, device=dev)
+        self.tokens = torch.zeros(groups - 1, rows, dtype=torch.long, device=dev)
+        self.codec_sum = torch.zeros(rows, c.talker_hidden, **bf)
+        self.logits = torch.zeros(groups - 1, rows, c.vocab, **bf)
+        # state and work buffers
+        self.kv_cache = torch.zeros(c.num_layers, rows, 2, groups, c.num_kv_heads, c.head_dim, **bf)
+        self.h = torch.zeros(rows, c.hidden, **bf)  # residual stream
+        self.x = torch.zeros(rows, c.hidden, **bf)  # normalised stream
+        self.qkv = torch.zeros(rows, c.qkv_width, **bf)
+        self.att = torch.zeros(rows, c.num_qo_heads, c.head_dim, **bf)
+        self.act = torch.zeros(rows, c.intermediate, **bf)
+        shapes = (
+            (c.hidden, c.talker_hidden, _lib.NQ_EPI_NONE),
+            (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
+            (c.hidden, c.num_qo_heads * c.head_dim, _lib.NQ_EPI_ADD_RMSNORM),
+            (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
+            (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
+            (c.vocab, c.hidden, _lib.NQ_EPI_NONE),
+        )
+        need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in shapes)
+        self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+
+    def _layers(self, cache_pos: int) -> None:
+        c, ws = self.w.config, self.workspace
+        n = self.rows
+        q_w, kv_w = c.num_qo_heads * c.head_dim, c.num_kv_heads * c.head_dim
+        positions = self.position_ids[:, cache_pos]
+        layers = self.w.layers
+        qwen3_tts_rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
+        for index, L in enumerate(layers):
+            linear(self.x, L.qkv, out=self.qkv, workspace=ws)
+            q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
+            k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
+            v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
+            cache = self.kv_cache[index]
+            paired_qk_norm_rope_dense_cache_(q, k, v, L.q_norm, L.k_norm, positions, c.rms_eps, c.rope_theta,
+                                             cache[:, 0], cache[:, 1], cache_pos)
+            decode_attn_nhd_short_cache(q, cache[:, 0], cache[:, 1], cache_pos + 1, out=self.att)
+            linear_add_rmsnorm(self.att.view(n, q_w), L.o, self.h, L.post_norm, c.rms_eps, self.x, ws)
+            linear_silu_mul(self.x, L.gate_up, out=self.act, workspace=ws)
+            nxt = self.w.final_norm if index + 1 == len(layers) else layers[index + 1].input_norm
+            linear_add_rmsnorm(self.act, L.down, self.h, nxt, c.rms_eps, self.x, ws)
+
+    def forward(self) -> tuple[torch.Tensor, torch.Tensor]:
+        c, w, ws = self.w.config, self.w, self.workspace
+        groups = c.num_code_groups
+        # pass 0: the talker hidden state fills cache position 0
+        linear(self.past_hidden, w.proj_w, out=self.h, workspace=ws, bias=w.proj_b)
+        self._layers(0)
+        self.frames[:, 0].copy_(self.layer0_token)
+        torch.index_select(w.layer0_embedding, 0, self.layer0_token, out=self.codec_sum)
+        torch.index_select(w.projected_layer0, 0, self.layer0_token, out=self.h)
+        for group in range(1, groups):
+            self._layers(group)
+            logits = self.logits[group - 1]
+            linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
+            u = self.uniforms[group - 1]
+            if self.use_counter_rng:
+                uniforms_from_counter(self.seed, self.offsets[:, group - 1], out=u)
+            token = self.tokens[group - 1]
+            sample_with_uniforms(logits, self.temperature, self.top_k, self.top_p, u, out=token)
+            self.codec_sum.add_(F.embedding(token, w.codec_embedding[group - 1]))
+            if group < groups - 1:
+                torch.index_select(w.projected_residual[group - 1], 0, token, out=self.h)
+        self.frames[:, 1:].copy_(self.tokens.t())
+        return self.frames, self.codec_sum
+
+
+__all__ = ["CodePredictorConfig", "CodePredictorFrame", "CodePredictorWeights"]

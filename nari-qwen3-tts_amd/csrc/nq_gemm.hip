@@ -53,7 +53,7 @@ __device__ __forceinline__ void gemm_load_w(uint4 (&wr)[KS / 32], const uint16_t
 template <int MT, int KS>
 __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint16_t *xs, int r16, int kq, int M,
                                           int N, int col, int slice, uint16_t *__restrict__ out, int64_t o_s0,
-                                          float *__restrict__ part) {
+                                          float *__restrict__ part, const uint16_t *__restrict__ bias) {
     floatx4_t acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -70,6 +70,11 @@ __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint
         if (j % 2 == 1) __builtin_amdgcn_sched_barrier(0);
     }
     col += kq * 4;
+    float b4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias && !part) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b4[e] = bf16_to_f32(bias[col + e]);
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const int row = m * 16 + r16;
@@ -79,8 +84,8 @@ __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint
             *reinterpret_cast<float4 *>(p) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
         } else {
             uint2 o;
-            o.x = pack2_bf16(acc[m][0], acc[m][1]);
-            o.y = pack2_bf16(acc[m][2], acc[m][3]);
+            o.x = pack2_bf16(acc[m][0] + b4[0], acc[m][1] + b4[1]);
+            o.y = pack2_bf16(acc[m][2] + b4[2], acc[m][3] + b4[3]);
             *reinterpret_cast<uint2 *>(out + row * o_s0 + col) = o;
         }
     }
@@ -93,7 +98,7 @@ template <int MT, int KS>
 __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w,
             int64_t w_s0, int N, int nb, uint16_t *__restrict__ out, int64_t o_s0,
-            float *__restrict__ part) {
+            float *__restrict__ part, const uint16_t *__restrict__ bias) {
     constexpr int kSteps = KS / 32;
     constexpr int kRows = 16 * MT;
     __shared__ __attribute__((aligned(16))) uint16_t xs[kRows * x_pitch<KS>()];
@@ -136,10 +141,10 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     for (int b = 0; b < nb; b += 2) {
         const int col_a = (band0 + b) * 64 + wave * 16;
         if (b + 1 < nb) gemm_load_w<KS>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
-        gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part);
+        gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part, bias);
         if (b + 1 >= nb) break;
         if (b + 2 < nb) gemm_load_w<KS>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
-        gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part);
+        gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part, bias);
     }
 }
 
@@ -147,7 +152,7 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
 // in index order (the same order the fused epilogues use).
 __global__ void __launch_bounds__(kGemmThreads)
 gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t *__restrict__ out,
-                   int64_t o_s0) {
+                   int64_t o_s0, const uint16_t *__restrict__ bias) {
     const int64_t total = static_cast<int64_t>(M) * N / 8;
     const int64_t plane = static_cast<int64_t>(M) * N;
     for (int64_t i = blockIdx.x * static_cast<int64_t>(kGemmThreads) + threadIdx.x; i < total;
@@ -156,6 +161,12 @@ gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t
         sum_partials8(part + i * 8, S, plane, v);
         const int64_t e = i * 8;
         const int row = static_cast<int>(e / N), col = static_cast<int>(e % N);
+        if (bias) {
+            float bv[8];
+            unpack8(*reinterpret_cast<const uint4 *>(bias + col), bv);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] += bv[k];
+        }
         uint4 o;
         o.x = pack2_bf16(v[0], v[1]);
         o.y = pack2_bf16(v[2], v[3]);
@@ -183,12 +194,12 @@ int bands_per_wg(int bands, int splits) {
 
 template <int MT, int KS>
 void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
-                 uint16_t *out, int64_t o_s0, float *part, hipStream_t st) {
+                 uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
     const int bands = N / 64, S = K / KS;
     const int nb = bands_per_wg(bands, S);
     dim3 grid(bands / nb, S);
     hipLaunchKernelGGL((gemm_kernel<MT, KS>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N, nb, out,
-                       o_s0, part);
+                       o_s0, part, bias);
 }
 
 }  // namespace
@@ -209,9 +220,9 @@ extern "C" int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue) 
 }
 
 extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
-                         int epilogue, uint16_t *out, int64_t o_s0, uint16_t *residual,
-                         const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
-                         void *stream) {
+                         int epilogue, const uint16_t *bias, uint16_t *out, int64_t o_s0,
+                         uint16_t *residual, const uint16_t *norm_weight, float eps, void *workspace,
+                         int64_t workspace_bytes, void *stream) {
     NQ_CHECK_ARG(x && w && M > 0 && N > 0 && K > 0);
     NQ_CHECK_ARG(epilogue >= NQ_EPI_NONE && epilogue <= NQ_EPI_PARTIALS);
     const int S = nq_linear_splits(M, N, K);
@@ -228,6 +239,7 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
         if (N > 8192) return NQ_ERR_UNSUPPORTED;
     }
     if (epilogue == NQ_EPI_SILU_MUL) NQ_CHECK_ARG(N % 16 == 0);
+    NQ_CHECK_ARG(!bias || (epilogue == NQ_EPI_NONE && reinterpret_cast<uintptr_t>(bias) % 16 == 0));
     const int64_t need = nq_linear_workspace_bytes(M, N, K, epilogue);
     NQ_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need &&
                                reinterpret_cast<uintptr_t>(workspace) % 16 == 0));
@@ -235,10 +247,10 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
     switch (mt) {
-        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
-        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
-        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
-        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, st); break;
+        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
+        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
+        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
+        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
     }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     switch (epilogue) {
@@ -247,7 +259,7 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
                 const int64_t vec = static_cast<int64_t>(M) * N / 8;
                 int blocks = static_cast<int>((vec + kGemmThreads - 1) / kGemmThreads);
                 hipLaunchKernelGGL(gemm_reduce_kernel, dim3(blocks > 2048 ? 2048 : blocks), dim3(kGemmThreads), 0,
-                                   st, part, S, M, N, out, o_s0);
+                                   st, part, S, M, N, out, o_s0, bias);
             }
             return NQ_LAUNCH_STATUS();
         case NQ_EPI_ADD_RMSNORM:

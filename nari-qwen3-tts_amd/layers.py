@@ -72,7 +72,8 @@ def linear_workspace_bytes(rows: int, out_features: int, in_features: int, epilo
     return n
 
 
-def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None, eps=0.0, workspace=None):
+def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None, eps=0.0, workspace=None,
+            bias=None):
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("linear needs bf16 activations and weights")
     if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or weight.stride(1) != 1:
@@ -90,7 +91,7 @@ def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     _lib.call(
         "nq_linear", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k, int(epilogue),
-        out.data_ptr(), out.stride(0), _lib.ptr(residual), _lib.ptr(norm_weight), float(eps),
+        _lib.ptr(bias), out.data_ptr(), out.stride(0), _lib.ptr(residual), _lib.ptr(norm_weight), float(eps),
         _lib.ptr(workspace) if need else None, workspace.numel() * workspace.element_size() if need else 0,
         _lib.stream(x.device),
     )
@@ -98,10 +99,14 @@ def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
-           workspace: torch.Tensor | None = None) -> torch.Tensor:
-    """out = x @ weight.T for bf16 x [rows, in] (row stride free) and weight [out, in]."""
+           workspace: torch.Tensor | None = None, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """out = x @ weight.T (+ bias) for bf16 x [rows, in] (row stride free) and weight [out, in]."""
 
-    return _linear(x, weight, _lib.NQ_EPI_NONE, out, weight.shape[0], workspace=workspace)
+    if bias is not None:
+        _check(bias, "bias")
+        if bias.shape != (weight.shape[0],):
+            raise ValueError("bias must match out_features")
+    return _linear(x, weight, _lib.NQ_EPI_NONE, out, weight.shape[0], workspace=workspace, bias=bias)
 
 
 def linear_add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,

@@ -11,7 +11,7 @@ Restates the arithmetic of the attention calls on the hot path:
   its CPU reference ``_depth_attention`` (model/components.py:235-252).
 
 All math is fp32 over bf16-valued inputs.  Pinned by
-tests/test_oracle_attention.py with closed forms (kv_len = 1 gives V, equal
+tests/test_oracle_numerics.py with closed forms (kv_len = 1 gives V, equal
 keys give the mean of V) and against torch's scaled_dot_product_attention
 on the CPU.
 """

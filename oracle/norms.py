@@ -3,7 +3,7 @@
 Restates model/layers.py:103-115 (RMSNorm: fp32 x * rsqrt(mean(x^2) + eps)
 * weight, cast back to bf16), :78-79 (residual = residual + hidden in bf16,
 then the norm of the rounded sum) and :39-40 (silu(gate) * up).  Pinned by
-tests/test_oracle_norms.py against torch's own CPU ops on the same inputs.
+tests/test_oracle_numerics.py against torch's own CPU ops on the same inputs.
 """
 
 from __future__ import annotations

@@ -12,7 +12,7 @@ the dense variant (:163-248):
 
 q and k are returned rotated (bf16 values as fp32); the K cache receives the
 rotated k, the V cache the unchanged v (:78-91).  Pinned by
-tests/test_oracle_qk_rope.py: position 0 is the identity rotation, the
+tests/test_oracle_numerics.py: position 0 is the identity rotation, the
 rotation preserves each (i, i+D/2) pair's norm, and the result matches the
 reference's CPU RoPE formulation (model/components.py:213-233) written with
 torch on the CPU.

@@ -129,11 +129,26 @@ def test_partials_epilogue_sums_to_the_projection(nq, device):
     w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
     splits = int(_lib.load().nq_linear_splits(m, n, k))
     ws = torch.empty(linear_workspace_bytes(m, n, k, _lib.NQ_EPI_PARTIALS), dtype=torch.uint8, device=device)
-    _lib.call("nq_linear", x.data_ptr(), k, w.data_ptr(), k, m, n, k, _lib.NQ_EPI_PARTIALS, None, 0, None, None,
-              0.0, ws.data_ptr(), ws.numel(), _lib.stream(device))
+    _lib.call("nq_linear", x.data_ptr(), k, w.data_ptr(), k, m, n, k, _lib.NQ_EPI_PARTIALS, None, None, 0, None,
+              None, 0.0, ws.data_ptr(), ws.numel(), _lib.stream(device))
     planes = ws.view(torch.float32)[: splits * m * n].view(splits, m, n)
     total = planes[0].clone()
     for s in range(1, splits):
         total += planes[s]
     torch.cuda.synchronize()
     assert torch.equal(total.to(torch.bfloat16), linear(x, w))
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 1024, 2048), (8, 128, 512)])
+def test_linear_bias_single_rounding(nq, device, m, n, k):
+    from nari_qwen3_tts_amd.layers import linear
+
+    g = torch.Generator(device=device)
+    g.manual_seed(41 + m)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    b = torch.randn(n, generator=g, device=device).to(torch.bfloat16)
+    y = linear(x, w, bias=b)
+    torch.cuda.synchronize()
+    ref = _reference(x, w) + b.float()
+    assert bool(((y.float() - ref).abs() <= 8e-3 * ref.abs() + 2e-3).all())
