@@ -416,7 +416,129 @@ def code_predictor_cpu_baseline(torch, np, weights, frame, budget_s: float = 10.
                 sample=f"oracle frame (numpy, teacher-forced) for {done} of {CP_ROWS} rows in {elapsed:.1f}s")
 
 
-WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor}
+CODEC_STREAMS = 32
+CODEC_SEED = 1005
+
+
+def codec_flops(cfg, frames: int) -> float:
+    """Multiply-adds x 2 of one step over `frames` fresh frames (convolutions as implicit GEMMs)."""
+
+    d, hd = cfg.dim, cfg.heads * cfg.head_dim
+    f = 2.0 * frames * d * d * 3                                   # pre-conv
+    f += 2.0 * frames * (d * d * 2 + cfg.layers * (d * 3 * hd + hd * d + 2 * d * cfg.mlp))
+    f += 2.0 * frames * cfg.layers * cfg.heads * cfg.window * cfg.head_dim * 2   # window attention
+    u = 1
+    for s in cfg.up_strides:
+        f += 2.0 * frames * u * d * d * 2 * s                      # transconv
+        u *= s
+        f += 2.0 * frames * u * (d * 7 + 2 * d * cfg.convnext_mlp)  # dwconv + pointwise pair
+    ch = cfg.dec_channels
+    f += 2.0 * frames * u * d * ch[0] * 7
+    for i, s in enumerate(cfg.dec_strides):
+        f += 2.0 * frames * u * ch[i] * ch[i + 1] * 2 * s
+        u *= s
+        f += 2.0 * frames * u * len(cfg.dilations) * (ch[i + 1] * ch[i + 1] * 8)
+    f += 2.0 * frames * u * ch[-1] * 7
+    return f
+
+
+def codec_step(args, torch, np) -> dict:
+    """Incremental codec step: 32 streams with warm state, fresh chunks of U{12..48} frames each."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.codec import CodecConfig, CodecWeights, IncrementalCodecDecoder
+
+    dev = torch.device("cuda:0")
+    cfg = CodecConfig()
+    weights = CodecWeights(cfg, dev, seed=CODEC_SEED)
+    dec = IncrementalCodecDecoder(weights, max_streams=CODEC_STREAMS)
+    rng = np.random.default_rng(CODEC_SEED)
+    states = [dec.new_state() for _ in range(CODEC_STREAMS)]
+
+    def chunk(frames):
+        return [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, int(f))))
+                for f in frames]
+
+    dec(chunk([cfg.retained_context] * CODEC_STREAMS), states)  # warm state: one full window per stream
+    frames = rng.integers(12, 49, size=CODEC_STREAMS)
+    batches = [chunk(frames) for _ in range(args.warmup + args.steps)]
+    for i in range(args.warmup):
+        dec(batches[i], states)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        wav, pcm = dec(batches[args.warmup + i], states)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1000.0 / args.steps
+    samples = int(frames.sum()) * cfg.samples_per_frame
+    flops = codec_flops(cfg, int(frames.sum()))
+    achieved = flops / (ms / 1e3) / 1e12
+    log(f"codec step: {ms:.3f} ms for {int(frames.sum())} frames / {samples} samples, {flops / 1e9:.1f} GFLOP "
+        f"-> {achieved:.1f} TFLOP/s")
+    result = {
+        "metric": "codec step: 24 kHz PCM samples/s (32 streams, fresh chunks U{12..48} frames)",
+        "value": round(samples * args.steps / elapsed, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (random-init causal decoder, random codes, warm 25-frame state)",
+        "config": {
+            "workload": "incremental codec step: 32 streams, chunks U{12..48} frames x 16 codebooks, dim 512, "
+                        "8 sliding-window layers, transconv+ConvNeXt x4, decoder blocks x500 -> 24 kHz fp32 PCM",
+            "global_batch": CODEC_STREAMS,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": 157.3,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / 157.3, 4),
+            "traffic": None,
+            "kernel": "whole step (fp32 convolutions, transconvs, window attention, projections)",
+            "flops_per_step": flops,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = codec_cpu_baseline(np, weights, cfg)
+    return result
+
+
+def codec_cpu_baseline(np, weights, cfg, budget_s: float = 10.0) -> dict:
+    """The oracle codec (numpy) on the host cores: as many 12-frame chunks as fit the budget."""
+
+    from oracle import codec as o_codec
+
+    w = weights.host()
+    rng = np.random.default_rng(CODEC_SEED + 1)
+    st = o_codec.empty_state(cfg.as_dict())
+    done, elapsed = 0, 0.0
+    while elapsed < budget_s:
+        codes = rng.integers(0, cfg.codebook_size, size=(12, cfg.num_quantizers))
+        t0 = time.perf_counter()
+        o_codec.decode_incremental(w, cfg.as_dict(), codes, st)
+        elapsed += time.perf_counter() - t0
+        done += 12
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # noqa: BLE001 - threadpoolctl is optional
+        cores = 1
+    return dict(value=done * cfg.samples_per_frame / elapsed, unit="samples/s", cores=int(cores), kind="port",
+                sample=f"oracle codec (numpy) over {done} frames of one stream in 12-frame chunks, {elapsed:.1f}s")
+
+
+WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor, "codec": codec_step}
 
 
 def main() -> int:

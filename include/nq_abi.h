@@ -233,6 +233,80 @@ int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, 
               const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
               void *stream);
 
+/*
+ * Incremental codec-decoder step (fp32, channels-last [T, C]).  Replaces the
+ * stateful pieces of Qwen3TTSIncrementalDecoder (model/incremental_codec.py):
+ * the fresh rows of B streams are concatenated; stream b owns frames
+ * [offsets[b], offsets[b+1]) (device int32 [B+1]) and, at a stage with u
+ * samples per frame, rows [offsets[b]*u, offsets[b+1]*u).  Stream b's state
+ * lives in slot slots[b] of the state arrays.
+ *
+ * nq_codec_embed_sum: out[t] = sum_q books[q][codes[t*Q + q]] (the codebook
+ *   sum of quantizer.decode); ids outside [0, V) set *status (device int32,
+ *   may be NULL) to NQ_ERR_INVALID_ARGUMENT and are skipped.
+ * nq_codec_causal_conv: causal Conv1d with per-stream left history
+ *   (_causal_conv, :58-88): w [Cout, Cin/groups, K], groups 1 or Cin
+ *   (depthwise), history [slots, (K-1)*dilation, Cin] holding post-activation
+ *   inputs.  Optional SnakeBeta on the input (act_alpha/act_beta: log-scale
+ *   per-channel parameters, x + sin(e^a x)^2 / e^b) and a residual added to the
+ *   output.  The history is advanced in place after the convolution.
+ * nq_codec_causal_transconv: causal ConvTranspose1d with kernel 2*stride and
+ *   a stride-long bias-free overlap carry (_causal_transconv, :90-138):
+ *   w [Cin, Cout, 2*stride], overlap [slots, stride, Cout]; optional SnakeBeta
+ *   on the input; output rows at u_in*stride samples per frame.
+ * nq_codec_window_attention: per-head RMSNorm + RoPE of q and k (positions =
+ *   frame_pos[slot] + fresh index), attention over the R = window-1 retained
+ *   and the fresh frames inside the sliding window, with retained slot j
+ *   valid when j >= R - ctx_len[slot]; then the retained K/V
+ *   ([slots, R, H, D] per layer, slot stride state_slot_stride) advance in
+ *   place (_pre_transformer, :193-381).  q, k, v rows share stride ld.
+ * nq_codec_advance: frame_pos[slot] += F; ctx_len[slot] = min(R, ctx + F)
+ *   (:375-380), once per step after the last layer.
+ * nq_codec_pcm16: wav = clamp(x, -1, 1); pcm = round-half-even(wav * 32767)
+ *   (executor/codec.py:236-238); either output may be NULL.
+ */
+int nq_codec_embed_sum(const int32_t *codes, int T, int Q, const float *books, int V, int C, float *out,
+                       int32_t *status, void *stream);
+int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                         const int32_t *slots, float *history, const float *w, const float *bias, int Cin,
+                         int Cout, int K, int dilation, int groups, const float *act_alpha,
+                         const float *act_beta, const float *residual, int64_t ldres, float *out,
+                         int64_t ldo, void *stream);
+int nq_codec_causal_transconv(const float *x, int64_t ldx, int64_t T_in, const int32_t *offsets, int B,
+                              int u_in, int stride_s, const int32_t *slots, float *overlap, const float *w,
+                              const float *bias, int Cin, int Cout, const float *act_alpha,
+                              const float *act_beta, float *out, int64_t ldo, void *stream);
+int nq_codec_window_attention(float *q, float *k, const float *v, int64_t ld, int T, int H, int D,
+                              const float *q_norm, const float *k_norm, float eps, float rope_theta,
+                              const int32_t *offsets, int B, const int32_t *slots, const int64_t *frame_pos,
+                              const int32_t *ctx_len, float *state_k, float *state_v,
+                              int64_t state_slot_stride, int R, int window, float *out, int64_t ldo,
+                              void *stream);
+int nq_codec_advance(const int32_t *offsets, int B, const int32_t *slots, int64_t *frame_pos,
+                     int32_t *ctx_len, int R, void *stream);
+int nq_codec_pcm16(const float *x, int64_t n, float *wav, int16_t *pcm, void *stream);
+
+/*
+ * GEMM form of the wide convolutions.  nq_codec_im2col gathers the operand a
+ * conv (or transconv) becomes one GEMM over: conv rows hold the K taps of the
+ * (activated) input, history included, as a[t, k*Cin + ci]; transconv rows
+ * hold [act(x[t]), act(x[t-1])] (zeros before a stream's first fresh frame;
+ * K must be 2).  Cin % 4 == 0.  After the GEMM, nq_codec_history_update
+ * advances a conv's history, and nq_codec_transconv_overlap adds the stored
+ * overlap to each stream's first `stride` output rows and stores the new one,
+ * new_overlap [B, stride * Cout] = (last fresh frame, activated) x (the
+ * kernel's second half), which the caller computes with a small GEMM.
+ */
+int nq_codec_im2col(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                    const int32_t *slots, const float *history, int Cin, int K, int dilation, int transconv,
+                    const float *act_alpha, const float *act_beta, float *a, int64_t lda, void *stream);
+int nq_codec_history_update(const float *x, int64_t ldx, const int32_t *offsets, int B, int u,
+                            const int32_t *slots, float *history, int C, int pad, const float *act_alpha,
+                            const float *act_beta, void *stream);
+int nq_codec_transconv_overlap(const int32_t *offsets, int B, int u_in, int stride_s,
+                               const int32_t *slots, float *overlap, const float *new_overlap, int Cout,
+                               float *out, int64_t ldo, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,16 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_splits": [_I, _I, _I],
     "nq_linear_workspace_bytes": [_I, _I, _I, _I],
     "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P, _F, _P, _L, _P],
+    "nq_codec_embed_sum": [_P, _I, _I, _P, _I, _I, _P, _P, _P],
+    "nq_codec_causal_conv": [_P, _L, _L, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P],
+    "nq_codec_causal_transconv": [_P, _L, _L, _P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _L, _P],
+    "nq_codec_window_attention": [_P, _P, _P, _L, _I, _I, _I, _P, _P, _F, _F, _P, _I, _P, _P, _P, _P, _P, _L, _I,
+                                  _I, _P, _L, _P],
+    "nq_codec_advance": [_P, _I, _P, _P, _P, _I, _P],
+    "nq_codec_pcm16": [_P, _L, _P, _P, _P],
+    "nq_codec_im2col": [_P, _L, _L, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _L, _P],
+    "nq_codec_history_update": [_P, _L, _P, _I, _I, _P, _P, _I, _I, _P, _P, _P],
+    "nq_codec_transconv_overlap": [_P, _I, _I, _I, _P, _P, _P, _I, _P, _L, _P],
 }
 _RESTYPES = {
     "nq_status_string": ctypes.c_char_p,

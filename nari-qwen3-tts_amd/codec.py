@@ -1,0 +1,368 @@
+"""Incremental codec-decoder step on the GPU for a batch of streams.
+
+Mirrors the ``incremental_decoder`` contract of CodecExecutor
+(executor/codec.py:69-118, 427-442): a callable ``(codes, states) -> wav`` with
+``samples_per_frame`` and ``retained_context`` attributes that mutates the
+streams' states (model/incremental_codec.py:383-466).  Chunks may be ragged:
+each stream brings its own number of fresh frames and all streams run in the
+same launches.
+
+The upstream decoder (qwen-tts 0.1.1) is not available, so the module tree is
+a random-init causal decoder of the same structure, sized by ``CodecConfig``:
+16-codebook embedding sum (dim 512), causal pre-conv, an 8-layer transformer
+with a 26-frame sliding window (25 retained frames), per-head q/k RMSNorm,
+RoPE by frame position and layer scales, two transconv(x2) + ConvNeXt
+upsample stages, a causal conv, four decoder blocks (SnakeBeta, causal
+transconv x5/x5/x4/x5, three dilated residual units), SnakeBeta and the final
+causal conv: 2000 samples per 12 Hz frame, 24 kHz fp32 PCM, clamped.
+
+State lives in device slot arrays (one slot per stream): conv histories,
+transconv overlaps, retained K/V, frame position and valid context count.
+The stateful operators are HIP kernels (``nq_codec_*``); the transformer and
+ConvNeXt projections are plain fp32 GEMMs (torch/hipBLASLt) and the norms and
+GELU in between are torch element-wise ops.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class CodecConfig:
+    num_quantizers: int = 16
+    codebook_size: int = 2048
+    dim: int = 512
+    layers: int = 8
+    heads: int = 8
+    head_dim: int = 64
+    mlp: int = 1536
+    window: int = 26
+    theta: float = 10000.0
+    eps: float = 1e-6
+    up_strides: tuple[int, ...] = (2, 2)
+    convnext_mlp: int = 1024
+    dec_channels: tuple[int, ...] = (128, 64, 32, 16, 8)
+    dec_strides: tuple[int, ...] = (5, 5, 4, 5)
+    dilations: tuple[int, ...] = (1, 3, 9)
+
+    @property
+    def samples_per_frame(self) -> int:
+        return int(np.prod(self.up_strides) * np.prod(self.dec_strides))
+
+    @property
+    def retained_context(self) -> int:
+        return self.window - 1
+
+    def as_dict(self) -> dict:
+        return dict(num_quantizers=self.num_quantizers, dim=self.dim, layers=self.layers, heads=self.heads,
+                    head_dim=self.head_dim, window=self.window, theta=self.theta, eps=self.eps,
+                    up_strides=tuple(self.up_strides), dec_channels=tuple(self.dec_channels),
+                    dec_strides=tuple(self.dec_strides), dilations=tuple(self.dilations))
+
+
+class CodecWeights:
+    """Random-init fp32 parameters; ``host()`` gives the numpy dict the oracle reads."""
+
+    def __init__(self, config: CodecConfig, device: torch.device, seed: int = 0) -> None:
+        self.config = c = config
+        g = torch.Generator(device="cpu")
+        g.manual_seed(seed)
+
+        def rnd(*shape, fan_in=None, scale=None):
+            s = scale if scale is not None else 1.0 / math.sqrt(fan_in)
+            return (torch.randn(*shape, generator=g) * s).to(device)
+
+        def ones(n):
+            return torch.ones(n, device=device)
+
+        d = c.dim
+        self.codebooks = rnd(c.num_quantizers, c.codebook_size, d, scale=0.25)
+        self.pre_conv_w, self.pre_conv_b = rnd(d, d, 3, fan_in=3 * d), rnd(d, scale=0.01)
+        self.in_w, self.in_b = rnd(d, d, fan_in=d), rnd(d, scale=0.01)
+        hd = c.heads * c.head_dim
+        self.tf = [
+            SimpleNamespace(
+                ln1=ones(d), wqkv=rnd(3 * hd, d, fan_in=d), qn=ones(c.head_dim), kn=ones(c.head_dim),
+                wo=rnd(d, hd, fan_in=hd), ls1=torch.full((d,), 0.1, device=device), ln2=ones(d),
+                w1=rnd(c.mlp, d, fan_in=d), w2=rnd(d, c.mlp, fan_in=c.mlp), ls2=torch.full((d,), 0.1, device=device),
+            )
+            for _ in range(c.layers)
+        ]
+        self.out_norm = ones(d)
+        self.out_w, self.out_b = rnd(d, d, fan_in=d), rnd(d, scale=0.01)
+        self.up = []
+        for s in c.up_strides:
+            self.up.append(SimpleNamespace(
+                tc_w=rnd(d, d, 2 * s, fan_in=2 * d), tc_b=rnd(d, scale=0.01),
+                dw_w=rnd(d, 1, 7, fan_in=7), dw_b=rnd(d, scale=0.01), ln_w=ones(d), ln_b=torch.zeros(d, device=device),
+                pw1_w=rnd(c.convnext_mlp, d, fan_in=d), pw1_b=rnd(c.convnext_mlp, scale=0.01),
+                pw2_w=rnd(d, c.convnext_mlp, fan_in=c.convnext_mlp), pw2_b=rnd(d, scale=0.01),
+                gamma=torch.full((d,), 0.1, device=device),
+            ))
+        ch = c.dec_channels
+        self.dec0_w, self.dec0_b = rnd(ch[0], d, 7, fan_in=7 * d), rnd(ch[0], scale=0.01)
+        self.blocks = []
+        for i, s in enumerate(c.dec_strides):
+            cin, cout = ch[i], ch[i + 1]
+            self.blocks.append(SimpleNamespace(
+                alpha=rnd(cin, scale=0.1), beta=rnd(cin, scale=0.1),
+                tc_w=rnd(cin, cout, 2 * s, fan_in=2 * cin), tc_b=rnd(cout, scale=0.01),
+                res=[SimpleNamespace(
+                    a1=rnd(cout, scale=0.1), b1=rnd(cout, scale=0.1), c1_w=rnd(cout, cout, 7, fan_in=7 * cout),
+                    c1_b=rnd(cout, scale=0.01), a2=rnd(cout, scale=0.1), b2=rnd(cout, scale=0.1),
+                    c2_w=rnd(cout, cout, 1, fan_in=cout) * 0.5, c2_b=rnd(cout, scale=0.01),
+                ) for _ in c.dilations],
+            ))
+        self.final_alpha, self.final_beta = rnd(ch[-1], scale=0.1), rnd(ch[-1], scale=0.1)
+        self.final_w, self.final_b = rnd(1, ch[-1], 7, fan_in=7 * ch[-1]), rnd(1, scale=0.01)
+
+    def host(self) -> dict:
+        def h(t):
+            return t.detach().float().cpu().numpy()
+
+        def ns(n):
+            return {k: ([ns(x) for x in v] if isinstance(v, list) else h(v)) for k, v in vars(n).items()}
+
+        return dict(
+            codebooks=h(self.codebooks), pre_conv_w=h(self.pre_conv_w), pre_conv_b=h(self.pre_conv_b),
+            in_w=h(self.in_w), in_b=h(self.in_b), out_norm=h(self.out_norm), out_w=h(self.out_w), out_b=h(self.out_b),
+            tf=[ns(L) | {"wq": h(L.wqkv[: self.config.heads * self.config.head_dim]),
+                         "wk": h(L.wqkv[self.config.heads * self.config.head_dim: 2 * self.config.heads * self.config.head_dim]),
+                         "wv": h(L.wqkv[2 * self.config.heads * self.config.head_dim:])} for L in self.tf],
+            up=[ns(U) for U in self.up], dec0_w=h(self.dec0_w), dec0_b=h(self.dec0_b),
+            blocks=[ns(B) for B in self.blocks], final_alpha=h(self.final_alpha), final_beta=h(self.final_beta),
+            final_w=h(self.final_w), final_b=h(self.final_b),
+        )
+
+
+@dataclass
+class CodecStreamState:
+    """One stream's handle on its state slot (the device arrays hold the values)."""
+
+    slot: int
+    frame_position: int = 0
+    transformer_context_length: int = 0
+    _pool: object = field(default=None, repr=False)
+
+
+class _StatePool:
+    def __init__(self, config: CodecConfig, slots: int, device: torch.device) -> None:
+        c = config
+        z = dict(dtype=torch.float32, device=device)
+        self.slots = slots
+        self.hist = {}
+        d = c.dim
+        self.hist["pre_conv"] = torch.zeros(slots, 2, d, **z)
+        for u in range(len(c.up_strides)):
+            self.hist[f"up{u}.dw"] = torch.zeros(slots, 6, d, **z)
+        self.hist["dec0"] = torch.zeros(slots, 6, d, **z)
+        for i in range(len(c.dec_strides)):
+            ch = c.dec_channels[i + 1]
+            for j, dil in enumerate(c.dilations):
+                self.hist[f"dec{i + 1}.res{j}.a"] = torch.zeros(slots, 6 * dil, ch, **z)
+        self.hist["final"] = torch.zeros(slots, 6, c.dec_channels[-1], **z)
+        self.overlap = {f"up{u}.tc": torch.zeros(slots, s, d, **z) for u, s in enumerate(c.up_strides)}
+        for i, s in enumerate(c.dec_strides):
+            self.overlap[f"dec{i + 1}.tc"] = torch.zeros(slots, s, c.dec_channels[i + 1], **z)
+        r = c.retained_context
+        self.k = torch.zeros(c.layers, slots, r, c.heads, c.head_dim, **z)
+        self.v = torch.zeros_like(self.k)
+        self.frame_pos = torch.zeros(slots, dtype=torch.long, device=device)
+        self.ctx = torch.zeros(slots, dtype=torch.int32, device=device)
+        self.free = list(range(slots))
+
+    def reset(self, slot: int) -> None:
+        for t in list(self.hist.values()) + list(self.overlap.values()):
+            t[slot].zero_()
+        self.k[:, slot].zero_()
+        self.v[:, slot].zero_()
+        self.frame_pos[slot] = 0
+        self.ctx[slot] = 0
+
+
+class IncrementalCodecDecoder:
+    """``decoder(codes, states) -> (wav, pcm16)`` over ragged chunks of many streams."""
+
+    def __init__(self, weights: CodecWeights, max_streams: int = 64) -> None:
+        self.w = weights
+        self.config = weights.config
+        self.device = weights.codebooks.device
+        self.samples_per_frame = self.config.samples_per_frame
+        self.retained_context = self.config.retained_context
+        self.pool = _StatePool(self.config, max_streams, self.device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._cache: dict = {}
+
+    def new_state(self) -> CodecStreamState:
+        if not self.pool.free:
+            raise RuntimeError("no free codec state slot")
+        slot = self.pool.free.pop(0)
+        self.pool.reset(slot)
+        return CodecStreamState(slot=slot, _pool=self.pool)
+
+    def release(self, state: CodecStreamState) -> None:
+        self.pool.free.append(state.slot)
+
+    # -- helpers ------------------------------------------------------------
+    # Wide convolutions (Cin * K >= 256 or Cin >= 64) run as one fp32 GEMM over a
+    # gathered operand; narrow ones run the direct HIP kernel.
+    GEMM_MIN_CIN_K = 256
+
+    def _derived(self, key, make):
+        got = self._cache.get(key)
+        if got is None:
+            got = make()
+            self._cache[key] = got
+        return got
+
+    def _conv(self, x, u, name, w, b, *, dilation=1, groups=1, act=None, residual=None):
+        c_in = x.shape[1]
+        c_out, _, k = w.shape
+        hist = self.pool.hist.get(name) if name else None
+        a_ptr = _lib.ptr(act[0]) if act else None
+        b_ptr = _lib.ptr(act[1]) if act else None
+        if groups == 1 and (c_in * k >= self.GEMM_MIN_CIN_K or c_in >= 64) and c_in % 4 == 0:
+            cols = torch.empty(x.shape[0], k * c_in, dtype=torch.float32, device=self.device)
+            _lib.call("nq_codec_im2col", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u,
+                      self._slots.data_ptr(), _lib.ptr(hist), c_in, k, dilation, 0, a_ptr, b_ptr, cols.data_ptr(),
+                      cols.stride(0), self._stream)
+            w_col = self._derived(("conv", id(w)), lambda: w.permute(0, 2, 1).reshape(c_out, k * c_in).t().contiguous())
+            out = torch.addmm(b, cols, w_col) if b is not None else cols @ w_col
+            if residual is not None:
+                out.add_(residual)
+            if k > 1:
+                _lib.call("nq_codec_history_update", x.data_ptr(), x.stride(0), self._off.data_ptr(), self._B, u,
+                          self._slots.data_ptr(), hist.data_ptr(), c_in, (k - 1) * dilation, a_ptr, b_ptr,
+                          self._stream)
+            return out
+        out = torch.empty(x.shape[0], c_out, dtype=torch.float32, device=self.device)
+        _lib.call("nq_codec_causal_conv", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u,
+                  self._slots.data_ptr(), _lib.ptr(hist), w.data_ptr(), _lib.ptr(b), c_in, c_out, k,
+                  dilation, groups, a_ptr, b_ptr, _lib.ptr(residual), residual.stride(0) if residual is not None else 0,
+                  out.data_ptr(), out.stride(0), self._stream)
+        return out
+
+    def _transconv(self, x, u_in, s, name, w, b, act=None):
+        c_in, c_out = w.shape[0], w.shape[1]
+        a_ptr = _lib.ptr(act[0]) if act else None
+        b_ptr = _lib.ptr(act[1]) if act else None
+        overlap = self.pool.overlap[name]
+        if c_in >= 64 and c_in % 4 == 0:
+            cols = torch.empty(x.shape[0], 2 * c_in, dtype=torch.float32, device=self.device)
+            _lib.call("nq_codec_im2col", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u_in,
+                      self._slots.data_ptr(), None, c_in, 2, 1, 1, a_ptr, b_ptr, cols.data_ptr(), cols.stride(0),
+                      self._stream)
+            w_t = self._derived(("tc", id(w)), lambda: w.view(c_in, c_out, 2, s).permute(2, 0, 3, 1)
+                                .reshape(2 * c_in, s * c_out).contiguous())
+            b_s = self._derived(("tcb", id(b)), lambda: b.repeat(s).contiguous())
+            out = torch.addmm(b_s, cols, w_t).view(x.shape[0] * s, c_out)
+            # new overlap: each stream's last fresh frame (activated: the first half of its
+            # gathered row) through the kernel's second half
+            last = (self._off[1:].long() * u_in - 1).clamp(min=0)
+            new_ov = cols.index_select(0, last)[:, :c_in] @ w_t[c_in:]
+            _lib.call("nq_codec_transconv_overlap", self._off.data_ptr(), self._B, u_in, s, self._slots.data_ptr(),
+                      overlap.data_ptr(), new_ov.data_ptr(), c_out, out.data_ptr(), out.stride(0), self._stream)
+            return out
+        out = torch.empty(x.shape[0] * s, c_out, dtype=torch.float32, device=self.device)
+        _lib.call("nq_codec_causal_transconv", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B,
+                  u_in, s, self._slots.data_ptr(), overlap.data_ptr(), w.data_ptr(), _lib.ptr(b),
+                  c_in, c_out, a_ptr, b_ptr, out.data_ptr(), out.stride(0), self._stream)
+        return out
+
+    @staticmethod
+    def _rms(x, w, eps):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+    # -- the step -------------------------------------------------------------
+    def __call__(self, codes, states: list[CodecStreamState]):
+        """codes: [B, Q, F] (equal chunks, the reference's layout) or a list of [Q, F_b] tensors.
+        Returns (wav list of [F_b * samples_per_frame] fp32, pcm16 list) per stream."""
+
+        c, w = self.config, self.w
+        chunks = list(codes) if not isinstance(codes, torch.Tensor) else [codes[i] for i in range(codes.shape[0])]
+        if len(chunks) != len(states):
+            raise ValueError(f"state count {len(states)} does not match batch {len(chunks)}")
+        for ch in chunks:
+            if ch.ndim != 2 or ch.shape[0] != c.num_quantizers:
+                raise ValueError(f"expected [{c.num_quantizers}, frames] codes per stream")
+        frames = [int(ch.shape[1]) for ch in chunks]
+        B = len(chunks)
+        off = np.zeros(B + 1, dtype=np.int32)
+        off[1:] = np.cumsum(frames)
+        T = int(off[-1])
+        spf = c.samples_per_frame
+        if T == 0:
+            return [torch.empty(0, device=self.device) for _ in chunks], [
+                torch.empty(0, dtype=torch.int16, device=self.device) for _ in chunks]
+        dev = self.device
+        self._B = B
+        self._off = torch.from_numpy(off).to(dev, non_blocking=True)
+        self._slots = torch.tensor([s.slot for s in states], dtype=torch.int32, device=dev)
+        self._stream = _lib.stream(dev)
+        packed = torch.cat([ch.t() for ch in chunks], dim=0).to(device=dev, dtype=torch.int32).contiguous()
+
+        x = torch.empty(T, c.dim, dtype=torch.float32, device=dev)
+        _lib.call("nq_codec_embed_sum", packed.data_ptr(), T, c.num_quantizers, w.codebooks.data_ptr(),
+                  c.codebook_size, c.dim, x.data_ptr(), self.status.data_ptr(), self._stream)
+        x = self._conv(x, 1, "pre_conv", w.pre_conv_w, w.pre_conv_b)
+
+        # transformer (model/incremental_codec.py:193-381)
+        hd = c.heads * c.head_dim
+        r = c.retained_context
+        h = torch.addmm(w.in_b, x, w.in_w.t())
+        att = torch.empty(T, hd, dtype=torch.float32, device=dev)
+        pool = self.pool
+        for li, L in enumerate(w.tf):
+            y = self._rms(h, L.ln1, c.eps)
+            qkv = y @ L.wqkv.t()
+            q, k, v = qkv[:, :hd], qkv[:, hd: 2 * hd], qkv[:, 2 * hd:]
+            _lib.call("nq_codec_window_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), qkv.stride(0), T, c.heads,
+                      c.head_dim, L.qn.data_ptr(), L.kn.data_ptr(), float(c.eps), float(c.theta), self._off.data_ptr(),
+                      B, self._slots.data_ptr(), pool.frame_pos.data_ptr(), pool.ctx.data_ptr(), pool.k[li].data_ptr(),
+                      pool.v[li].data_ptr(), pool.k.stride(1), r, c.window, att.data_ptr(), att.stride(0), self._stream)
+            h = h + (att @ L.wo.t()) * L.ls1
+            y = self._rms(h, L.ln2, c.eps)
+            h = h + (F.gelu(y @ L.w1.t()) @ L.w2.t()) * L.ls2
+        _lib.call("nq_codec_advance", self._off.data_ptr(), B, self._slots.data_ptr(), pool.frame_pos.data_ptr(),
+                  pool.ctx.data_ptr(), r, self._stream)
+        x = torch.addmm(w.out_b, self._rms(h, w.out_norm, c.eps), w.out_w.t())
+
+        # upsample: causal transconv + ConvNeXt
+        u = 1
+        for ui, (s, U) in enumerate(zip(c.up_strides, w.up)):
+            x = self._transconv(x, u, s, f"up{ui}.tc", U.tc_w, U.tc_b)
+            u *= s
+            y = self._conv(x, u, f"up{ui}.dw", U.dw_w, U.dw_b, groups=c.dim)
+            y = F.layer_norm(y, (c.dim,), U.ln_w, U.ln_b, 1e-6)
+            y = torch.addmm(U.pw2_b, F.gelu(torch.addmm(U.pw1_b, y, U.pw1_w.t())), U.pw2_w.t())
+            x = x + U.gamma * y
+        # decoder blocks
+        x = self._conv(x, u, "dec0", w.dec0_w, w.dec0_b)
+        for bi, (s, Bk) in enumerate(zip(c.dec_strides, w.blocks)):
+            x = self._transconv(x, u, s, f"dec{bi + 1}.tc", Bk.tc_w, Bk.tc_b, act=(Bk.alpha, Bk.beta))
+            u *= s
+            for j, (dil, R) in enumerate(zip(c.dilations, Bk.res)):
+                y = self._conv(x, u, f"dec{bi + 1}.res{j}.a", R.c1_w, R.c1_b, dilation=dil, act=(R.a1, R.b1))
+                x = self._conv(y, u, None, R.c2_w, R.c2_b, act=(R.a2, R.b2), residual=x)
+        y = self._conv(x, u, "final", w.final_w, w.final_b, act=(w.final_alpha, w.final_beta))
+        n = T * spf
+        wav = torch.empty(n, dtype=torch.float32, device=dev)
+        pcm = torch.empty(n, dtype=torch.int16, device=dev)
+        _lib.call("nq_codec_pcm16", y.data_ptr(), n, wav.data_ptr(), pcm.data_ptr(), self._stream)
+        for st, f in zip(states, frames):
+            st.frame_position += f
+            st.transformer_context_length = min(r, st.transformer_context_length + f)
+        bounds = off * spf
+        return ([wav[bounds[i]: bounds[i + 1]] for i in range(B)], [pcm[bounds[i]: bounds[i + 1]] for i in range(B)])
+
+
+__all__ = ["CodecConfig", "CodecStreamState", "CodecWeights", "IncrementalCodecDecoder"]

@@ -1,0 +1,750 @@
+// Incremental codec-decoder step: the stateful kernels of a batch of streams
+// decoded together (model/incremental_codec.py:58-466), fp32 like the
+// reference codec (no autocast, executor/build.py:91-95).
+//
+// Layout.  Activations are channels-last [T, C] with the fresh rows of all
+// streams concatenated: stream b owns rows [off[b] * u, off[b + 1] * u) of a
+// stage whose time axis is u samples per codec frame (u = 1 at the frame rate,
+// then x2, x4, x20 ... x2000 after the upsampling layers).  `off` is the
+// frame-level exclusive prefix of the streams' fresh frame counts, so ragged
+// chunks (12-48 frames) share every launch.  Each stream's state lives in slot
+// slots[b] of per-layer device arrays:
+//   - causal Conv1d history  [slots, pad, Cin]  (post-activation inputs)
+//   - ConvTranspose1d overlap [slots, s, Cout]  (bias-free expansion tail)
+//   - transformer K/V          [slots, R, H, D]  (rotated keys, R = window - 1)
+//   - frame position / valid context count [slots]
+// A conv or transconv reads the old state, then a second small kernel writes
+// the new state (in place: each thread owns one (stream, channel) column and
+// walks it forward, so no element is overwritten before it is read).
+#include "nq_common.h"
+
+namespace nq {
+namespace {
+
+constexpr int kCodecThreads = 256;
+
+// stream of stage row t: the largest b with off[b] * u <= t
+__device__ __forceinline__ int stream_of(const int32_t *__restrict__ off, int B, int64_t t, int u) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (static_cast<int64_t>(off[mid]) * u <= t) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// SnakeBeta x + sin(a x)^2 / b with a = exp(alpha), b = exp(beta) (per channel)
+__device__ __forceinline__ float snake(float x, float a, float inv_b) {
+    const float s = __sinf(a * x);
+    return x + inv_b * s * s;
+}
+
+struct Act {
+    const float *alpha;  // log-scale, [C] or null (identity)
+    const float *beta;
+    __device__ __forceinline__ float a_of(int c) const { return expf(alpha[c]); }
+    __device__ __forceinline__ float inv_b_of(int c) const { return 1.0f / (expf(beta[c]) + 1e-9f); }
+    __device__ __forceinline__ float apply(float x, int c) const {
+        if (!alpha) return x;
+        return snake(x, a_of(c), inv_b_of(c));
+    }
+};
+
+// ---------------------------------------------------------------------------
+// codebook sum: out[t, c] = sum_q book[q, codes[t, q], c]
+
+__global__ void __launch_bounds__(kCodecThreads)
+embed_sum_kernel(const int32_t *__restrict__ codes, int T, int Q, const float *__restrict__ books, int V, int C,
+                 float *__restrict__ out, int32_t *status) {
+    const int64_t n = static_cast<int64_t>(T) * C;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kCodecThreads) {
+        const int64_t t = i / C;
+        const int c = static_cast<int>(i - t * C);
+        float s = 0.f;
+        for (int q = 0; q < Q; ++q) {
+            const int id = codes[t * Q + q];
+            if (static_cast<unsigned>(id) >= static_cast<unsigned>(V)) {
+                if (status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+                continue;
+            }
+            s += books[(static_cast<int64_t>(q) * V + id) * C + c];
+        }
+        out[i] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// causal Conv1d (groups 1), direct form.  A workgroup covers 256 / CG rows and
+// CG groups of 16 output channels; weights of 16 input channels x K taps are
+// staged in LDS per round.  Row r, tap k reads input time local - (K-1-k)*dil
+// of its own stream: from x when >= 0, else from the stream's history.
+
+constexpr int kConvCi = 16;
+constexpr int kConvKMax = 7;
+
+template <int CG>
+__global__ void __launch_bounds__(kCodecThreads)
+conv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
+            const int32_t *__restrict__ slots, const float *__restrict__ hist, const float *__restrict__ w,
+            const float *__restrict__ bias, int Cin, int Cout, int K, int dil, Act act,
+            const float *__restrict__ res, int64_t ldres, float *__restrict__ out, int64_t ldo) {
+    constexpr int kRows = kCodecThreads / CG;
+    __shared__ float ws[CG * 16][kConvCi][kConvKMax];
+    __shared__ float sa[kConvCi], sb[kConvCi];
+    const int r = threadIdx.x % kRows;
+    const int cg = threadIdx.x / kRows;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + r;
+    const int co0 = blockIdx.y * CG * 16;
+    const int pad = (K - 1) * dil;
+    const bool live = row < T;
+    int b = 0;
+    int64_t local = 0, base = 0;
+    if (live) {
+        b = stream_of(off, B, row, u);
+        base = static_cast<int64_t>(off[b]) * u;
+        local = row - base;
+    }
+    const float *hrow = hist + static_cast<int64_t>(live ? slots[b] : 0) * pad * Cin;
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.f;
+
+    for (int ci0 = 0; ci0 < Cin; ci0 += kConvCi) {
+        const int nci = min(kConvCi, Cin - ci0);
+        __syncthreads();
+        for (int e = threadIdx.x; e < CG * 16 * kConvCi * K; e += kCodecThreads) {
+            const int co = e / (kConvCi * K);
+            const int rem = e - co * kConvCi * K;
+            const int ci = rem / K, k = rem - ci * K;
+            float v = 0.f;
+            if (co0 + co < Cout && ci < nci) v = w[(static_cast<int64_t>(co0 + co) * Cin + ci0 + ci) * K + k];
+            ws[co][ci][k] = v;
+        }
+        if (act.alpha && threadIdx.x < nci) {
+            sa[threadIdx.x] = act.a_of(ci0 + threadIdx.x);
+            sb[threadIdx.x] = act.inv_b_of(ci0 + threadIdx.x);
+        }
+        __syncthreads();
+        if (!live) continue;
+        for (int k = 0; k < K; ++k) {
+            const int64_t src = local - static_cast<int64_t>(K - 1 - k) * dil;
+            const float *p = src >= 0 ? x + (base + src) * ldx + ci0 : hrow + (pad + src) * Cin + ci0;
+            const bool activate = src >= 0 && act.alpha;
+            for (int ci = 0; ci < nci; ++ci) {
+                float xv = p[ci];
+                if (activate) xv = snake(xv, sa[ci], sb[ci]);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[j] += xv * ws[cg * 16 + j][ci][k];
+            }
+        }
+    }
+    if (!live) return;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int co = co0 + cg * 16 + j;
+        if (co >= Cout) break;
+        float y = acc[j] + (bias ? bias[co] : 0.f);
+        if (res) y += res[row * ldres + co];
+        out[row * ldo + co] = y;
+    }
+}
+
+// Narrow causal Conv1d (Cin, Cout <= 64): one thread per output row computing
+// every output channel.  The workgroup stages its 256 rows plus the `pad`
+// rows before them, activated once, in LDS (row pitch Cin + 1, so the 64 rows
+// a wave reads at one channel hit distinct banks) with the weights as
+// [ci][k][co].  A tap whose input time is >= 0 reads the staged row (it lies in
+// the same stream); a tap before the stream's first fresh row reads the
+// stream's history from global memory.
+template <int CO>
+__global__ void __launch_bounds__(kCodecThreads)
+conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
+                  const int32_t *__restrict__ slots, const float *__restrict__ hist, const float *__restrict__ w,
+                  const float *__restrict__ bias, int Cin, int Cout, int K, int dil, Act act,
+                  const float *__restrict__ res, int64_t ldres, float *__restrict__ out, int64_t ldo) {
+    extern __shared__ float lds[];
+    const int pad = (K - 1) * dil;
+    const int pitch = Cin + 1;
+    float *xs = lds;                                              // [(256 + pad) * pitch]
+    float *wsm = xs + ((kCodecThreads + pad) * pitch + 3) / 4 * 4;  // [Cin * K * CO], 16-byte aligned
+    float *sa = wsm + Cin * K * CO;                   // [Cin]
+    float *sb = sa + Cin;                             // [Cin]
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kCodecThreads;
+    for (int e = threadIdx.x; e < Cin * K * CO; e += kCodecThreads) {
+        const int co = e % CO;
+        const int ck = e / CO;
+        const int ci = ck / K, k = ck - ci * K;
+        wsm[e] = co < Cout ? w[(static_cast<int64_t>(co) * Cin + ci) * K + k] : 0.f;
+    }
+    if (act.alpha && threadIdx.x < Cin) {
+        sa[threadIdx.x] = act.a_of(threadIdx.x);
+        sb[threadIdx.x] = act.inv_b_of(threadIdx.x);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < (kCodecThreads + pad) * Cin; e += kCodecThreads) {
+        const int rr = e / Cin, c = e - rr * Cin;
+        const int64_t g = row0 - pad + rr;
+        float v = 0.f;
+        if (g >= 0 && g < T) {
+            v = x[g * ldx + c];
+            if (act.alpha) v = snake(v, sa[c], sb[c]);
+        }
+        xs[rr * pitch + c] = v;
+    }
+    __syncthreads();
+    const int64_t row = row0 + threadIdx.x;
+    if (row >= T) return;
+    const int b = stream_of(off, B, row, u);
+    const int64_t local = row - static_cast<int64_t>(off[b]) * u;
+    const float *hrow = pad ? hist + static_cast<int64_t>(slots[b]) * pad * Cin : nullptr;
+    float acc[CO];
+#pragma unroll
+    for (int j = 0; j < CO; ++j) acc[j] = 0.f;
+    for (int k = 0; k < K; ++k) {
+        const int back = (K - 1 - k) * dil;
+        const int64_t src = local - back;
+        const float *xr;
+        int step;
+        if (src >= 0) {
+            xr = xs + (threadIdx.x + pad - back) * pitch;
+            step = 1;
+        } else {
+            xr = hrow + (pad + src) * Cin;
+            step = 1;
+        }
+        const float *wk = wsm + k * CO;
+        for (int ci = 0; ci < Cin; ++ci) {
+            const float xv = xr[ci * step];
+            const float4 *w4 = reinterpret_cast<const float4 *>(wk + ci * K * CO);
+#pragma unroll
+            for (int j = 0; j < CO / 4; ++j) {
+                const float4 ww = w4[j];
+                acc[4 * j] += xv * ww.x;
+                acc[4 * j + 1] += xv * ww.y;
+                acc[4 * j + 2] += xv * ww.z;
+                acc[4 * j + 3] += xv * ww.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < CO; ++j) {
+        if (j >= Cout) break;
+        float y = acc[j] + (bias ? bias[j] : 0.f);
+        if (res) y += res[row * ldres + j];
+        out[row * ldo + j] = y;
+    }
+}
+
+size_t conv_small_lds(int Cin, int K, int dil, int CO) {
+    return (static_cast<size_t>(kCodecThreads + (K - 1) * dil) * (Cin + 1) + 3 + static_cast<size_t>(Cin) * K * CO +
+            2 * Cin) * sizeof(float);
+}
+
+// depthwise causal Conv1d (groups == C): one thread per (row, channel)
+__global__ void __launch_bounds__(kCodecThreads)
+dwconv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
+              const int32_t *__restrict__ slots, const float *__restrict__ hist, const float *__restrict__ w,
+              const float *__restrict__ bias, int C, int K, int dil, float *__restrict__ out, int64_t ldo) {
+    const int64_t n = T * C;
+    const int pad = (K - 1) * dil;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kCodecThreads) {
+        const int64_t row = i / C;
+        const int c = static_cast<int>(i - row * C);
+        const int b = stream_of(off, B, row, u);
+        const int64_t base = static_cast<int64_t>(off[b]) * u;
+        const int64_t local = row - base;
+        const float *hrow = hist + static_cast<int64_t>(slots[b]) * pad * C;
+        float y = bias ? bias[c] : 0.f;
+        for (int k = 0; k < K; ++k) {
+            const int64_t src = local - static_cast<int64_t>(K - 1 - k) * dil;
+            const float xv = src >= 0 ? x[(base + src) * ldx + c] : hrow[(pad + src) * C + c];
+            y += xv * w[c * K + k];
+        }
+        out[row * ldo + c] = y;
+    }
+}
+
+// new history = last pad rows of [history ; act(x)] per stream; thread per (stream, channel)
+__global__ void __launch_bounds__(kCodecThreads)
+history_update_kernel(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ off, int B, int u,
+                      const int32_t *__restrict__ slots, float *__restrict__ hist, int C, int pad, Act act) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
+    if (i >= static_cast<int64_t>(B) * C) return;
+    const int b = static_cast<int>(i / C);
+    const int c = static_cast<int>(i - static_cast<int64_t>(b) * C);
+    const int64_t base = static_cast<int64_t>(off[b]) * u;
+    const int64_t F = static_cast<int64_t>(off[b + 1]) * u - base;
+    float *h = hist + static_cast<int64_t>(slots[b]) * pad * C + c;
+    for (int j = 0; j < pad; ++j) {
+        float v;
+        if (j + F < pad) v = h[(j + F) * C];
+        else v = act.apply(x[(base + F - pad + j) * ldx + c], c);
+        h[static_cast<int64_t>(j) * C] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// causal ConvTranspose1d, kernel 2s, stride s, overlap s.  Output row p of a
+// stream (stage u * s): t0 = p / s, j = p % s,
+//   y = bias + x[t0] . W[:, :, j] + (t0 > 0 ? x[t0 - 1] . W[:, :, j + s] : overlap[j])
+
+template <int CG>
+__global__ void __launch_bounds__(kCodecThreads)
+transconv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T_out, const int32_t *__restrict__ off, int B,
+                 int u_in, int s, const int32_t *__restrict__ slots, const float *__restrict__ overlap,
+                 const float *__restrict__ w, const float *__restrict__ bias, int Cin, int Cout, Act act,
+                 float *__restrict__ out, int64_t ldo) {
+    constexpr int kRows = kCodecThreads / CG;
+    extern __shared__ float tw[];  // [16 ci][CG*16 co][2s]
+    __shared__ float sa[kConvCi], sb[kConvCi];
+    const int r = threadIdx.x % kRows;
+    const int cg = threadIdx.x / kRows;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + r;
+    const int co0 = blockIdx.y * CG * 16;
+    const int u_out = u_in * s;
+    const bool live = row < T_out;
+    int b = 0;
+    int64_t local = 0, base_in = 0;
+    if (live) {
+        b = stream_of(off, B, row, u_out);
+        local = row - static_cast<int64_t>(off[b]) * u_out;
+        base_in = static_cast<int64_t>(off[b]) * u_in;
+    }
+    const int64_t t0 = local / s;
+    const int j = static_cast<int>(local - t0 * s);
+    float acc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+    const int ks = 2 * s;
+    for (int ci0 = 0; ci0 < Cin; ci0 += kConvCi) {
+        const int nci = min(kConvCi, Cin - ci0);
+        __syncthreads();
+        for (int e = threadIdx.x; e < kConvCi * CG * 16 * ks; e += kCodecThreads) {
+            const int ci = e / (CG * 16 * ks);
+            const int rem = e - ci * CG * 16 * ks;
+            const int co = rem / ks, k = rem - co * ks;
+            float v = 0.f;
+            if (ci < nci && co0 + co < Cout) v = w[(static_cast<int64_t>(ci0 + ci) * Cout + co0 + co) * ks + k];
+            tw[e] = v;
+        }
+        if (act.alpha && threadIdx.x < nci) {
+            sa[threadIdx.x] = act.a_of(ci0 + threadIdx.x);
+            sb[threadIdx.x] = act.inv_b_of(ci0 + threadIdx.x);
+        }
+        __syncthreads();
+        if (!live) continue;
+        const float *x1 = x + (base_in + t0) * ldx + ci0;
+        const float *x0 = t0 > 0 ? x + (base_in + t0 - 1) * ldx + ci0 : nullptr;
+        for (int ci = 0; ci < nci; ++ci) {
+            float a1 = x1[ci], a0 = x0 ? x0[ci] : 0.f;
+            if (act.alpha) {
+                a1 = snake(a1, sa[ci], sb[ci]);
+                if (x0) a0 = snake(a0, sa[ci], sb[ci]);
+            }
+            const float *wr = tw + (ci * CG * 16 + cg * 16) * ks;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] += a1 * wr[q * ks + j] + a0 * wr[q * ks + j + s];
+        }
+    }
+    if (!live) return;
+    const float *ov = overlap + (static_cast<int64_t>(slots[b]) * s + j) * Cout;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int co = co0 + cg * 16 + q;
+        if (co >= Cout) break;
+        float y = acc[q] + (bias ? bias[co] : 0.f);
+        if (t0 == 0) y += ov[co];
+        out[row * ldo + co] = y;
+    }
+}
+
+// new overlap[j, co] = act(x[F - 1]) . W[:, co, s + j]; thread per (stream, j, co)
+__global__ void __launch_bounds__(kCodecThreads)
+overlap_update_kernel(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ off, int B, int u_in,
+                      int s, const int32_t *__restrict__ slots, float *__restrict__ overlap,
+                      const float *__restrict__ w, int Cin, int Cout, Act act) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
+    if (i >= static_cast<int64_t>(B) * s * Cout) return;
+    const int b = static_cast<int>(i / (static_cast<int64_t>(s) * Cout));
+    const int rem = static_cast<int>(i - static_cast<int64_t>(b) * s * Cout);
+    const int j = rem / Cout, co = rem - j * Cout;
+    const int64_t base = static_cast<int64_t>(off[b]) * u_in;
+    const int64_t F = static_cast<int64_t>(off[b + 1]) * u_in - base;
+    if (F <= 0) return;  // no fresh input: the stored overlap stays
+    const float *xl = x + (base + F - 1) * ldx;
+    float sum = 0.f;
+    for (int ci = 0; ci < Cin; ++ci) sum += act.apply(xl[ci], ci) * w[(static_cast<int64_t>(ci) * Cout + co) * 2 * s + s + j];
+    overlap[(static_cast<int64_t>(slots[b]) * s + j) * Cout + co] = sum;
+}
+
+// ---------------------------------------------------------------------------
+// Gathered operand for running a wide conv or transconv as one GEMM.
+//   conv:      A[t, k*Cin + ci] = input of row t at tap k (activated x, or raw history)
+//   transconv: A[t, ci] = act(x[t]), A[t, Cin + ci] = act(x[t - 1]) (0 for a stream's
+//              first fresh frame; its overlap is added after the GEMM)
+// One thread per (row, 4 channels); Cin % 4 == 0.
+
+__global__ void __launch_bounds__(kCodecThreads)
+im2col_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
+              const int32_t *__restrict__ slots, const float *__restrict__ hist, int Cin, int K, int dil, int transconv,
+              Act act, float *__restrict__ a, int64_t lda) {
+    const int c4 = Cin / 4;
+    const int64_t n = T * K * c4;
+    const int pad = transconv ? 0 : (K - 1) * dil;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kCodecThreads) {
+        const int64_t row = i / (K * c4);
+        const int rem = static_cast<int>(i - row * K * c4);
+        const int k = rem / c4, c = (rem - k * c4) * 4;
+        const int b = stream_of(off, B, row, u);
+        const int64_t base = static_cast<int64_t>(off[b]) * u;
+        const int64_t local = row - base;
+        const int64_t src = transconv ? local - k : local - static_cast<int64_t>(K - 1 - k) * dil;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (src >= 0) {
+            v = *reinterpret_cast<const float4 *>(x + (base + src) * ldx + c);
+            if (act.alpha) {
+                v.x = act.apply(v.x, c);
+                v.y = act.apply(v.y, c + 1);
+                v.z = act.apply(v.z, c + 2);
+                v.w = act.apply(v.w, c + 3);
+            }
+        } else if (!transconv) {
+            v = *reinterpret_cast<const float4 *>(hist + (static_cast<int64_t>(slots[b]) * pad + pad + src) * Cin + c);
+        }
+        *reinterpret_cast<float4 *>(a + row * lda + static_cast<int64_t>(k) * Cin + c) = v;
+    }
+}
+
+// GEMM-path transconv: add the stored overlap to each stream's first `s`
+// output rows, then store the new overlap, which the caller computed as
+// (last fresh frame) x (kernel tail): new_ov [B, s * Cout].  Thread per
+// (stream, j, co) touches one overlap element only.
+__global__ void __launch_bounds__(kCodecThreads)
+overlap_fixup_kernel(const int32_t *__restrict__ off, int B, int u_in, int s, const int32_t *__restrict__ slots,
+                     float *__restrict__ overlap, const float *__restrict__ new_ov, int Cout, float *__restrict__ out,
+                     int64_t ldo) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
+    if (i >= static_cast<int64_t>(B) * s * Cout) return;
+    const int b = static_cast<int>(i / (static_cast<int64_t>(s) * Cout));
+    const int rem = static_cast<int>(i - static_cast<int64_t>(b) * s * Cout);
+    const int j = rem / Cout, co = rem - j * Cout;
+    const int64_t base = static_cast<int64_t>(off[b]) * u_in;
+    const int64_t F = static_cast<int64_t>(off[b + 1]) * u_in - base;
+    if (F <= 0) return;
+    float *ov = overlap + (static_cast<int64_t>(slots[b]) * s + j) * Cout + co;
+    out[(base * s + j) * ldo + co] += *ov;
+    *ov = new_ov[static_cast<int64_t>(b) * s * Cout + rem];
+}
+
+// ---------------------------------------------------------------------------
+// transformer: per-head RMSNorm + RoPE of q and k (in place), positions =
+// frame_position[slot] + local frame.  One wave per (token, head); lane i
+// holds the pair (i, i + D/2) for D <= 128.
+
+__global__ void __launch_bounds__(kCodecThreads)
+codec_qk_rope_kernel(float *__restrict__ q, float *__restrict__ k, int64_t ld, int T, int H, int D,
+                     const float *__restrict__ qn, const float *__restrict__ kn, float eps, float log_theta,
+                     const int32_t *__restrict__ off, int B, const int32_t *__restrict__ slots,
+                     const int64_t *__restrict__ frame_pos) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t item = blockIdx.x * static_cast<int64_t>(kCodecThreads / kWave) + threadIdx.x / kWave;
+    if (item >= static_cast<int64_t>(T) * H * 2) return;
+    const int which = static_cast<int>(item & 1);
+    const int64_t th = item >> 1;
+    const int t = static_cast<int>(th / H), h = static_cast<int>(th - static_cast<int64_t>(t) * H);
+    const int b = stream_of(off, B, t, 1);
+    const float pos = static_cast<float>(frame_pos[slots[b]] + (t - off[b]));
+    float *v = (which ? k : q) + static_cast<int64_t>(t) * ld + h * D;
+    const float *wn = which ? kn : qn;
+    const int half = D / 2;
+    const bool on = lane < half;
+    const float x1 = on ? v[lane] : 0.f, x2 = on ? v[lane + half] : 0.f;
+    float ss = x1 * x1 + x2 * x2;
+    for (int m = 1; m < kWave; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+    if (!on) return;
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    const float f = x1 * inv * wn[lane], s2 = x2 * inv * wn[lane + half];
+    const float inv_freq = expf(-log_theta * (2.0f * static_cast<float>(lane) / static_cast<float>(D)));
+    float sn, cs;
+    sincosf(pos * inv_freq, &sn, &cs);
+    v[lane] = f * cs - s2 * sn;
+    v[lane + half] = s2 * cs + f * sn;
+}
+
+// sliding-window attention over [retained R frames ; fresh frames]: query i of
+// a stream (position P0 + i) sees retained slot j (position P0 - R + j) when
+// j >= R - ctx and j >= i, and fresh frame i' when i - window < i' <= i.
+// One wave per (token, head); lane = channel (D <= 64).
+
+__global__ void __launch_bounds__(kCodecThreads)
+window_attention_kernel(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+                        int64_t ld, int T, int H, int D, const int32_t *__restrict__ off, int B,
+                        const int32_t *__restrict__ slots, const float *__restrict__ state_k,
+                        const float *__restrict__ state_v, int64_t state_slot_stride, int R, int window,
+                        const int32_t *__restrict__ ctx_len, float scale, float *__restrict__ out, int64_t ldo) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t item = blockIdx.x * static_cast<int64_t>(kCodecThreads / kWave) + threadIdx.x / kWave;
+    if (item >= static_cast<int64_t>(T) * H) return;
+    const int t = static_cast<int>(item / H), h = static_cast<int>(item - static_cast<int64_t>(t) * H);
+    const int b = stream_of(off, B, t, 1);
+    const int i = t - off[b];
+    const int slot = slots[b];
+    const int ctx = ctx_len[slot];
+    const bool on = lane < D;
+    const float qv = on ? q[static_cast<int64_t>(t) * ld + h * D + lane] * scale : 0.f;
+    float m = -INFINITY, l = 0.f, acc = 0.f;
+    auto visit = [&](const float *kp, const float *vp) {
+        float sdot = on ? qv * kp[lane] : 0.f;
+        for (int s = 1; s < kWave; s <<= 1) sdot += __shfl_xor(sdot, s, kWave);
+        const float mn = fmaxf(m, sdot);
+        const float a = expf(m - mn), p = expf(sdot - mn);
+        l = l * a + p;
+        acc = acc * a + (on ? p * vp[lane] : 0.f);
+        m = mn;
+    };
+    const float *sk = state_k + static_cast<int64_t>(slot) * state_slot_stride;
+    const float *sv = state_v + static_cast<int64_t>(slot) * state_slot_stride;
+    const int j0 = max(R - ctx, i - window + 1 + R);  // retained slot j has position P0 - R + j
+    for (int j = max(j0, 0); j < R; ++j) visit(sk + (static_cast<int64_t>(j) * H + h) * D, sv + (static_cast<int64_t>(j) * H + h) * D);
+    for (int f = max(0, i - window + 1); f <= i; ++f) {
+        const int64_t tr = off[b] + f;
+        visit(k + tr * ld + h * D, v + tr * ld + h * D);
+    }
+    if (on) out[static_cast<int64_t>(t) * ldo + h * D + lane] = acc / l;
+}
+
+// retained K/V <- last R frames of [retained ; fresh]; thread per (stream, head, channel)
+__global__ void __launch_bounds__(kCodecThreads)
+kv_update_kernel(const float *__restrict__ k, const float *__restrict__ v, int64_t ld, int H, int D,
+                 const int32_t *__restrict__ off, int B, const int32_t *__restrict__ slots, float *__restrict__ state_k,
+                 float *__restrict__ state_v, int64_t state_slot_stride, int R) {
+    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
+    if (i >= static_cast<int64_t>(B) * H * D) return;
+    const int b = static_cast<int>(i / (static_cast<int64_t>(H) * D));
+    const int hd = static_cast<int>(i - static_cast<int64_t>(b) * H * D);
+    const int F = off[b + 1] - off[b];
+    float *sk = state_k + static_cast<int64_t>(slots[b]) * state_slot_stride + hd;
+    float *sv = state_v + static_cast<int64_t>(slots[b]) * state_slot_stride + hd;
+    const int64_t stride = static_cast<int64_t>(H) * D;
+    for (int j = 0; j < R; ++j) {
+        float kv, vv;
+        if (j + F < R) {
+            kv = sk[(j + F) * stride];
+            vv = sv[(j + F) * stride];
+        } else {
+            const int64_t tr = off[b] + F - R + j;
+            kv = k[tr * ld + hd];
+            vv = v[tr * ld + hd];
+        }
+        sk[j * stride] = kv;
+        sv[j * stride] = vv;
+    }
+}
+
+__global__ void advance_kernel(const int32_t *__restrict__ off, int B, const int32_t *__restrict__ slots,
+                               int64_t *__restrict__ frame_pos, int32_t *__restrict__ ctx_len, int R) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const int F = off[b + 1] - off[b];
+    const int slot = slots[b];
+    frame_pos[slot] += F;
+    ctx_len[slot] = min(R, ctx_len[slot] + F);
+}
+
+__global__ void __launch_bounds__(kCodecThreads)
+pcm16_kernel(const float *__restrict__ x, int64_t n, float *__restrict__ wav, int16_t *__restrict__ pcm) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kCodecThreads) {
+        const float c = fminf(fmaxf(x[i], -1.0f), 1.0f);
+        if (wav) wav[i] = c;
+        if (pcm) pcm[i] = static_cast<int16_t>(rintf(c * 32767.0f));
+    }
+}
+
+int grid_for(int64_t n) {
+    const int64_t g = (n + kCodecThreads - 1) / kCodecThreads;
+    return static_cast<int>(g < 1 ? 1 : g > 8192 ? 8192 : g);
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_codec_embed_sum(const int32_t *codes, int T, int Q, const float *books, int V, int C, float *out,
+                                  int32_t *status, void *stream) {
+    NQ_CHECK_ARG(codes && books && out && T >= 0 && Q > 0 && V > 0 && C > 0);
+    if (T == 0) return NQ_OK;
+    hipLaunchKernelGGL(embed_sum_kernel, dim3(grid_for(static_cast<int64_t>(T) * C)), dim3(kCodecThreads), 0,
+                       static_cast<hipStream_t>(stream), codes, T, Q, books, V, C, out, status);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                                    const int32_t *slots, float *history, const float *w, const float *bias, int Cin,
+                                    int Cout, int K, int dilation, int groups, const float *act_alpha,
+                                    const float *act_beta, const float *residual, int64_t ldres, float *out,
+                                    int64_t ldo, void *stream) {
+    NQ_CHECK_ARG(x && offsets && slots && w && out && B > 0 && u > 0 && T >= 0);
+    NQ_CHECK_ARG(Cin > 0 && Cout > 0 && K >= 1 && K <= kConvKMax && dilation >= 1);
+    NQ_CHECK_ARG(groups == 1 || (groups == Cin && Cin == Cout && !residual && !act_alpha));
+    NQ_CHECK_ARG((act_alpha == nullptr) == (act_beta == nullptr));
+    NQ_CHECK_ARG(ldx >= Cin && ldo >= Cout && (!residual || ldres >= Cout));
+    const int pad = (K - 1) * dilation;
+    NQ_CHECK_ARG(pad == 0 || history);
+    if (T == 0) return NQ_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const Act act{act_alpha, act_beta};
+    const int co_pad = Cout <= 8 ? 8 : Cout <= 16 ? 16 : Cout <= 32 ? 32 : 64;
+    if (groups == 1 && Cin <= 64 && Cout <= 64 && conv_small_lds(Cin, K, dilation, co_pad) <= 150 * 1024) {
+        const size_t lds = conv_small_lds(Cin, K, dilation, co_pad);
+        const dim3 grid(static_cast<unsigned>((T + kCodecThreads - 1) / kCodecThreads));
+#define NQ_SMALL(CO)                                                                                              \
+        hipLaunchKernelGGL(conv_small_kernel<CO>, grid, dim3(kCodecThreads), lds, st, x, ldx, T, offsets, B, u, slots,  \
+                           history, w, bias, Cin, Cout, K, dilation, act, residual, ldres, out, ldo)
+        if (co_pad == 8) NQ_SMALL(8);
+        else if (co_pad == 16) NQ_SMALL(16);
+        else if (co_pad == 32) NQ_SMALL(32);
+        else NQ_SMALL(64);
+#undef NQ_SMALL
+    } else if (groups == 1) {
+        const int cg = Cout <= 16 ? 1 : Cout <= 32 ? 2 : 4;
+        const int rows = kCodecThreads / cg;
+        dim3 grid(static_cast<unsigned>((T + rows - 1) / rows), static_cast<unsigned>((Cout + cg * 16 - 1) / (cg * 16)));
+        if (cg == 1)
+            hipLaunchKernelGGL(conv_kernel<1>, grid, dim3(kCodecThreads), 0, st, x, ldx, T, offsets, B, u, slots,
+                               history, w, bias, Cin, Cout, K, dilation, act, residual, ldres, out, ldo);
+        else if (cg == 2)
+            hipLaunchKernelGGL(conv_kernel<2>, grid, dim3(kCodecThreads), 0, st, x, ldx, T, offsets, B, u, slots,
+                               history, w, bias, Cin, Cout, K, dilation, act, residual, ldres, out, ldo);
+        else
+            hipLaunchKernelGGL(conv_kernel<4>, grid, dim3(kCodecThreads), 0, st, x, ldx, T, offsets, B, u, slots,
+                               history, w, bias, Cin, Cout, K, dilation, act, residual, ldres, out, ldo);
+    } else {
+        hipLaunchKernelGGL(dwconv_kernel, dim3(grid_for(T * Cin)), dim3(kCodecThreads), 0, st, x, ldx, T, offsets, B,
+                           u, slots, history, w, bias, Cin, K, dilation, out, ldo);
+    }
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    if (pad > 0) {
+        hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * Cin)), dim3(kCodecThreads),
+                           0, st, x, ldx, offsets, B, u, slots, history, Cin, pad, groups == 1 ? act : Act{nullptr, nullptr});
+    }
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_causal_transconv(const float *x, int64_t ldx, int64_t T_in, const int32_t *offsets, int B,
+                                         int u_in, int stride_s, const int32_t *slots, float *overlap, const float *w,
+                                         const float *bias, int Cin, int Cout, const float *act_alpha,
+                                         const float *act_beta, float *out, int64_t ldo, void *stream) {
+    NQ_CHECK_ARG(x && offsets && slots && overlap && w && out && B > 0 && u_in > 0 && stride_s >= 1 && T_in >= 0);
+    NQ_CHECK_ARG(Cin > 0 && Cout > 0 && ldx >= Cin && ldo >= Cout);
+    NQ_CHECK_ARG((act_alpha == nullptr) == (act_beta == nullptr));
+    if (T_in == 0) return NQ_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const Act act{act_alpha, act_beta};
+    const int cg = Cout <= 16 ? 1 : Cout <= 32 ? 2 : 4;
+    const int rows = kCodecThreads / cg;
+    const int64_t T_out = T_in * stride_s;
+    const size_t lds = static_cast<size_t>(kConvCi) * cg * 16 * 2 * stride_s * sizeof(float);
+    if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
+    dim3 grid(static_cast<unsigned>((T_out + rows - 1) / rows), static_cast<unsigned>((Cout + cg * 16 - 1) / (cg * 16)));
+    if (cg == 1)
+        hipLaunchKernelGGL(transconv_kernel<1>, grid, dim3(kCodecThreads), lds, st, x, ldx, T_out, offsets, B, u_in,
+                           stride_s, slots, overlap, w, bias, Cin, Cout, act, out, ldo);
+    else if (cg == 2)
+        hipLaunchKernelGGL(transconv_kernel<2>, grid, dim3(kCodecThreads), lds, st, x, ldx, T_out, offsets, B, u_in,
+                           stride_s, slots, overlap, w, bias, Cin, Cout, act, out, ldo);
+    else
+        hipLaunchKernelGGL(transconv_kernel<4>, grid, dim3(kCodecThreads), lds, st, x, ldx, T_out, offsets, B, u_in,
+                           stride_s, slots, overlap, w, bias, Cin, Cout, act, out, ldo);
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL(overlap_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * stride_s * Cout)),
+                       dim3(kCodecThreads), 0, st, x, ldx, offsets, B, u_in, stride_s, slots, overlap, w, Cin, Cout, act);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_window_attention(float *q, float *k, const float *v, int64_t ld, int T, int H, int D,
+                                         const float *q_norm, const float *k_norm, float eps, float rope_theta,
+                                         const int32_t *offsets, int B, const int32_t *slots, const int64_t *frame_pos,
+                                         const int32_t *ctx_len, float *state_k, float *state_v,
+                                         int64_t state_slot_stride, int R, int window, float *out, int64_t ldo,
+                                         void *stream) {
+    NQ_CHECK_ARG(q && k && v && q_norm && k_norm && offsets && slots && frame_pos && ctx_len && out);
+    NQ_CHECK_ARG(state_k && state_v && T >= 0 && B > 0 && H > 0 && D >= 2 && D <= kWave && D % 2 == 0);
+    NQ_CHECK_ARG(R >= 0 && window == R + 1 && state_slot_stride >= static_cast<int64_t>(R) * H * D);
+    NQ_CHECK_ARG(ld >= static_cast<int64_t>(H) * D && ldo >= static_cast<int64_t>(H) * D && rope_theta > 0.f);
+    if (T == 0) return NQ_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int wpb = kCodecThreads / kWave;
+    hipLaunchKernelGGL(codec_qk_rope_kernel, dim3(static_cast<unsigned>((static_cast<int64_t>(T) * H * 2 + wpb - 1) / wpb)),
+                       dim3(kCodecThreads), 0, st, q, k, ld, T, H, D, q_norm, k_norm, eps, logf(rope_theta), offsets, B,
+                       slots, frame_pos);
+    hipLaunchKernelGGL(window_attention_kernel, dim3(static_cast<unsigned>((static_cast<int64_t>(T) * H + wpb - 1) / wpb)),
+                       dim3(kCodecThreads), 0, st, q, k, v, ld, T, H, D, offsets, B, slots, state_k, state_v,
+                       state_slot_stride, R, window, ctx_len, 1.0f / sqrtf(static_cast<float>(D)), out, ldo);
+    if (R > 0)
+        hipLaunchKernelGGL(kv_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * H * D)), dim3(kCodecThreads), 0, st,
+                           k, v, ld, H, D, offsets, B, slots, state_k, state_v, state_slot_stride, R);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_advance(const int32_t *offsets, int B, const int32_t *slots, int64_t *frame_pos,
+                                int32_t *ctx_len, int R, void *stream) {
+    NQ_CHECK_ARG(offsets && slots && frame_pos && ctx_len && B > 0 && R >= 0);
+    hipLaunchKernelGGL(advance_kernel, dim3((B + 63) / 64), dim3(64), 0, static_cast<hipStream_t>(stream), offsets, B,
+                       slots, frame_pos, ctx_len, R);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_pcm16(const float *x, int64_t n, float *wav, int16_t *pcm, void *stream) {
+    NQ_CHECK_ARG(x && n >= 0 && (wav || pcm));
+    if (n == 0) return NQ_OK;
+    hipLaunchKernelGGL(pcm16_kernel, dim3(grid_for(n)), dim3(kCodecThreads), 0, static_cast<hipStream_t>(stream), x, n,
+                       wav, pcm);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_im2col(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                               const int32_t *slots, const float *history, int Cin, int K, int dilation, int transconv,
+                               const float *act_alpha, const float *act_beta, float *a, int64_t lda, void *stream) {
+    NQ_CHECK_ARG(x && offsets && slots && a && B > 0 && u > 0 && T >= 0 && Cin > 0 && Cin % 4 == 0);
+    NQ_CHECK_ARG(ldx % 4 == 0 && lda % 4 == 0 && ldx >= Cin);
+    NQ_CHECK_ARG((act_alpha == nullptr) == (act_beta == nullptr));
+    if (transconv) {
+        NQ_CHECK_ARG(K == 2);
+    } else {
+        NQ_CHECK_ARG(K >= 1 && dilation >= 1 && (K == 1 || history));
+    }
+    NQ_CHECK_ARG(lda >= static_cast<int64_t>(K) * Cin);
+    if (T == 0) return NQ_OK;
+    hipLaunchKernelGGL(im2col_kernel, dim3(grid_for(T * K * (Cin / 4))), dim3(kCodecThreads), 0,
+                       static_cast<hipStream_t>(stream), x, ldx, T, offsets, B, u, slots, history, Cin, K, dilation,
+                       transconv, Act{act_alpha, act_beta}, a, lda);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_history_update(const float *x, int64_t ldx, const int32_t *offsets, int B, int u,
+                                       const int32_t *slots, float *history, int C, int pad, const float *act_alpha,
+                                       const float *act_beta, void *stream) {
+    NQ_CHECK_ARG(x && offsets && slots && history && B > 0 && u > 0 && C > 0 && pad > 0 && ldx >= C);
+    NQ_CHECK_ARG((act_alpha == nullptr) == (act_beta == nullptr));
+    hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * C)), dim3(kCodecThreads), 0,
+                       static_cast<hipStream_t>(stream), x, ldx, offsets, B, u, slots, history, C, pad,
+                       Act{act_alpha, act_beta});
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_transconv_overlap(const int32_t *offsets, int B, int u_in, int stride_s,
+                                          const int32_t *slots, float *overlap, const float *new_overlap, int Cout,
+                                          float *out, int64_t ldo, void *stream) {
+    NQ_CHECK_ARG(offsets && slots && overlap && new_overlap && out && B > 0 && u_in > 0 && stride_s >= 1);
+    NQ_CHECK_ARG(Cout > 0 && ldo >= Cout);
+    hipLaunchKernelGGL(overlap_fixup_kernel, dim3(grid_for(static_cast<int64_t>(B) * stride_s * Cout)),
+                       dim3(kCodecThreads), 0, static_cast<hipStream_t>(stream), offsets, B, u_in, stride_s, slots,
+                       overlap, new_overlap, Cout, out, ldo);
+    return NQ_LAUNCH_STATUS();
+}

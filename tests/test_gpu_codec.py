@@ -1,0 +1,89 @@
+"""Incremental codec step on the GPU vs the oracle: ragged chunks of several streams over two
+consecutive calls (state carried on the device), PCM within 1e-3 RMS of the oracle's waveform."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec as o_codec
+from test_oracle_codec import small_config
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(cfg, device, seed, calls):
+    from nari_qwen3_tts_amd.codec import CodecWeights, IncrementalCodecDecoder
+
+    weights = CodecWeights(cfg, device, seed=seed)
+    dec = IncrementalCodecDecoder(weights, max_streams=8)
+    rng = np.random.default_rng(seed + 1)
+    streams = len(calls[0])
+    states = [dec.new_state() for _ in range(streams)]
+    host_states = [o_codec.empty_state(cfg.as_dict()) for _ in range(streams)]
+    w = weights.host()
+    worst_rms, worst_max = 0.0, 0.0
+    for frames in calls:
+        codes = [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, f))) for f in frames]
+        wav, pcm = dec(codes, states)
+        torch.cuda.synchronize()
+        for b, f in enumerate(frames):
+            want = o_codec.decode_incremental(w, cfg.as_dict(), codes[b].numpy().T, host_states[b])
+            got = wav[b].cpu().numpy()
+            assert got.shape == want.shape == (f * cfg.samples_per_frame,)
+            err = got - want
+            worst_rms = max(worst_rms, float(np.sqrt(np.mean(err * err))) if f else 0.0)
+            worst_max = max(worst_max, float(np.abs(err).max()) if f else 0.0)
+            if f:
+                # PCM16 is the clamped waveform rounded to 1/32767 steps
+                pcm_err = np.abs(pcm[b].cpu().numpy().astype(np.int32) - o_codec.pcm16(want).astype(np.int32))
+                assert pcm_err.max() <= 40
+            assert states[b].frame_position == host_states[b]["frame_position"]
+    return worst_rms, worst_max, dec, states
+
+
+def test_small_codec_two_calls(nq, device):
+    rms, mx, _, _ = _run(small_config(), device, 11, [[5, 1, 7], [3, 4, 0]])
+    print(f"small codec: worst PCM rms err {rms:.3g}, max {mx:.3g}")
+    assert rms <= 1e-4 and mx <= 1e-3, (rms, mx)
+
+
+def test_full_codec_ragged_two_calls(nq, device):
+    from nari_qwen3_tts_amd.codec import CodecConfig
+
+    rms, mx, dec, states = _run(CodecConfig(), device, 21, [[3, 5], [2, 1]])
+    print(f"full codec: worst PCM rms err {rms:.3g}, max {mx:.3g}")
+    assert rms <= 1e-3, (rms, mx)
+    pool = dec.pool
+    assert pool.frame_pos[states[0].slot].item() == 5 and pool.ctx[states[1].slot].item() == 6
+
+
+def test_chunking_does_not_change_the_audio(nq, device):
+    """One stream decoded as 4+3+5 frames on the device equals the same 12 frames in one call."""
+
+    from nari_qwen3_tts_amd.codec import CodecWeights, IncrementalCodecDecoder
+
+    cfg = small_config()
+    dec = IncrementalCodecDecoder(CodecWeights(cfg, device, seed=31), max_streams=4)
+    codes = torch.from_numpy(np.random.default_rng(32).integers(0, cfg.codebook_size, size=(cfg.num_quantizers, 12)))
+    a, b = dec.new_state(), dec.new_state()
+    whole, _ = dec([codes], [a])
+    parts = []
+    for lo, hi in ((0, 4), (4, 7), (7, 12)):
+        wav, _ = dec([codes[:, lo:hi]], [b])
+        parts.append(wav[0])
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(torch.cat(parts).cpu().numpy(), whole[0].cpu().numpy(), atol=2e-5, rtol=1e-4)
+
+
+def test_pcm16_kernel_known_answers(nq, device):
+    from nari_qwen3_tts_amd import _lib
+
+    x = torch.tensor([-2.0, -0.5, 0.0, 0.5, 2.0], device=device)
+    wav = torch.empty_like(x)
+    pcm = torch.empty(5, dtype=torch.int16, device=device)
+    _lib.call("nq_codec_pcm16", x.data_ptr(), 5, wav.data_ptr(), pcm.data_ptr(), _lib.stream(device))
+    torch.cuda.synchronize()
+    assert pcm.tolist() == [-32767, -16384, 0, 16384, 32767]
+    assert wav.tolist() == [-1.0, -0.5, 0.0, 0.5, 1.0]
