@@ -538,7 +538,140 @@ def codec_cpu_baseline(np, weights, cfg, budget_s: float = 10.0) -> dict:
                 sample=f"oracle codec (numpy) over {done} frames of one stream in 12-frame chunks, {elapsed:.1f}s")
 
 
-WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor, "codec": codec_step}
+MIXED_SEED = 1003
+MIXED_PREFILL, MIXED_DECODE = 16, 112
+
+
+class PrefillKey:
+    def __init__(self, capture_batch_size: int, token_capacity: int) -> None:
+        self.capture_batch_size = capture_batch_size
+        self.token_capacity = token_capacity
+        self.capture_sequence_length = None
+
+
+def mixed_attention(args, torch, np) -> dict:
+    """Mixed chunked-prefill + decode batch on the talker attention shape: 16 prefill chunks (qo U{32..256},
+    prior U{0..512}) + 112 decode rows (KV U{64..2048}); GPU planner, then the 28 layers' attention."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
+    from nari_qwen3_tts_amd.talker import TalkerConfig
+    from nari_qwen3_tts_amd.talker_kv import PagedTalkerKV
+
+    dev = torch.device("cuda:0")
+    cfg = TalkerConfig()
+    layers = cfg.num_layers
+    rng = np.random.default_rng(MIXED_SEED)
+    pre_prior = rng.integers(0, 513, size=MIXED_PREFILL)
+    pre_adv = rng.integers(32, 257, size=MIXED_PREFILL)
+    dec_prior = rng.integers(64, 2049, size=MIXED_DECODE)
+    tokens = int(pre_adv.sum()) + MIXED_DECODE
+
+    def build(priors, advances, rows):
+        kv = PagedTalkerKV(num_layers=layers, num_kv_heads=cfg.num_kv_heads, num_qo_heads=cfg.num_qo_heads,
+                           head_dim=cfg.head_dim, total_pages=POOL_PAGES, page_size=PAGE_SIZE,
+                           scratch_page_count=max(rows, -(-int(sum(advances)) // PAGE_SIZE) + 8), workspace_bytes=0,
+                           device=dev, dtype=torch.bfloat16)
+        g = torch.Generator(device=dev)
+        g.manual_seed(MIXED_SEED)
+        for layer in range(layers):
+            kv.storage[layer].normal_(generator=g)
+        pool = rng.permutation(np.asarray(kv.allocator.free_list()))
+        rids, at = [], 0
+        for i, n in enumerate(priors):
+            rid = f"m{i}"
+            kv.add_request(rid)
+            need = -(-int(n) // PAGE_SIZE)
+            if need:
+                kv.adopt_request(rid, pool[at: at + need], int(n))
+            at += need
+            rids.append(rid)
+        key = PrefillKey(rows, int(sum(advances)))
+        ctx = kv.create_prefill(key, slot=0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 20
+        for _ in range(reps):  # the planner: host staging + GPU page table + attention plan
+            pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(int(a) for a in advances))
+            kv.abort(pubs)
+        torch.cuda.synchronize()
+        plan_us = (time.perf_counter() - t0) / reps * 1e6
+        pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(int(a) for a in advances))
+        q = torch.randn(key.token_capacity, cfg.num_qo_heads, cfg.head_dim, device=dev).to(torch.bfloat16)
+        call = HipGraphCaptureDriver(device=dev).capture(lambda: [ctx.run_attention(q, i) for i in range(layers)])
+        call.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            call.replay()
+        end.record()
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / (args.steps * layers)
+        if int(ctx.attention_status.item()) != 0:
+            raise RuntimeError("attention status")
+        return us, plan_us, kv, ctx, q, pubs
+
+    priors = np.concatenate([pre_prior, dec_prior])
+    advances = np.concatenate([pre_adv, np.ones(MIXED_DECODE, dtype=np.int64)])
+    mixed_us, plan_us, kv, ctx, q, pubs = build(priors, advances, MIXED_PREFILL + MIXED_DECODE)
+    del kv, ctx, q, pubs
+    torch.cuda.empty_cache()
+    pre_us, _, kv2, ctx2, q2, pubs2 = build(pre_prior, pre_adv, MIXED_PREFILL)
+    del kv2, ctx2, q2, pubs2
+    torch.cuda.empty_cache()
+    # algorithmic work
+    kv_len = pre_prior + pre_adv
+    pre_flops = float(np.sum(4.0 * cfg.num_qo_heads * cfg.head_dim * (pre_adv * pre_prior + pre_adv * (pre_adv + 1) / 2)))
+    dec_bytes = float(np.sum(dec_prior + 1)) * cfg.num_kv_heads * cfg.head_dim * 4
+    pre_bytes = float(np.sum(kv_len)) * cfg.num_kv_heads * cfg.head_dim * 4
+    tflops = pre_flops / (pre_us / 1e6) / 1e12
+    log(f"mixed batch: {mixed_us:.1f} us/layer (prefill rows alone {pre_us:.1f} us/layer = {tflops:.1f} TFLOP/s); "
+        f"planner {plan_us:.0f} us per decision")
+    result = {
+        "metric": "mixed chunked-prefill + decode attention: us per layer (16 prefill chunks + 112 decode rows)",
+        "value": round(mixed_us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": 1,
+        "ms_per_step": round(mixed_us * layers / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) KV pool, random page permutation, random queries)",
+        "config": {
+            "workload": "talker attention shape (16q/8kv x 128, 28 layers), 16 prefill chunks qo U{32..256} with "
+                        "prior U{0..512} + 112 decode rows KV U{64..2048}, page size 16, 32768-page pool",
+            "global_batch": MIXED_PREFILL + MIXED_DECODE,
+            "tokens": tokens,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": 2500.0,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / 2500.0, 4),
+            "traffic": None,
+            "kernel": "prefill_tile_kernel<128> (prefill rows alone)",
+            "flops_per_launch": pre_flops,
+            "us_per_launch": round(pre_us, 2),
+        },
+        "decode_part": {
+            "bytes_per_layer": dec_bytes + pre_bytes,
+            "achieved_GBps_whole_launch": round((dec_bytes + pre_bytes) / (mixed_us / 1e6) / 1e9, 1),
+        },
+        "planner_us_per_decision": round(plan_us, 1),
+    }
+    return result
+
+
+WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor, "codec": codec_step,
+             "mixed": mixed_attention}
 
 
 def main() -> int:

@@ -46,8 +46,13 @@ constexpr int kPlanGrid = 8;
 
 enum MetaSlot {
     kMetaChunks = 0, kMetaChunkTok = 1, kMetaStatus = 2, kMetaQueries = 3,
-    kMetaDecRows = 4, kMetaBlocks = 5
+    kMetaDecRows = 4, kMetaBlocks = 5, kMetaPTiles = 6
 };
+
+// Prefill MFMA tiles: 32 queries of one row (x 2 query heads = 64 score rows)
+// against 64-key tiles.
+constexpr int kPrefQ = 32;
+constexpr int kPrefK = 64;
 
 // Prefill chunk descriptor.
 struct alignas(16) ChunkDesc {
@@ -66,8 +71,8 @@ struct alignas(16) ChunkDesc {
 
 struct PlanLayout {
     int64_t meta, chunk_indptr, desc, part_ml, part_o;
-    int64_t dec_rows, blocks, spart_ml, spart_o, total;
-    int64_t max_chunks, max_blocks, max_slots;
+    int64_t dec_rows, blocks, spart_ml, spart_o, ptiles, total;
+    int64_t max_chunks, max_blocks, max_slots, max_ptiles;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -80,6 +85,7 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
                    static_cast<int64_t>(max_pages) * page_size / kMaxChunkTokens + 64;
     L.max_blocks = static_cast<int64_t>(max_pages) * (page_size > kBlockTok ? page_size / kBlockTok : 1) + T;
     L.max_slots = kStreamWaves + static_cast<int64_t>(Hkv) * T;
+    L.max_ptiles = (static_cast<int64_t>(T) + kPrefQ - 1) / kPrefQ + kPlanThreads;
     int64_t off = 0;
     L.meta = off;         off = align256(off + 8 * 4);
     L.chunk_indptr = off; off = align256(off + (static_cast<int64_t>(T) + 1) * 4);
@@ -90,6 +96,7 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     L.blocks = off;       off = align256(off + L.max_blocks * 16);
     L.spart_ml = off;     off = align256(off + L.max_slots * G * 2 * 4);
     L.spart_o = off;      off = align256(off + L.max_slots * G * D * 4);
+    L.ptiles = off;       off = align256(off + L.max_ptiles * 16);
     L.total = off;
     return L;
 }
@@ -180,6 +187,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             meta[kMetaQueries] = 0;
             meta[kMetaDecRows] = 0;
             meta[kMetaBlocks] = 0;
+            meta[kMetaPTiles] = 0;
         }
     };
     if (T < 0 || T > max_queries) {
@@ -224,6 +232,29 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         blocks[b] = make_int4(page, slot0 | (ntok << 24), s_dec[r], s_qo[r]);
     }
     if (!lead) return;
+
+    // Prefill rows: 32-query tiles {first query, queries, first page offset,
+    // key limit of the first query (bottom-right causal)}.
+    {
+        int nt = 0;
+        if (tid < n_rows) {
+            const int qo_len = s_qo[tid + 1] - s_qo[tid];
+            if (qo_len > 1) nt = (qo_len + kPrefQ - 1) / kPrefQ;
+        }
+        int n_ptiles;
+        const int t0 = plan_block_scan(nt, s_tmp, &n_ptiles);
+        if (n_ptiles > L.max_ptiles) {
+            fail(NQ_ERR_CAPACITY);
+            return;
+        }
+        int4 *ptiles = reinterpret_cast<int4 *>(ws + L.ptiles);
+        for (int t = 0; t < nt; ++t) {
+            const int qo_len = s_qo[tid + 1] - s_qo[tid];
+            ptiles[t0 + t] = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
+                                       s_kvlen[tid] - qo_len + t * kPrefQ + 1);
+        }
+        if (tid == 0) meta[kMetaPTiles] = n_ptiles;
+    }
 
     // Prefill queries: key chunks per query.
     auto query_keys = [&](int q, int *row_out) {
@@ -943,6 +974,180 @@ dense_short_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ---------------------------------------------------------------------------
+// Prefill rows on MFMA (head dim 128, two query heads per kv head).  A
+// workgroup takes one 32-query tile of a row and one kv head; wave w owns 16
+// queries (w & 1) of query head 2h + (w >> 1).  Per 64-key tile the workgroup
+// stages K ([key][d]) and V transposed ([d][key]) in LDS; each wave computes
+// S = Q K^T with v_mfma_f32_16x16x32_bf16 (Q held in registers as the A
+// operand), masks bottom-right causal limits, runs the online softmax in the
+// exp2 domain on the MFMA output layout (a row's 16 columns sit in 16 lanes),
+// stores P as bf16 in its LDS slice and accumulates O += P V with a second
+// MFMA chain.  Keys past the tile's last query limit are never loaded.
+
+typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf_floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ pf_bf16x8 pf_as_bf16x8(const uint4 &v) {
+    pf_bf16x8 r;
+    __builtin_memcpy(&r, &v, sizeof(r));
+    return r;
+}
+
+template <int Width>
+__device__ __forceinline__ float group_max16(float v) {
+    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f32<kDppMirror>(v));
+    return v;
+}
+
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads)
+prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
+                    const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
+                    int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
+                    int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
+                    int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
+    constexpr int KP = D + 8;        // K row pitch (bf16)
+    constexpr int VP = kPrefK + 8;   // V^T / P row pitch (bf16)
+    constexpr int DT = D / 16;       // 16-wide output column tiles
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[D * VP];
+    __shared__ __attribute__((aligned(16))) uint16_t pbuf[kWaves * 16 * VP];
+    __shared__ int pages[kPrefK];
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) return;
+    const int4 *ptiles = reinterpret_cast<const int4 *>(ws + L.ptiles);
+    const int64_t n_items = static_cast<int64_t>(meta[kMetaPTiles]) * num_kv_heads;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int ps_mask = (1 << ps_log2) - 1;
+    uint16_t *pw = pbuf + wave * 16 * VP;
+    bool bad = false;
+    for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int tile = static_cast<int>(item / num_kv_heads);
+        const int h = static_cast<int>(item - static_cast<int64_t>(tile) * num_kv_heads);
+        const int4 td = ptiles[tile];
+        const int q0 = td.x, nq = td.y, page_start = td.z, lim0 = td.w;
+        const int head = 2 * h + (wave >> 1);
+        const int qsub = (wave & 1) * 16;
+        uint4 qa[D / 32];
+        {
+            const bool ok = qsub + r16 < nq;
+            const uint16_t *qp = q + static_cast<int64_t>(q0 + qsub + r16) * q_s0 + head * q_s1 + kq * 8;
+#pragma unroll
+            for (int kk = 0; kk < D / 32; ++kk)
+                qa[kk] = ok ? *reinterpret_cast<const uint4 *>(qp + kk * 32) : make_uint4(0, 0, 0, 0);
+        }
+        float m[4], l[4];
+        pf_floatx4 acc[DT];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            m[i] = -INFINITY;
+            l[i] = 0.f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
+        const int n_keys = lim0 + nq - 1;
+        for (int kt0 = 0; kt0 < n_keys; kt0 += kPrefK) {
+            __syncthreads();  // the previous tile's LDS reads are done
+            if (threadIdx.x < kPrefK) {
+                const int kk = kt0 + threadIdx.x;
+                const int at = page_start + (kk >> ps_log2);
+                int pg = -1;
+                if (kk < n_keys && at < index_limit) pg = kv_indices[at];
+                if (kk < n_keys && static_cast<unsigned>(pg) >= static_cast<unsigned>(num_pages)) bad = true;
+                pages[threadIdx.x] = pg;
+            }
+            __syncthreads();
+            for (int e = threadIdx.x; e < kPrefK * (D / 8); e += kAttnThreads) {
+                const int key = e / (D / 8), c8 = e - key * (D / 8);
+                const int pg = pages[key];
+                const bool ok = static_cast<unsigned>(pg) < static_cast<unsigned>(num_pages);
+                uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+                if (ok) {
+                    const int64_t off = static_cast<int64_t>(pg) * c_page +
+                                        static_cast<int64_t>((kt0 + key) & ps_mask) * c_slot + h * c_head + c8 * 8;
+                    kv = *reinterpret_cast<const uint4 *>(cache + off);
+                    vv = *reinterpret_cast<const uint4 *>(cache + off + c_kind);
+                }
+                *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kv;
+                const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vt[(c8 * 8 + j) * VP + key] = v16[j];
+            }
+            __syncthreads();
+            // S = Q K^T over 4 key subtiles; lane holds S[qsub + kq*4 + i][kt0 + nt*16 + r16]
+            pf_floatx4 sc[4];
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                sc[nt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < D / 32; ++kk) {
+                    const uint4 kb = *reinterpret_cast<const uint4 *>(ks + (nt * 16 + r16) * KP + kk * 32 + kq * 8);
+                    sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(qa[kk]), pf_as_bf16x8(kb), sc[nt],
+                                                                      0, 0, 0);
+                }
+            }
+            float alpha[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int qj = qsub + kq * 4 + i;
+                const int limit = qj < nq ? lim0 + qj : 0;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    const int key = kt0 + nt * 16 + r16;
+                    const float v = key < limit ? sc[nt][i] * scale_log2 : -INFINITY;
+                    sc[nt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+                mx = group_max16<16>(mx);
+                const float mn = fmaxf(m[i], mx);
+                alpha[i] = m[i] == -INFINITY ? 0.f : exp2f(m[i] - mn);
+                float rs = 0.f;
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    const float p = sc[nt][i] == -INFINITY ? 0.f : exp2f(sc[nt][i] - mn);
+                    rs += p;
+                    pw[(kq * 4 + i) * VP + nt * 16 + r16] = f32_to_bf16(p);
+                }
+                rs = group_sum<16>(rs);
+                l[i] = l[i] * alpha[i] + rs;
+                m[i] = mn;
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha[i];
+            __syncthreads();  // P visible to the whole wave (and V^T already staged)
+#pragma unroll
+            for (int kh = 0; kh < kPrefK / 32; ++kh) {
+                const uint4 pa = *reinterpret_cast<const uint4 *>(pw + r16 * VP + kh * 32 + kq * 8);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const uint4 vb = *reinterpret_cast<const uint4 *>(vt + (dt * 16 + r16) * VP + kh * 32 + kq * 8);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(pa), pf_as_bf16x8(vb), acc[dt],
+                                                                       0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int qj = qsub + kq * 4 + i;
+            if (qj >= nq) continue;
+            const float inv = l[i] > 0.f ? 1.0f / l[i] : 0.f;
+            uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + head * o_s1 + r16;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) op[dt * 16] = f32_to_bf16(acc[dt][i] * inv);
+        }
+    }
+    if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+}
+
 template <int D, int G>
 int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
                  int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,
@@ -970,6 +1175,14 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
                        L, Hkv, sgrid * kWaves, out, o_s0, o_s1);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     if (!prefill_rows) return NQ_OK;
+    if constexpr (D == 128 && G == 2) {
+        const int64_t titems = L.max_ptiles * Hkv;
+        const int tgrid = static_cast<int>(titems < 4096 ? titems : 4096);
+        hipLaunchKernelGGL((prefill_tile_kernel<D>), dim3(tgrid), dim3(kAttnThreads), 0, stream, q, q_s0, q_s1,
+                           cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2,
+                           scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+        return NQ_LAUNCH_STATUS();
+    }
     const int64_t items = L.max_chunks * Hkv;
     const int grid = static_cast<int>(items < 8192 ? items : 8192);
     hipLaunchKernelGGL((paged_chunk_kernel<D, G>), dim3(grid), dim3(kAttnThreads), 0, stream, q,

@@ -123,6 +123,34 @@ def test_mixed_prefill_and_decode_rows(nq, device):
     kv.abort(pubs)
 
 
+@pytest.mark.parametrize("ps,priors,advances", [
+    (16, [0, 17, 300, 5], [2, 33, 64, 100]),
+    (16, [512, 0], [256, 255]),
+    (4, [9, 0, 40], [31, 2, 70]),
+    (32, [100, 31, 0], [1, 45, 96]),
+])
+def test_prefill_rows_match_oracle(nq, device, ps, priors, advances):
+    """Causal prefill rows (MFMA tile path for 16/8 heads of 128) at tile remainders, page sizes and
+    prior lengths that straddle pages, with a decode row mixed in where an advance is 1."""
+
+    rng = np.random.default_rng(sum(advances) + ps)
+    scratch = max(32, -(-(sum(advances) + 5) // ps) + 4)  # padding tokens live in scratch slots
+    kv = make_kv(nq, device, pages=4096, ps=ps, scratch=scratch)
+    g = torch.Generator(device=device)
+    g.manual_seed(ps)
+    kv.storage.copy_(torch.randn(kv.storage.shape, generator=g, device=device).to(torch.bfloat16))
+    rids = adopt_random(kv, rng, np.asarray(priors))
+    key = PrefillKey(len(priors) + 2, sum(advances) + 5)
+    ctx = kv.create_prefill(key, slot=0)
+    pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(advances))
+    q = torch.randn(key.token_capacity, 16, 128, generator=g, device=device).to(torch.bfloat16)
+    out = _run(nq, ctx, q)
+    n = sum(advances)
+    mx, mean = attention_error(to_np(out)[:n], _oracle(ctx, q)[:n])
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"max {mx:.3g} mean {mean:.3g}"
+    kv.abort(pubs)
+
+
 def test_attend_runs_rope_write_and_attention(nq, device):
     """TalkerAttentionContext.attend: K1-style q/k transform, paged write, then attention."""
 
