@@ -148,6 +148,25 @@ int nq_qk_norm_rope_kv_write(uint16_t *q, int64_t q_s0, int64_t q_s1, uint16_t *
                              int cache_position, void *stream);
 
 /*
+ * nq_qk_norm_rope_kv_write reading q, k and v straight from the fp32 split-K
+ * partial planes [splits, tokens, (Hq + 2 Hkv) * D] that nq_linear leaves with
+ * NQ_EPI_PARTIALS (packed QKV projection, model/layers.py:296-306): every
+ * value is the plane-order sum rounded to bf16, exactly the bf16 projection
+ * output.  Rotated q goes to q_out, rotated k to k_out (may be NULL) and the
+ * cache, v to the cache.  The paged / dense cache addressing is that of
+ * nq_qk_norm_rope_kv_write.
+ */
+int nq_qkv_partials_norm_rope_kv_write(const float *partials, int splits, int tokens, uint16_t *q_out,
+                                       int64_t q_s0, int64_t q_s1, uint16_t *k_out, int64_t k_s0,
+                                       int64_t k_s1, const uint16_t *q_weight, const uint16_t *k_weight,
+                                       const int64_t *positions, int64_t pos_stride, int num_qo_heads,
+                                       int num_kv_heads, int head_dim, float eps, float rope_theta,
+                                       int round_to_input, uint16_t *cache, int64_t c_page,
+                                       int64_t c_kind, int64_t c_slot, int64_t c_head,
+                                       const int64_t *write_pages, const int64_t *write_offsets,
+                                       int cache_position, void *stream);
+
+/*
  * Fused sampler with caller-supplied uniforms, one row per workgroup:
  * optional logit masks, repetition penalty on seen ids (x>0 ? x/r : x*r),
  * division by temperature, top-k (value desc, id asc), top-p nucleus and an

@@ -121,6 +121,27 @@ def linear_add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Te
     return _linear(x, weight, _lib.NQ_EPI_ADD_RMSNORM, out, weight.shape[0], residual, norm_weight, eps, workspace)
 
 
+def linear_partials(x: torch.Tensor, weight: torch.Tensor, workspace: torch.Tensor) -> int:
+    """Run the projection but leave its fp32 split-K planes [S, rows, out] at the start of
+    ``workspace`` for a consumer that sums them; returns S."""
+
+    rows, k = x.shape
+    n = weight.shape[0]
+    splits = int(_lib.load().nq_linear_splits(rows, n, k))
+    if splits < 1:
+        raise TypeError(f"no HIP projection for rows={rows}, out={n}, in={k}")
+    need = linear_workspace_bytes(rows, n, k, _lib.NQ_EPI_PARTIALS)
+    if workspace.numel() * workspace.element_size() < need:
+        raise ValueError("workspace too small for the projection partials")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 or weight.stride(1) != 1:
+        raise TypeError("linear needs bf16 tensors with unit inner stride")
+    _lib.require_device(x, weight, workspace)
+    _lib.call("nq_linear", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k,
+              _lib.NQ_EPI_PARTIALS, None, None, 0, None, None, 0.0, workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), _lib.stream(x.device))
+    return splits
+
+
 def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
                     workspace: torch.Tensor | None = None) -> torch.Tensor:
     """SwiGLU input: y = x @ weight.T with weight [2 * I, in] (gate rows, then up rows);
@@ -134,6 +155,7 @@ def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | N
 __all__ = [
     "linear",
     "linear_add_rmsnorm",
+    "linear_partials",
     "linear_silu_mul",
     "linear_workspace_bytes",
     "qwen3_tts_add_rmsnorm",

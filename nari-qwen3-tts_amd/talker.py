@@ -27,6 +27,7 @@ from . import _lib
 from .layers import (
     linear,
     linear_add_rmsnorm,
+    linear_partials,
     linear_silu_mul,
     linear_workspace_bytes,
     qwen3_tts_add_rmsnorm,
@@ -131,7 +132,7 @@ class TalkerDecodeStep:
         self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
         q_w = c.num_qo_heads * c.head_dim
         projections = (
-            (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
+            (c.qkv_width, c.hidden, _lib.NQ_EPI_PARTIALS),
             (c.hidden, q_w, _lib.NQ_EPI_ADD_RMSNORM),
             (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
             (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
@@ -157,13 +158,16 @@ class TalkerDecodeStep:
             ctx.select_layer(index)
             nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
             if self.use_hip_linear:
-                linear(self.hidden, layer.qkv, out=self.qkv, workspace=ws)
+                # the split-K planes of the QKV projection feed the q/k norm + RoPE + KV write directly
+                splits = linear_partials(self.hidden, layer.qkv, ws)
+                q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
+                attended = ctx.attend_partials(layer.attention, ws, splits, q).view(n, q_w)
             else:
                 torch.matmul(self.hidden, layer.qkv.t(), out=self.qkv)
-            q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
-            k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
-            v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
-            attended = ctx.attend(layer.attention, q, k, v).view(n, q_w)
+                q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
+                k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
+                v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
+                attended = ctx.attend(layer.attention, q, k, v).view(n, q_w)
             if self.use_hip_linear:
                 linear_add_rmsnorm(attended, layer.o, self.residual, layer.post_norm, c.rms_eps, self.hidden, ws)
                 linear_silu_mul(self.hidden, layer.gate_up, out=self.act, workspace=ws)

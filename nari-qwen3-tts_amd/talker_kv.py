@@ -195,6 +195,29 @@ class _HipBindingBase:
         )
         return self.run_attention(query, self._layer_index, stream)
 
+    def attend_partials(self, attention: object, partials: torch.Tensor, splits: int,
+                        query_out: torch.Tensor) -> torch.Tensor:
+        """``attend`` fed by the packed QKV projection's fp32 split-K planes (``linear_partials``):
+        q/k norm + RoPE + K/V write straight from the planes, rotated q into ``query_out``
+        [tokens, Hq, D], then paged attention."""
+
+        tokens = self.token_capacity
+        if query_out.shape != (tokens, self.num_qo_heads, self.head_dim) or query_out.stride(-1) != 1:
+            raise ValueError("query_out must be [tokens, Hq, D] with unit inner stride")
+        qw, kw = attention.q_norm.weight, attention.k_norm.weight
+        layer = self.storage[self._layer_index]
+        b = self.buffers
+        stream = _lib.stream(self.device)
+        _lib.call(
+            "nq_qkv_partials_norm_rope_kv_write",
+            partials.data_ptr(), int(splits), tokens, query_out.data_ptr(), query_out.stride(0), query_out.stride(1),
+            None, 0, 0, qw.data_ptr(), kw.data_ptr(), b.position_ids.data_ptr(), 1, self.num_qo_heads,
+            self.num_kv_heads, self.head_dim, float(attention.q_norm.variance_epsilon), float(attention.rope_theta), 1,
+            layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
+            b.write_pages.data_ptr(), b.write_offsets.data_ptr(), 0, stream,
+        )
+        return self.run_attention(query_out, self._layer_index, stream)
+
     def run_attention(self, query: torch.Tensor, layer_index: int, stream: int | None = None) -> torch.Tensor:
         """Paged attention of ``query`` over one layer with the planned metadata (no q/k transform)."""
 

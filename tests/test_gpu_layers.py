@@ -92,3 +92,40 @@ def test_add_rmsnorm_rmsnorm_silu(nq, device):
     gf, uf = gu.float().chunk(2, dim=-1)
     ref = torch.nn.functional.silu(gf) * uf
     assert (act.float() - ref).abs().max().item() <= 3e-2
+
+
+def test_qk_rope_from_projection_partials_equals_bf16_path(nq, device):
+    """q/k norm + RoPE + paged KV write fed by the QKV projection's split-K planes gives the same bits
+    as the projection's bf16 output fed through the in-place kernel."""
+
+    from nari_qwen3_tts_amd import _lib, kernels
+    from nari_qwen3_tts_amd.layers import linear, linear_partials, linear_workspace_bytes
+
+    g = torch.Generator(device=device)
+    g.manual_seed(61)
+    rows, hidden, hq, hkv, d, pages, ps = 64, 2048, 16, 8, 128, 96, 16
+    x = torch.randn(rows, hidden, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn((hq + 2 * hkv) * d, hidden, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    qn = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    kn = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    pos = torch.randint(0, 5000, (rows,), generator=g, device=device)
+    wp = torch.randperm(pages, generator=g, device=device)[:rows]
+    wo = torch.randint(0, ps, (rows,), generator=g, device=device)
+    cache_a = torch.zeros(pages, 2, ps, hkv, d, dtype=torch.bfloat16, device=device)
+    cache_b = torch.zeros_like(cache_a)
+    qkv = linear(x, w)
+    q = qkv[:, : hq * d].view(rows, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(rows, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(rows, hkv, d)
+    kernels.paired_qk_norm_rope_paged_cache_(q, k, v, qn, kn, pos, 1e-6, 1e6, cache_a, wp, wo)
+    ws = torch.empty(linear_workspace_bytes(rows, w.shape[0], hidden, _lib.NQ_EPI_PARTIALS), dtype=torch.uint8,
+                     device=device)
+    splits = linear_partials(x, w, ws)
+    q_out = torch.empty(rows, hq, d, dtype=torch.bfloat16, device=device)
+    _lib.call("nq_qkv_partials_norm_rope_kv_write", ws.data_ptr(), splits, rows, q_out.data_ptr(), q_out.stride(0),
+              q_out.stride(1), None, 0, 0, qn.data_ptr(), kn.data_ptr(), pos.data_ptr(), 1, hq, hkv, d, 1e-6, 1e6, 1,
+              cache_b.data_ptr(), cache_b.stride(0), cache_b.stride(1), cache_b.stride(2), cache_b.stride(3),
+              wp.data_ptr(), wo.data_ptr(), 0, _lib.stream(device))
+    torch.cuda.synchronize()
+    assert torch.equal(q_out, q)
+    assert torch.equal(cache_a, cache_b)
