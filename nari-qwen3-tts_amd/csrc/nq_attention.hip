@@ -747,19 +747,37 @@ merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads,
         if (i0 == i1) continue;  // one wave saw the whole row and wrote it
         for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
             const int jj = t / D, d = t % D;
-            float mx = -INFINITY;
-            for (int i = i0; i <= i1; ++i)
-                mx = fmaxf(mx, part_ml[((static_cast<int64_t>(i + j) * num_kv_heads + h) * G + jj) * 2]);
-            float ls = 0.f, os = 0.f;
-            if (mx != -INFINITY) {
-#pragma unroll 4
-                for (int i = i0; i <= i1; ++i) {
-                    const int64_t slot = static_cast<int64_t>(i + j) * num_kv_heads + h;
-                    const float mk = part_ml[(slot * G + jj) * 2];
-                    const float sc = mk == -INFINITY ? 0.f : exp2f(mk - mx);
-                    ls += part_ml[(slot * G + jj) * 2 + 1] * sc;
-                    os += part_o[(slot * G + jj) * D + d] * sc;
+            // up to 16 contributors per round: all their (m, l, o) loads in flight together
+            constexpr int kR = 16;
+            float mx = -INFINITY, ls = 0.f, os = 0.f;
+            for (int c0 = i0; c0 <= i1; c0 += kR) {
+                float mk[kR], lk[kR], ok[kR];
+#pragma unroll
+                for (int u = 0; u < kR; ++u) {
+                    mk[u] = -INFINITY;
+                    lk[u] = 0.f;
+                    ok[u] = 0.f;
+                    if (c0 + u <= i1) {
+                        const int64_t slot = static_cast<int64_t>(c0 + u + j) * num_kv_heads + h;
+                        mk[u] = part_ml[(slot * G + jj) * 2];
+                        lk[u] = part_ml[(slot * G + jj) * 2 + 1];
+                        ok[u] = part_o[(slot * G + jj) * D + d];
+                    }
                 }
+                float cm = mx;
+#pragma unroll
+                for (int u = 0; u < kR; ++u) cm = fmaxf(cm, mk[u]);
+                if (cm == -INFINITY) continue;
+                const float keep = mx == -INFINITY ? 0.f : exp2f(mx - cm);
+                ls *= keep;
+                os *= keep;
+#pragma unroll
+                for (int u = 0; u < kR; ++u) {
+                    const float sc = mk[u] == -INFINITY ? 0.f : exp2f(mk[u] - cm);
+                    ls += lk[u] * sc;
+                    os += ok[u] * sc;
+                }
+                mx = cm;
             }
             out[dr.y * o_s0 + (h * G + jj) * o_s1 + d] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
         }
