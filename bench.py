@@ -35,9 +35,10 @@ PAGE_SIZE = 16
 POOL_PAGES = 32768
 KV_LO, KV_HI = 64, 2048
 SEED = 1002
-# HBM bytes one attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE counter passes
-# in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device copy: x2.0 and x1.0).
-ATTENTION_TRAFFIC_BYTES = 251_622_400
+# HBM bytes one attention launch of this workload moves (stream + merge kernels), from the FETCH_SIZE /
+# WRITE_SIZE counter passes in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device
+# copy: x2.0 and x1.0).
+ATTENTION_TRAFFIC_BYTES = 256_354_600
 
 
 def log(*a):
