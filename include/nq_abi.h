@@ -101,16 +101,21 @@ int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
  *   (kind 0 = K, 1 = V; the reference layout is [pages, 2, ps, Hkv, D]).
  * out: bf16 [tokens, num_qo_heads, head_dim] with strides (o_s0, o_s1, 1).
  * The plan in `workspace` must come from nq_attention_plan for the same
- * metadata and the same (max_query_tokens, max_pages).  prefill_rows = 0
- * promises the plan holds no row with more than one query (the chunked
- * prefill kernels are then not launched).  status (device int32, may be NULL) is set to NQ_ERR_INVALID_
- * ARGUMENT when a page id outside [0, num_pages) is met (that page is skipped).
+ * metadata and the same (max_query_tokens, max_pages).  `parts` selects the
+ * launches: NQ_ATTN_DECODE (rows with one query: stream + merge kernels),
+ * NQ_ATTN_PREFILL (rows with several queries), or both.  The two parts read
+ * the same plan and write disjoint output rows, so a caller may issue them on
+ * two streams to run them concurrently; NQ_ATTN_DECODE alone promises the plan
+ * holds no row with more than one query.  status (device int32, may be NULL)
+ * is set to NQ_ERR_INVALID_ARGUMENT when a page id outside [0, num_pages) is
+ * met (that page is skipped).
  */
+enum nq_attention_parts { NQ_ATTN_DECODE = 1, NQ_ATTN_PREFILL = 2 };
 int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
                        int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
                        int num_pages, const int32_t *kv_indices, int page_size, int num_qo_heads,
                        int num_kv_heads, int head_dim, float sm_scale, uint16_t *out, int64_t o_s0,
-                       int64_t o_s1, int max_query_tokens, int max_pages, int prefill_rows,
+                       int64_t o_s1, int max_query_tokens, int max_pages, int parts,
                        void *workspace, int64_t workspace_bytes, int32_t *status, void *stream);
 
 /*

@@ -28,6 +28,8 @@ NQ_EPI_NONE = 0
 NQ_EPI_ADD_RMSNORM = 1
 NQ_EPI_SILU_MUL = 2
 NQ_EPI_PARTIALS = 3
+NQ_ATTN_DECODE = 1
+NQ_ATTN_PREFILL = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

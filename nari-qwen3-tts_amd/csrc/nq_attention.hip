@@ -53,6 +53,7 @@ enum MetaSlot {
 // against 64-key tiles.
 constexpr int kPrefQ = 32;
 constexpr int kPrefK = 64;
+constexpr int kPrefPages = 1024;  // page ids of one prefill item kept in LDS
 
 // Prefill chunk descriptor.
 struct alignas(16) ChunkDesc {
@@ -727,21 +728,22 @@ __global__ void __launch_bounds__(kAttnThreads) paged_stream_kernel(NQ_STREAM_AR
 // one wave touched: one workgroup per pair, one thread per output element.
 template <int D, int G>
 __global__ void __launch_bounds__(kAttnThreads)
-merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads, int worker_cap,
+merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads, int worker_cap, int max_rows,
                     uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1) {
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
-    if (meta[kMetaStatus] != NQ_OK) return;
-    const int n_dec = meta[kMetaDecRows];
-    const int NBT = meta[kMetaBlocks];
-    if (NBT == 0) return;
-    const int S = stream_spans(NBT, worker_cap / num_kv_heads);
     const int4 *dec_rows = reinterpret_cast<const int4 *>(ws + L.dec_rows);
     const float *part_ml = reinterpret_cast<const float *>(ws + L.spart_ml);
     const float *part_o = reinterpret_cast<const float *>(ws + L.spart_o);
-    const int n_pairs = n_dec * num_kv_heads;
-    for (int p = blockIdx.x; p < n_pairs; p += gridDim.x) {
-        const int h = p / n_dec, j = p - h * n_dec;
+    // pair p = (decode row j, kv head h) with j = p / Hkv: the row descriptor load does not wait
+    // for the plan's counters
+    for (int p = blockIdx.x; p < max_rows * num_kv_heads; p += gridDim.x) {
+        const int j = p / num_kv_heads, h = p - j * num_kv_heads;
         const int4 dr = dec_rows[j];
+        if (meta[kMetaStatus] != NQ_OK) return;
+        const int n_dec = meta[kMetaDecRows];
+        const int NBT = meta[kMetaBlocks];
+        if (j >= n_dec || NBT == 0) return;  // pairs only grow with p
+        const int S = stream_spans(NBT, worker_cap / num_kv_heads);
         const int i0 = span_of(dr.z, NBT, S);
         const int i1 = span_of(dr.z + dr.w - 1, NBT, S);
         if (i0 == i1) continue;  // one wave saw the whole row and wrote it
@@ -1001,7 +1003,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 // operand), masks bottom-right causal limits, runs the online softmax in the
 // exp2 domain on the MFMA output layout (a row's 16 columns sit in 16 lanes),
 // stores P as bf16 in its LDS slice and accumulates O += P V with a second
-// MFMA chain.  Keys past the tile's last query limit are never loaded.
+// MFMA chain.  Keys past the tile's last query limit are never loaded.  V^T
+// rows keep their 8-key chunks XOR-swizzled by (d >> 3) & 7, which spreads the
+// transposing writes over the banks while each MFMA operand read stays one
+// contiguous 16-byte chunk.
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_floatx4 __attribute__((ext_vector_type(4)));
@@ -1034,7 +1039,7 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
     __shared__ __attribute__((aligned(16))) uint16_t vt[D * VP];
     __shared__ __attribute__((aligned(16))) uint16_t pbuf[kWaves * 16 * VP];
-    __shared__ int pages[kPrefK];
+    __shared__ int pages[kPrefPages];
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
     if (meta[kMetaStatus] != NQ_OK) return;
     const int4 *ptiles = reinterpret_cast<const int4 *>(ws + L.ptiles);
@@ -1070,34 +1075,69 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
         const int n_keys = lim0 + nq - 1;
+        // K/V of the next 64-key tile are loaded into registers while the current tile is
+        // computed; each thread owns kStageVec (key, 8-channel) pieces of a tile.
+        constexpr int kStageVec = kPrefK * (D / 8) / kAttnThreads;
+        uint4 kr[kStageVec], vr[kStageVec];
+        // the item's page list goes to LDS once (when it fits), so a tile's K/V loads do not wait
+        // for an index load
+        const int n_pg = n_keys > 0 ? ((n_keys - 1) >> ps_log2) + 1 : 0;
+        const bool lds_pages = n_pg <= kPrefPages;
+        __syncthreads();  // the previous item's page reads are done
+        if (lds_pages) {
+            for (int t = threadIdx.x; t < n_pg; t += kAttnThreads) {
+                const int at = page_start + t;
+                const int pg = at < index_limit ? kv_indices[at] : -1;
+                if (static_cast<unsigned>(pg) >= static_cast<unsigned>(num_pages)) bad = true;
+                pages[t] = pg;
+            }
+        }
+        __syncthreads();
+        auto issue = [&](int kt) {
+            int pg[kStageVec];
+#pragma unroll
+            for (int v = 0; v < kStageVec; ++v) {
+                const int e = threadIdx.x + v * kAttnThreads;
+                const int kk = kt + e / (D / 8);
+                if (lds_pages) {
+                    pg[v] = kk < n_keys ? pages[kk >> ps_log2] : -1;
+                } else {
+                    const int at = page_start + (kk >> ps_log2);
+                    pg[v] = (kk < n_keys && at < index_limit) ? kv_indices[at] : -1;
+                    if (kk < n_keys && static_cast<unsigned>(pg[v]) >= static_cast<unsigned>(num_pages)) bad = true;
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < kStageVec; ++v) {
+                const int e = threadIdx.x + v * kAttnThreads;
+                const int key = e / (D / 8), c8 = e - key * (D / 8);
+                kr[v] = make_uint4(0, 0, 0, 0);
+                vr[v] = make_uint4(0, 0, 0, 0);
+                if (static_cast<unsigned>(pg[v]) < static_cast<unsigned>(num_pages)) {
+                    const int64_t off = static_cast<int64_t>(pg[v]) * c_page +
+                                        static_cast<int64_t>((kt + key) & ps_mask) * c_slot + h * c_head + c8 * 8;
+                    kr[v] = *reinterpret_cast<const uint4 *>(cache + off);
+                    vr[v] = *reinterpret_cast<const uint4 *>(cache + off + c_kind);
+                }
+            }
+        };
+        if (n_keys > 0) issue(0);
         for (int kt0 = 0; kt0 < n_keys; kt0 += kPrefK) {
             __syncthreads();  // the previous tile's LDS reads are done
-            if (threadIdx.x < kPrefK) {
-                const int kk = kt0 + threadIdx.x;
-                const int at = page_start + (kk >> ps_log2);
-                int pg = -1;
-                if (kk < n_keys && at < index_limit) pg = kv_indices[at];
-                if (kk < n_keys && static_cast<unsigned>(pg) >= static_cast<unsigned>(num_pages)) bad = true;
-                pages[threadIdx.x] = pg;
-            }
-            __syncthreads();
-            for (int e = threadIdx.x; e < kPrefK * (D / 8); e += kAttnThreads) {
-                const int key = e / (D / 8), c8 = e - key * (D / 8);
-                const int pg = pages[key];
-                const bool ok = static_cast<unsigned>(pg) < static_cast<unsigned>(num_pages);
-                uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-                if (ok) {
-                    const int64_t off = static_cast<int64_t>(pg) * c_page +
-                                        static_cast<int64_t>((kt0 + key) & ps_mask) * c_slot + h * c_head + c8 * 8;
-                    kv = *reinterpret_cast<const uint4 *>(cache + off);
-                    vv = *reinterpret_cast<const uint4 *>(cache + off + c_kind);
-                }
-                *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kv;
-                const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vv);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) vt[(c8 * 8 + j) * VP + key] = v16[j];
+            for (int v = 0; v < kStageVec; ++v) {
+                const int e = threadIdx.x + v * kAttnThreads;
+                const int key = e / (D / 8), c8 = e - key * (D / 8);
+                *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kr[v];
+                const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vr[v]);
+                // rows d = c8*8 + j; 8-key chunks swizzled by (d >> 3) & 7 == c8 & 7 so the lanes
+                // of one key (consecutive c8) land on different banks
+                const int pos = (((key >> 3) ^ (c8 & 7)) << 3) + (key & 7);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vt[(c8 * 8 + j) * VP + pos] = v16[j];
             }
             __syncthreads();
+            if (kt0 + kPrefK < n_keys) issue(kt0 + kPrefK);
             // S = Q K^T over 4 key subtiles; lane holds S[qsub + kq*4 + i][kt0 + nt*16 + r16]
             pf_floatx4 sc[4];
 #pragma unroll
@@ -1147,7 +1187,9 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 const uint4 pa = *reinterpret_cast<const uint4 *>(pw + r16 * VP + kh * 32 + kq * 8);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    const uint4 vb = *reinterpret_cast<const uint4 *>(vt + (dt * 16 + r16) * VP + kh * 32 + kq * 8);
+                    const int d = dt * 16 + r16;
+                    const uint4 vb =
+                        *reinterpret_cast<const uint4 *>(vt + d * VP + (((kh * 4 + kq) ^ ((d >> 3) & 7)) << 3));
                     acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(pa), pf_as_bf16x8(vb), acc[dt],
                                                                        0, 0, 0);
                 }
@@ -1171,8 +1213,9 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
                  int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,
                  const int32_t *kv_indices, int index_limit, int Hkv, int ps_log2, float scale,
                  uint16_t *out, int64_t o_s0, int64_t o_s1, char *ws, const PlanLayout &L,
-                 int max_queries, int prefill_rows, int32_t *status, hipStream_t stream) {
+                 int max_queries, int parts, int32_t *status, hipStream_t stream) {
     const int sgrid = kStreamWaves / kWaves;
+    if (parts & NQ_ATTN_DECODE) {
 #define NQ_LAUNCH_STREAM(KERNEL, SMALL)                                                          \
     hipLaunchKernelGGL((KERNEL<D, G, SMALL>), dim3(sgrid), dim3(kAttnThreads), 0, stream, q, q_s0, \
                        q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,         \
@@ -1190,9 +1233,10 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
     const int64_t pairs = static_cast<int64_t>(max_queries) * Hkv;
     const int mgrid = static_cast<int>(pairs < 2048 ? pairs : 2048);
     hipLaunchKernelGGL((merge_stream_kernel<D, G>), dim3(mgrid), dim3(kAttnThreads), 0, stream, ws,
-                       L, Hkv, sgrid * kWaves, out, o_s0, o_s1);
+                       L, Hkv, sgrid * kWaves, max_queries, out, o_s0, o_s1);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
-    if (!prefill_rows) return NQ_OK;
+    }
+    if (!(parts & NQ_ATTN_PREFILL)) return NQ_OK;
     if constexpr (D == 128 && G == 2) {
         const int64_t titems = L.max_ptiles * Hkv;
         const int tgrid = static_cast<int>(titems < 4096 ? titems : 4096);
@@ -1270,9 +1314,10 @@ extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,
                                   const int32_t *kv_indices, int page_size, int num_qo_heads,
                                   int num_kv_heads, int head_dim, float sm_scale, uint16_t *out,
                                   int64_t o_s0, int64_t o_s1, int max_query_tokens, int max_pages,
-                                  int prefill_rows, void *workspace, int64_t workspace_bytes,
+                                  int parts, void *workspace, int64_t workspace_bytes,
                                   int32_t *status, void *stream) {
     NQ_CHECK_ARG(q && cache && kv_indices && out && workspace);
+    NQ_CHECK_ARG(parts >= 1 && parts <= (NQ_ATTN_DECODE | NQ_ATTN_PREFILL));
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1);
     NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
     NQ_CHECK_ARG(max_query_tokens >= 1 && max_pages >= 1);
@@ -1291,7 +1336,7 @@ extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,
         return nq::launch_paged<DD, GG>(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head,     \
                                         num_pages, kv_indices, max_pages, num_kv_heads, ps_log2,  \
                                         sm_scale, out, o_s0, o_s1, ws, L, max_query_tokens,       \
-                                        prefill_rows, status, s);
+                                        parts, status, s);
     NQ_PAGED(128, 1) NQ_PAGED(128, 2) NQ_PAGED(128, 4) NQ_PAGED(128, 8)
     NQ_PAGED(64, 1) NQ_PAGED(64, 2) NQ_PAGED(64, 4) NQ_PAGED(64, 8)
 #undef NQ_PAGED

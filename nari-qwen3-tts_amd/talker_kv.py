@@ -113,6 +113,7 @@ class _HipBindingBase:
         self.write_offsets = self.buffers.write_offsets
         self.metadata: TalkerAttentionMetadata | None = None
         self._layer_index = 0
+        self._side: torch.cuda.Stream | None = None
 
     # -- planning ---------------------------------------------------------
     def _stage(self, metadata: TalkerAttentionMetadata) -> None:
@@ -193,7 +194,7 @@ class _HipBindingBase:
             layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
             b.write_pages.data_ptr(), b.write_offsets.data_ptr(), 0, stream,
         )
-        return self.run_attention(query, self._layer_index, stream)
+        return self.run_attention(query, self._layer_index)
 
     def attend_partials(self, attention: object, partials: torch.Tensor, splits: int,
                         query_out: torch.Tensor) -> torch.Tensor:
@@ -216,11 +217,30 @@ class _HipBindingBase:
             layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3),
             b.write_pages.data_ptr(), b.write_offsets.data_ptr(), 0, stream,
         )
-        return self.run_attention(query_out, self._layer_index, stream)
+        return self.run_attention(query_out, self._layer_index)
 
     def run_attention(self, query: torch.Tensor, layer_index: int, stream: int | None = None) -> torch.Tensor:
-        """Paged attention of ``query`` over one layer with the planned metadata (no q/k transform)."""
+        """Paged attention of ``query`` over one layer with the planned metadata (no q/k transform).
 
+        Prefill bindings run the prefill rows on a side stream while the decode rows run on the
+        caller's stream (fork/join through events, so the pair is graph-capturable)."""
+
+        if not self.prefill or stream is not None:
+            return self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE | (
+                _lib.NQ_ATTN_PREFILL if self.prefill else 0), _lib.stream(self.device) if stream is None else stream)
+        main = torch.cuda.current_stream(self.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(self.device)
+            self._fork, self._join = torch.cuda.Event(), torch.cuda.Event()
+        self._fork.record(main)
+        self._side.wait_event(self._fork)
+        self._attention_call(query, layer_index, _lib.NQ_ATTN_PREFILL, self._side.cuda_stream)
+        out = self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE, main.cuda_stream)
+        self._join.record(self._side)
+        main.wait_event(self._join)
+        return out
+
+    def _attention_call(self, query: torch.Tensor, layer_index: int, parts: int, stream: int) -> torch.Tensor:
         layer = self.storage[layer_index]
         out = self.output
         _lib.call(
@@ -230,9 +250,8 @@ class _HipBindingBase:
             layer.shape[0], self.buffers.kv_indices.data_ptr(),
             self.page_size, self.num_qo_heads, self.num_kv_heads, self.head_dim, float(self.head_dim) ** -0.5,
             out.data_ptr(), out.stride(0), out.stride(1),
-            self.token_capacity, self.index_capacity, int(self.prefill), self.workspace.data_ptr(),
-            self.workspace.numel(), self.attention_status.data_ptr(),
-            _lib.stream(self.device) if stream is None else stream,
+            self.token_capacity, self.index_capacity, int(parts), self.workspace.data_ptr(),
+            self.workspace.numel(), self.attention_status.data_ptr(), stream,
         )
         return out
 
