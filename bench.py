@@ -201,7 +201,12 @@ def cpu_baseline(torch, np, w, budget_s: float = 10.0):
         L = wts.layers[li]
         layer_np = dict(input_norm=host(L.input_norm), qkv=host(L.qkv), o=host(L.o), post_norm=host(L.post_norm),
                         gate_up=host(L.gate_up), down=host(L.down), q_norm=host(L.attention.q_norm.weight),
-                        k_norm=host(L.attention.k_norm.weight))
+                        k_norm=host(L.attention.k_norm.weight), fp8_gate_up=wts.fp8_gate_up)
+        if wts.fp8_gate_up:
+            # FP8 weight blocks are prepared at load time, outside the timed step (bit-identical
+            # to the oracle's own quantizer)
+            layer_np["gate_up_q"] = L.gate_up_q.view(torch.uint8).cpu().numpy()
+            layer_np["gate_up_s"] = L.gate_up_scales.cpu().numpy()
         nxt = host(wts.final_norm) if li + 1 == cfg.num_layers else host(wts.layers[li + 1].input_norm)
         cache = np.zeros((1, len(pages_used) + ROWS, 2, PAGE_SIZE, cfg.num_kv_heads, cfg.head_dim), dtype=np.float32)
         cache[0, : len(pages_used)] = host(kv.storage[li].index_select(0, idx))
@@ -275,6 +280,8 @@ def talker_decode(args, torch, np) -> dict:
             "global_batch": ROWS,
             "seq_len": f"U[{KV_LO},{KV_HI}] prior KV",
             "parallelism": "single GPU",
+            "gate_up": ("fp8 e4m3, 128x128 weight blocks, 1x128 activation groups (the reference serving build)"
+                        if w["weights"].fp8_gate_up else "bf16"),
         },
         "roofline": {
             "bound": "hbm",

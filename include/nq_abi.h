@@ -258,6 +258,82 @@ int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, 
               void *stream);
 
 /*
+ * FP8 (OCP e4m3fn) block quantization of a bf16 weight matrix w [N, K] into
+ * codes q [N, K] and fp32 scales [N / 128, K / 128]: per 128 x 128 block,
+ * scale = 2^ceil(log2(max(max|w|, 1e-4) / 448)) and q = e4m3fn(w / scale)
+ * rounded to nearest even.  Replaces quantize_fp8_weight_blocks
+ * (model/layers.py:10-25) as run by GatedMLP.initialize_fp8_gate_up_weight
+ * (model/layers.py:226-239).  N, K multiples of 128 (else
+ * NQ_ERR_INVALID_ARGUMENT, the reference's ValueError); strides in elements.
+ */
+int nq_quantize_fp8_blocks(const uint16_t *w, int64_t w_s0, int N, int K, uint8_t *q, int64_t q_s0,
+                           float *scales, int64_t s_s0, void *stream);
+
+/*
+ * Activation quantization of the block-scaled FP8 GEMM: bf16 x [M, K] ->
+ * codes q [M, K] and fp32 scales [M, K / 128], per row and 128 columns
+ * scale = max|x| / 448 (1 for an all-zero group), q = e4m3fn(x / scale).  The
+ * bf16-input half of flashinfer fp8_blockscale_gemm_sm90 as called at
+ * model/layers.py:253-261 (published DeepGEMM / DeepSeek-V3 1 x 128 scheme).
+ */
+int nq_quantize_fp8_rows(const uint16_t *x, int64_t x_s0, int M, int K, uint8_t *q, int64_t q_s0,
+                         float *scales, int64_t s_s0, void *stream);
+
+/*
+ * nq_add_rmsnorm with the normalised row stored quantized (codes xq [rows,
+ * width], scales sx [rows, width / 128], as nq_quantize_fp8_rows of the bf16
+ * result) instead of in `hidden`: the post-attention add-RMSNorm feeding the
+ * FP8 gate/up projection (model/components.py:56-63 into GatedMLP.forward,
+ * model/layers.py:264-270).  width % 128 == 0.
+ */
+int nq_add_rmsnorm_fp8(const uint16_t *hidden, uint16_t *residual, const uint16_t *weight, int rows,
+                       int width, float eps, uint8_t *xq, int64_t xq_s0, float *sx, int64_t sx_s0,
+                       void *stream);
+
+/*
+ * nq_linear with NQ_EPI_ADD_RMSNORM whose normalised output is stored as
+ * nq_add_rmsnorm_fp8 stores it: the o_proj + post-attention add-RMSNorm of a
+ * talker layer with FP8 gate/up.  N % 128 == 0; workspace as
+ * nq_linear_workspace_bytes(M, N, K, NQ_EPI_ADD_RMSNORM).
+ */
+int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M,
+                              int N, int K, uint16_t *residual, const uint16_t *norm_weight, float eps,
+                              uint8_t *xq, int64_t xq_s0, float *sx, int64_t sx_s0, void *workspace,
+                              int64_t workspace_bytes, void *stream);
+
+/*
+ * Block-scaled FP8 projection for M <= 128 rows: Y[m, n] = sum over 128-wide
+ * K blocks kb of sx[m, kb] * sw[n / 128, kb] * (q_x[m, kb] . q_w[n, kb]) with
+ * fp32 accumulation (flashinfer fp8_blockscale_gemm_sm90 as called by
+ * GatedMLP._project_gate_up, model/layers.py:241-262), epilogues as
+ * nq_linear: NQ_EPI_NONE (out = bf16(Y)), NQ_EPI_SILU_MUL (the SwiGLU of the
+ * gate/up output, model/layers.py:264-270) or NQ_EPI_PARTIALS.  N % 128 == 0,
+ * K % 1024 == 0 (K % 512 when M > 64); codes 16-byte aligned with strides
+ * multiple of 16 bytes; scale strides in elements.
+ */
+int nq_linear_fp8_splits(int M, int N, int K);
+int64_t nq_linear_fp8_workspace_bytes(int M, int N, int K, int epilogue);
+int nq_linear_fp8(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, const uint8_t *wq,
+                  int64_t w_s0, const float *sw, int64_t sw_s0, int M, int N, int K, int epilogue,
+                  uint16_t *out, int64_t o_s0, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Gate/up with the SwiGLU fused, for the talker's MLP shape (M <= 64 rows,
+ * K = 2048, I % 24 == 0; else NQ_ERR_UNSUPPORTED and the caller uses
+ * nq_linear_fp8 with NQ_EPI_SILU_MUL): out[M, I] = silu(bf16(gate)) *
+ * bf16(up) of the block-scaled FP8 product (GatedMLP.forward with FP8
+ * gate/up, model/layers.py:241-270), whole dot products per workgroup (no
+ * split-K planes, no second kernel).  The weight codes are the
+ * nq_quantize_fp8_blocks codes with their rows interleaved by
+ * nq_fp8_pack_swiglu (the block scales stay those of the [gate; up] layout).
+ */
+int nq_fp8_pack_swiglu(const uint8_t *q, int64_t q_s0, int I, int K, uint8_t *packed, int64_t p_s0,
+                       void *stream);
+int nq_linear_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, int M,
+                         const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
+                         uint16_t *out, int64_t o_s0, void *stream);
+
+/*
  * Incremental codec-decoder step (fp32, channels-last [T, C]).  Replaces the
  * stateful pieces of Qwen3TTSIncrementalDecoder (model/incremental_codec.py):
  * the fresh rows of B streams are concatenated; stream b owns frames

@@ -59,6 +59,15 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_splits": [_I, _I, _I],
     "nq_linear_workspace_bytes": [_I, _I, _I, _I],
     "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P, _F, _P, _L, _P],
+    "nq_quantize_fp8_blocks": [_P, _L, _I, _I, _P, _L, _P, _L, _P],
+    "nq_quantize_fp8_rows": [_P, _L, _I, _I, _P, _L, _P, _L, _P],
+    "nq_add_rmsnorm_fp8": [_P, _P, _P, _I, _I, _F, _P, _L, _P, _L, _P],
+    "nq_linear_add_rmsnorm_fp8": [_P, _L, _P, _L, _I, _I, _I, _P, _P, _F, _P, _L, _P, _L, _P, _L, _P],
+    "nq_linear_fp8_splits": [_I, _I, _I],
+    "nq_linear_fp8_workspace_bytes": [_I, _I, _I, _I],
+    "nq_linear_fp8": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P],
+    "nq_fp8_pack_swiglu": [_P, _L, _I, _I, _P, _L, _P],
+    "nq_linear_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
     "nq_codec_embed_sum": [_P, _I, _I, _P, _I, _I, _P, _P, _P],
     "nq_codec_causal_conv": [_P, _L, _L, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P],
     "nq_codec_causal_transconv": [_P, _L, _L, _P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _L, _P],
@@ -74,6 +83,7 @@ _RESTYPES = {
     "nq_status_string": ctypes.c_char_p,
     "nq_attention_workspace_bytes": ctypes.c_int64,
     "nq_linear_workspace_bytes": ctypes.c_int64,
+    "nq_linear_fp8_workspace_bytes": ctypes.c_int64,
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -1,0 +1,499 @@
+// FP8 (OCP e4m3fn) gate/up projection of the talker decode step.
+//
+// Weights: the 128 x 128 block quantization of model/layers.py:10-25 -- per
+// block, max |w| clamped to >= 1e-4, a power-of-two scale 2^ceil(log2(max /
+// 448)) and e4m3fn codes of w / scale rounded to nearest even.
+//
+// GEMM: the block-scaled FP8 product that model/layers.py:241-262 runs through
+// flashinfer's fp8_blockscale_gemm_sm90 (the DeepGEMM fine-grained scheme):
+// activations quantized per row and 128 columns (scale = max |x| / 448, codes
+// of x / scale), fp32 accumulation with both scales applied per 128-wide K
+// block, y[m, n] = sum_kb sx[m, kb] sw[n / 128, kb] (qx[m, kb] . qw[n, kb]).
+//
+// The GEMM keeps the bf16 skinny GEMM's plan -- each weight byte read from
+// HBM once with one-shot 128-bit loads, the X slice staged in LDS, split-K
+// fp32 partial planes summed in plane order by the consumer -- and runs the
+// gfx950 MFMA v_mfma_scale_f32_16x16x128_f8f6f4 (formats e4m3 x e4m3, unit
+// E8M0 scales): one instruction covers exactly one 128-wide K block of a
+// 16-column tile, so the block's scale product is applied once to each
+// instruction result.  An FP8 weight row slice of 1024 bytes carries the same
+// 64 KiB per workgroup in flight as the bf16 GEMM's 512-element slice, with
+// half the K splits.
+#include "nq_common.h"
+#include "nq_internal.h"
+
+namespace nq {
+
+namespace {
+
+constexpr int kFp8Threads = 256;
+constexpr int kFp8Waves = kFp8Threads / kWave;
+
+// Smallest power of two >= v for a positive normal v.
+__device__ __forceinline__ float pow2_ceil(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x7fffffu) == 0 ? v : __uint_as_float((u & 0x7f800000u) + 0x00800000u);
+}
+
+// One workgroup per 128 x 128 block: thread t holds rows t/16 + 16 i (i < 8),
+// columns (t % 16) * 8 .. + 7 of the block.
+__global__ void __launch_bounds__(kFp8Threads)
+quantize_blocks_kernel(const uint16_t *__restrict__ w, int64_t w_s0, uint8_t *__restrict__ q, int64_t q_s0,
+                       float *__restrict__ scales, int64_t s_s0) {
+    __shared__ float wmax[kFp8Waves];
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 128 + threadIdx.x / 16;
+    const int c0 = blockIdx.x * 128 + (threadIdx.x & 15) * 8;
+    float v[8][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        unpack8(*reinterpret_cast<const uint4 *>(w + (r0 + 16 * i) * w_s0 + c0), v[i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+    amax = group_max<kWave>(amax);
+    if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kFp8Waves; ++k) amax = fmaxf(amax, wmax[k]);
+    const float s = pow2_ceil(fmaxf(amax, 1e-4f) / 448.0f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint2 *>(q + (r0 + 16 * i) * q_s0 + c0) = e4m3_pack8(v[i], s);
+    if (threadIdx.x == 0) scales[blockIdx.y * s_s0 + blockIdx.x] = s;
+}
+
+// Thread per 8 columns; the 16 threads of a 128-column group share its scale.
+__global__ void __launch_bounds__(kFp8Threads)
+quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, int K, uint8_t *__restrict__ q,
+                     int64_t q_s0, float *__restrict__ scales, int64_t s_s0) {
+    const int vecs = K / 8;
+    const int64_t total = static_cast<int64_t>(M) * vecs;
+    // whole 16-thread groups stay together: total and the stride are multiples of 16
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kFp8Threads + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * kFp8Threads) {
+        const int64_t row = i / vecs;
+        const int col = static_cast<int>(i - row * vecs) * 8;
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4 *>(x + row * x_s0 + col), v);
+        float amax = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+        const float s = row_group_scale(group_max<16>(amax));
+        *reinterpret_cast<uint2 *>(q + row * q_s0 + col) = e4m3_pack8(v, s);
+        if ((col & 127) == 0) scales[row * s_s0 + col / 128] = s;
+    }
+}
+
+typedef int int8v_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+// LDS pitch of the staged X slice in bytes: 16 bytes of padding put the 16
+// rows one B-operand read touches on distinct 4-bank groups.
+template <int KS>
+constexpr int fp8_pitch() {
+    return KS + 16;
+}
+
+// Lane (r16, kq) of a wave holds, for every 128-wide K block j of the slice,
+// bytes j*128 + kq*32 .. +31 of weight row n_row: the same K positions the
+// B operand takes from the staged X rows, so each MFMA sums matching products.
+template <int KS>
+__device__ __forceinline__ void fp8_load_w(int8v_t (&wr)[KS / 128], const uint8_t *__restrict__ w, int64_t w_s0,
+                                           int n_row, int k0, int kq) {
+    const uint8_t *row = w + static_cast<int64_t>(n_row) * w_s0 + k0 + kq * 32;
+#pragma unroll
+    for (int j = 0; j < KS / 128; ++j) wr[j] = *reinterpret_cast<const int8v_t *>(row + j * 128);
+}
+
+// One 16-column tile over the slice: per K block an MFMA from zero, scaled by
+// sx[row, kb] * sw[col / 128, kb] into the fp32 sum; then the store (the lane
+// holds Y[m*16 + r16][col + kq*4 + 0..3]).
+template <int MT, int KS>
+__device__ __forceinline__ void fp8_tile(const int8v_t (&wr)[KS / 128], const uint8_t *xs, const float *sxs,
+                                         const float (&swv)[KS / 128], int r16, int kq, int M, int N, int col,
+                                         int slice, uint16_t *__restrict__ out, int64_t o_s0, float *__restrict__ part) {
+    constexpr int kSteps = KS / 128;
+    floatx4_t acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+        const float swj = swv[j];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const uint8_t *bp = xs + (m * 16 + r16) * fp8_pitch<KS>() + j * 128 + kq * 32;
+            const int8v_t b = *reinterpret_cast<const int8v_t *>(bp);
+            const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+            const float s = sxs[(m * 16 + r16) * kSteps + j] * swj;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[m][e] = fmaf(t[e], s, acc[m][e]);
+        }
+        // one K block's B operands (8 VGPRs per row tile) live at a time: the
+        // instruction selector may otherwise sink every MFMA (they start from zero
+        // and touch no memory) below all LDS reads, so each block's sums are pinned
+        // here before the next block's reads
+#pragma unroll
+        for (int m = 0; m < MT; ++m) asm volatile("" : "+v"(acc[m]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    col += kq * 4;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int row = m * 16 + r16;
+        if (row >= M) continue;
+        if (part) {
+            float *p = part + (static_cast<int64_t>(slice) * M + row) * N + col;
+            *reinterpret_cast<float4 *>(p) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+        } else {
+            uint2 o;
+            o.x = pack2_bf16(acc[m][0], acc[m][1]);
+            o.y = pack2_bf16(acc[m][2], acc[m][3]);
+            *reinterpret_cast<uint2 *>(out + row * o_s0 + col) = o;
+        }
+    }
+}
+
+// Workgroup (bx, by): K slice by of KS bytes, 64-column band bx (wave w owns
+// columns bx*64 + w*16 .. + 15).  One band per workgroup: at KS = 1024 the
+// band's weights already fill 64 VGPRs per lane, and the talker's gate/up
+// shape gives 384 workgroups.
+template <int MT, int KS>
+__global__ void __launch_bounds__(kFp8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_fp8_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__restrict__ sx, int64_t sx_s0, int M,
+                const uint8_t *__restrict__ w, int64_t w_s0, const float *__restrict__ sw, int64_t sw_s0, int N,
+                uint16_t *__restrict__ out, int64_t o_s0, float *__restrict__ part) {
+    constexpr int kSteps = KS / 128;
+    constexpr int kRows = 16 * MT;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kRows * fp8_pitch<KS>()];
+    __shared__ float sxs[kRows * kSteps];  // activation scales of the slice's K blocks, per row
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int col = blockIdx.x * 64 + wave * 16;
+    const int k0 = blockIdx.y * KS;
+    const int kb0 = k0 / 128;
+
+    // 1. the band's weight scales (one per K block, wave-uniform), the X slice
+    // (rows >= M are zero) and the activation scales
+    float swv[kSteps];
+    const float *sw_row = sw + (col / 128) * sw_s0 + kb0;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) swv[j] = sw_row[j];
+    constexpr int kVecPerRow = KS / 16;
+    constexpr int kXVec = kRows * kVecPerRow / kFp8Threads;
+    static_assert(kRows * kVecPerRow % kFp8Threads == 0, "X block splits evenly over the threads");
+    uint4 xr[kXVec];
+#pragma unroll
+    for (int q = 0; q < kXVec; ++q) {
+        const int i = threadIdx.x + q * kFp8Threads;
+        const int row = i / kVecPerRow, c = i % kVecPerRow;
+        xr[q] = row < M ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + k0 + c * 16) : make_uint4(0, 0, 0, 0);
+    }
+    for (int i = threadIdx.x; i < kRows * kSteps; i += kFp8Threads) {
+        const int row = i / kSteps, j = i % kSteps;
+        sxs[i] = row < M ? sx[row * sx_s0 + kb0 + j] : 0.f;
+    }
+
+    // 2. the band's weights, all in flight together
+    int8v_t wa[kSteps];
+    fp8_load_w<KS>(wa, w, w_s0, col + r16, k0, kq);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int q = 0; q < kXVec; ++q) {
+        const int i = threadIdx.x + q * kFp8Threads;
+        const int row = i / kVecPerRow, c = i % kVecPerRow;
+        *reinterpret_cast<uint4 *>(xs + row * fp8_pitch<KS>() + c * 16) = xr[q];
+    }
+    __syncthreads();
+
+    fp8_tile<MT, KS>(wa, xs, sxs, swv, r16, kq, M, N, col, blockIdx.y, out, o_s0, part);
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up with the SwiGLU fused, for <= 64 rows and K = 2048 (the talker's
+// MLP).  The FP8 activation block [64, K] is 128 KiB, so one workgroup per CU
+// stages all of it in LDS and computes whole dot products: no split-K planes
+// and no second kernel.  The gate/up weight rows are held interleaved
+// (nq_fp8_pack_swiglu): 16-row tile t holds, for q = 0..3, gate rows
+// 8t + 2q, 8t + 2q + 1 then up rows 8t + 2q, 8t + 2q + 1, so MFMA lane group q
+// ends with two gate/up pairs of the same act columns 8t + 2q + {0, 1}.  The
+// workgroup owns kSwTiles tiles; its kSwTiles * kSwQuarters waves each take
+// one tile over one quarter of K (twelve waves keep three per SIMD to hide
+// the load and MFMA latencies), and the quarters are summed in order through
+// LDS before the epilogue rounds gate and up to bf16 and stores
+// bf16(silu(g) * u).
+
+constexpr int kSwTiles = 3;
+constexpr int kSwQuarters = 4;
+constexpr int kSwThreads = kSwTiles * kSwQuarters * kWave;
+constexpr int kSwK = 2048;
+constexpr int kSwRows = 64;
+
+template <int K>
+__global__ void __launch_bounds__(kSwThreads)
+fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__restrict__ sx, int64_t sx_s0, int M,
+                  const uint8_t *__restrict__ w, int64_t w_s0, const float *__restrict__ sw, int64_t sw_s0, int I,
+                  uint16_t *__restrict__ out, int64_t o_s0) {
+    constexpr int KB = K / 128;                    // K blocks
+    constexpr int QS = K / kSwQuarters / 128;      // K blocks per quarter
+    constexpr int P = K + 16;                      // LDS pitch of an X row in bytes
+    __shared__ __attribute__((aligned(16))) uint8_t xs[kSwRows * P];
+    __shared__ float sxs[kSwRows * KB];
+    static_assert((kSwQuarters - 1) * kSwTiles * kWave * 16 * 4 <= kSwRows * P, "reduction fits the X area");
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int tl = wave % kSwTiles;
+    const int quarter = wave / kSwTiles;
+    const int tile = blockIdx.x * kSwTiles + tl;
+    const int kb0 = quarter * QS;
+
+    // 1. the wave's weights (16 packed rows over its K quarter) and scales:
+    // gate rows 8t.. lie in 128-row block t / 16, up rows in (I + 8t) / 128
+    int8v_t wr[QS];
+    {
+        const uint8_t *row = w + static_cast<int64_t>(tile * 16 + r16) * w_s0 + kb0 * 128 + kq * 32;
+#pragma unroll
+        for (int j = 0; j < QS; ++j) wr[j] = *reinterpret_cast<const int8v_t *>(row + j * 128);
+    }
+    float swg[QS], swu[QS];
+    {
+        const float *g = sw + static_cast<int64_t>(tile * 8 / 128) * sw_s0 + kb0;
+        const float *u = sw + static_cast<int64_t>((I + tile * 8) / 128) * sw_s0 + kb0;
+#pragma unroll
+        for (int j = 0; j < QS; ++j) {
+            swg[j] = g[j];
+            swu[j] = u[j];
+        }
+    }
+    // 2. the activation block and its scales into LDS (rows >= M zero): every
+    // load of the thread is issued before the first LDS store
+    constexpr int kVec = kSwRows * (K / 16);
+    constexpr int kPer = (kVec + kSwThreads - 1) / kSwThreads;
+    constexpr int kSx = kSwRows * KB;
+    constexpr int kSxPer = (kSx + kSwThreads - 1) / kSwThreads;
+    {
+        uint4 xr[kPer];
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = threadIdx.x + u * kSwThreads;
+            const int row = i / (K / 16), c = i % (K / 16);
+            xr[u] = (i < kVec && row < M) ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + c * 16)
+                                          : make_uint4(0, 0, 0, 0);
+        }
+        float sr[kSxPer];
+#pragma unroll
+        for (int u = 0; u < kSxPer; ++u) {
+            const int i = threadIdx.x + u * kSwThreads;
+            sr[u] = (i < kSx && i / KB < M) ? sx[(i / KB) * sx_s0 + i % KB] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = threadIdx.x + u * kSwThreads;
+            if (i < kVec) *reinterpret_cast<uint4 *>(xs + (i / (K / 16)) * P + (i % (K / 16)) * 16) = xr[u];
+        }
+#pragma unroll
+        for (int u = 0; u < kSxPer; ++u) {
+            const int i = threadIdx.x + u * kSwThreads;
+            if (i < kSx) sxs[i] = sr[u];
+        }
+    }
+    __syncthreads();
+
+    // 3. the quarter's MFMAs, scaled per K block: lane columns 0, 1 are gate, 2, 3 up
+    floatx4_t acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < QS; ++j) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = m * 16 + r16;
+            const int8v_t b = *reinterpret_cast<const int8v_t *>(xs + row * P + (kb0 + j) * 128 + kq * 32);
+            const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+            const float sxv = sxs[row * KB + kb0 + j];
+            const float sg = sxv * swg[j], su = sxv * swu[j];
+            acc[m][0] = fmaf(t[0], sg, acc[m][0]);
+            acc[m][1] = fmaf(t[1], sg, acc[m][1]);
+            acc[m][2] = fmaf(t[2], su, acc[m][2]);
+            acc[m][3] = fmaf(t[3], su, acc[m][3]);
+        }
+        // pin the block's sums here: the MFMAs (which start from zero and touch no
+        // memory) may otherwise sink below every later LDS read
+#pragma unroll
+        for (int m = 0; m < 4; ++m) asm volatile("" : "+v"(acc[m]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 4. quarters 1.. hand their sums to quarter 0 through the (now free) X area
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(xs);
+    if (quarter > 0) {
+        float *dst = red + (((quarter - 1) * kSwTiles + tl) * kWave + lane) * 16;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            *reinterpret_cast<float4 *>(dst + m * 4) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    }
+    __syncthreads();
+    if (quarter != 0) return;
+#pragma unroll
+    for (int q = 1; q < kSwQuarters; ++q) {
+        const float *src = red + (((q - 1) * kSwTiles + tl) * kWave + lane) * 16;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + m * 4);
+            acc[m][0] += v.x;
+            acc[m][1] += v.y;
+            acc[m][2] += v.z;
+            acc[m][3] += v.w;
+        }
+    }
+    // 5. SwiGLU of the bf16 projection values: act columns 8t + 2kq + {0, 1}
+    const int col = tile * 8 + kq * 2;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int row = m * 16 + r16;
+        if (row >= M) continue;
+        float a[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float g = bf16_to_f32(f32_to_bf16(acc[m][e]));
+            const float u = bf16_to_f32(f32_to_bf16(acc[m][2 + e]));
+            a[e] = g / (1.0f + expf(-g)) * u;
+        }
+        *reinterpret_cast<uint32_t *>(out + row * o_s0 + col) = pack2_bf16(a[0], a[1]);
+    }
+}
+
+// Packed row p = 16 t + 4 q + e of the interleaved gate/up matrix is gate row
+// 8t + 2q + e (e < 2) or up row 8t + 2q + e - 2 (e >= 2) of the [gate; up] one.
+__global__ void __launch_bounds__(256)
+pack_swiglu_kernel(const uint8_t *__restrict__ q, int64_t q_s0, int I, int K, uint8_t *__restrict__ packed,
+                   int64_t p_s0) {
+    const int p = blockIdx.x;
+    const int t = p / 16, qq = (p % 16) / 4, e = p % 4;
+    const int src = e < 2 ? 8 * t + 2 * qq + e : I + 8 * t + 2 * qq + e - 2;
+    for (int c = threadIdx.x * 16; c < K; c += 256 * 16)
+        *reinterpret_cast<uint4 *>(packed + static_cast<int64_t>(p) * p_s0 + c) =
+            *reinterpret_cast<const uint4 *>(q + static_cast<int64_t>(src) * q_s0 + c);
+}
+
+constexpr int kFp8Slice = 1024;  // K bytes per workgroup slice (M <= 64)
+
+int fp8_slice_of(int M) { return M > 64 ? 512 : kFp8Slice; }
+
+template <int MT, int KS>
+void launch_fp8(const uint8_t *x, int64_t x_s0, const float *sx, int64_t sx_s0, int M, const uint8_t *w,
+                int64_t w_s0, const float *sw, int64_t sw_s0, int N, int K, uint16_t *out, int64_t o_s0,
+                float *part, hipStream_t st) {
+    dim3 grid(N / 64, K / KS);
+    hipLaunchKernelGGL((gemm_fp8_kernel<MT, KS>), grid, dim3(kFp8Threads), 0, st, x, x_s0, sx, sx_s0, M, w, w_s0,
+                       sw, sw_s0, N, out, o_s0, part);
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" int nq_quantize_fp8_blocks(const uint16_t *w, int64_t w_s0, int N, int K, uint8_t *q, int64_t q_s0,
+                                      float *scales, int64_t s_s0, void *stream) {
+    NQ_CHECK_ARG(w && q && scales && N >= 0 && K >= 0);
+    NQ_CHECK_ARG(N % 128 == 0 && K % 128 == 0);
+    NQ_CHECK_ARG(w_s0 >= K && q_s0 >= K && s_s0 >= K / 128 && w_s0 % 8 == 0 && q_s0 % 8 == 0);
+    NQ_CHECK_ARG(al16(w) && reinterpret_cast<uintptr_t>(q) % 8 == 0);
+    if (N == 0 || K == 0) return NQ_OK;
+    hipLaunchKernelGGL(quantize_blocks_kernel, dim3(K / 128, N / 128), dim3(kFp8Threads), 0,
+                       static_cast<hipStream_t>(stream), w, w_s0, q, q_s0, scales, s_s0);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_quantize_fp8_rows(const uint16_t *x, int64_t x_s0, int M, int K, uint8_t *q, int64_t q_s0,
+                                    float *scales, int64_t s_s0, void *stream) {
+    NQ_CHECK_ARG(x && q && scales && M >= 0 && K >= 0 && K % 128 == 0);
+    NQ_CHECK_ARG(x_s0 >= K && q_s0 >= K && s_s0 >= K / 128 && x_s0 % 8 == 0 && q_s0 % 8 == 0);
+    NQ_CHECK_ARG(al16(x) && reinterpret_cast<uintptr_t>(q) % 8 == 0);
+    if (M == 0 || K == 0) return NQ_OK;
+    const int64_t total = static_cast<int64_t>(M) * (K / 8);
+    const int64_t blocks = (total + kFp8Threads - 1) / kFp8Threads;
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3(static_cast<unsigned>(blocks > 4096 ? 4096 : blocks)),
+                       dim3(kFp8Threads), 0, static_cast<hipStream_t>(stream), x, x_s0, M, K, q, q_s0, scales, s_s0);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_linear_fp8_splits(int M, int N, int K) {
+    if (M <= 0 || M > 128 || N <= 0 || N % 128 != 0 || K <= 0 || K % fp8_slice_of(M) != 0) return -1;
+    return K / fp8_slice_of(M);
+}
+
+extern "C" int64_t nq_linear_fp8_workspace_bytes(int M, int N, int K, int epilogue) {
+    const int S = nq_linear_fp8_splits(M, N, K);
+    if (S < 0 || (epilogue != NQ_EPI_NONE && epilogue != NQ_EPI_SILU_MUL && epilogue != NQ_EPI_PARTIALS)) return -1;
+    if (S == 1 && epilogue == NQ_EPI_NONE) return 0;
+    return static_cast<int64_t>(S) * M * N * 4;
+}
+
+extern "C" int nq_linear_fp8(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, const uint8_t *wq,
+                             int64_t w_s0, const float *sw, int64_t sw_s0, int M, int N, int K, int epilogue,
+                             uint16_t *out, int64_t o_s0, void *workspace, int64_t workspace_bytes, void *stream) {
+    NQ_CHECK_ARG(xq && sx && wq && sw && M > 0 && N > 0 && K > 0);
+    NQ_CHECK_ARG(epilogue == NQ_EPI_NONE || epilogue == NQ_EPI_SILU_MUL || epilogue == NQ_EPI_PARTIALS);
+    const int S = nq_linear_fp8_splits(M, N, K);
+    if (S < 0) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 16 == 0 && w_s0 % 16 == 0 && al16(xq) && al16(wq));
+    NQ_CHECK_ARG(sx_s0 >= K / 128 && sw_s0 >= K / 128);
+    const int out_width = epilogue == NQ_EPI_SILU_MUL ? N / 2 : N;
+    if (epilogue != NQ_EPI_PARTIALS) NQ_CHECK_ARG(out && o_s0 >= out_width && o_s0 % 8 == 0 && al16(out));
+    const int64_t need = nq_linear_fp8_workspace_bytes(M, N, K, epilogue);
+    NQ_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && al16(workspace)));
+    float *part = need ? static_cast<float *>(workspace) : nullptr;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    switch (mt) {
+        case 1: launch_fp8<1, kFp8Slice>(xq, x_s0, sx, sx_s0, M, wq, w_s0, sw, sw_s0, N, K, out, o_s0, part, st); break;
+        case 2: launch_fp8<2, kFp8Slice>(xq, x_s0, sx, sx_s0, M, wq, w_s0, sw, sw_s0, N, K, out, o_s0, part, st); break;
+        case 4: launch_fp8<4, kFp8Slice>(xq, x_s0, sx, sx_s0, M, wq, w_s0, sw, sw_s0, N, K, out, o_s0, part, st); break;
+        default: launch_fp8<8, 512>(xq, x_s0, sx, sx_s0, M, wq, w_s0, sw, sw_s0, N, K, out, o_s0, part, st); break;
+    }
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    switch (epilogue) {
+        case NQ_EPI_NONE:
+            return S > 1 ? launch_reduce_partials(part, S, M, N, out, o_s0, nullptr, st) : NQ_OK;
+        case NQ_EPI_SILU_MUL:
+            return launch_silu_mul_partials(part, S, M, N / 2, out, o_s0, st);
+        default:
+            return NQ_OK;
+    }
+}
+
+extern "C" int nq_fp8_pack_swiglu(const uint8_t *q, int64_t q_s0, int I, int K, uint8_t *packed, int64_t p_s0,
+                                  void *stream) {
+    NQ_CHECK_ARG(q && packed && I > 0 && K > 0 && I % 8 == 0 && K % 16 == 0);
+    NQ_CHECK_ARG(q_s0 >= K && p_s0 >= K && q_s0 % 16 == 0 && p_s0 % 16 == 0 && al16(q) && al16(packed));
+    NQ_CHECK_ARG(q != packed);
+    hipLaunchKernelGGL(pack_swiglu_kernel, dim3(2 * I), dim3(256), 0, static_cast<hipStream_t>(stream), q, q_s0, I,
+                       K, packed, p_s0);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_linear_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, int M,
+                                    const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
+                                    uint16_t *out, int64_t o_s0, void *stream) {
+    NQ_CHECK_ARG(xq && sx && packed && sw && out && M > 0 && I > 0 && K > 0);
+    if (M > kSwRows || K != kSwK || I % (8 * kSwTiles) != 0 || I % 128 != 0) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 16 == 0 && w_s0 % 16 == 0 && al16(xq) && al16(packed));
+    NQ_CHECK_ARG(sx_s0 >= K / 128 && sw_s0 >= K / 128 && o_s0 >= I && o_s0 % 2 == 0);
+    NQ_CHECK_ARG(reinterpret_cast<uintptr_t>(out) % 4 == 0);
+    hipLaunchKernelGGL((fp8_swiglu_kernel<kSwK>), dim3(I / (8 * kSwTiles)), dim3(kSwThreads), 0,
+                       static_cast<hipStream_t>(stream), xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, out, o_s0);
+    return NQ_LAUNCH_STATUS();
+}

@@ -181,17 +181,6 @@ gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t
 // fp32 partial plane.
 int slice_of(int M) { return M > 64 ? 256 : 512; }
 
-// Bands per workgroup: the largest divisor of the band count that still
-// leaves at least one workgroup per CU; more bands per workgroup share one
-// staged X slice.
-int bands_per_wg(int bands, int splits) {
-    constexpr int kTargetWgs = 256;
-    int best = 1;
-    for (int nb = 2; nb <= 8; ++nb)
-        if (bands % nb == 0 && (bands / nb) * splits >= kTargetWgs) best = nb;
-    return best;
-}
-
 template <int MT, int KS>
 void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
                  uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
@@ -203,6 +192,27 @@ void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int6
 }
 
 }  // namespace
+
+// Bands per workgroup: the largest divisor of the band count that still
+// leaves at least one workgroup per CU; more bands per workgroup share one
+// staged X slice.
+int bands_per_wg(int bands, int splits) {
+    constexpr int kTargetWgs = 256;
+    int best = 1;
+    for (int nb = 2; nb <= 8; ++nb)
+        if (bands % nb == 0 && (bands / nb) * splits >= kTargetWgs) best = nb;
+    return best;
+}
+
+int launch_reduce_partials(const float *part, int S, int M, int N, uint16_t *out, int64_t o_s0,
+                           const uint16_t *bias, hipStream_t st) {
+    const int64_t vec = static_cast<int64_t>(M) * N / 8;
+    int blocks = static_cast<int>((vec + kGemmThreads - 1) / kGemmThreads);
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(blocks > 2048 ? 2048 : blocks), dim3(kGemmThreads), 0, st, part, S,
+                       M, N, out, o_s0, bias);
+    return NQ_LAUNCH_STATUS();
+}
+
 }  // namespace nq
 
 using namespace nq;
@@ -255,13 +265,7 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     switch (epilogue) {
         case NQ_EPI_NONE:
-            if (S > 1) {
-                const int64_t vec = static_cast<int64_t>(M) * N / 8;
-                int blocks = static_cast<int>((vec + kGemmThreads - 1) / kGemmThreads);
-                hipLaunchKernelGGL(gemm_reduce_kernel, dim3(blocks > 2048 ? 2048 : blocks), dim3(kGemmThreads), 0,
-                                   st, part, S, M, N, out, o_s0, bias);
-            }
-            return NQ_LAUNCH_STATUS();
+            return S > 1 ? launch_reduce_partials(part, S, M, N, out, o_s0, bias, st) : NQ_LAUNCH_STATUS();
         case NQ_EPI_ADD_RMSNORM:
             return launch_add_rmsnorm_partials(part, S, M, N, out, o_s0, residual, norm_weight, eps, st);
         case NQ_EPI_SILU_MUL:
@@ -269,4 +273,30 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
         default:
             return NQ_OK;  // partials stay in the workspace for the caller's consumer
     }
+}
+
+extern "C" int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M,
+                                         int N, int K, uint16_t *residual, const uint16_t *norm_weight, float eps,
+                                         uint8_t *xq, int64_t xq_s0, float *sx, int64_t sx_s0, void *workspace,
+                                         int64_t workspace_bytes, void *stream) {
+    NQ_CHECK_ARG(x && w && residual && norm_weight && xq && sx && M > 0 && N > 0 && K > 0);
+    const int S = nq_linear_splits(M, N, K);
+    if (S < 0 || N % 128 != 0 || N > 8192) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 8 == 0 && w_s0 % 8 == 0);
+    NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0);
+    NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(norm_weight)) % 16 == 0);
+    NQ_CHECK_ARG(xq_s0 >= N && xq_s0 % 8 == 0 && reinterpret_cast<uintptr_t>(xq) % 8 == 0 && sx_s0 >= N / 128);
+    const int64_t need = nq_linear_workspace_bytes(M, N, K, NQ_EPI_ADD_RMSNORM);
+    NQ_CHECK_ARG(workspace && workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 16 == 0);
+    float *part = static_cast<float *>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    switch (mt) {
+        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
+        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
+        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
+        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
+    }
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    return launch_add_rmsnorm_partials_fp8(part, S, M, N, residual, norm_weight, eps, xq, xq_s0, sx, sx_s0, st);
 }

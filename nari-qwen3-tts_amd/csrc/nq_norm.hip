@@ -2,7 +2,10 @@
 // talker decode step (model/layers.py:28-115), bf16 in and out, fp32 math.
 // One workgroup per row; each thread keeps its 8-element slices in registers
 // between the sum-of-squares reduction and the scaled store, so a row is read
-// and written exactly once.
+// and written exactly once.  The add-RMSNorm that feeds the FP8 gate/up
+// projection can instead store its bf16 result quantized to e4m3fn codes with
+// one scale per 128 columns (max |y| / 448), the activation quantization of the
+// block-scaled FP8 GEMM, so that GEMM reads one byte per activation.
 #include "nq_common.h"
 #include "nq_internal.h"
 
@@ -47,11 +50,20 @@ struct PartialSrc {
     }
 };
 
-template <typename Src>
+// Quantized output of the normalised row: codes [rows, width] and scales
+// [rows, width / 128].
+struct Fp8Out {
+    uint8_t *q;
+    int64_t q_s0;
+    float *s;
+    int64_t s_s0;
+};
+
+template <typename Src, bool kFp8>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
                    uint16_t *__restrict__ residual, const uint16_t *__restrict__ weight, int width,
-                   float eps) {
+                   float eps, Fp8Out fp8) {
     __shared__ float tmp[kNormThreads / kWave];
     const int64_t row = blockIdx.x;
     const int nvec = width / 8;
@@ -87,12 +99,26 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
     for (int i = 0; i < kMaxVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
-            uint4 packed;
-            uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+            if constexpr (kFp8) {
+                // the 16 threads of a 128-column group are consecutive and all inside the row
+                float y[8];
+                float amax = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e += 2)
-                pw[e / 2] = pack2_bf16(x[i][e] * inv * w[i][e], x[i][e + 1] * inv * w[i][e + 1]);
-            *reinterpret_cast<uint4 *>(hidden_out + row * ho_s0 + vi * 8) = packed;
+                for (int e = 0; e < 8; ++e) {
+                    y[e] = bf16_to_f32(f32_to_bf16(x[i][e] * inv * w[i][e]));
+                    amax = fmaxf(amax, fabsf(y[e]));
+                }
+                const float sc = row_group_scale(group_max<16>(amax));
+                *reinterpret_cast<uint2 *>(fp8.q + row * fp8.q_s0 + vi * 8) = e4m3_pack8(y, sc);
+                if ((vi & 15) == 0) fp8.s[row * fp8.s_s0 + vi / 16] = sc;
+            } else {
+                uint4 packed;
+                uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
+#pragma unroll
+                for (int e = 0; e < 8; e += 2)
+                    pw[e / 2] = pack2_bf16(x[i][e] * inv * w[i][e], x[i][e + 1] * inv * w[i][e + 1]);
+                *reinterpret_cast<uint4 *>(hidden_out + row * ho_s0 + vi * 8) = packed;
+            }
         }
     }
 }
@@ -170,8 +196,18 @@ int launch_add_rmsnorm_partials(const float *part, int S, int rows, int width, u
                                 hipStream_t st) {
     if (width % 8 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
     const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
-    hipLaunchKernelGGL(add_rmsnorm_kernel<PartialSrc>, dim3(rows), dim3(kNormThreads), 0, st, src, hidden_out,
-                       ho_s0, residual, weight, width, eps);
+    hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, false>), dim3(rows), dim3(kNormThreads), 0, st, src,
+                       hidden_out, ho_s0, residual, weight, width, eps, Fp8Out{});
+    return NQ_LAUNCH_STATUS();
+}
+
+int launch_add_rmsnorm_partials_fp8(const float *part, int S, int rows, int width, uint16_t *residual,
+                                    const uint16_t *weight, float eps, uint8_t *xq, int64_t xq_s0, float *sx,
+                                    int64_t sx_s0, hipStream_t st) {
+    if (width % 128 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
+    const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
+    hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, true>), dim3(rows), dim3(kNormThreads), 0, st, src, nullptr,
+                       0, residual, weight, width, eps, Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -192,9 +228,25 @@ extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16
     if (!nq::al16(hidden) || !nq::al16(residual) || !nq::al16(weight)) return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     const nq::Bf16Src src{hidden, width};
-    hipLaunchKernelGGL(nq::add_rmsnorm_kernel<nq::Bf16Src>, dim3(rows), dim3(nq::kNormThreads), 0,
+    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, false>), dim3(rows), dim3(nq::kNormThreads), 0,
                        static_cast<hipStream_t>(stream), src, hidden, static_cast<int64_t>(width), residual,
-                       weight, width, eps);
+                       weight, width, eps, nq::Fp8Out{});
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_add_rmsnorm_fp8(const uint16_t *hidden, uint16_t *residual, const uint16_t *weight, int rows,
+                                  int width, float eps, uint8_t *xq, int64_t xq_s0, float *sx, int64_t sx_s0,
+                                  void *stream) {
+    NQ_CHECK_ARG(hidden && residual && weight && xq && sx && rows >= 0 && width >= 128);
+    if (width % 128 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(xq_s0 >= width && xq_s0 % 8 == 0 && sx_s0 >= width / 128);
+    if (!nq::al16(hidden) || !nq::al16(residual) || !nq::al16(weight) || reinterpret_cast<uintptr_t>(xq) % 8)
+        return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    const nq::Bf16Src src{hidden, width};
+    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, true>), dim3(rows), dim3(nq::kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), src, nullptr, 0, residual, weight, width, eps,
+                       nq::Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 

@@ -5,6 +5,12 @@ mirror model/layers.py:28-100: the fused add-norm updates both inputs in
 place (residual <- residual + hidden, hidden <- rmsnorm(residual)).
 ``linear`` is the bias-free nn.Linear of model/layers.py:195-270 for decode
 row counts (<= 128), computed by the skinny HIP GEMM.
+
+FP8 gate/up (model/layers.py:10-25, 195-262): ``quantize_fp8_weight_blocks``
+keeps the reference's name, block layout and errors; the activations are
+quantized per row and 128 columns by the add-RMSNorm that produces them
+(``add_rmsnorm_fp8`` / ``linear_add_rmsnorm_fp8``) or by
+``quantize_fp8_rows``, and ``linear_fp8`` runs the block-scaled product.
 """
 
 from __future__ import annotations
@@ -152,12 +158,198 @@ def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | N
     return _linear(x, weight, _lib.NQ_EPI_SILU_MUL, out, weight.shape[0] // 2, workspace=workspace)
 
 
+FP8 = torch.float8_e4m3fn
+
+
+def quantize_fp8_weight_blocks(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize a row-major bf16 gate/up matrix into 128 x 128 FP8 blocks (model/layers.py:10-25):
+    returns (e4m3fn codes with the weight's shape, fp32 power-of-two scales [rows/128, cols/128])."""
+
+    if weight.ndim != 2 or not weight.is_contiguous():
+        raise ValueError("FP8 block quantization requires a contiguous matrix")
+    rows, columns = weight.shape
+    if rows % 128 or columns % 128:
+        raise ValueError(
+            f"FP8 block quantization requires dimensions divisible by 128, got {tuple(weight.shape)}"
+        )
+    _check(weight, "weight")
+    q = torch.empty((rows, columns), dtype=FP8, device=weight.device)
+    scales = torch.empty((rows // 128, columns // 128), dtype=torch.float32, device=weight.device)
+    _lib.call("nq_quantize_fp8_blocks", weight.data_ptr(), weight.stride(0), rows, columns, q.data_ptr(),
+              q.stride(0), scales.data_ptr(), scales.stride(0), _lib.stream(weight.device))
+    return q, scales
+
+
+def _fp8_out(rows: int, width: int, device, q: torch.Tensor | None, scales: torch.Tensor | None):
+    q = torch.empty((rows, width), dtype=FP8, device=device) if q is None else q
+    scales = torch.empty((rows, width // 128), dtype=torch.float32, device=device) if scales is None else scales
+    if q.dtype != FP8 or q.shape != (rows, width) or q.stride(1) != 1:
+        raise ValueError(f"FP8 codes must be float8_e4m3fn [{rows}, {width}] with unit inner stride")
+    if scales.dtype != torch.float32 or scales.shape != (rows, width // 128) or scales.stride(1) != 1:
+        raise ValueError(f"FP8 scales must be fp32 [{rows}, {width // 128}]")
+    _lib.require_device(q, scales)
+    return q, scales
+
+
+def quantize_fp8_rows(x: torch.Tensor, q: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """bf16 [rows, K] -> (e4m3fn codes, fp32 scales [rows, K/128]): scale = max|x| / 448 per 128 columns."""
+
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
+        raise TypeError("row quantization needs bf16 [rows, K] with unit inner stride")
+    rows, k = x.shape
+    if k % 128:
+        raise ValueError("row quantization needs a multiple of 128 columns")
+    _lib.require_device(x)
+    q, scales = _fp8_out(rows, k, x.device, q, scales)
+    _lib.call("nq_quantize_fp8_rows", x.data_ptr(), x.stride(0), rows, k, q.data_ptr(), q.stride(0),
+              scales.data_ptr(), scales.stride(0), _lib.stream(x.device))
+    return q, scales
+
+
+def add_rmsnorm_fp8(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                    q: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """residual += hidden; the rmsnorm of residual is returned quantized as (codes, scales)."""
+
+    _check(hidden, "hidden_states")
+    _check(residual, "residual")
+    _check(weight, "norm weight")
+    if hidden.shape != residual.shape or hidden.dim() != 2:
+        raise ValueError("fused add-RMSNorm needs 2-D tensors of one shape")
+    rows, width = hidden.shape
+    if weight.shape != (width,):
+        raise ValueError("norm weight must match the hidden width")
+    q, scales = _fp8_out(rows, width, hidden.device, q, scales)
+    _lib.call("nq_add_rmsnorm_fp8", hidden.data_ptr(), residual.data_ptr(), weight.data_ptr(), rows, width,
+              float(eps), q.data_ptr(), q.stride(0), scales.data_ptr(), scales.stride(0), _lib.stream(hidden.device))
+    return q, scales
+
+
+def linear_add_rmsnorm_fp8(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
+                           eps: float, q: torch.Tensor, scales: torch.Tensor, workspace: torch.Tensor | None = None):
+    """linear_add_rmsnorm with the normalised output stored quantized in (q, scales)."""
+
+    for t, name in ((residual, "residual"), (norm_weight, "norm weight")):
+        _check(t, name)
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 or weight.stride(1) != 1:
+        raise TypeError("linear needs bf16 tensors with unit inner stride")
+    rows, k = x.shape
+    n = weight.shape[0]
+    if residual.shape != (rows, n) or norm_weight.shape != (n,):
+        raise ValueError("residual / norm weight must match the projection output")
+    q, scales = _fp8_out(rows, n, x.device, q, scales)
+    need = linear_workspace_bytes(rows, n, k, _lib.NQ_EPI_ADD_RMSNORM)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.require_device(x, weight, workspace)
+    _lib.call("nq_linear_add_rmsnorm_fp8", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n,
+              k, residual.data_ptr(), norm_weight.data_ptr(), float(eps), q.data_ptr(), q.stride(0),
+              scales.data_ptr(), scales.stride(0), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+              _lib.stream(x.device))
+    return q, scales
+
+
+def linear_fp8_workspace_bytes(rows: int, out_features: int, in_features: int,
+                               epilogue: int = _lib.NQ_EPI_NONE) -> int:
+    """fp32 split-K scratch of the FP8 projection for up to 128 rows (0 when none)."""
+
+    n = int(_lib.load().nq_linear_fp8_workspace_bytes(int(min(rows, 128)), int(out_features), int(in_features),
+                                                      int(epilogue)))
+    if n < 0:
+        raise TypeError(f"no FP8 projection for rows={rows}, out={out_features}, in={in_features}")
+    return n
+
+
+def linear_fp8(q: torch.Tensor, scales: torch.Tensor, weight_q: torch.Tensor, weight_scales: torch.Tensor,
+               epilogue: int = _lib.NQ_EPI_NONE, out: torch.Tensor | None = None,
+               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Block-scaled FP8 projection y = dequant(q) @ dequant(weight_q).T in fp32, bf16 out
+    (NQ_EPI_NONE) or silu(y[:, :N/2]) * y[:, N/2:] (NQ_EPI_SILU_MUL).  Rows beyond 128 run in
+    128-row pieces."""
+
+    if q.dtype != FP8 or weight_q.dtype != FP8:
+        raise TypeError("FP8 projection needs float8_e4m3fn codes")
+    if epilogue not in (_lib.NQ_EPI_NONE, _lib.NQ_EPI_SILU_MUL):
+        raise ValueError("FP8 projection epilogue must be NONE or SILU_MUL")
+    rows, k = q.shape
+    n = weight_q.shape[0]
+    if weight_q.shape[1] != k or scales.shape != (rows, k // 128) or weight_scales.shape != (n // 128, k // 128):
+        raise ValueError("FP8 codes and scales do not match")
+    for t in (scales, weight_scales):
+        if t.dtype != torch.float32 or t.stride(1) != 1:
+            raise TypeError("FP8 scales must be fp32 with unit inner stride")
+    _lib.require_device(q, scales, weight_q, weight_scales)
+    width = n // 2 if epilogue == _lib.NQ_EPI_SILU_MUL else n
+    out = torch.empty((rows, width), dtype=torch.bfloat16, device=q.device) if out is None else out
+    if out.shape != (rows, width) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError(f"out must be bf16 [{rows}, {width}] with unit inner stride")
+    need = linear_fp8_workspace_bytes(rows, n, k, epilogue)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    for r0 in range(0, rows, 128):
+        m = min(128, rows - r0)
+        _lib.call("nq_linear_fp8", q[r0:].data_ptr(), q.stride(0), scales[r0:].data_ptr(), scales.stride(0),
+                  weight_q.data_ptr(), weight_q.stride(0), weight_scales.data_ptr(), weight_scales.stride(0), m, n, k,
+                  int(epilogue), out[r0:].data_ptr(), out.stride(0), _lib.ptr(workspace) if need else None,
+                  workspace.numel() * workspace.element_size() if need else 0, _lib.stream(q.device))
+    return out
+
+
+def pack_fp8_swiglu(weight_q: torch.Tensor) -> torch.Tensor:
+    """Interleave the rows of FP8 [gate; up] codes [2I, K] for linear_fp8_swiglu (the block
+    scales stay those of the original layout)."""
+
+    if weight_q.dtype != FP8 or weight_q.dim() != 2 or weight_q.shape[0] % 16 or weight_q.stride(1) != 1:
+        raise ValueError("FP8 gate/up codes [2I, K] with I % 8 == 0 expected")
+    _lib.require_device(weight_q)
+    packed = torch.empty_like(weight_q)
+    _lib.call("nq_fp8_pack_swiglu", weight_q.data_ptr(), weight_q.stride(0), weight_q.shape[0] // 2,
+              weight_q.shape[1], packed.data_ptr(), packed.stride(0), _lib.stream(weight_q.device))
+    return packed
+
+
+def linear_fp8_swiglu(q: torch.Tensor, scales: torch.Tensor, packed: torch.Tensor, weight_scales: torch.Tensor,
+                      out: torch.Tensor, weight_q: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of the FP8 gate/up projection in one kernel where the shape allows it
+    (<= 64 rows, K = 2048), else through linear_fp8 on the unpacked codes ``weight_q``."""
+
+    rows, k = q.shape
+    inter = packed.shape[0] // 2
+    if out.shape != (rows, inter) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be bf16 [{rows}, {inter}] with unit inner stride")
+    if q.dtype != FP8 or packed.dtype != FP8 or packed.shape[1] != k:
+        raise TypeError("FP8 codes expected")
+    if scales.shape != (rows, k // 128) or weight_scales.shape != (2 * inter // 128, k // 128):
+        raise ValueError("FP8 scales do not match")
+    _lib.require_device(q, scales, packed, weight_scales, out)
+    rc = _lib.load().nq_linear_fp8_swiglu(q.data_ptr(), q.stride(0), scales.data_ptr(), scales.stride(0), rows,
+                                          packed.data_ptr(), packed.stride(0), weight_scales.data_ptr(),
+                                          weight_scales.stride(0), inter, k, out.data_ptr(), out.stride(0),
+                                          _lib.stream(q.device))
+    if rc == _lib.NQ_ERR_UNSUPPORTED:
+        if weight_q is None:
+            raise TypeError("shape not covered by the fused FP8 SwiGLU and no unpacked codes given")
+        return linear_fp8(q, scales, weight_q, weight_scales, epilogue=_lib.NQ_EPI_SILU_MUL, out=out,
+                          workspace=workspace)
+    _lib.check(rc, "nq_linear_fp8_swiglu")
+    return out
+
+
 __all__ = [
+    "FP8",
+    "linear_fp8_swiglu",
+    "pack_fp8_swiglu",
+    "add_rmsnorm_fp8",
     "linear",
     "linear_add_rmsnorm",
+    "linear_add_rmsnorm_fp8",
+    "linear_fp8",
+    "linear_fp8_workspace_bytes",
     "linear_partials",
     "linear_silu_mul",
     "linear_workspace_bytes",
+    "quantize_fp8_rows",
+    "quantize_fp8_weight_blocks",
     "qwen3_tts_add_rmsnorm",
     "qwen3_tts_rmsnorm",
     "qwen3_tts_silu_and_mul",

@@ -11,8 +11,13 @@ seen mask, temperature, top-k, top-p, draw) with the seen-mask update.
 The projections run on the HIP library's skinny GEMM with the following
 kernel fused in (o_proj and down with the residual add-RMSNorm, gate_up with
 SiLU-mul) whenever the bucket has at most 128 rows; larger buckets use
-torch.matmul.  Weights are random (N(0, 0.02), norm weights 1) because no
-checkpoint is available; shapes follow the Qwen3-TTS 1.7B talker.
+torch.matmul.  With ``fp8_gate_up`` (the default, as the reference's serving
+build requires FP8 gate/up for every talker layer, executor/build.py:73 and
+executor/optimizations.py:22-46) the gate/up weights are held as 128 x 128
+FP8 blocks, the post-attention add-RMSNorm stores its output quantized per
+128 columns, and gate/up runs as the block-scaled FP8 product
+(model/layers.py:226-262).  Weights are random (N(0, 0.02), norm weights 1)
+because no checkpoint is available; shapes follow the Qwen3-TTS 1.7B talker.
 """
 
 from __future__ import annotations
@@ -25,14 +30,21 @@ import torch.nn.functional as F
 
 from . import _lib
 from .layers import (
+    FP8,
+    add_rmsnorm_fp8,
     linear,
     linear_add_rmsnorm,
+    linear_add_rmsnorm_fp8,
+    linear_fp8_swiglu,
+    linear_fp8_workspace_bytes,
+    pack_fp8_swiglu,
     linear_partials,
     linear_silu_mul,
     linear_workspace_bytes,
     qwen3_tts_add_rmsnorm,
     qwen3_tts_rmsnorm,
     qwen3_tts_silu_and_mul,
+    quantize_fp8_weight_blocks,
 )
 from .sampling import sample_with_uniforms, uniforms_from_counter
 
@@ -58,9 +70,12 @@ class TalkerConfig:
 
 
 class TalkerWeights:
-    """Random-init talker parameters in bf16 on one device."""
+    """Random-init talker parameters in bf16 on one device; with ``fp8_gate_up`` each layer also
+    holds its gate/up weights as FP8 blocks (``gate_up_q``, ``gate_up_scales``), as
+    GatedMLP.initialize_fp8_gate_up_weight prepares them (model/layers.py:226-239)."""
 
-    def __init__(self, config: TalkerConfig, device: torch.device, seed: int = 0, std: float = 0.02) -> None:
+    def __init__(self, config: TalkerConfig, device: torch.device, seed: int = 0, std: float = 0.02,
+                 fp8_gate_up: bool = True) -> None:
         self.config = config
         g = torch.Generator(device=device)
         g.manual_seed(seed)
@@ -90,13 +105,25 @@ class TalkerWeights:
         self.final_norm = torch.ones(c.hidden, **bf)
         self.codec_head = randn(c.vocab, c.hidden)
         self.text_embedding = randn(c.text_vocab, c.hidden)
+        self.fp8_gate_up = fp8_gate_up
+        for layer in self.layers:
+            layer.gate_up_q, layer.gate_up_scales = (
+                quantize_fp8_weight_blocks(layer.gate_up) if fp8_gate_up else (None, None))
+            # the same codes with gate/up rows interleaved for the fused SwiGLU kernel
+            layer.gate_up_packed = pack_fp8_swiglu(layer.gate_up_q) if fp8_gate_up else None
 
     def weight_bytes(self) -> int:
-        total = self.final_norm.numel() + self.codec_head.numel()
+        """Bytes of weights one decode step reads (FP8 codes + scales for gate/up when enabled)."""
+
+        total = 2 * (self.final_norm.numel() + self.codec_head.numel())
         for layer in self.layers:
-            total += sum(t.numel() for t in (layer.input_norm, layer.qkv, layer.o, layer.post_norm, layer.gate_up, layer.down))
-            total += layer.attention.q_norm.weight.numel() + layer.attention.k_norm.weight.numel()
-        return 2 * total
+            total += 2 * sum(t.numel() for t in (layer.input_norm, layer.qkv, layer.o, layer.post_norm, layer.down))
+            total += 2 * (layer.attention.q_norm.weight.numel() + layer.attention.k_norm.weight.numel())
+            if self.fp8_gate_up:
+                total += layer.gate_up_q.numel() + 4 * layer.gate_up_scales.numel()
+            else:
+                total += 2 * layer.gate_up.numel()
+        return total
 
 
 class TalkerDecodeStep:
@@ -139,10 +166,16 @@ class TalkerDecodeStep:
             (c.vocab, c.hidden, _lib.NQ_EPI_NONE),
         )
         self.use_hip_linear = all(_lib.load().nq_linear_splits(rows, n, k) > 0 for n, k, _ in projections)
-        self.linear_workspace = None
+        self.fp8 = weights.fp8_gate_up
+        need = 16
         if self.use_hip_linear:
-            need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in projections)
-            self.linear_workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+            need = max(need, max(linear_workspace_bytes(rows, n, k, e) for n, k, e in projections))
+        if self.fp8:
+            # activation codes / scales of the gate/up input
+            self.act_q = torch.zeros(rows, c.hidden, dtype=FP8, device=dev)
+            self.act_scales = torch.zeros(rows, c.hidden // 128, dtype=torch.float32, device=dev)
+            need = max(need, linear_fp8_workspace_bytes(rows, 2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL))
+        self.linear_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
 
     def forward(self) -> torch.Tensor:
         c = self.w.config
@@ -168,15 +201,28 @@ class TalkerDecodeStep:
                 k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
                 v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
                 attended = ctx.attend(layer.attention, q, k, v).view(n, q_w)
-            if self.use_hip_linear:
+            if self.fp8:
+                # post-attention add-RMSNorm quantized per 128 columns, block-scaled FP8 gate/up + SwiGLU
+                if self.use_hip_linear:
+                    linear_add_rmsnorm_fp8(attended, layer.o, self.residual, layer.post_norm, c.rms_eps,
+                                           self.act_q, self.act_scales, ws)
+                else:
+                    torch.matmul(attended, layer.o.t(), out=self.hidden)
+                    add_rmsnorm_fp8(self.hidden, self.residual, layer.post_norm, c.rms_eps, self.act_q,
+                                    self.act_scales)
+                linear_fp8_swiglu(self.act_q, self.act_scales, layer.gate_up_packed, layer.gate_up_scales,
+                                  self.act, weight_q=layer.gate_up_q, workspace=ws)
+            elif self.use_hip_linear:
                 linear_add_rmsnorm(attended, layer.o, self.residual, layer.post_norm, c.rms_eps, self.hidden, ws)
                 linear_silu_mul(self.hidden, layer.gate_up, out=self.act, workspace=ws)
-                linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
             else:
                 torch.matmul(attended, layer.o.t(), out=self.hidden)
                 qwen3_tts_add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
                 torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
                 qwen3_tts_silu_and_mul(self.gate_up, out=self.act)
+            if self.use_hip_linear:
+                linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
+            else:
                 torch.matmul(self.act, layer.down.t(), out=self.hidden)
                 qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
         ctx.advance_sequence_lengths()

@@ -27,4 +27,5 @@ def add_rmsnorm(hidden: np.ndarray, residual: np.ndarray, weight: np.ndarray, ep
 
 def silu_mul(gate_up: np.ndarray) -> np.ndarray:
     g, u = np.split(gate_up.astype(np.float32), 2, axis=-1)
-    return bf16.round_f32(g / (np.float32(1.0) + np.exp(-g)) * u)
+    with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g gives silu = -0, as on the device
+        return bf16.round_f32(g / (np.float32(1.0) + np.exp(-g)) * u)

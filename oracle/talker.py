@@ -6,15 +6,18 @@ split and o-proj, executor/talker_kv.py:104-129 attend, executor/talker.py:
 231-262 embedding and codec head) over the oracle's attention, q/k RoPE,
 norm and sampler restatements.  GEMMs run in fp32 numpy on bf16-valued
 weights with bf16 rounding at the points where the GPU stores bf16, so the
-result tracks the device within bf16 tolerance.  Also the CPU baseline of the
-benchmark (``decode_layers``).
+result tracks the device within bf16 tolerance.  A layer dict with
+``fp8_gate_up`` set runs gate/up as the block-scaled FP8 product of the
+serving build (model/layers.py:226-262 via the FP8 oracle): the normalised
+hidden state quantized per 128 columns, the weights per 128 x 128 block.
+Also the CPU baseline of the benchmark (``decode_layers``).
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from . import attention, bf16, norms, qk_rope
+from . import attention, bf16, fp8, norms, qk_rope
 
 
 def _mm(x: np.ndarray, w: np.ndarray) -> np.ndarray:
@@ -63,7 +66,13 @@ def decode_layers(
         att = bf16.round_f32(att)
         o = _mm(att.reshape(n, hq * d), L["o"])
         hidden, res = norms.add_rmsnorm(o, res, L["post_norm"], eps)
-        gu = _mm(hidden, L["gate_up"])
+        if L.get("fp8_gate_up"):
+            if "gate_up_q" not in L:
+                L["gate_up_q"], L["gate_up_s"] = fp8.quantize_weight_blocks(L["gate_up"])
+            xq, sx = fp8.quantize_rows(hidden)
+            gu = bf16.round_f32(fp8.blockscale_gemm(xq, sx, L["gate_up_q"], L["gate_up_s"]).astype(np.float32))
+        else:
+            gu = _mm(hidden, L["gate_up"])
         act = norms.silu_mul(gu)
         down = _mm(act, L["down"])
         if i + 1 < len(layers) and i + 1 in layer_range:

@@ -68,6 +68,24 @@ def test_paged_decode_matches_oracle(nq, device, label, seed, rows, lo, hi, hq, 
     kv.abort(pubs)
 
 
+def test_split_rows_identical_across_launches(nq, device):
+    """Rows split over several waves are merged by whichever wave arrives last;
+    the merge order is fixed, so every launch must give the same bits."""
+    lengths = np.random.default_rng(77).integers(64, 2049, size=64)
+    kv, ctx, pubs, q = _decode_case(nq, device, 77, lengths, pages=32768, capture=64)
+    first = _run(nq, ctx, q).clone()
+    mx, mean = attention_error(to_np(first), _oracle(ctx, q))
+    assert mx <= MAX_ABS and mean <= MEAN_ABS
+    outs = []
+    for i in range(200):
+        outs.append(ctx.run_attention(q, 0).clone())
+    torch.cuda.synchronize()
+    assert int(ctx.attention_status.item()) == 0
+    for i, o in enumerate(outs):
+        assert torch.equal(o, first), f"launch {i} differs"
+    kv.abort(pubs)
+
+
 def test_single_key_returns_value_exactly(nq, device):
     """kv_len = 1: softmax of one score is 1, so the output is V itself."""
 
