@@ -258,6 +258,31 @@ int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, 
               void *stream);
 
 /*
+ * Decode attention with the q/k norm + RoPE + K/V write fused in, for bindings
+ * whose rows are all decode rows: the work of nq_qkv_partials_norm_rope_kv_write
+ * (from the packed QKV projection's split-K planes [splits, tokens, (Hq + 2 Hkv)
+ * D]) followed by nq_paged_attention with NQ_ATTN_DECODE, in one kernel plus a
+ * merge launch that only works when a row had to be split across workgroups
+ * (the TalkerAttentionContext.attend path, executor/talker_kv.py:104-129 with
+ * model/kernels.py:15-91, for decode bindings).  Uses the plan of
+ * nq_attention_plan: rows are dealt whole to 256 workgroups (sorted by length,
+ * snake order; rows longer than a workgroup's share are cut), so partial
+ * results merge inside a workgroup.  The rotated q is not stored (attend returns
+ * the attention output only).  head_dim 128 with 1 or 2 query heads per kv
+ * head; other shapes return NQ_ERR_UNSUPPORTED and the caller runs the two
+ * entry points it replaces.
+ */
+int nq_paged_decode_rope_attention(const float *partials, int splits, int tokens, const uint16_t *q_weight,
+                                   const uint16_t *k_weight, const int64_t *positions, float eps,
+                                   float rope_theta, int round_to_input, uint16_t *cache, int64_t c_page,
+                                   int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,
+                                   const int64_t *write_pages, const int64_t *write_offsets,
+                                   const int32_t *kv_indices, int page_size, int num_qo_heads, int num_kv_heads,
+                                   int head_dim, float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
+                                   int max_query_tokens, int max_pages, void *workspace, int64_t workspace_bytes,
+                                   int32_t *status, void *stream);
+
+/*
  * FP8 (OCP e4m3fn) block quantization of a bf16 weight matrix w [N, K] into
  * codes q [N, K] and fp32 scales [N / 128, K / 128]: per 128 x 128 block,
  * scale = 2^ceil(log2(max(max|w|, 1e-4) / 448)) and q = e4m3fn(w / scale)

@@ -28,6 +28,7 @@
 // BatchPrefillWithPagedKVCacheWrapper(causal=True) (talker_kv.py:218) and the
 // short-cache kernel of model/kernels.py:408-463.
 #include "nq_common.h"
+#include "nq_internal.h"
 
 namespace nq {
 namespace {
@@ -46,8 +47,23 @@ constexpr int kPlanGrid = 8;
 
 enum MetaSlot {
     kMetaChunks = 0, kMetaChunkTok = 1, kMetaStatus = 2, kMetaQueries = 3,
-    kMetaDecRows = 4, kMetaBlocks = 5, kMetaPTiles = 6
+    kMetaDecRows = 4, kMetaBlocks = 5, kMetaPTiles = 6, kMetaPieces = 7, kMetaBinSlots = 8,
+    kMetaSplitRows = 9, kMetaCount = 16
 };
+
+// Decode bins: the fused decode kernel runs kBinWgs workgroups of kBinWaves
+// waves (one workgroup per CU, the same 4096 waves as the stream kernel);
+// workgroup (bin, kv head) owns whole (decode row, kv head) items.
+constexpr int kBinWgs = 256;
+constexpr int kBinWaves = 16;
+constexpr int kBinThreads = kBinWaves * kWave;
+constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
+constexpr int kBinSortCap = 2048;  // pieces the plan can sort
+
+__host__ __device__ inline int bins_per_head(int num_kv_heads) {
+    const int nb = kBinWgs / num_kv_heads;
+    return nb < 1 ? 1 : nb;
+}
 
 // Prefill MFMA tiles: 32 queries of one row (x 2 query heads = 64 score rows)
 // against 64-key tiles.
@@ -72,8 +88,8 @@ struct alignas(16) ChunkDesc {
 
 struct PlanLayout {
     int64_t meta, chunk_indptr, desc, part_ml, part_o;
-    int64_t dec_rows, blocks, spart_ml, spart_o, ptiles, total;
-    int64_t max_chunks, max_blocks, max_slots, max_ptiles;
+    int64_t dec_rows, blocks, spart_ml, spart_o, ptiles, pieces, bins, piece_ml, piece_o, arrivals, total;
+    int64_t max_chunks, max_blocks, max_slots, max_ptiles, max_pieces;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -87,8 +103,9 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     L.max_blocks = static_cast<int64_t>(max_pages) * (page_size > kBlockTok ? page_size / kBlockTok : 1) + T;
     L.max_slots = kStreamWaves + static_cast<int64_t>(Hkv) * T;
     L.max_ptiles = (static_cast<int64_t>(T) + kPrefQ - 1) / kPrefQ + kPlanThreads;
+    L.max_pieces = static_cast<int64_t>(T) + bins_per_head(Hkv);
     int64_t off = 0;
-    L.meta = off;         off = align256(off + 8 * 4);
+    L.meta = off;         off = align256(off + kMetaCount * 4);
     L.chunk_indptr = off; off = align256(off + (static_cast<int64_t>(T) + 1) * 4);
     L.desc = off;         off = align256(off + L.max_chunks * static_cast<int64_t>(sizeof(ChunkDesc)));
     L.part_ml = off;      off = align256(off + L.max_chunks * Hq * 2 * 4);
@@ -98,6 +115,11 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     L.spart_ml = off;     off = align256(off + L.max_slots * G * 2 * 4);
     L.spart_o = off;      off = align256(off + L.max_slots * G * D * 4);
     L.ptiles = off;       off = align256(off + L.max_ptiles * 16);
+    L.pieces = off;       off = align256(off + L.max_pieces * 16);
+    L.bins = off;         off = align256(off + (L.max_pieces + bins_per_head(Hkv)) * 4);
+    L.piece_ml = off;     off = align256(off + L.max_pieces * Hq * 2 * 4);
+    L.piece_o = off;      off = align256(off + L.max_pieces * Hq * D * 4);
+    L.arrivals = off;     off = align256(off + static_cast<int64_t>(T) * Hkv * 4);
     L.total = off;
     return L;
 }
@@ -157,6 +179,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     __shared__ int s_dec[kPlanThreads];
     __shared__ unsigned long long s_cand[8];
     __shared__ int s_tmp[kWave + 1];
+    __shared__ unsigned s_keys[kBinSortCap];
 
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
     int32_t *chunk_indptr = reinterpret_cast<int32_t *>(ws + L.chunk_indptr);
@@ -189,6 +212,9 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             meta[kMetaDecRows] = 0;
             meta[kMetaBlocks] = 0;
             meta[kMetaPTiles] = 0;
+            meta[kMetaPieces] = 0;
+            meta[kMetaBinSlots] = 0;
+            meta[kMetaSplitRows] = 0;
         }
     };
     if (T < 0 || T > max_queries) {
@@ -214,6 +240,68 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         return;
     }
     if (lead && is_dec) dec_rows[dec_idx] = make_int4(tid, s_qo[tid], boff, nblk);
+
+    // Decode bins (lead workgroup): rows longer than a bin's average load C are
+    // cut into k = ceil(blocks / C) near-equal pieces; pieces are sorted by size
+    // (descending, then piece id) and dealt to the bins in snake order
+    // (0, 1, .., NB-1, NB-1, .., 0, ..), which evens the bins' loads.  Piece
+    // descriptor: {decode row, first block, block count, (first piece << 9) | k
+    // for a split row, else -1}; bin table [NB][slots] of piece ids (-1 empty).
+    // The split rows' arrival counters (decode row x kv head) start at zero.
+    if (lead) {
+        const int NB = bins_per_head(num_kv_heads);
+        const int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
+        const int k = is_dec ? (nblk + C - 1) / C : 0;
+        int P;
+        const int p0 = plan_block_scan(k, s_tmp, &P);
+        int n_split;
+        plan_block_scan(k > 1 ? 1 : 0, s_tmp, &n_split);
+        const int slots = (P + NB - 1) / NB;
+        if (P > L.max_pieces || P > kBinSortCap || NB + 1 > 511) {
+            fail(NQ_ERR_CAPACITY);
+            return;
+        }
+        int32_t *arrivals = reinterpret_cast<int32_t *>(ws + L.arrivals);
+        for (int i = tid; i < n_dec * num_kv_heads; i += blockDim.x) arrivals[i] = 0;
+        int4 *pieces = reinterpret_cast<int4 *>(ws + L.pieces);
+        for (int i = 0; i < k; ++i) {
+            const int first = boff + static_cast<int>(static_cast<int64_t>(i) * nblk / k);
+            const int last = boff + static_cast<int>(static_cast<int64_t>(i + 1) * nblk / k);
+            pieces[p0 + i] = make_int4(dec_idx, first, last - first, k > 1 ? (p0 << 9) | k : -1);
+            const unsigned cnt = static_cast<unsigned>(last - first) > 0xFFFFu ? 0xFFFFu : static_cast<unsigned>(last - first);
+            s_keys[p0 + i] = ((0xFFFFu - cnt) << 16) | static_cast<unsigned>(p0 + i);
+        }
+        int np2 = 1;
+        while (np2 < P) np2 <<= 1;
+        for (int i = P + tid; i < np2; i += blockDim.x) s_keys[i] = 0xFFFFFFFFu;
+        for (int size = 2; size <= np2; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                __syncthreads();
+                for (int i = tid; i < np2 / 2; i += blockDim.x) {
+                    const int lo = 2 * i - (i & (stride - 1));
+                    const int hi = lo + stride;
+                    const unsigned a = s_keys[lo], b = s_keys[hi];
+                    if ((a > b) == ((lo & size) == 0)) {
+                        s_keys[lo] = b;
+                        s_keys[hi] = a;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        int32_t *bins = reinterpret_cast<int32_t *>(ws + L.bins);
+        for (int e = tid; e < NB * slots; e += blockDim.x) {
+            const int bin = e / slots, round = e % slots;
+            const int i = round * NB + ((round & 1) ? NB - 1 - bin : bin);
+            bins[e] = i < P ? static_cast<int>(s_keys[i] & 0xFFFFu) : -1;
+        }
+        if (tid == 0) {
+            meta[kMetaPieces] = P;
+            meta[kMetaBinSlots] = slots;
+            meta[kMetaSplitRows] = n_split;
+        }
+        __syncthreads();
+    }
 
     const int gstride = gridDim.x * blockDim.x;
     for (int b = blockIdx.x * blockDim.x + tid; b < n_blocks; b += gstride) {
@@ -783,6 +871,349 @@ merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads,
             }
             out[dr.y * o_s0 + (h * G + jj) * o_s1 + d] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode kernel over bins, for batches of decode rows.
+//
+// Workgroup (bin b, kv head h) = blockIdx b * Hkv + h, 16 waves.  Prologue:
+// for every piece of the bin the G query heads of kv head h of its row are
+// normalised and rotated from the packed QKV projection's split-K planes into
+// LDS, and the piece holding the row's last block also writes the new token's
+// K (normalised, rotated) and V into its cache slot -- the q/k norm + RoPE +
+// KV write of nq_qkv_partials_norm_rope_kv_write, through the same
+// norm_rope_pair arithmetic.  After a barrier the bin's blocks (its pieces'
+// blocks in slot order) are cut into 16 equal spans, one per wave, and
+// streamed as in the stream kernel.  A piece wholly inside a span is finished
+// in registers; the (at most two) boundary pieces of a span leave their
+// (m, l, acc) in LDS and are merged in wave order after a second barrier.  A
+// finished piece of an unsplit row is that row's output (bf16).  A row split
+// across bins (only rows longer than a bin's share) leaves fp32 piece
+// partials, written and read with agent-scope relaxed atomics (coherent across
+// the XCDs' L2s without a cache flush) and ordered by waiting for the stores
+// before an arrival count on the (row, kv head) counter; the piece that
+// completes the count merges all pieces in piece order and resets the counter.
+// No workgroup waits for another, and unsplit rows pay nothing for this.
+
+struct RopeSrc {
+    const float *partials;  // [splits][tokens][(Hq + 2 Hkv) D] fp32 planes
+    int splits, tokens;
+    int64_t plane, row;
+    const uint16_t *q_weight, *k_weight;
+    const int64_t *positions, *write_pages, *write_offsets;
+    float eps, log_theta;
+    int round_to_input;
+};
+
+template <int D, int G>
+struct BinPart {
+    static constexpr int kFloats = G * D + 2 * G;  // acc [G][D], then (m, l) per head
+};
+
+// Finished piece from a merge-layout lane (elements e0 .. e0 + V of the G*D
+// outputs): bf16 output of an unsplit row, else the piece's fp32 partial.
+template <int D, int G, int V>
+__device__ __forceinline__ void bin_store(const float (&os)[V], float mx, float ls, int e0, bool split, int pid, int h,
+                                          int query, int Hq, uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1,
+                                          float *__restrict__ piece_ml, float *__restrict__ piece_o) {
+    const int jj = e0 / D, d0 = e0 - jj * D;
+    const int qh = h * G + jj;
+    if (!split) {
+        const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+        uint16_t *op = out + query * o_s0 + qh * o_s1 + d0;
+#pragma unroll
+        for (int v = 0; v < V; ++v) op[v] = f32_to_bf16(os[v] * inv);
+        return;
+    }
+    float *po = piece_o + (static_cast<int64_t>(pid) * Hq + qh) * D + d0;
+#pragma unroll
+    for (int v = 0; v < V; ++v) __hip_atomic_store(po + v, os[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d0 == 0) {
+        __hip_atomic_store(piece_ml + (static_cast<int64_t>(pid) * Hq + qh) * 2, mx, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(piece_ml + (static_cast<int64_t>(pid) * Hq + qh) * 2 + 1, ls, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__device__ __forceinline__ float coherent_load(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A wave that has stored its piece of a split row counts the arrival; the
+// piece completing the count merges the row's pieces (whole wave, G*D outputs).
+template <int D, int G>
+__device__ __forceinline__ void bin_arrive(int4 pc, int h, int num_kv_heads, int query, int lane,
+                                           int32_t *__restrict__ arrivals, const float *__restrict__ piece_ml,
+                                           const float *__restrict__ piece_o, uint16_t *__restrict__ out,
+                                           int64_t o_s0, int64_t o_s1) {
+    // the piece's coherent stores are complete before the arrival counts
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int32_t *counter = arrivals + pc.x * num_kv_heads + h;
+    int before = 0;
+    if (lane == 0) before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    before = __shfl(before, 0, kWave);
+    const int p0 = pc.w >> 9, k = pc.w & 511;
+    if (before != k - 1) return;
+    const int Hq = num_kv_heads * G;
+    for (int t = lane; t < G * D; t += kWave) {
+        const int jj = t / D, d = t - jj * D;
+        const int qh = h * G + jj;
+        float mx = -INFINITY, ls = 0.f, os = 0.f;
+        for (int q = p0; q < p0 + k; ++q) {
+            const float mk = coherent_load(piece_ml + (static_cast<int64_t>(q) * Hq + qh) * 2);
+            const float lk = coherent_load(piece_ml + (static_cast<int64_t>(q) * Hq + qh) * 2 + 1);
+            const float ok = coherent_load(piece_o + (static_cast<int64_t>(q) * Hq + qh) * D + d);
+            if (mk == -INFINITY) continue;
+            const float cm = fmaxf(mx, mk);
+            const float keep = mx == -INFINITY ? 0.f : exp2f(mx - cm);
+            const float sc = exp2f(mk - cm);
+            ls = ls * keep + lk * sc;
+            os = os * keep + ok * sc;
+            mx = cm;
+        }
+        out[query * o_s0 + qh * o_s1 + d] = f32_to_bf16(ls > 0.f ? os / ls : 0.f);
+    }
+    if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int G, bool kSmallPages>
+__global__ void __launch_bounds__(kBinThreads)
+bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
+                  int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
+                  int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out, int64_t o_s0,
+                  int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
+    using LN = Lanes<D, G>;
+    constexpr int kPart = BinPart<D, G>::kFloats;
+    constexpr int HALF = D / 2;
+    __shared__ int4 s_piece[kBinMaxSlots];
+    __shared__ int s_pid[kBinMaxSlots];
+    __shared__ int s_start[kBinMaxSlots + 1];
+    __shared__ int s_n;
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[kBinMaxSlots * G * D];
+    __shared__ __attribute__((aligned(16))) float s_part[kBinWaves * 2 * kPart];
+
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && status) atomicExch(status, meta[kMetaStatus]);
+        return;
+    }
+    const int NB = bins_per_head(num_kv_heads);
+    const int bin = blockIdx.x / num_kv_heads, h = blockIdx.x - (blockIdx.x / num_kv_heads) * num_kv_heads;
+    const int slots = meta[kMetaBinSlots];
+    if (bin >= NB || slots <= 0) return;
+    if (slots > kBinMaxSlots) {
+        if (threadIdx.x == 0 && status) atomicExch(status, NQ_ERR_CAPACITY);
+        return;
+    }
+    const int4 *pieces = reinterpret_cast<const int4 *>(ws + L.pieces);
+    const int32_t *bins = reinterpret_cast<const int32_t *>(ws + L.bins);
+    const int4 *dec_rows = reinterpret_cast<const int4 *>(ws + L.dec_rows);
+    const int4 *blocks = reinterpret_cast<const int4 *>(ws + L.blocks);
+    float *piece_ml = reinterpret_cast<float *>(ws + L.piece_ml);
+    float *piece_o = reinterpret_cast<float *>(ws + L.piece_o);
+    int32_t *arrivals = reinterpret_cast<int32_t *>(ws + L.arrivals);
+    const int Hq = num_kv_heads * G;
+
+    // the bin's pieces (empty slots come last) and their block offsets
+    if (threadIdx.x < slots) {
+        const int pid = bins[bin * slots + threadIdx.x];
+        s_pid[threadIdx.x] = pid;
+        s_piece[threadIdx.x] = pid >= 0 ? pieces[pid] : make_int4(-1, 0, 0, -1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0, n = 0;
+        for (int i = 0; i < slots; ++i) {
+            s_start[i] = acc;
+            if (s_pid[i] >= 0) {
+                acc += s_piece[i].z;
+                n = i + 1;
+            }
+        }
+        s_start[slots] = acc;
+        for (int i = n; i <= slots; ++i) s_start[i] = acc;
+        s_n = n;
+    }
+    __syncthreads();
+    const int nslots = s_n;
+    const int NBB = s_start[nslots];
+    if (NBB == 0) return;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    bool bad = false;
+
+    // 1. q/k norm + RoPE + K/V write for the bin's rows (one wave per head unit)
+    for (int u = wave; u < nslots * (G + 2); u += kBinWaves) {
+        const int sl = u / (G + 2), kind = u - sl * (G + 2);
+        const int4 pc = s_piece[sl];
+        const int4 dr = dec_rows[pc.x];
+        const bool row_last = pc.y + pc.z == dr.z + dr.w;
+        if (kind >= G && !row_last) continue;  // the row's new K/V belong to its last piece
+        const int64_t tok = dr.y;
+        if (tok >= rs.tokens) {  // a query beyond the projection's rows
+            bad = true;
+            continue;
+        }
+        const int col = kind < G ? (h * G + kind) * D : (kind == G ? Hq + h : Hq + num_kv_heads + h) * D;
+        const bool on = lane < HALF;
+        float x1 = 0.f, x2 = 0.f;
+        if (on) {
+            const float *e = rs.partials + tok * rs.row + col + lane;
+            for (int i = 0; i < rs.splits; ++i) {
+                x1 += e[i * rs.plane];
+                x2 += e[i * rs.plane + HALF];
+            }
+            x1 = bf16_to_f32(f32_to_bf16(x1));
+            x2 = bf16_to_f32(f32_to_bf16(x2));
+        }
+        const int64_t page = rs.write_pages[tok], woff = rs.write_offsets[tok];
+        const bool slot_ok = static_cast<uint64_t>(page) < static_cast<uint64_t>(num_pages) &&
+                             static_cast<uint64_t>(woff) < (static_cast<uint64_t>(1) << ps_log2);
+        if (kind >= G && !slot_ok) {
+            bad = true;
+            continue;
+        }
+        uint16_t *cslot = cache + page * c_page + woff * c_slot + h * c_head;
+        if (kind == G + 1) {
+            if (on) {
+                cslot[c_kind + lane] = f32_to_bf16(x1);
+                cslot[c_kind + lane + HALF] = f32_to_bf16(x2);
+            }
+            continue;
+        }
+        uint16_t o1 = 0, o2 = 0;
+        norm_rope_pair<D>(x1, x2, on, kind < G ? rs.q_weight : rs.k_weight, lane, rs.eps, rs.log_theta,
+                          static_cast<float>(rs.positions[tok]), rs.round_to_input, o1, o2);
+        if (!on) continue;
+        if (kind < G) {
+            s_q[(sl * G + kind) * D + lane] = o1;
+            s_q[(sl * G + kind) * D + lane + HALF] = o2;
+        } else {
+            cslot[lane] = o1;
+            cslot[lane + HALF] = o2;
+        }
+    }
+    __syncthreads();  // rotated q in LDS, the new K/V in the cache for every wave of the workgroup
+
+    // 2. stream the wave's span of the bin's blocks
+    const int g = lane / LN::LPT;
+    const int sub = lane % LN::LPT;
+    const int s0 = span_start(wave, NBB, kBinWaves);
+    const int s1 = span_start(wave + 1, NBB, kBinWaves);
+    if (s0 < s1) {
+        // descriptors of the span, 64 at a time, one per lane (lane -> bin-local block -> global block)
+        auto global_block = [&](int lb) {
+            int sl = 0;
+            while (sl + 1 < nslots && s_start[sl + 1] <= lb) ++sl;
+            return s_piece[sl].y + lb - s_start[sl];
+        };
+        int win = s0;
+        int4 dwin = make_int4(-1, 0, 0, 0);
+        if (s0 + lane < s1) dwin = blocks[global_block(s0 + lane)];
+        auto desc_of = [&](int w) {
+            if (w - win >= kWave) {
+                win += kWave;
+                dwin = win + lane < s1 ? blocks[global_block(win + lane)] : make_int4(-1, 0, 0, 0);
+            }
+            return shfl_int4(dwin, w - win);
+        };
+        SoftmaxState<D, G> st;
+        int cur = -1;
+        while (s_start[cur + 1] <= s0) ++cur;  // slot of the span's first block
+        st.reset();
+        st.load_q(s_q + cur * G * D, D, 0, sub, scale_log2);
+        // finish slot sl's part of this span: whole pieces go out, boundary ones to LDS
+        auto flush = [&](int sl) {
+            st.combine_lane_groups();
+            const bool whole = s_start[sl] >= s0 && s_start[sl + 1] <= s1;
+            if (whole) {
+                const int4 pc = s_piece[sl];
+                const int query = dec_rows[pc.x].y;
+                if (g == 0) {
+#pragma unroll
+                    for (int j = 0; j < G; ++j) {
+                        float os[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) os[e] = st.acc[j][e];
+                        bin_store<D, G, 8>(os, st.m[j], st.l[j], j * D + sub * 8, pc.w >= 0, s_pid[sl], h, query, Hq,
+                                           out, o_s0, o_s1, piece_ml, piece_o);
+                    }
+                }
+                if (pc.w >= 0)
+                    bin_arrive<D, G>(pc, h, num_kv_heads, query, lane, arrivals, piece_ml, piece_o, out, o_s0, o_s1);
+            } else if (g == 0) {
+                float *pp = s_part + (wave * 2 + (s_start[sl] > s0 ? 1 : 0)) * kPart;
+#pragma unroll
+                for (int j = 0; j < G; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pp[j * D + sub * 8 + e] = st.acc[j][e];
+                    if (sub == 0) {
+                        pp[G * D + 2 * j] = st.m[j];
+                        pp[G * D + 2 * j + 1] = st.l[j];
+                    }
+                }
+            }
+        };
+        uint4 kc[LN::NL], vc[LN::NL];
+        bool okc[LN::NL];
+        for (int w = s0; w < s1; ++w) {
+            if (w == s_start[cur + 1]) {
+                flush(cur);
+                ++cur;
+                st.reset();
+                st.load_q(s_q + cur * G * D, D, 0, sub, scale_log2);
+            }
+            const int4 dc = desc_of(w);
+            stream_issue<D, G, kSmallPages>(dc, h, cache, c_page, c_kind, c_slot, c_head, num_pages, ps_log2,
+                                            kv_indices, index_limit, g, sub, kc, vc, okc, &bad);
+            st.consume(kc, vc, okc);
+        }
+        flush(cur);
+    }
+    if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+    __syncthreads();
+
+    // 3. pieces shared by several waves: merge their LDS partials in wave order
+    constexpr int EPL = G * D / kWave;
+    constexpr int V = EPL < 4 ? EPL : 4;
+    constexpr int NG = EPL / V;
+    for (int sl = wave; sl < nslots; sl += kBinWaves) {
+        const int a = s_start[sl], b = s_start[sl + 1];
+        if (a == b) continue;
+        const int w0 = span_of(a, NBB, kBinWaves), w1 = span_of(b - 1, NBB, kBinWaves);
+        if (w0 == w1) continue;  // finished by its wave
+        const int4 pc = s_piece[sl];
+        const int query = dec_rows[pc.x].y;
+        for (int grp = 0; grp < NG; ++grp) {
+            const int e0 = (grp * kWave + lane) * V;
+            const int jj = e0 / D;
+            float mx = -INFINITY, ls = 0.f, os[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) os[v] = 0.f;
+            for (int w = w0; w <= w1; ++w) {
+                const int ws0 = span_start(w, NBB, kBinWaves);
+                if (ws0 == span_start(w + 1, NBB, kBinWaves)) continue;  // an empty span (bins of < 16 blocks)
+                const float *pp = s_part + (w * 2 + (a > ws0 ? 1 : 0)) * kPart;
+                const float mk = pp[G * D + 2 * jj], lk = pp[G * D + 2 * jj + 1];
+                if (mk == -INFINITY) continue;
+                const float cm = fmaxf(mx, mk);
+                const float keep = mx == -INFINITY ? 0.f : exp2f(mx - cm);
+                const float sc = exp2f(mk - cm);
+                ls = ls * keep + lk * sc;
+#pragma unroll
+                for (int v = 0; v < V; ++v) os[v] = os[v] * keep + pp[e0 + v] * sc;
+                mx = cm;
+            }
+            bin_store<D, G, V>(os, mx, ls, e0, pc.w >= 0, s_pid[sl], h, query, Hq, out, o_s0, o_s1, piece_ml,
+                               piece_o);
+        }
+        if (pc.w >= 0)
+            bin_arrive<D, G>(pc, h, num_kv_heads, query, lane, arrivals, piece_ml, piece_o, out, o_s0, o_s1);
     }
 }
 
@@ -1363,4 +1794,55 @@ extern "C" int nq_cp_short_attention(const uint16_t *q, int64_t q_s0, int64_t q_
     NQ_DENSE(64, 1) NQ_DENSE(64, 2) NQ_DENSE(64, 4) NQ_DENSE(64, 8)
 #undef NQ_DENSE
     return NQ_ERR_UNSUPPORTED;
+}
+
+extern "C" int nq_paged_decode_rope_attention(const float *partials, int splits, int tokens, const uint16_t *q_weight,
+                                              const uint16_t *k_weight, const int64_t *positions, float eps,
+                                              float rope_theta, int round_to_input, uint16_t *cache, int64_t c_page,
+                                              int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages,
+                                              const int64_t *write_pages, const int64_t *write_offsets,
+                                              const int32_t *kv_indices, int page_size, int num_qo_heads,
+                                              int num_kv_heads, int head_dim, float sm_scale, uint16_t *out,
+                                              int64_t o_s0, int64_t o_s1, int max_query_tokens, int max_pages,
+                                              void *workspace, int64_t workspace_bytes, int32_t *status,
+                                              void *stream) {
+    NQ_CHECK_ARG(partials && splits >= 1 && tokens >= 1 && q_weight && k_weight && positions && cache);
+    NQ_CHECK_ARG(write_pages && write_offsets && kv_indices && out && workspace);
+    NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1 && rope_theta > 0.f);
+    NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
+    NQ_CHECK_ARG(max_query_tokens >= 1 && max_pages >= 1 && tokens <= max_query_tokens);
+    const int G = num_qo_heads / num_kv_heads;
+    const int NB = nq::bins_per_head(num_kv_heads);
+    // shapes the fused kernel does not take: the caller runs the rope and attention kernels instead
+    if (head_dim != 128 || (G != 1 && G != 2) || num_kv_heads > nq::kBinWgs ||
+        (max_query_tokens + NB - 1) / NB + 1 > nq::kBinMaxSlots)
+        return NQ_ERR_UNSUPPORTED;
+    if (!nq::aligned16(cache) || !nq::aligned16(out)) return NQ_ERR_UNSUPPORTED;
+    if ((c_page | c_kind | c_slot | c_head | o_s0 | o_s1) & 7) return NQ_ERR_UNSUPPORTED;
+    const PlanLayout L =
+        nq::plan_layout(max_query_tokens, max_pages, page_size, num_qo_heads, num_kv_heads, head_dim);
+    NQ_CHECK_ARG(workspace_bytes >= L.total);
+    int ps_log2 = 0;
+    while ((1 << ps_log2) < page_size) ++ps_log2;
+    const int64_t row = static_cast<int64_t>(num_qo_heads + 2 * num_kv_heads) * head_dim;
+    const nq::RopeSrc rs{partials, splits, tokens, static_cast<int64_t>(tokens) * row, row, q_weight, k_weight,
+                         positions, write_pages, write_offsets, eps, logf(rope_theta), round_to_input};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char *ws = static_cast<char *>(workspace);
+    const float scale_log2 = sm_scale * nq::kLog2e;
+    const dim3 grid(static_cast<unsigned>(NB * num_kv_heads));
+#define NQ_BIN(GG, SMALL)                                                                                    \
+    hipLaunchKernelGGL((nq::bin_decode_kernel<128, GG, SMALL>), grid, dim3(nq::kBinThreads), 0, st, rs, cache, \
+                       c_page, c_kind, c_slot, c_head, num_pages, kv_indices, max_pages, num_kv_heads, ps_log2,  \
+                       scale_log2, out, o_s0, o_s1, ws, L, status)
+    const bool small_pages = ps_log2 < 4;
+    if (G == 2) {
+        if (small_pages) NQ_BIN(2, true);
+        else NQ_BIN(2, false);
+    } else {
+        if (small_pages) NQ_BIN(1, true);
+        else NQ_BIN(1, false);
+    }
+#undef NQ_BIN
+    return NQ_LAUNCH_STATUS();
 }

@@ -75,6 +75,33 @@ __device__ __forceinline__ uint2 e4m3_pack8(const float (&x)[8], float s) {
 // group (whose codes are then all zero).
 __device__ __forceinline__ float row_group_scale(float amax) { return amax > 0.f ? amax / 448.0f : 1.0f; }
 
+// q/k RMSNorm (with weight) and rotate-half RoPE of one head of D values held
+// as lane pairs: lane i < D/2 holds elements i and i + D/2 (x1, x2); lanes at
+// or above D/2 pass on = false.  inv_freq = exp(-ln(theta) * 2i / D), the
+// normalised values are rounded to bf16 first when round_to_input is set.
+// Every caller (the rope kernel and the fused decode attention) goes through
+// this one sequence of operations, so their q and K agree bit for bit.
+template <int D>
+__device__ __forceinline__ void norm_rope_pair(float x1, float x2, bool on, const uint16_t *__restrict__ weight,
+                                               int lane, float eps, float log_theta, float position,
+                                               int round_to_input, uint16_t &o1, uint16_t &o2) {
+    constexpr int HALF = D / 2;
+    const float ss = group_sum<(HALF < kWave ? HALF : kWave)>(on ? x1 * x1 + x2 * x2 : 0.f);
+    if (!on) return;
+    const float inv_rms = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    float f = x1 * inv_rms * bf16_to_f32(weight[lane]);
+    float s = x2 * inv_rms * bf16_to_f32(weight[lane + HALF]);
+    if (round_to_input) {
+        f = bf16_to_f32(f32_to_bf16(f));
+        s = bf16_to_f32(f32_to_bf16(s));
+    }
+    const float inv_freq = expf(-log_theta * (static_cast<float>(lane) * 2.0f / static_cast<float>(D)));
+    float sn, cs;
+    sincosf(position * inv_freq, &sn, &cs);
+    o1 = f32_to_bf16(f * cs - s * sn);
+    o2 = f32_to_bf16(s * cs + f * sn);
+}
+
 // Bands (64 output columns each) per GEMM workgroup for `splits` K slices.
 int bands_per_wg(int bands, int splits);
 

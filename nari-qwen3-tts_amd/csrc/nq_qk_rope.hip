@@ -100,22 +100,10 @@ qk_norm_rope_kernel(Src src, RopeOut dst, const uint16_t *__restrict__ q_weight,
         x1 = src.load(kind, tok, head, lane);
         x2 = src.load(kind, tok, head, lane + HALF);
     }
-    const float ss = group_sum<(HALF < kWave ? HALF : kWave)>(x1 * x1 + x2 * x2);
+    uint16_t o1 = 0, o2 = 0;
+    norm_rope_pair<D>(x1, x2, on, kind == kUnitQ ? q_weight : k_weight, lane, eps, log_theta,
+                      static_cast<float>(positions[tok * pos_stride]), round_to_input, o1, o2);
     if (!on) return;
-    const uint16_t *w = kind == kUnitQ ? q_weight : k_weight;
-    const float inv_rms = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-    float f = x1 * inv_rms * bf16_to_f32(w[lane]);
-    float s = x2 * inv_rms * bf16_to_f32(w[lane + HALF]);
-    if (round_to_input) {
-        f = bf16_to_f32(f32_to_bf16(f));
-        s = bf16_to_f32(f32_to_bf16(s));
-    }
-    const float position = static_cast<float>(positions[tok * pos_stride]);
-    const float inv_freq = expf(-log_theta * (static_cast<float>(lane) * 2.0f / static_cast<float>(D)));
-    float sn, cs;
-    sincosf(position * inv_freq, &sn, &cs);
-    const uint16_t o1 = f32_to_bf16(f * cs - s * sn);
-    const uint16_t o2 = f32_to_bf16(s * cs + f * sn);
     if (kind == kUnitQ) {
         uint16_t *qo = dst.q + tok * dst.q_s0 + head * dst.q_s1;
         qo[lane] = o1;

@@ -113,6 +113,8 @@ class _HipBindingBase:
         self.write_offsets = self.buffers.write_offsets
         self.metadata: TalkerAttentionMetadata | None = None
         self._layer_index = 0
+        # decode bindings take the fused bins kernel in attend_partials while the library accepts the shape
+        self.fused_decode = True
         self._side: torch.cuda.Stream | None = None
 
     # -- planning ---------------------------------------------------------
@@ -209,6 +211,22 @@ class _HipBindingBase:
         layer = self.storage[self._layer_index]
         b = self.buffers
         stream = _lib.stream(self.device)
+        if not self.prefill and self.fused_decode:
+            # decode rows: one fused kernel (bins of whole rows, q/k norm + RoPE + K/V write in its
+            # prologue); shapes it does not take fall back to the two-kernel path below, for good
+            out = self.output
+            rc = _lib.load().nq_paged_decode_rope_attention(
+                partials.data_ptr(), int(splits), tokens, qw.data_ptr(), kw.data_ptr(), b.position_ids.data_ptr(),
+                float(attention.q_norm.variance_epsilon), float(attention.rope_theta), 1,
+                layer.data_ptr(), layer.stride(0), layer.stride(1), layer.stride(2), layer.stride(3), layer.shape[0],
+                b.write_pages.data_ptr(), b.write_offsets.data_ptr(), b.kv_indices.data_ptr(), self.page_size,
+                self.num_qo_heads, self.num_kv_heads, self.head_dim, float(self.head_dim) ** -0.5,
+                out.data_ptr(), out.stride(0), out.stride(1), self.token_capacity, self.index_capacity,
+                self.workspace.data_ptr(), self.workspace.numel(), self.attention_status.data_ptr(), stream)
+            if rc != _lib.NQ_ERR_UNSUPPORTED:
+                _lib.check(rc, "nq_paged_decode_rope_attention")
+                return out
+            self.fused_decode = False
         _lib.call(
             "nq_qkv_partials_norm_rope_kv_write",
             partials.data_ptr(), int(splits), tokens, query_out.data_ptr(), query_out.stride(0), query_out.stride(1),

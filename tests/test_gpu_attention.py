@@ -223,3 +223,69 @@ def test_code_predictor_short_cache(nq, device, valid_length):
     mx, mean = attention_error(to_np(out[:, 0]), want)
     assert out.shape == q.shape
     assert mx <= MAX_ABS and mean <= MEAN_ABS
+
+
+def _fused_case(nq, device, seed, lengths, capture, pages, ps=16):
+    rng = np.random.default_rng(seed)
+    kv = make_kv(nq, device, layers=1, pages=pages, ps=ps, scratch=capture)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    kv.storage.copy_(torch.randn(kv.storage.shape, generator=g, device=device).to(torch.bfloat16))
+    rids = adopt_random(kv, rng, lengths)
+    key = DecodeKey(capture)
+    ctx = kv.create_decode(key, slot=0)
+    pubs = kv.prepare_decode(ctx, key, tuple(rids))
+    splits, row = 4, (16 + 2 * 8) * 128
+    planes = (torch.randn(splits * capture * row, generator=g, device=device) * 0.5).float()
+    qw = torch.rand(128, generator=g, device=device) + 0.5
+    kw = torch.rand(128, generator=g, device=device) + 0.5
+    att = attention_module(128, weights=(qw, kw), device=device)
+    return kv, ctx, pubs, planes, splits, att
+
+
+def _lengths(kind, rng):
+    if kind == "cfg2":
+        return rng.integers(64, 2049, size=64), 64, 32768
+    if kind == "small":
+        return rng.integers(16, 513, size=8), 8, 4096
+    if kind == "skewed":  # one row far beyond a bin's share: split across bins and merged
+        return np.concatenate([[6000], rng.integers(10, 100, size=20)]), 21, 4096
+    if kind == "tiny":  # bins of fewer than 16 blocks: waves with empty spans
+        return rng.integers(1, 4, size=13), 16, 1024
+    return rng.integers(1, 300, size=40), 40, 4096
+
+
+@pytest.mark.parametrize("kind", ["cfg2", "small", "skewed", "tiny", "mixed-len"])
+def test_fused_decode_rope_attention(nq, device, kind):
+    """attend_partials on a decode binding: the fused bins kernel vs the two-kernel path (rope kernel,
+    then stream + merge) on the same cache, and vs the oracle."""
+    rng = np.random.default_rng(hash(kind) % 1000)
+    lengths, capture, pages = _lengths(kind, rng)
+    kv, ctx, pubs, planes, splits, att = _fused_case(nq, device, 900 + len(kind), lengths, capture, pages)
+    q_out = torch.zeros(capture, 16, 128, dtype=torch.bfloat16, device=device)
+    before = kv.storage.clone()
+    assert ctx.fused_decode
+    out_f = ctx.attend_partials(att, planes, splits, q_out).clone()
+    out_f2 = ctx.attend_partials(att, planes, splits, q_out).clone()  # the same K/V rewritten: same inputs
+    torch.cuda.synchronize()
+    assert int(ctx.attention_status.item()) == 0
+    assert ctx.fused_decode, "the library declined the fused shape"
+    meta = ctx.workspace[:64].view(torch.int32).cpu().numpy()
+    if kind == "skewed":
+        assert meta[9] > 0, "no row was split across bins"
+    cache_f = kv.storage.clone()
+    kv.storage.copy_(before)
+    ctx.fused_decode = False
+    out_u = ctx.attend_partials(att, planes, splits, q_out).clone()
+    torch.cuda.synchronize()
+    assert int(ctx.attention_status.item()) == 0
+    # the new K/V come from the same norm + RoPE arithmetic: bit-exact
+    assert torch.equal(cache_f, kv.storage)
+    assert torch.equal(out_f, out_f2)
+    m = ctx.metadata
+    want = o_att.paged_attention(to_np(q_out), to_np(kv.storage[0]), to_np(m.paged_kv_indptr),
+                                 to_np(m.paged_kv_indices), to_np(m.paged_kv_last_page_len))
+    for got in (out_f, out_u):
+        mx, mean = attention_error(to_np(got), want)
+        assert mx <= MAX_ABS and mean <= MEAN_ABS, (kind, mx, mean)
+    kv.abort(pubs)
