@@ -6,15 +6,16 @@ Workload (the serving metric's configuration): random-init Qwen3-style talker,
 every page of every sequence drawn from a random permutation of a 32768-page
 pool filled with N(0,1) bf16 K/V.  One step = GPU metadata planning for the
 64 rows (ragged page table + attention plan) + one hipGraph replay of the
-forward (28 x [norm, QKV GEMM, q/k norm+RoPE+paged KV write, paged attention,
-o-proj, add-norm, SwiGLU MLP, add-norm], codec head, Philox uniforms, fused
+forward (28 x [norm, QKV GEMM, fused q/k norm+RoPE+paged KV write+paged
+attention, o-proj, add-norm, FP8 gate/up+SwiGLU, down, add-norm], codec head,
+Philox uniforms, fused
 sampler with masks / repetition penalty / top-k 50 / top-p 0.95 / T 0.9 and
 seen-mask update) + publishing the KV of the new token.  Sequences grow by one
 token per step.
 
-Prints one JSON line: tok/s over the timed steps, the paged-attention kernel's
-achieved HBM bandwidth against the 8 TB/s peak (``roofline``), and the CPU
-oracle on a bounded sample of the same step (``cpu_baseline``).
+Prints one JSON line: tok/s over the timed steps, the fused decode-attention
+kernel's achieved HBM bandwidth against the 8 TB/s peak (``roofline``), and the
+CPU oracle on a bounded sample of the same step (``cpu_baseline``).
 """
 
 from __future__ import annotations
@@ -35,10 +36,10 @@ PAGE_SIZE = 16
 POOL_PAGES = 32768
 KV_LO, KV_HI = 64, 2048
 SEED = 1002
-# HBM bytes one attention launch of this workload moves (stream + merge kernels), from the FETCH_SIZE /
-# WRITE_SIZE counter passes in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device
-# copy: x2.0 and x1.0).
-ATTENTION_TRAFFIC_BYTES = 256_354_600
+# HBM bytes one fused decode-attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE
+# counter passes in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device copy:
+# x2.0 and x1.0).
+ATTENTION_TRAFFIC_BYTES = 251_312_343
 
 
 def log(*a):
@@ -125,18 +126,27 @@ def kv_tokens(w) -> int:
 
 
 def attention_probe(torch, w, replays: int = 20):
-    """Average duration of the paged-attention kernel: a graph of its 28 layer launches, timed with events."""
+    """Average duration of the fused decode-attention kernel as the step runs it (q/k norm + RoPE +
+    K/V write from the QKV projection's split-K planes, then paged attention): a graph of its 28
+    layer launches, timed with events on the launch stream."""
 
-    kv, ctx, cfg = w["kv"], w["ctx"], w["cfg"]
+    kv, ctx, cfg, step = w["kv"], w["ctx"], w["cfg"], w["step"]
     pubs = kv.prepare_decode(ctx, w["key"], w["rids"])  # metadata for one more token per row
-    q = torch.randn(ROWS, cfg.num_qo_heads, cfg.head_dim, device="cuda").to(torch.bfloat16)
+    splits = 2048 // 512
+    planes = torch.randn(splits * ROWS * cfg.qkv_width, device="cuda") * 0.5
+    q_out = torch.empty(ROWS, cfg.num_qo_heads, cfg.head_dim, dtype=torch.bfloat16, device="cuda")
+    att = w["weights"].layers[0].attention
+
     def launches():
         for layer_index in range(cfg.num_layers):
-            ctx.run_attention(q, layer_index)
+            ctx.select_layer(layer_index)
+            ctx.attend_partials(att, planes, splits, q_out)
 
     from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
 
-    call = HipGraphCaptureDriver(device=q.device).capture(launches)
+    call = HipGraphCaptureDriver(device=q_out.device).capture(launches)
+    if not ctx.fused_decode:
+        raise RuntimeError("the fused decode-attention kernel declined the workload")
     tokens_per_launch = sum(kv.state(r).sequence_length + 1 for r in w["rids"])
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -152,8 +162,12 @@ def attention_probe(torch, w, replays: int = 20):
     status = int(ctx.attention_status.item())
     if status != 0:
         raise RuntimeError(f"attention status {status}")
-    bytes_per_launch = tokens_per_launch * cfg.num_kv_heads * cfg.head_dim * 2 * 2  # K and V, bf16
-    return avg_ms, bytes_per_launch, tokens_per_launch
+    # K/V read (8 heads x 128 x bf16 x {K, V} per token) + the split-K planes the q/k/v of the rows
+    # come from + the new K/V and the output written
+    kv_bytes = tokens_per_launch * cfg.num_kv_heads * cfg.head_dim * 2 * 2
+    plane_bytes = splits * ROWS * cfg.qkv_width * 4
+    write_bytes = ROWS * (2 * cfg.num_kv_heads + cfg.num_qo_heads) * cfg.head_dim * 2
+    return avg_ms, kv_bytes + plane_bytes + write_bytes, tokens_per_launch
 
 
 def cpu_baseline(torch, np, w, budget_s: float = 10.0):
@@ -290,7 +304,7 @@ def talker_decode(args, torch, np) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": ATTENTION_TRAFFIC_BYTES,
-            "kernel": "nq_paged_attention: paged_stream_kernel<128,2> + merge_stream_kernel<128,2>",
+            "kernel": "nq_paged_decode_rope_attention: bin_decode_kernel<128,2> (q/k norm + RoPE + K/V write + attention)",
             "bytes_per_launch": bytes_per_launch,
             "us_per_launch": round(avg_ms * 1e3, 2),
         },
