@@ -125,7 +125,7 @@ __device__ __forceinline__ void fp8_tile(const int8v_t (&wr)[KS / 128], const ui
             const int8v_t b = *reinterpret_cast<const int8v_t *>(bp);
             const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-            const float s = sxs[(m * 16 + r16) * kSteps + j] * swj;
+            const float s = sxs[j * (16 * MT) + m * 16 + r16] * swj;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[m][e] = fmaf(t[e], s, acc[m][e]);
         }
@@ -166,7 +166,7 @@ gemm_fp8_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__rest
     constexpr int kSteps = KS / 128;
     constexpr int kRows = 16 * MT;
     __shared__ __attribute__((aligned(16))) uint8_t xs[kRows * fp8_pitch<KS>()];
-    __shared__ float sxs[kRows * kSteps];  // activation scales of the slice's K blocks, per row
+    __shared__ float sxs[kSteps * kRows];  // activation scales [K block][row] (a wave's rows on distinct banks)
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -194,7 +194,7 @@ gemm_fp8_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__rest
     }
     for (int i = threadIdx.x; i < kRows * kSteps; i += kFp8Threads) {
         const int row = i / kSteps, j = i % kSteps;
-        sxs[i] = row < M ? sx[row * sx_s0 + kb0 + j] : 0.f;
+        sxs[j * kRows + row] = row < M ? sx[row * sx_s0 + kb0 + j] : 0.f;
     }
 
     // 2. the band's weights, all in flight together
@@ -242,7 +242,7 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
     constexpr int QS = K / kSwQuarters / 128;      // K blocks per quarter
     constexpr int P = K + 16;                      // LDS pitch of an X row in bytes
     __shared__ __attribute__((aligned(16))) uint8_t xs[kSwRows * P];
-    __shared__ float sxs[kSwRows * KB];
+    __shared__ float sxs[KB * kSwRows];  // [K block][row]: a wave's 16 rows hit 16 banks
     static_assert((kSwQuarters - 1) * kSwTiles * kWave * 16 * 4 <= kSwRows * P, "reduction fits the X area");
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -291,7 +291,8 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
 #pragma unroll
         for (int u = 0; u < kSxPer; ++u) {
             const int i = threadIdx.x + u * kSwThreads;
-            sr[u] = (i < kSx && i / KB < M) ? sx[(i / KB) * sx_s0 + i % KB] : 0.f;
+            // element i of the [K block][row] table
+            sr[u] = (i < kSx && i % kSwRows < M) ? sx[(i % kSwRows) * sx_s0 + i / kSwRows] : 0.f;
         }
 #pragma unroll
         for (int u = 0; u < kPer; ++u) {
@@ -318,7 +319,7 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
             const int8v_t b = *reinterpret_cast<const int8v_t *>(xs + row * P + (kb0 + j) * 128 + kq * 32);
             const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-            const float sxv = sxs[row * KB + kb0 + j];
+            const float sxv = sxs[(kb0 + j) * kSwRows + row];
             const float sg = sxv * swg[j], su = sxv * swu[j];
             acc[m][0] = fmaf(t[0], sg, acc[m][0]);
             acc[m][1] = fmaf(t[1], sg, acc[m][1]);
@@ -335,20 +336,21 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
     // 4. quarters 1.. hand their sums to quarter 0 through the (now free) X area
     __syncthreads();
     float *red = reinterpret_cast<float *>(xs);
+    // layout [quarter - 1][tile][m][lane][4]: a float4 access touches 64 consecutive float4s
     if (quarter > 0) {
-        float *dst = red + (((quarter - 1) * kSwTiles + tl) * kWave + lane) * 16;
+        float *dst = red + (((quarter - 1) * kSwTiles + tl) * 4 * kWave + lane) * 4;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            *reinterpret_cast<float4 *>(dst + m * 4) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+            *reinterpret_cast<float4 *>(dst + m * kWave * 4) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
     }
     __syncthreads();
     if (quarter != 0) return;
 #pragma unroll
     for (int q = 1; q < kSwQuarters; ++q) {
-        const float *src = red + (((q - 1) * kSwTiles + tl) * kWave + lane) * 16;
+        const float *src = red + (((q - 1) * kSwTiles + tl) * 4 * kWave + lane) * 4;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + m * 4);
+            const float4 v = *reinterpret_cast<const float4 *>(src + m * kWave * 4);
             acc[m][0] += v.x;
             acc[m][1] += v.y;
             acc[m][2] += v.z;
