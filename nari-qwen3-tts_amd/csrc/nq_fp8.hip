@@ -87,12 +87,38 @@ quantize_rows_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, int K,
 typedef int int8v_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-// LDS pitch of the staged X slice in bytes: 16 bytes of padding put the 16
-// rows one B-operand read touches on distinct 4-bank groups.
-template <int KS>
-constexpr int fp8_pitch() {
-    return KS + 16;
-}
+// LDS layout of a staged FP8 X slice of R rows x KS bytes.  A lane group takes
+// 32 bytes per 128-wide K block (bytes kq*32 .. +31), read as two 16-byte
+// halves; the halves live in two planes [half][row][64 bytes per K block] with
+// a row pitch of KS/2 + 32 bytes, so each ds_read_b128 reads 16-byte chunks at
+// a 32-byte row offset -- the conflict-free pattern on gfx950 (the unsplit
+// layout's 32-byte chunks conflict at every padding tried).
+template <int R, int KS>
+struct Fp8Lds {
+    static constexpr int kPitch = KS / 2 + 32;
+    static constexpr int kBytes = 2 * R * kPitch;
+    // LDS offset of the 16-byte vector c (bytes 16c .. 16c + 15) of staged row `row`
+    __device__ static __forceinline__ int stage_offset(int row, int c) {
+        const int kb = c >> 3, w = c & 7;
+        return (w & 1) * (R * kPitch) + row * kPitch + kb * 64 + (w >> 1) * 16;
+    }
+    // the 32 bytes of K block j for lane group kq of staged row `row`
+    __device__ static __forceinline__ int8v_t read(const uint8_t *xs, int row, int j, int kq) {
+        const uint8_t *p = xs + row * kPitch + j * 64 + kq * 16;
+        const uint4 lo = *reinterpret_cast<const uint4 *>(p);
+        const uint4 hi = *reinterpret_cast<const uint4 *>(p + R * kPitch);
+        int8v_t r;
+        r[0] = static_cast<int>(lo.x);
+        r[1] = static_cast<int>(lo.y);
+        r[2] = static_cast<int>(lo.z);
+        r[3] = static_cast<int>(lo.w);
+        r[4] = static_cast<int>(hi.x);
+        r[5] = static_cast<int>(hi.y);
+        r[6] = static_cast<int>(hi.z);
+        r[7] = static_cast<int>(hi.w);
+        return r;
+    }
+};
 
 // Lane (r16, kq) of a wave holds, for every 128-wide K block j of the slice,
 // bytes j*128 + kq*32 .. +31 of weight row n_row: the same K positions the
@@ -121,8 +147,7 @@ __device__ __forceinline__ void fp8_tile(const int8v_t (&wr)[KS / 128], const ui
         const float swj = swv[j];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const uint8_t *bp = xs + (m * 16 + r16) * fp8_pitch<KS>() + j * 128 + kq * 32;
-            const int8v_t b = *reinterpret_cast<const int8v_t *>(bp);
+            const int8v_t b = Fp8Lds<16 * MT, KS>::read(xs, m * 16 + r16, j, kq);
             const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
             const float s = sxs[j * (16 * MT) + m * 16 + r16] * swj;
@@ -165,7 +190,7 @@ gemm_fp8_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__rest
                 uint16_t *__restrict__ out, int64_t o_s0, float *__restrict__ part) {
     constexpr int kSteps = KS / 128;
     constexpr int kRows = 16 * MT;
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kRows * fp8_pitch<KS>()];
+    __shared__ __attribute__((aligned(16))) uint8_t xs[Fp8Lds<kRows, KS>::kBytes];
     __shared__ float sxs[kSteps * kRows];  // activation scales [K block][row] (a wave's rows on distinct banks)
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -202,11 +227,15 @@ gemm_fp8_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__rest
     fp8_load_w<KS>(wa, w, w_s0, col + r16, k0, kq);
     __builtin_amdgcn_sched_barrier(0);
 
+    // one LDS plane per store (adjacent vectors belong to the two planes, whose starts share banks)
 #pragma unroll
-    for (int q = 0; q < kXVec; ++q) {
-        const int i = threadIdx.x + q * kFp8Threads;
-        const int row = i / kVecPerRow, c = i % kVecPerRow;
-        *reinterpret_cast<uint4 *>(xs + row * fp8_pitch<KS>() + c * 16) = xr[q];
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int q = 0; q < kXVec; ++q) {
+            const int i = threadIdx.x + q * kFp8Threads;
+            const int row = i / kVecPerRow, c = i % kVecPerRow;
+            if ((c & 1) == h) *reinterpret_cast<uint4 *>(xs + Fp8Lds<kRows, KS>::stage_offset(row, c)) = xr[q];
+        }
     }
     __syncthreads();
 
@@ -240,10 +269,10 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
                   uint16_t *__restrict__ out, int64_t o_s0) {
     constexpr int KB = K / 128;                    // K blocks
     constexpr int QS = K / kSwQuarters / 128;      // K blocks per quarter
-    constexpr int P = K + 16;                      // LDS pitch of an X row in bytes
-    __shared__ __attribute__((aligned(16))) uint8_t xs[kSwRows * P];
+    using Lds = Fp8Lds<kSwRows, K>;
+    __shared__ __attribute__((aligned(16))) uint8_t xs[Lds::kBytes];
     __shared__ float sxs[KB * kSwRows];  // [K block][row]: a wave's 16 rows hit 16 banks
-    static_assert((kSwQuarters - 1) * kSwTiles * kWave * 16 * 4 <= kSwRows * P, "reduction fits the X area");
+    static_assert((kSwQuarters - 1) * kSwTiles * kWave * 16 * 4 <= Lds::kBytes, "reduction fits the X area");
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -294,10 +323,16 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
             // element i of the [K block][row] table
             sr[u] = (i < kSx && i % kSwRows < M) ? sx[(i % kSwRows) * sx_s0 + i / kSwRows] : 0.f;
         }
+        // adjacent vectors belong to the two LDS planes (whose starts share banks): each store
+        // writes one plane, so its active lanes fill consecutive 16-byte chunks
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int i = threadIdx.x + u * kSwThreads;
-            if (i < kVec) *reinterpret_cast<uint4 *>(xs + (i / (K / 16)) * P + (i % (K / 16)) * 16) = xr[u];
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int i = threadIdx.x + u * kSwThreads;
+                if (i < kVec && (i & 1) == h)
+                    *reinterpret_cast<uint4 *>(xs + Lds::stage_offset(i / (K / 16), i % (K / 16))) = xr[u];
+            }
         }
 #pragma unroll
         for (int u = 0; u < kSxPer; ++u) {
@@ -316,7 +351,7 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int row = m * 16 + r16;
-            const int8v_t b = *reinterpret_cast<const int8v_t *>(xs + row * P + (kb0 + j) * 128 + kq * 32);
+            const int8v_t b = Lds::read(xs, row, kb0 + j, kq);
             const floatx4_t t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 wr[j], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
             const float sxv = sxs[(kb0 + j) * kSwRows + row];

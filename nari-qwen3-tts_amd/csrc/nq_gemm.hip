@@ -33,11 +33,13 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4 &v) {
     return r;
 }
 
-// LDS row pitch of the staged X block: KS bf16 + 8 bf16 of padding, so the
-// 16 rows one B-operand read touches start on distinct 4-bank groups.
+// LDS row pitch of the staged X block: KS bf16 + 16 bf16 (32 bytes) of
+// padding.  gfx950 serves a ds_read_b128 in lane groups that pair rows of
+// different 16-byte k chunks; with a 32-byte row offset those groups cover
+// every bank once (a 16-byte offset measured 4 conflict cycles per read).
 template <int KS>
 constexpr int x_pitch() {
-    return KS + 8;
+    return KS + 16;
 }
 
 template <int KS>
