@@ -274,6 +274,24 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         int np2 = 1;
         while (np2 < P) np2 <<= 1;
         for (int i = P + tid; i < np2; i += blockDim.x) s_keys[i] = 0xFFFFFFFFu;
+        if (np2 <= kWave) {
+            // up to 64 pieces: one wave sorts them in registers (lane i holds key i), no barriers
+            __syncthreads();
+            if (tid < kWave) {
+                unsigned key = tid < np2 ? s_keys[tid] : 0xFFFFFFFFu;
+                for (int size = 2; size <= np2; size <<= 1) {
+                    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                        const unsigned other = __shfl_xor(key, stride, kWave);
+                        const bool low = (tid & stride) == 0;       // the lower index of the pair
+                        const bool asc = (tid & size) == 0;         // the pair's direction
+                        const unsigned lo = key < other ? key : other, hi = key < other ? other : key;
+                        key = (low == asc) ? lo : hi;
+                    }
+                }
+                if (tid < np2) s_keys[tid] = key;
+            }
+            np2 = 1;  // the LDS network below has nothing left to do
+        }
         for (int size = 2; size <= np2; size <<= 1) {
             for (int stride = size >> 1; stride > 0; stride >>= 1) {
                 __syncthreads();
@@ -370,8 +388,20 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             cand[c] += n > 0 ? n : 1;
         }
     }
+    // wave sums first, then one LDS atomic per wave and candidate (and none for a zero sum: a
+    // decode-only batch adds nothing) -- per-thread 64-bit atomics on five addresses serialize
 #pragma unroll
-    for (int c = 0; c < n_cand; ++c) atomicAdd(&s_cand[c], cand[c]);
+    for (int c = 0; c < n_cand; ++c) {
+        unsigned lo = static_cast<unsigned>(cand[c]), hi = static_cast<unsigned>(cand[c] >> 32);
+        unsigned long long v = cand[c];
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            lo = __shfl_xor(static_cast<unsigned>(v), m, kWave);
+            hi = __shfl_xor(static_cast<unsigned>(v >> 32), m, kWave);
+            v += (static_cast<unsigned long long>(hi) << 32) | lo;
+        }
+        if ((tid & (kWave - 1)) == 0 && v != 0) atomicAdd(&s_cand[c], v);
+    }
     __syncthreads();
     int chosen = -1;
     for (int c = 0; c < n_cand; ++c)
