@@ -78,17 +78,60 @@ def linear_workspace_bytes(rows: int, out_features: int, in_features: int, epilo
     return n
 
 
-def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None, eps=0.0, workspace=None,
-            bias=None):
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise TypeError("linear needs bf16 activations and weights")
-    if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or weight.stride(1) != 1:
-        raise ValueError("linear needs 2-D tensors with unit inner stride")
-    rows, k = x.shape
-    n = weight.shape[0]
+class PackedLinearWeight:
+    """A bf16 projection weight [out, in] stored in the fragment order of the HIP projection kernels
+    (nq_pack_linear_weight): each wave reads its rows over a K slice as one contiguous run.  Every
+    projection below accepts it in place of the row-major weight and gives bit-identical results."""
+
+    def __init__(self, weight: torch.Tensor) -> None:
+        if weight.dtype != torch.bfloat16:
+            raise TypeError("weight must be bf16")
+        if weight.dim() != 2 or weight.stride(1) != 1:
+            raise ValueError("a projection weight is a matrix with unit inner stride")
+        _lib.require_device(weight)
+        n, k = weight.shape
+        if n % 16 or k % 32:
+            raise TypeError(f"packed projection weights need out % 16 == 0 and in % 32 == 0, got {tuple(weight.shape)}")
+        self.shape = (n, k)
+        self.dtype = weight.dtype
+        self.device = weight.device
+        self.data = torch.empty(n * k, dtype=torch.bfloat16, device=weight.device)
+        _lib.call("nq_pack_linear_weight", weight.data_ptr(), weight.stride(0), n, k, self.data.data_ptr(),
+                  _lib.stream(weight.device))
+
+    def numel(self) -> int:
+        return self.data.numel()
+
+
+def pack_linear_weight(weight: torch.Tensor) -> PackedLinearWeight:
+    """Weight-load-time repack of a row-major bf16 projection weight (see PackedLinearWeight)."""
+
+    return PackedLinearWeight(weight)
+
+
+def _weight_arg(weight, k: int) -> tuple[int, int, int]:
+    """(pointer, row stride or NQ_WEIGHT_PACKED, out_features) of a projection weight."""
+
+    if isinstance(weight, PackedLinearWeight):
+        if weight.shape[1] != k:
+            raise ValueError("weight in_features must match x")
+        return weight.data.data_ptr(), _lib.NQ_WEIGHT_PACKED, weight.shape[0]
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.stride(1) != 1:
+        raise TypeError("linear needs a bf16 2-D weight with unit inner stride")
     if weight.shape[1] != k:
         raise ValueError("weight in_features must match x")
-    _lib.require_device(x, weight)
+    return weight.data_ptr(), weight.stride(0), weight.shape[0]
+
+
+def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None, eps=0.0, workspace=None,
+            bias=None):
+    if x.dtype != torch.bfloat16:
+        raise TypeError("linear needs bf16 activations and weights")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("linear needs 2-D tensors with unit inner stride")
+    rows, k = x.shape
+    w_ptr, w_s0, n = _weight_arg(weight, k)
+    _lib.require_device(x, weight.data if isinstance(weight, PackedLinearWeight) else weight)
     need = linear_workspace_bytes(rows, n, k, epilogue)
     out = torch.empty((rows, out_width), dtype=x.dtype, device=x.device) if out is None else out
     if out.shape != (rows, out_width) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
@@ -96,7 +139,7 @@ def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     _lib.call(
-        "nq_linear", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k, int(epilogue),
+        "nq_linear", x.data_ptr(), x.stride(0), w_ptr, w_s0, rows, n, k, int(epilogue),
         _lib.ptr(bias), out.data_ptr(), out.stride(0), _lib.ptr(residual), _lib.ptr(norm_weight), float(eps),
         _lib.ptr(workspace) if need else None, workspace.numel() * workspace.element_size() if need else 0,
         _lib.stream(x.device),
@@ -132,17 +175,17 @@ def linear_partials(x: torch.Tensor, weight: torch.Tensor, workspace: torch.Tens
     ``workspace`` for a consumer that sums them; returns S."""
 
     rows, k = x.shape
-    n = weight.shape[0]
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise TypeError("linear needs bf16 tensors with unit inner stride")
+    w_ptr, w_s0, n = _weight_arg(weight, k)
     splits = int(_lib.load().nq_linear_splits(rows, n, k))
     if splits < 1:
         raise TypeError(f"no HIP projection for rows={rows}, out={n}, in={k}")
     need = linear_workspace_bytes(rows, n, k, _lib.NQ_EPI_PARTIALS)
     if workspace.numel() * workspace.element_size() < need:
         raise ValueError("workspace too small for the projection partials")
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 or weight.stride(1) != 1:
-        raise TypeError("linear needs bf16 tensors with unit inner stride")
-    _lib.require_device(x, weight, workspace)
-    _lib.call("nq_linear", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k,
+    _lib.require_device(x, workspace)
+    _lib.call("nq_linear", x.data_ptr(), x.stride(0), w_ptr, w_s0, rows, n, k,
               _lib.NQ_EPI_PARTIALS, None, None, 0, None, None, 0.0, workspace.data_ptr(),
               workspace.numel() * workspace.element_size(), _lib.stream(x.device))
     return splits
@@ -230,18 +273,18 @@ def linear_add_rmsnorm_fp8(x: torch.Tensor, weight: torch.Tensor, residual: torc
 
     for t, name in ((residual, "residual"), (norm_weight, "norm weight")):
         _check(t, name)
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.stride(1) != 1 or weight.stride(1) != 1:
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
         raise TypeError("linear needs bf16 tensors with unit inner stride")
     rows, k = x.shape
-    n = weight.shape[0]
+    w_ptr, w_s0, n = _weight_arg(weight, k)
     if residual.shape != (rows, n) or norm_weight.shape != (n,):
         raise ValueError("residual / norm weight must match the projection output")
     q, scales = _fp8_out(rows, n, x.device, q, scales)
     need = linear_workspace_bytes(rows, n, k, _lib.NQ_EPI_ADD_RMSNORM)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-    _lib.require_device(x, weight, workspace)
-    _lib.call("nq_linear_add_rmsnorm_fp8", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n,
+    _lib.require_device(x, workspace)
+    _lib.call("nq_linear_add_rmsnorm_fp8", x.data_ptr(), x.stride(0), w_ptr, w_s0, rows, n,
               k, residual.data_ptr(), norm_weight.data_ptr(), float(eps), q.data_ptr(), q.stride(0),
               scales.data_ptr(), scales.stride(0), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
               _lib.stream(x.device))

@@ -152,3 +152,68 @@ def test_linear_bias_single_rounding(nq, device, m, n, k):
     torch.cuda.synchronize()
     ref = _reference(x, w) + b.float()
     assert bool(((y.float() - ref).abs() <= 8e-3 * ref.abs() + 2e-3).all())
+
+
+_PACKED_OFF = pytest.mark.skip(reason="packed projection weights are switched off: the GPU run that exercised them ended in a device fault whose cause is not found (index arithmetic emulated in bounds)")
+
+
+@_PACKED_OFF
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_packed_weights_give_identical_results(nq, device, m, n, k):
+    from nari_qwen3_tts_amd.layers import linear, pack_linear_weight
+
+    g = torch.Generator(device=device)
+    g.manual_seed(m * 11 + n + 3 * k)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    packed = pack_linear_weight(w)
+    # the layout: fragment (row group, 32-k step), lane (k group, row) of 8 consecutive k
+    want = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(packed.data, want)
+    # the same lanes see the same operands in the same order: bit-identical products
+    assert torch.equal(linear(x, packed), linear(x, w))
+
+
+@_PACKED_OFF
+def test_packed_weights_in_fused_epilogues(nq, device):
+    from nari_qwen3_tts_amd.layers import (
+        linear_add_rmsnorm, linear_add_rmsnorm_fp8, linear_partials, linear_workspace_bytes, pack_linear_weight,
+    )
+    from nari_qwen3_tts_amd import _lib
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    m, n, k = 64, 2048, 6144
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    # a weight view with a row stride wider than K packs like its contiguous copy
+    wide = (torch.randn(n, k + 64, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    w = wide[:, :k]
+    packed = pack_linear_weight(w)
+    assert torch.equal(packed.data, pack_linear_weight(w.contiguous()).data)
+    res = torch.randn(m, n, generator=g, device=device).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(n, generator=g, device=device)).to(torch.bfloat16)
+    ws = torch.empty(linear_workspace_bytes(m, n, k, _lib.NQ_EPI_ADD_RMSNORM), dtype=torch.uint8, device=device)
+    ws2 = torch.empty_like(ws)
+    s1 = linear_partials(x, w, ws)
+    s2 = linear_partials(x, packed, ws2)
+    assert s1 == s2 and torch.equal(ws, ws2)
+    outs = []
+    for weight in (w, packed):
+        r = res.clone()
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+        linear_add_rmsnorm(x, weight, r, nw, 1e-6, out, ws)
+        r8 = res.clone()
+        q, sc = linear_add_rmsnorm_fp8(x, weight, r8, nw, 1e-6, None, None, ws)
+        outs.append((r, out, r8, q.view(torch.uint8).clone(), sc.clone()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@_PACKED_OFF
+def test_pack_rejects_unsupported_shapes(nq, device):
+    from nari_qwen3_tts_amd.layers import pack_linear_weight
+
+    with pytest.raises(TypeError):
+        pack_linear_weight(torch.zeros(24, 64, dtype=torch.bfloat16, device=device))
+    with pytest.raises(TypeError):
+        pack_linear_weight(torch.zeros(32, 48, dtype=torch.bfloat16, device=device))
