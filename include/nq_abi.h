@@ -80,12 +80,17 @@ int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start, const int32
  * into chunks whose size the plan picks on the GPU from the total work.
  * Writes into `workspace` (size from nq_attention_workspace_bytes for the same
  * maxima).  max_pages bounds the pages of all rows together (the length of
- * kv_indices).
+ * kv_indices).  position_ids / write_pages / write_offsets ([max_query_tokens]
+ * int64, the RoPE positions and K/V write slots of the same metadata) may be
+ * NULL; nq_paged_decode_rope_attention needs a plan that was given them (it
+ * reads each decode row's position and write slot from the plan).
  */
 int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pages, int page_size,
                                      int num_qo_heads, int num_kv_heads, int head_dim);
 int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
-                      const int32_t *last_page_len, const int32_t *kv_indices, int n_rows,
+                      const int32_t *last_page_len, const int32_t *kv_indices,
+                      const int64_t *position_ids, const int64_t *write_pages,
+                      const int64_t *write_offsets, int n_rows,
                       int max_query_tokens, int max_pages, int page_size, int num_qo_heads,
                       int num_kv_heads, int head_dim, void *workspace, int64_t workspace_bytes,
                       void *stream);
@@ -279,16 +284,19 @@ int nq_pack_linear_weight(const uint16_t *w, int64_t w_s0, int N, int K, uint16_
  * Decode attention with the q/k norm + RoPE + K/V write fused in, for bindings
  * whose rows are all decode rows: the work of nq_qkv_partials_norm_rope_kv_write
  * (from the packed QKV projection's split-K planes [splits, tokens, (Hq + 2 Hkv)
- * D]) followed by nq_paged_attention with NQ_ATTN_DECODE, in one kernel plus a
- * merge launch that only works when a row had to be split across workgroups
- * (the TalkerAttentionContext.attend path, executor/talker_kv.py:104-129 with
+ * D]) followed by nq_paged_attention with NQ_ATTN_DECODE, in one kernel (the
+ * TalkerAttentionContext.attend path, executor/talker_kv.py:104-129 with
  * model/kernels.py:15-91, for decode bindings).  Uses the plan of
  * nq_attention_plan: rows are dealt whole to 256 workgroups (sorted by length,
- * snake order; rows longer than a workgroup's share are cut), so partial
- * results merge inside a workgroup.  The rotated q is not stored (attend returns
- * the attention output only).  head_dim 128 with 1 or 2 query heads per kv
- * head; other shapes return NQ_ERR_UNSUPPORTED and the caller runs the two
- * entry points it replaces.
+ * snake order; rows longer than a workgroup's share are cut, and the last
+ * arriving piece of a cut row merges it), so partial results merge inside a
+ * workgroup.  Each decode row's position and K/V write slot come from the
+ * plan, which must have been given the same positions / write_pages /
+ * write_offsets as this call (a plan without them makes every K/V write
+ * invalid: status NQ_ERR_INVALID_ARGUMENT).  The rotated q is not stored
+ * (attend returns the attention output only).  head_dim 128 with 1 or 2 query
+ * heads per kv head; other shapes return NQ_ERR_UNSUPPORTED and the caller runs
+ * the two entry points it replaces.
  */
 int nq_paged_decode_rope_attention(const float *partials, int splits, int tokens, const uint16_t *q_weight,
                                    const uint16_t *k_weight, const int64_t *positions, float eps,

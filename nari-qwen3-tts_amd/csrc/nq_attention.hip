@@ -116,7 +116,7 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     L.spart_o = off;      off = align256(off + L.max_slots * G * D * 4);
     L.ptiles = off;       off = align256(off + L.max_ptiles * 16);
     L.pieces = off;       off = align256(off + L.max_pieces * 16);
-    L.bins = off;         off = align256(off + (L.max_pieces + bins_per_head(Hkv)) * 4);
+    L.bins = off;         off = align256(off + static_cast<int64_t>(bins_per_head(Hkv)) * kBinMaxSlots * 48);
     L.piece_ml = off;     off = align256(off + L.max_pieces * Hq * 2 * 4);
     L.piece_o = off;      off = align256(off + L.max_pieces * Hq * D * 4);
     L.arrivals = off;     off = align256(off + static_cast<int64_t>(T) * Hkv * 4);
@@ -169,9 +169,10 @@ __device__ __forceinline__ int find_le(const int *off, int n, int x) {
 __global__ void __launch_bounds__(kPlanThreads)
 attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__restrict__ kv_indptr,
                       const int32_t *__restrict__ last_page_len,
-                      const int32_t *__restrict__ kv_indices, int n_rows, int max_queries,
-                      int index_limit, int page_size, int num_kv_heads, char *__restrict__ ws,
-                      PlanLayout L) {
+                      const int32_t *__restrict__ kv_indices, const int64_t *__restrict__ position_ids,
+                      const int64_t *__restrict__ write_pages, const int64_t *__restrict__ write_offsets,
+                      int n_rows, int max_queries, int index_limit, int page_size, int num_kv_heads,
+                      char *__restrict__ ws, PlanLayout L) {
     __shared__ int s_qo[kPlanThreads + 1];
     __shared__ int s_kvlen[kPlanThreads];
     __shared__ int s_base[kPlanThreads];
@@ -180,6 +181,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     __shared__ unsigned long long s_cand[8];
     __shared__ int s_tmp[kWave + 1];
     __shared__ unsigned s_keys[kBinSortCap];
+    __shared__ int4 s_pa[kBinSortCap], s_pb[kBinSortCap];
 
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
     int32_t *chunk_indptr = reinterpret_cast<int32_t *>(ws + L.chunk_indptr);
@@ -246,8 +248,14 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     // (descending, then piece id) and dealt to the bins in snake order
     // (0, 1, .., NB-1, NB-1, .., 0, ..), which evens the bins' loads.  Piece
     // descriptor: {decode row, first block, block count, (first piece << 9) | k
-    // for a split row, else -1}; bin table [NB][slots] of piece ids (-1 empty).
-    // The split rows' arrival counters (decode row x kv head) start at zero.
+    // for a split row, else -1}.  Bin table [NB][kBinMaxSlots] of three int4
+    // each: the piece, {query token, position, write page, write offset |
+    // (last piece of its row) << 31} (what the fused decode kernel's q/k
+    // RoPE and K/V write need, so its prologue reads one row of this table
+    // instead of chasing ids), and {piece id or -1 for an empty slot}.  A
+    // missing or out-of-range position / write slot stores write page -1,
+    // which the fused kernel reports.  The split rows' arrival counters
+    // (decode row x kv head) start at zero.
     if (lead) {
         const int NB = bins_per_head(num_kv_heads);
         const int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
@@ -264,10 +272,26 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         int32_t *arrivals = reinterpret_cast<int32_t *>(ws + L.arrivals);
         for (int i = tid; i < n_dec * num_kv_heads; i += blockDim.x) arrivals[i] = 0;
         int4 *pieces = reinterpret_cast<int4 *>(ws + L.pieces);
+        int4 rope = make_int4(0, 0, -1, 0);
+        if (k > 0) {
+            const int tok = s_qo[tid];
+            rope.x = tok;
+            if (position_ids && write_pages && write_offsets) {
+                const int64_t pos = position_ids[tok], pg = write_pages[tok], off = write_offsets[tok];
+                const bool ok = pos >= 0 && pos <= 0x7fffffff && pg >= 0 && pg <= 0x7fffffff && off >= 0 &&
+                                off <= 0x7fffffff;
+                rope = make_int4(tok, ok ? static_cast<int>(pos) : 0, ok ? static_cast<int>(pg) : -1,
+                                 ok ? static_cast<int>(off) : 0);
+            }
+        }
         for (int i = 0; i < k; ++i) {
             const int first = boff + static_cast<int>(static_cast<int64_t>(i) * nblk / k);
             const int last = boff + static_cast<int>(static_cast<int64_t>(i + 1) * nblk / k);
-            pieces[p0 + i] = make_int4(dec_idx, first, last - first, k > 1 ? (p0 << 9) | k : -1);
+            const int4 pc = make_int4(dec_idx, first, last - first, k > 1 ? (p0 << 9) | k : -1);
+            pieces[p0 + i] = pc;
+            s_pa[p0 + i] = pc;  // p0 + i < P <= kBinSortCap (checked above)
+            s_pb[p0 + i] = make_int4(rope.x, rope.y, rope.z,
+                                     static_cast<int>(static_cast<unsigned>(rope.w) | (i == k - 1 ? 0x80000000u : 0u)));
             const unsigned cnt = static_cast<unsigned>(last - first) > 0xFFFFu ? 0xFFFFu : static_cast<unsigned>(last - first);
             s_keys[p0 + i] = ((0xFFFFu - cnt) << 16) | static_cast<unsigned>(p0 + i);
         }
@@ -307,11 +331,14 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             }
         }
         __syncthreads();
-        int32_t *bins = reinterpret_cast<int32_t *>(ws + L.bins);
-        for (int e = tid; e < NB * slots; e += blockDim.x) {
-            const int bin = e / slots, round = e % slots;
+        int4 *table = reinterpret_cast<int4 *>(ws + L.bins);
+        for (int e = tid; e < NB * kBinMaxSlots; e += blockDim.x) {
+            const int bin = e / kBinMaxSlots, round = e % kBinMaxSlots;
             const int i = round * NB + ((round & 1) ? NB - 1 - bin : bin);
-            bins[e] = i < P ? static_cast<int>(s_keys[i] & 0xFFFFu) : -1;
+            const int pid = round < slots && i < P ? static_cast<int>(s_keys[i] & 0xFFFFu) : -1;
+            table[3 * e] = pid >= 0 ? s_pa[pid] : make_int4(-1, 0, 0, -1);
+            table[3 * e + 1] = pid >= 0 ? s_pb[pid] : make_int4(0, 0, -1, 0);
+            table[3 * e + 2] = make_int4(pid, 0, 0, 0);
         }
         if (tid == 0) {
             meta[kMetaPieces] = P;
@@ -1020,6 +1047,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     constexpr int kPart = BinPart<D, G>::kFloats;
     constexpr int HALF = D / 2;
     __shared__ int4 s_piece[kBinMaxSlots];
+    __shared__ int4 s_rope[kBinMaxSlots];  // {query token, position, write page, write offset | last << 31}
     __shared__ int s_pid[kBinMaxSlots];
     __shared__ int s_start[kBinMaxSlots + 1];
     __shared__ int s_n;
@@ -1027,21 +1055,28 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     __shared__ __attribute__((aligned(16))) float s_part[kBinWaves * 2 * kPart];
 
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
-    if (meta[kMetaStatus] != NQ_OK) {
-        if (blockIdx.x == 0 && threadIdx.x == 0 && status) atomicExch(status, meta[kMetaStatus]);
-        return;
-    }
     const int NB = bins_per_head(num_kv_heads);
     const int bin = blockIdx.x / num_kv_heads, h = blockIdx.x - (blockIdx.x / num_kv_heads) * num_kv_heads;
-    const int slots = meta[kMetaBinSlots];
-    if (bin >= NB || slots <= 0) return;
+    if (bin >= NB) return;
+    // one round trip: the plan's status and slot count, and this bin's table row
+    // (fixed stride, so its address does not wait for either)
+    const int4 *table = reinterpret_cast<const int4 *>(ws + L.bins) + static_cast<int64_t>(bin) * kBinMaxSlots * 3;
+    int4 t_piece = make_int4(-1, 0, 0, -1), t_rope = make_int4(0, 0, -1, 0), t_id = make_int4(-1, 0, 0, 0);
+    if (threadIdx.x < kBinMaxSlots) {
+        t_piece = table[3 * threadIdx.x];
+        t_rope = table[3 * threadIdx.x + 1];
+        t_id = table[3 * threadIdx.x + 2];
+    }
+    const int plan_status = meta[kMetaStatus], slots = meta[kMetaBinSlots];
+    if (plan_status != NQ_OK) {
+        if (blockIdx.x == 0 && threadIdx.x == 0 && status) atomicExch(status, plan_status);
+        return;
+    }
+    if (slots <= 0) return;
     if (slots > kBinMaxSlots) {
         if (threadIdx.x == 0 && status) atomicExch(status, NQ_ERR_CAPACITY);
         return;
     }
-    const int4 *pieces = reinterpret_cast<const int4 *>(ws + L.pieces);
-    const int32_t *bins = reinterpret_cast<const int32_t *>(ws + L.bins);
-    const int4 *dec_rows = reinterpret_cast<const int4 *>(ws + L.dec_rows);
     const int4 *blocks = reinterpret_cast<const int4 *>(ws + L.blocks);
     float *piece_ml = reinterpret_cast<float *>(ws + L.piece_ml);
     float *piece_o = reinterpret_cast<float *>(ws + L.piece_o);
@@ -1050,9 +1085,9 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
 
     // the bin's pieces (empty slots come last) and their block offsets
     if (threadIdx.x < slots) {
-        const int pid = bins[bin * slots + threadIdx.x];
-        s_pid[threadIdx.x] = pid;
-        s_piece[threadIdx.x] = pid >= 0 ? pieces[pid] : make_int4(-1, 0, 0, -1);
+        s_pid[threadIdx.x] = t_id.x;
+        s_piece[threadIdx.x] = t_piece;
+        s_rope[threadIdx.x] = t_rope;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1077,14 +1112,27 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     const int wave = threadIdx.x / kWave;
     bool bad = false;
 
+    // the wave's span of the bin's blocks and its first 64 block descriptors
+    // (one per lane: lane -> bin-local block -> global block), fetched now so
+    // that they arrive during the RoPE work below
+    const int s0 = span_start(wave, NBB, kBinWaves);
+    const int s1 = span_start(wave + 1, NBB, kBinWaves);
+    auto global_block = [&](int lb) {
+        int sl = 0;
+        while (sl + 1 < nslots && s_start[sl + 1] <= lb) ++sl;
+        return s_piece[sl].y + lb - s_start[sl];
+    };
+    int win = s0;
+    int4 dwin = make_int4(-1, 0, 0, 0);
+    if (s0 + lane < s1) dwin = blocks[global_block(s0 + lane)];
+
     // 1. q/k norm + RoPE + K/V write for the bin's rows (one wave per head unit)
     for (int u = wave; u < nslots * (G + 2); u += kBinWaves) {
         const int sl = u / (G + 2), kind = u - sl * (G + 2);
-        const int4 pc = s_piece[sl];
-        const int4 dr = dec_rows[pc.x];
-        const bool row_last = pc.y + pc.z == dr.z + dr.w;
+        const int4 rp = s_rope[sl];
+        const bool row_last = rp.w < 0;
         if (kind >= G && !row_last) continue;  // the row's new K/V belong to its last piece
-        const int64_t tok = dr.y;
+        const int64_t tok = rp.x;
         if (tok >= rs.tokens) {  // a query beyond the projection's rows
             bad = true;
             continue;
@@ -1101,7 +1149,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
             x1 = bf16_to_f32(f32_to_bf16(x1));
             x2 = bf16_to_f32(f32_to_bf16(x2));
         }
-        const int64_t page = rs.write_pages[tok], woff = rs.write_offsets[tok];
+        const int64_t page = rp.z, woff = rp.w & 0x7fffffff;
         const bool slot_ok = static_cast<uint64_t>(page) < static_cast<uint64_t>(num_pages) &&
                              static_cast<uint64_t>(woff) < (static_cast<uint64_t>(1) << ps_log2);
         if (kind >= G && !slot_ok) {
@@ -1118,7 +1166,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         }
         uint16_t o1 = 0, o2 = 0;
         norm_rope_pair<D>(x1, x2, on, kind < G ? rs.q_weight : rs.k_weight, lane, rs.eps, rs.log_theta,
-                          static_cast<float>(rs.positions[tok]), rs.round_to_input, o1, o2);
+                          static_cast<float>(rp.y), rs.round_to_input, o1, o2);
         if (!on) continue;
         if (kind < G) {
             s_q[(sl * G + kind) * D + lane] = o1;
@@ -1133,18 +1181,8 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     // 2. stream the wave's span of the bin's blocks
     const int g = lane / LN::LPT;
     const int sub = lane % LN::LPT;
-    const int s0 = span_start(wave, NBB, kBinWaves);
-    const int s1 = span_start(wave + 1, NBB, kBinWaves);
     if (s0 < s1) {
-        // descriptors of the span, 64 at a time, one per lane (lane -> bin-local block -> global block)
-        auto global_block = [&](int lb) {
-            int sl = 0;
-            while (sl + 1 < nslots && s_start[sl + 1] <= lb) ++sl;
-            return s_piece[sl].y + lb - s_start[sl];
-        };
-        int win = s0;
-        int4 dwin = make_int4(-1, 0, 0, 0);
-        if (s0 + lane < s1) dwin = blocks[global_block(s0 + lane)];
+        // further descriptors of the span, 64 at a time
         auto desc_of = [&](int w) {
             if (w - win >= kWave) {
                 win += kWave;
@@ -1163,7 +1201,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
             const bool whole = s_start[sl] >= s0 && s_start[sl + 1] <= s1;
             if (whole) {
                 const int4 pc = s_piece[sl];
-                const int query = dec_rows[pc.x].y;
+                const int query = s_rope[sl].x;
                 if (g == 0) {
 #pragma unroll
                     for (int j = 0; j < G; ++j) {
@@ -1218,7 +1256,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         const int w0 = span_of(a, NBB, kBinWaves), w1 = span_of(b - 1, NBB, kBinWaves);
         if (w0 == w1) continue;  // finished by its wave
         const int4 pc = s_piece[sl];
-        const int query = dec_rows[pc.x].y;
+        const int query = s_rope[sl].x;
         for (int grp = 0; grp < NG; ++grp) {
             const int e0 = (grp * kWave + lane) * V;
             const int jj = e0 / D;
@@ -1750,6 +1788,8 @@ extern "C" int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pa
 
 extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
                                  const int32_t *last_page_len, const int32_t *kv_indices,
+                                 const int64_t *position_ids, const int64_t *write_pages,
+                                 const int64_t *write_offsets,
                                  int n_rows, int max_query_tokens, int max_pages, int page_size,
                                  int num_qo_heads, int num_kv_heads, int head_dim, void *workspace,
                                  int64_t workspace_bytes, void *stream) {
@@ -1764,8 +1804,8 @@ extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_ind
     NQ_CHECK_ARG(workspace_bytes >= L.total);
     hipLaunchKernelGGL(nq::attention_plan_kernel, dim3(nq::kPlanGrid), dim3(nq::kPlanThreads), 0,
                        static_cast<hipStream_t>(stream), qo_indptr, kv_indptr, last_page_len,
-                       kv_indices, n_rows, max_query_tokens, max_pages, page_size, num_kv_heads,
-                       static_cast<char *>(workspace), L);
+                       kv_indices, position_ids, write_pages, write_offsets, n_rows, max_query_tokens,
+                       max_pages, page_size, num_kv_heads, static_cast<char *>(workspace), L);
     return NQ_LAUNCH_STATUS();
 }
 

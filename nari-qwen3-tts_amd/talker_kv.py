@@ -150,6 +150,9 @@ class _HipBindingBase:
             _lib.ptr(b.kv_indptr),
             _lib.ptr(b.last_page_len),
             _lib.ptr(b.kv_indices),
+            _lib.ptr(b.position_ids),
+            _lib.ptr(b.write_pages),
+            _lib.ptr(b.write_offsets),
             self.capture_batch_size,
             self.token_capacity,
             self.index_capacity,
