@@ -261,6 +261,7 @@ constexpr int kSwQuarters = 4;
 constexpr int kSwThreads = kSwTiles * kSwQuarters * kWave;
 constexpr int kSwK = 2048;
 constexpr int kSwRows = 64;
+static_assert(kSwRows / 16 == kSwQuarters, "the wave of quarter q finishes 16-row tile q");
 
 template <int K>
 __global__ void __launch_bounds__(kSwThreads)
@@ -272,7 +273,7 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
     using Lds = Fp8Lds<kSwRows, K>;
     __shared__ __attribute__((aligned(16))) uint8_t xs[Lds::kBytes];
     __shared__ float sxs[KB * kSwRows];  // [K block][row]: a wave's 16 rows hit 16 banks
-    static_assert((kSwQuarters - 1) * kSwTiles * kWave * 16 * 4 <= Lds::kBytes, "reduction fits the X area");
+    static_assert(kSwQuarters * kSwTiles * kWave * 16 * 4 <= Lds::kBytes, "reduction fits the X area");
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -283,7 +284,35 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
     const int tile = blockIdx.x * kSwTiles + tl;
     const int kb0 = quarter * QS;
 
-    // 1. the wave's weights (16 packed rows over its K quarter) and scales:
+    // 1. the activation block and its scales (rows >= M zero), issued first:
+    // loads complete in issue order, so the wait for them below leaves the
+    // weights in flight and the X block reaches LDS long before the weights
+    constexpr int kVec = kSwRows * (K / 16);
+    constexpr int kPer = (kVec + kSwThreads - 1) / kSwThreads;
+    constexpr int kSx = kSwRows * KB;
+    constexpr int kSxPer = (kSx + kSwThreads - 1) / kSwThreads;
+    // Every workgroup reads the same block: each starts at its own (even)
+    // rotation of it, so the CUs of an XCD do not all ask the same L2 lines
+    // at the same moment.  Vector i of the thread is block vector rot(i).
+    const int rot = (blockIdx.x * 258) % kVec;
+    auto rot_of = [&](int i) { return i + rot < kVec ? i + rot : i + rot - kVec; };
+    uint4 xr[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = threadIdx.x + u * kSwThreads;
+        const int v = rot_of(i);
+        const int row = v / (K / 16), c = v % (K / 16);
+        xr[u] = (i < kVec && row < M) ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + c * 16)
+                                      : make_uint4(0, 0, 0, 0);
+    }
+    float sr[kSxPer];
+#pragma unroll
+    for (int u = 0; u < kSxPer; ++u) {
+        const int i = threadIdx.x + u * kSwThreads;
+        // element i of the [K block][row] table
+        sr[u] = (i < kSx && i % kSwRows < M) ? sx[(i % kSwRows) * sx_s0 + i / kSwRows] : 0.f;
+    }
+    // 2. the wave's weights (16 packed rows over its K quarter) and scales:
     // gate rows 8t.. lie in 128-row block t / 16, up rows in (I + 8t) / 128
     int8v_t wr[QS];
     {
@@ -301,28 +330,9 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
             swu[j] = u[j];
         }
     }
-    // 2. the activation block and its scales into LDS (rows >= M zero): every
-    // load of the thread is issued before the first LDS store
-    constexpr int kVec = kSwRows * (K / 16);
-    constexpr int kPer = (kVec + kSwThreads - 1) / kSwThreads;
-    constexpr int kSx = kSwRows * KB;
-    constexpr int kSxPer = (kSx + kSwThreads - 1) / kSwThreads;
+    // keep every weight load ahead of the wait for the X block
+    __builtin_amdgcn_sched_barrier(0);
     {
-        uint4 xr[kPer];
-#pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int i = threadIdx.x + u * kSwThreads;
-            const int row = i / (K / 16), c = i % (K / 16);
-            xr[u] = (i < kVec && row < M) ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + c * 16)
-                                          : make_uint4(0, 0, 0, 0);
-        }
-        float sr[kSxPer];
-#pragma unroll
-        for (int u = 0; u < kSxPer; ++u) {
-            const int i = threadIdx.x + u * kSwThreads;
-            // element i of the [K block][row] table
-            sr[u] = (i < kSx && i % kSwRows < M) ? sx[(i % kSwRows) * sx_s0 + i / kSwRows] : 0.f;
-        }
         // adjacent vectors belong to the two LDS planes (whose starts share banks): each store
         // writes one plane, so its active lanes fill consecutive 16-byte chunks
 #pragma unroll
@@ -330,8 +340,9 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
 #pragma unroll
             for (int u = 0; u < kPer; ++u) {
                 const int i = threadIdx.x + u * kSwThreads;
+                const int v = rot_of(i);  // same parity as i: rot is even
                 if (i < kVec && (i & 1) == h)
-                    *reinterpret_cast<uint4 *>(xs + Lds::stage_offset(i / (K / 16), i % (K / 16))) = xr[u];
+                    *reinterpret_cast<uint4 *>(xs + Lds::stage_offset(v / (K / 16), v % (K / 16))) = xr[u];
             }
         }
 #pragma unroll
@@ -368,41 +379,46 @@ fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__re
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // 4. quarters 1.. hand their sums to quarter 0 through the (now free) X area
+    // 4. every quarter wave hands its sums over through the (now free) X area;
+    // the wave of quarter q then finishes 16-row tile m = q of its column tile,
+    // adding the quarters in order 0, 1, 2, 3
     __syncthreads();
     float *red = reinterpret_cast<float *>(xs);
-    // layout [quarter - 1][tile][m][lane][4]: a float4 access touches 64 consecutive float4s
-    if (quarter > 0) {
-        float *dst = red + (((quarter - 1) * kSwTiles + tl) * 4 * kWave + lane) * 4;
+    // layout [quarter][tile][m][lane][4]: a float4 access touches 64 consecutive float4s
+    {
+        float *dst = red + ((quarter * kSwTiles + tl) * 4 * kWave + lane) * 4;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
             *reinterpret_cast<float4 *>(dst + m * kWave * 4) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
     }
     __syncthreads();
-    if (quarter != 0) return;
+    const int m = quarter;
+    float sum[4];
+    {
+        const float4 v0 = *reinterpret_cast<const float4 *>(red + ((tl * 4 + m) * kWave + lane) * 4);
+        sum[0] = v0.x;
+        sum[1] = v0.y;
+        sum[2] = v0.z;
+        sum[3] = v0.w;
+    }
 #pragma unroll
     for (int q = 1; q < kSwQuarters; ++q) {
-        const float *src = red + (((q - 1) * kSwTiles + tl) * 4 * kWave + lane) * 4;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + m * kWave * 4);
-            acc[m][0] += v.x;
-            acc[m][1] += v.y;
-            acc[m][2] += v.z;
-            acc[m][3] += v.w;
-        }
+        const float4 v = *reinterpret_cast<const float4 *>(red + (((q * kSwTiles + tl) * 4 + m) * kWave + lane) * 4);
+        sum[0] += v.x;
+        sum[1] += v.y;
+        sum[2] += v.z;
+        sum[3] += v.w;
     }
     // 5. SwiGLU of the bf16 projection values: act columns 8t + 2kq + {0, 1}
     const int col = tile * 8 + kq * 2;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    {
         const int row = m * 16 + r16;
-        if (row >= M) continue;
+        if (row >= M) return;
         float a[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const float g = bf16_to_f32(f32_to_bf16(acc[m][e]));
-            const float u = bf16_to_f32(f32_to_bf16(acc[m][2 + e]));
+            const float g = bf16_to_f32(f32_to_bf16(sum[e]));
+            const float u = bf16_to_f32(f32_to_bf16(sum[2 + e]));
             a[e] = g / (1.0f + expf(-g)) * u;
         }
         *reinterpret_cast<uint32_t *>(out + row * o_s0 + col) = pack2_bf16(a[0], a[1]);

@@ -129,11 +129,16 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     constexpr int kVecPerRow = KS / 8;
     constexpr int kXVec = kRows * kVecPerRow / kGemmThreads;
     static_assert(kRows * kVecPerRow % kGemmThreads == 0, "X block splits evenly over the threads");
+    // The workgroups of one K slice all read this block: each starts at its own
+    // rotation of it, so that they do not ask the same L2 lines at once.
+    constexpr int kXTotal = kRows * kVecPerRow;
+    const int rot = static_cast<int>((blockIdx.x * 66u) % kXTotal);
+    auto rot_of = [&](int i) { return i + rot < kXTotal ? i + rot : i + rot - kXTotal; };
     uint4 xr[kXVec];
 #pragma unroll
     for (int q = 0; q < kXVec; ++q) {
-        const int i = threadIdx.x + q * kGemmThreads;
-        const int row = i / kVecPerRow, col = i % kVecPerRow;
+        const int v = rot_of(threadIdx.x + q * kGemmThreads);
+        const int row = v / kVecPerRow, col = v % kVecPerRow;
         xr[q] = row < M ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + k0 + col * 8) : make_uint4(0, 0, 0, 0);
     }
 
@@ -145,8 +150,8 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
 
 #pragma unroll
     for (int q = 0; q < kXVec; ++q) {
-        const int i = threadIdx.x + q * kGemmThreads;
-        const int row = i / kVecPerRow, col = i % kVecPerRow;
+        const int v = rot_of(threadIdx.x + q * kGemmThreads);
+        const int row = v / kVecPerRow, col = v % kVecPerRow;
         *reinterpret_cast<uint4 *>(xs + row * x_pitch<KS>() + col * 8) = xr[q];
     }
     __syncthreads();
