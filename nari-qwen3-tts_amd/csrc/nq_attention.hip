@@ -1053,6 +1053,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     __shared__ int s_n;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[kBinMaxSlots * G * D];
     __shared__ __attribute__((aligned(16))) float s_part[kBinWaves * 2 * kPart];
+    __shared__ int s_wsp[kBinWaves + 1];  // wave span starts
 
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
     const int NB = bins_per_head(num_kv_heads);
@@ -1107,6 +1108,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     const int nslots = s_n;
     const int NBB = s_start[nslots];
     if (NBB == 0) return;
+    if (threadIdx.x <= kBinWaves) s_wsp[threadIdx.x] = span_start(threadIdx.x, NBB, kBinWaves);
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -1246,36 +1248,66 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
     __syncthreads();
 
-    // 3. pieces shared by several waves: merge their LDS partials in wave order
+    // 3. pieces shared by several waves: merge their LDS partials.  All
+    // contributors' maxima are read at once and the row maximum taken first,
+    // then every (l, o) is read independently and added with its scale in
+    // wave order, so the merge costs a few LDS round trips instead of one
+    // chain per contributor (and stays deterministic).
     constexpr int EPL = G * D / kWave;
     constexpr int V = EPL < 4 ? EPL : 4;
     constexpr int NG = EPL / V;
+    // wave span starts in registers; the wave whose span holds bin-local block b
+    // is the number of later span starts <= b (they never decrease)
+    int wsp[kBinWaves + 1];
+#pragma unroll
+    for (int w = 0; w <= kBinWaves; ++w) wsp[w] = s_wsp[w];
+    auto wave_of = [&](int b) {
+        int w = 0;
+#pragma unroll
+        for (int i = 1; i < kBinWaves; ++i) w += wsp[i] <= b ? 1 : 0;
+        return w;
+    };
     for (int sl = wave; sl < nslots; sl += kBinWaves) {
         const int a = s_start[sl], b = s_start[sl + 1];
         if (a == b) continue;
-        const int w0 = span_of(a, NBB, kBinWaves), w1 = span_of(b - 1, NBB, kBinWaves);
+        const int w0 = wave_of(a), w1 = wave_of(b - 1);
         if (w0 == w1) continue;  // finished by its wave
         const int4 pc = s_piece[sl];
         const int query = s_rope[sl].x;
         for (int grp = 0; grp < NG; ++grp) {
             const int e0 = (grp * kWave + lane) * V;
             const int jj = e0 / D;
-            float mx = -INFINITY, ls = 0.f, os[V];
+            // wave w contributes when w0 <= w <= w1 and its span is not empty (bins
+            // of < 16 blocks); its partial of this piece is its first slot when the
+            // piece starts in its span, else its second.  Every slot read stays
+            // inside s_part; a non-contributor's value (its slot may never have
+            // been written) is dropped by a select, never multiplied in.
+            float mk[kBinWaves];
+            int base[kBinWaves];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kBinWaves; ++w) {
+                const bool on = w >= w0 && w <= w1 && wsp[w] != wsp[w + 1];
+                base[w] = (w * 2 + (a > wsp[w] ? 1 : 0)) * kPart;
+                const float m = s_part[base[w] + G * D + 2 * jj];
+                mk[w] = on ? m : -INFINITY;
+                mx = fmaxf(mx, mk[w]);
+            }
+            float ls = 0.f, os[V];
 #pragma unroll
             for (int v = 0; v < V; ++v) os[v] = 0.f;
-            for (int w = w0; w <= w1; ++w) {
-                const int ws0 = span_start(w, NBB, kBinWaves);
-                if (ws0 == span_start(w + 1, NBB, kBinWaves)) continue;  // an empty span (bins of < 16 blocks)
-                const float *pp = s_part + (w * 2 + (a > ws0 ? 1 : 0)) * kPart;
-                const float mk = pp[G * D + 2 * jj], lk = pp[G * D + 2 * jj + 1];
-                if (mk == -INFINITY) continue;
-                const float cm = fmaxf(mx, mk);
-                const float keep = mx == -INFINITY ? 0.f : exp2f(mx - cm);
-                const float sc = exp2f(mk - cm);
-                ls = ls * keep + lk * sc;
 #pragma unroll
-                for (int v = 0; v < V; ++v) os[v] = os[v] * keep + pp[e0 + v] * sc;
-                mx = cm;
+            for (int w = 0; w < kBinWaves; ++w) {
+                const bool on = mk[w] != -INFINITY;
+                const float sc = on ? exp2f(mk[w] - mx) : 0.f;
+                const float *pp = s_part + base[w];
+                const float lk = pp[G * D + 2 * jj + 1];
+                ls += on ? lk * sc : 0.f;
+#pragma unroll
+                for (int v = 0; v < V; ++v) {
+                    const float ov = pp[e0 + v];
+                    os[v] += on ? ov * sc : 0.f;
+                }
             }
             bin_store<D, G, V>(os, mx, ls, e0, pc.w >= 0, s_pid[sl], h, query, Hq, out, o_s0, o_s1, piece_ml,
                                piece_o);
