@@ -198,7 +198,14 @@ gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t
 // K slice per workgroup: 512 columns of K (256 when the X block has 128 rows,
 // which keeps the staged block inside 64 KiB of LDS).  Every slice is one
 // fp32 partial plane.
-int slice_of(int M) { return M > 64 ? 256 : 512; }
+int slice_of(int M, int N, int K) {
+    // 512 K columns per workgroup for up to 64 rows (256 above); a projection
+    // whose grid would still fit one workgroup per CU with 256-column slices
+    // (bands x slices <= 256) takes those, so that every CU streams weights
+    if (M > 64) return 256;
+    return (N % 64 == 0 && K % 256 == 0 && (N / 64) * (K / 256) <= 256) ? 256 : 512;
+}
+
 
 // w_s0 == NQ_WEIGHT_PACKED selects the packed-fragment layout.  The packed
 // path is switched off (its entry points return NQ_ERR_UNSUPPORTED): the one
@@ -219,6 +226,28 @@ void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int6
     } else {
         hipLaunchKernelGGL((gemm_kernel<MT, KS, false>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N,
                            nb, out, o_s0, part, bias);
+    }
+}
+
+// The launch for M rows with the K slice slice_of picks.
+void dispatch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
+                   uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    const bool narrow = slice_of(M, N, K) == 256;
+    switch (mt) {
+        case 1:
+            narrow ? launch_gemm<1, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st)
+                   : launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st);
+            break;
+        case 2:
+            narrow ? launch_gemm<2, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st)
+                   : launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st);
+            break;
+        case 4:
+            narrow ? launch_gemm<4, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st)
+                   : launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st);
+            break;
+        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
     }
 }
 
@@ -267,8 +296,8 @@ int launch_reduce_partials(const float *part, int S, int M, int N, uint16_t *out
 using namespace nq;
 
 extern "C" int nq_linear_splits(int M, int N, int K) {
-    if (M <= 0 || M > 128 || N <= 0 || N % 64 != 0 || K <= 0 || K % slice_of(M) != 0) return -1;
-    return K / slice_of(M);
+    if (M <= 0 || M > 128 || N <= 0 || N % 64 != 0 || K <= 0 || K % slice_of(M, N, K) != 0) return -1;
+    return K / slice_of(M, N, K);
 }
 
 extern "C" int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue) {
@@ -305,13 +334,7 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
                                reinterpret_cast<uintptr_t>(workspace) % 16 == 0));
     float *part = need ? static_cast<float *>(workspace) : nullptr;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    switch (mt) {
-        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
-        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
-        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
-        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
-    }
+    dispatch_gemm(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     switch (epilogue) {
         case NQ_EPI_NONE:
@@ -341,13 +364,7 @@ extern "C" int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const 
     NQ_CHECK_ARG(workspace && workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 16 == 0);
     float *part = static_cast<float *>(workspace);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
-    switch (mt) {
-        case 1: launch_gemm<1, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
-        case 2: launch_gemm<2, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
-        case 4: launch_gemm<4, 512>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
-        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st); break;
-    }
+    dispatch_gemm(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     return launch_add_rmsnorm_partials_fp8(part, S, M, N, residual, norm_weight, eps, xq, xq_s0, sx, sx_s0, st);
 }
