@@ -1128,7 +1128,15 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     int4 dwin = make_int4(-1, 0, 0, 0);
     if (s0 + lane < s1) dwin = blocks[global_block(s0 + lane)];
 
-    // 1. q/k norm + RoPE + K/V write for the bin's rows (one wave per head unit)
+    // 1. q/k norm + RoPE + K/V write for the bin's rows (one wave per head unit);
+    // the norm weights are in registers before the first unit's planes arrive
+    float qw1 = 0.f, qw2 = 0.f, kw1 = 0.f, kw2 = 0.f;
+    if (lane < HALF) {
+        qw1 = bf16_to_f32(rs.q_weight[lane]);
+        qw2 = bf16_to_f32(rs.q_weight[lane + HALF]);
+        kw1 = bf16_to_f32(rs.k_weight[lane]);
+        kw2 = bf16_to_f32(rs.k_weight[lane + HALF]);
+    }
     for (int u = wave; u < nslots * (G + 2); u += kBinWaves) {
         const int sl = u / (G + 2), kind = u - sl * (G + 2);
         const int4 rp = s_rope[sl];
@@ -1143,10 +1151,24 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         const bool on = lane < HALF;
         float x1 = 0.f, x2 = 0.f;
         if (on) {
+            // the split-K planes four at a time (all loads in flight together),
+            // added in plane order
             const float *e = rs.partials + tok * rs.row + col + lane;
-            for (int i = 0; i < rs.splits; ++i) {
-                x1 += e[i * rs.plane];
-                x2 += e[i * rs.plane + HALF];
+            for (int i0 = 0; i0 < rs.splits; i0 += 4) {
+                float a[4], c[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const bool ok = i0 + v < rs.splits;
+                    a[v] = ok ? e[(i0 + v) * rs.plane] : 0.f;
+                    c[v] = ok ? e[(i0 + v) * rs.plane + HALF] : 0.f;
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (i0 + v < rs.splits) {
+                        x1 += a[v];
+                        x2 += c[v];
+                    }
+                }
             }
             x1 = bf16_to_f32(f32_to_bf16(x1));
             x2 = bf16_to_f32(f32_to_bf16(x2));
@@ -1167,7 +1189,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
             continue;
         }
         uint16_t o1 = 0, o2 = 0;
-        norm_rope_pair<D>(x1, x2, on, kind < G ? rs.q_weight : rs.k_weight, lane, rs.eps, rs.log_theta,
+        norm_rope_pair<D>(x1, x2, on, kind < G ? qw1 : kw1, kind < G ? qw2 : kw2, lane, rs.eps, rs.log_theta,
                           static_cast<float>(rp.y), rs.round_to_input, o1, o2);
         if (!on) continue;
         if (kind < G) {

@@ -76,21 +76,22 @@ __device__ __forceinline__ uint2 e4m3_pack8(const float (&x)[8], float s) {
 __device__ __forceinline__ float row_group_scale(float amax) { return amax > 0.f ? amax / 448.0f : 1.0f; }
 
 // q/k RMSNorm (with weight) and rotate-half RoPE of one head of D values held
-// as lane pairs: lane i < D/2 holds elements i and i + D/2 (x1, x2); lanes at
-// or above D/2 pass on = false.  inv_freq = exp(-ln(theta) * 2i / D), the
+// as lane pairs: lane i < D/2 holds elements i and i + D/2 (x1, x2) and their
+// norm weights (w1, w2, loaded by the caller with its inputs); lanes at or
+// above D/2 pass on = false.  inv_freq = exp(-ln(theta) * 2i / D), the
 // normalised values are rounded to bf16 first when round_to_input is set.
 // Every caller (the rope kernel and the fused decode attention) goes through
 // this one sequence of operations, so their q and K agree bit for bit.
 template <int D>
-__device__ __forceinline__ void norm_rope_pair(float x1, float x2, bool on, const uint16_t *__restrict__ weight,
-                                               int lane, float eps, float log_theta, float position,
-                                               int round_to_input, uint16_t &o1, uint16_t &o2) {
+__device__ __forceinline__ void norm_rope_pair(float x1, float x2, bool on, float w1, float w2, int lane, float eps,
+                                               float log_theta, float position, int round_to_input, uint16_t &o1,
+                                               uint16_t &o2) {
     constexpr int HALF = D / 2;
     const float ss = group_sum<(HALF < kWave ? HALF : kWave)>(on ? x1 * x1 + x2 * x2 : 0.f);
     if (!on) return;
     const float inv_rms = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-    float f = x1 * inv_rms * bf16_to_f32(weight[lane]);
-    float s = x2 * inv_rms * bf16_to_f32(weight[lane + HALF]);
+    float f = x1 * inv_rms * w1;
+    float s = x2 * inv_rms * w2;
     if (round_to_input) {
         f = bf16_to_f32(f32_to_bf16(f));
         s = bf16_to_f32(f32_to_bf16(s));

@@ -48,7 +48,15 @@ struct PartialHeads {
         const int col = (kind == kUnitQ ? head : kind == kUnitK ? Hq + head : Hq + Hkv + head) * D + d;
         const float *e = p + tok * row + col;
         float s = 0.f;
-        for (int i = 0; i < S; ++i) s += e[i * plane];
+        // four planes in flight at a time, added in plane order
+        for (int i0 = 0; i0 < S; i0 += 4) {
+            float a[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) a[v] = i0 + v < S ? e[(i0 + v) * plane] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (i0 + v < S) s += a[v];
+        }
         return bf16_to_f32(f32_to_bf16(s));
     }
 };
@@ -95,14 +103,18 @@ qk_norm_rope_kernel(Src src, RopeOut dst, const uint16_t *__restrict__ q_weight,
         return;
     }
     const bool on = lane < HALF;
-    float x1 = 0.f, x2 = 0.f;
+    float x1 = 0.f, x2 = 0.f, w1 = 0.f, w2 = 0.f;
     if (on) {
+        // the norm weights are loaded with the inputs, not after their reduction
+        const uint16_t *wt = kind == kUnitQ ? q_weight : k_weight;
+        w1 = bf16_to_f32(wt[lane]);
+        w2 = bf16_to_f32(wt[lane + HALF]);
         x1 = src.load(kind, tok, head, lane);
         x2 = src.load(kind, tok, head, lane + HALF);
     }
     uint16_t o1 = 0, o2 = 0;
-    norm_rope_pair<D>(x1, x2, on, kind == kUnitQ ? q_weight : k_weight, lane, eps, log_theta,
-                      static_cast<float>(positions[tok * pos_stride]), round_to_input, o1, o2);
+    norm_rope_pair<D>(x1, x2, on, w1, w2, lane, eps, log_theta, static_cast<float>(positions[tok * pos_stride]),
+                      round_to_input, o1, o2);
     if (!on) return;
     if (kind == kUnitQ) {
         uint16_t *qo = dst.q + tok * dst.q_s0 + head * dst.q_s1;
