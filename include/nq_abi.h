@@ -193,13 +193,27 @@ int nq_qkv_partials_norm_rope_kv_write(const float *partials, int splits, int to
  * seen: uint8/bool [rows, vocab] (row stride seen_s0) or NULL.
  * top_k: int32 (<= 0 means the whole vocabulary).  Masks: ids >= mask_from
  * except eos_id become -inf; eos_id becomes -inf where suppress_eos[row] != 0
- * (suppress_eos may be NULL).  tokens: int64 [rows].  vocab <= 8192.
+ * (suppress_eos may be NULL).  tokens: int64 [rows].  vocab <= 4096 (else
+ * NQ_ERR_UNSUPPORTED).
  */
 int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows, int vocab,
               const float *temperature, const int32_t *top_k, const float *top_p,
               const float *repetition_penalty, uint8_t *seen, int64_t seen_s0,
               const float *uniforms, int mask_from, int eos_id, const uint8_t *suppress_eos,
               int update_seen, int64_t *tokens, void *stream);
+
+/*
+ * nq_sample with row r's uniform drawn inside the kernel from its (seed,
+ * offset) counter exactly as nq_uniforms_from_counter computes it (the
+ * reference draws the talker's uniform from its stateless (seed, offset) pair
+ * in the same sampling call, executor/sampling.py:183-195): one launch
+ * instead of two, same tokens.
+ */
+int nq_sample_counter(const void *logits, int logits_dtype, int64_t logits_s0, int rows, int vocab,
+                      const float *temperature, const int32_t *top_k, const float *top_p,
+                      const float *repetition_penalty, uint8_t *seen, int64_t seen_s0, const int64_t *seed,
+                      int64_t seed_stride, const int64_t *offset, int64_t offset_stride, int mask_from,
+                      int eos_id, const uint8_t *suppress_eos, int update_seen, int64_t *tokens, void *stream);
 
 /*
  * Uniform draws in [0,1) from (seed, offset) counters with Philox-4x32-10

@@ -40,7 +40,7 @@ import torch.nn.functional as F
 from . import _lib
 from .kernels import decode_attn_nhd_short_cache, paired_qk_norm_rope_dense_cache_
 from .layers import linear, linear_add_rmsnorm, linear_silu_mul, linear_workspace_bytes, qwen3_tts_rmsnorm
-from .sampling import sample_with_uniforms, uniforms_from_counter
+from .sampling import sample_with_counter, sample_with_uniforms
 
 
 @dataclass(frozen=True)
@@ -189,11 +189,13 @@ class CodePredictorFrame:
             self._layers(group)
             logits = self.logits[group - 1]
             linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
-            u = self.uniforms[group - 1]
-            if self.use_counter_rng:
-                uniforms_from_counter(self.seed, self.offsets[:, group - 1], out=u)
             token = self.tokens[group - 1]
-            sample_with_uniforms(logits, self.temperature, self.top_k, self.top_p, u, out=token)
+            if self.use_counter_rng:
+                sample_with_counter(logits, self.temperature, self.top_k, self.top_p, self.seed,
+                                    self.offsets[:, group - 1], out=token)
+            else:
+                sample_with_uniforms(logits, self.temperature, self.top_k, self.top_p, self.uniforms[group - 1],
+                                     out=token)
             self.codec_sum.add_(F.embedding(token, w.codec_embedding[group - 1]))
             if group < groups - 1:
                 torch.index_select(w.projected_residual[group - 1], 0, token, out=self.h)

@@ -69,33 +69,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-__device__ int samp_block_scan(int v, int *tmp, int *total) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        int o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
-    if (lane == kWave - 1) tmp[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int w = 0; w < kSampThreads / kWave; ++w) {
-            const int x = tmp[w];
-            tmp[w] = acc;
-            acc += x;
-        }
-        tmp[kWave] = acc;
-    }
-    __syncthreads();
-    const int res = tmp[wave] + incl - v;
-    *total = tmp[kWave];
-    __syncthreads();
-    return res;
-}
-
 template <typename InT>
 __device__ __forceinline__ float load_logit(const InT *p);
 template <>
@@ -103,19 +76,77 @@ __device__ __forceinline__ float load_logit<float>(const float *p) { return *p; 
 template <>
 __device__ __forceinline__ float load_logit<uint16_t>(const uint16_t *p) { return bf16_to_f32(*p); }
 
+// Eight consecutive logits from a 16- (bf16) or 32-byte (fp32) aligned address.
+template <typename InT>
+__device__ __forceinline__ void load_logits8(const InT *p, float *x);
+template <>
+__device__ __forceinline__ void load_logits8<float>(const float *p, float *x) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load_logits8<uint16_t>(const uint16_t *p, float *x) {
+    float t[8];
+    unpack8(*reinterpret_cast<const uint4 *>(p), t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = t[e];
+}
+
+// Lanes of this wave below the calling lane among those whose bit is set.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+
+
+constexpr int kSampPer = kMaxVocab / kSampThreads;  // elements per thread (8 consecutive, twice)
+
+// Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds, key bumped by
+// the Weyl constants.  Returns the first output word.
+__device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                                 uint32_t k0, uint32_t k1) {
+    constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+    constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+        const uint64_t p0 = static_cast<uint64_t>(M0) * c0;
+        const uint64_t p1 = static_cast<uint64_t>(M1) * c2;
+        const uint32_t hi0 = static_cast<uint32_t>(p0 >> 32), lo0 = static_cast<uint32_t>(p0);
+        const uint32_t hi1 = static_cast<uint32_t>(p1 >> 32), lo1 = static_cast<uint32_t>(p1);
+        const uint32_t n0 = hi1 ^ c1 ^ k0;
+        const uint32_t n1 = lo1;
+        const uint32_t n2 = hi0 ^ c3 ^ k1;
+        const uint32_t n3 = lo0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += W0;
+        k1 += W1;
+    }
+    return c0;
+}
+
+// The uniform of a (seed, offset) counter: the top 24 bits of the first Philox word.
+__device__ __forceinline__ float counter_uniform(int64_t seed, int64_t offset) {
+    const uint64_t sd = static_cast<uint64_t>(seed), o = static_cast<uint64_t>(offset);
+    const uint32_t x = philox_first(static_cast<uint32_t>(o), static_cast<uint32_t>(o >> 32), 0u, 0u,
+                                    static_cast<uint32_t>(sd), static_cast<uint32_t>(sd >> 32));
+    return static_cast<float>(x >> 8) * (1.0f / 16777216.0f);
+}
+
 template <typename InT>
 __global__ void __launch_bounds__(kSampThreads)
 sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
               const float *__restrict__ temperature, const int32_t *__restrict__ top_k,
               const float *__restrict__ top_p, const float *__restrict__ penalty,
               uint8_t *__restrict__ seen, int64_t seen_s0, const float *__restrict__ uniforms,
-              int mask_from, int eos_id, const uint8_t *__restrict__ suppress_eos,
+              const int64_t *__restrict__ seed, int64_t seed_stride, const int64_t *__restrict__ offset,
+              int64_t offset_stride, int mask_from, int eos_id, const uint8_t *__restrict__ suppress_eos,
               int update_seen, int64_t *__restrict__ tokens) {
     __shared__ float s_val[kMaxVocab];
     __shared__ uint64_t s_sort[kMaxVocab];
-    __shared__ uint32_t s_hist[256];
-    __shared__ int s_tmp[kWave + 1];
-    __shared__ int s_bin, s_above;
+    __shared__ uint32_t s_hist[2][256];
+    __shared__ int s_bin, s_above, s_count, s_whole;
     __shared__ uint64_t s_red[kSampThreads / kWave];
 
     const int row = blockIdx.x;
@@ -129,21 +160,68 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
     const bool sup_eos = suppress_eos && suppress_eos[row];
     uint8_t *srow = seen ? seen + row * seen_s0 : nullptr;
 
-    // 1. masks, penalty, temperature into LDS.
-    for (int id = tid; id < vocab; id += kSampThreads) {
-        float x = load_logit<InT>(lrow + id);
-        if ((id >= mask_from && id != eos_id) || (id == eos_id && sup_eos)) x = -INFINITY;
-        if (srow && srow[id]) x = x > 0.0f ? x / r : x * r;
-        s_val[id] = greedy ? x : x / T;
+    // 1. masks, penalty, temperature: thread t owns ids 8t .. 8t + 7 and
+    // 8 (t + 256) .. + 7, loaded in one round trip; values go to LDS and stay in
+    // registers with their sortable keys (ids past the vocabulary get key 0,
+    // below every value)
+    float val[kSampPer];
+    uint32_t key[kSampPer];
+    {
+        // whole 8-id groups as one vector load each when the rows allow it
+        const bool vec = vocab % 8 == 0 && reinterpret_cast<uintptr_t>(lrow) % (8 * sizeof(InT)) == 0 &&
+                         (!srow || reinterpret_cast<uintptr_t>(srow) % 8 == 0);
+        float x[kSampPer];
+        uint8_t sn[kSampPer];
+#pragma unroll
+        for (int h = 0; h < kSampPer / 8; ++h) {
+            const int id0 = (tid + h * kSampThreads) * 8;
+            if (vec) {
+                if (id0 < vocab) {
+                    load_logits8<InT>(lrow + id0, &x[h * 8]);
+                    const uint2 m = srow ? *reinterpret_cast<const uint2 *>(srow + id0) : make_uint2(0u, 0u);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sn[h * 8 + e] = static_cast<uint8_t>((e < 4 ? m.x : m.y) >> (8 * (e % 4)));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        x[h * 8 + e] = 0.f;
+                        sn[h * 8 + e] = 0;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int id = id0 + e;
+                    x[h * 8 + e] = id < vocab ? load_logit<InT>(lrow + id) : 0.f;
+                    sn[h * 8 + e] = (srow && id < vocab) ? srow[id] : 0;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kSampPer; ++i) {
+            const int id = (tid + (i / 8) * kSampThreads) * 8 + i % 8;
+            float xv = x[i];
+            if ((id >= mask_from && id != eos_id) || (id == eos_id && sup_eos)) xv = -INFINITY;
+            if (sn[i]) xv = xv > 0.0f ? xv / r : xv * r;
+            val[i] = greedy ? xv : xv / T;
+            key[i] = id < vocab ? sort_key(val[i]) : 0u;
+            if (id < vocab) s_val[id] = val[i];
+        }
     }
+    for (int i = tid; i < 2 * 256; i += kSampThreads) (&s_hist[0][0])[i] = 0u;
+    if (tid == 0) s_count = 0;
     __syncthreads();
 
     int token;
     if (greedy) {
         uint64_t best = 0;
-        for (int id = tid; id < vocab; id += kSampThreads) {
-            const uint64_t c = composite(s_val[id], id);
-            best = c > best ? c : best;
+#pragma unroll
+        for (int i = 0; i < kSampPer; ++i) {
+            const int id = (tid + (i / 8) * kSampThreads) * 8 + i % 8;
+            if (id < vocab) {
+                const uint64_t c = composite(val[i], id);
+                best = c > best ? c : best;
+            }
         }
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) {
@@ -161,84 +239,97 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
         float p = top_p[row];
         p = p < 1.0f ? p : 1.0f;
 
-        // 2. radix select of the k_eff-th largest sortable key.
+        // 2. radix select of the k_eff-th largest sortable key, 8 bits a pass from
+        // the top; wave 0 locates each pass's digit (lane L scans bins
+        // 255 - 4L .. 252 - 4L) and clears the other histogram for the next pass
         uint32_t prefix = 0, pmask = 0;
         int remaining = k_eff;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            s_hist[tid] = 0;
+        // once the bin holding the k_eff-th key is needed whole, the keys at or
+        // above its lowest key are exactly the selection: the select stops there
+        if (tid == 0) s_whole = 0;
+        for (int pass = 0; pass < 4; ++pass) {
+            const int shift = 24 - 8 * pass;
+            uint32_t *hist = s_hist[pass & 1];
+#pragma unroll
+            for (int i = 0; i < kSampPer; ++i)
+                if (key[i] != 0u && (key[i] & pmask) == prefix) atomicAdd(&hist[(key[i] >> shift) & 255u], 1u);
             __syncthreads();
-            for (int id = tid; id < vocab; id += kSampThreads) {
-                const uint32_t key = sort_key(s_val[id]);
-                if ((key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            const int bin = 255 - tid;
-            const int v = static_cast<int>(s_hist[bin]);
-            int tot;
-            const int above = samp_block_scan(v, s_tmp, &tot);  // count in bins > bin
-            if (above < remaining && remaining <= above + v) {
-                s_bin = bin;
-                s_above = above;
+            if (wave == 0) {
+                uint32_t c[4];
+                uint32_t tot = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    c[j] = hist[255 - 4 * lane - j];
+                    tot += c[j];
+                }
+                uint32_t incl = tot;
+#pragma unroll
+                for (int d = 1; d < kWave; d <<= 1) {
+                    const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d, kWave));
+                    if (lane >= d) incl += o;
+                }
+                uint32_t above = incl - tot;  // count in the bins above this lane's
+                const int rem = remaining;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (static_cast<int>(above) < rem && rem <= static_cast<int>(above + c[j])) {
+                        s_bin = 255 - 4 * lane - j;
+                        s_above = static_cast<int>(above);
+                        s_whole = rem == static_cast<int>(above + c[j]) ? 1 : 0;
+                    }
+                    above += c[j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s_hist[(pass + 1) & 1][lane * 4 + j] = 0u;
             }
             __syncthreads();
             prefix |= static_cast<uint32_t>(s_bin) << shift;
             pmask |= 255u << shift;
             remaining -= s_above;
-            __syncthreads();
+            if (s_whole) break;  // uniform: every thread read the same flag
         }
         const uint32_t thr = prefix;
-        const int need_eq = remaining;
 
-        // 3. compact the selected ids in id order.
-        const int per = (vocab + kSampThreads - 1) / kSampThreads;
-        const int lo_id = tid * per;
-        const int hi_id = min(vocab, lo_id + per);
-        int n_eq = 0;
-        for (int id = lo_id; id < hi_id; ++id) n_eq += sort_key(s_val[id]) == thr;
-        int tot;
-        const int eq_base = samp_block_scan(n_eq, s_tmp, &tot);
-        int n_sel = 0, eq_seen = 0;
-        for (int id = lo_id; id < hi_id; ++id) {
-            const uint32_t key = sort_key(s_val[id]);
-            const bool eq = key == thr;
-            n_sel += (key > thr) || (eq && eq_base + eq_seen < need_eq);
-            eq_seen += eq;
-        }
-        const int sel_base = samp_block_scan(n_sel, s_tmp, &tot);
-        {
-            int at = sel_base;
-            eq_seen = 0;
-            for (int id = lo_id; id < hi_id; ++id) {
-                const float f = s_val[id];
-                const uint32_t key = sort_key(f);
-                const bool eq = key == thr;
-                if ((key > thr) || (eq && eq_base + eq_seen < need_eq)) s_sort[at++] = composite(f, id);
-                eq_seen += eq;
+        // 3. every entry at or above the threshold (ties included), in any order:
+        // the sort below puts them in (value desc, id asc) order and the first
+        // k_eff are the selection
+#pragma unroll
+        for (int i = 0; i < kSampPer; ++i) {
+            const bool sel = key[i] != 0u && key[i] >= thr;
+            const uint64_t m = __ballot(sel);
+            if (m) {
+                int base = 0;
+                const int leader = __ffsll(static_cast<long long>(m)) - 1;
+                if (lane == leader) base = atomicAdd(&s_count, __popcll(m));
+                base = __shfl(base, leader, kWave);
+                const int id = (tid + (i / 8) * kSampThreads) * 8 + i % 8;
+                if (sel) s_sort[base + lanes_below(m)] = composite(val[i], id);
             }
         }
         __syncthreads();
+        const int n_c = s_count;
 
-        // 4. sort the k_eff selected entries by (value desc, id asc).
-        if (k_eff <= kWave) {
+        // 4. sort the n_c collected entries by (value desc, id asc).
+        if (n_c <= kWave) {
             if (wave == 0) {
-                uint64_t key = lane < k_eff ? s_sort[lane] : 0ull;
+                uint64_t kv = lane < n_c ? s_sort[lane] : 0ull;
 #pragma unroll
                 for (int kk = 2; kk <= kWave; kk <<= 1) {
 #pragma unroll
                     for (int j = kk >> 1; j > 0; j >>= 1) {
-                        const uint64_t other = shfl_xor_u64(key, j);
+                        const uint64_t other = shfl_xor_u64(kv, j);
                         const bool lower = (lane & j) == 0;
                         const bool asc = (lane & kk) == 0;
                         const bool take_max = lower == asc;
-                        key = take_max ? (key > other ? key : other) : (key < other ? key : other);
+                        kv = take_max ? (kv > other ? kv : other) : (kv < other ? kv : other);
                     }
                 }
-                if (lane < k_eff) s_sort[lane] = key;
+                if (lane < n_c) s_sort[lane] = kv;
             }
         } else {
             int n2 = 1;
-            while (n2 < k_eff) n2 <<= 1;
-            for (int i = k_eff + tid; i < n2; i += kSampThreads) s_sort[i] = 0ull;
+            while (n2 < n_c) n2 <<= 1;
+            for (int i = n_c + tid; i < n2; i += kSampThreads) s_sort[i] = 0ull;
             __syncthreads();
             for (int kk = 2; kk <= n2; kk <<= 1) {
                 for (int j = kk >> 1; j > 0; j >>= 1) {
@@ -305,7 +396,9 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
             for (int m = 1; m < kWave; m <<= 1) first_drop = min(first_drop, __shfl_xor(first_drop, m, kWave));
             const int kept = first_drop > 0 ? first_drop : 1;
             const float mass = s_val[kept - 1];
-            const float um = uniforms[row] * mass;
+            // the row's uniform: given, or drawn here from its (seed, offset) counter
+            const float u = uniforms ? uniforms[row] : counter_uniform(seed[row * seed_stride], offset[row * offset_stride]);
+            const float um = u * mass;
             int pick = kept - 1;
             for (int rr = r0; rr < min(r1, kept); ++rr)
                 if (s_val[rr] >= um) { pick = rr; break; }
@@ -323,51 +416,27 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
     }
 }
 
-// Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds, key bumped by
-// the Weyl constants.  Returns the first output word.
-__device__ __forceinline__ uint32_t philox_first(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
-                                                 uint32_t k0, uint32_t k1) {
-    constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
-    constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-    for (int i = 0; i < 10; ++i) {
-        const uint64_t p0 = static_cast<uint64_t>(M0) * c0;
-        const uint64_t p1 = static_cast<uint64_t>(M1) * c2;
-        const uint32_t hi0 = static_cast<uint32_t>(p0 >> 32), lo0 = static_cast<uint32_t>(p0);
-        const uint32_t hi1 = static_cast<uint32_t>(p1 >> 32), lo1 = static_cast<uint32_t>(p1);
-        const uint32_t n0 = hi1 ^ c1 ^ k0;
-        const uint32_t n1 = lo1;
-        const uint32_t n2 = hi0 ^ c3 ^ k1;
-        const uint32_t n3 = lo0;
-        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
-        k0 += W0;
-        k1 += W1;
-    }
-    return c0;
-}
-
 __global__ void uniforms_kernel(const int64_t *__restrict__ seed, int64_t seed_stride,
                                 const int64_t *__restrict__ offset, int64_t offset_stride, int rows,
                                 float *__restrict__ out) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= rows) return;
-    const uint64_t s = static_cast<uint64_t>(seed[i * seed_stride]);
-    const uint64_t o = static_cast<uint64_t>(offset[i * offset_stride]);
-    const uint32_t x = philox_first(static_cast<uint32_t>(o), static_cast<uint32_t>(o >> 32), 0u, 0u,
-                                    static_cast<uint32_t>(s), static_cast<uint32_t>(s >> 32));
-    out[i] = static_cast<float>(x >> 8) * (1.0f / 16777216.0f);
+    out[i] = counter_uniform(seed[i * seed_stride], offset[i * offset_stride]);
 }
 
 }  // namespace
 }  // namespace nq
 
-extern "C" int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows,
-                         int vocab, const float *temperature, const int32_t *top_k,
-                         const float *top_p, const float *repetition_penalty, uint8_t *seen,
-                         int64_t seen_s0, const float *uniforms, int mask_from, int eos_id,
-                         const uint8_t *suppress_eos, int update_seen, int64_t *tokens,
-                         void *stream) {
-    NQ_CHECK_ARG(logits && temperature && top_k && top_p && uniforms && tokens);
+namespace {
+
+int launch_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows, int vocab,
+                  const float *temperature, const int32_t *top_k, const float *top_p,
+                  const float *repetition_penalty, uint8_t *seen, int64_t seen_s0, const float *uniforms,
+                  const int64_t *seed, int64_t seed_stride, const int64_t *offset, int64_t offset_stride,
+                  int mask_from, int eos_id, const uint8_t *suppress_eos, int update_seen, int64_t *tokens,
+                  void *stream) {
+    NQ_CHECK_ARG(logits && temperature && top_k && top_p && tokens);
+    NQ_CHECK_ARG(uniforms || (seed && offset));
     NQ_CHECK_ARG(rows >= 0 && vocab >= 1);
     NQ_CHECK_ARG(!update_seen || seen);
     if (vocab > nq::kMaxVocab) return NQ_ERR_UNSUPPORTED;
@@ -375,18 +444,44 @@ extern "C" int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (logits_dtype == NQ_F32) {
         hipLaunchKernelGGL(nq::sample_kernel<float>, dim3(rows), dim3(nq::kSampThreads), 0, s,
-                           static_cast<const float *>(logits), logits_s0, vocab, temperature,
-                           top_k, top_p, repetition_penalty, seen, seen_s0, uniforms, mask_from,
-                           eos_id, suppress_eos, update_seen, tokens);
+                           static_cast<const float *>(logits), logits_s0, vocab, temperature, top_k, top_p,
+                           repetition_penalty, seen, seen_s0, uniforms, seed, seed_stride, offset, offset_stride,
+                           mask_from, eos_id, suppress_eos, update_seen, tokens);
     } else if (logits_dtype == NQ_BF16) {
         hipLaunchKernelGGL(nq::sample_kernel<uint16_t>, dim3(rows), dim3(nq::kSampThreads), 0, s,
-                           static_cast<const uint16_t *>(logits), logits_s0, vocab, temperature,
-                           top_k, top_p, repetition_penalty, seen, seen_s0, uniforms, mask_from,
-                           eos_id, suppress_eos, update_seen, tokens);
+                           static_cast<const uint16_t *>(logits), logits_s0, vocab, temperature, top_k, top_p,
+                           repetition_penalty, seen, seen_s0, uniforms, seed, seed_stride, offset, offset_stride,
+                           mask_from, eos_id, suppress_eos, update_seen, tokens);
     } else {
         return NQ_ERR_UNSUPPORTED;
     }
     return NQ_LAUNCH_STATUS();
+}
+
+}  // namespace
+
+extern "C" int nq_sample(const void *logits, int logits_dtype, int64_t logits_s0, int rows,
+                         int vocab, const float *temperature, const int32_t *top_k,
+                         const float *top_p, const float *repetition_penalty, uint8_t *seen,
+                         int64_t seen_s0, const float *uniforms, int mask_from, int eos_id,
+                         const uint8_t *suppress_eos, int update_seen, int64_t *tokens,
+                         void *stream) {
+    NQ_CHECK_ARG(uniforms);
+    return launch_sample(logits, logits_dtype, logits_s0, rows, vocab, temperature, top_k, top_p,
+                         repetition_penalty, seen, seen_s0, uniforms, nullptr, 0, nullptr, 0, mask_from, eos_id,
+                         suppress_eos, update_seen, tokens, stream);
+}
+
+extern "C" int nq_sample_counter(const void *logits, int logits_dtype, int64_t logits_s0, int rows, int vocab,
+                                 const float *temperature, const int32_t *top_k, const float *top_p,
+                                 const float *repetition_penalty, uint8_t *seen, int64_t seen_s0,
+                                 const int64_t *seed, int64_t seed_stride, const int64_t *offset,
+                                 int64_t offset_stride, int mask_from, int eos_id, const uint8_t *suppress_eos,
+                                 int update_seen, int64_t *tokens, void *stream) {
+    NQ_CHECK_ARG(seed && offset);
+    return launch_sample(logits, logits_dtype, logits_s0, rows, vocab, temperature, top_k, top_p,
+                         repetition_penalty, seen, seen_s0, nullptr, seed, seed_stride, offset, offset_stride,
+                         mask_from, eos_id, suppress_eos, update_seen, tokens, stream);
 }
 
 extern "C" int nq_uniforms_from_counter(const int64_t *seed, int64_t seed_stride,

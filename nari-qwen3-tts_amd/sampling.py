@@ -2,11 +2,12 @@
 
 ``sample_with_uniforms`` is the north-star entry: caller-supplied uniforms,
 token ids bit-exact against the oracle.  The three reference entry points
-keep their signatures (executor/sampling.py:156-198, 201-239, 305-336): they
-turn each row's (seed, offset) counter into a uniform with Philox-4x32-10
-(``uniforms_from_counter``) and then run the same fused kernel, so a
-request's draw depends only on its own counter (row-local, batch- and
-permutation-invariant like model/sampling.py:192-195).
+keep their signatures (executor/sampling.py:156-198, 201-239, 305-336): the
+same fused kernel draws each row's uniform from its (seed, offset) counter
+with Philox-4x32-10 (``sample_with_counter``, identical to
+``uniforms_from_counter`` then ``sample_with_uniforms``), so a request's draw
+depends only on its own counter (row-local, batch- and permutation-invariant
+like model/sampling.py:192-195).
 """
 
 from __future__ import annotations
@@ -32,12 +33,14 @@ def uniforms_from_counter(seed: torch.Tensor, offset: torch.Tensor, out: torch.T
     return out
 
 
-def sample_with_uniforms(
+def _sample(
     logits: torch.Tensor,
     temperature: torch.Tensor,
     top_k: torch.Tensor,
     top_p: torch.Tensor,
-    uniforms: torch.Tensor,
+    uniforms: torch.Tensor | None,
+    seed: torch.Tensor | None,
+    offset: torch.Tensor | None,
     *,
     repetition_penalty: torch.Tensor | None = None,
     seen_token_mask: torch.Tensor | None = None,
@@ -47,8 +50,6 @@ def sample_with_uniforms(
     update_seen: bool = False,
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """One token per row: masks, penalty, temperature, top-k, top-p, inverse-CDF draw."""
-
     if logits.ndim != 2 or logits.shape[0] < 1:
         raise ValueError("logits must have shape (rows, vocabulary)")
     rows, vocab = logits.shape
@@ -60,16 +61,19 @@ def sample_with_uniforms(
         raise TypeError("logits must be float32 or bfloat16")
     if logits.stride(1) != 1:
         raise ValueError("logits rows must be contiguous")
-    for name, t, dtype in (
-        ("temperature", temperature, torch.float32),
-        ("top_k", top_k, torch.int32),
-        ("top_p", top_p, torch.float32),
-        ("uniforms", uniforms, torch.float32),
-    ):
+    vectors = [("temperature", temperature, torch.float32), ("top_k", top_k, torch.int32), ("top_p", top_p, torch.float32)]
+    if uniforms is not None:
+        vectors.append(("uniforms", uniforms, torch.float32))
+    for name, t, dtype in vectors:
         if t.dtype != dtype:
             raise TypeError(f"{name} must use {dtype}, got {t.dtype}")
         if t.shape != (rows,) or (rows > 1 and t.stride(0) != 1):
             raise ValueError(f"{name} must be a contiguous row vector with {rows} entries")
+    if uniforms is None:
+        if seed.dtype != torch.long or offset.dtype != torch.long:
+            raise TypeError("seed and offset must use torch.int64")
+        if seed.shape != (rows,) or offset.shape != (rows,):
+            raise ValueError(f"seed and offset must be row vectors with {rows} entries")
     if repetition_penalty is not None:
         if repetition_penalty.dtype != torch.float32:
             raise TypeError("repetition_penalty must use torch.float32")
@@ -84,17 +88,33 @@ def sample_with_uniforms(
         raise ValueError("update_seen needs a seen_token_mask")
     if suppress_eos is not None and (suppress_eos.dtype != torch.bool or suppress_eos.shape != (rows,)):
         raise ValueError("suppress_eos must be a bool row vector")
-    _lib.require_device(logits, temperature, top_k, top_p, uniforms, repetition_penalty, seen_token_mask, suppress_eos)
+    _lib.require_device(logits, temperature, top_k, top_p, uniforms, seed, offset, repetition_penalty, seen_token_mask,
+                        suppress_eos)
     tokens = torch.empty(rows, dtype=torch.long, device=logits.device) if out is None else out
-    _lib.call(
-        "nq_sample",
-        logits.data_ptr(), code, logits.stride(0), rows, vocab,
-        temperature.data_ptr(), top_k.data_ptr(), top_p.data_ptr(), _lib.ptr(repetition_penalty),
-        _lib.ptr(seen_token_mask), 0 if seen_token_mask is None else seen_token_mask.stride(0),
-        uniforms.data_ptr(), vocab if mask_from is None else int(mask_from), int(eos_id),
-        _lib.ptr(suppress_eos), int(update_seen), tokens.data_ptr(), _lib.stream(logits.device),
-    )
+    head = (logits.data_ptr(), code, logits.stride(0), rows, vocab, temperature.data_ptr(), top_k.data_ptr(),
+            top_p.data_ptr(), _lib.ptr(repetition_penalty), _lib.ptr(seen_token_mask),
+            0 if seen_token_mask is None else seen_token_mask.stride(0))
+    tail = (vocab if mask_from is None else int(mask_from), int(eos_id), _lib.ptr(suppress_eos), int(update_seen),
+            tokens.data_ptr(), _lib.stream(logits.device))
+    if uniforms is not None:
+        _lib.call("nq_sample", *head, uniforms.data_ptr(), *tail)
+    else:
+        _lib.call("nq_sample_counter", *head, seed.data_ptr(), seed.stride(0), offset.data_ptr(), offset.stride(0), *tail)
     return tokens
+
+
+def sample_with_uniforms(logits, temperature, top_k, top_p, uniforms, **kwargs) -> torch.Tensor:
+    """One token per row: masks, penalty, temperature, top-k, top-p, inverse-CDF draw with the
+    caller's uniforms."""
+
+    return _sample(logits, temperature, top_k, top_p, uniforms, None, None, **kwargs)
+
+
+def sample_with_counter(logits, temperature, top_k, top_p, seed, offset, **kwargs) -> torch.Tensor:
+    """As sample_with_uniforms with row r's uniform drawn in the same launch from its (seed, offset)
+    counter exactly as uniforms_from_counter computes it (same tokens, one launch)."""
+
+    return _sample(logits, temperature, top_k, top_p, None, seed, offset, **kwargs)
 
 
 def sample_talker_cuda_graph(
@@ -109,28 +129,29 @@ def sample_talker_cuda_graph(
 ) -> torch.Tensor:
     """Talker draw with penalty over seen ids; the caller updates ``seen``."""
 
-    u = uniforms_from_counter(seed, offset)
-    return sample_with_uniforms(
-        logits, temperature, top_k, top_p, u, repetition_penalty=repetition_penalty, seen_token_mask=seen_token_mask
+    return sample_with_counter(
+        logits, temperature, top_k, top_p, seed, offset, repetition_penalty=repetition_penalty,
+        seen_token_mask=seen_token_mask,
     )
 
 
 def sample_logits_cuda_graph(logits, temperature, top_k, top_p, seed, offset) -> torch.Tensor:
     """General-route draw (any top_k, no penalty)."""
 
-    return sample_with_uniforms(logits, temperature, top_k, top_p, uniforms_from_counter(seed, offset))
+    return sample_with_counter(logits, temperature, top_k, top_p, seed, offset)
 
 
 def sample_code_predictor_cuda_graph(logits, temperature, top_k, top_p, seed, offset) -> torch.Tensor:
     """Fused code-predictor draw; ``offset`` may be a strided column of [rows, 15]."""
 
-    return sample_with_uniforms(logits, temperature, top_k, top_p, uniforms_from_counter(seed, offset))
+    return sample_with_counter(logits, temperature, top_k, top_p, seed, offset)
 
 
 __all__ = [
     "sample_code_predictor_cuda_graph",
     "sample_logits_cuda_graph",
     "sample_talker_cuda_graph",
+    "sample_with_counter",
     "sample_with_uniforms",
     "uniforms_from_counter",
 ]

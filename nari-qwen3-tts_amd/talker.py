@@ -46,7 +46,7 @@ from .layers import (
     qwen3_tts_silu_and_mul,
     quantize_fp8_weight_blocks,
 )
-from .sampling import sample_with_uniforms, uniforms_from_counter
+from .sampling import sample_with_counter, sample_with_uniforms
 
 
 @dataclass(frozen=True)
@@ -230,22 +230,14 @@ class TalkerDecodeStep:
             linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
         else:
             torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
+        options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
+                       eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
         if self.use_counter_rng:
-            uniforms_from_counter(self.seed, self.offsets, out=self.uniforms)
-        sample_with_uniforms(
-            self.logits,
-            self.temperature,
-            self.top_k,
-            self.top_p,
-            self.uniforms,
-            repetition_penalty=self.penalty,
-            seen_token_mask=self.seen,
-            mask_from=c.codec_vocab,
-            eos_id=c.eos_id,
-            suppress_eos=self.suppress_eos,
-            update_seen=True,
-            out=self.tokens,
-        )
+            # the uniform comes from each row's (seed, offset) counter inside the sampling launch
+            sample_with_counter(self.logits, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
+                                **options)
+        else:
+            sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
         return self.tokens
 
 

@@ -148,3 +148,23 @@ def test_reference_signatures_are_row_local(nq, device):
     assert torch.equal(batch, single)
     cp = sample_code_predictor_cuda_graph(logits, t, k, p, seed, off)
     assert cp.dtype == torch.long and cp.shape == (12,)
+
+
+def test_counter_draw_equals_uniforms_then_sample(nq, device):
+    """One launch with the in-kernel Philox draw gives the tokens of uniforms_from_counter followed by
+    sample_with_uniforms, including a strided offset column and the seen-mask update."""
+
+    from nari_qwen3_tts_amd.sampling import sample_with_counter, sample_with_uniforms, uniforms_from_counter
+
+    logits, t, k, p, _, r, seen = _inputs(device, 21, 40, 3072)
+    seed = torch.arange(40, dtype=torch.long, device=device) * 7919 + 3
+    table = (torch.arange(40 * 15, dtype=torch.long, device=device).view(40, 15) * 97) % 100003
+    for off in (table[:, 0].contiguous(), table[:, 6]):
+        u = uniforms_from_counter(seed, off)
+        seen_a, seen_b = seen.clone(), seen.clone()
+        want = sample_with_uniforms(logits, t, k, p, u, repetition_penalty=r, seen_token_mask=seen_a, mask_from=2048,
+                                    eos_id=2150, update_seen=True)
+        got = sample_with_counter(logits, t, k, p, seed, off, repetition_penalty=r, seen_token_mask=seen_b,
+                                  mask_from=2048, eos_id=2150, update_seen=True)
+        assert torch.equal(got, want)
+        assert torch.equal(seen_a, seen_b)
