@@ -233,6 +233,20 @@ int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16_t *weight,
                    int width, float eps, void *stream);
 
 /*
+ * The talker step's input: residual[r] = bf16(addend[r] + table[ids[r]])
+ * (the codec-step embedding plus the text embedding of materialize_decode,
+ * executor/talker.py:256-262) and out[r] = rmsnorm(residual[r]) * weight (the
+ * first layer's input norm, model/layers.py:82-115), in one launch; the same
+ * bits as the add, then nq_rmsnorm.  table [num_embeddings, width] (row stride
+ * table_s0), addend [rows, width] (row stride addend_s0), residual and out
+ * contiguous; bf16, 16-byte aligned.  An id outside [0, num_embeddings) reads
+ * row 0 and stores NQ_ERR_INVALID_ARGUMENT in *status (status may be NULL).
+ */
+int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, int64_t table_s0, int64_t num_embeddings,
+                         const uint16_t *addend, int64_t addend_s0, const uint16_t *weight, int rows, int width,
+                         float eps, uint16_t *residual, uint16_t *out, int32_t *status, void *stream);
+
+/*
  * out = rmsnorm(x) (model/layers.py:82-115).  bf16 [rows, width]; out may alias x.
  */
 int nq_rmsnorm(const uint16_t *x, const uint16_t *weight, uint16_t *out, int rows, int width,

@@ -50,6 +50,25 @@ struct PartialSrc {
     }
 };
 
+// Source of the "hidden" operand gathered from an embedding table by token
+// id: row r reads table[ids[r]]; an id outside [0, n) reads row 0 and reports
+// NQ_ERR_INVALID_ARGUMENT in *status (when given), where nn.Embedding raises.
+struct GatherSrc {
+    const uint16_t *table;
+    int64_t s0;
+    const int64_t *ids;
+    int64_t n;
+    int32_t *status;
+    __device__ __forceinline__ void load8(int64_t row, int col, float (&x)[8]) const {
+        int64_t id = ids[row];
+        if (id < 0 || id >= n) {
+            if (status && col == 0) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+            id = 0;
+        }
+        unpack8(*reinterpret_cast<const uint4 *>(table + id * s0 + col), x);
+    }
+};
+
 // Quantized output of the normalised row: codes [rows, width] and scales
 // [rows, width / 128].
 struct Fp8Out {
@@ -62,8 +81,8 @@ struct Fp8Out {
 template <typename Src, bool kFp8>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
-                   uint16_t *__restrict__ residual, const uint16_t *__restrict__ weight, int width,
-                   float eps, Fp8Out fp8) {
+                   uint16_t *__restrict__ residual, const uint16_t *__restrict__ residual_in, int64_t ri_s0,
+                   const uint16_t *__restrict__ weight, int width, float eps, Fp8Out fp8) {
     __shared__ float tmp[kNormThreads / kWave];
     const int64_t row = blockIdx.x;
     const int nvec = width / 8;
@@ -76,7 +95,9 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
             hidden.load8(row, vi * 8, a[i]);
-            unpack8(*reinterpret_cast<const uint4 *>(residual + row * width + vi * 8), b[i]);
+            // the residual is read from residual_in when given (then only written to residual)
+            const uint16_t *rin = residual_in ? residual_in + row * ri_s0 : residual + row * width;
+            unpack8(*reinterpret_cast<const uint4 *>(rin + vi * 8), b[i]);
             unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w[i]);
         }
     }
@@ -197,7 +218,7 @@ int launch_add_rmsnorm_partials(const float *part, int S, int rows, int width, u
     if (width % 8 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
     const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
     hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, false>), dim3(rows), dim3(kNormThreads), 0, st, src,
-                       hidden_out, ho_s0, residual, weight, width, eps, Fp8Out{});
+                       hidden_out, ho_s0, residual, nullptr, 0, weight, width, eps, Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -207,7 +228,7 @@ int launch_add_rmsnorm_partials_fp8(const float *part, int S, int rows, int widt
     if (width % 128 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
     const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
     hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, true>), dim3(rows), dim3(kNormThreads), 0, st, src, nullptr,
-                       0, residual, weight, width, eps, Fp8Out{xq, xq_s0, sx, sx_s0});
+                       0, residual, nullptr, 0, weight, width, eps, Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -230,7 +251,7 @@ extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16
     const nq::Bf16Src src{hidden, width};
     hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, false>), dim3(rows), dim3(nq::kNormThreads), 0,
                        static_cast<hipStream_t>(stream), src, hidden, static_cast<int64_t>(width), residual,
-                       weight, width, eps, nq::Fp8Out{});
+                       nullptr, 0, weight, width, eps, nq::Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -245,8 +266,8 @@ extern "C" int nq_add_rmsnorm_fp8(const uint16_t *hidden, uint16_t *residual, co
     if (rows == 0) return NQ_OK;
     const nq::Bf16Src src{hidden, width};
     hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, true>), dim3(rows), dim3(nq::kNormThreads), 0,
-                       static_cast<hipStream_t>(stream), src, nullptr, 0, residual, weight, width, eps,
-                       nq::Fp8Out{xq, xq_s0, sx, sx_s0});
+                       static_cast<hipStream_t>(stream), src, nullptr, 0, residual, nullptr, 0, weight, width,
+                       eps, nq::Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -270,5 +291,23 @@ extern "C" int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int
     const nq::Bf16Src src{gate_up, 2 * static_cast<int64_t>(width)};
     hipLaunchKernelGGL(nq::silu_mul_kernel<nq::Bf16Src>, dim3(nq::silu_grid(rows, width)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), src, out, static_cast<int64_t>(width), rows, width);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, int64_t table_s0, int64_t num_embeddings,
+                                    const uint16_t *addend, int64_t addend_s0, const uint16_t *weight, int rows,
+                                    int width, float eps, uint16_t *residual, uint16_t *out, int32_t *status,
+                                    void *stream) {
+    NQ_CHECK_ARG(ids && table && addend && weight && residual && out && rows >= 0 && width >= 8);
+    NQ_CHECK_ARG(num_embeddings >= 1 && table_s0 >= width && addend_s0 >= width);
+    if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
+    if (!nq::al16(table) || !nq::al16(addend) || !nq::al16(weight) || !nq::al16(residual) || !nq::al16(out) ||
+        table_s0 % 8 || addend_s0 % 8)
+        return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    const nq::GatherSrc src{table, table_s0, ids, num_embeddings, status};
+    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::GatherSrc, false>), dim3(rows), dim3(nq::kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), src, out, static_cast<int64_t>(width), residual, addend,
+                       addend_s0, weight, width, eps, nq::Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }

@@ -58,6 +58,31 @@ def qwen3_tts_rmsnorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float, ou
     return out
 
 
+def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tensor, weight: torch.Tensor, eps: float,
+                      residual: torch.Tensor, out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
+    """residual = bf16(addend + table[ids]); out = rmsnorm(residual) * weight, one launch (the talker step's
+    input embedding and first input norm).  ``status`` (int32 [1], optional) receives NQ_ERR_INVALID_ARGUMENT
+    for an id outside the table."""
+
+    for t, name in ((table, "embedding table"), (addend, "addend"), (weight, "norm weight"), (residual, "residual"),
+                    (out, "out")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise TypeError(f"{name} must be bf16 with unit inner stride")
+    if ids.dtype != torch.long or ids.ndim != 1:
+        raise TypeError("ids must be an int64 vector")
+    rows, width = addend.shape
+    if ids.shape != (rows,) or table.shape[1] != width or weight.shape != (width,):
+        raise ValueError("ids / table / norm weight do not match the addend")
+    if residual.shape != (rows, width) or out.shape != (rows, width) or not residual.is_contiguous() \
+            or not out.is_contiguous():
+        raise ValueError("residual and out must be contiguous [rows, width]")
+    _lib.require_device(ids, table, addend, weight, residual, out, status)
+    _lib.call("nq_embed_add_rmsnorm", ids.data_ptr(), table.data_ptr(), table.stride(0), table.shape[0],
+              addend.data_ptr(), addend.stride(0), weight.data_ptr(), rows, width, float(eps), residual.data_ptr(),
+              out.data_ptr(), _lib.ptr(status), _lib.stream(addend.device))
+    return out
+
+
 def qwen3_tts_silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     _check(gate_up, "gate_up")
     width = gate_up.shape[-1] // 2
@@ -380,6 +405,8 @@ def linear_fp8_swiglu(q: torch.Tensor, scales: torch.Tensor, packed: torch.Tenso
 
 __all__ = [
     "FP8",
+    "PackedLinearWeight",
+    "embed_add_rmsnorm",
     "linear_fp8_swiglu",
     "pack_fp8_swiglu",
     "add_rmsnorm_fp8",
@@ -391,6 +418,7 @@ __all__ = [
     "linear_partials",
     "linear_silu_mul",
     "linear_workspace_bytes",
+    "pack_linear_weight",
     "quantize_fp8_rows",
     "quantize_fp8_weight_blocks",
     "qwen3_tts_add_rmsnorm",

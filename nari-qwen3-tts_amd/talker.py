@@ -26,12 +26,12 @@ from dataclasses import dataclass
 from types import SimpleNamespace
 
 import torch
-import torch.nn.functional as F
 
 from . import _lib
 from .layers import (
     FP8,
     add_rmsnorm_fp8,
+    embed_add_rmsnorm,
     linear,
     linear_add_rmsnorm,
     linear_add_rmsnorm_fp8,
@@ -42,7 +42,6 @@ from .layers import (
     linear_silu_mul,
     linear_workspace_bytes,
     qwen3_tts_add_rmsnorm,
-    qwen3_tts_rmsnorm,
     qwen3_tts_silu_and_mul,
     quantize_fp8_weight_blocks,
 )
@@ -181,9 +180,9 @@ class TalkerDecodeStep:
         c = self.w.config
         ctx = self.context
         n = self.rows
-        # materialize_decode (executor/talker.py:256-262)
-        torch.add(self.step_embed, F.embedding(self.text_ids, self.w.text_embedding), out=self.residual)
-        qwen3_tts_rmsnorm(self.residual, self.w.layers[0].input_norm, c.rms_eps, out=self.hidden)
+        # materialize_decode (executor/talker.py:256-262) and the first input norm, one launch
+        embed_add_rmsnorm(self.text_ids, self.w.text_embedding, self.step_embed, self.w.layers[0].input_norm,
+                          c.rms_eps, self.residual, self.hidden)
         q_w = c.num_qo_heads * c.head_dim
         kv_w = c.num_kv_heads * c.head_dim
         ws = self.linear_workspace

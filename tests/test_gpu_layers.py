@@ -129,3 +129,44 @@ def test_qk_rope_from_projection_partials_equals_bf16_path(nq, device):
     torch.cuda.synchronize()
     assert torch.equal(q_out, q)
     assert torch.equal(cache_a, cache_b)
+
+
+def test_embed_add_rmsnorm_equals_gather_add_then_norm(nq, device):
+    """The talker step's input (executor/talker.py:256-262: step embedding + text embedding of the
+    step's text token) and the first layer's input norm in one launch give the same bits as the
+    gather, the bf16 add and the RMSNorm kernel run one after another; an id outside the table is
+    reported in status."""
+    import torch.nn.functional as F
+
+    from nari_qwen3_tts_amd import _lib
+    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, qwen3_tts_rmsnorm
+
+    g = torch.Generator(device=device)
+    g.manual_seed(3)
+    vocab, width = 1000, 2048
+    for rows in (1, 64, 37):
+        table = torch.randn(vocab, width, generator=g, device=device).to(torch.bfloat16)
+        # a strided addend: the first `width` columns of a wider buffer
+        wide = torch.randn(rows, width + 64, generator=g, device=device).to(torch.bfloat16)
+        addend = wide[:, :width]
+        weight = (torch.rand(width, generator=g, device=device) + 0.5).to(torch.bfloat16)
+        ids = torch.randint(0, vocab, (rows,), generator=g, device=device)
+        residual = torch.empty(rows, width, dtype=torch.bfloat16, device=device)
+        out = torch.empty_like(residual)
+        status = torch.zeros(1, dtype=torch.int32, device=device)
+        embed_add_rmsnorm(ids, table, addend, weight, 1e-6, residual, out, status)
+        want_r = torch.add(addend, F.embedding(ids, table))
+        want_o = qwen3_tts_rmsnorm(want_r, weight, 1e-6)
+        assert torch.equal(residual, want_r)
+        assert torch.equal(out, want_o)
+        assert int(status.item()) == 0
+        # fp32 restatement of the same math (model/layers.py:110-115)
+        rf = want_r.float()
+        ref = (rf * torch.rsqrt(rf.square().mean(-1, keepdim=True) + 1e-6) * weight.float()).to(torch.bfloat16)
+        assert (out.float() - ref.float()).abs().max().item() <= 2e-2
+    bad = ids.clone()
+    bad[-1] = vocab
+    embed_add_rmsnorm(bad, table, addend, weight, 1e-6, residual, out, status)
+    assert int(status.item()) == _lib.NQ_ERR_INVALID_ARGUMENT
+    # the rows with valid ids are unaffected
+    assert torch.equal(residual[:-1], want_r[:-1])
