@@ -139,7 +139,11 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     for (int q = 0; q < kXVec; ++q) {
         const int v = rot_of(threadIdx.x + q * kGemmThreads);
         const int row = v / kVecPerRow, col = v % kVecPerRow;
-        xr[q] = row < M ? *reinterpret_cast<const uint4 *>(x + row * x_s0 + k0 + col * 8) : make_uint4(0, 0, 0, 0);
+        // unconditional load (rows past M read row 0, M >= 1) so that no branch
+        // splits the prologue: the weight loads below must stay ahead of the
+        // barrier, and the compiler only keeps them there in straight-line code
+        const uint4 t = *reinterpret_cast<const uint4 *>(x + (row < M ? row : 0) * x_s0 + k0 + col * 8);
+        xr[q] = row < M ? t : make_uint4(0, 0, 0, 0);
     }
 
     // 2. the first band's weights, all in flight together
@@ -156,14 +160,18 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     }
     __syncthreads();
 
-    // 3. bands in pairs: the loads of one buffer fly while the other is used
-    for (int b = 0; b < nb; b += 2) {
+    // 3. bands in pairs: the loads of one buffer fly while the other is used.
+    // The body runs at least once (nb >= 1): with a loop that might run zero
+    // times the compiler sinks the first band's loads into the loop guard,
+    // after the barrier, and the weight stream then waits for the X block.
+    for (int b = 0;; b += 2) {
         const int col_a = (band0 + b) * 64 + wave * 16;
         if (b + 1 < nb) gemm_load_w<KS, kPacked>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
         gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part, bias);
         if (b + 1 >= nb) break;
         if (b + 2 < nb) gemm_load_w<KS, kPacked>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
         gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part, bias);
+        if (b + 2 >= nb) break;
     }
 }
 

@@ -8,15 +8,17 @@
 namespace nq {
 
 // x[0..8) = sum over s = 0..S-1 (in that order) of p[s * plane + 0..8); the
-// planes are fp32, 16-byte aligned at p; four planes are loaded per round.
+// planes are fp32, 16-byte aligned at p; kGroup planes are loaded per round
+// (each round waits for its loads before the next is issued).
+template <int kGroup = 4>
 __device__ __forceinline__ void sum_partials8(const float *__restrict__ p, int S, int64_t plane,
                                               float (&x)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    for (int s0 = 0; s0 < S; s0 += 4) {
-        float4 v[4][2];
+    for (int s0 = 0; s0 < S; s0 += kGroup) {
+        float4 v[kGroup][2];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kGroup; ++u) {
             if (s0 + u < S) {
                 const float4 *q = reinterpret_cast<const float4 *>(p + (s0 + u) * plane);
                 v[u][0] = q[0];
@@ -27,7 +29,7 @@ __device__ __forceinline__ void sum_partials8(const float *__restrict__ p, int S
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kGroup; ++u) {
             if (s0 + u < S) {
                 x[0] += v[u][0].x;
                 x[1] += v[u][0].y;

@@ -44,7 +44,9 @@ struct PartialSrc {
     int64_t plane;  // elements per partial plane
     int64_t s0;     // row stride of a plane
     __device__ __forceinline__ void load8(int64_t row, int col, float (&x)[8]) const {
-        sum_partials8(p + row * s0 + col, S, plane, x);
+        // every plane of the projection in flight at once (up to 16): the norm
+        // runs one workgroup per row, so each round trip is paid in full
+        sum_partials8<16>(p + row * s0 + col, S, plane, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16(x[e]));
     }
@@ -78,7 +80,7 @@ struct Fp8Out {
     int64_t s_s0;
 };
 
-template <typename Src, bool kFp8>
+template <typename Src, bool kFp8, int kVec>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
                    uint16_t *__restrict__ residual, const uint16_t *__restrict__ residual_in, int64_t ri_s0,
@@ -86,23 +88,33 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
     __shared__ float tmp[kNormThreads / kWave];
     const int64_t row = blockIdx.x;
     const int nvec = width / 8;
-    float x[kMaxVec][8], w[kMaxVec][8];
+    float x[kVec][8], w[kVec][8];
     float ss = 0.f;
-    // every load of the row first (hidden, residual, weight), then the math
-    float a[kMaxVec][8], b[kMaxVec][8];
+    // every load of the row first (residual and weight as raw words, then the
+    // hidden operand, whose split-K source waits for its planes), then the math
+    float a[kVec][8], b[kVec][8];
+    uint4 rb[kVec], rw[kVec];
+    // the residual is read from residual_in when given (then only written to residual)
+    const uint16_t *rin = residual_in ? residual_in + row * ri_s0 : residual + row * width;
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
+    for (int i = 0; i < kVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
-            hidden.load8(row, vi * 8, a[i]);
-            // the residual is read from residual_in when given (then only written to residual)
-            const uint16_t *rin = residual_in ? residual_in + row * ri_s0 : residual + row * width;
-            unpack8(*reinterpret_cast<const uint4 *>(rin + vi * 8), b[i]);
-            unpack8(*reinterpret_cast<const uint4 *>(weight + vi * 8), w[i]);
+            rb[i] = *reinterpret_cast<const uint4 *>(rin + vi * 8);
+            rw[i] = *reinterpret_cast<const uint4 *>(weight + vi * 8);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
+    for (int i = 0; i < kVec; ++i) {
+        const int vi = threadIdx.x + i * kNormThreads;
+        if (vi < nvec) {
+            hidden.load8(row, vi * 8, a[i]);
+            unpack8(rb[i], b[i]);
+            unpack8(rw[i], w[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
             uint4 packed;
@@ -117,7 +129,7 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
     }
     const float inv = rsqrtf(norm_block_sum(ss, tmp) / static_cast<float>(width) + eps);
 #pragma unroll
-    for (int i = 0; i < kMaxVec; ++i) {
+    for (int i = 0; i < kVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
             if constexpr (kFp8) {
@@ -202,6 +214,20 @@ silu_mul_kernel(Src gate_up, uint16_t *__restrict__ out, int64_t o_s0, int rows,
     }
 }
 
+// Launch with the fewest 8-column vectors per thread that cover the row, so
+// that a narrow row keeps no registers for vectors it does not have.
+template <typename Src, bool kFp8, typename... Args>
+void launch_add_rmsnorm(int rows, int width, hipStream_t st, Src src, Args... args) {
+    const int nv = (width / 8 + kNormThreads - 1) / kNormThreads;
+    const dim3 grid(rows), block(kNormThreads);
+    if (nv <= 1)
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 1>), grid, block, 0, st, src, args...);
+    else if (nv <= 2)
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 2>), grid, block, 0, st, src, args...);
+    else
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, kMaxVec>), grid, block, 0, st, src, args...);
+}
+
 int silu_grid(int rows, int width) {
     const int64_t total = static_cast<int64_t>(rows) * (width / 8);
     int64_t grid = (total + 255) / 256;
@@ -217,8 +243,8 @@ int launch_add_rmsnorm_partials(const float *part, int S, int rows, int width, u
                                 hipStream_t st) {
     if (width % 8 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
     const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
-    hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, false>), dim3(rows), dim3(kNormThreads), 0, st, src,
-                       hidden_out, ho_s0, residual, nullptr, 0, weight, width, eps, Fp8Out{});
+    launch_add_rmsnorm<PartialSrc, false>(rows, width, st, src, hidden_out, ho_s0, residual, nullptr, 0, weight,
+                                          width, eps, Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -227,8 +253,8 @@ int launch_add_rmsnorm_partials_fp8(const float *part, int S, int rows, int widt
                                     int64_t sx_s0, hipStream_t st) {
     if (width % 128 || width > kNormThreads * 8 * kMaxVec) return NQ_ERR_UNSUPPORTED;
     const PartialSrc src{part, S, static_cast<int64_t>(rows) * width, width};
-    hipLaunchKernelGGL((add_rmsnorm_kernel<PartialSrc, true>), dim3(rows), dim3(kNormThreads), 0, st, src, nullptr,
-                       0, residual, nullptr, 0, weight, width, eps, Fp8Out{xq, xq_s0, sx, sx_s0});
+    launch_add_rmsnorm<PartialSrc, true>(rows, width, st, src, nullptr, 0, residual, nullptr, 0, weight, width,
+                                         eps, Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -249,9 +275,9 @@ extern "C" int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16
     if (!nq::al16(hidden) || !nq::al16(residual) || !nq::al16(weight)) return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     const nq::Bf16Src src{hidden, width};
-    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, false>), dim3(rows), dim3(nq::kNormThreads), 0,
-                       static_cast<hipStream_t>(stream), src, hidden, static_cast<int64_t>(width), residual,
-                       nullptr, 0, weight, width, eps, nq::Fp8Out{});
+    nq::launch_add_rmsnorm<nq::Bf16Src, false>(rows, width, static_cast<hipStream_t>(stream), src, hidden,
+                                               static_cast<int64_t>(width), residual, nullptr, 0, weight, width,
+                                               eps, nq::Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -265,9 +291,9 @@ extern "C" int nq_add_rmsnorm_fp8(const uint16_t *hidden, uint16_t *residual, co
         return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     const nq::Bf16Src src{hidden, width};
-    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::Bf16Src, true>), dim3(rows), dim3(nq::kNormThreads), 0,
-                       static_cast<hipStream_t>(stream), src, nullptr, 0, residual, nullptr, 0, weight, width,
-                       eps, nq::Fp8Out{xq, xq_s0, sx, sx_s0});
+    nq::launch_add_rmsnorm<nq::Bf16Src, true>(rows, width, static_cast<hipStream_t>(stream), src, nullptr, 0,
+                                              residual, nullptr, 0, weight, width, eps,
+                                              nq::Fp8Out{xq, xq_s0, sx, sx_s0});
     return NQ_LAUNCH_STATUS();
 }
 
@@ -306,8 +332,8 @@ extern "C" int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, i
         return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     const nq::GatherSrc src{table, table_s0, ids, num_embeddings, status};
-    hipLaunchKernelGGL((nq::add_rmsnorm_kernel<nq::GatherSrc, false>), dim3(rows), dim3(nq::kNormThreads), 0,
-                       static_cast<hipStream_t>(stream), src, out, static_cast<int64_t>(width), residual, addend,
-                       addend_s0, weight, width, eps, nq::Fp8Out{});
+    nq::launch_add_rmsnorm<nq::GatherSrc, false>(rows, width, static_cast<hipStream_t>(stream), src, out,
+                                                 static_cast<int64_t>(width), residual, addend, addend_s0, weight,
+                                                 width, eps, nq::Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
