@@ -124,26 +124,30 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     return L;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (every lane active):
+// row_shr 1, 2, 4, 8 inside each 16-lane row (lanes shifted in from outside
+// the row add 0), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into
+// rows 2 and 3.  Six DPP adds, no LDS round trips.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 __device__ int plan_block_scan(int v, int *tmp, int *total) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        int o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_scan(v);
     if (lane == kWave - 1) tmp[wave] = incl;
     __syncthreads();
     if (wave == 0) {
         const int nw = blockDim.x / kWave;
-        int w = lane < nw ? tmp[lane] : 0;
-        int wi = w;
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-            int o = __shfl_up(wi, d, kWave);
-            if (lane >= d) wi += o;
-        }
+        const int w = lane < nw ? tmp[lane] : 0;
+        const int wi = wave_incl_scan(w);
         if (lane < nw) tmp[lane] = wi - w;
         if (lane == nw - 1) tmp[kWave] = wi;
     }
@@ -152,6 +156,39 @@ __device__ int plan_block_scan(int v, int *tmp, int *total) {
     *total = tmp[kWave];
     __syncthreads();
     return res;
+}
+
+// Exclusive prefix sums of N values per thread over the workgroup in one
+// pass (three barriers for all N); tmp holds N * (kWave + 1) ints.
+template <int N>
+__device__ void plan_block_scan_n(const int (&v)[N], int *tmp, int (&excl)[N], int (&total)[N]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) incl[i] = wave_incl_scan(v[i]);
+    if (lane == kWave - 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) tmp[i * (kWave + 1) + wave] = incl[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int nw = blockDim.x / kWave;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int w = lane < nw ? tmp[i * (kWave + 1) + lane] : 0;
+            const int wi = wave_incl_scan(w);
+            if (lane < nw) tmp[i * (kWave + 1) + lane] = wi - w;
+            if (lane == nw - 1) tmp[i * (kWave + 1) + kWave] = wi;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        excl[i] = tmp[i * (kWave + 1) + wave] + incl[i] - v[i];
+        total[i] = tmp[i * (kWave + 1) + kWave];
+    }
+    __syncthreads();
 }
 
 // Largest r in [0, n) with off[r] <= x (off non-decreasing, off[0] == 0).
@@ -179,8 +216,9 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     __shared__ int s_boff[kPlanThreads];
     __shared__ int s_dec[kPlanThreads];
     __shared__ unsigned long long s_cand[8];
-    __shared__ int s_tmp[kWave + 1];
-    __shared__ unsigned s_keys[kBinSortCap];
+    __shared__ int s_tmp[3 * (kWave + 1)];
+    __shared__ __attribute__((aligned(16))) unsigned s_keys[kBinSortCap];
+    __shared__ unsigned s_sorted[kBinSortCap];
     __shared__ int4 s_pa[kBinSortCap], s_pb[kBinSortCap];
 
     int32_t *meta = reinterpret_cast<int32_t *>(ws + L.meta);
@@ -193,6 +231,16 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     const bool lead = blockIdx.x == 0;
     int ps_log2 = 0;
     while ((1 << ps_log2) < page_size) ++ps_log2;
+    // Without packed queries row r's query token is r: the lead issues its
+    // position / write-slot loads now, with the row loads, rather than after
+    // the scans.
+    const bool early_pos = lead && !qo_indptr && position_ids && write_pages && write_offsets && tid < n_rows;
+    int64_t e_pos = 0, e_pg = 0, e_off = 0;
+    if (early_pos) {
+        e_pos = position_ids[tid];
+        e_pg = write_pages[tid];
+        e_off = write_offsets[tid];
+    }
     if (tid < n_rows) {
         const int np = kv_indptr[tid + 1] - kv_indptr[tid];
         int last = last_page_len[tid];
@@ -224,16 +272,23 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         return;
     }
 
-    // Decode rows and their key blocks.
-    int is_dec = 0, nblk = 0;
-    if (tid < n_rows && s_qo[tid + 1] - s_qo[tid] == 1) {
-        is_dec = 1;
-        nblk = (s_kvlen[tid] + kBlockTok - 1) / kBlockTok;
-        nblk = nblk < 1 ? 1 : nblk;
+    // Decode rows and their key blocks, and prefill rows' 32-query tiles, in
+    // one scan.
+    int is_dec = 0, nblk = 0, nt = 0;
+    if (tid < n_rows) {
+        const int qo_len = s_qo[tid + 1] - s_qo[tid];
+        if (qo_len == 1) {
+            is_dec = 1;
+            nblk = (s_kvlen[tid] + kBlockTok - 1) / kBlockTok;
+            nblk = nblk < 1 ? 1 : nblk;
+        } else if (qo_len > 1) {
+            nt = (qo_len + kPrefQ - 1) / kPrefQ;
+        }
     }
-    int n_dec, n_blocks;
-    const int dec_idx = plan_block_scan(is_dec, s_tmp, &n_dec);
-    const int boff = plan_block_scan(nblk, s_tmp, &n_blocks);
+    int sc_excl[3], sc_total[3];
+    plan_block_scan_n<3>({is_dec, nblk, nt}, s_tmp, sc_excl, sc_total);
+    const int dec_idx = sc_excl[0], boff = sc_excl[1], t0_tiles = sc_excl[2];
+    const int n_dec = sc_total[0], n_blocks = sc_total[1], n_ptiles = sc_total[2];
     s_dec[tid] = dec_idx;
     s_boff[tid] = boff;
     __syncthreads();
@@ -260,10 +315,9 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         const int NB = bins_per_head(num_kv_heads);
         const int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
         const int k = is_dec ? (nblk + C - 1) / C : 0;
-        int P;
-        const int p0 = plan_block_scan(k, s_tmp, &P);
-        int n_split;
-        plan_block_scan(k > 1 ? 1 : 0, s_tmp, &n_split);
+        int pc_excl[2], pc_total[2];
+        plan_block_scan_n<2>({k, k > 1 ? 1 : 0}, s_tmp, pc_excl, pc_total);
+        const int p0 = pc_excl[0], P = pc_total[0], n_split = pc_total[1];
         const int slots = (P + NB - 1) / NB;
         if (P > L.max_pieces || P > kBinSortCap || NB + 1 > 511) {
             fail(NQ_ERR_CAPACITY);
@@ -277,16 +331,26 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             const int tok = s_qo[tid];
             rope.x = tok;
             if (position_ids && write_pages && write_offsets) {
-                const int64_t pos = position_ids[tok], pg = write_pages[tok], off = write_offsets[tok];
+                const int64_t pos = early_pos ? e_pos : position_ids[tok];
+                const int64_t pg = early_pos ? e_pg : write_pages[tok];
+                const int64_t off = early_pos ? e_off : write_offsets[tok];
                 const bool ok = pos >= 0 && pos <= 0x7fffffff && pg >= 0 && pg <= 0x7fffffff && off >= 0 &&
                                 off <= 0x7fffffff;
                 rope = make_int4(tok, ok ? static_cast<int>(pos) : 0, ok ? static_cast<int>(pg) : -1,
                                  ok ? static_cast<int>(off) : 0);
             }
         }
+        // piece i covers blocks [i * nblk / k, (i + 1) * nblk / k); 32-bit
+        // arithmetic where the product fits (an inlined 64-bit division is slow)
+        const bool narrow = nblk < (1 << 20) && k <= (1 << 11);
+        auto cut = [&](int i) {
+            return narrow ? static_cast<int>(static_cast<unsigned>(i) * static_cast<unsigned>(nblk) /
+                                             static_cast<unsigned>(k))
+                          : static_cast<int>(static_cast<int64_t>(i) * nblk / k);
+        };
         for (int i = 0; i < k; ++i) {
-            const int first = boff + static_cast<int>(static_cast<int64_t>(i) * nblk / k);
-            const int last = boff + static_cast<int>(static_cast<int64_t>(i + 1) * nblk / k);
+            const int first = boff + cut(i);
+            const int last = boff + cut(i + 1);
             const int4 pc = make_int4(dec_idx, first, last - first, k > 1 ? (p0 << 9) | k : -1);
             pieces[p0 + i] = pc;
             s_pa[p0 + i] = pc;  // p0 + i < P <= kBinSortCap (checked above)
@@ -298,7 +362,27 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         int np2 = 1;
         while (np2 < P) np2 <<= 1;
         for (int i = P + tid; i < np2; i += blockDim.x) s_keys[i] = 0xFFFFFFFFu;
-        if (np2 <= kWave) {
+        const unsigned *sorted = s_keys;
+        if (np2 > kWave) {
+            // more than 64 pieces: each key's place is the count of smaller keys
+            // (the keys are distinct: the low half is the piece id), one pass
+            // with one barrier instead of a log^2 network of them
+            __syncthreads();
+            // (four keys per LDS read; the padding keys up to np2 are all ones,
+            // never below a piece key)
+            const uint4 *keys4 = reinterpret_cast<const uint4 *>(s_keys);
+            for (int i = tid; i < P; i += blockDim.x) {
+                const unsigned key = s_keys[i];
+                int rank = 0;
+                for (int j = 0; j < np2 / 4; ++j) {
+                    const uint4 q = keys4[j];
+                    rank += (q.x < key ? 1 : 0) + (q.y < key ? 1 : 0) + (q.z < key ? 1 : 0) + (q.w < key ? 1 : 0);
+                }
+                s_sorted[rank] = key;
+            }
+            sorted = s_sorted;
+            np2 = 1;  // the LDS network below has nothing left to do
+        } else {
             // up to 64 pieces: one wave sorts them in registers (lane i holds key i), no barriers
             __syncthreads();
             if (tid < kWave) {
@@ -335,7 +419,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         for (int e = tid; e < NB * kBinMaxSlots; e += blockDim.x) {
             const int bin = e / kBinMaxSlots, round = e % kBinMaxSlots;
             const int i = round * NB + ((round & 1) ? NB - 1 - bin : bin);
-            const int pid = round < slots && i < P ? static_cast<int>(s_keys[i] & 0xFFFFu) : -1;
+            const int pid = round < slots && i < P ? static_cast<int>(sorted[i] & 0xFFFFu) : -1;
             table[3 * e] = pid >= 0 ? s_pa[pid] : make_int4(-1, 0, 0, -1);
             table[3 * e + 1] = pid >= 0 ? s_pb[pid] : make_int4(0, 0, -1, 0);
             table[3 * e + 2] = make_int4(pid, 0, 0, 0);
@@ -345,11 +429,16 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             meta[kMetaBinSlots] = slots;
             meta[kMetaSplitRows] = n_split;
         }
-        __syncthreads();
+        // no barrier here: nothing below reads the sort's LDS, and a barrier
+        // would wait for the table's stores to complete
     }
 
-    const int gstride = gridDim.x * blockDim.x;
-    for (int b = blockIdx.x * blockDim.x + tid; b < n_blocks; b += gstride) {
+    // the block table: the other workgroups when there are any (the lead has
+    // the bins and the row tables to write)
+    const int fillers = gridDim.x > 1 ? gridDim.x - 1 : 1;
+    const int filler = gridDim.x > 1 ? static_cast<int>(blockIdx.x) - 1 : 0;
+    const int gstride = fillers * blockDim.x;
+    for (int b = filler * blockDim.x + tid; filler >= 0 && b < n_blocks; b += gstride) {
         const int r = find_le(s_boff, n_rows, b);
         const int tok0 = (b - s_boff[r]) * kBlockTok;
         int ntok = s_kvlen[r] - tok0;
@@ -370,13 +459,6 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     // Prefill rows: 32-query tiles {first query, queries, first page offset,
     // key limit of the first query (bottom-right causal)}.
     {
-        int nt = 0;
-        if (tid < n_rows) {
-            const int qo_len = s_qo[tid + 1] - s_qo[tid];
-            if (qo_len > 1) nt = (qo_len + kPrefQ - 1) / kPrefQ;
-        }
-        int n_ptiles;
-        const int t0 = plan_block_scan(nt, s_tmp, &n_ptiles);
         if (n_ptiles > L.max_ptiles) {
             fail(NQ_ERR_CAPACITY);
             return;
@@ -384,10 +466,25 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         int4 *ptiles = reinterpret_cast<int4 *>(ws + L.ptiles);
         for (int t = 0; t < nt; ++t) {
             const int qo_len = s_qo[tid + 1] - s_qo[tid];
-            ptiles[t0 + t] = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
-                                       s_kvlen[tid] - qo_len + t * kPrefQ + 1);
+            ptiles[t0_tiles + t] = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
+                                             s_kvlen[tid] - qo_len + t * kPrefQ + 1);
         }
         if (tid == 0) meta[kMetaPTiles] = n_ptiles;
+    }
+    if (n_ptiles == 0) {
+        // no prefill rows: no query has key chunks, so every chunk offset is 0
+        // and the chunk size is the smallest candidate (what the general path
+        // below computes for such a batch, without its scans)
+        for (int q = tid; q <= T; q += blockDim.x) chunk_indptr[q] = 0;
+        if (tid == 0) {
+            meta[kMetaChunks] = 0;
+            meta[kMetaChunkTok] = kMinChunkTokens < page_size ? page_size : kMinChunkTokens;
+            meta[kMetaQueries] = T;
+            meta[kMetaDecRows] = n_dec;
+            meta[kMetaBlocks] = n_blocks;
+            meta[kMetaStatus] = NQ_OK;
+        }
+        return;
     }
 
     // Prefill queries: key chunks per query.
