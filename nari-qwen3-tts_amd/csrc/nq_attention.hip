@@ -124,20 +124,6 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     return L;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (every lane active):
-// row_shr 1, 2, 4, 8 inside each 16-lane row (lanes shifted in from outside
-// the row add 0), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into
-// rows 2 and 3.  Six DPP adds, no LDS round trips.
-__device__ __forceinline__ int wave_incl_scan(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
-    return v;
-}
-
 __device__ int plan_block_scan(int v, int *tmp, int *total) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -156,39 +142,6 @@ __device__ int plan_block_scan(int v, int *tmp, int *total) {
     *total = tmp[kWave];
     __syncthreads();
     return res;
-}
-
-// Exclusive prefix sums of N values per thread over the workgroup in one
-// pass (three barriers for all N); tmp holds N * (kWave + 1) ints.
-template <int N>
-__device__ void plan_block_scan_n(const int (&v)[N], int *tmp, int (&excl)[N], int (&total)[N]) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    int incl[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) incl[i] = wave_incl_scan(v[i]);
-    if (lane == kWave - 1) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) tmp[i * (kWave + 1) + wave] = incl[i];
-    }
-    __syncthreads();
-    if (wave == 0) {
-        const int nw = blockDim.x / kWave;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const int w = lane < nw ? tmp[i * (kWave + 1) + lane] : 0;
-            const int wi = wave_incl_scan(w);
-            if (lane < nw) tmp[i * (kWave + 1) + lane] = wi - w;
-            if (lane == nw - 1) tmp[i * (kWave + 1) + kWave] = wi;
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        excl[i] = tmp[i * (kWave + 1) + wave] + incl[i] - v[i];
-        total[i] = tmp[i * (kWave + 1) + kWave];
-    }
-    __syncthreads();
 }
 
 // Largest r in [0, n) with off[r] <= x (off non-decreasing, off[0] == 0).
@@ -286,7 +239,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         }
     }
     int sc_excl[3], sc_total[3];
-    plan_block_scan_n<3>({is_dec, nblk, nt}, s_tmp, sc_excl, sc_total);
+    block_exclusive_scan_n<3>({is_dec, nblk, nt}, s_tmp, sc_excl, sc_total);
     const int dec_idx = sc_excl[0], boff = sc_excl[1], t0_tiles = sc_excl[2];
     const int n_dec = sc_total[0], n_blocks = sc_total[1], n_ptiles = sc_total[2];
     s_dec[tid] = dec_idx;
@@ -316,7 +269,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         const int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
         const int k = is_dec ? (nblk + C - 1) / C : 0;
         int pc_excl[2], pc_total[2];
-        plan_block_scan_n<2>({k, k > 1 ? 1 : 0}, s_tmp, pc_excl, pc_total);
+        block_exclusive_scan_n<2>({k, k > 1 ? 1 : 0}, s_tmp, pc_excl, pc_total);
         const int p0 = pc_excl[0], P = pc_total[0], n_split = pc_total[1];
         const int slots = (P + NB - 1) / NB;
         if (P > L.max_pieces || P > kBinSortCap || NB + 1 > 511) {

@@ -72,6 +72,54 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (every lane active):
+// row_shr 1, 2, 4, 8 inside each 16-lane row (lanes shifted in from outside
+// the row add 0), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into
+// rows 2 and 3.  Six DPP adds, no LDS round trips.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
+// Exclusive prefix sums of N values per thread over the workgroup (all of its
+// threads active) in one pass: three barriers for all N.  tmp holds
+// N * (kWave + 1) ints; total[i] receives the workgroup sum of value i.
+template <int N>
+__device__ void block_exclusive_scan_n(const int (&v)[N], int *tmp, int (&excl)[N], int (&total)[N]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) incl[i] = wave_incl_scan(v[i]);
+    if (lane == kWave - 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) tmp[i * (kWave + 1) + wave] = incl[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int nw = blockDim.x / kWave;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int w = lane < nw ? tmp[i * (kWave + 1) + lane] : 0;
+            const int wi = wave_incl_scan(w);
+            if (lane < nw) tmp[i * (kWave + 1) + lane] = wi - w;  // exclusive wave offsets
+            if (lane == nw - 1) tmp[i * (kWave + 1) + kWave] = wi;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        excl[i] = tmp[i * (kWave + 1) + wave] + incl[i] - v[i];
+        total[i] = tmp[i * (kWave + 1) + kWave];
+    }
+    __syncthreads();
+}
+
 template <int Width>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll

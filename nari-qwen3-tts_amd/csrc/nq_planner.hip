@@ -12,38 +12,6 @@ namespace {
 
 constexpr int kPlanThreads = 1024;  // also the largest capture bucket supported
 
-// Block-wide exclusive scan of one int per thread.  Returns the exclusive
-// prefix; *total receives the block sum.  `tmp` holds >= kPlanThreads/64 ints.
-__device__ int block_exclusive_scan(int v, int *tmp, int *total) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        int o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
-    if (lane == kWave - 1) tmp[wave] = incl;
-    __syncthreads();
-    if (wave == 0) {
-        const int nw = blockDim.x / kWave;
-        int w = lane < nw ? tmp[lane] : 0;
-        int wi = w;
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-            int o = __shfl_up(wi, d, kWave);
-            if (lane >= d) wi += o;
-        }
-        if (lane < nw) tmp[lane] = wi - w;  // exclusive wave offsets
-        if (lane == nw - 1) tmp[kWave] = wi;
-    }
-    __syncthreads();
-    const int res = tmp[wave] + incl - v;
-    *total = tmp[kWave];
-    __syncthreads();
-    return res;
-}
-
 // Largest r in [0, n) with off[r] <= x (off non-decreasing, off[0] == 0).
 __device__ __forceinline__ int find_row(const int *off, int n, int x) {
     int lo = 0, hi = n;  // invariant: off[lo] <= x, answer in [lo, hi)
@@ -68,28 +36,34 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
     __shared__ int s_page_off[kPlanThreads];
     __shared__ int s_tok_off[kPlanThreads];
     __shared__ int s_miss_off[kPlanThreads];
-    __shared__ int s_tmp[kWave + 1];
+    // the rows' descriptors, read once here for the fill loops below
+    __shared__ int s_seq[kPlanThreads], s_prior[kPlanThreads], s_trow[kPlanThreads], s_pos[kPlanThreads];
+    __shared__ int s_tmp[5 * (kWave + 1)];
 
     const int r = threadIdx.x;
-    int npages = 0, ntok = 0, miss = 0, adv_real = 0, bad = 0;
+    int npages = 0, ntok = 0, miss = 0, adv_real = 0, bad = 0, total = 0;
     if (r < n_rows) {
-        const int total = seq_len[r] + advance[r];
+        const int sl = seq_len[r], adv = advance[r], pr = prior_pages[r];
+        s_seq[r] = sl;
+        s_prior[r] = pr;
+        s_trow[r] = table_row[r];
+        s_pos[r] = pos_start[r];
+        total = sl + adv;
         const int needed = (total + page_size - 1) / page_size;
-        miss = needed - prior_pages[r];
-        if (miss < 0 || advance[r] < 1) bad = 1;
+        miss = needed - pr;
+        if (miss < 0 || adv < 1) bad = 1;
         npages = needed;
-        ntok = advance[r];
-        adv_real = advance[r];
+        ntok = adv;
+        adv_real = adv;
     } else if (r < capture_rows) {
         npages = 1;
         ntok = prefill ? 0 : 1;
     }
-    int total_pages, total_tok, total_miss, sum_adv, any_bad;
-    const int page_off = block_exclusive_scan(npages, s_tmp, &total_pages);
-    const int tok_off = block_exclusive_scan(ntok, s_tmp, &total_tok);
-    const int miss_off = block_exclusive_scan(miss > 0 ? miss : 0, s_tmp, &total_miss);
-    block_exclusive_scan(adv_real, s_tmp, &sum_adv);
-    block_exclusive_scan(bad, s_tmp, &any_bad);
+    // page, token and new-page offsets, the real advance and the error flag in one scan
+    int ex[5], tot[5];
+    block_exclusive_scan_n<5>({npages, ntok, miss > 0 ? miss : 0, adv_real, bad}, s_tmp, ex, tot);
+    const int page_off = ex[0], tok_off = ex[1], miss_off = ex[2];
+    const int total_pages = tot[0], total_tok = tot[1], total_miss = tot[2], sum_adv = tot[3], any_bad = tot[4];
     s_page_off[r] = page_off;
     s_tok_off[r] = tok_off;
     s_miss_off[r] = miss_off;
@@ -110,7 +84,6 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
         kv_indptr[r + 1] = page_off + npages;
         if (r == 0) kv_indptr[0] = 0;
         if (r < n_rows) {
-            const int total = seq_len[r] + advance[r];
             const int rem = total % page_size;
             last_page_len[r] = rem ? rem : page_size;
         } else {
@@ -132,8 +105,8 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
         const int i = static_cast<int>(j) - s_page_off[row];
         int page;
         if (row < n_rows) {
-            const int prior = prior_pages[row];
-            int32_t *trow = page_table + static_cast<int64_t>(table_row[row]) * table_stride;
+            const int prior = s_prior[row];
+            int32_t *trow = page_table + static_cast<int64_t>(s_trow[row]) * table_stride;
             if (i < prior) {
                 page = trow[i];
             } else {
@@ -153,15 +126,15 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
             const int row = find_row(s_tok_off, capture_rows, static_cast<int>(t));
             const int o = static_cast<int>(t) - s_tok_off[row];
             if (row < n_rows) {
-                const int abs_pos = seq_len[row] + o;
+                const int abs_pos = s_seq[row] + o;
                 const int pidx = abs_pos / page_size;
-                const int prior = prior_pages[row];
+                const int prior = s_prior[row];
                 if (pidx < prior)
-                    wpage = page_table[static_cast<int64_t>(table_row[row]) * table_stride + pidx];
+                    wpage = page_table[static_cast<int64_t>(s_trow[row]) * table_stride + pidx];
                 else
                     wpage = free_pages[s_miss_off[row] + (pidx - prior)];
                 woff = abs_pos % page_size;
-                pos = static_cast<int64_t>(pos_start[row]) + o;
+                pos = static_cast<int64_t>(s_pos[row]) + o;
             } else {  // decode padding row: scratch slot 0 of its own page
                 wpage = scratch_pages[row];
                 woff = 0;
