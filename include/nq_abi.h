@@ -216,6 +216,23 @@ int nq_sample_counter(const void *logits, int logits_dtype, int64_t logits_s0, i
                       int eos_id, const uint8_t *suppress_eos, int update_seen, int64_t *tokens, void *stream);
 
 /*
+ * nq_sample_counter reading the logits from a projection's fp32 split-K
+ * planes [splits][rows][row_stride] (nq_linear with NQ_EPI_PARTIALS): each
+ * logit is the planes' sum in plane order rounded to bf16, the value
+ * nq_linear's own reduction stores, so the tokens are those of nq_linear
+ * followed by nq_sample_counter, in one launch instead of two (the talker's
+ * codec-head logits and their draw, executor/talker.py:173-183, 240-243,
+ * 373).  The bf16 logits also go to logits_out (row stride out_s0) when it is
+ * not NULL.  splits in [1, 64].
+ */
+int nq_sample_counter_planes(const float *planes, int splits, int64_t row_stride, int rows, int vocab,
+                             const float *temperature, const int32_t *top_k, const float *top_p,
+                             const float *repetition_penalty, uint8_t *seen, int64_t seen_s0, const int64_t *seed,
+                             int64_t seed_stride, const int64_t *offset, int64_t offset_stride, int mask_from,
+                             int eos_id, const uint8_t *suppress_eos, int update_seen, uint16_t *logits_out,
+                             int64_t out_s0, int64_t *tokens, void *stream);
+
+/*
  * Uniform draws in [0,1) from (seed, offset) counters with Philox-4x32-10
  * (Salmon et al., SC'11): key = seed, counter = (offset, 0); u = (x0 >> 8) * 2^-24.
  * Stands in for the stateless (seed, offset) draws of the reference

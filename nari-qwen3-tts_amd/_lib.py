@@ -56,6 +56,8 @@ _SIGNATURES: dict[str, list] = {
                                        _I, _I, _F, _P, _L, _L, _I, _I, _P, _L, _P, _P],
     "nq_sample": [_P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P, _I, _I, _P, _I, _P, _P],
     "nq_sample_counter": [_P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P, _L, _P, _L, _I, _I, _P, _I, _P, _P],
+    "nq_sample_counter_planes": [_P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _L, _P, _L, _P, _L, _I, _I, _P, _I, _P, _L,
+                                 _P, _P],
     "nq_uniforms_from_counter": [_P, _L, _P, _L, _I, _P, _P],
     "nq_add_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "nq_embed_add_rmsnorm": [_P, _P, _L, _L, _P, _L, _P, _I, _I, _F, _P, _P, _P, _P],

@@ -23,6 +23,7 @@
 // nq_exp is Cody-Waite range reduction (ln 2 split as in Cephes' expf) with a
 // degree-7 Taylor polynomial in Horner form; inputs below -87 give 0.
 #include "nq_common.h"
+#include "nq_internal.h"
 
 namespace nq {
 namespace {
@@ -134,7 +135,11 @@ __device__ __forceinline__ float counter_uniform(int64_t seed, int64_t offset) {
     return static_cast<float>(x >> 8) * (1.0f / 16777216.0f);
 }
 
-template <typename InT>
+// kPlanes: `logits` is `splits` fp32 split-K planes of a projection, `plane`
+// elements apart; each logit is their sum in plane order rounded to bf16 (the
+// value the projection's reduction would store), also written to logits_out
+// (bf16, row stride out_s0) when that is given.
+template <typename InT, bool kPlanes>
 __global__ void __launch_bounds__(kSampThreads)
 sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
               const float *__restrict__ temperature, const int32_t *__restrict__ top_k,
@@ -142,7 +147,8 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
               uint8_t *__restrict__ seen, int64_t seen_s0, const float *__restrict__ uniforms,
               const int64_t *__restrict__ seed, int64_t seed_stride, const int64_t *__restrict__ offset,
               int64_t offset_stride, int mask_from, int eos_id, const uint8_t *__restrict__ suppress_eos,
-              int update_seen, int64_t *__restrict__ tokens) {
+              int update_seen, int64_t *__restrict__ tokens, int splits, int64_t plane,
+              uint16_t *__restrict__ logits_out, int64_t out_s0) {
     __shared__ float s_val[kMaxVocab];
     __shared__ uint64_t s_sort[kMaxVocab];
     __shared__ uint32_t s_hist[2][256];
@@ -169,7 +175,9 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
     {
         // whole 8-id groups as one vector load each when the rows allow it
         const bool vec = vocab % 8 == 0 && reinterpret_cast<uintptr_t>(lrow) % (8 * sizeof(InT)) == 0 &&
-                         (!srow || reinterpret_cast<uintptr_t>(srow) % 8 == 0);
+                         (!srow || reinterpret_cast<uintptr_t>(srow) % 8 == 0) &&
+                         (!kPlanes || (plane % 8 == 0 && (!logits_out || (out_s0 % 8 == 0 &&
+                                                          reinterpret_cast<uintptr_t>(logits_out) % 16 == 0))));
         float x[kSampPer];
         uint8_t sn[kSampPer];
 #pragma unroll
@@ -177,7 +185,21 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
             const int id0 = (tid + h * kSampThreads) * 8;
             if (vec) {
                 if (id0 < vocab) {
-                    load_logits8<InT>(lrow + id0, &x[h * 8]);
+                    if constexpr (kPlanes) {
+                        float t[8];
+                        sum_partials8<4>(reinterpret_cast<const float *>(lrow) + id0, splits, plane, t);
+                        uint4 o;
+                        o.x = pack2_bf16(t[0], t[1]);
+                        o.y = pack2_bf16(t[2], t[3]);
+                        o.z = pack2_bf16(t[4], t[5]);
+                        o.w = pack2_bf16(t[6], t[7]);
+                        if (logits_out) *reinterpret_cast<uint4 *>(logits_out + row * out_s0 + id0) = o;
+                        unpack8(o, t);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) x[h * 8 + e] = t[e];
+                    } else {
+                        load_logits8<InT>(lrow + id0, &x[h * 8]);
+                    }
                     const uint2 m = srow ? *reinterpret_cast<const uint2 *>(srow + id0) : make_uint2(0u, 0u);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) sn[h * 8 + e] = static_cast<uint8_t>((e < 4 ? m.x : m.y) >> (8 * (e % 4)));
@@ -192,7 +214,19 @@ sample_kernel(const InT *__restrict__ logits, int64_t logits_s0, int vocab,
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int id = id0 + e;
-                    x[h * 8 + e] = id < vocab ? load_logit<InT>(lrow + id) : 0.f;
+                    if constexpr (kPlanes) {
+                        float acc = 0.f;
+                        if (id < vocab) {
+                            for (int sp = 0; sp < splits; ++sp)
+                                acc += reinterpret_cast<const float *>(lrow)[sp * plane + id];
+                            const uint16_t b = f32_to_bf16(acc);
+                            if (logits_out) logits_out[row * out_s0 + id] = b;
+                            acc = bf16_to_f32(b);
+                        }
+                        x[h * 8 + e] = acc;
+                    } else {
+                        x[h * 8 + e] = id < vocab ? load_logit<InT>(lrow + id) : 0.f;
+                    }
                     sn[h * 8 + e] = (srow && id < vocab) ? srow[id] : 0;
                 }
             }
@@ -434,7 +468,7 @@ int launch_sample(const void *logits, int logits_dtype, int64_t logits_s0, int r
                   const float *repetition_penalty, uint8_t *seen, int64_t seen_s0, const float *uniforms,
                   const int64_t *seed, int64_t seed_stride, const int64_t *offset, int64_t offset_stride,
                   int mask_from, int eos_id, const uint8_t *suppress_eos, int update_seen, int64_t *tokens,
-                  void *stream) {
+                  void *stream, int splits = 0, uint16_t *logits_out = nullptr, int64_t out_s0 = 0) {
     NQ_CHECK_ARG(logits && temperature && top_k && top_p && tokens);
     NQ_CHECK_ARG(uniforms || (seed && offset));
     NQ_CHECK_ARG(rows >= 0 && vocab >= 1);
@@ -442,16 +476,25 @@ int launch_sample(const void *logits, int logits_dtype, int64_t logits_s0, int r
     if (vocab > nq::kMaxVocab) return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (logits_dtype == NQ_F32) {
-        hipLaunchKernelGGL(nq::sample_kernel<float>, dim3(rows), dim3(nq::kSampThreads), 0, s,
-                           static_cast<const float *>(logits), logits_s0, vocab, temperature, top_k, top_p,
-                           repetition_penalty, seen, seen_s0, uniforms, seed, seed_stride, offset, offset_stride,
-                           mask_from, eos_id, suppress_eos, update_seen, tokens);
+    const dim3 grid(rows), block(nq::kSampThreads);
+    if (splits > 0) {
+        // fp32 planes [splits][rows][logits_s0]
+        const int64_t plane = static_cast<int64_t>(rows) * logits_s0;
+        hipLaunchKernelGGL((nq::sample_kernel<float, true>), grid, block, 0, s, static_cast<const float *>(logits),
+                           logits_s0, vocab, temperature, top_k, top_p, repetition_penalty, seen, seen_s0, uniforms,
+                           seed, seed_stride, offset, offset_stride, mask_from, eos_id, suppress_eos, update_seen,
+                           tokens, splits, plane, logits_out, out_s0);
+    } else if (logits_dtype == NQ_F32) {
+        hipLaunchKernelGGL((nq::sample_kernel<float, false>), grid, block, 0, s, static_cast<const float *>(logits),
+                           logits_s0, vocab, temperature, top_k, top_p, repetition_penalty, seen, seen_s0, uniforms,
+                           seed, seed_stride, offset, offset_stride, mask_from, eos_id, suppress_eos, update_seen,
+                           tokens, 0, int64_t{0}, static_cast<uint16_t *>(nullptr), int64_t{0});
     } else if (logits_dtype == NQ_BF16) {
-        hipLaunchKernelGGL(nq::sample_kernel<uint16_t>, dim3(rows), dim3(nq::kSampThreads), 0, s,
+        hipLaunchKernelGGL((nq::sample_kernel<uint16_t, false>), grid, block, 0, s,
                            static_cast<const uint16_t *>(logits), logits_s0, vocab, temperature, top_k, top_p,
                            repetition_penalty, seen, seen_s0, uniforms, seed, seed_stride, offset, offset_stride,
-                           mask_from, eos_id, suppress_eos, update_seen, tokens);
+                           mask_from, eos_id, suppress_eos, update_seen, tokens, 0, int64_t{0},
+                           static_cast<uint16_t *>(nullptr), int64_t{0});
     } else {
         return NQ_ERR_UNSUPPORTED;
     }
@@ -482,6 +525,20 @@ extern "C" int nq_sample_counter(const void *logits, int logits_dtype, int64_t l
     return launch_sample(logits, logits_dtype, logits_s0, rows, vocab, temperature, top_k, top_p,
                          repetition_penalty, seen, seen_s0, nullptr, seed, seed_stride, offset, offset_stride,
                          mask_from, eos_id, suppress_eos, update_seen, tokens, stream);
+}
+
+extern "C" int nq_sample_counter_planes(const float *planes, int splits, int64_t row_stride, int rows, int vocab,
+                                        const float *temperature, const int32_t *top_k, const float *top_p,
+                                        const float *repetition_penalty, uint8_t *seen, int64_t seen_s0,
+                                        const int64_t *seed, int64_t seed_stride, const int64_t *offset,
+                                        int64_t offset_stride, int mask_from, int eos_id, const uint8_t *suppress_eos,
+                                        int update_seen, uint16_t *logits_out, int64_t out_s0, int64_t *tokens,
+                                        void *stream) {
+    NQ_CHECK_ARG(seed && offset && planes && splits >= 1 && splits <= 64 && row_stride >= vocab);
+    NQ_CHECK_ARG(!logits_out || out_s0 >= vocab);
+    return launch_sample(planes, NQ_F32, row_stride, rows, vocab, temperature, top_k, top_p, repetition_penalty,
+                         seen, seen_s0, nullptr, seed, seed_stride, offset, offset_stride, mask_from, eos_id,
+                         suppress_eos, update_seen, tokens, stream, splits, logits_out, out_s0);
 }
 
 extern "C" int nq_uniforms_from_counter(const int64_t *seed, int64_t seed_stride,

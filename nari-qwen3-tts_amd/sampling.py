@@ -49,7 +49,17 @@ def _sample(
     suppress_eos: torch.Tensor | None = None,
     update_seen: bool = False,
     out: torch.Tensor | None = None,
+    planes: torch.Tensor | None = None,
+    logits_out: torch.Tensor | None = None,
 ) -> torch.Tensor:
+    if planes is not None:
+        # fp32 split-K planes [S, rows, vocab] of the projection that makes the logits
+        if planes.dtype != torch.float32 or planes.ndim != 3 or not planes.is_contiguous():
+            raise TypeError("planes must be a contiguous float32 [splits, rows, vocabulary] tensor")
+        logits = planes[0]
+        if logits_out is not None and (logits_out.dtype != torch.bfloat16 or logits_out.shape != logits.shape
+                                       or logits_out.stride(1) != 1):
+            raise ValueError("logits_out must be a bf16 [rows, vocabulary] tensor with contiguous rows")
     if logits.ndim != 2 or logits.shape[0] < 1:
         raise ValueError("logits must have shape (rows, vocabulary)")
     rows, vocab = logits.shape
@@ -89,14 +99,20 @@ def _sample(
     if suppress_eos is not None and (suppress_eos.dtype != torch.bool or suppress_eos.shape != (rows,)):
         raise ValueError("suppress_eos must be a bool row vector")
     _lib.require_device(logits, temperature, top_k, top_p, uniforms, seed, offset, repetition_penalty, seen_token_mask,
-                        suppress_eos)
+                        suppress_eos, logits_out)
     tokens = torch.empty(rows, dtype=torch.long, device=logits.device) if out is None else out
     head = (logits.data_ptr(), code, logits.stride(0), rows, vocab, temperature.data_ptr(), top_k.data_ptr(),
             top_p.data_ptr(), _lib.ptr(repetition_penalty), _lib.ptr(seen_token_mask),
             0 if seen_token_mask is None else seen_token_mask.stride(0))
     tail = (vocab if mask_from is None else int(mask_from), int(eos_id), _lib.ptr(suppress_eos), int(update_seen),
             tokens.data_ptr(), _lib.stream(logits.device))
-    if uniforms is not None:
+    if planes is not None:
+        if uniforms is not None:
+            raise ValueError("the split-K plane source draws its uniforms from (seed, offset)")
+        _lib.call("nq_sample_counter_planes", planes.data_ptr(), planes.shape[0], logits.stride(0), rows, vocab,
+                  *head[5:], seed.data_ptr(), seed.stride(0), offset.data_ptr(), offset.stride(0), *tail[:4],
+                  _lib.ptr(logits_out), 0 if logits_out is None else logits_out.stride(0), *tail[4:])
+    elif uniforms is not None:
         _lib.call("nq_sample", *head, uniforms.data_ptr(), *tail)
     else:
         _lib.call("nq_sample_counter", *head, seed.data_ptr(), seed.stride(0), offset.data_ptr(), offset.stride(0), *tail)
@@ -115,6 +131,17 @@ def sample_with_counter(logits, temperature, top_k, top_p, seed, offset, **kwarg
     counter exactly as uniforms_from_counter computes it (same tokens, one launch)."""
 
     return _sample(logits, temperature, top_k, top_p, None, seed, offset, **kwargs)
+
+
+def sample_with_counter_from_planes(planes, temperature, top_k, top_p, seed, offset, *, logits_out=None,
+                                    **kwargs) -> torch.Tensor:
+    """sample_with_counter over the logits held as a projection's fp32 split-K planes [S, rows, vocab]
+    (``layers.linear_partials``): each logit is the planes' sum in plane order rounded to bf16, the
+    value ``layers.linear`` stores, so the tokens are those of linear + sample_with_counter, in one
+    launch; the bf16 logits also go to ``logits_out`` when given."""
+
+    return _sample(None, temperature, top_k, top_p, None, seed, offset, planes=planes, logits_out=logits_out,
+                   **kwargs)
 
 
 def sample_talker_cuda_graph(
@@ -152,6 +179,7 @@ __all__ = [
     "sample_logits_cuda_graph",
     "sample_talker_cuda_graph",
     "sample_with_counter",
+    "sample_with_counter_from_planes",
     "sample_with_uniforms",
     "uniforms_from_counter",
 ]

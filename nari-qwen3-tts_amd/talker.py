@@ -45,7 +45,7 @@ from .layers import (
     qwen3_tts_silu_and_mul,
     quantize_fp8_weight_blocks,
 )
-from .sampling import sample_with_counter, sample_with_uniforms
+from .sampling import sample_with_counter, sample_with_counter_from_planes, sample_with_uniforms
 
 
 @dataclass(frozen=True)
@@ -162,7 +162,7 @@ class TalkerDecodeStep:
             (c.hidden, q_w, _lib.NQ_EPI_ADD_RMSNORM),
             (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
             (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
-            (c.vocab, c.hidden, _lib.NQ_EPI_NONE),
+            (c.vocab, c.hidden, _lib.NQ_EPI_PARTIALS),  # the codec head's planes feed the sampler
         )
         self.use_hip_linear = all(_lib.load().nq_linear_splits(rows, n, k) > 0 for n, k, _ in projections)
         self.fp8 = weights.fp8_gate_up
@@ -225,12 +225,20 @@ class TalkerDecodeStep:
                 torch.matmul(self.act, layer.down.t(), out=self.hidden)
                 qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
         ctx.advance_sequence_lengths()
+        options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
+                       eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
+        if self.use_hip_linear and self.use_counter_rng:
+            # codec head as split-K planes, summed, rounded and drawn from in the sampling launch
+            # (the same logits and tokens as the projection followed by the sampler)
+            splits = linear_partials(self.hidden, self.w.codec_head, ws)
+            planes = ws[: splits * n * c.vocab * 4].view(torch.float32).view(splits, n, c.vocab)
+            sample_with_counter_from_planes(planes, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
+                                            logits_out=self.logits, **options)
+            return self.tokens
         if self.use_hip_linear:
             linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
         else:
             torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
-        options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
-                       eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
         if self.use_counter_rng:
             # the uniform comes from each row's (seed, offset) counter inside the sampling launch
             sample_with_counter(self.logits, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,

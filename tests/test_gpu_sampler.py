@@ -168,3 +168,45 @@ def test_counter_draw_equals_uniforms_then_sample(nq, device):
                                   mask_from=2048, eos_id=2150, update_seen=True)
         assert torch.equal(got, want)
         assert torch.equal(seen_a, seen_b)
+
+
+@pytest.mark.parametrize("rows", [64, 7])
+def test_draw_from_projection_planes_equals_projection_then_draw(nq, device, rows):
+    """The codec head's split-K planes summed, rounded and drawn from in the sampling launch give the
+    logits and tokens of the bf16 projection followed by sample_with_counter (the talker step's head,
+    executor/talker.py:173-183, 240-243, 373), seen update included."""
+
+    from nari_qwen3_tts_amd.layers import linear, linear_partials, linear_workspace_bytes
+    from nari_qwen3_tts_amd.sampling import sample_with_counter, sample_with_counter_from_planes
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    hidden, vocab = 2048, 3072
+    x = torch.randn(rows, hidden, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.randn(vocab, hidden, generator=g, device=device) * 0.05).to(torch.bfloat16)
+    ws = torch.empty(max(16, linear_workspace_bytes(rows, vocab, hidden, nq._lib.NQ_EPI_PARTIALS)), dtype=torch.uint8,
+                     device=device)
+    t = torch.full((rows,), 0.9, device=device)
+    k = torch.full((rows,), 50, dtype=torch.int32, device=device)
+    p = torch.full((rows,), 0.95, device=device)
+    r = torch.full((rows,), 1.05, device=device)
+    seed = torch.arange(rows, dtype=torch.long, device=device) * 7919 + 11
+    off = torch.arange(rows, dtype=torch.long, device=device) * 3 + 512
+    seen = torch.rand(rows, vocab, generator=g, device=device) < 0.02
+    want_logits = linear(x, w, workspace=ws)
+    seen_a, seen_b = seen.clone(), seen.clone()
+    want = sample_with_counter(want_logits, t, k, p, seed, off, repetition_penalty=r, seen_token_mask=seen_a,
+                               mask_from=2048, eos_id=2150, update_seen=True)
+    splits = linear_partials(x, w, ws)
+    assert splits > 1
+    planes = ws[: splits * rows * vocab * 4].view(torch.float32).view(splits, rows, vocab)
+    got_logits = torch.zeros(rows, vocab, dtype=torch.bfloat16, device=device)
+    got = sample_with_counter_from_planes(planes, t, k, p, seed, off, logits_out=got_logits, repetition_penalty=r,
+                                          seen_token_mask=seen_b, mask_from=2048, eos_id=2150, update_seen=True)
+    assert torch.equal(got_logits, want_logits)
+    assert torch.equal(got, want)
+    assert torch.equal(seen_a, seen_b)
+    # without a logits output
+    got2 = sample_with_counter_from_planes(planes, t, k, p, seed, off, repetition_penalty=r,
+                                           seen_token_mask=seen.clone(), mask_from=2048, eos_id=2150)
+    assert torch.equal(got2, want)
