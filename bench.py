@@ -709,7 +709,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the serving path shards by independent request rows with no "
-              "per-step exchange, and this build has no multi-GPU leg (use --gpus 1).", file=sys.stderr)
+              "per-step exchange, and this benchmark has no multi-GPU leg (use --gpus 1).", file=sys.stderr)
         return 2
 
     import numpy as np

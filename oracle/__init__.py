@@ -1,7 +1,7 @@
 """CPU oracle for the serving hot path -- TEST INFRASTRUCTURE ONLY.
 
 This package restates, in numpy, the algorithms of nari-labs/nari-qwen3-tts
-that the HIP kernels replace.  It is the checker, never the product: only
+that the HIP kernels replace.  It checks the product and is never part of it: only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it.  The product package fails loudly when its HIP
 library is missing and never falls back to anything here.
