@@ -38,9 +38,16 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .kernels import decode_attn_nhd_short_cache, paired_qk_norm_rope_dense_cache_
-from .layers import linear, linear_add_rmsnorm, linear_silu_mul, linear_workspace_bytes, qwen3_tts_rmsnorm
-from .sampling import sample_with_counter, sample_with_uniforms
+from .kernels import decode_attn_nhd_short_cache, qkv_partials_norm_rope_dense_cache_
+from .layers import (
+    linear,
+    linear_add_rmsnorm,
+    linear_partials,
+    linear_silu_mul,
+    linear_workspace_bytes,
+    qwen3_tts_rmsnorm,
+)
+from .sampling import sample_with_counter_from_planes, sample_with_uniforms
 
 
 @dataclass(frozen=True)
@@ -141,16 +148,16 @@ class CodePredictorFrame:
         self.kv_cache = torch.zeros(c.num_layers, rows, 2, groups, c.num_kv_heads, c.head_dim, **bf)
         self.h = torch.zeros(rows, c.hidden, **bf)  # residual stream
         self.x = torch.zeros(rows, c.hidden, **bf)  # normalised stream
-        self.qkv = torch.zeros(rows, c.qkv_width, **bf)
         self.att = torch.zeros(rows, c.num_qo_heads, c.head_dim, **bf)
+        self.q = torch.zeros(rows, c.num_qo_heads, c.head_dim, **bf)  # rotated queries
         self.act = torch.zeros(rows, c.intermediate, **bf)
         shapes = (
             (c.hidden, c.talker_hidden, _lib.NQ_EPI_NONE),
-            (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
+            (c.qkv_width, c.hidden, _lib.NQ_EPI_PARTIALS),  # planes feed the q/k norm + RoPE
             (c.hidden, c.num_qo_heads * c.head_dim, _lib.NQ_EPI_ADD_RMSNORM),
             (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
             (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
-            (c.vocab, c.hidden, _lib.NQ_EPI_NONE),
+            (c.vocab, c.hidden, _lib.NQ_EPI_PARTIALS),  # planes feed the sampler
         )
         need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in shapes)
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
@@ -158,19 +165,18 @@ class CodePredictorFrame:
     def _layers(self, cache_pos: int) -> None:
         c, ws = self.w.config, self.workspace
         n = self.rows
-        q_w, kv_w = c.num_qo_heads * c.head_dim, c.num_kv_heads * c.head_dim
+        q_w = c.num_qo_heads * c.head_dim
         positions = self.position_ids[:, cache_pos]
         layers = self.w.layers
         qwen3_tts_rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
         for index, L in enumerate(layers):
-            linear(self.x, L.qkv, out=self.qkv, workspace=ws)
-            q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
-            k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
-            v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
             cache = self.kv_cache[index]
-            paired_qk_norm_rope_dense_cache_(q, k, v, L.q_norm, L.k_norm, positions, c.rms_eps, c.rope_theta,
-                                             cache[:, 0], cache[:, 1], cache_pos)
-            decode_attn_nhd_short_cache(q, cache[:, 0], cache[:, 1], cache_pos + 1, out=self.att)
+            # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write
+            # (the same bits as the bf16 projection followed by paired_qk_norm_rope_dense_cache_)
+            splits = linear_partials(self.x, L.qkv, ws)
+            qkv_partials_norm_rope_dense_cache_(ws, splits, self.q, L.q_norm, L.k_norm, positions, c.rms_eps,
+                                                c.rope_theta, cache[:, 0], cache[:, 1], cache_pos)
+            decode_attn_nhd_short_cache(self.q, cache[:, 0], cache[:, 1], cache_pos + 1, out=self.att)
             linear_add_rmsnorm(self.att.view(n, q_w), L.o, self.h, L.post_norm, c.rms_eps, self.x, ws)
             linear_silu_mul(self.x, L.gate_up, out=self.act, workspace=ws)
             nxt = self.w.final_norm if index + 1 == len(layers) else layers[index + 1].input_norm
@@ -188,12 +194,15 @@ class CodePredictorFrame:
         for group in range(1, groups):
             self._layers(group)
             logits = self.logits[group - 1]
-            linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
             token = self.tokens[group - 1]
             if self.use_counter_rng:
-                sample_with_counter(logits, self.temperature, self.top_k, self.top_p, self.seed,
-                                    self.offsets[:, group - 1], out=token)
+                # the head's split-K planes summed, rounded and drawn from in the sampling launch
+                splits = linear_partials(self.x, w.lm_head[group - 1], ws)
+                planes = ws[: splits * self.rows * c.vocab * 4].view(torch.float32).view(splits, self.rows, c.vocab)
+                sample_with_counter_from_planes(planes, self.temperature, self.top_k, self.top_p, self.seed,
+                                                self.offsets[:, group - 1], logits_out=logits, out=token)
             else:
+                linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
                 sample_with_uniforms(logits, self.temperature, self.top_k, self.top_p, self.uniforms[group - 1],
                                      out=token)
             self.codec_sum.add_(F.embedding(token, w.codec_embedding[group - 1]))

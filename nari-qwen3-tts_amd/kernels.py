@@ -142,6 +142,44 @@ def paired_qk_norm_rope_dense_cache_(
     return query, key
 
 
+def qkv_partials_norm_rope_dense_cache_(
+    partials, splits: int, q_out, query_weight, key_weight, positions, epsilon, rope_theta, key_cache, value_cache,
+    cache_position: int,
+):
+    """paired_qk_norm_rope_dense_cache_ fed by the packed QKV projection's fp32 split-K planes
+    [splits, tokens, (Hq + 2 Hkv) * D] (``layers.linear_partials`` leaves them at the start of its
+    workspace): each value is the plane-order sum rounded to bf16, the bf16 projection output, so
+    the rotated q (into ``q_out`` [tokens, Hq, D]) and the cache rows are those of the projection
+    followed by paired_qk_norm_rope_dense_cache_, without the projection's reduction launch."""
+
+    _require_bf16(q_out, query_weight, key_weight, key_cache, value_cache)
+    tokens, hq, d = q_out.shape
+    hk = key_cache.shape[2]
+    if key_cache.shape != (tokens, key_cache.shape[1], hk, d) or value_cache.shape != key_cache.shape:
+        raise ValueError("dense CP cache shape mismatch")
+    if not 0 <= cache_position < key_cache.shape[1]:
+        raise ValueError("dense CP cache position is invalid")
+    if key_cache.stride() != value_cache.stride() or key_cache.stride(-1) != 1 or q_out.stride(-1) != 1:
+        raise ValueError("dense CP K and V caches must share one layout")
+    if positions.dtype != torch.long or positions.shape[0] != tokens:
+        raise ValueError("positions must be int64 with one entry per token")
+    if partials.numel() * partials.element_size() < splits * tokens * (hq + 2 * hk) * d * 4:
+        raise ValueError("partials hold fewer planes than splits")
+    delta = value_cache.data_ptr() - key_cache.data_ptr()
+    if delta % key_cache.element_size():
+        raise ValueError("dense CP K and V caches are misaligned")
+    _lib.require_device(partials, q_out, query_weight, key_weight, positions, key_cache, value_cache)
+    _lib.call(
+        "nq_qkv_partials_norm_rope_kv_write", partials.data_ptr(), int(splits), tokens,
+        q_out.data_ptr(), q_out.stride(0), q_out.stride(1), None, 0, 0,
+        query_weight.data_ptr(), key_weight.data_ptr(), positions.data_ptr(), positions.stride(0), hq, hk, d,
+        float(epsilon), float(rope_theta), 0,
+        key_cache.data_ptr(), key_cache.stride(0), delta // key_cache.element_size(), key_cache.stride(1),
+        key_cache.stride(2), None, None, int(cache_position), _lib.stream(q_out.device),
+    )
+    return q_out
+
+
 def decode_attn_nhd_short_cache(query, key_cache, value_cache, cache_length: int, out=None):
     """Fixed 16-position code-predictor attention (one query per row)."""
 
@@ -182,5 +220,6 @@ __all__ = [
     "decode_attn_nhd_short_cache",
     "paired_qk_norm_rope_",
     "paired_qk_norm_rope_dense_cache_",
+    "qkv_partials_norm_rope_dense_cache_",
     "paired_qk_norm_rope_paged_cache_",
 ]
