@@ -258,10 +258,29 @@ int nq_add_rmsnorm(uint16_t *hidden, uint16_t *residual, const uint16_t *weight,
  * table_s0), addend [rows, width] (row stride addend_s0), residual and out
  * contiguous; bf16, 16-byte aligned.  An id outside [0, num_embeddings) reads
  * row 0 and stores NQ_ERR_INVALID_ARGUMENT in *status (status may be NULL).
+ * With addend == NULL the residual is the gathered row itself (the code
+ * predictor's projected codec embedding as the next input,
+ * executor/code_predictor.py:72-88, then the first input norm).
  */
 int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, int64_t table_s0, int64_t num_embeddings,
                          const uint16_t *addend, int64_t addend_s0, const uint16_t *weight, int rows, int width,
                          float eps, uint16_t *residual, uint16_t *out, int32_t *status, void *stream);
+
+/*
+ * out[r] = first_table[first_ids[r]] + tables[0][ids[0][r]] + ... +
+ * tables[groups-1][ids[groups-1][r]], added in group order with every partial
+ * sum rounded to bf16: the code predictor's codec_sum (layer-0 embedding plus
+ * the codec embedding of each group's token, executor/code_predictor.py:
+ * 159-235 and model/components.py:254-411) in one launch, the same bits as
+ * adding the rows one at a time in bf16.  ids[g][r] at ids + g * ids_s0 +
+ * r * ids_s1; table g, row t at tables + g * table_s0 + t * table_s1.  bf16,
+ * 16-byte aligned rows; width % 8 == 0.  An id outside its table reads row 0
+ * and stores NQ_ERR_INVALID_ARGUMENT in *status (status may be NULL).
+ */
+int nq_gather_sum_rows(const int64_t *first_ids, const uint16_t *first_table, int64_t first_s0, int64_t first_rows,
+                       const int64_t *ids, int64_t ids_s0, int64_t ids_s1, const uint16_t *tables, int64_t table_s0,
+                       int64_t table_s1, int64_t table_rows, int groups, int rows, int width, uint16_t *out,
+                       int64_t out_s0, int32_t *status, void *stream);
 
 /*
  * out = rmsnorm(x) (model/layers.py:82-115).  bf16 [rows, width]; out may alias x.

@@ -40,6 +40,8 @@ import torch.nn.functional as F
 from . import _lib
 from .kernels import decode_attn_nhd_short_cache, qkv_partials_norm_rope_dense_cache_
 from .layers import (
+    embed_add_rmsnorm,
+    gather_sum_rows,
     linear,
     linear_add_rmsnorm,
     linear_partials,
@@ -162,13 +164,16 @@ class CodePredictorFrame:
         need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in shapes)
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
 
-    def _layers(self, cache_pos: int) -> None:
+    def _layers(self, cache_pos: int, normed: bool = False) -> None:
+        """The 5 layers at cache position ``cache_pos``; ``normed``: self.x already holds the first
+        input norm of self.h."""
         c, ws = self.w.config, self.workspace
         n = self.rows
         q_w = c.num_qo_heads * c.head_dim
         positions = self.position_ids[:, cache_pos]
         layers = self.w.layers
-        qwen3_tts_rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
+        if not normed:
+            qwen3_tts_rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
         for index, L in enumerate(layers):
             cache = self.kv_cache[index]
             # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write
@@ -189,10 +194,11 @@ class CodePredictorFrame:
         linear(self.past_hidden, w.proj_w, out=self.h, workspace=ws, bias=w.proj_b)
         self._layers(0)
         self.frames[:, 0].copy_(self.layer0_token)
-        torch.index_select(w.layer0_embedding, 0, self.layer0_token, out=self.codec_sum)
-        torch.index_select(w.projected_layer0, 0, self.layer0_token, out=self.h)
+        # the next input (a projected embedding row) and the first input norm in one launch
+        first_norm = w.layers[0].input_norm
+        embed_add_rmsnorm(self.layer0_token, w.projected_layer0, None, first_norm, c.rms_eps, self.h, self.x)
         for group in range(1, groups):
-            self._layers(group)
+            self._layers(group, normed=True)
             logits = self.logits[group - 1]
             token = self.tokens[group - 1]
             if self.use_counter_rng:
@@ -205,9 +211,11 @@ class CodePredictorFrame:
                 linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
                 sample_with_uniforms(logits, self.temperature, self.top_k, self.top_p, self.uniforms[group - 1],
                                      out=token)
-            self.codec_sum.add_(F.embedding(token, w.codec_embedding[group - 1]))
             if group < groups - 1:
-                torch.index_select(w.projected_residual[group - 1], 0, token, out=self.h)
+                embed_add_rmsnorm(token, w.projected_residual[group - 1], None, first_norm, c.rms_eps, self.h,
+                                  self.x)
+        # codec_sum: the layer-0 embedding plus each group's codec embedding, added in group order
+        gather_sum_rows(self.layer0_token, w.layer0_embedding, self.tokens, w.codec_embedding, self.codec_sum)
         self.frames[:, 1:].copy_(self.tokens.t())
         return self.frames, self.codec_sum
 

@@ -80,7 +80,9 @@ struct Fp8Out {
     int64_t s_s0;
 };
 
-template <typename Src, bool kFp8, int kVec>
+// kAdd false: the residual row is the hidden operand itself (a gathered
+// embedding row, copied exactly), nothing is added.
+template <typename Src, bool kFp8, int kVec, bool kAdd = true>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
                    uint16_t *__restrict__ residual, const uint16_t *__restrict__ residual_in, int64_t ri_s0,
@@ -100,7 +102,7 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
     for (int i = 0; i < kVec; ++i) {
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
-            rb[i] = *reinterpret_cast<const uint4 *>(rin + vi * 8);
+            if constexpr (kAdd) rb[i] = *reinterpret_cast<const uint4 *>(rin + vi * 8);
             rw[i] = *reinterpret_cast<const uint4 *>(weight + vi * 8);
         }
     }
@@ -109,7 +111,7 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
         const int vi = threadIdx.x + i * kNormThreads;
         if (vi < nvec) {
             hidden.load8(row, vi * 8, a[i]);
-            unpack8(rb[i], b[i]);
+            if constexpr (kAdd) unpack8(rb[i], b[i]);
             unpack8(rw[i], w[i]);
         }
     }
@@ -120,7 +122,12 @@ add_rmsnorm_kernel(Src hidden, uint16_t *__restrict__ hidden_out, int64_t ho_s0,
             uint4 packed;
             uint32_t *pw = reinterpret_cast<uint32_t *>(&packed);
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) pw[e / 2] = pack2_bf16(a[i][e] + b[i][e], a[i][e + 1] + b[i][e + 1]);
+            for (int e = 0; e < 8; e += 2) {
+                if constexpr (kAdd)
+                    pw[e / 2] = pack2_bf16(a[i][e] + b[i][e], a[i][e + 1] + b[i][e + 1]);
+                else
+                    pw[e / 2] = pack2_bf16(a[i][e], a[i][e + 1]);  // bf16 values: exact
+            }
             *reinterpret_cast<uint4 *>(residual + row * width + vi * 8) = packed;
             unpack8(packed, x[i]);
 #pragma unroll
@@ -216,16 +223,16 @@ silu_mul_kernel(Src gate_up, uint16_t *__restrict__ out, int64_t o_s0, int rows,
 
 // Launch with the fewest 8-column vectors per thread that cover the row, so
 // that a narrow row keeps no registers for vectors it does not have.
-template <typename Src, bool kFp8, typename... Args>
+template <typename Src, bool kFp8, bool kAdd = true, typename... Args>
 void launch_add_rmsnorm(int rows, int width, hipStream_t st, Src src, Args... args) {
     const int nv = (width / 8 + kNormThreads - 1) / kNormThreads;
     const dim3 grid(rows), block(kNormThreads);
     if (nv <= 1)
-        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 1>), grid, block, 0, st, src, args...);
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 1, kAdd>), grid, block, 0, st, src, args...);
     else if (nv <= 2)
-        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 2>), grid, block, 0, st, src, args...);
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, 2, kAdd>), grid, block, 0, st, src, args...);
     else
-        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, kMaxVec>), grid, block, 0, st, src, args...);
+        hipLaunchKernelGGL((add_rmsnorm_kernel<Src, kFp8, kMaxVec, kAdd>), grid, block, 0, st, src, args...);
 }
 
 int silu_grid(int rows, int width) {
@@ -236,6 +243,48 @@ int silu_grid(int rows, int width) {
 
 bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+
+// out[r] = t0[first_ids[r]] + t[0][ids[0][r]] + ... + t[G-1][ids[G-1][r]], the
+// adds in group order with each partial sum rounded to bf16 (the value of
+// adding the rows one launch at a time in bf16).  One thread per 8 columns of
+// a row; an id outside its table reads row 0 and reports in *status.
+__global__ void __launch_bounds__(256)
+gather_sum_rows_kernel(const int64_t *__restrict__ first_ids, const uint16_t *__restrict__ first_table,
+                       int64_t first_s0, int64_t first_rows, const int64_t *__restrict__ ids, int64_t ids_s0,
+                       int64_t ids_s1, const uint16_t *__restrict__ tables, int64_t table_s0, int64_t table_s1,
+                       int64_t table_rows, int groups, int rows, int width, uint16_t *__restrict__ out,
+                       int64_t out_s0, int32_t *status) {
+    const int nvec = width / 8;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<int64_t>(rows) * nvec) return;
+    const int r = static_cast<int>(i / nvec), col = static_cast<int>(i % nvec) * 8;
+    bool bad = false;
+    int64_t id = first_ids[r];
+    if (id < 0 || id >= first_rows) {
+        bad = true;
+        id = 0;
+    }
+    float acc[8];
+    unpack8(*reinterpret_cast<const uint4 *>(first_table + id * first_s0 + col), acc);
+    for (int g = 0; g < groups; ++g) {
+        int64_t t = ids[g * ids_s0 + r * ids_s1];
+        if (t < 0 || t >= table_rows) {
+            bad = true;
+            t = 0;
+        }
+        float e[8];
+        unpack8(*reinterpret_cast<const uint4 *>(tables + g * table_s0 + t * table_s1 + col), e);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] = bf16_to_f32(f32_to_bf16(acc[k] + e[k]));
+    }
+    uint4 o;
+    o.x = pack2_bf16(acc[0], acc[1]);
+    o.y = pack2_bf16(acc[2], acc[3]);
+    o.z = pack2_bf16(acc[4], acc[5]);
+    o.w = pack2_bf16(acc[6], acc[7]);
+    *reinterpret_cast<uint4 *>(out + r * out_s0 + col) = o;
+    if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+}
 }  // namespace
 
 int launch_add_rmsnorm_partials(const float *part, int S, int rows, int width, uint16_t *hidden_out,
@@ -324,16 +373,41 @@ extern "C" int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, i
                                     const uint16_t *addend, int64_t addend_s0, const uint16_t *weight, int rows,
                                     int width, float eps, uint16_t *residual, uint16_t *out, int32_t *status,
                                     void *stream) {
-    NQ_CHECK_ARG(ids && table && addend && weight && residual && out && rows >= 0 && width >= 8);
-    NQ_CHECK_ARG(num_embeddings >= 1 && table_s0 >= width && addend_s0 >= width);
+    NQ_CHECK_ARG(ids && table && weight && residual && out && rows >= 0 && width >= 8);
+    NQ_CHECK_ARG(num_embeddings >= 1 && table_s0 >= width && (!addend || addend_s0 >= width));
     if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec) return NQ_ERR_UNSUPPORTED;
-    if (!nq::al16(table) || !nq::al16(addend) || !nq::al16(weight) || !nq::al16(residual) || !nq::al16(out) ||
-        table_s0 % 8 || addend_s0 % 8)
+    if (!nq::al16(table) || (addend && !nq::al16(addend)) || !nq::al16(weight) || !nq::al16(residual) ||
+        !nq::al16(out) || table_s0 % 8 || (addend && addend_s0 % 8))
         return NQ_ERR_UNSUPPORTED;
     if (rows == 0) return NQ_OK;
     const nq::GatherSrc src{table, table_s0, ids, num_embeddings, status};
+    if (!addend) {  // residual = the gathered row
+        nq::launch_add_rmsnorm<nq::GatherSrc, false, false>(rows, width, static_cast<hipStream_t>(stream), src, out,
+                                                            static_cast<int64_t>(width), residual, nullptr, 0,
+                                                            weight, width, eps, nq::Fp8Out{});
+        return NQ_LAUNCH_STATUS();
+    }
     nq::launch_add_rmsnorm<nq::GatherSrc, false>(rows, width, static_cast<hipStream_t>(stream), src, out,
                                                  static_cast<int64_t>(width), residual, addend, addend_s0, weight,
                                                  width, eps, nq::Fp8Out{});
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_gather_sum_rows(const int64_t *first_ids, const uint16_t *first_table, int64_t first_s0,
+                                  int64_t first_rows, const int64_t *ids, int64_t ids_s0, int64_t ids_s1,
+                                  const uint16_t *tables, int64_t table_s0, int64_t table_s1, int64_t table_rows,
+                                  int groups, int rows, int width, uint16_t *out, int64_t out_s0, int32_t *status,
+                                  void *stream) {
+    NQ_CHECK_ARG(first_ids && first_table && out && rows >= 0 && width >= 8 && groups >= 0);
+    NQ_CHECK_ARG(first_rows >= 1 && first_s0 >= width && out_s0 >= width);
+    NQ_CHECK_ARG(groups == 0 || (ids && tables && table_rows >= 1 && table_s1 >= width));
+    if (width % 8 || first_s0 % 8 || out_s0 % 8 || (groups && (table_s1 % 8 || table_s0 % 8)) ||
+        !nq::al16(first_table) || !nq::al16(out) || (groups && !nq::al16(tables)))
+        return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    const int64_t threads = static_cast<int64_t>(rows) * (width / 8);
+    hipLaunchKernelGGL(nq::gather_sum_rows_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), first_ids, first_table, first_s0, first_rows, ids, ids_s0,
+                       ids_s1, tables, table_s0, table_s1, table_rows, groups, rows, width, out, out_s0, status);
     return NQ_LAUNCH_STATUS();
 }

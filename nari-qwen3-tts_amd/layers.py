@@ -58,28 +58,55 @@ def qwen3_tts_rmsnorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float, ou
     return out
 
 
-def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tensor, weight: torch.Tensor, eps: float,
-                      residual: torch.Tensor, out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
-    """residual = bf16(addend + table[ids]); out = rmsnorm(residual) * weight, one launch (the talker step's
-    input embedding and first input norm).  ``status`` (int32 [1], optional) receives NQ_ERR_INVALID_ARGUMENT
-    for an id outside the table."""
+def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tensor | None, weight: torch.Tensor,
+                      eps: float, residual: torch.Tensor, out: torch.Tensor,
+                      status: torch.Tensor | None = None) -> torch.Tensor:
+    """residual = bf16(addend + table[ids]) (the gathered row itself when ``addend`` is None);
+    out = rmsnorm(residual) * weight, one launch (the talker step's input embedding and first input
+    norm; the code predictor's next input and first input norm).  ``status`` (int32 [1], optional)
+    receives NQ_ERR_INVALID_ARGUMENT for an id outside the table."""
 
     for t, name in ((table, "embedding table"), (addend, "addend"), (weight, "norm weight"), (residual, "residual"),
                     (out, "out")):
-        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+        if t is not None and (t.dtype != torch.bfloat16 or t.stride(-1) != 1):
             raise TypeError(f"{name} must be bf16 with unit inner stride")
     if ids.dtype != torch.long or ids.ndim != 1:
         raise TypeError("ids must be an int64 vector")
-    rows, width = addend.shape
+    rows, width = residual.shape
     if ids.shape != (rows,) or table.shape[1] != width or weight.shape != (width,):
-        raise ValueError("ids / table / norm weight do not match the addend")
-    if residual.shape != (rows, width) or out.shape != (rows, width) or not residual.is_contiguous() \
-            or not out.is_contiguous():
+        raise ValueError("ids / table / norm weight do not match the residual")
+    if addend is not None and addend.shape != (rows, width):
+        raise ValueError("addend must match the residual")
+    if out.shape != (rows, width) or not residual.is_contiguous() or not out.is_contiguous():
         raise ValueError("residual and out must be contiguous [rows, width]")
     _lib.require_device(ids, table, addend, weight, residual, out, status)
     _lib.call("nq_embed_add_rmsnorm", ids.data_ptr(), table.data_ptr(), table.stride(0), table.shape[0],
-              addend.data_ptr(), addend.stride(0), weight.data_ptr(), rows, width, float(eps), residual.data_ptr(),
-              out.data_ptr(), _lib.ptr(status), _lib.stream(addend.device))
+              _lib.ptr(addend), 0 if addend is None else addend.stride(0), weight.data_ptr(), rows, width, float(eps),
+              residual.data_ptr(), out.data_ptr(), _lib.ptr(status), _lib.stream(residual.device))
+    return out
+
+
+def gather_sum_rows(first_ids: torch.Tensor, first_table: torch.Tensor, ids: torch.Tensor, tables: torch.Tensor,
+                    out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
+    """out[r] = first_table[first_ids[r]] + sum over g of tables[g][ids[g, r]], added in group order
+    with each partial sum rounded to bf16 (the code predictor's codec_sum in one launch).
+    ``ids`` int64 [G, rows] (any strides); ``tables`` bf16 [>= G, V, width]."""
+
+    if first_ids.dtype != torch.long or ids.dtype != torch.long or first_ids.ndim != 1 or ids.ndim != 2:
+        raise TypeError("ids must be int64: first_ids [rows], ids [groups, rows]")
+    for t, name in ((first_table, "first table"), (tables, "tables"), (out, "out")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise TypeError(f"{name} must be bf16 with unit inner stride")
+    groups, rows = ids.shape
+    width = out.shape[1]
+    if first_ids.shape != (rows,) or out.shape[0] != rows or first_table.shape[1] != width or tables.ndim != 3 \
+            or tables.shape[0] < groups or tables.shape[2] != width:
+        raise ValueError("ids / tables / out shapes do not match")
+    _lib.require_device(first_ids, first_table, ids, tables, out, status)
+    _lib.call("nq_gather_sum_rows", first_ids.data_ptr(), first_table.data_ptr(), first_table.stride(0),
+              first_table.shape[0], ids.data_ptr(), ids.stride(0), ids.stride(1), tables.data_ptr(), tables.stride(0),
+              tables.stride(1), tables.shape[1], groups, rows, width, out.data_ptr(), out.stride(0), _lib.ptr(status),
+              _lib.stream(out.device))
     return out
 
 
@@ -407,6 +434,7 @@ __all__ = [
     "FP8",
     "PackedLinearWeight",
     "embed_add_rmsnorm",
+    "gather_sum_rows",
     "linear_fp8_swiglu",
     "pack_fp8_swiglu",
     "add_rmsnorm_fp8",

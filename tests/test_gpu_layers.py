@@ -170,3 +170,50 @@ def test_embed_add_rmsnorm_equals_gather_add_then_norm(nq, device):
     assert int(status.item()) == _lib.NQ_ERR_INVALID_ARGUMENT
     # the rows with valid ids are unaffected
     assert torch.equal(residual[:-1], want_r[:-1])
+
+
+def test_gather_sum_rows_and_gather_norm_equal_their_torch_steps(nq, device):
+    """The code predictor's codec_sum (layer-0 embedding plus each group's codec embedding,
+    executor/code_predictor.py:159-235) in one launch gives the bits of index_select followed by one
+    bf16 add per group; the gathered-row norm (no addend) gives those of index_select + RMSNorm."""
+    import torch.nn.functional as F
+
+    from nari_qwen3_tts_amd import _lib
+    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, gather_sum_rows, qwen3_tts_rmsnorm
+
+    g = torch.Generator(device=device)
+    g.manual_seed(9)
+    rows, width, groups, v0, v = 128, 2048, 15, 3072, 2048
+    first = torch.randn(v0, width, generator=g, device=device).to(torch.bfloat16)
+    tables = torch.randn(groups + 1, v, width, generator=g, device=device).to(torch.bfloat16)
+    first_ids = torch.randint(0, v0, (rows,), generator=g, device=device)
+    ids = torch.randint(0, v, (groups, rows), generator=g, device=device)
+    want = torch.index_select(first, 0, first_ids)
+    for k in range(groups):
+        want.add_(F.embedding(ids[k], tables[k]))
+    out = torch.empty(rows, width, dtype=torch.bfloat16, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    gather_sum_rows(first_ids, first, ids, tables, out, status)
+    assert torch.equal(out, want)
+    assert int(status.item()) == 0
+    # strided ids (a transposed view) give the same rows
+    out2 = torch.empty_like(out)
+    gather_sum_rows(first_ids, first, ids.t().contiguous().t(), tables, out2)
+    assert torch.equal(out2, want)
+    bad = ids.clone()
+    bad[3, 5] = v
+    gather_sum_rows(first_ids, first, bad, tables, out2, status)
+    assert int(status.item()) == _lib.NQ_ERR_INVALID_ARGUMENT
+
+    hidden = 1024
+    proj = torch.randn(v, hidden, generator=g, device=device).to(torch.bfloat16)
+    proj[7, :16] = -0.0  # signed zeros stay as they are (nothing is added)
+    weight = (torch.rand(hidden, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    tok = ids[0].clone()
+    tok[0] = 7
+    h = torch.empty(rows, hidden, dtype=torch.bfloat16, device=device)
+    x = torch.empty_like(h)
+    embed_add_rmsnorm(tok, proj, None, weight, 1e-6, h, x)
+    want_h = torch.index_select(proj, 0, tok)
+    assert torch.equal(h.view(torch.int16), want_h.view(torch.int16))
+    assert torch.equal(x, qwen3_tts_rmsnorm(want_h, weight, 1e-6))
