@@ -266,16 +266,33 @@ gather_sum_rows_kernel(const int64_t *__restrict__ first_ids, const uint16_t *__
     }
     float acc[8];
     unpack8(*reinterpret_cast<const uint4 *>(first_table + id * first_s0 + col), acc);
-    for (int g = 0; g < groups; ++g) {
-        int64_t t = ids[g * ids_s0 + r * ids_s1];
-        if (t < 0 || t >= table_rows) {
-            bad = true;
-            t = 0;
-        }
-        float e[8];
-        unpack8(*reinterpret_cast<const uint4 *>(tables + g * table_s0 + t * table_s1 + col), e);
+    // up to 16 groups per round: every id, then every row, in flight together
+    // (indexes past the last group repeat it, so that no load is conditional;
+    // their rows are not added)
+    constexpr int kRound = 16;
+    for (int g0 = 0; g0 < groups; g0 += kRound) {
+        int64_t t[kRound];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc[k] = bf16_to_f32(f32_to_bf16(acc[k] + e[k]));
+        for (int u = 0; u < kRound; ++u) {
+            const int gi = g0 + u < groups ? g0 + u : groups - 1;
+            t[u] = ids[gi * ids_s0 + r * ids_s1];
+        }
+        uint4 rowv[kRound];
+#pragma unroll
+        for (int u = 0; u < kRound; ++u) {
+            const int gi = g0 + u < groups ? g0 + u : groups - 1;
+            const bool in = t[u] >= 0 && t[u] < table_rows;
+            bad = bad || !in;
+            rowv[u] = *reinterpret_cast<const uint4 *>(tables + gi * table_s0 + (in ? t[u] : 0) * table_s1 + col);
+        }
+#pragma unroll
+        for (int u = 0; u < kRound; ++u) {
+            float e[8];
+            unpack8(rowv[u], e);
+            const bool use = g0 + u < groups;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = use ? bf16_to_f32(f32_to_bf16(acc[k] + e[k])) : acc[k];
+        }
     }
     uint4 o;
     o.x = pack2_bf16(acc[0], acc[1]);
