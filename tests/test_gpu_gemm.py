@@ -15,6 +15,9 @@ SHAPES = [
     (64, 2048, 2048),
     (64, 12288, 2048),
     (64, 2048, 6144),
+    (16, 2048, 6144),  # 768-column K slices with one and two 16-row tiles
+    (32, 2048, 6144),
+    (7, 4096, 3072),
     (64, 3072, 2048),
     (128, 4096, 1024),
     (128, 1024, 2048),
