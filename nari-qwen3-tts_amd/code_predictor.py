@@ -47,7 +47,7 @@ from .layers import (
     linear_partials,
     linear_silu_mul,
     linear_workspace_bytes,
-    qwen3_tts_rmsnorm,
+    rmsnorm,
 )
 from .sampling import sample_with_counter_from_planes, sample_with_uniforms
 
@@ -173,7 +173,7 @@ class CodePredictorFrame:
         positions = self.position_ids[:, cache_pos]
         layers = self.w.layers
         if not normed:
-            qwen3_tts_rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
+            rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
         for index, L in enumerate(layers):
             cache = self.kv_cache[index]
             # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write

@@ -1,8 +1,12 @@
 """Norm, SwiGLU and projection entry points with the reference's call shapes.
 
 ``qwen3_tts_add_rmsnorm`` / ``qwen3_tts_rmsnorm`` / ``qwen3_tts_silu_and_mul``
-mirror model/layers.py:28-100: the fused add-norm updates both inputs in
-place (residual <- residual + hidden, hidden <- rmsnorm(residual)).
+keep the signatures of model/layers.py:28-100 (the RMSNorm module, the
+``use_cuda_kernel`` keyword and the reference's own torch math for inputs it
+does not send to a kernel); the fused add-norm updates both inputs in place
+(residual <- residual + hidden, hidden <- rmsnorm(residual)).  The
+(weight, eps) forms ``add_rmsnorm`` / ``rmsnorm`` / ``silu_mul`` are what the
+step code calls.
 ``linear`` is the bias-free nn.Linear of model/layers.py:195-270 for decode
 row counts (<= 128), computed by the skinny HIP GEMM.
 
@@ -28,7 +32,16 @@ def _check(t: torch.Tensor, name: str) -> None:
     _lib.require_device(t)
 
 
-def qwen3_tts_add_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+def _check_out(out: torch.Tensor, like: torch.Tensor, shape, name: str = "out") -> None:
+    if out.dtype != like.dtype or out.device != like.device:
+        raise TypeError(f"{name} must match the input's dtype and device")
+    if tuple(out.shape) != tuple(shape) or not out.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous tensor of shape {tuple(shape)}")
+
+
+def add_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """In place: residual <- bf16(residual + hidden), hidden <- rmsnorm(residual) * weight."""
+
     _check(hidden, "hidden_states")
     _check(residual, "residual")
     _check(weight, "norm weight")
@@ -44,18 +57,103 @@ def qwen3_tts_add_rmsnorm(hidden: torch.Tensor, residual: torch.Tensor, weight: 
     return hidden, residual
 
 
-def qwen3_tts_rmsnorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None):
+def rmsnorm(hidden: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None):
+    """out = rmsnorm(hidden) * weight (bf16 in and out, fp32 statistics)."""
+
     _check(hidden, "hidden_states")
     _check(weight, "norm weight")
     width = hidden.shape[-1]
     if weight.shape != (width,):
         raise ValueError("norm weight must match the hidden width")
-    out = torch.empty_like(hidden) if out is None else out
+    if out is None:
+        out = torch.empty_like(hidden)
+    else:
+        _check_out(out, hidden, hidden.shape)
     _lib.call(
         "nq_rmsnorm", hidden.data_ptr(), weight.data_ptr(), out.data_ptr(), hidden.numel() // width, width,
         float(eps), _lib.stream(hidden.device),
     )
     return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = silu(gate) * up over the two halves of the last dimension (bf16)."""
+
+    _check(gate_up, "gate_up")
+    width = gate_up.shape[-1] // 2
+    if gate_up.shape[-1] != 2 * width:
+        raise ValueError("gate_up must have an even last dimension")
+    rows = gate_up.numel() // gate_up.shape[-1]
+    shape = (*gate_up.shape[:-1], width)
+    if out is None:
+        out = torch.empty(shape, dtype=gate_up.dtype, device=gate_up.device)
+    else:
+        _check_out(out, gate_up, shape)
+    _lib.call("nq_silu_mul", gate_up.data_ptr(), out.data_ptr(), rows, width, _lib.stream(gate_up.device))
+    return out
+
+
+def _kernel_input(t: torch.Tensor, use_cuda_kernel: bool) -> bool:
+    """The reference's dispatch guard (model/layers.py:34,63-71,89): a kernel takes CUDA-device
+    half-precision inputs; everything else runs the reference's own torch math.  Here the kernel
+    is bf16 only, so an fp16 device tensor that the reference would send to its kernel is refused
+    instead of being computed some other way."""
+
+    if not (use_cuda_kernel and t.is_cuda and t.dtype in (torch.float16, torch.bfloat16)):
+        return False
+    if t.dtype != torch.bfloat16:
+        raise TypeError("the HIP norm / SwiGLU kernels take bf16 device tensors (fp16 is not built)")
+    return True
+
+
+def _norm_weight(norm) -> torch.Tensor:
+    weight = norm.weight
+    if weight.dtype != torch.bfloat16:
+        raise TypeError("RMSNorm weight must be bf16 for the HIP kernel")
+    return weight.detach()
+
+
+def qwen3_tts_silu_and_mul(gate_up: torch.Tensor, *, use_cuda_kernel: bool = True) -> torch.Tensor:
+    """Drop-in for model/layers.py:28-39: SwiGLU of the two halves of ``gate_up``'s last dimension.
+
+    bf16 device tensors run ``nq_silu_mul``; other inputs take the reference's torch math, as the
+    reference does for them."""
+
+    if _kernel_input(gate_up, use_cuda_kernel):
+        return silu_mul(gate_up if gate_up.is_contiguous() else gate_up.contiguous())
+    gate, up = gate_up.chunk(2, dim=-1)
+    return torch.nn.functional.silu(gate) * up
+
+
+def qwen3_tts_add_rmsnorm(hidden_states: torch.Tensor, residual: torch.Tensor, norm, *,
+                          use_cuda_kernel: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """Drop-in for model/layers.py:42-78: residual add + the following RMSNorm (``norm`` is the
+    reference's RMSNorm module: ``weight`` and ``variance_epsilon`` are read from it).
+
+    Device inputs that the reference hands to its fused kernel (half precision, contiguous, same
+    shape, distinct storage) run ``nq_add_rmsnorm`` in place on both tensors and are returned;
+    the others take the reference's own torch math and return new tensors."""
+
+    if (
+        _kernel_input(hidden_states, use_cuda_kernel)
+        and hidden_states.is_contiguous()
+        and residual.is_contiguous()
+        and hidden_states.shape == residual.shape
+        and hidden_states.data_ptr() != residual.data_ptr()
+    ):
+        add_rmsnorm(hidden_states, residual, _norm_weight(norm), float(norm.variance_epsilon))
+        return hidden_states, residual
+    residual = residual + hidden_states
+    return norm(residual), residual
+
+
+def qwen3_tts_rmsnorm(hidden_states: torch.Tensor, norm, *, use_cuda_kernel: bool = True) -> torch.Tensor:
+    """Drop-in for model/layers.py:81-100: one RMSNorm (``norm.weight``, ``norm.variance_epsilon``)."""
+
+    if _kernel_input(hidden_states, use_cuda_kernel):
+        x = hidden_states if hidden_states.is_contiguous() else hidden_states.contiguous()
+        return rmsnorm(x, _norm_weight(norm), float(norm.variance_epsilon))
+    return norm(hidden_states)
 
 
 def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tensor | None, weight: torch.Tensor,
@@ -72,6 +170,8 @@ def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tens
             raise TypeError(f"{name} must be bf16 with unit inner stride")
     if ids.dtype != torch.long or ids.ndim != 1:
         raise TypeError("ids must be an int64 vector")
+    if ids.stride(0) != 1:
+        raise ValueError("ids must be a unit-stride vector")
     rows, width = residual.shape
     if ids.shape != (rows,) or table.shape[1] != width or weight.shape != (width,):
         raise ValueError("ids / table / norm weight do not match the residual")
@@ -94,6 +194,8 @@ def gather_sum_rows(first_ids: torch.Tensor, first_table: torch.Tensor, ids: tor
 
     if first_ids.dtype != torch.long or ids.dtype != torch.long or first_ids.ndim != 1 or ids.ndim != 2:
         raise TypeError("ids must be int64: first_ids [rows], ids [groups, rows]")
+    if first_ids.stride(0) != 1:
+        raise ValueError("first_ids must be a unit-stride vector")
     for t, name in ((first_table, "first table"), (tables, "tables"), (out, "out")):
         if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
             raise TypeError(f"{name} must be bf16 with unit inner stride")
@@ -107,17 +209,6 @@ def gather_sum_rows(first_ids: torch.Tensor, first_table: torch.Tensor, ids: tor
               first_table.shape[0], ids.data_ptr(), ids.stride(0), ids.stride(1), tables.data_ptr(), tables.stride(0),
               tables.stride(1), tables.shape[1], groups, rows, width, out.data_ptr(), out.stride(0), _lib.ptr(status),
               _lib.stream(out.device))
-    return out
-
-
-def qwen3_tts_silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    _check(gate_up, "gate_up")
-    width = gate_up.shape[-1] // 2
-    if gate_up.shape[-1] != 2 * width:
-        raise ValueError("gate_up must have an even last dimension")
-    rows = gate_up.numel() // gate_up.shape[-1]
-    out = torch.empty((*gate_up.shape[:-1], width), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
-    _lib.call("nq_silu_mul", gate_up.data_ptr(), out.data_ptr(), rows, width, _lib.stream(gate_up.device))
     return out
 
 
@@ -449,7 +540,10 @@ __all__ = [
     "pack_linear_weight",
     "quantize_fp8_rows",
     "quantize_fp8_weight_blocks",
+    "add_rmsnorm",
     "qwen3_tts_add_rmsnorm",
     "qwen3_tts_rmsnorm",
     "qwen3_tts_silu_and_mul",
+    "rmsnorm",
+    "silu_mul",
 ]

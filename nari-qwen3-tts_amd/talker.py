@@ -41,8 +41,8 @@ from .layers import (
     linear_partials,
     linear_silu_mul,
     linear_workspace_bytes,
-    qwen3_tts_add_rmsnorm,
-    qwen3_tts_silu_and_mul,
+    add_rmsnorm,
+    silu_mul,
     quantize_fp8_weight_blocks,
 )
 from .sampling import sample_with_counter, sample_with_counter_from_planes, sample_with_uniforms
@@ -216,14 +216,14 @@ class TalkerDecodeStep:
                 linear_silu_mul(self.hidden, layer.gate_up, out=self.act, workspace=ws)
             else:
                 torch.matmul(attended, layer.o.t(), out=self.hidden)
-                qwen3_tts_add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
+                add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
                 torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
-                qwen3_tts_silu_and_mul(self.gate_up, out=self.act)
+                silu_mul(self.gate_up, out=self.act)
             if self.use_hip_linear:
                 linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
             else:
                 torch.matmul(self.act, layer.down.t(), out=self.hidden)
-                qwen3_tts_add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
+                add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
         ctx.advance_sequence_lengths()
         options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
                        eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)

@@ -25,8 +25,11 @@ Everything is float32 numpy over channels-last arrays [T, C].  `decode_whole`
 runs a full sequence with zero initial state; `decode_incremental` runs one
 chunk against explicit state and returns the new state.  Pinned by the
 invariant the reference's adapter docstring claims (:11-19): decoding a
-sequence in chunks equals decoding it whole; and by the PCM16 known answers of
-tests/job_separation/test_codec.py:192-194.
+sequence in chunks equals decoding it whole; by the PCM16 known answers of
+tests/job_separation/test_codec.py:192-194; and primitive by primitive against
+torch's CPU routines (conv1d, conv_transpose1d, scaled_dot_product_attention
+with a band mask, layer_norm, rms_norm, gelu, complex-rotation RoPE and the
+cosine form of SnakeBeta), whole-sequence against chunked.
 """
 
 from __future__ import annotations
@@ -116,6 +119,30 @@ def rope(x: np.ndarray, positions: np.ndarray, theta: float) -> np.ndarray:
     return np.concatenate([a * cos - bb * sin, bb * cos + a * sin], axis=-1).astype(F32)
 
 
+def window_attention(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, p0: int, ctx: int,
+                     window: int) -> np.ndarray:
+    """Sliding-window attention of n fresh queries at positions p0 .. p0+n-1 over the r = window-1
+    retained keys (positions p0-r .. p0-1, of which the last ``ctx`` are valid) followed by the n
+    fresh keys: a query at position t sees valid keys at positions t-window < s <= t, scale 1/sqrt(D)
+    (model/incremental_codec.py:227-262,318-326).  q [n, H, D], keys / vals [r + n, H, D]."""
+
+    n, _, d = q.shape
+    r = window - 1
+    pos = p0 + np.arange(n)
+    kpos = np.concatenate([p0 - r + np.arange(r), pos])
+    kvalid = np.concatenate([np.arange(r) >= r - ctx, np.ones(n, dtype=bool)])
+    att = np.zeros(q.shape, dtype=F32)
+    scale = F32(1.0 / math.sqrt(d))
+    for i in range(n):
+        m = kvalid & (kpos <= pos[i]) & (kpos > pos[i] - window)
+        s = np.einsum("hd,khd->hk", q[i], keys[m]) * scale
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        att[i] = np.einsum("hk,khd->hd", p, vals[m])
+    return att
+
+
 # ---------------------------------------------------------------------------
 # the decoder
 
@@ -177,17 +204,7 @@ def _transformer(w: dict, cfg: dict, x: np.ndarray, st: dict) -> np.ndarray:
         k = rope(rmsnorm(k, L["kn"], cfg["eps"]), pos, cfg["theta"])
         keys = np.concatenate([st["k"][li], k], axis=0)  # [r + n, H, D]
         vals = np.concatenate([st["v"][li], v], axis=0)
-        kpos = np.concatenate([p0 - r + np.arange(r), pos])
-        kvalid = np.concatenate([np.arange(r) >= r - ctx, np.ones(n, dtype=bool)])
-        att = np.zeros((n, h_, d), dtype=F32)
-        scale = F32(1.0 / math.sqrt(d))
-        for i in range(n):
-            m = kvalid & (kpos <= pos[i]) & (kpos > pos[i] - cfg["window"])
-            s = np.einsum("hd,khd->hk", q[i], keys[m]) * scale
-            s = s - s.max(axis=-1, keepdims=True)
-            p = np.exp(s)
-            p /= p.sum(axis=-1, keepdims=True)
-            att[i] = np.einsum("hk,khd->hd", p, vals[m])
+        att = window_attention(q, keys, vals, p0, ctx, cfg["window"])
         h = h + (att.reshape(n, h_ * d) @ L["wo"].T) * L["ls1"]
         y = rmsnorm(h, L["ln2"], cfg["eps"])
         h = h + (gelu(y @ L["w1"].T) @ L["w2"].T) * L["ls2"]

@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -259,7 +261,7 @@ def _lengths(kind, rng):
 def test_fused_decode_rope_attention(nq, device, kind):
     """attend_partials on a decode binding: the fused bins kernel vs the two-kernel path (rope kernel,
     then stream + merge) on the same cache, and vs the oracle."""
-    rng = np.random.default_rng(hash(kind) % 1000)
+    rng = np.random.default_rng(zlib.crc32(kind.encode()) % 1000)
     lengths, capture, pages = _lengths(kind, rng)
     kv, ctx, pubs, planes, splits, att = _fused_case(nq, device, 900 + len(kind), lengths, capture, pages)
     q_out = torch.zeros(capture, 16, 128, dtype=torch.bfloat16, device=device)

@@ -98,7 +98,7 @@ def test_gemm_exact_on_integer_codes(nq, device, m, n, k):
 @pytest.mark.parametrize("m", [64, 5, 128])
 def test_gemm_and_silu_match_oracle(nq, device, m):
     from nari_qwen3_tts_amd import _lib
-    from nari_qwen3_tts_amd.layers import linear_fp8, qwen3_tts_silu_and_mul, quantize_fp8_rows, quantize_fp8_weight_blocks
+    from nari_qwen3_tts_amd.layers import linear_fp8, silu_mul, quantize_fp8_rows, quantize_fp8_weight_blocks
 
     n, k = 1536, 2048
     g = torch.Generator(device=device)
@@ -121,12 +121,12 @@ def test_gemm_and_silu_match_oracle(nq, device, m):
     assert np.all(err <= 2.0 ** -8 * np.abs(want_act) + 1e-6)
     # and the split-K planes summed by the fused SwiGLU equal the bf16 projection the NONE path
     # stores: the fused result is the unfused kernel's on that projection, bit for bit
-    assert torch.equal(act, qwen3_tts_silu_and_mul(y))
+    assert torch.equal(act, silu_mul(y))
 
 
 def test_fused_add_rmsnorm_quantizes_like_unfused(nq, device):
     from nari_qwen3_tts_amd.layers import (add_rmsnorm_fp8, linear_add_rmsnorm, linear_add_rmsnorm_fp8,
-                                           qwen3_tts_add_rmsnorm, quantize_fp8_rows)
+                                           add_rmsnorm, quantize_fp8_rows)
 
     m, n, k = 64, 2048, 2048
     g = torch.Generator(device=device)
@@ -141,11 +141,11 @@ def test_fused_add_rmsnorm_quantizes_like_unfused(nq, device):
     normed = torch.empty(m, n, dtype=torch.bfloat16, device=device)
     linear_add_rmsnorm(x, w, r2, nw, 1e-6, normed)
     q2, s2 = quantize_fp8_rows(normed)
-    # bf16 add-RMSNorm -> FP8 == qwen3_tts_add_rmsnorm -> row quantizer
+    # bf16 add-RMSNorm -> FP8 == add_rmsnorm -> row quantizer
     h = torch.randn(m, n, generator=g, device=device).to(torch.bfloat16)
     r3, r4, h4 = res0.clone(), res0.clone(), h.clone()
     q3, s3 = add_rmsnorm_fp8(h, r3, nw, 1e-6)
-    qwen3_tts_add_rmsnorm(h4, r4, nw, 1e-6)
+    add_rmsnorm(h4, r4, nw, 1e-6)
     q4, s4 = quantize_fp8_rows(h4)
     torch.cuda.synchronize()
     assert torch.equal(r1, r2) and torch.equal(s1, s2) and torch.equal(q1.view(torch.uint8), q2.view(torch.uint8))

@@ -84,7 +84,7 @@ def test_linear_rejects_unsupported_shapes(nq, device):
 
 @pytest.mark.parametrize("m", [64, 37, 128])
 def test_fused_add_rmsnorm_equals_unfused(nq, device, m):
-    from nari_qwen3_tts_amd.layers import linear, linear_add_rmsnorm, qwen3_tts_add_rmsnorm
+    from nari_qwen3_tts_amd.layers import linear, linear_add_rmsnorm, add_rmsnorm
 
     g = torch.Generator(device=device)
     g.manual_seed(11 + m)
@@ -96,7 +96,7 @@ def test_fused_add_rmsnorm_equals_unfused(nq, device, m):
     # unfused: projection, then the add-RMSNorm kernel
     y = linear(x, w)
     res_a = res.clone()
-    qwen3_tts_add_rmsnorm(y, res_a, nw, 1e-6)
+    add_rmsnorm(y, res_a, nw, 1e-6)
     # fused
     res_b = res.clone()
     out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
@@ -108,14 +108,14 @@ def test_fused_add_rmsnorm_equals_unfused(nq, device, m):
 
 @pytest.mark.parametrize("m", [64, 5])
 def test_fused_silu_mul_equals_unfused(nq, device, m):
-    from nari_qwen3_tts_amd.layers import linear, linear_silu_mul, qwen3_tts_silu_and_mul
+    from nari_qwen3_tts_amd.layers import linear, linear_silu_mul, silu_mul
 
     g = torch.Generator(device=device)
     g.manual_seed(21 + m)
     k, inter = 2048, 6144
     x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
     w = (torch.randn(2 * inter, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
-    want = qwen3_tts_silu_and_mul(linear(x, w))
+    want = silu_mul(linear(x, w))
     got = linear_silu_mul(x, w)
     torch.cuda.synchronize()
     assert torch.equal(want, got)

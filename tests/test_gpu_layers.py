@@ -68,7 +68,7 @@ def test_paged_cache_variant_writes_pages(nq, device):
 
 
 def test_add_rmsnorm_rmsnorm_silu(nq, device):
-    from nari_qwen3_tts_amd.layers import qwen3_tts_add_rmsnorm, qwen3_tts_rmsnorm, qwen3_tts_silu_and_mul
+    from nari_qwen3_tts_amd.layers import add_rmsnorm, rmsnorm, silu_mul
 
     g = torch.Generator(device=device)
     g.manual_seed(0)
@@ -77,18 +77,18 @@ def test_add_rmsnorm_rmsnorm_silu(nq, device):
     residual = torch.randn(rows, width, generator=g, device=device).to(torch.bfloat16)
     weight = (torch.rand(width, generator=g, device=device) + 0.5).to(torch.bfloat16)
     h0, r0 = to_np(hidden), to_np(residual)
-    qwen3_tts_add_rmsnorm(hidden, residual, weight, 1e-6)
+    add_rmsnorm(hidden, residual, weight, 1e-6)
     want_h, want_r = o_norms.add_rmsnorm(h0, r0, to_np(weight), 1e-6)
     np.testing.assert_array_equal(to_np(residual), want_r)
     np.testing.assert_allclose(to_np(hidden), want_h, atol=2e-2, rtol=1e-2)
     # torch fp32 reference of RMSNorm (model/layers.py:110-115)
     x = torch.randn(rows, width, generator=g, device=device).to(torch.bfloat16)
-    out = qwen3_tts_rmsnorm(x, weight, 1e-6)
+    out = rmsnorm(x, weight, 1e-6)
     xf = x.float()
     ref = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + 1e-6) * weight.float()).to(torch.bfloat16)
     assert (out.float() - ref.float()).abs().max().item() <= 2e-2
     gu = torch.randn(rows, 2 * 6144, generator=g, device=device).to(torch.bfloat16)
-    act = qwen3_tts_silu_and_mul(gu)
+    act = silu_mul(gu)
     gf, uf = gu.float().chunk(2, dim=-1)
     ref = torch.nn.functional.silu(gf) * uf
     assert (act.float() - ref).abs().max().item() <= 3e-2
@@ -139,7 +139,7 @@ def test_embed_add_rmsnorm_equals_gather_add_then_norm(nq, device):
     import torch.nn.functional as F
 
     from nari_qwen3_tts_amd import _lib
-    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, qwen3_tts_rmsnorm
+    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, rmsnorm
 
     g = torch.Generator(device=device)
     g.manual_seed(3)
@@ -156,7 +156,7 @@ def test_embed_add_rmsnorm_equals_gather_add_then_norm(nq, device):
         status = torch.zeros(1, dtype=torch.int32, device=device)
         embed_add_rmsnorm(ids, table, addend, weight, 1e-6, residual, out, status)
         want_r = torch.add(addend, F.embedding(ids, table))
-        want_o = qwen3_tts_rmsnorm(want_r, weight, 1e-6)
+        want_o = rmsnorm(want_r, weight, 1e-6)
         assert torch.equal(residual, want_r)
         assert torch.equal(out, want_o)
         assert int(status.item()) == 0
@@ -179,7 +179,7 @@ def test_gather_sum_rows_and_gather_norm_equal_their_torch_steps(nq, device):
     import torch.nn.functional as F
 
     from nari_qwen3_tts_amd import _lib
-    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, gather_sum_rows, qwen3_tts_rmsnorm
+    from nari_qwen3_tts_amd.layers import embed_add_rmsnorm, gather_sum_rows, rmsnorm
 
     g = torch.Generator(device=device)
     g.manual_seed(9)
@@ -216,4 +216,4 @@ def test_gather_sum_rows_and_gather_norm_equal_their_torch_steps(nq, device):
     embed_add_rmsnorm(tok, proj, None, weight, 1e-6, h, x)
     want_h = torch.index_select(proj, 0, tok)
     assert torch.equal(h.view(torch.int16), want_h.view(torch.int16))
-    assert torch.equal(x, qwen3_tts_rmsnorm(want_h, weight, 1e-6))
+    assert torch.equal(x, rmsnorm(want_h, weight, 1e-6))
