@@ -323,9 +323,9 @@ CP_ROWS = 128
 CP_SEED = 1004
 
 
-def code_predictor(args, torch, np) -> dict:
-    """Code-predictor frame batch: 128 frames, 5 layers (hidden 1024, 16/8 heads of 64, SwiGLU 3072),
-    15 sequential codebook groups over a 2048 vocab, top-k 50 / T 0.9, one hipGraph replay per batch."""
+def build_code_predictor(torch):
+    """The code-predictor frame batch the benchmark replays: random-init weights, 128 rows with
+    random layer-0 tokens and talker states, counter RNG, captured into a hipGraph."""
 
     from __graft_entry__ import load_package
 
@@ -347,6 +347,14 @@ def code_predictor(args, torch, np) -> dict:
     frame.seed.copy_(torch.randint(0, 1 << 40, (CP_ROWS,), generator=gen))
     frame.offsets.copy_(torch.arange(CP_ROWS * 15).view(CP_ROWS, 15))
     call = HipGraphCaptureDriver(device=dev).capture(frame.forward)
+    return cfg, weights, frame, call
+
+
+def code_predictor(args, torch, np) -> dict:
+    """Code-predictor frame batch: 128 frames, 5 layers (hidden 1024, 16/8 heads of 64, SwiGLU 3072),
+    15 sequential codebook groups over a 2048 vocab, top-k 50 / T 0.9, one hipGraph replay per batch."""
+
+    cfg, weights, frame, call = build_code_predictor(torch)
     for _ in range(args.warmup):
         call.replay()
     torch.cuda.synchronize()

@@ -175,6 +175,9 @@ class TalkerDecodeStep:
             self.act_scales = torch.zeros(rows, c.hidden // 128, dtype=torch.float32, device=dev)
             need = max(need, linear_fp8_workspace_bytes(rows, 2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL))
         self.linear_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        # optional [layers + 1, rows, hidden] bf16 record of the residual stream: the step input, then
+        # the residual after each layer (device-to-device copies, for layer-by-layer checks)
+        self.trace: torch.Tensor | None = None
 
     def forward(self) -> torch.Tensor:
         c = self.w.config
@@ -183,6 +186,9 @@ class TalkerDecodeStep:
         # materialize_decode (executor/talker.py:256-262) and the first input norm, one launch
         embed_add_rmsnorm(self.text_ids, self.w.text_embedding, self.step_embed, self.w.layers[0].input_norm,
                           c.rms_eps, self.residual, self.hidden)
+        trace = self.trace
+        if trace is not None:
+            trace[0].copy_(self.residual)
         q_w = c.num_qo_heads * c.head_dim
         kv_w = c.num_kv_heads * c.head_dim
         ws = self.linear_workspace
@@ -224,6 +230,8 @@ class TalkerDecodeStep:
             else:
                 torch.matmul(self.act, layer.down.t(), out=self.hidden)
                 add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
+            if trace is not None:
+                trace[index + 1].copy_(self.residual)
         ctx.advance_sequence_lengths()
         options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
                        eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)

@@ -98,3 +98,43 @@ def test_frame_replays_in_a_graph(nq, device):
         torch.cuda.synchronize()
         assert torch.equal(graph_frames, frame.frames)
         assert torch.equal(graph_sum, frame.codec_sum)
+
+
+@pytest.mark.timeout(300)
+def test_bench_frame_b128_matches_oracle(nq, device):
+    """The frame batch bench.py replays (5 layers, 128 rows, counter RNG, hipGraph) vs the oracle,
+    teacher-forced with the replay's own tokens: logits of every group within bf16 tolerance, every
+    draw bit-exact, codec_sum exact; a second replay gives the same bits."""
+    import bench
+
+    cfg, w, frame, call = bench.build_code_predictor(torch)
+    rows = frame.tokens.shape[1]
+    call.replay()
+    torch.cuda.synchronize()
+    first = [frame.frames.clone(), frame.codec_sum.clone(), frame.logits.clone()]
+    call.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(first[0], frame.frames) and torch.equal(first[1], frame.codec_sum)
+    assert torch.equal(first[2], frame.logits)
+
+    hw = _host_weights(w)
+    hcfg = dict(num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
+                rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta, num_code_groups=cfg.num_code_groups)
+    tokens = to_np(frame.tokens)
+    logits, csum, cache = o_cp.whole_frame(hw, hcfg, to_np(frame.layer0_token), to_np(frame.past_hidden), tokens)
+    got = to_np(frame.logits)
+    # relative to the logits' RMS (about 0.64 here): the device and the oracle round the same bf16
+    # pipeline from fp32 sums taken in different orders, and each keeps its own bf16 K/V cache over
+    # the 16 passes x 5 layers, so differences of one bf16 step (0.4 % at the RMS) carry from pass
+    # to pass; a wrong position, slot or weight moves logits by the order of the RMS itself
+    err = np.abs(got - logits)
+    rms = float(np.sqrt(np.mean(logits.astype(np.float64) ** 2)))
+    assert err.mean() <= 8e-3 * rms and err.max() <= 8e-2 * rms, (err.mean() / rms, err.max() / rms)
+    seeds, offs = to_np(frame.seed), to_np(frame.offsets)
+    for k in range(15):
+        u = np.array([o_samp.uniform_from_counter(int(seeds[r]), int(offs[r, k])) for r in range(rows)], np.float32)
+        want_tok = o_samp.sample(got[k], to_np(frame.temperature), to_np(frame.top_k), to_np(frame.top_p), u)
+        np.testing.assert_array_equal(tokens[k], want_tok)
+    np.testing.assert_array_equal(to_np(frame.frames)[:, 1:], tokens.T)
+    np.testing.assert_array_equal(to_np(frame.codec_sum), csum)
+    np.testing.assert_allclose(to_np(frame.kv_cache), cache, atol=3e-2, rtol=2e-2)

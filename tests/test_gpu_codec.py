@@ -13,11 +13,11 @@ from test_oracle_codec import small_config
 pytestmark = pytest.mark.gpu
 
 
-def _run(cfg, device, seed, calls):
+def _run(cfg, device, seed, calls, max_streams=8):
     from nari_qwen3_tts_amd.codec import CodecWeights, IncrementalCodecDecoder
 
     weights = CodecWeights(cfg, device, seed=seed)
-    dec = IncrementalCodecDecoder(weights, max_streams=8)
+    dec = IncrementalCodecDecoder(weights, max_streams=max_streams)
     rng = np.random.default_rng(seed + 1)
     streams = len(calls[0])
     states = [dec.new_state() for _ in range(streams)]
@@ -25,7 +25,7 @@ def _run(cfg, device, seed, calls):
     w = weights.host()
     worst_rms, worst_max = 0.0, 0.0
     for frames in calls:
-        codes = [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, f))) for f in frames]
+        codes = [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, int(f)))) for f in frames]
         wav, pcm = dec(codes, states)
         torch.cuda.synchronize()
         for b, f in enumerate(frames):
@@ -57,6 +57,24 @@ def test_full_codec_ragged_two_calls(nq, device):
     assert rms <= 1e-3, (rms, mx)
     pool = dec.pool
     assert pool.frame_pos[states[0].slot].item() == 5 and pool.ctx[states[1].slot].item() == 6
+
+
+@pytest.mark.timeout(400)
+def test_full_codec_32_streams_past_the_window(nq, device):
+    """The full synthetic decoder at its serving shape: 32 streams, three consecutive calls of
+    U{12..48} fresh frames each, so every stream's retained K/V window (25 frames) is filled,
+    crossed and evicted, against the oracle with per-stream state carried on the host."""
+    from nari_qwen3_tts_amd.codec import CodecConfig
+
+    rng = np.random.default_rng(1005)
+    calls = [list(rng.integers(12, 49, size=32)) for _ in range(3)]
+    rms, mx, dec, states = _run(CodecConfig(), device, 41, calls, max_streams=32)
+    print(f"32-stream codec: worst PCM rms err {rms:.3g}, max {mx:.3g}")
+    assert rms <= 1e-3, (rms, mx)
+    for b, st in enumerate(states):
+        total = sum(c[b] for c in calls)
+        assert dec.pool.frame_pos[st.slot].item() == total
+        assert dec.pool.ctx[st.slot].item() == min(total, CodecConfig().retained_context)
 
 
 def test_chunking_does_not_change_the_audio(nq, device):
