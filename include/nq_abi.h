@@ -124,6 +124,31 @@ int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint
                        void *workspace, int64_t workspace_bytes, int32_t *status, void *stream);
 
 /*
+ * nq_attention_plan followed by nq_paged_attention (positions and write slots
+ * not planned, so not usable before nq_paged_decode_rope_attention), with the
+ * plan and partials in the library's own static device scratch instead of a
+ * caller workspace: this call allocates nothing, never synchronises and issues
+ * no memset.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under hipGraph capture that forbids it, tight
+ * serving loops, harnesses without an allocator).  Limit: the workspace that
+ * nq_attention_workspace_bytes reports for (max_query_tokens, max_pages, ...)
+ * must not exceed NQ_NOALLOC_SCRATCH_BYTES (32 MiB per GPU, held until the
+ * process ends; a 128-row decode batch over a 32768-page pool needs about 22
+ * MiB), else NQ_ERR_INVALID_ARGUMENT before any launch.  Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (two streams, two
+ * threads) race; calls in stream order do not.
+ */
+#define NQ_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                               const int32_t *last_page_len, const int32_t *kv_indices, int n_rows,
+                               const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
+                               int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
+                               int num_pages, int page_size, int num_qo_heads, int num_kv_heads,
+                               int head_dim, float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
+                               int max_query_tokens, int max_pages, int parts, int32_t *status,
+                               void *stream);
+
+/*
  * Code-predictor short-cache attention: one query per row over the first
  * valid_length positions of a dense per-row cache.
  * Replaces decode_attn_nhd_short_cache (model/kernels.py:408-520).

@@ -31,6 +31,7 @@ NQ_EPI_PARTIALS = 3
 NQ_WEIGHT_PACKED = -1
 NQ_ATTN_DECODE = 1
 NQ_ATTN_PREFILL = 2
+NQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -47,6 +48,8 @@ _SIGNATURES: dict[str, list] = {
     "nq_attention_plan": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P],
     "nq_paged_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _P, _I, _I, _I, _I, _F, _P, _L, _L,
                            _I, _I, _I, _P, _L, _P, _P],
+    "nq_paged_attention_noalloc": [_P, _P, _P, _P, _I, _P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F,
+                                   _P, _L, _L, _I, _I, _I, _P, _P],
     "nq_cp_short_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _L, _L, _P],
     "nq_qk_norm_rope_kv_write": [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _I, _I, _I, _I, _F,
                                  _F, _I, _P, _L, _L, _L, _L, _P, _P, _I, _P],

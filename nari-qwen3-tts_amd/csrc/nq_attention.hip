@@ -27,6 +27,8 @@
 // accumulation, bf16 output), the bottom-right causal rule of
 // BatchPrefillWithPagedKVCacheWrapper(causal=True) (talker_kv.py:218) and the
 // short-cache kernel of model/kernels.py:408-463.
+#include <mutex>
+
 #include "nq_common.h"
 #include "nq_internal.h"
 
@@ -2019,4 +2021,74 @@ extern "C" int nq_paged_decode_rope_attention(const float *partials, int splits,
     }
 #undef NQ_BIN
     return NQ_LAUNCH_STATUS();
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of nq_attention_plan + nq_paged_attention.
+//
+// The plan and the partial results live in `scratch`, a file-scope device
+// array (one copy per GPU, held until the process ends).  In host code the
+// name `scratch` is only a host-side stand-in: its device address is fetched
+// once per device with hipGetSymbolAddress and only that pointer is passed to
+// the kernels.  The plan kernel writes every counter the attention kernels
+// read (and zeroes the split-row arrival counts), so nothing is cleared on
+// the host.  Calls that overlap on one GPU share the array and race.
+
+static __device__ __align__(256) char scratch[NQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+char *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first call there).
+int scratch_on_current_device(char **out) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return NQ_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return NQ_ERR_LAUNCH;
+        g_scratch_ptr[device] = static_cast<char *>(ptr);
+    }
+    *out = g_scratch_ptr[device];
+    return NQ_OK;
+}
+
+}  // namespace
+
+extern "C" int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                                          const int32_t *last_page_len, const int32_t *kv_indices, int n_rows,
+                                          const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
+                                          int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
+                                          int num_pages, int page_size, int num_qo_heads, int num_kv_heads,
+                                          int head_dim, float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
+                                          int max_query_tokens, int max_pages, int parts, int32_t *status,
+                                          void *stream) {
+    // every check of the two entry points it stands for, before anything is launched
+    NQ_CHECK_ARG(n_rows >= 1 && max_query_tokens >= 1 && max_pages >= 1);
+    if (n_rows > nq::kPlanThreads) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(q && cache && kv_indptr && last_page_len && kv_indices && out);
+    NQ_CHECK_ARG(qo_indptr || n_rows <= max_query_tokens);
+    NQ_CHECK_ARG(parts >= 1 && parts <= (NQ_ATTN_DECODE | NQ_ATTN_PREFILL));
+    NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1);
+    NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
+    if (!nq::aligned16(q) || !nq::aligned16(cache) || !nq::aligned16(out)) return NQ_ERR_UNSUPPORTED;
+    if ((q_s0 | q_s1 | c_page | c_kind | c_slot | c_head | o_s0 | o_s1) & 7) return NQ_ERR_UNSUPPORTED;
+    const int G = num_qo_heads / num_kv_heads;
+    if ((head_dim != 64 && head_dim != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return NQ_ERR_UNSUPPORTED;
+    const PlanLayout L =
+        nq::plan_layout(max_query_tokens, max_pages, page_size, num_qo_heads, num_kv_heads, head_dim);
+    if (L.total > NQ_NOALLOC_SCRATCH_BYTES) return NQ_ERR_INVALID_ARGUMENT;  // beyond the static scratch
+    char *ws = nullptr;
+    const int rc = scratch_on_current_device(&ws);
+    if (rc != NQ_OK) return rc;
+    const int planned = nq_attention_plan(qo_indptr, kv_indptr, last_page_len, kv_indices, nullptr, nullptr,
+                                          nullptr, n_rows, max_query_tokens, max_pages, page_size, num_qo_heads,
+                                          num_kv_heads, head_dim, ws, NQ_NOALLOC_SCRATCH_BYTES, stream);
+    if (planned != NQ_OK) return planned;
+    return nq_paged_attention(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,
+                              page_size, num_qo_heads, num_kv_heads, head_dim, sm_scale, out, o_s0, o_s1,
+                              max_query_tokens, max_pages, parts, ws, NQ_NOALLOC_SCRATCH_BYTES, status, stream);
 }

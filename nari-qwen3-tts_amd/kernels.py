@@ -216,7 +216,46 @@ def decode_attn_nhd_short_cache(query, key_cache, value_cache, cache_length: int
     return output.unsqueeze(1) if squeeze else output
 
 
+def paged_attention_noalloc(query: torch.Tensor, layer_cache: torch.Tensor, metadata, *, max_pages: int,
+                            sm_scale: float | None = None, parts: int = _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_PREFILL,
+                            status: torch.Tensor | None = None, out: torch.Tensor) -> torch.Tensor:
+    """Paged attention of ``query`` [tokens, Hq, D] over one layer ``[pages, 2, ps, Hkv, D]`` of the
+    cache with ``metadata`` (a TalkerAttentionMetadata), planned and run with the library's static
+    scratch (``nq_paged_attention_noalloc``): no device allocation, no workspace argument.  ``out``
+    is required for the same reason.  Calls that overlap on one GPU share the scratch and race."""
+
+    _require_bf16(query, layer_cache, out)
+    if query.ndim != 3 or layer_cache.ndim != 5 or layer_cache.shape[1] != 2:
+        raise ValueError("query must be [tokens, Hq, D] and the cache [pages, 2, page_size, Hkv, D]")
+    tokens, hq, d = query.shape
+    pages, _, page_size, hkv, d_cache = layer_cache.shape
+    if d_cache != d or out.shape != query.shape or out.stride(-1) != 1 or query.stride(-1) != 1:
+        raise ValueError("query, cache and out disagree on the head layout")
+    rows = metadata.paged_kv_indptr.numel() - 1
+    need = int(_lib.load().nq_attention_workspace_bytes(tokens, int(max_pages), page_size, hq, hkv, d))
+    _lib.check(min(need, 0), "nq_attention_workspace_bytes")
+    if need > _lib.NQ_NOALLOC_SCRATCH_BYTES:
+        raise ValueError(f"this batch needs {need} bytes of attention scratch; the no-allocation entry point "
+                         f"holds {_lib.NQ_NOALLOC_SCRATCH_BYTES} per GPU (use the workspace path)")
+    for t in (metadata.paged_kv_indptr, metadata.paged_kv_last_page_len, metadata.paged_kv_indices):
+        if t.dtype != torch.int32:
+            raise TypeError("paged metadata must be int32")
+    _lib.require_device(query, layer_cache, out, metadata.paged_kv_indptr, status)
+    scale = float(d) ** -0.5 if sm_scale is None else float(sm_scale)
+    _lib.call(
+        "nq_paged_attention_noalloc",
+        _lib.ptr(metadata.qo_indptr), metadata.paged_kv_indptr.data_ptr(),
+        metadata.paged_kv_last_page_len.data_ptr(), metadata.paged_kv_indices.data_ptr(), rows,
+        query.data_ptr(), query.stride(0), query.stride(1), layer_cache.data_ptr(), layer_cache.stride(0),
+        layer_cache.stride(1), layer_cache.stride(2), layer_cache.stride(3), pages, page_size, hq, hkv, d, scale,
+        out.data_ptr(), out.stride(0), out.stride(1), tokens, int(max_pages), int(parts), _lib.ptr(status),
+        _lib.stream(query.device),
+    )
+    return out
+
+
 __all__ = [
+    "paged_attention_noalloc",
     "decode_attn_nhd_short_cache",
     "paired_qk_norm_rope_",
     "paired_qk_norm_rope_dense_cache_",
