@@ -114,11 +114,24 @@ def build_workload(torch, np):
 
 
 def run_step(w):
+    """One decision: GPU planning, the graph replay, the step report's copy to the host, the KV
+    publication.  The report of the previous step is read here (fail closed: a bad status raises),
+    so the host never waits for the step it just queued."""
+
     pubs = w["kv"].prepare_decode(w["ctx"], w["key"], w["rids"])
     w["call"].replay()
+    ticket = w["step"].report.fetch()
     w["step"].offsets.add_(512)
     for p in pubs:
         p.publish()
+    previous, w["report"] = w.get("report"), ticket
+    if previous is not None:
+        w["step"].report.read(previous)
+
+
+def finish_steps(w):
+    if w.get("report") is not None:
+        w["step"].report.read(w.pop("report"))
 
 
 def kv_tokens(w) -> int:
@@ -261,6 +274,7 @@ def talker_decode(args, torch, np) -> dict:
     t0 = time.perf_counter()
     for _ in range(args.steps):
         run_step(w)
+    finish_steps(w)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kv_after = kv_tokens(w)
@@ -620,14 +634,22 @@ def mixed_attention(args, torch, np) -> dict:
             rids.append(rid)
         key = PrefillKey(rows, int(sum(advances)))
         ctx = kv.create_prefill(key, slot=0)
+        rows_t, adv_t = tuple(rids), tuple(int(a) for a in advances)
+        for _ in range(5):  # first calls allocate the pinned staging rings
+            kv.abort(kv.prepare_prefill(ctx, key, rows_t, adv_t))
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        reps = 20
-        for _ in range(reps):  # the planner: host staging + GPU page table + attention plan
-            pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(int(a) for a in advances))
+        reps, plan_s, abort_s = 50, 0.0, 0.0
+        for _ in range(reps):  # a decision: ledger + staging + GPU page table + attention plan; then the returns
+            t0 = time.perf_counter()
+            pubs = kv.prepare_prefill(ctx, key, rows_t, adv_t)
+            t1 = time.perf_counter()
             kv.abort(pubs)
+            abort_s += time.perf_counter() - t1
+            plan_s += t1 - t0
         torch.cuda.synchronize()
-        plan_us = (time.perf_counter() - t0) / reps * 1e6
+        plan_us = plan_s / reps * 1e6
+        log(f"planner host time: {plan_us:.0f} us per decision, {abort_s / reps * 1e6:.0f} us per abort of "
+            f"{len(rows_t)} rows (pages returned to the device free list by a GPU merge)")
         pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(int(a) for a in advances))
         q = torch.randn(key.token_capacity, cfg.num_qo_heads, cfg.head_dim, device=dev).to(torch.bfloat16)
         call = HipGraphCaptureDriver(device=dev).capture(lambda: [ctx.run_attention(q, i) for i in range(layers)])

@@ -69,6 +69,38 @@ int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start, const int32
                    int grid_blocks, void *stream);
 
 /*
+ * Return pages to the device copy of the sorted free list: out[0, n_free +
+ * n_returned) = the sorted union of free_pages[0, n_free) and returned[0,
+ * n_returned), both sorted ascending and distinct (out must not alias either).
+ * The device side of PagedKVAllocator's page returns (executor/cache.py:
+ * 129-133 remove_request, :208-211 discard), so the free list the planner
+ * reads never has to be uploaded from the host again.  A returned page that is
+ * already free sets status[0] (may be NULL) to NQ_ERR_INVALID_ARGUMENT and is
+ * dropped.
+ */
+int nq_free_list_merge(const int32_t *free_pages, int n_free, const int32_t *returned, int n_returned,
+                       int32_t *out, int32_t *status, void *stream);
+
+/*
+ * One decode step's report in one small device buffer, so the host reads it
+ * with a single copy per decision (replaces the per-row
+ * `int(tokens[index].item()) == codec_eos_token_id` reads of
+ * engine/pipeline.py:585-593 and makes the step fail closed):
+ *   report[0] = plan_status[0] (the planner's NQ_OK / NQ_ERR_CAPACITY),
+ *   report[1] = merge_status[0] (nq_free_list_merge), report[2] =
+ *               attention_status[0], report[3] = embed_status[0]: each of
+ *               these three is then reset to NQ_OK for the next step (any of
+ *               the four status pointers may be NULL: reported as NQ_OK),
+ *   report[4] = number of tokens outside [0, vocab), report[5..7] = 0,
+ *   report[NQ_REPORT_HEAD + r] = tokens[r] == eos_id, r < rows.
+ * One workgroup; graph-capturable.
+ */
+#define NQ_REPORT_HEAD 8
+int nq_step_report(const int32_t *plan_status, int32_t *merge_status, int32_t *attention_status,
+                   int32_t *embed_status, const int64_t *tokens, int rows, int64_t eos_id, int64_t vocab,
+                   int32_t *report, void *stream);
+
+/*
  * Work decomposition for nq_paged_attention, computed on the GPU from the
  * ragged metadata.  Replaces the host-side plan() of the FlashInfer wrappers
  * (executor/talker_kv.py:175-223 prefill, :259-303 decode).

@@ -32,6 +32,7 @@ NQ_WEIGHT_PACKED = -1
 NQ_ATTN_DECODE = 1
 NQ_ATTN_PREFILL = 2
 NQ_NOALLOC_SCRATCH_BYTES = 32 << 20
+NQ_REPORT_HEAD = 8
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -44,6 +45,8 @@ _SIGNATURES: dict[str, list] = {
     "nq_status_string": [_I],
     "nq_plan_ragged": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P, _I, _P, _I, _P, _P, _P, _L,
                        _P, _P, _P, _P, _P, _I, _P],
+    "nq_free_list_merge": [_P, _I, _P, _I, _P, _P, _P],
+    "nq_step_report": [_P, _P, _P, _P, _P, _I, _L, _L, _P, _P],
     "nq_attention_workspace_bytes": [_I, _I, _I, _I, _I, _I],
     "nq_attention_plan": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P],
     "nq_paged_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _P, _I, _I, _I, _I, _F, _P, _L, _L,

@@ -1,28 +1,43 @@
-"""Host-side page ownership with pending / publish / discard KV transactions.
+"""Host ledger of KV page ownership for the paged talker KV.
 
-Mirrors the behaviour of the reference allocator (executor/cache.py:19-212):
-a sorted free list whose lowest pages are handed out in row order (:153-162),
-publications that become the request's committed state only on publish
-(:186-207), discards that return the proposed new pages (:208-211), stale
-publications rejected with StaleKVPublicationError (:62-75), rollback of a
-failed multi-row reservation (:178-183).
+Every live request owns a ledger slot, a small integer that is also the request's row of the
+device page table.  The committed numbers of each request (sequence length, RoPE position start,
+page count) sit in numpy arrays indexed by slot, so the planner's per-row inputs are array
+gathers; the page ids are kept as one tuple per request because the engine-facing proposal
+carries them as a tuple.  The free pages are one sorted numpy array with a consumed front: a
+reservation hands out the lowest free pages in row order by moving the front, a return inserts
+the pages back in sorted position.
 
-On top of that, the allocator counts how many free pages a reservation took
-from the front of the free list and flags when pages came back, so the
-device copy of the free list (read by the GPU planner) can follow it with an
-upload only when pages are returned.
+The device copy of the free list is not uploaded from here.  Every change to the free list is
+also appended to an ordered log (pages taken from the front, sorted pages returned); the owner of
+the device copy replays the log on the GPU before its next planner launch (front offset moves,
+``nq_free_list_merge`` for returns), so both copies stay equal.
+
+Contract kept from the reference allocator (executor/cache.py:43-212), with its messages: a
+reservation is all-or-nothing and returns one pending publication per row; a publication becomes
+the request's committed state only when published, and a discard gives its new pages back; a
+publication whose request has since changed, or that was already published or discarded, is stale
+(``StaleKVPublicationError``); a request with a reservation in flight can neither reserve again
+nor be removed (``SlotBusyError``); running out of pages raises ``KVAllocationError`` before
+anything is taken.
 """
 
 from __future__ import annotations
 
-import bisect
+import heapq
 from dataclasses import dataclass
 
+import numpy as np
+
 from .errors import KVAllocationError, SlotBusyError, StaleKVPublicationError
+
+_STALE = "Talker KV publication is stale or no longer pending"
 
 
 @dataclass(frozen=True, slots=True)
 class RequestKVState:
+    """Committed KV of one request (field names of executor/cache.py:25-31)."""
+
     request_id: str
     page_indices: tuple[int, ...] = ()
     sequence_length: int = 0
@@ -39,41 +54,53 @@ class KVPublicationProposal:
     length: int
 
 
-@dataclass(slots=True)
-class _Pending:
-    token: int
-    prior: RequestKVState
-    proposed_pages: tuple[int, ...]
-    new_pages: tuple[int, ...]
-    sequence_advance: int
-    status: str = "pending"
-
-
-@dataclass(slots=True)
 class PendingKVPublication:
-    _allocator: "PagedKVAllocator"
-    request_id: str
-    token: int
-    prior_version: int
-    page_indices: tuple[int, ...]
-    sequence_advance: int
+    """One row of a reservation: publish() commits it, discard() gives its new pages back.  The
+    ledger keeps this object as the request's in-flight entry; it stays live while it is that
+    entry and the request's committed state is still the one it was made against."""
+
+    __slots__ = ("_ledger", "request_id", "token", "prior_version", "sequence_advance", "_prior", "_advance",
+                 "_taken", "_lo", "_hi", "_pages")
+
+    def __init__(self, ledger: "PagedKVAllocator", request_id: str, token: int, prior: RequestKVState,
+                 taken: np.ndarray, lo: int, hi: int, advance: int) -> None:
+        self._ledger = ledger
+        self.request_id = request_id
+        self.token = token
+        self.prior_version = prior.version
+        self.sequence_advance = advance
+        self._prior = prior
+        self._advance = advance
+        self._taken, self._lo, self._hi = taken, lo, hi
+        self._pages: tuple[int, ...] | None = None
+
+    @property
+    def new_pages(self) -> np.ndarray:
+        return self._taken[self._lo: self._hi]
+
+    @property
+    def page_indices(self) -> tuple[int, ...]:
+        """The request's pages if published: its committed pages, then the new ones."""
+
+        if self._pages is None:
+            self._pages = self._prior.page_indices + tuple(self._taken[self._lo: self._hi].tolist())
+        return self._pages
 
     def proposal(self) -> KVPublicationProposal:
-        current = self._allocator.state(self.request_id)
+        current = self._ledger.state(self.request_id)
         return KVPublicationProposal(self.request_id, self.page_indices, current.sequence_length + self.sequence_advance)
 
     def validate(self) -> None:
-        self._allocator._check_live(self)
-        if self.sequence_advance < 1:
-            raise StaleKVPublicationError("Talker KV publication is stale or no longer pending")
+        self._ledger._live(self)
 
     def publish(self) -> None:
-        self.validate()
-        self._allocator._finish(self, publish=True)
+        self._ledger._settle(self, commit=True)
 
     def discard(self) -> None:
-        self.validate()
-        self._allocator._finish(self, publish=False)
+        self._ledger._settle(self, commit=False)
+
+    def __repr__(self) -> str:
+        return f"PendingKVPublication({self.request_id!r}, token={self.token}, advance={self.sequence_advance})"
 
 
 @dataclass(frozen=True, slots=True)
@@ -83,43 +110,127 @@ class KVReservation:
 
 
 class PagedKVAllocator:
-    """Fixed-capacity page allocator; no scheduling, no transfers."""
+    """Fixed-capacity page ledger; no scheduling, no transfers, no device memory."""
 
     def __init__(self, *, total_pages: int, page_size: int) -> None:
         if total_pages < 1 or page_size < 1:
             raise ValueError("paged KV capacity must be positive")
         self.total_pages = total_pages
         self.page_size = page_size
-        self._free: list[int] = list(range(total_pages))
+        self._free = np.arange(total_pages, dtype=np.int32)
+        self._front = 0
         self._states: dict[str, RequestKVState] = {}
-        self._pending: dict[str, _Pending] = {}
-        self._tokens = 0
-        # Incremented whenever pages return to the free list (device copy is stale).
-        self.free_list_epoch = 0
+        self._slot_of: dict[str, int] = {}
+        self._spare: list[int] = []
+        self._capacity = 0
+        self.length = np.zeros(0, dtype=np.int32)
+        self.position = np.zeros(0, dtype=np.int32)
+        self.page_count = np.zeros(0, dtype=np.int32)
+        self._grow(64)
+        self._inflight: dict[str, PendingKVPublication] = {}
+        self._serial = 0
+        # ordered changes of the free list the device copy has not seen: ("take", n) / ("return", pages)
+        self._log: list[tuple[str, object]] = []
+        self._returning: list[np.ndarray] = []
+        # set when the free list changed in a way the log does not describe (device copy must be re-sent)
+        self.resend_free_list = False
+
+    # -- capacity --------------------------------------------------------------
+    def _grow(self, capacity: int) -> None:
+        for name in ("length", "position", "page_count"):
+            old = getattr(self, name)
+            grown = np.zeros(capacity, dtype=np.int32)
+            grown[: old.shape[0]] = old
+            setattr(self, name, grown)
+        heapq.heapify(self._spare)
+        for slot in range(self._capacity, capacity):
+            heapq.heappush(self._spare, slot)
+        self._capacity = capacity
+
+    @property
+    def slot_capacity(self) -> int:
+        return self._capacity
 
     @property
     def free_pages(self) -> int:
-        return len(self._free)
+        self._merge_returns()
+        return int(self._free.shape[0] - self._front)
 
     def free_list(self) -> tuple[int, ...]:
-        return tuple(self._free)
+        self._merge_returns()
+        return tuple(self._free[self._front:].tolist())
+
+    def free_array(self) -> np.ndarray:
+        """The sorted free pages (a read-only view)."""
+
+        self._merge_returns()
+        view = self._free[self._front:]
+        view.flags.writeable = False
+        return view
+
+    def _take_front(self, count: int) -> np.ndarray:
+        self._merge_returns()
+        taken = self._free[self._front: self._front + count]
+        self._front += count
+        if count:
+            self._log.append(("take", count))
+        return taken
+
+    def _give_back(self, pages: np.ndarray) -> None:
+        """Queue pages for return; they join the free list (in one merge) before it is next read."""
+
+        if pages.shape[0]:
+            self._returning.append(pages)
+
+    def _merge_returns(self) -> None:
+        if not self._returning:
+            return
+        ret = self._returning[0] if len(self._returning) == 1 else np.concatenate(self._returning)
+        self._returning = []
+        ret = np.sort(ret.astype(np.int32, copy=False))
+        live = self._free[self._front:]
+        at = np.searchsorted(live, ret)
+        if (ret.shape[0] > 1 and np.any(ret[1:] == ret[:-1])) or (
+                live.shape[0] and np.any(live[np.minimum(at, live.shape[0] - 1)] == ret)):
+            raise RuntimeError("a KV page was returned while already free")
+        self._free = np.insert(live, at, ret)
+        self._front = 0
+        self._log.append(("return", ret))
+
+    def drain_log(self) -> list[tuple[str, object]]:
+        """The free-list changes since the last drain, in order (for the device copy)."""
+
+        self._merge_returns()
+        log, self._log = self._log, []
+        return log
 
     def claim_scratch_pages(self, count: int) -> tuple[int, ...]:
         if isinstance(count, bool) or not isinstance(count, int) or count < 1:
             raise ValueError("scratch page count must be a positive integer")
-        if count > len(self._free):
+        if count > self.free_pages:
             raise KVAllocationError(f"cannot reserve {count} Talker scratch pages")
-        taken = tuple(self._free[:count])
-        self._free = self._free[count:]
-        self.free_list_epoch += 1
-        return taken
+        return tuple(self._take_front(count).tolist())
 
+    # -- requests --------------------------------------------------------------
     def add_request(self, request_id: str) -> None:
         if not isinstance(request_id, str) or not request_id:
             raise ValueError("request_id must be a non-empty string")
         if request_id in self._states:
             raise ValueError(f"request {request_id!r} already owns KV state")
+        if not self._spare:
+            self._grow(2 * self._capacity)
+        slot = heapq.heappop(self._spare)
+        self.length[slot] = self.position[slot] = self.page_count[slot] = 0
+        self._slot_of[request_id] = slot
         self._states[request_id] = RequestKVState(request_id)
+
+    def slot(self, request_id: str) -> int:
+        """The request's ledger slot (its row of the device page table)."""
+
+        slot = self._slot_of.get(request_id)
+        if slot is None:
+            raise KeyError(f"unknown Talker KV request {request_id!r}")
+        return slot
 
     def state(self, request_id: str) -> RequestKVState:
         state = self._states.get(request_id)
@@ -128,110 +239,110 @@ class PagedKVAllocator:
         return state
 
     def remove_request(self, request_id: str) -> None:
-        if request_id in self._pending:
+        if request_id in self._inflight:
             raise SlotBusyError(f"request {request_id!r} KV is in flight")
         state = self.state(request_id)
-        self._return_pages(state.page_indices)
+        self._give_back(np.asarray(state.page_indices, dtype=np.int32))
         del self._states[request_id]
+        heapq.heappush(self._spare, self._slot_of.pop(request_id))
 
     def adopt(self, request_id: str, pages: tuple[int, ...], sequence_length: int, position_start: int) -> None:
         """Install a committed state that owns ``pages`` (benchmark and test setup).
 
-        Lets a workload start from pages scattered over the pool, which the
-        lowest-free-page policy never produces by itself.
+        Lets a workload start from pages scattered over the pool, which the lowest-free-page policy
+        never produces by itself; the device copy of the free list is then re-sent once.
         """
 
         state = self.state(request_id)
-        if state.page_indices or request_id in self._pending:
+        if state.page_indices or request_id in self._inflight:
             raise ValueError(f"request {request_id!r} already owns pages")
-        needed = -(-sequence_length // self.page_size)
-        if len(pages) != needed:
+        if len(pages) != -(-sequence_length // self.page_size):
             raise ValueError("adopted pages do not match the sequence length")
-        free = set(self._free)
-        if len(set(pages)) != len(pages) or any(p not in free for p in pages):
+        want = np.asarray(pages, dtype=np.int32)
+        self._merge_returns()
+        live = self._free[self._front:]
+        if np.unique(want).shape[0] != want.shape[0] or not np.isin(want, live).all():
             raise KVAllocationError("adopted pages must be distinct free pages")
-        taken = set(pages)
-        self._free = [p for p in self._free if p not in taken]
-        self.free_list_epoch += 1
-        self._states[request_id] = RequestKVState(
-            request_id, tuple(pages), sequence_length, position_start, state.version + 1
-        )
+        self._free = live[~np.isin(live, want)]
+        self._front = 0
+        self.resend_free_list = True
+        self._log.clear()
+        slot = self._slot_of[request_id]
+        self.length[slot], self.position[slot], self.page_count[slot] = sequence_length, position_start, len(pages)
+        self._states[request_id] = RequestKVState(request_id, tuple(int(p) for p in pages), sequence_length,
+                                                  position_start, state.version + 1)
 
-    def _return_pages(self, pages) -> None:
-        if not pages:
-            return
-        for page in pages:
-            bisect.insort(self._free, page)
-        self.free_list_epoch += 1
+    # -- reservations ----------------------------------------------------------
+    def slots(self, request_ids: tuple[str, ...]) -> np.ndarray:
+        try:
+            return np.fromiter(map(self._slot_of.__getitem__, request_ids), dtype=np.int64, count=len(request_ids))
+        except KeyError as missing:
+            raise KeyError(f"unknown Talker KV request {missing.args[0]!r}") from None
 
     def reserve(self, request_ids: tuple[str, ...], advances: tuple[int, ...]) -> KVReservation:
-        if not request_ids or len(request_ids) != len(advances):
+        rows = len(request_ids)
+        if not rows or rows != len(advances):
             raise ValueError("KV reservation rows must be non-empty and aligned")
-        if len(set(request_ids)) != len(request_ids):
+        if len(set(request_ids)) != rows:
             raise ValueError("KV reservation request rows must be unique")
-        states = [self.state(rid) for rid in request_ids]
-        for rid, advance in zip(request_ids, advances):
-            if rid in self._pending:
-                raise SlotBusyError(f"request {rid!r} KV is already in flight")
-            if isinstance(advance, bool) or not isinstance(advance, int) or advance < 1:
-                raise ValueError("KV sequence advances must be positive integers")
-        # Page demand of every row first, so a failure leaves nothing behind.
-        missing = []
-        for rid, state, advance in zip(request_ids, states, advances):
-            needed = -(-(state.sequence_length + advance) // self.page_size)
-            missing.append(needed - len(state.page_indices))
-        taken = 0
-        for rid, miss in zip(request_ids, missing):
-            if miss > len(self._free) - taken:
-                raise KVAllocationError(
-                    f"Talker KV needs {miss} pages for {rid!r}, only {len(self._free) - taken} remain"
-                )
-            taken += max(miss, 0)
-        publications = []
-        cursor = 0
-        for rid, state, advance, miss in zip(request_ids, states, advances, missing):
-            new = tuple(self._free[cursor : cursor + max(miss, 0)])
-            cursor += len(new)
-            self._tokens += 1
-            proposed = state.page_indices + new
-            self._pending[rid] = _Pending(self._tokens, state, proposed, new, advance)
-            publications.append(
-                PendingKVPublication(self, rid, self._tokens, state.version, proposed, advance)
-            )
-        self._free = self._free[cursor:]
-        return KVReservation(tuple(publications), cursor)
+        slots = self.slots(request_ids)
+        if not self._inflight.keys().isdisjoint(request_ids):
+            busy = next(r for r in request_ids if r in self._inflight)
+            raise SlotBusyError(f"request {busy!r} KV is already in flight")
+        if any(isinstance(a, bool) or not isinstance(a, int) or a < 1 for a in advances):
+            raise ValueError("KV sequence advances must be positive integers")
+        adv = np.asarray(advances, dtype=np.int64)
+        ps = self.page_size
+        need = (self.length[slots] + adv + ps - 1) // ps - self.page_count[slots]
+        np.maximum(need, 0, out=need)
+        end = np.cumsum(need)
+        available = self.free_pages
+        if end[-1] > available:
+            k = int(np.argmax(end > available))
+            left = available - int(end[k] - need[k])
+            raise KVAllocationError(f"Talker KV needs {int(need[k])} pages for {request_ids[k]!r}, only {left} remain")
+        taken = self._take_front(int(end[-1]))
+        lo = (end - need).tolist()
+        hi = end.tolist()
+        serial = self._serial
+        self._serial += rows
+        states, inflight = self._states, self._inflight
+        publications = tuple(
+            PendingKVPublication(self, rid, serial + i + 1, states[rid], taken, lo[i], hi[i], advances[i])
+            for i, rid in enumerate(request_ids)
+        )
+        inflight.update(zip(request_ids, publications))
+        return KVReservation(publications, int(end[-1]))
 
-    def _check_live(self, publication: PendingKVPublication) -> _Pending:
-        pending = self._pending.get(publication.request_id)
-        current = self._states.get(publication.request_id)
+    def _live(self, publication: PendingKVPublication) -> None:
+        """StaleKVPublicationError unless ``publication`` is its request's in-flight entry and the
+        request's committed state is still the one the reservation was made against."""
+
+        rid = publication.request_id
         if (
-            pending is None
-            or current is None
-            or pending.status != "pending"
-            or pending.token != publication.token
-            or pending.prior.version != publication.prior_version
-            or current != pending.prior
-            or pending.proposed_pages != publication.page_indices
+            self._inflight.get(rid) is not publication
+            or self._states.get(rid) is not publication._prior
+            or publication.prior_version != publication._prior.version
+            or publication.sequence_advance != publication._advance
+            or publication.sequence_advance < 1
         ):
-            raise StaleKVPublicationError("Talker KV publication is stale or no longer pending")
-        return pending
+            raise StaleKVPublicationError(_STALE)
 
-    def _finish(self, publication: PendingKVPublication, *, publish: bool) -> None:
-        pending = self._check_live(publication)
-        current = self._states[publication.request_id]
-        if publish:
-            self._states[publication.request_id] = RequestKVState(
-                request_id=publication.request_id,
-                page_indices=pending.proposed_pages,
-                sequence_length=current.sequence_length + pending.sequence_advance,
-                position_start=current.position_start + pending.sequence_advance,
-                version=current.version + 1,
-            )
-            pending.status = "published"
-        else:
-            self._return_pages(pending.new_pages)
-            pending.status = "discarded"
-        del self._pending[publication.request_id]
+    def _settle(self, publication: PendingKVPublication, *, commit: bool) -> None:
+        self._live(publication)
+        rid = publication.request_id
+        del self._inflight[rid]
+        if not commit:
+            self._give_back(publication.new_pages)
+            return
+        prior, advance = publication._prior, publication._advance
+        slot = self._slot_of[rid]
+        pages = publication.page_indices
+        self.length[slot] = prior.sequence_length + advance
+        self.position[slot] = prior.position_start + advance
+        self.page_count[slot] = len(pages)
+        self._states[rid] = RequestKVState(rid, pages, prior.sequence_length + advance, prior.position_start + advance,
+                                           prior.version + 1)
 
 
 __all__ = [

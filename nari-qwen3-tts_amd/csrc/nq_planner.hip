@@ -188,6 +188,100 @@ extern "C" int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start,
     return NQ_LAUNCH_STATUS();
 }
 
+namespace nq {
+namespace {
+
+constexpr int kMergeThreads = 256;
+
+// Number of elements of the sorted array v[0, n) that are smaller than x.
+__device__ __forceinline__ int count_below(const int32_t *v, int n, int32_t x) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (v[mid] < x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+// out = the sorted union of a[0, na) and b[0, nb) (both sorted, distinct): every element finds
+// its output position by one binary search in the other list.  A page present in both lists is
+// reported as NQ_ERR_INVALID_ARGUMENT (it would be handed out twice).
+__global__ void __launch_bounds__(kMergeThreads)
+free_list_merge_kernel(const int32_t *__restrict__ a, int na, const int32_t *__restrict__ b, int nb,
+                       int32_t *__restrict__ out, int32_t *__restrict__ status) {
+    const int i = blockIdx.x * kMergeThreads + threadIdx.x;
+    if (i < na) {
+        const int32_t v = a[i];
+        out[i + count_below(b, nb, v)] = v;
+    } else if (i < na + nb) {
+        const int j = i - na;
+        const int32_t v = b[j];
+        const int below = count_below(a, na, v);
+        if (below < na && a[below] == v) {
+            if (status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+            return;
+        }
+        out[j + below] = v;
+    }
+}
+
+// One decode step's report: the planner status (written by every planner launch), then the
+// free-list merge, attention and embedding status words (each read, then cleared for the next
+// step), the number of tokens outside [0, vocab), and per row whether the token is the
+// end-of-speech id.
+__global__ void __launch_bounds__(kMergeThreads)
+step_report_kernel(const int32_t *__restrict__ plan_status, int32_t *__restrict__ merge_status,
+                   int32_t *__restrict__ attention_status, int32_t *__restrict__ embed_status,
+                   const int64_t *__restrict__ tokens, int rows, int64_t eos_id, int64_t vocab,
+                   int32_t *__restrict__ report) {
+    __shared__ int s_bad;
+    if (threadIdx.x == 0) s_bad = 0;
+    __syncthreads();
+    int bad = 0;
+    for (int r = threadIdx.x; r < rows; r += kMergeThreads) {
+        const int64_t t = tokens[r];
+        bad += (t < 0 || t >= vocab) ? 1 : 0;
+        report[NQ_REPORT_HEAD + r] = t == eos_id ? 1 : 0;
+    }
+    if (bad) atomicAdd(&s_bad, bad);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t *cleared[3] = {merge_status, attention_status, embed_status};
+        report[0] = plan_status ? plan_status[0] : NQ_OK;
+        for (int i = 0; i < 3; ++i) {
+            report[1 + i] = cleared[i] ? cleared[i][0] : NQ_OK;
+            if (cleared[i]) cleared[i][0] = NQ_OK;
+        }
+        report[4] = s_bad;
+        for (int i = 5; i < NQ_REPORT_HEAD; ++i) report[i] = 0;
+    }
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" int nq_free_list_merge(const int32_t *free_pages, int n_free, const int32_t *returned, int n_returned,
+                                  int32_t *out, int32_t *status, void *stream) {
+    NQ_CHECK_ARG(n_free >= 0 && n_returned >= 0 && out);
+    NQ_CHECK_ARG((n_free == 0 || free_pages) && (n_returned == 0 || returned));
+    const int n = n_free + n_returned;
+    if (n == 0) return NQ_OK;
+    hipLaunchKernelGGL(nq::free_list_merge_kernel, dim3((n + nq::kMergeThreads - 1) / nq::kMergeThreads),
+                       dim3(nq::kMergeThreads), 0, static_cast<hipStream_t>(stream), free_pages, n_free, returned,
+                       n_returned, out, status);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_step_report(const int32_t *plan_status, int32_t *merge_status, int32_t *attention_status,
+                              int32_t *embed_status, const int64_t *tokens, int rows, int64_t eos_id, int64_t vocab,
+                              int32_t *report, void *stream) {
+    NQ_CHECK_ARG(tokens && report && rows >= 1 && vocab >= 1);
+    hipLaunchKernelGGL(nq::step_report_kernel, dim3(1), dim3(nq::kMergeThreads), 0,
+                       static_cast<hipStream_t>(stream), plan_status, merge_status, attention_status, embed_status,
+                       tokens, rows, eos_id, vocab, report);
+    return NQ_LAUNCH_STATUS();
+}
+
 extern "C" int nq_abi_version(void) { return NQ_ABI_VERSION; }
 
 extern "C" const char *nq_status_string(int status) {

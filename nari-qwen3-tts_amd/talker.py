@@ -45,6 +45,7 @@ from .layers import (
     silu_mul,
     quantize_fp8_weight_blocks,
 )
+from .errors import KVAllocationError
 from .sampling import sample_with_counter, sample_with_counter_from_planes, sample_with_uniforms
 
 
@@ -125,6 +126,57 @@ class TalkerWeights:
         return total
 
 
+def check_step_report(head) -> None:
+    """Fail closed on a decode step's report (the status words of ``nq_step_report``): map each
+    non-zero word to the reference's exception type (KVAllocationError for the planner running out
+    of pages, ValueError for inputs outside their tables, RuntimeError otherwise)."""
+
+    plan, merge, attention, embed, bad_tokens = (int(x) for x in head[:5])
+    if plan == _lib.NQ_ERR_CAPACITY:
+        raise KVAllocationError("the GPU planner ran out of free Talker KV pages")
+    if plan != _lib.NQ_OK:
+        raise RuntimeError(f"GPU planner status {plan} ({_lib.status_string(plan)})")
+    if merge != _lib.NQ_OK:
+        raise RuntimeError("a returned KV page was already on the device free list")
+    if attention != _lib.NQ_OK:
+        raise ValueError("paged attention met a page id outside the KV pool or an invalid K/V write slot")
+    if embed != _lib.NQ_OK:
+        raise ValueError("a text token id lies outside the embedding table")
+    if bad_tokens:
+        raise RuntimeError(f"{bad_tokens} sampled token ids lie outside the vocabulary")
+
+
+class StepReport:
+    """The device report of a decode step and pinned host copies of it: ``fetch`` queues one
+    device-to-host copy on the current stream, ``read`` waits for it, fails closed on the status
+    words and returns the per-row end-of-speech flags."""
+
+    def __init__(self, rows: int, device, depth: int = 4) -> None:
+        head = _lib.NQ_REPORT_HEAD
+        self.rows = rows
+        self.device = torch.zeros(head + rows, dtype=torch.int32, device=device)
+        self._host = [torch.zeros(head + rows, dtype=torch.int32, pin_memory=True) for _ in range(depth)]
+        self._events: list[torch.cuda.Event | None] = [None] * depth
+        self._next = 0
+
+    def fetch(self) -> int:
+        i = self._next
+        self._next = (i + 1) % len(self._host)
+        if self._events[i] is not None:
+            self._events[i].synchronize()
+        self._host[i].copy_(self.device, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._events[i] = ev
+        return i
+
+    def read(self, ticket: int):
+        self._events[ticket].synchronize()
+        words = self._host[ticket].numpy()
+        check_step_report(words[: _lib.NQ_REPORT_HEAD])
+        return words[_lib.NQ_REPORT_HEAD:].astype(bool)
+
+
 class TalkerDecodeStep:
     """Static buffers and the forward of one decode bucket (``rows`` physical rows)."""
 
@@ -178,6 +230,9 @@ class TalkerDecodeStep:
         # optional [layers + 1, rows, hidden] bf16 record of the residual stream: the step input, then
         # the residual after each layer (device-to-device copies, for layer-by-layer checks)
         self.trace: torch.Tensor | None = None
+        # fail-closed report: planner / free-list / attention / embedding status and per-row EOS flags
+        self.embed_status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.report = StepReport(rows, dev)
 
     def forward(self) -> torch.Tensor:
         c = self.w.config
@@ -185,7 +240,7 @@ class TalkerDecodeStep:
         n = self.rows
         # materialize_decode (executor/talker.py:256-262) and the first input norm, one launch
         embed_add_rmsnorm(self.text_ids, self.w.text_embedding, self.step_embed, self.w.layers[0].input_norm,
-                          c.rms_eps, self.residual, self.hidden)
+                          c.rms_eps, self.residual, self.hidden, status=self.embed_status)
         trace = self.trace
         if trace is not None:
             trace[0].copy_(self.residual)
@@ -233,6 +288,22 @@ class TalkerDecodeStep:
             if trace is not None:
                 trace[index + 1].copy_(self.residual)
         ctx.advance_sequence_lengths()
+        self._sample()
+        self._report()
+        return self.tokens
+
+    def _report(self) -> None:
+        ctx, c = self.context, self.w.config
+        buffers = getattr(ctx, "buffers", None)
+        _lib.call("nq_step_report", _lib.ptr(None if buffers is None else buffers.status),
+                  _lib.ptr(getattr(ctx, "free_list_status", None)), _lib.ptr(getattr(ctx, "attention_status", None)),
+                  self.embed_status.data_ptr(), self.tokens.data_ptr(), self.rows, c.eos_id, c.vocab,
+                  self.report.device.data_ptr(), _lib.stream(self.device))
+
+    def _sample(self) -> None:
+        c = self.w.config
+        n = self.rows
+        ws = self.linear_workspace
         options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
                        eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
         if self.use_hip_linear and self.use_counter_rng:
@@ -242,7 +313,7 @@ class TalkerDecodeStep:
             planes = ws[: splits * n * c.vocab * 4].view(torch.float32).view(splits, n, c.vocab)
             sample_with_counter_from_planes(planes, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
                                             logits_out=self.logits, **options)
-            return self.tokens
+            return
         if self.use_hip_linear:
             linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
         else:
@@ -253,7 +324,6 @@ class TalkerDecodeStep:
                                 **options)
         else:
             sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
-        return self.tokens
 
 
-__all__ = ["TalkerConfig", "TalkerDecodeStep", "TalkerWeights"]
+__all__ = ["StepReport", "TalkerConfig", "TalkerDecodeStep", "TalkerWeights", "check_step_report"]

@@ -26,6 +26,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -116,6 +117,7 @@ class _HipBindingBase:
         # decode bindings take the fused bins kernel in attend_partials while the library accepts the shape
         self.fused_decode = True
         self._side: torch.cuda.Stream | None = None
+        self.free_list_status: torch.Tensor | None = None
 
     # -- planning ---------------------------------------------------------
     def _stage(self, metadata: TalkerAttentionMetadata) -> None:
@@ -290,35 +292,40 @@ class HipDecodeBinding(_HipBindingBase):
     prefill = False
 
 
-class _Staging:
-    """Ring of pinned host rows -> device rows for the planner's inputs."""
+class _PinnedRing:
+    """Pinned host buffers for small host-to-device copies on the current stream: a buffer is
+    reused only after the copy that read it has finished."""
 
-    FIELDS = 5  # seq_len, pos_start, advance, prior_pages, table_row
-
-    def __init__(self, rows: int, device, depth: int = 4) -> None:
-        self.rows = rows
-        self.host = [torch.zeros((self.FIELDS, rows), dtype=torch.int32, pin_memory=True) for _ in range(depth)]
-        self.dev = [torch.zeros((self.FIELDS, rows), dtype=torch.int32, device=device) for _ in range(depth)]
-        self.events = [None] * depth
+    def __init__(self, shape: tuple[int, ...], device, depth: int = 4) -> None:
+        self.host = [torch.zeros(shape, dtype=torch.int32, pin_memory=True) for _ in range(depth)]
+        self.view = [h.numpy() for h in self.host]
+        self.events: list[torch.cuda.Event | None] = [None] * depth
         self.next = 0
 
-    def stage(self, values: list[list[int]]):
+    def acquire(self) -> tuple[int, np.ndarray]:
         i = self.next
         self.next = (i + 1) % len(self.host)
         if self.events[i] is not None:
             self.events[i].synchronize()
-        host = self.host[i]
-        n = len(values[0])
-        host[:, :n] = torch.tensor(values, dtype=torch.int32)
-        self.dev[i][:, :n].copy_(host[:, :n], non_blocking=True)
+        return i, self.view[i]
+
+    def send(self, i: int, dst: torch.Tensor, count: int) -> None:
+        """Copy the first ``count`` elements (along dim -1) of buffer i to ``dst``."""
+
+        dst[..., :count].copy_(self.host[i][..., :count], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
         self.events[i] = ev
-        return self.dev[i]
 
 
 class PagedTalkerKV:
-    """Request state, device page tables and one HIP binding per captured slot."""
+    """Request ledger, device page table, device free list and one HIP binding per captured slot.
+
+    The device free list is a sorted int32 array with a consumed front, double-buffered: pages
+    taken by a reservation move the front (the planner kernel reads new pages from it), returned
+    pages are merged in on the GPU (``nq_free_list_merge``) before the next planner launch, by
+    replaying the ledger's ordered log of free-list changes.  The list is uploaded whole only at
+    construction and after ``adopt_request`` (setup)."""
 
     def __init__(
         self,
@@ -361,34 +368,74 @@ class PagedTalkerKV:
         self._binding_factory = binding_factory
         self._next_capture = 0
         self._capture_requests: dict[int, tuple[str, ...]] = {}
-        # Device page table: one row of page ids per live request.
-        self._max_pages_per_request = total_pages
-        self._table = torch.zeros((64, self._max_pages_per_request), dtype=torch.int32, device=device)
-        self._table_row: dict[str, int] = {}
-        self._free_rows: list[int] = list(range(63, -1, -1))
-        # Device copy of the sorted free list and how much of its front is consumed.
-        self._free_dev = torch.zeros(max(total_pages, 1), dtype=torch.int32, device=device)
-        self._free_host = torch.zeros(max(total_pages, 1), dtype=torch.int32, pin_memory=True)
-        self._free_upload_event: torch.cuda.Event | None = None
-        self._free_epoch = -1
-        self._free_count = 0
-        self._free_head = 0
-        self._staging: _Staging | None = None
+        # device page table: row = ledger slot, up to total_pages page ids per request
+        self._table = torch.zeros((self.allocator.slot_capacity, total_pages), dtype=torch.int32, device=device)
+        # device free list (two buffers: a merge writes the other one), its front and length
+        self._free_dev = [torch.zeros(max(total_pages, 1), dtype=torch.int32, device=device) for _ in range(2)]
+        self._returned_dev = torch.zeros(max(total_pages, 1), dtype=torch.int32, device=device)
+        self._free_cur = 0
+        self._free_front = 0
+        self._free_len = 0
+        # device status word of the free-list merges (read and cleared by the step report)
+        self.free_list_status = torch.zeros(1, dtype=torch.int32, device=device)
+        self._pages_ring = _PinnedRing((max(total_pages, 1),), device)
+        self._rows_ring: _PinnedRing | None = None
+        self.allocator.resend_free_list = True
+
+    # -- the device free list ---------------------------------------------------
+    def _sync_free_list(self) -> None:
+        """Bring the device free list to the ledger's: replay its log of takes and returns."""
+
+        a = self.allocator
+        stream = _lib.stream(self.device)
+        if a.resend_free_list:
+            a.resend_free_list = False
+            a.drain_log()
+            free = a.free_array()
+            i, buf = self._pages_ring.acquire()
+            buf[: free.shape[0]] = free
+            self._free_cur = 0
+            self._pages_ring.send(i, self._free_dev[0], free.shape[0])
+            self._free_front, self._free_len = 0, int(free.shape[0])
+            return
+        returned: list[np.ndarray] = []
+        for kind, value in a.drain_log() + [("take", 0)]:
+            if kind == "return":
+                returned.append(value)
+                continue
+            if returned:  # a run of returns: one merge
+                pages = returned[0] if len(returned) == 1 else np.sort(np.concatenate(returned))
+                returned = []
+                i, buf = self._pages_ring.acquire()
+                m = int(pages.shape[0])
+                buf[:m] = pages
+                self._pages_ring.send(i, self._returned_dev, m)
+                src = self._free_dev[self._free_cur]
+                dst = self._free_dev[1 - self._free_cur]
+                live = self._free_len - self._free_front
+                _lib.call("nq_free_list_merge", src.data_ptr() + 4 * self._free_front, live,
+                          self._returned_dev.data_ptr(), m, dst.data_ptr(), self.free_list_status.data_ptr(), stream)
+                self._free_cur = 1 - self._free_cur
+                self._free_front, self._free_len = 0, live + m
+            self._free_front += value
+
+    def device_free_list(self) -> torch.Tensor:
+        """The device copy of the sorted free list (after replaying pending changes)."""
+
+        self._sync_free_list()
+        return self._free_dev[self._free_cur][self._free_front: self._free_len]
 
     # -- request lifecycle ----------------------------------------------------
     def add_request(self, request_id: str) -> None:
         self.allocator.add_request(request_id)
-        if not self._free_rows:
-            old = self._table
-            grown = torch.zeros((old.shape[0] * 2, old.shape[1]), dtype=torch.int32, device=self.device)
-            grown[: old.shape[0]].copy_(old)
+        rows = self.allocator.slot_capacity
+        if rows > self._table.shape[0]:
+            grown = torch.zeros((rows, self._table.shape[1]), dtype=torch.int32, device=self.device)
+            grown[: self._table.shape[0]].copy_(self._table)
             self._table = grown
-            self._free_rows = list(range(grown.shape[0] - 1, old.shape[0] - 1, -1))
-        self._table_row[request_id] = self._free_rows.pop()
 
     def remove_request(self, request_id: str) -> None:
         self.allocator.remove_request(request_id)
-        self._free_rows.append(self._table_row.pop(request_id))
 
     def state(self, request_id: str) -> RequestKVState:
         return self.allocator.state(request_id)
@@ -400,9 +447,8 @@ class PagedTalkerKV:
         self.allocator.adopt(
             request_id, pages, sequence_length, sequence_length if position_start is None else position_start
         )
-        row = self._table_row[request_id]
         if pages:
-            self._table[row, : len(pages)].copy_(torch.tensor(pages, dtype=torch.int32))
+            self._table[self.allocator.slot(request_id), : len(pages)].copy_(torch.tensor(pages, dtype=torch.int32))
 
     # -- bindings -----------------------------------------------------------
     def _binding(self, key, slot: int):
@@ -422,7 +468,11 @@ class PagedTalkerKV:
         )
         if self._binding_factory is not None:
             arguments.update(slot=slot, metadata=None)
-        return factory(**arguments)
+        binding = factory(**arguments)
+        if isinstance(binding, _HipBindingBase):
+            # the step report reads the free-list merge status next to the binding's own words
+            binding.free_list_status = self.free_list_status
+        return binding
 
     def create_prefill(self, key, *, slot: int):
         return self._binding(key, slot)
@@ -443,23 +493,6 @@ class PagedTalkerKV:
         if token_capacity > len(self._scratch_pages) * self.page_size:
             raise ValueError("Talker token capacity exceeds executor-private scratch slots")
 
-    def _sync_free_list(self) -> None:
-        if self.allocator.free_list_epoch == self._free_epoch:
-            return
-        free = self.allocator.free_list()
-        if self._free_upload_event is not None:
-            self._free_upload_event.synchronize()
-        n = len(free)
-        if n:
-            self._free_host[:n] = torch.tensor(free, dtype=torch.int32)
-            self._free_dev[:n].copy_(self._free_host[:n], non_blocking=True)
-            ev = torch.cuda.Event()
-            ev.record()
-            self._free_upload_event = ev
-        self._free_epoch = self.allocator.free_list_epoch
-        self._free_count = n
-        self._free_head = 0
-
     def _metadata(
         self,
         *,
@@ -472,15 +505,27 @@ class PagedTalkerKV:
         reuse_attention_plan: bool = True,
     ) -> tuple[tuple[PendingKVPublication, ...], TalkerAttentionMetadata]:
         self._validate_scratch_capacity(capture_rows=capture_rows, token_capacity=token_capacity)
-        if len(request_ids) > capture_rows:
+        n = len(request_ids)
+        if n > capture_rows:
             raise ValueError("Talker request rows do not fit the capture")
-        if sum(advances) + (0 if prefill else capture_rows - len(request_ids)) > token_capacity:
+        if sum(advances) + (0 if prefill else capture_rows - n) > token_capacity:
             raise ValueError("Talker KV metadata exceeds the captured token capacity")
         self._sync_free_list()
-        priors = [self.state(rid) for rid in request_ids]
-        reservation = self.allocator.reserve(request_ids, advances)
+        a = self.allocator
+        slots = a.slots(request_ids)
+        if self._rows_ring is None or self._rows_ring.view[0].shape[1] < capture_rows:
+            self._rows_ring = _PinnedRing((5, max(capture_rows, 64)), self.device)
+            self._rows_dev = torch.zeros((5, max(capture_rows, 64)), dtype=torch.int32, device=self.device)
+        # the rows' committed numbers, read before the reservation (it does not change them)
+        i, rows = self._rows_ring.acquire()
+        rows[0, :n] = a.length[slots]
+        rows[1, :n] = a.position[slots]
+        rows[3, :n] = a.page_count[slots]
+        rows[4, :n] = slots
+        reservation = a.reserve(request_ids, advances)
         publications = reservation.publications
         try:
+            rows[2, :n] = advances
             if isinstance(context, _HipBindingBase):
                 buffers = context.buffers
             else:
@@ -491,32 +536,24 @@ class PagedTalkerKV:
                     prefill=prefill,
                     device=self.device,
                 )
-            if self._staging is None or self._staging.rows < capture_rows:
-                self._staging = _Staging(max(capture_rows, 64), self.device)
-            rows = self._staging.stage(
-                [
-                    [p.sequence_length for p in priors],
-                    [p.position_start for p in priors],
-                    list(advances),
-                    [len(p.page_indices) for p in priors],
-                    [self._table_row[rid] for rid in request_ids],
-                ]
-            )
-            free_view = self._free_dev[self._free_head :]
+            staged = self._rows_dev
+            self._rows_ring.send(i, staged, staged.shape[1])  # the whole (small, contiguous) block
+            free = self._free_dev[self._free_cur]
+            # the planner takes this reservation's pages from the current front; the ledger logged
+            # the take, and the next sync moves the device front past them
             _lib.call(
                 "nq_plan_ragged",
-                rows[0].data_ptr(), rows[1].data_ptr(), rows[2].data_ptr(), rows[3].data_ptr(),
-                rows[4].data_ptr(), len(request_ids), capture_rows, token_capacity, self.page_size,
+                staged[0].data_ptr(), staged[1].data_ptr(), staged[2].data_ptr(), staged[3].data_ptr(),
+                staged[4].data_ptr(), n, capture_rows, token_capacity, self.page_size,
                 int(prefill), self._table.data_ptr(), self._table.stride(0),
-                free_view.data_ptr(), self._free_count - self._free_head,
+                free.data_ptr() + 4 * self._free_front, self._free_len - self._free_front,
                 self._scratch_dev.data_ptr(), len(self._scratch_pages),
                 _lib.ptr(buffers.qo_indptr), buffers.kv_indptr.data_ptr(), buffers.kv_indices.data_ptr(),
                 buffers.kv_indices.numel(), buffers.last_page_len.data_ptr(),
                 buffers.position_ids.data_ptr(), buffers.write_pages.data_ptr(),
                 buffers.write_offsets.data_ptr(), buffers.status.data_ptr(), 0, _lib.stream(self.device),
             )
-            self._free_head += reservation.pages_taken
-            total_pages = sum(len(p.page_indices) for p in publications) + (capture_rows - len(request_ids))
+            total_pages = int(a.page_count[slots].sum()) + reservation.pages_taken + (capture_rows - n)
             metadata = TalkerAttentionMetadata(
                 qo_indptr=buffers.qo_indptr,
                 paged_kv_indptr=buffers.kv_indptr,

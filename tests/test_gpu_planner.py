@@ -140,7 +140,7 @@ def test_decode_metadata_matches_oracle(nq, device, label, seed, rows, capture, 
     taken = sum(len(p.page_indices) - len(s.page_indices) for p, s in zip(pubs, priors))
     assert int(_np(ctx.buffers.status)[1]) == taken
     for rid, pub in zip(rids, pubs):
-        row = kv._table_row[rid]
+        row = kv.allocator.slot(rid)
         np.testing.assert_array_equal(_np(kv._table[row, : len(pub.page_indices)]), np.asarray(pub.page_indices))
     kv.abort(pubs)
 
@@ -206,3 +206,6 @@ def test_multi_step_lifecycle_tracks_oracle_allocator(nq, device):
             kv.remove_request(gone)
             oracle.remove(gone)
         assert list(kv.allocator.free_list()) == oracle.free
+        # the device copy, kept by front moves and GPU merges only, equals the ledger's list
+        assert kv.device_free_list().cpu().tolist() == oracle.free
+        assert int(kv.free_list_status.item()) == 0

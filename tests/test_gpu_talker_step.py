@@ -69,8 +69,8 @@ def test_captured_b64_talker_step_matches_oracle(nq, device):
         pubs = kv.prepare_decode(ctx, key, rids)
         seen0 = step.seen.clone()
         call.replay()
-        torch.cuda.synchronize()
-        assert int(ctx.attention_status.item()) == 0
+        eos = step.report.read(step.report.fetch())  # fails closed on any status word
+        np.testing.assert_array_equal(eos, step.tokens.cpu().numpy() == cfg.eos_id)
         m = ctx.metadata
         wp, wo = m.write_pages.long(), m.write_offsets.long()
         out_a = [step.logits.clone(), step.tokens.clone(), step.seen.clone(), kv.storage[:, wp, :, wo].clone()]

@@ -79,7 +79,9 @@ def test_capacity_recycles_across_more_requests_than_pages(nq):
         assert a.free_pages == lit["total_pages"]
 
 
-def test_lowest_pages_in_row_order_and_epoch_tracking(nq):
+def test_lowest_pages_in_row_order_and_free_list_log(nq):
+    """Reservations take the lowest free pages in row order; every change of the free list is logged
+    in order (takes, sorted returns) for the device copy to replay."""
     from nari_qwen3_tts_amd.cache import PagedKVAllocator
 
     a = PagedKVAllocator(total_pages=20, page_size=2)
@@ -87,16 +89,62 @@ def test_lowest_pages_in_row_order_and_epoch_tracking(nq):
     assert scratch == (0, 1, 2)
     for r in "abc":
         a.add_request(r)
+    a.drain_log()
     res = a.reserve(("a", "b", "c"), (3, 1, 4))
     assert [p.page_indices for p in res.publications] == [(3, 4), (5,), (6, 7)]
     assert res.pages_taken == 5
-    epoch = a.free_list_epoch
     for p in res.publications:
         p.publish()
-    assert a.free_list_epoch == epoch  # publishing returns nothing
+    assert a.drain_log() == [("take", 5)]  # publishing returns nothing
     a.remove_request("b")
-    assert a.free_list_epoch == epoch + 1
+    res = a.reserve(("c",), (2,))
+    res.publications[0].discard()
+    log = a.drain_log()
+    assert [k for k, _ in log] == ["return", "take", "return"]
+    assert log[0][1].tolist() == [5] and log[1][1] == 1 and log[2][1].tolist() == [5]
     assert a.free_list()[0] == 5
+    # the slots of removed requests are reused lowest first
+    assert a.slot("a") == 0 and a.slot("c") == 2
+    a.add_request("d")
+    assert a.slot("d") == 1
+
+
+def test_free_list_log_replayed_on_a_copy_equals_the_ledger(nq):
+    """Replaying the log (front moves, sorted merges) on a second array reproduces the ledger's
+    free list exactly, over random reserve / publish / discard / remove traffic."""
+    import numpy as np
+
+    from nari_qwen3_tts_amd.cache import PagedKVAllocator
+
+    rng = np.random.default_rng(3)
+    a = PagedKVAllocator(total_pages=300, page_size=4)
+    a.claim_scratch_pages(4)
+    copy, front = np.asarray(a.free_list(), dtype=np.int32), 0
+    a.drain_log()
+    live = []
+    for step in range(200):
+        if len(live) < 12 and rng.random() < 0.5:
+            rid = f"r{step}"
+            a.add_request(rid)
+            live.append(rid)
+        if live:
+            rows = tuple(rng.choice(live, size=min(len(live), int(rng.integers(1, 6))), replace=False).tolist())
+            try:
+                pubs = a.reserve(rows, tuple(int(x) for x in rng.integers(1, 9, size=len(rows)))).publications
+            except Exception:  # noqa: BLE001 - pool exhausted: nothing taken
+                pubs = ()
+            for p in pubs:
+                (p.publish if rng.random() < 0.7 else p.discard)()
+            if rng.random() < 0.2:
+                a.remove_request(live.pop(int(rng.integers(len(live)))))
+        for kind, value in a.drain_log():
+            if kind == "take":
+                front += value
+            else:
+                rest = copy[front:]
+                copy = np.sort(np.concatenate([rest, value]))  # a different formulation of the merge
+                front = 0
+        assert copy[front:].tolist() == list(a.free_list())
 
 
 def test_adopt_installs_scattered_pages(nq):
