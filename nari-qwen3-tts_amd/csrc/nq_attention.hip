@@ -604,10 +604,17 @@ struct SoftmaxState {
     __device__ __forceinline__ void consume(const uint4 (&kr)[Lanes<D, G>::NL],
                                             const uint4 (&vr)[Lanes<D, G>::NL],
                                             const bool (&valid)[Lanes<D, G>::NL]) {
+        float s[Lanes<D, G>::NL][G];
+        scores(kr, valid, s);
+        accumulate(vr, s);
+    }
+
+    // The block's scaled scores (log2 domain), -inf for masked tokens.
+    __device__ __forceinline__ void scores(const uint4 (&kr)[Lanes<D, G>::NL],
+                                           const bool (&valid)[Lanes<D, G>::NL],
+                                           float (&s)[Lanes<D, G>::NL][G]) const {
         constexpr int NL = Lanes<D, G>::NL;
         constexpr int LPT = Lanes<D, G>::LPT;
-        static_assert(NL % 2 == 0, "tokens are paired for P.V");
-        float s[NL][G];
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
 #pragma unroll
@@ -620,44 +627,48 @@ struct SoftmaxState {
                 s[i][j] = valid[i] ? part : -INFINITY;
             }
         }
-        // V words of token pairs (2u, 2u+1) interleaved: (v_a[e], v_b[e]).
-        uint32_t vlo[NL / 2][4], vhi[NL / 2][4];
-#pragma unroll
-        for (int u = 0; u < NL / 2; ++u) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint32_t a = word(vr[2 * u], w), b = word(vr[2 * u + 1], w);
-                vlo[u][w] = __builtin_amdgcn_perm(b, a, 0x05040100u);
-                vhi[u][w] = __builtin_amdgcn_perm(b, a, 0x07060302u);
-            }
-        }
+    }
+
+    // Online-softmax update with the block's scores and its V rows.
+    __device__ __forceinline__ void accumulate(const uint4 (&vr)[Lanes<D, G>::NL],
+                                               const float (&s)[Lanes<D, G>::NL][G]) {
+        constexpr int NL = Lanes<D, G>::NL;
+        static_assert(NL % 2 == 0, "tokens are paired for P.V");
+        // softmax of each query head first: P packed as bf16 token pairs, the old sums rescaled
+        uint32_t pp[G][NL / 2];
 #pragma unroll
         for (int j = 0; j < G; ++j) {
             float mb = s[0][j];
 #pragma unroll
             for (int i = 1; i < NL; ++i) mb = fmaxf(mb, s[i][j]);
             const float mn = fmaxf(m[j], mb);
-            if (mn == -INFINITY) continue;
-            const float alpha = exp2f(m[j] - mn);
-            m[j] = mn;
+            const bool live = mn != -INFINITY;  // else nothing seen yet: P = 0, state unchanged
+            const float alpha = live ? exp2f(m[j] - mn) : 1.f;
+            m[j] = live ? mn : m[j];
             float lsum = 0.f;
-            uint32_t pp[NL / 2];
 #pragma unroll
             for (int u = 0; u < NL / 2; ++u) {
-                pp[u] = pack_bf16x2(exp2f(s[2 * u][j] - mn), exp2f(s[2 * u + 1][j] - mn));
-                lsum += __uint_as_float(pp[u] << 16) + __uint_as_float(pp[u] & 0xffff0000u);
+                pp[j][u] = live ? pack_bf16x2(exp2f(s[2 * u][j] - mn), exp2f(s[2 * u + 1][j] - mn)) : 0u;
+                lsum += __uint_as_float(pp[j][u] << 16) + __uint_as_float(pp[j][u] & 0xffff0000u);
             }
             l[j] = l[j] * alpha + lsum;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                float a0 = acc[j][2 * w] * alpha, a1 = acc[j][2 * w + 1] * alpha;
+            for (int e = 0; e < 8; ++e) acc[j][e] *= alpha;
+        }
+        // then P.V over V words of token pairs (2u, 2u+1) interleaved as (v_a[e], v_b[e]), each
+        // pair built just before its use so only one is live at a time
 #pragma unroll
-                for (int u = 0; u < NL / 2; ++u) {
-                    a0 = dot2_bf16(pp[u], vlo[u][w], a0);
-                    a1 = dot2_bf16(pp[u], vhi[u][w], a1);
+        for (int w = 0; w < 4; ++w) {
+#pragma unroll
+            for (int u = 0; u < NL / 2; ++u) {
+                const uint32_t a = word(vr[2 * u], w), b = word(vr[2 * u + 1], w);
+                const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
+#pragma unroll
+                for (int j = 0; j < G; ++j) {
+                    acc[j][2 * w] = dot2_bf16(pp[j][u], lo, acc[j][2 * w]);
+                    acc[j][2 * w + 1] = dot2_bf16(pp[j][u], hi, acc[j][2 * w + 1]);
                 }
-                acc[j][2 * w] = a0;
-                acc[j][2 * w + 1] = a1;
             }
         }
     }
@@ -732,6 +743,59 @@ __device__ __forceinline__ void stream_issue(const int4 &dsc, int h, const uint1
         vr[i] = *reinterpret_cast<const uint4 *>(head_base + off + c_kind);
     }
 }
+
+// stream_issue in two halves, so the K and V loads of a block can be issued at different times.
+// BlockRef holds what the loads of one block need: for page sizes >= 16 a block lies in one page
+// and the wave's tokens i*TPL + g sit at a fixed slot stride from one base offset (every slot of
+// the page is a valid address, tokens past the block's count are masked); smaller pages keep one
+// offset per token.
+template <int D, int G, bool kSmallPages>
+struct BlockRef {
+    static constexpr int NL = Lanes<D, G>::NL;
+    static constexpr int TPL = Lanes<D, G>::TPL;
+    int64_t off[kSmallPages ? NL : 1];
+    unsigned valid;  // bit i: token i*TPL + g is a real key
+
+    __device__ __forceinline__ void make(const int4 &dsc, int64_t c_page, int64_t c_slot, int num_pages, int ps_log2,
+                                         const int32_t *__restrict__ kv_indices, int index_limit, int g, bool *bad) {
+        const int ntok = static_cast<int>(static_cast<unsigned>(dsc.y) >> 24);
+        const int slot0 = dsc.y & 0xffffff;
+        valid = 0;
+        if constexpr (kSmallPages) {
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                const int t = i * TPL + g;
+                const int at = dsc.x + (t >> ps_log2);
+                const int page = (t < ntok && at < index_limit) ? kv_indices[at] : 0;
+                const bool page_ok = static_cast<unsigned>(page) < static_cast<unsigned>(num_pages);
+                if (t < ntok && !page_ok) *bad = true;
+                const bool ok = t < ntok && page_ok;
+                valid |= ok ? 1u << i : 0u;
+                off[i] = static_cast<int64_t>(page_ok ? page : 0) * c_page +
+                         static_cast<int64_t>(ok ? (t & ((1 << ps_log2) - 1)) : 0) * c_slot;
+            }
+        } else {
+            const bool page_ok = static_cast<unsigned>(dsc.x) < static_cast<unsigned>(num_pages);
+#pragma unroll
+            for (int i = 0; i < NL; ++i) valid |= (i * TPL + g < ntok && page_ok) ? 1u << i : 0u;
+            if (ntok > 0 && !page_ok) *bad = true;
+            off[0] = static_cast<int64_t>(page_ok ? dsc.x : 0) * c_page + static_cast<int64_t>(slot0 + g) * c_slot;
+        }
+    }
+
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ base, int64_t c_slot, uint4 (&r)[NL]) const {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int64_t o = kSmallPages ? off[kSmallPages ? i : 0] : off[0] + static_cast<int64_t>(i * TPL) * c_slot;
+            r[i] = *reinterpret_cast<const uint4 *>(base + o);
+        }
+    }
+
+    __device__ __forceinline__ void flags(bool (&ok)[NL]) const {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) ok[i] = (valid >> i) & 1u;
+    }
+};
 
 __device__ __forceinline__ int4 shfl_int4(const int4 &v, int src) {
     return make_int4(__shfl(v.x, src, kWave), __shfl(v.y, src, kWave), __shfl(v.z, src, kWave),
@@ -1180,6 +1244,10 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     int4 dwin = make_int4(-1, 0, 0, 0);
     if (s0 + lane < s1) dwin = blocks[global_block(s0 + lane)];
 
+    const int g = lane / LN::LPT;
+    const int sub = lane % LN::LPT;
+    const uint16_t *head_base = cache + h * c_head + sub * 8;
+
     // 1. q/k norm + RoPE + K/V write for the bin's rows (one wave per head unit);
     // the norm weights are in registers before the first unit's planes arrive
     float qw1 = 0.f, qw2 = 0.f, kw1 = 0.f, kw2 = 0.f;
@@ -1252,11 +1320,26 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
             cslot[lane + HALF] = o2;
         }
     }
+    // the span's first block goes in flight as soon as the wave's RoPE units are done (at once for
+    // the waves without any), under the other waves' RoPE work and the barrier, unless it is the
+    // block that receives a row's new K/V (written by this workgroup before the barrier)
+    uint4 kc[LN::NL], vc[LN::NL];
+    BlockRef<D, G, kSmallPages> ref;
+    bool issued = false;
+    if (s0 < s1) {
+        int sl0 = 0;
+        while (sl0 + 1 < nslots && s_start[sl0 + 1] <= s0) ++sl0;
+        const bool write_block = s_rope[sl0].w < 0 && s0 == s_start[sl0 + 1] - 1;
+        if (!write_block) {
+            ref.make(shfl_int4(dwin, 0), c_page, c_slot, num_pages, ps_log2, kv_indices, index_limit, g, &bad);
+            ref.load(head_base, c_slot, kc);
+            ref.load(head_base + c_kind, c_slot, vc);
+            issued = true;
+        }
+    }
     __syncthreads();  // rotated q in LDS, the new K/V in the cache for every wave of the workgroup
 
     // 2. stream the wave's span of the bin's blocks
-    const int g = lane / LN::LPT;
-    const int sub = lane % LN::LPT;
     if (s0 < s1) {
         // further descriptors of the span, 64 at a time
         auto desc_of = [&](int w) {
@@ -1303,8 +1386,6 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
                 }
             }
         };
-        uint4 kc[LN::NL], vc[LN::NL];
-        bool okc[LN::NL];
         for (int w = s0; w < s1; ++w) {
             if (w == s_start[cur + 1]) {
                 flush(cur);
@@ -1312,10 +1393,14 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
                 st.reset();
                 st.load_q(s_q + cur * G * D, D, 0, sub, scale_log2);
             }
-            const int4 dc = desc_of(w);
-            stream_issue<D, G, kSmallPages>(dc, h, cache, c_page, c_kind, c_slot, c_head, num_pages, ps_log2,
-                                            kv_indices, index_limit, g, sub, kc, vc, okc, &bad);
-            st.consume(kc, vc, okc);
+            if (w != s0 || !issued) {
+                ref.make(desc_of(w), c_page, c_slot, num_pages, ps_log2, kv_indices, index_limit, g, &bad);
+                ref.load(head_base, c_slot, kc);
+                ref.load(head_base + c_kind, c_slot, vc);
+            }
+            bool ok[LN::NL];
+            ref.flags(ok);
+            st.consume(kc, vc, ok);
         }
         flush(cur);
     }
