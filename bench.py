@@ -722,7 +722,60 @@ def mixed_attention(args, torch, np) -> dict:
     return result
 
 
-WORKLOADS = {"talker-decode": talker_decode, "code-predictor": code_predictor, "codec": codec_step,
+def kv_read_ceiling(args, torch, np) -> dict:
+    """The read ceiling of the decode attention's access pattern: the K/V pages of the batch-64 decode
+    workload (64 rows, KV U[64, 2048], permuted 32768-page pool) read whole by nq_kv_read_probe, one
+    launch per layer over 28 distinct layers (no reuse from the Infinity Cache), no arithmetic."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd import _lib
+
+    dev = torch.device("cuda:0")
+    layers, page_bytes = 28, 2 * PAGE_SIZE * 8 * 128 * 2
+    storage = torch.empty((layers, POOL_PAGES, page_bytes // 2), dtype=torch.int16, device=dev)
+    for layer in range(layers):
+        storage[layer].random_()
+    rng = np.random.default_rng(SEED)
+    lengths = rng.integers(KV_LO, KV_HI + 1, size=ROWS)
+    need = int(sum(-(-int(n) // PAGE_SIZE) for n in lengths))
+    pages = torch.from_numpy(rng.permutation(POOL_PAGES)[:need].astype(np.int32)).to(dev)
+    out = torch.zeros(1024, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream()
+
+    def launches():
+        for layer in range(layers):
+            _lib.check(lib.nq_kv_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(), need,
+                                             1024, out.data_ptr(), stream.cuda_stream), "nq_kv_read_probe")
+
+    launches()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        launches()
+    end.record(stream)
+    end.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (args.steps * layers)
+    nbytes = need * page_bytes
+    gbs = nbytes / us / 1e3
+    log(f"KV page read ceiling: {need} pages = {nbytes / 1e6:.1f} MB per layer in {us:.1f} us -> {gbs:.0f} GB/s")
+    return {
+        "metric": "KV page read ceiling GB/s (decode attention access pattern, no arithmetic)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 1,
+        "ms_per_step": round(us * layers / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random pages)",
+        "config": {"workload": "K/V pages of 64 rows, KV U[64,2048], page size 16, 32768-page permuted pool, "
+                               "28 distinct layers", "global_batch": ROWS, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "nq_kv_read_probe",
+                     "bytes_per_launch": nbytes, "us_per_launch": round(us, 2)},
+    }
+
+
+WORKLOADS = {"talker-decode": talker_decode, "kv-read-ceiling": kv_read_ceiling, "code-predictor": code_predictor, "codec": codec_step,
              "mixed": mixed_attention}
 
 

@@ -181,6 +181,17 @@ int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_t *kv_indpt
                                void *stream);
 
 /*
+ * Read-bandwidth yardstick (no reference counterpart; benchmark calibration):
+ * reads pages[0 .. n_pages) of a paged buffer whole (page_bytes each, a
+ * multiple of 64 KiB; ids outside [0, num_pages) are skipped) with 128-bit
+ * loads like the decode attention's stream and no
+ * arithmetic, so its time bounds what the attention can reach on the same
+ * pages.  out: >= grid uint32 words (written only for an impossible value).
+ */
+int nq_kv_read_probe(const void *base, int num_pages, int64_t page_bytes, const int32_t *pages, int n_pages,
+                     int grid, uint32_t *out, void *stream);
+
+/*
  * Code-predictor short-cache attention: one query per row over the first
  * valid_length positions of a dense per-row cache.
  * Replaces decode_attn_nhd_short_cache (model/kernels.py:408-520).

@@ -2177,3 +2177,44 @@ extern "C" int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_
                               page_size, num_qo_heads, num_kv_heads, head_dim, sm_scale, out, o_s0, o_s1,
                               max_query_tokens, max_pages, parts, ws, NQ_NOALLOC_SCRATCH_BYTES, status, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Read-bandwidth yardstick for the decode attention's access pattern: every
+// page of `pages` read whole (page_bytes, a multiple of 4 KiB) and folded into
+// one xor per thread, nothing else; ids outside [0, num_pages) are skipped.  One workgroup of 256 threads per page at
+// a time, 16 x 128-bit loads per thread in flight.  `out` (>= grid words) is
+// written only for an impossible xor value, so the loads stay live.
+
+namespace nq {
+namespace {
+
+__global__ void __launch_bounds__(256)
+kv_read_probe_kernel(const uint4 *__restrict__ base, int num_pages, const int32_t *__restrict__ pages, int n_pages,
+                     int64_t page_vec, uint32_t *__restrict__ out) {
+    uint32_t acc = 0;
+    for (int p = blockIdx.x; p < n_pages; p += gridDim.x) {
+        const int page = pages[p];
+        if (static_cast<unsigned>(page) >= static_cast<unsigned>(num_pages)) continue;
+        const uint4 *src = base + static_cast<int64_t>(page) * page_vec;
+        for (int64_t at = 0; at < page_vec; at += 16 * 256) {
+            uint4 v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = src[at + i * 256 + threadIdx.x];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+        }
+    }
+    if (acc == 0x9e3779b9u) out[blockIdx.x] = acc;
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" int nq_kv_read_probe(const void *base, int num_pages, int64_t page_bytes, const int32_t *pages,
+                                int n_pages, int grid, uint32_t *out, void *stream) {
+    NQ_CHECK_ARG(base && pages && out && n_pages >= 1 && num_pages >= 1 && grid >= 1);
+    if (page_bytes <= 0 || page_bytes % (16 * 16 * 256) != 0 || !nq::aligned16(base)) return NQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(nq::kv_read_probe_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint4 *>(base), num_pages, pages, n_pages, page_bytes / 16, out);
+    return NQ_LAUNCH_STATUS();
+}
