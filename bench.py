@@ -505,15 +505,15 @@ def codec_step(args, torch, np) -> dict:
         return [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, int(f))))
                 for f in frames]
 
-    dec(chunk([cfg.retained_context] * CODEC_STREAMS), states)  # warm state: one full window per stream
+    dec.decode_ragged(chunk([cfg.retained_context] * CODEC_STREAMS), states)  # warm state: one full window per stream
     frames = rng.integers(12, 49, size=CODEC_STREAMS)
     batches = [chunk(frames) for _ in range(args.warmup + args.steps)]
     for i in range(args.warmup):
-        dec(batches[i], states)
+        dec.decode_ragged(batches[i], states)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        wav, pcm = dec(batches[args.warmup + i], states)
+        wav, pcm = dec.decode_ragged(batches[args.warmup + i], states)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed * 1000.0 / args.steps

@@ -1,11 +1,16 @@
 """Incremental codec-decoder step on the GPU for a batch of streams.
 
-Mirrors the ``incremental_decoder`` contract of CodecExecutor
-(executor/codec.py:69-118, 427-442): a callable ``(codes, states) -> wav`` with
-``samples_per_frame`` and ``retained_context`` attributes that mutates the
-streams' states (model/incremental_codec.py:383-466).  Chunks may be ragged:
-each stream brings its own number of fresh frames and all streams run in the
-same launches.
+``IncrementalCodecDecoder`` is the ``incremental_decoder`` CodecExecutor injects
+(executor/codec.py:69-118): ``decoder(codes [B, Q, F], states, *, position_ids=None,
+context_lengths=None) -> wav [B, 1, F * samples_per_frame]`` over the reference's
+per-row ``IncrementalCodecState`` objects, whose mapping tensors it reads and
+replaces and whose frame position and context length it advances
+(model/incremental_codec.py:383-466), with ``samples_per_frame`` and
+``retained_context`` attributes.  The state is staged into device slot arrays
+for the step and written back as new tensors, so the call can be captured into
+a hipGraph the way executor/codec.py:444-467 captures it.  ``decode_ragged`` is
+the same step over ragged chunks of streams whose state stays in the decoder's
+own slots (no staging).
 
 The upstream decoder (qwen-tts 0.1.1) is not available, so the module tree is
 a random-init causal decoder of the same structure, sized by ``CodecConfig``:
@@ -154,25 +159,39 @@ class CodecStreamState:
     _pool: object = field(default=None, repr=False)
 
 
+def _history_shapes(c: CodecConfig) -> dict[str, tuple[int, int]]:
+    """Causal convolutions with history: name -> (input channels, history length)."""
+
+    shapes = {"pre_conv": (c.dim, 2)}
+    for u in range(len(c.up_strides)):
+        shapes[f"up{u}.dw"] = (c.dim, 6)
+    shapes["dec0"] = (c.dim, 6)
+    for i in range(len(c.dec_strides)):
+        for j, dil in enumerate(c.dilations):
+            shapes[f"dec{i + 1}.res{j}.a"] = (c.dec_channels[i + 1], 6 * dil)
+    shapes["final"] = (c.dec_channels[-1], 6)
+    return shapes
+
+
+def _overlap_shapes(c: CodecConfig) -> dict[str, tuple[int, int]]:
+    """Causal transposed convolutions: name -> (output channels, stride = overlap length)."""
+
+    shapes = {f"up{u}.tc": (c.dim, s) for u, s in enumerate(c.up_strides)}
+    for i, s in enumerate(c.dec_strides):
+        shapes[f"dec{i + 1}.tc"] = (c.dec_channels[i + 1], s)
+    return shapes
+
+
 class _StatePool:
+    """Per-slot decoder state, channels last: histories [slots, pad, C], overlaps [slots, stride, C],
+    retained K/V [layers, slots, retained, heads, head_dim], frame position and valid context."""
+
     def __init__(self, config: CodecConfig, slots: int, device: torch.device) -> None:
         c = config
         z = dict(dtype=torch.float32, device=device)
         self.slots = slots
-        self.hist = {}
-        d = c.dim
-        self.hist["pre_conv"] = torch.zeros(slots, 2, d, **z)
-        for u in range(len(c.up_strides)):
-            self.hist[f"up{u}.dw"] = torch.zeros(slots, 6, d, **z)
-        self.hist["dec0"] = torch.zeros(slots, 6, d, **z)
-        for i in range(len(c.dec_strides)):
-            ch = c.dec_channels[i + 1]
-            for j, dil in enumerate(c.dilations):
-                self.hist[f"dec{i + 1}.res{j}.a"] = torch.zeros(slots, 6 * dil, ch, **z)
-        self.hist["final"] = torch.zeros(slots, 6, c.dec_channels[-1], **z)
-        self.overlap = {f"up{u}.tc": torch.zeros(slots, s, d, **z) for u, s in enumerate(c.up_strides)}
-        for i, s in enumerate(c.dec_strides):
-            self.overlap[f"dec{i + 1}.tc"] = torch.zeros(slots, s, c.dec_channels[i + 1], **z)
+        self.hist = {name: torch.zeros(slots, pad, cin, **z) for name, (cin, pad) in _history_shapes(c).items()}
+        self.overlap = {name: torch.zeros(slots, s, cout, **z) for name, (cout, s) in _overlap_shapes(c).items()}
         r = c.retained_context
         self.k = torch.zeros(c.layers, slots, r, c.heads, c.head_dim, **z)
         self.v = torch.zeros_like(self.k)
@@ -201,6 +220,9 @@ class IncrementalCodecDecoder:
         self.pool = _StatePool(self.config, max_streams, self.device)
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._cache: dict = {}
+        self._staging_pools: dict[int, _StatePool] = {}
+        self._shape_cache: dict = {}
+        self._pool = self.pool
 
     def new_state(self) -> CodecStreamState:
         if not self.pool.free:
@@ -227,7 +249,7 @@ class IncrementalCodecDecoder:
     def _conv(self, x, u, name, w, b, *, dilation=1, groups=1, act=None, residual=None):
         c_in = x.shape[1]
         c_out, _, k = w.shape
-        hist = self.pool.hist.get(name) if name else None
+        hist = self._pool.hist.get(name) if name else None
         a_ptr = _lib.ptr(act[0]) if act else None
         b_ptr = _lib.ptr(act[1]) if act else None
         if groups == 1 and (c_in * k >= self.GEMM_MIN_CIN_K or c_in >= 64) and c_in % 4 == 0:
@@ -255,7 +277,7 @@ class IncrementalCodecDecoder:
         c_in, c_out = w.shape[0], w.shape[1]
         a_ptr = _lib.ptr(act[0]) if act else None
         b_ptr = _lib.ptr(act[1]) if act else None
-        overlap = self.pool.overlap[name]
+        overlap = self._pool.overlap[name]
         if c_in >= 64 and c_in % 4 == 0:
             cols = torch.empty(x.shape[0], 2 * c_in, dtype=torch.float32, device=self.device)
             _lib.call("nq_codec_im2col", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u_in,
@@ -282,12 +304,156 @@ class IncrementalCodecDecoder:
     def _rms(x, w, eps):
         return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
 
-    # -- the step -------------------------------------------------------------
-    def __call__(self, codes, states: list[CodecStreamState]):
-        """codes: [B, Q, F] (equal chunks, the reference's layout) or a list of [Q, F_b] tensors.
-        Returns (wav list of [F_b * samples_per_frame] fp32, pcm16 list) per stream."""
+    # -- the reference's call: state objects in, waveform out ---------------------------------
+    def reference_keys(self) -> tuple[dict[str, str], dict[str, str]]:
+        """Our state names -> the reference's state-mapping keys (model/incremental_codec.py:383-466):
+        conv histories and transconv overlaps named after the upstream module path."""
 
-        c, w = self.config, self.w
+        c = self.config
+        hist = {"pre_conv": "pre_conv", "dec0": "decoder.0", "final": f"decoder.{len(c.dec_strides) + 2}"}
+        over = {}
+        for u in range(len(c.up_strides)):
+            hist[f"up{u}.dw"] = f"upsample.{u}.convnext.dwconv"
+            over[f"up{u}.tc"] = f"upsample.{u}.transconv"
+        for i in range(len(c.dec_strides)):
+            over[f"dec{i + 1}.tc"] = f"decoder.{i + 1}.transconv"
+            for j in range(len(c.dilations)):
+                hist[f"dec{i + 1}.res{j}.a"] = f"decoder.{i + 1}.residual.{j}.conv1"
+        return hist, over
+
+    def _staging(self, rows: int) -> "_StatePool":
+        pool = self._staging_pools.get(rows)
+        if pool is None:
+            pool = _StatePool(self.config, rows, self.device)
+            self._staging_pools[rows] = pool
+        return pool
+
+    def _shape_tensors(self, rows: int, frames: int):
+        """Device offsets / slot ids of an equal-chunk batch (made once per shape, so a captured call
+        issues no host-to-device copy)."""
+
+        key = (rows, frames)
+        got = self._shape_cache.get(key)
+        if got is None:
+            off = torch.arange(rows + 1, dtype=torch.int32, device=self.device) * frames
+            slots = torch.arange(rows, dtype=torch.int32, device=self.device)
+            got = (off, np.arange(rows + 1, dtype=np.int64) * frames, slots)
+            self._shape_cache[key] = got
+        return got
+
+    def _stage_in(self, states, pool: "_StatePool", rows: int, frames: int, position_ids, context_lengths) -> None:
+        c = self.config
+        dev = self.device
+        hist_keys, over_keys = self.reference_keys()
+
+        def gather(mapping: str, key, shape, dst_rows):
+            values = [getattr(st, mapping).get(key) for st in states]
+            for v in values:
+                if v is not None and tuple(v.shape) != shape:
+                    raise ValueError(f"invalid incremental state {key!r}: expected {shape}, got {tuple(v.shape)}")
+            if all(v is None for v in values):
+                dst_rows.zero_()
+                return
+            zero = None
+            rows_in = []
+            for v in values:
+                if v is None:
+                    zero = torch.zeros(shape, dtype=torch.float32, device=dev) if zero is None else zero
+                    v = zero
+                rows_in.append(v.to(device=dev, dtype=torch.float32))
+            dst_rows.copy_(torch.stack(rows_in).transpose(1, 2))
+
+        for name, (cin, pad) in _history_shapes(c).items():
+            gather("conv_histories", hist_keys[name], (cin, pad), pool.hist[name][:rows])
+        for name, (cout, stride) in _overlap_shapes(c).items():
+            gather("transconv_overlaps", over_keys[name], (cout, stride), pool.overlap[name][:rows])
+        r = c.retained_context
+        for li in range(c.layers):
+            gather("transformer_keys", li, (c.heads, r, c.head_dim), pool.k[li, :rows])
+            gather("transformer_values", li, (c.heads, r, c.head_dim), pool.v[li, :rows])
+        if position_ids is None:
+            pool.frame_pos[:rows].copy_(torch.tensor([st.frame_position for st in states], dtype=torch.long))
+        else:
+            if tuple(position_ids.shape) != (rows, frames):
+                raise ValueError(f"incremental position_ids must have shape {(rows, frames)}, got "
+                                 f"{tuple(position_ids.shape)}")
+            pool.frame_pos[:rows].copy_(position_ids[:, 0])
+        if context_lengths is None:
+            pool.ctx[:rows].copy_(torch.tensor([st.transformer_context_length for st in states], dtype=torch.int32))
+        else:
+            if tuple(context_lengths.shape) != (rows,):
+                raise ValueError(f"incremental context_lengths must have shape {(rows,)}, got "
+                                 f"{tuple(context_lengths.shape)}")
+            pool.ctx[:rows].copy_(context_lengths)
+
+    def _stage_out(self, states, pool: "_StatePool", rows: int, frames: int) -> None:
+        c = self.config
+        hist_keys, over_keys = self.reference_keys()
+        for name in _history_shapes(c):
+            new = pool.hist[name][:rows].transpose(1, 2).contiguous()
+            for st, row in zip(states, new.unbind(0)):
+                st.conv_histories[hist_keys[name]] = row
+        for name in _overlap_shapes(c):
+            new = pool.overlap[name][:rows].transpose(1, 2).contiguous()
+            for st, row in zip(states, new.unbind(0)):
+                st.transconv_overlaps[over_keys[name]] = row
+        for li in range(c.layers):
+            keys = pool.k[li, :rows].transpose(1, 2).contiguous()
+            values = pool.v[li, :rows].transpose(1, 2).contiguous()
+            for st, k, v in zip(states, keys.unbind(0), values.unbind(0)):
+                st.transformer_keys[li] = k
+                st.transformer_values[li] = v
+        r = c.retained_context
+        for st in states:
+            st.frame_position += frames
+            st.transformer_context_length = min(r, st.transformer_context_length + frames)
+
+    def __call__(self, codes: torch.Tensor, states, *, position_ids: torch.Tensor | None = None,
+                 context_lengths: torch.Tensor | None = None) -> torch.Tensor:
+        """The reference's ``incremental_decoder`` call (model/incremental_codec.py:383-466, as
+        CodecExecutor calls it at executor/codec.py:311-314 and 432-441): ``codes`` [B, Q, F]
+        (equal fresh frames per row), one reference ``IncrementalCodecState`` per row (its mapping
+        tensors are read, then replaced by new ones, and its frame position and context length
+        advanced), optional device ``position_ids`` [B, F] (consecutive per row) and
+        ``context_lengths`` [B].  Returns the clamped waveform [B, 1, F * samples_per_frame].
+
+        Graph-capturable after one eager call of the same shape (the shape's device constants and
+        staging buffers are made then) when position_ids and context_lengths are given."""
+
+        c = self.config
+        if not isinstance(codes, torch.Tensor) or codes.ndim != 3:
+            raise ValueError(f"expected codec codes with rank 3, got shape {tuple(getattr(codes, 'shape', ()))}")
+        rows, q, frames = (int(x) for x in codes.shape)
+        if rows != len(states):
+            raise ValueError(f"state count {len(states)} does not match batch {rows}")
+        if q != c.num_quantizers:
+            raise ValueError(f"expected {c.num_quantizers} codebooks, got {q}")
+        if frames == 0:
+            return torch.empty((rows, 1, 0), dtype=torch.float32, device=self.device)
+        pool = self._staging(rows)
+        self._stage_in(states, pool, rows, frames, position_ids, context_lengths)
+        off_dev, off_host, slots = self._shape_tensors(rows, frames)
+        packed = codes.to(device=self.device).permute(0, 2, 1).reshape(rows * frames, q).to(torch.int32).contiguous()
+        wav, _ = self._run(packed, rows, off_dev, off_host, slots, pool)
+        self._stage_out(states, pool, rows, frames)
+        return wav.view(rows, 1, frames * c.samples_per_frame)
+
+    def raise_on_status(self) -> None:
+        """Fail closed at a point where the caller synchronizes anyway: a codec id outside the
+        codebooks raises ValueError (the kernel used row 0 for it)."""
+
+        code = int(self.status.item())
+        if code != 0:
+            self.status.zero_()
+            raise ValueError("codec id outside the codebook range")
+
+    # -- ragged chunks over the decoder's own state slots --------------------------------------
+    def decode_ragged(self, codes, states: list[CodecStreamState]):
+        """codes: [B, Q, F] or a list of [Q, F_b] tensors, one per stream (ragged); ``states`` are
+        slots of this decoder (``new_state``).  Returns (wav list of [F_b * samples_per_frame] fp32,
+        pcm16 list) per stream."""
+
+        c = self.config
         chunks = list(codes) if not isinstance(codes, torch.Tensor) else [codes[i] for i in range(codes.shape[0])]
         if len(chunks) != len(states):
             raise ValueError(f"state count {len(states)} does not match batch {len(chunks)}")
@@ -296,19 +462,39 @@ class IncrementalCodecDecoder:
                 raise ValueError(f"expected [{c.num_quantizers}, frames] codes per stream")
         frames = [int(ch.shape[1]) for ch in chunks]
         B = len(chunks)
-        off = np.zeros(B + 1, dtype=np.int32)
+        off = np.zeros(B + 1, dtype=np.int64)
         off[1:] = np.cumsum(frames)
-        T = int(off[-1])
-        spf = c.samples_per_frame
-        if T == 0:
+        if off[-1] == 0:
             return [torch.empty(0, device=self.device) for _ in chunks], [
                 torch.empty(0, dtype=torch.int16, device=self.device) for _ in chunks]
         dev = self.device
-        self._B = B
-        self._off = torch.from_numpy(off).to(dev, non_blocking=True)
-        self._slots = torch.tensor([s.slot for s in states], dtype=torch.int32, device=dev)
-        self._stream = _lib.stream(dev)
+        off_dev = torch.from_numpy(off.astype(np.int32)).to(dev, non_blocking=True)
+        slots = torch.tensor([st.slot for st in states], dtype=torch.int32, device=dev)
         packed = torch.cat([ch.t() for ch in chunks], dim=0).to(device=dev, dtype=torch.int32).contiguous()
+        wav, pcm = self._run(packed, B, off_dev, off, slots, self.pool)
+        r = c.retained_context
+        for st, f in zip(states, frames):
+            st.frame_position += f
+            st.transformer_context_length = min(r, st.transformer_context_length + f)
+        bounds = off * c.samples_per_frame
+        return ([wav[bounds[i]: bounds[i + 1]] for i in range(B)], [pcm[bounds[i]: bounds[i + 1]] for i in range(B)])
+
+    # -- the step -------------------------------------------------------------
+    def _run(self, packed: torch.Tensor, B: int, off_dev: torch.Tensor, off_host: np.ndarray, slots: torch.Tensor,
+             pool: "_StatePool"):
+        """One step over B streams whose fresh frames are the rows of ``packed`` [T, Q] (stream b owns
+        rows off[b] .. off[b+1]), with state in ``pool`` slots ``slots``.  Returns (wav, pcm16), each
+        [T * samples_per_frame]."""
+
+        c, w = self.config, self.w
+        dev = self.device
+        T = int(off_host[-1])
+        spf = c.samples_per_frame
+        self._B = B
+        self._off = off_dev
+        self._slots = slots
+        self._pool = pool
+        self._stream = _lib.stream(dev)
 
         x = torch.empty(T, c.dim, dtype=torch.float32, device=dev)
         _lib.call("nq_codec_embed_sum", packed.data_ptr(), T, c.num_quantizers, w.codebooks.data_ptr(),
@@ -320,7 +506,6 @@ class IncrementalCodecDecoder:
         r = c.retained_context
         h = torch.addmm(w.in_b, x, w.in_w.t())
         att = torch.empty(T, hd, dtype=torch.float32, device=dev)
-        pool = self.pool
         for li, L in enumerate(w.tf):
             y = self._rms(h, L.ln1, c.eps)
             qkv = y @ L.wqkv.t()
@@ -358,11 +543,9 @@ class IncrementalCodecDecoder:
         wav = torch.empty(n, dtype=torch.float32, device=dev)
         pcm = torch.empty(n, dtype=torch.int16, device=dev)
         _lib.call("nq_codec_pcm16", y.data_ptr(), n, wav.data_ptr(), pcm.data_ptr(), self._stream)
-        for st, f in zip(states, frames):
-            st.frame_position += f
-            st.transformer_context_length = min(r, st.transformer_context_length + f)
-        bounds = off * spf
-        return ([wav[bounds[i]: bounds[i + 1]] for i in range(B)], [pcm[bounds[i]: bounds[i + 1]] for i in range(B)])
+        return wav, pcm
+
+
 
 
 __all__ = ["CodecConfig", "CodecStreamState", "CodecWeights", "IncrementalCodecDecoder"]

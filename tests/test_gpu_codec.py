@@ -26,7 +26,7 @@ def _run(cfg, device, seed, calls, max_streams=8):
     worst_rms, worst_max = 0.0, 0.0
     for frames in calls:
         codes = [torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(cfg.num_quantizers, int(f)))) for f in frames]
-        wav, pcm = dec(codes, states)
+        wav, pcm = dec.decode_ragged(codes, states)
         torch.cuda.synchronize()
         for b, f in enumerate(frames):
             want = o_codec.decode_incremental(w, cfg.as_dict(), codes[b].numpy().T, host_states[b])
@@ -86,10 +86,10 @@ def test_chunking_does_not_change_the_audio(nq, device):
     dec = IncrementalCodecDecoder(CodecWeights(cfg, device, seed=31), max_streams=4)
     codes = torch.from_numpy(np.random.default_rng(32).integers(0, cfg.codebook_size, size=(cfg.num_quantizers, 12)))
     a, b = dec.new_state(), dec.new_state()
-    whole, _ = dec([codes], [a])
+    whole, _ = dec.decode_ragged([codes], [a])
     parts = []
     for lo, hi in ((0, 4), (4, 7), (7, 12)):
-        wav, _ = dec([codes[:, lo:hi]], [b])
+        wav, _ = dec.decode_ragged([codes[:, lo:hi]], [b])
         parts.append(wav[0])
     torch.cuda.synchronize()
     np.testing.assert_allclose(torch.cat(parts).cpu().numpy(), whole[0].cpu().numpy(), atol=2e-5, rtol=1e-4)
