@@ -1,0 +1,182 @@
+"""The captured talker decode buckets of the serving path.
+
+Follows TalkerExecutor._capture_decode / _reserve / _replay_decode (executor/talker.py:461-560,
+:592-607) over the balanced profile's decode catalog (profiles/balanced.yaml:10-12, 33): every bucket
+size is captured ``capture_slots`` times, each capture slot with its own static inputs, attention
+binding and hipGraph; a bucket's slots are taken in rotation, each under a lease; all captures share
+one graph memory pool, so a decision runs under one pool fence.  Bindings and decode steps of one
+slot index share that slot's attention workspace and projection workspace (their graphs never run at
+the same time), as executor/talker_kv.py:361 shares FlashInfer workspaces.
+
+A decision's logical rows are lowered onto the buckets (planner/catalog.py:43-71: full largest
+buckets, then the smallest bucket that holds the rest, padded).  Padding rows get the reference's
+neutral sampling inputs (greedy, top-k 1, top-p 1, penalty 1, seed 0, offset 0; executor/talker.py:
+532-552).  Each part is planned and replayed before the next is planned, so parts that land on the
+same slot index never see each other's attention plan.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .graphs import GraphPoolFence, HipGraphCaptureDriver, SlotLeases, lower_rows
+from .talker import TalkerDecodeStep, TalkerWeights
+
+DECODE_BUCKETS = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 16, 24, 32, 40, 48, 56, 64)
+CAPTURE_SLOTS = 4
+
+
+class DecodeKey:
+    """TalkerDecodeCaptureKey's shape field (contract of TalkerKVBackend.create_decode)."""
+
+    def __init__(self, capture_batch_size: int) -> None:
+        self.capture_batch_size = capture_batch_size
+
+
+@dataclass(frozen=True)
+class DecodeRows:
+    """One decision's logical rows, staged by the executor (device tensors, first dim = rows)."""
+
+    request_ids: tuple[str, ...]
+    step_embed: torch.Tensor  # [n, hidden] bf16
+    text_ids: torch.Tensor  # [n] int64
+    temperature: torch.Tensor  # [n] fp32
+    top_k: torch.Tensor  # [n] int32
+    top_p: torch.Tensor  # [n] fp32
+    repetition_penalty: torch.Tensor  # [n] fp32
+    seed: torch.Tensor  # [n] int64
+    offsets: torch.Tensor  # [n] int64
+    seen: torch.Tensor  # [n, vocab] bool
+    suppress_eos: torch.Tensor  # [n] bool
+
+
+@dataclass(frozen=True)
+class DecodeResult:
+    tokens: torch.Tensor  # [n] int64
+    logits: torch.Tensor  # [n, vocab] bf16
+    seen: torch.Tensor  # [n, vocab] bool, with this step's token marked
+    publications: tuple
+    end_of_speech: np.ndarray  # [n] bool (one device-to-host copy per part, read once per decision)
+    parts: tuple  # (bucket, slot) per lowered part
+
+
+@dataclass
+class _Slot:
+    key: DecodeKey
+    context: object
+    step: TalkerDecodeStep
+    call: object
+    leases: SlotLeases
+
+
+class TalkerDecodeCatalog:
+    def __init__(self, weights: TalkerWeights, kv, *, buckets: tuple[int, ...] = DECODE_BUCKETS,
+                 capture_slots: int = CAPTURE_SLOTS, use_counter_rng: bool = True,
+                 driver: HipGraphCaptureDriver | None = None) -> None:
+        if not buckets or any(int(b) < 1 for b in buckets) or capture_slots < 1:
+            raise ValueError("the decode catalog needs positive bucket sizes and at least one capture slot")
+        self.weights = weights
+        self.kv = kv
+        self.buckets = tuple(sorted(set(int(b) for b in buckets)))
+        self.capture_slots = capture_slots
+        self.device = weights.codec_head.device
+        self.driver = driver or HipGraphCaptureDriver(device=self.device)
+        self.fence = GraphPoolFence(device=self.device)
+        self._slots: dict[int, tuple[_Slot, ...]] = {}
+        self._next: dict[int, int] = {}
+        workspaces: dict[int, torch.Tensor] = {}
+        # largest bucket first: each slot index's projection workspace is sized once, by it
+        for rows in reversed(self.buckets):
+            captured = []
+            for index in range(capture_slots):
+                key = DecodeKey(rows)
+                context = kv.create_decode(key, slot=index)
+                step = TalkerDecodeStep(weights, context, rows, use_counter_rng=use_counter_rng,
+                                        workspace=workspaces.get(index))
+                workspaces.setdefault(index, step.linear_workspace)
+                publications = kv.prepare_capture(context, key)
+                try:
+                    call = self.driver.capture(step.forward)
+                finally:
+                    kv.finish_capture(context, publications)
+                captured.append(_Slot(key, context, step, call, SlotLeases()))
+            self._slots[rows] = tuple(captured)
+            self._next[rows] = 0
+
+    def lower(self, rows: int):
+        return lower_rows(rows, self.buckets)
+
+    def _take(self, bucket: int) -> tuple[int, _Slot, int]:
+        index = self._next[bucket]
+        self._next[bucket] = (index + 1) % self.capture_slots
+        slot = self._slots[bucket][index]
+        return index, slot, slot.leases.reserve()
+
+    @staticmethod
+    def _stage(step: TalkerDecodeStep, rows: DecodeRows, a: int, b: int) -> None:
+        k = b - a
+        for dst, src, pad in ((step.step_embed, rows.step_embed, 0), (step.text_ids, rows.text_ids, 0),
+                              (step.temperature, rows.temperature, 0), (step.top_k, rows.top_k, 1),
+                              (step.top_p, rows.top_p, 1), (step.penalty, rows.repetition_penalty, 1),
+                              (step.seed, rows.seed, 0), (step.offsets, rows.offsets, 0), (step.seen, rows.seen, 0),
+                              (step.suppress_eos, rows.suppress_eos, 0)):
+            dst[:k].copy_(src[a:b])
+            if k < dst.shape[0]:
+                dst[k:].fill_(pad)
+
+    def decode(self, rows: DecodeRows) -> DecodeResult:
+        n = len(rows.request_ids)
+        if n < 1:
+            raise ValueError("a decode decision needs at least one row")
+        for name in ("step_embed", "text_ids", "temperature", "top_k", "top_p", "repetition_penalty", "seed",
+                     "offsets", "seen", "suppress_eos"):
+            if getattr(rows, name).shape[0] != n:
+                raise ValueError(f"decode rows: {name} does not have one entry per request")
+        vocab = self.weights.config.vocab
+        tokens = torch.empty(n, dtype=torch.long, device=self.device)
+        logits = torch.empty(n, vocab, dtype=torch.bfloat16, device=self.device)
+        seen = torch.empty(n, vocab, dtype=torch.bool, device=self.device)
+        publications: list = []
+        tickets: list = []
+        parts = []
+        fence = self.fence.reserve()
+        try:
+            for part in self.lower(n):
+                a, b = part.start, part.stop
+                index, slot, lease = self._take(part.capture_rows)
+                try:
+                    step = slot.step
+                    self._stage(step, rows, a, b)
+                    pubs = self.kv.prepare_decode(slot.context, slot.key, rows.request_ids[a:b])
+                    try:
+                        slot.call.replay()
+                        tickets.append((slot, step.report.fetch(), a, b))
+                    except Exception:
+                        self.kv.abort(pubs)
+                        raise
+                    publications.extend(pubs)
+                    tokens[a:b].copy_(step.tokens[: b - a])
+                    logits[a:b].copy_(step.logits[: b - a])
+                    seen[a:b].copy_(step.seen[: b - a])
+                    parts.append((part.capture_rows, index))
+                finally:
+                    slot.leases.release(lease)
+        except Exception:
+            self.kv.abort(tuple(publications))
+            raise
+        finally:
+            self.fence.release(fence)
+        eos = np.zeros(n, dtype=bool)
+        try:
+            for slot, ticket, a, b in tickets:
+                eos[a:b] = slot.step.report.read(ticket)[: b - a]
+        except Exception:
+            self.kv.abort(tuple(publications))
+            raise
+        return DecodeResult(tokens, logits, seen, tuple(publications), eos, tuple(parts))
+
+
+__all__ = ["CAPTURE_SLOTS", "DECODE_BUCKETS", "DecodeKey", "DecodeResult", "DecodeRows", "TalkerDecodeCatalog"]

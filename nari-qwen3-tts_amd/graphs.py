@@ -6,15 +6,20 @@ pool, and returns a call whose ``replay()`` launches the graph and returns
 the static outputs (executor/cuda_graph.py:15-77).  PyTorch-ROCm's graph
 object is a hipGraph; the HIP kernels launch on the capturing stream and
 issue no memset/memcpy nodes.  ``lower_rows`` splits a logical batch over
-the capture buckets as planner/catalog.py:43-71 does.
+the capture buckets as planner/catalog.py:43-71 does; ``SlotLeases`` and
+``GraphPoolFence`` are the slot and shared-pool guards of
+executor/cuda_graph.py:111-185.
 """
 
 from __future__ import annotations
 
 from collections.abc import Callable
 from dataclasses import dataclass
+from threading import Lock
 
 import torch
+
+from .errors import SlotBusyError
 
 
 @dataclass(slots=True)
@@ -54,6 +59,71 @@ class HipGraphCaptureDriver:
         return CapturedCall(graph, output)
 
 
+class SlotLeases:
+    """Exclusive use of one captured slot's static buffers (executor/cuda_graph.py:111-137): a slot is
+    taken by ``reserve()`` and given back by ``release(ticket)`` with the ticket it got; taking a busy
+    slot or giving back with a stale ticket raises SlotBusyError."""
+
+    __slots__ = ("_holder", "_count")
+
+    def __init__(self) -> None:
+        self._holder: int | None = None
+        self._count = 0
+
+    @property
+    def available(self) -> bool:
+        return self._holder is None
+
+    def reserve(self) -> int:
+        if self._holder is not None:
+            raise SlotBusyError("static CUDA Graph slot is in flight")
+        self._count += 1
+        self._holder = self._count
+        return self._count
+
+    def release(self, ticket: int) -> None:
+        if self._holder is None or self._holder != ticket:
+            raise SlotBusyError("stale or unowned static CUDA Graph slot lease")
+        self._holder = None
+
+
+class GraphPoolFence:
+    """One submission at a time over graphs that share a memory pool (executor/cuda_graph.py:140-185):
+    a second submission while one is open raises SlotBusyError instead of waiting, and each submission
+    starts behind the GPU work the previous one enqueued (an event recorded at release)."""
+
+    def __init__(self, *, device: torch.device) -> None:
+        self.device = torch.device(device)
+        self._lock = Lock()
+        self._done: torch.cuda.Event | None = None
+        self._open: int | None = None
+        self._count = 0
+
+    def reserve(self) -> int:
+        if not self._lock.acquire(blocking=False):
+            raise SlotBusyError("shared CUDA Graph memory pool is in flight")
+        try:
+            if self._done is not None:
+                torch.cuda.current_stream(self.device).wait_event(self._done)
+            self._count += 1
+            self._open = self._count
+            return self._count
+        except Exception:
+            self._lock.release()
+            raise
+
+    def release(self, ticket: int) -> None:
+        if self._open is None or self._open != ticket:
+            raise SlotBusyError("stale or unowned static CUDA Graph slot lease")
+        try:
+            done = torch.cuda.Event()
+            done.record(torch.cuda.current_stream(self.device))
+            self._done = done
+            self._open = None
+        finally:
+            self._lock.release()
+
+
 @dataclass(frozen=True, slots=True)
 class RowSlice:
     start: int
@@ -86,4 +156,4 @@ def lower_rows(logical_rows: int, sizes: tuple[int, ...]) -> tuple[RowSlice, ...
     return tuple(parts)
 
 
-__all__ = ["CapturedCall", "HipGraphCaptureDriver", "RowSlice", "lower_rows"]
+__all__ = ["CapturedCall", "GraphPoolFence", "HipGraphCaptureDriver", "RowSlice", "SlotLeases", "lower_rows"]

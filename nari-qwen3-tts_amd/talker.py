@@ -180,7 +180,8 @@ class StepReport:
 class TalkerDecodeStep:
     """Static buffers and the forward of one decode bucket (``rows`` physical rows)."""
 
-    def __init__(self, weights: TalkerWeights, context, rows: int, *, use_counter_rng: bool = False) -> None:
+    def __init__(self, weights: TalkerWeights, context, rows: int, *, use_counter_rng: bool = False,
+                 workspace: torch.Tensor | None = None) -> None:
         c = weights.config
         self.w = weights
         self.context = context
@@ -226,7 +227,11 @@ class TalkerDecodeStep:
             self.act_q = torch.zeros(rows, c.hidden, dtype=FP8, device=dev)
             self.act_scales = torch.zeros(rows, c.hidden // 128, dtype=torch.float32, device=dev)
             need = max(need, linear_fp8_workspace_bytes(rows, 2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL))
-        self.linear_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        # split-K planes of the projections; may be shared by steps whose graphs never run at once
+        if workspace is not None and workspace.numel() >= need:
+            self.linear_workspace = workspace
+        else:
+            self.linear_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
         # optional [layers + 1, rows, hidden] bf16 record of the residual stream: the step input, then
         # the residual after each layer (device-to-device copies, for layer-by-layer checks)
         self.trace: torch.Tensor | None = None

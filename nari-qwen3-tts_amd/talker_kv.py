@@ -80,6 +80,7 @@ class _HipBindingBase:
         total_pages: int,
         device: torch.device,
         dtype: torch.dtype,
+        workspace: torch.Tensor | None = None,
         **_: object,
     ) -> None:
         self.storage = storage
@@ -106,7 +107,11 @@ class _HipBindingBase:
             token_capacity, self.index_capacity, page_size, num_qo_heads, num_kv_heads, head_dim
         )
         _lib.check(min(int(nbytes), 0), "nq_attention_workspace_bytes")
-        self.workspace = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        if workspace is not None and workspace.numel() < int(nbytes):
+            raise ValueError(f"the attention workspace holds {workspace.numel()} bytes; this binding needs {int(nbytes)}")
+        # plan + partials; shared by the bindings of one capture slot (their graphs never run at once)
+        self.workspace = workspace if workspace is not None else torch.zeros(int(nbytes), dtype=torch.uint8,
+                                                                             device=device)
         self.attention_status = torch.zeros(1, dtype=torch.int32, device=device)
         self.output = torch.zeros((token_capacity, num_qo_heads, head_dim), dtype=dtype, device=device)
         self.position_ids = self.buffers.position_ids
@@ -366,6 +371,7 @@ class PagedTalkerKV:
         self._scratch_pages = self.allocator.claim_scratch_pages(scratch_page_count)
         self._scratch_dev = torch.tensor(self._scratch_pages, dtype=torch.int32, device=device)
         self._binding_factory = binding_factory
+        self._workspaces: dict[int, torch.Tensor] = {}
         self._next_capture = 0
         self._capture_requests: dict[int, tuple[str, ...]] = {}
         # device page table: row = ledger slot, up to total_pages page ids per request
@@ -468,11 +474,29 @@ class PagedTalkerKV:
         )
         if self._binding_factory is not None:
             arguments.update(slot=slot, metadata=None)
+        else:
+            arguments.update(workspace=self._slot_workspace(slot, key, prefill))
         binding = factory(**arguments)
         if isinstance(binding, _HipBindingBase):
             # the step report reads the free-list merge status next to the binding's own words
             binding.free_list_status = self.free_list_status
         return binding
+
+    def _slot_workspace(self, slot: int, key, prefill: bool) -> torch.Tensor:
+        """The attention workspace of capture slot ``slot``, shared by every binding of that slot
+        (executor/talker_kv.py:361): at least ``workspace_bytes``, grown (for later bindings; earlier
+        ones keep theirs) when a bucket needs more."""
+
+        tokens = key.token_capacity if prefill else key.capture_batch_size
+        need = int(_lib.load().nq_attention_workspace_bytes(
+            tokens, self.total_pages + key.capture_batch_size, self.page_size, self.num_qo_heads, self.num_kv_heads,
+            self.head_dim))
+        _lib.check(min(need, 0), "nq_attention_workspace_bytes")
+        ws = self._workspaces.get(slot)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(max(need, int(self.workspace_bytes)), dtype=torch.uint8, device=self.device)
+            self._workspaces[slot] = ws
+        return ws
 
     def create_prefill(self, key, *, slot: int):
         return self._binding(key, slot)

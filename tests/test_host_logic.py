@@ -181,3 +181,22 @@ def test_product_fails_loudly_without_gpu_tensors(nq):
     cpu = torch.zeros(2, 8)
     with pytest.raises(ValueError, match="GPU"):
         sample_with_uniforms(cpu, torch.zeros(2), torch.ones(2, dtype=torch.int32), torch.ones(2), torch.zeros(2))
+
+
+def test_slot_leases_fail_closed(nq):
+    from nari_qwen3_tts_amd.errors import SlotBusyError
+    from nari_qwen3_tts_amd.graphs import SlotLeases
+
+    leases = SlotLeases()
+    first = leases.reserve()
+    assert not leases.available
+    with pytest.raises(SlotBusyError, match="in flight"):
+        leases.reserve()
+    with pytest.raises(SlotBusyError, match="stale"):
+        leases.release(first + 1)
+    leases.release(first)
+    second = leases.reserve()
+    assert second != first
+    leases.release(second)
+    with pytest.raises(SlotBusyError):
+        leases.release(second)
