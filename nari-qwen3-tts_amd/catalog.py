@@ -12,7 +12,9 @@ A decision's logical rows are lowered onto the buckets (planner/catalog.py:43-71
 buckets, then the smallest bucket that holds the rest, padded).  Padding rows get the reference's
 neutral sampling inputs (greedy, top-k 1, top-p 1, penalty 1, seed 0, offset 0; executor/talker.py:
 532-552).  Each part is planned and replayed before the next is planned, so parts that land on the
-same slot index never see each other's attention plan.
+same slot index never see each other's attention plan.  ``decode`` returns without waiting for the
+GPU: the result's ``end_of_speech()`` reads the step reports (one copy per part) when the caller is
+ready to finalize.
 """
 
 from __future__ import annotations
@@ -55,12 +57,28 @@ class DecodeRows:
 
 @dataclass(frozen=True)
 class DecodeResult:
+    """A submitted decision.  The device outputs are valid in stream order at once; the host learns
+    whether the step succeeded and which rows reached end-of-speech from ``end_of_speech()``, which
+    waits for the decision's report copies (one per part) -- the host finalize of
+    engine/pipeline.py:585-610 with one copy per part instead of one ``.item()`` per row.
+    ``completion_fence`` (ready / wait) lets a submission window keep several decisions in flight."""
+
     tokens: torch.Tensor  # [n] int64
     logits: torch.Tensor  # [n, vocab] bf16
     seen: torch.Tensor  # [n, vocab] bool, with this step's token marked
     publications: tuple
-    end_of_speech: np.ndarray  # [n] bool (one device-to-host copy per part, read once per decision)
     parts: tuple  # (bucket, slot) per lowered part
+    reports: tuple  # (StepReport, ticket, first row, end row) per part
+    completion_fence: object
+
+    def end_of_speech(self) -> np.ndarray:
+        """[n] bool; raises the mapped error (fail closed) if any part reported a bad status."""
+
+        n = self.tokens.shape[0]
+        eos = np.zeros(n, dtype=bool)
+        for report, ticket, a, b in self.reports:
+            eos[a:b] = report.read(ticket)[: b - a]
+        return eos
 
 
 @dataclass
@@ -169,14 +187,10 @@ class TalkerDecodeCatalog:
             raise
         finally:
             self.fence.release(fence)
-        eos = np.zeros(n, dtype=bool)
-        try:
-            for slot, ticket, a, b in tickets:
-                eos[a:b] = slot.step.report.read(ticket)[: b - a]
-        except Exception:
-            self.kv.abort(tuple(publications))
-            raise
-        return DecodeResult(tokens, logits, seen, tuple(publications), eos, tuple(parts))
+        reports = tuple((slot.step.report, ticket, a, b) for slot, ticket, a, b in tickets)
+        last_report, last_ticket = reports[-1][0], reports[-1][1]
+        return DecodeResult(tokens, logits, seen, tuple(publications), tuple(parts), reports,
+                            last_report.fence(last_ticket))
 
 
 __all__ = ["CAPTURE_SLOTS", "DECODE_BUCKETS", "DecodeKey", "DecodeResult", "DecodeRows", "TalkerDecodeCatalog"]

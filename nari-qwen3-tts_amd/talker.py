@@ -176,6 +176,26 @@ class StepReport:
         check_step_report(words[: _lib.NQ_REPORT_HEAD])
         return words[_lib.NQ_REPORT_HEAD:].astype(bool)
 
+    def fence(self, ticket: int) -> "ReportFence":
+        return ReportFence(self._events[ticket])
+
+
+class ReportFence:
+    """Completion fence of one report copy: ``ready()`` without blocking, ``wait()`` blocking -- the
+    interface the reference's SubmissionWindow polls before a host finalize
+    (executor/submission.py:126-228)."""
+
+    __slots__ = ("_event",)
+
+    def __init__(self, event) -> None:
+        self._event = event
+
+    def ready(self) -> bool:
+        return bool(self._event.query())
+
+    def wait(self) -> None:
+        self._event.synchronize()
+
 
 class TalkerDecodeStep:
     """Static buffers and the forward of one decode bucket (``rows`` physical rows)."""
@@ -331,4 +351,4 @@ class TalkerDecodeStep:
             sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
 
 
-__all__ = ["StepReport", "TalkerConfig", "TalkerDecodeStep", "TalkerWeights", "check_step_report"]
+__all__ = ["ReportFence", "StepReport", "TalkerConfig", "TalkerDecodeStep", "TalkerWeights", "check_step_report"]

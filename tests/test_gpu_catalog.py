@@ -118,7 +118,8 @@ def test_catalog_lowers_rotates_and_matches_oracle(nq, device, profile):
         want_seen = seen0.copy()
         want_seen[np.arange(n), want_tok] = True
         np.testing.assert_array_equal(to_np(result.seen), want_seen)
-        np.testing.assert_array_equal(result.end_of_speech, want_tok == cfg.eos_id)
+        np.testing.assert_array_equal(result.end_of_speech(), want_tok == cfg.eos_id)
+        assert result.completion_fence.ready()
         for p in pubs:
             p.publish()
         rows = DecodeRows(**{**rows.__dict__, "seen": result.seen.clone(), "offsets": rows.offsets + 512})

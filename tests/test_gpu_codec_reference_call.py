@@ -155,3 +155,36 @@ def test_captured_reference_call_replays_like_eager(nq, device):
         # carry: the requests continue from the eager results (frame positions advance)
         live = reference
         dec.raise_on_status()
+
+
+def test_pcm16_and_pinned_transfer_of_the_decoded_waveform(nq, device):
+    """CodecExecutor._pcm16 (executor/codec.py:236-238) on the device, then the PCM's device-to-host
+    handoff through the transfer pool's interface (executor/pcm.py:55-143): the bytes equal the
+    oracle's PCM16 of the same waveform; lanes are leased and returned."""
+    from nari_qwen3_tts_amd.pcm import PcmTransferPool, pcm16
+
+    cfg, weights, dec = _decoder(device, seed=71)
+    rng = np.random.default_rng(72)
+    states = [IncrementalCodecState() for _ in range(2)]
+    codes = torch.from_numpy(rng.integers(0, cfg.codebook_size, size=(2, 9, 16))).to(device)
+    wav = dec(codes.transpose(1, 2), states).squeeze(1)
+    pcm = pcm16(wav * 1.7)  # scaled so that the clamp is exercised
+    pool = PcmTransferPool(maximum_samples=wav.shape[1], device=device)
+    pool.prepare(3)
+    assert pool.available == 3 and pool.active == 0
+    transfers = [pool.begin(pcm[b]) for b in range(2)]
+    assert pool.active == 2
+    for b, tr in enumerate(transfers):
+        payload = None
+        while payload is None:
+            payload = tr.poll()
+        want = o_codec.pcm16((wav[b] * 1.7).cpu().numpy())
+        assert payload == want.tobytes()
+    assert pool.active == 0 and pool.available == 3
+    with pytest.raises(RuntimeError, match="capacity"):
+        pool.begin(torch.zeros(wav.shape[1] + 1, dtype=torch.int16, device=device))
+    late = pool.begin(pcm[0])
+    late.discard_when_ready()
+    assert pool.active == 0
+    assert o_codec.pcm16(np.array([-2.0, -0.5, 0.0, 0.5, 2.0], np.float32)).tolist() == \
+        pcm16(torch.tensor([-2.0, -0.5, 0.0, 0.5, 2.0], device=device)).tolist()
