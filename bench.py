@@ -722,6 +722,109 @@ def mixed_attention(args, torch, np) -> dict:
     return result
 
 
+def talker_prefill(args, torch, np) -> dict:
+    """The prefill part of the mixed batch as talker prefill steps: 16 prompt chunks (qo U{32..256}) over
+    prior context U{0..512} on the 28-layer talker, lowered onto the balanced profile's prefill captures
+    (at most 8 rows and 640 tokens per part), each part replayed from its hipGraph: embeddings, every
+    layer's projections (128-row pieces of the HIP GEMMs, FP8 gate/up), causal paged prefill attention,
+    the last-token codec head and the sampler.  Timed per decision (all parts), publications discarded."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.catalog import PrefillRows, TalkerPrefillCatalog, lower_prefill, prefill_keys
+    from nari_qwen3_tts_amd.talker import TalkerConfig, TalkerWeights
+    from nari_qwen3_tts_amd.talker_kv import PagedTalkerKV
+
+    dev = torch.device("cuda:0")
+    cfg = TalkerConfig()
+    rng = np.random.default_rng(MIXED_SEED)
+    prior = rng.integers(0, 513, size=MIXED_PREFILL)
+    lengths = tuple(int(x) for x in rng.integers(32, 257, size=MIXED_PREFILL))
+    t0 = time.perf_counter()
+    kv = PagedTalkerKV(num_layers=cfg.num_layers, num_kv_heads=cfg.num_kv_heads, num_qo_heads=cfg.num_qo_heads,
+                       head_dim=cfg.head_dim, total_pages=POOL_PAGES, page_size=PAGE_SIZE, scratch_page_count=64,
+                       workspace_bytes=0, device=dev, dtype=torch.bfloat16)
+    g = torch.Generator(device=dev)
+    g.manual_seed(MIXED_SEED)
+    for layer in range(cfg.num_layers):
+        kv.storage[layer].normal_(generator=g)
+    pool = rng.permutation(np.asarray(kv.allocator.free_list()))
+    rids, at = [], 0
+    for i, n in enumerate(prior):
+        rid = f"p{i}"
+        kv.add_request(rid)
+        need = -(-int(n) // PAGE_SIZE)
+        if need:
+            kv.adopt_request(rid, pool[at: at + need], int(n))
+        at += need
+        rids.append(rid)
+    weights = TalkerWeights(cfg, dev, seed=MIXED_SEED, fp8_gate_up=True)
+    parts = lower_prefill(lengths, prefill_keys())
+    keys = {p.key for p in parts}
+    catalog = TalkerPrefillCatalog(weights, kv, keys=keys, capture_slots=1)
+    n, total = MIXED_PREFILL, sum(lengths)
+    gen = torch.Generator(device="cpu").manual_seed(MIXED_SEED)
+    rows = PrefillRows(
+        request_ids=tuple(rids), lengths=lengths,
+        text_ids=torch.randint(0, cfg.text_vocab, (total,), generator=gen).to(dev),
+        codec_ids=torch.randint(0, cfg.vocab, (total,), generator=gen).to(dev),
+        codec_mask=(torch.rand(total, generator=gen) < 0.5).to(dev),
+        temperature=torch.full((n,), 0.9, device=dev), top_k=torch.full((n,), 50, dtype=torch.int32, device=dev),
+        top_p=torch.full((n,), 0.95, device=dev), repetition_penalty=torch.full((n,), 1.05, device=dev),
+        seed=torch.arange(n, device=dev) + MIXED_SEED, offsets=torch.zeros(n, dtype=torch.long, device=dev),
+        seen=torch.zeros(n, cfg.vocab, dtype=torch.bool, device=dev), suppress_eos=torch.ones(n, dtype=torch.bool,
+                                                                                             device=dev))
+    log(f"setup {time.perf_counter() - t0:.1f}s; {total} prompt tokens in {len(parts)} parts: "
+        + ", ".join(f"{p.stop - p.start} rows/{sum(lengths[p.start:p.stop])} tok -> B{p.key.capture_batch_size}/"
+                    f"T{p.key.token_capacity}" for p in parts))
+
+    def decision():
+        result = catalog.prefill(rows)
+        kv.abort(result.publications)
+        return result
+
+    for _ in range(args.warmup):
+        decision()
+    last = decision()
+    last.end_of_speech()  # fails closed on any status word
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t1 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        decision()
+    end.record()
+    end.synchronize()
+    wall_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    ms = start.elapsed_time(end) / args.steps
+    # algorithmic work of the real tokens: projections + causal attention over prior context
+    layer_params = cfg.qkv_width * cfg.hidden + cfg.hidden * cfg.num_qo_heads * cfg.head_dim \
+        + 2 * cfg.intermediate * cfg.hidden + cfg.hidden * cfg.intermediate
+    adv = np.asarray(lengths, dtype=np.float64)
+    pri = prior.astype(np.float64)
+    attn = float(np.sum(4.0 * cfg.num_qo_heads * cfg.head_dim * (adv * pri + adv * (adv + 1) / 2)))
+    flops = cfg.num_layers * (2.0 * total * layer_params + attn) + 2.0 * n * cfg.vocab * cfg.hidden
+    padded = sum(p.key.token_capacity for p in parts)
+    tflops = flops / (ms / 1e3) / 1e12
+    tok_s = total / (wall_ms / 1e3)
+    log(f"prefill decision: {ms:.2f} ms GPU ({wall_ms:.2f} ms wall) for {total} tokens ({padded} captured) -> "
+        f"{tok_s:.0f} prompt tok/s, {tflops:.1f} TFLOP/s algorithmic")
+    return {
+        "metric": "talker prefill: prompt tokens/s (16 chunks U{32..256} over prior U{0..512}, captured buckets)",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (FP8 e4m3 gate/up)", "data": "synthetic (random-init 28-layer talker, N(0,1) KV pool)",
+        "config": {"workload": "talker prefill, 28 layers, hidden 2048, 16q/8kv x 128, FFN 6144, 16 chunks qo "
+                               "U{32..256} with prior U{0..512}, page size 16, 32768-page pool, balanced prefill "
+                               "captures", "global_batch": n, "tokens": total, "captured_tokens": padded,
+                   "parts": len(parts), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4), "traffic": None, "kernel": "whole prefill decision",
+                     "flops_per_step": flops, "gpu_ms_per_step": round(ms, 4)},
+    }
+
+
 def kv_read_ceiling(args, torch, np) -> dict:
     """The read ceiling of the decode attention's access pattern: the K/V pages of the batch-64 decode
     workload (64 rows, KV U[64, 2048], permuted 32768-page pool) read whole by nq_kv_read_probe, one
@@ -776,7 +879,7 @@ def kv_read_ceiling(args, torch, np) -> dict:
 
 
 WORKLOADS = {"talker-decode": talker_decode, "kv-read-ceiling": kv_read_ceiling, "code-predictor": code_predictor, "codec": codec_step,
-             "mixed": mixed_attention}
+             "mixed": mixed_attention, "talker-prefill": talker_prefill}
 
 
 def main() -> int:

@@ -335,6 +335,21 @@ int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, int64_t tabl
                          float eps, uint16_t *residual, uint16_t *out, int32_t *status, void *stream);
 
 /*
+ * Talker prefill input embedding and the first input norm in one launch
+ * (TalkerExecutor.materialize_prefill, executor/talker.py:246-254, then the
+ * first layer's input RMSNorm): residual[r] = text[text_ids[r]] +
+ * codec[codec_ids[r]] (a bf16 add) where mask[r] != 0, else text[text_ids[r]];
+ * out[r] = rmsnorm(residual[r]) * weight.  bf16 [rows, width], residual / out
+ * contiguous; an id outside its table reads row 0 and stores
+ * NQ_ERR_INVALID_ARGUMENT in *status (may be NULL).
+ */
+int nq_prefill_embed_rmsnorm(const int64_t *text_ids, const uint16_t *text_table, int64_t text_s0,
+                             int64_t text_rows, const int64_t *codec_ids, const uint16_t *codec_table,
+                             int64_t codec_s0, int64_t codec_rows, const uint8_t *mask, const uint16_t *weight,
+                             int rows, int width, float eps, uint16_t *residual, uint16_t *out, int32_t *status,
+                             void *stream);
+
+/*
  * out[r] = first_table[first_ids[r]] + tables[0][ids[0][r]] + ... +
  * tables[groups-1][ids[groups-1][r]], added in group order with every partial
  * sum rounded to bf16: the code predictor's codec_sum (layer-0 embedding plus

@@ -68,6 +68,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_uniforms_from_counter": [_P, _L, _P, _L, _I, _P, _P],
     "nq_add_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "nq_embed_add_rmsnorm": [_P, _P, _L, _L, _P, _L, _P, _I, _I, _F, _P, _P, _P, _P],
+    "nq_prefill_embed_rmsnorm": [_P, _P, _L, _L, _P, _P, _L, _L, _P, _P, _I, _I, _F, _P, _P, _P, _P],
     "nq_gather_sum_rows": [_P, _P, _L, _L, _P, _L, _L, _P, _L, _L, _L, _I, _I, _I, _P, _L, _P, _P],
     "nq_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
     "nq_silu_mul": [_P, _P, _I, _I, _P],

@@ -24,8 +24,9 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
+from .errors import CaptureCoverageError
 from .graphs import GraphPoolFence, HipGraphCaptureDriver, SlotLeases, lower_rows
-from .talker import TalkerDecodeStep, TalkerWeights
+from .talker import TalkerDecodeStep, TalkerPrefillStep, TalkerWeights
 
 DECODE_BUCKETS = (1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 16, 24, 32, 40, 48, 56, 64)
 CAPTURE_SLOTS = 4
@@ -83,9 +84,9 @@ class DecodeResult:
 
 @dataclass
 class _Slot:
-    key: DecodeKey
+    key: object
     context: object
-    step: TalkerDecodeStep
+    step: object
     call: object
     leases: SlotLeases
 
@@ -193,4 +194,243 @@ class TalkerDecodeCatalog:
                             last_report.fence(last_ticket))
 
 
-__all__ = ["CAPTURE_SLOTS", "DECODE_BUCKETS", "DecodeKey", "DecodeResult", "DecodeRows", "TalkerDecodeCatalog"]
+# The balanced profile's prefill catalog (profiles/balanced.yaml:4-9): token buckets for batch sizes
+# 1, 2, 4, 8 and exact 10-token captures for 1..8 rows.
+PREFILL_BATCH_SIZES = (1, 2, 4, 8)
+PREFILL_TOKEN_BUCKETS = (32, 64, 128, 192, 384, 640)
+PREFILL_EXACT_SEQUENCE_LENGTHS = (10,)
+PREFILL_EXACT_BATCH_SIZES = (1, 2, 3, 4, 5, 6, 7, 8)
+PREFILL_MAX_BATCH = 8
+
+
+@dataclass(frozen=True)
+class PrefillKey:
+    """TalkerPrefillCaptureKey (contract/stage.py:39-48): rows, packed token capacity and, for an
+    exact capture, the one sequence length it was built for."""
+
+    capture_batch_size: int
+    token_capacity: int
+    capture_sequence_length: int | None = None
+
+    def __post_init__(self) -> None:
+        for name in ("capture_batch_size", "token_capacity"):
+            value = getattr(self, name)
+            if isinstance(value, bool) or not isinstance(value, int) or value < 1:
+                raise ValueError(f"{name.replace('_', ' ')} must be a positive integer")
+        length = self.capture_sequence_length
+        if length is not None and (isinstance(length, bool) or not isinstance(length, int) or length < 1):
+            raise ValueError("capture sequence length must be a positive integer")
+
+
+def prefill_keys(*, batch_sizes=PREFILL_BATCH_SIZES, token_buckets=PREFILL_TOKEN_BUCKETS,
+                 exact_sequence_lengths=PREFILL_EXACT_SEQUENCE_LENGTHS,
+                 exact_batch_sizes=PREFILL_EXACT_BATCH_SIZES) -> frozenset:
+    """Every prefill capture of a profile (CaptureCatalog.from_config, planner/catalog.py:86-97)."""
+
+    exact = {PrefillKey(b, b * s, s) for s in exact_sequence_lengths for b in exact_batch_sizes}
+    return frozenset(exact | {PrefillKey(b, t) for b in batch_sizes for t in token_buckets})
+
+
+@dataclass(frozen=True)
+class PrefillSlice:
+    key: PrefillKey
+    start: int
+    stop: int
+    capture_rows: int
+    padding: int
+
+
+def lower_prefill(sequence_lengths: tuple[int, ...], keys, max_batch_size: int = PREFILL_MAX_BATCH):
+    """Pack consecutive requests into prefill captures (lower_talker_prefill, planner/catalog.py:
+    262-314): a part takes requests while it has fewer than ``max_batch_size`` and their tokens fit
+    the largest token capacity; it runs on the capture with the least token capacity, then the
+    fewest rows, bucketed before exact, that covers its rows and tokens."""
+
+    if not isinstance(sequence_lengths, tuple) or not sequence_lengths:
+        raise ValueError("Talker prefill sequence lengths must be a non-empty tuple")
+    if any(isinstance(n, bool) or not isinstance(n, int) or n <= 0 for n in sequence_lengths):
+        raise ValueError("Talker prefill sequence lengths must be positive integers")
+    keys = tuple(keys)
+    most = max(k.token_capacity for k in keys)
+    order = sorted(keys, key=lambda k: (k.token_capacity, k.capture_batch_size, k.capture_sequence_length is None,
+                                        k.capture_sequence_length or 0))
+    parts = []
+    start = 0
+    count = len(sequence_lengths)
+    while start < count:
+        if sequence_lengths[start] > most:
+            raise CaptureCoverageError("Talker prefill capture token capacity exceeded")
+        stop, tokens = start, 0
+        while stop < count and stop - start < max_batch_size and tokens + sequence_lengths[stop] <= most:
+            tokens += sequence_lengths[stop]
+            stop += 1
+        rows = stop - start
+        key = next((k for k in order if k.capture_batch_size >= rows and k.token_capacity >= tokens), None)
+        if key is None:
+            raise CaptureCoverageError(f"no Talker prefill capture covers {rows} rows and {tokens} tokens")
+        parts.append(PrefillSlice(key, start, stop, key.capture_batch_size, key.capture_batch_size - rows))
+        start = stop
+    return tuple(parts)
+
+
+@dataclass(frozen=True)
+class PrefillRows:
+    """One prefill decision's requests, staged by the executor: the rows' prompt tokens packed in row
+    order (device tensors of sum(lengths) entries) and per-row sampling inputs (first dim = rows)."""
+
+    request_ids: tuple[str, ...]
+    lengths: tuple[int, ...]
+    text_ids: torch.Tensor  # [tokens] int64
+    codec_ids: torch.Tensor  # [tokens] int64
+    codec_mask: torch.Tensor  # [tokens] bool
+    temperature: torch.Tensor  # [n] fp32
+    top_k: torch.Tensor  # [n] int32
+    top_p: torch.Tensor  # [n] fp32
+    repetition_penalty: torch.Tensor  # [n] fp32
+    seed: torch.Tensor  # [n] int64
+    offsets: torch.Tensor  # [n] int64
+    seen: torch.Tensor  # [n, vocab] bool
+    suppress_eos: torch.Tensor  # [n] bool
+
+
+@dataclass(frozen=True)
+class PrefillResult:
+    """A submitted prefill decision (TalkerExecutionResult of executor/rows.py:126-130 over every
+    part): tokens, last-token hidden states, logits and next seen masks of the rows, the pending
+    KV publications, and the parts' step reports (``end_of_speech()`` reads them, fail closed)."""
+
+    tokens: torch.Tensor  # [n] int64
+    last_hidden: torch.Tensor  # [n, hidden] bf16
+    logits: torch.Tensor  # [n, vocab] bf16
+    seen: torch.Tensor  # [n, vocab] bool
+    publications: tuple
+    parts: tuple  # (key, slot) per lowered part
+    reports: tuple
+    completion_fence: object
+
+    end_of_speech = DecodeResult.end_of_speech
+
+
+class TalkerPrefillCatalog:
+    """Every prefill capture key x ``capture_slots`` captured prefill steps sharing one graph pool
+    (TalkerExecutor._capture_prefill, executor/talker.py:397-459); decisions are lowered with
+    ``lower_prefill`` and replayed part by part like the decode catalog (slot rotation under leases,
+    one pool fence).  Steps of one slot index share the slot's projection workspace."""
+
+    def __init__(self, weights: TalkerWeights, kv, *, keys=None, capture_slots: int = CAPTURE_SLOTS,
+                 max_batch_size: int = PREFILL_MAX_BATCH, driver: HipGraphCaptureDriver | None = None,
+                 fence: GraphPoolFence | None = None) -> None:
+        keys = prefill_keys() if keys is None else frozenset(keys)
+        if not keys or capture_slots < 1:
+            raise ValueError("the prefill catalog needs at least one key and one capture slot")
+        self.weights = weights
+        self.kv = kv
+        self.keys = keys
+        self.capture_slots = capture_slots
+        self.max_batch_size = max_batch_size
+        self.device = weights.codec_head.device
+        self.driver = driver or HipGraphCaptureDriver(device=self.device)
+        self.fence = fence or GraphPoolFence(device=self.device)
+        self._slots: dict[PrefillKey, tuple[_Slot, ...]] = {}
+        self._next: dict[PrefillKey, int] = {}
+        workspaces: dict[int, torch.Tensor] = {}
+        for key in sorted(keys, key=lambda k: (-k.token_capacity, -k.capture_batch_size)):
+            captured = []
+            for index in range(capture_slots):
+                context = kv.create_prefill(key, slot=index)
+                step = TalkerPrefillStep(weights, context, key.capture_batch_size, key.token_capacity,
+                                         workspace=workspaces.get(index))
+                workspaces.setdefault(index, step.linear_workspace)
+                publications = kv.prepare_capture(context, key)
+                try:
+                    call = self.driver.capture(step.forward)
+                finally:
+                    kv.finish_capture(context, publications)
+                captured.append(_Slot(key, context, step, call, SlotLeases()))
+            self._slots[key] = tuple(captured)
+            self._next[key] = 0
+
+    def lower(self, lengths: tuple[int, ...]):
+        return lower_prefill(tuple(lengths), self.keys, self.max_batch_size)
+
+    def _take(self, key: PrefillKey):
+        index = self._next[key]
+        self._next[key] = (index + 1) % self.capture_slots
+        slot = self._slots[key][index]
+        return index, slot, slot.leases.reserve()
+
+    @staticmethod
+    def _stage(step: TalkerPrefillStep, rows: PrefillRows, a: int, b: int, t0: int, t1: int) -> None:
+        k, t = b - a, t1 - t0
+        for dst, src in ((step.text_ids, rows.text_ids), (step.codec_ids, rows.codec_ids),
+                         (step.codec_mask, rows.codec_mask)):
+            dst[:t].copy_(src[t0:t1])
+            if t < dst.shape[0]:
+                dst[t:].fill_(0)
+        for dst, src, pad in ((step.temperature, rows.temperature, 0), (step.top_k, rows.top_k, 1),
+                              (step.top_p, rows.top_p, 1), (step.penalty, rows.repetition_penalty, 1),
+                              (step.seed, rows.seed, 0), (step.offsets, rows.offsets, 0), (step.seen, rows.seen, 0),
+                              (step.suppress_eos, rows.suppress_eos, 1)):
+            dst[:k].copy_(src[a:b])
+            if k < dst.shape[0]:
+                dst[k:].fill_(pad)
+
+    def prefill(self, rows: PrefillRows) -> PrefillResult:
+        n = len(rows.request_ids)
+        if n < 1 or len(rows.lengths) != n:
+            raise ValueError("Talker prefill row count does not match request IDs")
+        total = sum(rows.lengths)
+        for name in ("text_ids", "codec_ids", "codec_mask"):
+            if getattr(rows, name).shape != (total,):
+                raise ValueError("Talker prefill row tensors must have equal sequence lengths")
+        for name in ("temperature", "top_k", "top_p", "repetition_penalty", "seed", "offsets", "seen",
+                     "suppress_eos"):
+            if getattr(rows, name).shape[0] != n:
+                raise ValueError(f"prefill rows: {name} does not have one entry per request")
+        c = self.weights.config
+        tokens = torch.empty(n, dtype=torch.long, device=self.device)
+        hidden = torch.empty(n, c.hidden, dtype=torch.bfloat16, device=self.device)
+        logits = torch.empty(n, c.vocab, dtype=torch.bfloat16, device=self.device)
+        seen = torch.empty(n, c.vocab, dtype=torch.bool, device=self.device)
+        starts = np.concatenate([[0], np.cumsum(rows.lengths)])
+        publications: list = []
+        tickets: list = []
+        parts = []
+        fence = self.fence.reserve()
+        try:
+            for part in self.lower(tuple(rows.lengths)):
+                a, b = part.start, part.stop
+                index, slot, lease = self._take(part.key)
+                try:
+                    step = slot.step
+                    self._stage(step, rows, a, b, int(starts[a]), int(starts[b]))
+                    pubs = self.kv.prepare_prefill(slot.context, part.key, rows.request_ids[a:b], rows.lengths[a:b])
+                    try:
+                        slot.call.replay()
+                        tickets.append((slot, step.report.fetch(), a, b))
+                    except Exception:
+                        self.kv.abort(pubs)
+                        raise
+                    publications.extend(pubs)
+                    k = b - a
+                    tokens[a:b].copy_(step.tokens[:k])
+                    hidden[a:b].copy_(step.last_hidden[:k])
+                    logits[a:b].copy_(step.logits[:k])
+                    seen[a:b].copy_(step.seen[:k])
+                    parts.append((part.key, index))
+                finally:
+                    slot.leases.release(lease)
+        except Exception:
+            self.kv.abort(tuple(publications))
+            raise
+        finally:
+            self.fence.release(fence)
+        reports = tuple((slot.step.report, ticket, a, b) for slot, ticket, a, b in tickets)
+        return PrefillResult(tokens, hidden, logits, seen, tuple(publications), tuple(parts), reports,
+                             reports[-1][0].fence(reports[-1][1]))
+
+
+__all__ = ["CAPTURE_SLOTS", "DECODE_BUCKETS", "PREFILL_BATCH_SIZES", "PREFILL_EXACT_BATCH_SIZES",
+           "PREFILL_EXACT_SEQUENCE_LENGTHS", "PREFILL_MAX_BATCH", "PREFILL_TOKEN_BUCKETS", "DecodeKey", "DecodeResult",
+           "DecodeRows", "PrefillKey", "PrefillResult", "PrefillRows", "PrefillSlice", "TalkerDecodeCatalog",
+           "TalkerPrefillCatalog", "lower_prefill", "prefill_keys"]

@@ -71,6 +71,23 @@ struct GatherSrc {
     }
 };
 
+// Prefill input embedding (materialize_prefill, executor/talker.py:246-254): row r is
+// text[text_ids[r]] + codec[codec_ids[r]] added in bf16 where mask[r], else text[text_ids[r]]
+// exactly.  Ids outside their tables read row 0 and report NQ_ERR_INVALID_ARGUMENT.
+struct MaskedPairSrc {
+    GatherSrc text;
+    GatherSrc codec;
+    const uint8_t *mask;
+    __device__ __forceinline__ void load8(int64_t row, int col, float (&x)[8]) const {
+        text.load8(row, col, x);
+        if (!mask[row]) return;
+        float c[8];
+        codec.load8(row, col, c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16(x[e] + c[e]));
+    }
+};
+
 // Quantized output of the normalised row: codes [rows, width] and scales
 // [rows, width / 128].
 struct Fp8Out {
@@ -407,6 +424,26 @@ extern "C" int nq_embed_add_rmsnorm(const int64_t *ids, const uint16_t *table, i
     nq::launch_add_rmsnorm<nq::GatherSrc, false>(rows, width, static_cast<hipStream_t>(stream), src, out,
                                                  static_cast<int64_t>(width), residual, addend, addend_s0, weight,
                                                  width, eps, nq::Fp8Out{});
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_prefill_embed_rmsnorm(const int64_t *text_ids, const uint16_t *text_table, int64_t text_s0,
+                                        int64_t text_rows, const int64_t *codec_ids, const uint16_t *codec_table,
+                                        int64_t codec_s0, int64_t codec_rows, const uint8_t *mask,
+                                        const uint16_t *weight, int rows, int width, float eps, uint16_t *residual,
+                                        uint16_t *out, int32_t *status, void *stream) {
+    NQ_CHECK_ARG(text_ids && text_table && codec_ids && codec_table && mask && weight && residual && out);
+    NQ_CHECK_ARG(rows >= 0 && width >= 8 && text_rows >= 1 && codec_rows >= 1 && text_s0 >= width &&
+                 codec_s0 >= width);
+    if (width % 8 || width > nq::kNormThreads * 8 * nq::kMaxVec || text_s0 % 8 || codec_s0 % 8 ||
+        !nq::al16(text_table) || !nq::al16(codec_table) || !nq::al16(residual) || !nq::al16(out))
+        return NQ_ERR_UNSUPPORTED;
+    if (rows == 0) return NQ_OK;
+    const nq::MaskedPairSrc src{nq::GatherSrc{text_table, text_s0, text_ids, text_rows, status},
+                                nq::GatherSrc{codec_table, codec_s0, codec_ids, codec_rows, status}, mask};
+    nq::launch_add_rmsnorm<nq::MaskedPairSrc, false, false>(rows, width, static_cast<hipStream_t>(stream), src, out,
+                                                             static_cast<int64_t>(width), residual, nullptr, 0,
+                                                             weight, width, eps, nq::Fp8Out{});
     return NQ_LAUNCH_STATUS();
 }
 

@@ -1,7 +1,8 @@
 """Exception types with the reference's names and meaning.
 
 KVAllocationError / StaleKVPublicationError mirror executor/cache.py:11-16,
-SlotBusyError mirrors executor/cuda_graph.py:102-103.
+SlotBusyError mirrors executor/cuda_graph.py:102-103, CaptureCoverageError
+planner/catalog.py:19-20.
 """
 
 from __future__ import annotations
@@ -16,4 +17,8 @@ class StaleKVPublicationError(RuntimeError):
 
 
 class SlotBusyError(RuntimeError):
+    pass
+
+
+class CaptureCoverageError(RuntimeError):
     pass

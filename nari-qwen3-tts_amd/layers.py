@@ -186,6 +186,49 @@ def embed_add_rmsnorm(ids: torch.Tensor, table: torch.Tensor, addend: torch.Tens
     return out
 
 
+def prefill_embed_rmsnorm(text_ids: torch.Tensor, text_table: torch.Tensor, codec_ids: torch.Tensor,
+                          codec_table: torch.Tensor, mask: torch.Tensor, weight: torch.Tensor, eps: float,
+                          residual: torch.Tensor, out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill input embedding (executor/talker.py:246-254) and the first input norm in one launch:
+    residual = where(mask, text_table[text_ids] + codec_table[codec_ids], text_table[text_ids]) (bf16),
+    out = rmsnorm(residual) * weight."""
+
+    for t, name in ((text_table, "text table"), (codec_table, "codec table"), (weight, "norm weight"),
+                    (residual, "residual"), (out, "out")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise TypeError(f"{name} must be bf16 with unit inner stride")
+    for ids, name in ((text_ids, "text_ids"), (codec_ids, "codec_ids")):
+        if ids.dtype != torch.long or ids.ndim != 1 or ids.stride(0) != 1:
+            raise TypeError(f"{name} must be a unit-stride int64 vector")
+    if mask.dtype != torch.bool or mask.ndim != 1 or mask.stride(0) != 1:
+        raise TypeError("mask must be a unit-stride bool vector")
+    rows, width = residual.shape
+    if text_ids.shape != (rows,) or codec_ids.shape != (rows,) or mask.shape != (rows,):
+        raise ValueError("ids / mask must have one entry per row")
+    if text_table.shape[1] != width or codec_table.shape[1] != width or weight.shape != (width,):
+        raise ValueError("tables / norm weight do not match the residual width")
+    if out.shape != (rows, width) or not residual.is_contiguous() or not out.is_contiguous():
+        raise ValueError("residual and out must be contiguous [rows, width]")
+    _lib.require_device(text_ids, text_table, codec_ids, codec_table, mask, weight, residual, out, status)
+    _lib.call("nq_prefill_embed_rmsnorm", text_ids.data_ptr(), text_table.data_ptr(), text_table.stride(0),
+              text_table.shape[0], codec_ids.data_ptr(), codec_table.data_ptr(), codec_table.stride(0),
+              codec_table.shape[0], mask.data_ptr(), weight.data_ptr(), rows, width, float(eps), residual.data_ptr(),
+              out.data_ptr(), _lib.ptr(status), _lib.stream(residual.device))
+    return out
+
+
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor | None = None,
+                chunk: int = 128) -> torch.Tensor:
+    """out = x @ weight.T for any number of rows: the decode-sized projection over row pieces of at
+    most ``chunk`` rows (each piece streams the weights again; the prefill buckets' projections)."""
+
+    rows = x.shape[0]
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        linear(x[r0:r1], weight, out=out[r0:r1], workspace=workspace)
+    return out
+
+
 def gather_sum_rows(first_ids: torch.Tensor, first_table: torch.Tensor, ids: torch.Tensor, tables: torch.Tensor,
                     out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
     """out[r] = first_table[first_ids[r]] + sum over g of tables[g][ids[g, r]], added in group order
@@ -526,6 +569,8 @@ __all__ = [
     "PackedLinearWeight",
     "embed_add_rmsnorm",
     "gather_sum_rows",
+    "linear_rows",
+    "prefill_embed_rmsnorm",
     "linear_fp8_swiglu",
     "pack_fp8_swiglu",
     "add_rmsnorm_fp8",

@@ -32,6 +32,7 @@ from .layers import (
     FP8,
     add_rmsnorm_fp8,
     embed_add_rmsnorm,
+    gather_sum_rows,
     linear,
     linear_add_rmsnorm,
     linear_add_rmsnorm_fp8,
@@ -41,6 +42,7 @@ from .layers import (
     linear_partials,
     linear_silu_mul,
     linear_workspace_bytes,
+    prefill_embed_rmsnorm,
     add_rmsnorm,
     silu_mul,
     quantize_fp8_weight_blocks,
@@ -105,6 +107,8 @@ class TalkerWeights:
         self.final_norm = torch.ones(c.hidden, **bf)
         self.codec_head = randn(c.vocab, c.hidden)
         self.text_embedding = randn(c.text_vocab, c.hidden)
+        # codec token embeddings (Qwen3TTSTalkerInnerModel.codec_embedding, model/components.py:71)
+        self.codec_embedding = randn(c.vocab, c.hidden)
         self.fp8_gate_up = fp8_gate_up
         for layer in self.layers:
             layer.gate_up_q, layer.gate_up_scales = (
@@ -351,4 +355,141 @@ class TalkerDecodeStep:
             sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
 
 
-__all__ = ["ReportFence", "StepReport", "TalkerConfig", "TalkerDecodeStep", "TalkerWeights", "check_step_report"]
+class TalkerPrefillStep:
+    """Static buffers and the forward of one prefill bucket: ``tokens`` packed prompt tokens of at
+    most ``rows`` requests (TalkerPrefillCaptureKey: token_capacity, capture_batch_size).
+
+    Follows the reference's captured prefill operation (executor/talker.py:397-459 with
+    materialize_prefill :246-254 and forward_logits :231-244): input embedding = text embedding
+    plus, where the codec mask is set, the codec embedding; the layer stack over every packed token
+    (causal prefill attention over the paged KV, writing each token's K/V); the final-norm hidden
+    state of each request's last token (``last`` indices); the codec head, the logit masks and the
+    sampler on those rows.  Every projection runs on the HIP skinny GEMM in pieces of at most 128
+    token rows (per-row epilogues, so a piece is a full result; the layer's weights stay resident
+    in the 256 MB Infinity Cache between pieces), with the decode step's fused epilogues and FP8
+    gate/up."""
+
+    CHUNK = 128
+
+    def __init__(self, weights: TalkerWeights, context, rows: int, tokens: int, *,
+                 workspace: torch.Tensor | None = None) -> None:
+        if rows < 1 or tokens < rows:
+            raise ValueError("a prefill bucket needs at least one row and one token per row")
+        c = weights.config
+        self.w = weights
+        self.context = context
+        self.rows = rows
+        self.tokens_capacity = tokens
+        dev = weights.codec_head.device
+        self.device = dev
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        # static inputs (the reference's _PrefillSlot text / codec / mask / last / suppress / sampling)
+        self.text_ids = torch.zeros(tokens, dtype=torch.long, device=dev)
+        self.codec_ids = torch.zeros(tokens, dtype=torch.long, device=dev)
+        self.codec_mask = torch.zeros(tokens, dtype=torch.bool, device=dev)
+        self.last = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.derive_last = True  # False: ``last`` is staged by the caller
+        self.suppress_eos = torch.ones(rows, dtype=torch.bool, device=dev)
+        self.temperature = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.top_k = torch.ones(rows, dtype=torch.int32, device=dev)
+        self.top_p = torch.ones(rows, dtype=torch.float32, device=dev)
+        self.penalty = torch.ones(rows, dtype=torch.float32, device=dev)
+        self.seed = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.offsets = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.seen = torch.zeros(rows, c.vocab, dtype=torch.bool, device=dev)
+        # work buffers
+        q_w = c.num_qo_heads * c.head_dim
+        self.residual = torch.zeros(tokens, c.hidden, **bf)
+        self.hidden = torch.zeros(tokens, c.hidden, **bf)
+        self.qkv = torch.zeros(tokens, c.qkv_width, **bf)
+        self.act = torch.zeros(tokens, c.intermediate, **bf)
+        self.last_hidden = torch.zeros(rows, c.hidden, **bf)
+        self.logits = torch.zeros(rows, c.vocab, **bf)
+        self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
+        self.fp8 = weights.fp8_gate_up
+        piece = min(tokens, self.CHUNK)
+        projections = (
+            (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
+            (c.hidden, q_w, _lib.NQ_EPI_ADD_RMSNORM),
+            (2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL),
+            (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
+        )
+        need = max(16, max(linear_workspace_bytes(piece, n, k, e) for n, k, e in projections),
+                   linear_workspace_bytes(rows, c.vocab, c.hidden, _lib.NQ_EPI_NONE))
+        if self.fp8:
+            self.act_q = torch.zeros(tokens, c.hidden, dtype=FP8, device=dev)
+            self.act_scales = torch.zeros(tokens, c.hidden // 128, dtype=torch.float32, device=dev)
+            need = max(need, linear_fp8_workspace_bytes(piece, 2 * c.intermediate, c.hidden, _lib.NQ_EPI_SILU_MUL))
+        if workspace is not None and workspace.numel() >= need:
+            self.linear_workspace = workspace
+        else:
+            self.linear_workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        self.embed_status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.report = StepReport(rows, dev)
+        # optional [layers + 1, tokens, hidden] record of the residual stream (as the decode step's)
+        self.trace: torch.Tensor | None = None
+        # the last-token gather is gather_sum_rows with no summed groups
+        self._no_ids = torch.zeros((0, rows), dtype=torch.long, device=dev)
+        self._no_tables = torch.zeros((0, 1, c.hidden), **bf)
+
+    def _pieces(self):
+        t = self.tokens_capacity
+        return [(r0, min(t, r0 + self.CHUNK)) for r0 in range(0, t, self.CHUNK)]
+
+    def forward(self) -> torch.Tensor:
+        c = self.w.config
+        ctx = self.context
+        t = self.tokens_capacity
+        ws = self.linear_workspace
+        q_w = c.num_qo_heads * c.head_dim
+        kv_w = c.num_kv_heads * c.head_dim
+        pieces = self._pieces()
+        # materialize_prefill and the first input norm, one launch
+        prefill_embed_rmsnorm(self.text_ids, self.w.text_embedding, self.codec_ids, self.w.codec_embedding,
+                              self.codec_mask, self.w.layers[0].input_norm, c.rms_eps, self.residual, self.hidden,
+                              status=self.embed_status)
+        trace = self.trace
+        if trace is not None:
+            trace[0].copy_(self.residual)
+        for index, layer in enumerate(self.w.layers):
+            ctx.select_layer(index)
+            nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
+            for a, b in pieces:
+                linear(self.hidden[a:b], layer.qkv, out=self.qkv[a:b], workspace=ws)
+            q = self.qkv[:, :q_w].view(t, c.num_qo_heads, c.head_dim)
+            k = self.qkv[:, q_w : q_w + kv_w].view(t, c.num_kv_heads, c.head_dim)
+            v = self.qkv[:, q_w + kv_w :].view(t, c.num_kv_heads, c.head_dim)
+            attended = ctx.attend(layer.attention, q, k, v).view(t, q_w)
+            for a, b in pieces:
+                if self.fp8:
+                    linear_add_rmsnorm_fp8(attended[a:b], layer.o, self.residual[a:b], layer.post_norm, c.rms_eps,
+                                           self.act_q[a:b], self.act_scales[a:b], ws)
+                    linear_fp8_swiglu(self.act_q[a:b], self.act_scales[a:b], layer.gate_up_packed,
+                                      layer.gate_up_scales, self.act[a:b], weight_q=layer.gate_up_q, workspace=ws)
+                else:
+                    linear_add_rmsnorm(attended[a:b], layer.o, self.residual[a:b], layer.post_norm, c.rms_eps,
+                                       self.hidden[a:b], ws)
+                    linear_silu_mul(self.hidden[a:b], layer.gate_up, out=self.act[a:b], workspace=ws)
+                linear_add_rmsnorm(self.act[a:b], layer.down, self.residual[a:b], nxt, c.rms_eps, self.hidden[a:b],
+                                   ws)
+            if trace is not None:
+                trace[index + 1].copy_(self.residual)
+        ctx.advance_sequence_lengths()
+        # forward_logits: the final-norm hidden state of each request's last token.  With the planner's
+        # qo_indptr on the device, last = qo_indptr[1:] - 1: the reference's host cumsum - 1 for every
+        # real row (padding rows, which hold no tokens, repeat the previous row's index), without a copy
+        qo = getattr(getattr(ctx, "buffers", None), "qo_indptr", None)
+        if qo is not None and self.derive_last:
+            torch.sub(qo[1 : self.rows + 1], 1, out=self.last)
+        gather_sum_rows(self.last, self.hidden, self._no_ids, self._no_tables, self.last_hidden,
+                        status=self.embed_status)
+        linear(self.last_hidden, self.w.codec_head, out=self.logits, workspace=ws)
+        sample_with_counter(self.logits, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
+                            repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
+                            eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
+        TalkerDecodeStep._report(self)
+        return self.tokens
+
+
+__all__ = ["ReportFence", "StepReport", "TalkerConfig", "TalkerDecodeStep", "TalkerPrefillStep", "TalkerWeights",
+           "check_step_report"]

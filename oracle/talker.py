@@ -3,7 +3,7 @@
 Restates the decode forward of the reference talker (model/components.py:
 29-90 layer loop with the fused add-norm carry, model/layers.py:296-317 QKV
 split and o-proj, executor/talker_kv.py:104-129 attend, executor/talker.py:
-231-262 embedding and codec head) over the oracle's attention, q/k RoPE,
+231-262 embeddings and codec head) over the oracle's attention, q/k RoPE,
 norm and sampler restatements.  GEMMs run in fp32 numpy on bf16-valued
 weights with bf16 rounding at the points where the GPU stores bf16, so the
 result tracks the device within bf16 tolerance.  A layer dict with
@@ -83,6 +83,16 @@ def decode_layers(
             nxt = final_norm
         hidden, res = norms.add_rmsnorm(down, res, nxt, eps)
     return hidden, res
+
+
+def prefill_embedding(text_table: np.ndarray, codec_table: np.ndarray, text_ids: np.ndarray, codec_ids: np.ndarray,
+                      mask: np.ndarray) -> np.ndarray:
+    """TalkerExecutor.materialize_prefill (executor/talker.py:246-254): the text embedding, plus the
+    codec embedding where the mask is set, added in bf16 (bf16-valued fp32 out)."""
+
+    text = text_table[text_ids].astype(np.float32)
+    both = bf16.round_f32(text + codec_table[codec_ids].astype(np.float32))
+    return np.where(np.asarray(mask, bool)[:, None], both, text)
 
 
 def logits(hidden: np.ndarray, codec_head: np.ndarray) -> np.ndarray:
