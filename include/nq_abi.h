@@ -533,6 +533,36 @@ int nq_linear_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64
                          uint16_t *out, int64_t o_s0, void *stream);
 
 /*
+ * Prefill-sized projections (the talker layer's QKV / o / gate_up / down,
+ * model/layers.py:195-317, at the prefill captures' token counts,
+ * planner/catalog.py:262-314): tiled MFMA GEMMs for any M >= 1 (128 x 128
+ * tiles, LDS-staged 64-wide K slices with two slices of global loads in
+ * flight, XCD-grouped tiles; K split into S slices when the tiles alone would
+ * leave CUs idle).  The argument meanings, epilogues and workspace rules are
+ * those of nq_linear / nq_linear_add_rmsnorm_fp8 (NQ_EPI_SILU_MUL on
+ * [gate; up] weights, NQ_EPI_PARTIALS leaving S fp32 planes [S, M, N] at the
+ * workspace start); N % 128 == 0 (I % 64 == 0 for SwiGLU), K % 64 == 0,
+ * 16-byte aligned X / W with row strides % 8 elements, else
+ * NQ_ERR_UNSUPPORTED.  nq_tgemm_splits is S (-1 for unsupported shapes);
+ * nq_tgemm_workspace_bytes is the workspace an epilogue needs.
+ *
+ * nq_tgemm_fp8_swiglu: the block-scaled FP8 gate/up + SwiGLU of
+ * nq_linear_fp8_swiglu (same codes, scales, interleaved weight rows and
+ * output) for any M; K % 128 == 0 and I % 128 == 0.
+ */
+int nq_tgemm_splits(int M, int N, int K);
+int64_t nq_tgemm_workspace_bytes(int M, int N, int K, int epilogue);
+int nq_tgemm(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K, int epilogue,
+             uint16_t *out, int64_t o_s0, uint16_t *residual, const uint16_t *norm_weight, float eps,
+             void *workspace, int64_t workspace_bytes, void *stream);
+int nq_tgemm_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
+                             uint16_t *residual, const uint16_t *norm_weight, float eps, uint8_t *xq, int64_t xq_s0,
+                             float *sx, int64_t sx_s0, void *workspace, int64_t workspace_bytes, void *stream);
+int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, int M,
+                        const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
+                        uint16_t *out, int64_t o_s0, void *stream);
+
+/*
  * Incremental codec-decoder step (fp32, channels-last [T, C]).  Replaces the
  * stateful pieces of Qwen3TTSIncrementalDecoder (model/incremental_codec.py):
  * the fresh rows of B streams are concatenated; stream b owns frames

@@ -85,6 +85,11 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_fp8": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P],
     "nq_fp8_pack_swiglu": [_P, _L, _I, _I, _P, _L, _P],
     "nq_linear_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
+    "nq_tgemm_splits": [_I, _I, _I],
+    "nq_tgemm_workspace_bytes": [_I, _I, _I, _I],
+    "nq_tgemm": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _L, _P],
+    "nq_tgemm_add_rmsnorm_fp8": [_P, _L, _P, _L, _I, _I, _I, _P, _P, _F, _P, _L, _P, _L, _P, _L, _P],
+    "nq_tgemm_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
     "nq_codec_embed_sum": [_P, _I, _I, _P, _I, _I, _P, _P, _P],
     "nq_codec_causal_conv": [_P, _L, _L, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P],
     "nq_codec_causal_transconv": [_P, _L, _L, _P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _L, _P],
@@ -101,6 +106,7 @@ _RESTYPES = {
     "nq_attention_workspace_bytes": ctypes.c_int64,
     "nq_linear_workspace_bytes": ctypes.c_int64,
     "nq_linear_fp8_workspace_bytes": ctypes.c_int64,
+    "nq_tgemm_workspace_bytes": ctypes.c_int64,
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -438,6 +438,201 @@ pack_swiglu_kernel(const uint8_t *__restrict__ q, int64_t q_s0, int I, int K, ui
             *reinterpret_cast<const uint4 *>(q + static_cast<int64_t>(src) * q_s0 + c);
 }
 
+// ---------------------------------------------------------------------------
+// Pieces of the tiled FP8 gate/up + SwiGLU below.
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));  // staging registers (a plain vector type
+                                                                    // keeps them out of scratch)
+
+// Global loads of K block kb of the X codes, the weight codes and (thread t < rows) the row scale.
+template <int XV, int WV>
+__device__ __forceinline__ void tf8_load(u32x4_t (&xr)[XV], u32x4_t (&wr)[WV], float &sr,
+                                         const uint8_t *const (&xp)[XV], const uint8_t *const (&wp)[WV],
+                                         const float *sxp, int kb, int rows) {
+#pragma unroll
+    for (int q = 0; q < WV; ++q) wr[q] = *reinterpret_cast<const u32x4_t *>(wp[q] + kb * 128);
+#pragma unroll
+    for (int q = 0; q < XV; ++q) xr[q] = *reinterpret_cast<const u32x4_t *>(xp[q] + kb * 128);
+    if (static_cast<int>(threadIdx.x) < rows) sr = sxp[kb];
+}
+
+// A register set into LDS (one plane per pass: the two planes' starts share banks).
+template <int BM, int BN, int XV, int WV>
+__device__ __forceinline__ void tf8_store(const u32x4_t (&xr)[XV], const u32x4_t (&wr)[WV], float sr, uint8_t *xs,
+                                          uint8_t *ws, float *sxs, int chunk) {
+    using XL = Fp8Lds<BM, 128>;
+    using WL = Fp8Lds<BN, 128>;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if ((chunk & 1) != h) continue;
+#pragma unroll
+        for (int q = 0; q < XV; ++q)
+            *reinterpret_cast<u32x4_t *>(xs + XL::stage_offset((threadIdx.x + q * kFp8Threads) / 8, chunk)) = xr[q];
+#pragma unroll
+        for (int q = 0; q < WV; ++q)
+            *reinterpret_cast<u32x4_t *>(ws + WL::stage_offset((threadIdx.x + q * kFp8Threads) / 8, chunk)) = wr[q];
+    }
+    if (static_cast<int>(threadIdx.x) < BM) sxs[threadIdx.x] = sr;
+}
+
+// The scaled MFMAs of one staged K block: per 16 x 16 tile one MFMA from zero, then
+// acc += t * sx[row] * (gate scale on lane columns 0, 1 | up scale on 2, 3).
+template <int MT, int NT>
+__device__ __forceinline__ void tf8_compute(floatx4_t (&acc)[MT][NT], const uint8_t *xs, const uint8_t *ws,
+                                            const float *sxs, const float *const (&swg)[NT],
+                                            const float *const (&swu)[NT], int kb, int wm, int wn, int r16, int kq) {
+    using XL = Fp8Lds<32 * MT, 128>;
+    using WL = Fp8Lds<32 * NT, 128>;
+    float gs[NT], us[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        gs[n] = swg[n][kb];
+        us[n] = swu[n][kb];
+    }
+    int8v_t a[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) a[n] = WL::read(ws, wn * 16 * NT + n * 16 + r16, 0, kq);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int row = wm * 16 * MT + m * 16 + r16;
+        const int8v_t b = XL::read(xs, row, 0, kq);
+        const float sxv = sxs[row];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const floatx4_t tt = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                a[n], b, floatx4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+            const float sg = sxv * gs[n], su = sxv * us[n];
+            acc[m][n][0] = fmaf(tt[0], sg, acc[m][n][0]);
+            acc[m][n][1] = fmaf(tt[1], sg, acc[m][n][1]);
+            acc[m][n][2] = fmaf(tt[2], su, acc[m][n][2]);
+            acc[m][n][3] = fmaf(tt[3], su, acc[m][n][3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tiled FP8 gate/up + SwiGLU for prefill-sized row counts (a prefill bucket's
+// packed prompt tokens, up to 640 rows).  A workgroup owns (32 MT) activation
+// rows x (32 NT) rows of the interleaved gate/up matrix (16 NT act columns);
+// its 2 x 2 waves a (16 MT) x (16 NT) quarter.  The K loop stages one 128-byte
+// K block -- one scale block -- of the X codes, their scales and the packed
+// weight rows per stage through LDS, double buffered, with two register stages
+// keeping the global loads of the next two blocks in flight while the MFMAs
+// run.  Per block and 16 x 16 tile: one scaled MFMA from zero, then acc += t * sx[row, kb] * sw[block, kb] with the gate scale on
+// lane columns 0, 1 and the up scale on 2, 3 -- the per-block arithmetic of the
+// decode kernels -- and the epilogue is the fused kernel's SwiGLU.
+template <int MT, int NT>
+__global__ void __launch_bounds__(kFp8Threads)
+tgemm_fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float *__restrict__ sx, int64_t sx_s0,
+                        int M, const uint8_t *__restrict__ w, int64_t w_s0, const float *__restrict__ sw,
+                        int64_t sw_s0, int I, int K, uint16_t *__restrict__ out, int64_t o_s0, int tiles_m,
+                        int tiles) {
+    constexpr int BM = 32 * MT, BN = 32 * NT;
+    using XL = Fp8Lds<BM, 128>;
+    using WL = Fp8Lds<BN, 128>;
+    constexpr int XV = BM * 8 / kFp8Threads;  // 16-byte vectors per thread and stage (8 per 128-byte row)
+    constexpr int WV = BN * 8 / kFp8Threads;
+    static_assert(XV >= 1 && WV >= 1 && BM <= kFp8Threads, "stage splits evenly over the threads");
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][XL::kBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t ws[2][WL::kBytes];
+    __shared__ float sxs[2][BM];
+
+    // tile of this workgroup: XCD b % 8 takes tiles (b % 8) * per .. + per - 1, m fastest
+    const int per = (tiles + 7) / 8;
+    const int t = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (t >= tiles) return;
+    const int tm = t % tiles_m, tn = t / tiles_m;
+    const int m0 = tm * BM, p0 = tn * BN;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int chunk = threadIdx.x & 7;  // the thread's 16-byte vector of every staged row
+
+    const uint8_t *xp[XV];
+    const uint8_t *wp[WV];
+#pragma unroll
+    for (int q = 0; q < XV; ++q) {
+        const int row = m0 + (threadIdx.x + q * kFp8Threads) / 8;
+        xp[q] = x + static_cast<int64_t>(row < M ? row : M - 1) * x_s0 + chunk * 16;
+    }
+#pragma unroll
+    for (int q = 0; q < WV; ++q)
+        wp[q] = w + static_cast<int64_t>(p0 + (threadIdx.x + q * kFp8Threads) / 8) * w_s0 + chunk * 16;
+    const int srow = m0 + static_cast<int>(threadIdx.x);
+    const float *sxp = sx + static_cast<int64_t>(srow < M ? srow : M - 1) * sx_s0;
+    // gate rows 8 pt .. of packed tile pt lie in 128-row block 8 pt / 128, up rows in (I + 8 pt) / 128
+    const float *swg[NT];
+    const float *swu[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int pt = (p0 + wn * 16 * NT + n * 16) / 16;
+        swg[n] = sw + static_cast<int64_t>(pt * 8 / 128) * sw_s0;
+        swu[n] = sw + static_cast<int64_t>((I + pt * 8) / 128) * sw_s0;
+    }
+
+    // two register stages: the global loads of two K blocks are in flight while the MFMAs run
+    u32x4_t xa[XV], wa[WV], xb[XV], wb[WV];
+    float sa = 0.f, sb = 0.f;
+
+    floatx4_t acc[MT][NT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[m][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    // block k sits in register set k % 2 (a, b) and LDS buffer k % 2.  Step k: MFMAs on buffer
+    // k % 2, block k + 1 to LDS, then the loads of block k + 3 into the set block k + 1 left free.
+    const int blocks = K / 128;
+    tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, 0, BM);
+    tf8_store<BM, BN, XV, WV>(xa, wa, sa, xs[0], ws[0], sxs[0], chunk);
+    if (blocks > 1) tf8_load<XV, WV>(xb, wb, sb, xp, wp, sxp, 1, BM);
+    if (blocks > 2) tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, 2, BM);
+    __syncthreads();
+    for (int kb = 0; kb < blocks; kb += 2) {
+        tf8_compute<MT, NT>(acc, xs[0], ws[0], sxs[0], swg, swu, kb, wm, wn, r16, kq);
+        if (kb + 1 < blocks) tf8_store<BM, BN, XV, WV>(xb, wb, sb, xs[1], ws[1], sxs[1], chunk);
+        if (kb + 3 < blocks) tf8_load<XV, WV>(xb, wb, sb, xp, wp, sxp, kb + 3, BM);
+        __syncthreads();
+        if (kb + 1 >= blocks) break;
+        tf8_compute<MT, NT>(acc, xs[1], ws[1], sxs[1], swg, swu, kb + 1, wm, wn, r16, kq);
+        if (kb + 2 < blocks) tf8_store<BM, BN, XV, WV>(xa, wa, sa, xs[0], ws[0], sxs[0], chunk);
+        if (kb + 4 < blocks) tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, kb + 4, BM);
+        __syncthreads();
+    }
+
+    // act columns 8 pt + 2 kq + {0, 1} of row m0 + wm 16 MT + 16 m + r16
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int row = m0 + wm * 16 * MT + m * 16 + r16;
+        if (row >= M) continue;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const int col = (p0 + wn * 16 * NT + n * 16) / 2 + kq * 2;
+            float a2[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float g = bf16_to_f32(f32_to_bf16(acc[m][n][e]));
+                const float u = bf16_to_f32(f32_to_bf16(acc[m][n][2 + e]));
+                a2[e] = g / (1.0f + expf(-g)) * u;
+            }
+            *reinterpret_cast<uint32_t *>(out + static_cast<int64_t>(row) * o_s0 + col) = pack2_bf16(a2[0], a2[1]);
+        }
+    }
+}
+
+template <int MT, int NT>
+int launch_tgemm_fp8_swiglu(const uint8_t *x, int64_t x_s0, const float *sx, int64_t sx_s0, int M, const uint8_t *w,
+                            int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K, uint16_t *out, int64_t o_s0,
+                            hipStream_t st) {
+    constexpr int BM = 32 * MT, BN = 32 * NT;
+    const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * (2 * I / BN);
+    hipLaunchKernelGGL((tgemm_fp8_swiglu_kernel<MT, NT>), dim3((tiles + 7) / 8 * 8), dim3(kFp8Threads), 0, st, x,
+                       x_s0, sx, sx_s0, M, w, w_s0, sw, sw_s0, I, K, out, o_s0, tiles_m, tiles);
+    return NQ_LAUNCH_STATUS();
+}
+
 constexpr int kFp8Slice = 1024;  // K bytes per workgroup slice (M <= 64)
 
 int fp8_slice_of(int M) { return M > 64 ? 512 : kFp8Slice; }
@@ -549,4 +744,21 @@ extern "C" int nq_linear_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float
     hipLaunchKernelGGL((fp8_swiglu_kernel<kSwK>), dim3(I / (8 * kSwTiles)), dim3(kSwThreads), 0,
                        static_cast<hipStream_t>(stream), xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, out, o_s0);
     return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, int M,
+                                   const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
+                                   uint16_t *out, int64_t o_s0, void *stream) {
+    NQ_CHECK_ARG(xq && sx && packed && sw && out && M > 0 && I > 0 && K > 0);
+    if (K % 128 || I % 128) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 16 == 0 && w_s0 % 16 == 0 && al16(xq) && al16(packed));
+    NQ_CHECK_ARG(sx_s0 >= K / 128 && sw_s0 >= K / 128 && o_s0 >= I && o_s0 % 2 == 0);
+    NQ_CHECK_ARG(reinterpret_cast<uintptr_t>(out) % 4 == 0);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int n128 = 2 * I / 128;
+    if ((M + 127) / 128 * n128 >= 256)
+        return launch_tgemm_fp8_swiglu<4, 4>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
+    if ((M + 63) / 64 * n128 >= 256)
+        return launch_tgemm_fp8_swiglu<2, 4>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
+    return launch_tgemm_fp8_swiglu<2, 2>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
 }

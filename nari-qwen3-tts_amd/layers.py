@@ -229,6 +229,104 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, worksp
     return out
 
 
+def tgemm_workspace_bytes(rows: int, out_features: int, in_features: int,
+                          epilogue: int = _lib.NQ_EPI_NONE) -> int:
+    """fp32 split-K planes the tiled prefill GEMM needs (0 when none); raises for shapes it does not cover."""
+
+    n = int(_lib.load().nq_tgemm_workspace_bytes(int(rows), int(out_features), int(in_features), int(epilogue)))
+    if n < 0:
+        raise TypeError(f"no tiled projection for rows={rows}, out={out_features}, in={in_features}")
+    return n
+
+
+def _tgemm_args(x, weight):
+    for t, name in ((x, "x"), (weight, "weight")):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+            raise TypeError(f"{name} must be a bf16 matrix with unit inner stride")
+    if weight.shape[1] != x.shape[1]:
+        raise ValueError("weight in_features must match x")
+    _lib.require_device(x, weight)
+    return x.shape[0], weight.shape[0], x.shape[1]
+
+
+def _workspace(ws, need, device):
+    if need and (ws is None or ws.numel() * ws.element_size() < need):
+        raise ValueError(f"the tiled projection needs a workspace of {need} bytes")
+    return (ws.data_ptr(), ws.numel() * ws.element_size()) if need else (None, 0)
+
+
+def tgemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, epilogue: int = _lib.NQ_EPI_NONE,
+          residual: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 0.0,
+          workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The tiled prefill GEMM for any number of rows, with the epilogues of ``linear``: out = x @ weight.T
+    (NQ_EPI_NONE), silu(bf16(gate)) * bf16(up) on [gate; up] weights (NQ_EPI_SILU_MUL), or
+    residual += x @ weight.T, out = rmsnorm(residual) * norm_weight (NQ_EPI_ADD_RMSNORM)."""
+
+    rows, n, k = _tgemm_args(x, weight)
+    width = n // 2 if epilogue == _lib.NQ_EPI_SILU_MUL else n
+    if out.dtype != torch.bfloat16 or out.shape != (rows, width) or out.stride(1) != 1:
+        raise ValueError(f"out must be bf16 [{rows}, {width}] with unit inner stride")
+    if epilogue == _lib.NQ_EPI_ADD_RMSNORM:
+        for t, name in ((residual, "residual"), (norm_weight, "norm weight")):
+            _check(t, name)
+        if residual.shape != (rows, n) or norm_weight.shape != (n,) or not residual.is_contiguous():
+            raise ValueError("residual / norm weight must match the projection output")
+    ws, ws_bytes = _workspace(workspace, tgemm_workspace_bytes(rows, n, k, epilogue), x.device)
+    _lib.call("nq_tgemm", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k, int(epilogue),
+              out.data_ptr(), out.stride(0), _lib.ptr(residual), _lib.ptr(norm_weight), float(eps), ws, ws_bytes,
+              _lib.stream(x.device))
+    return out
+
+
+def tgemm_partials(x: torch.Tensor, weight: torch.Tensor, workspace: torch.Tensor) -> int:
+    """The tiled GEMM leaving its fp32 split-K planes [S, rows, out] at the start of ``workspace``
+    (the layout ``linear_partials`` leaves); returns S."""
+
+    rows, n, k = _tgemm_args(x, weight)
+    ws, ws_bytes = _workspace(workspace, tgemm_workspace_bytes(rows, n, k, _lib.NQ_EPI_PARTIALS), x.device)
+    _lib.call("nq_tgemm", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n, k,
+              _lib.NQ_EPI_PARTIALS, None, 0, None, None, 0.0, ws, ws_bytes, _lib.stream(x.device))
+    return int(_lib.load().nq_tgemm_splits(rows, n, k))
+
+
+def tgemm_add_rmsnorm_fp8(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
+                          eps: float, q: torch.Tensor, scales: torch.Tensor, workspace: torch.Tensor):
+    """The tiled GEMM followed by the add-RMSNorm with the normalised rows stored as FP8 codes and
+    per-128-column scales (linear_add_rmsnorm_fp8 for any number of rows)."""
+
+    rows, n, k = _tgemm_args(x, weight)
+    for t, name in ((residual, "residual"), (norm_weight, "norm weight")):
+        _check(t, name)
+    if residual.shape != (rows, n) or norm_weight.shape != (n,):
+        raise ValueError("residual / norm weight must match the projection output")
+    q, scales = _fp8_out(rows, n, x.device, q, scales)
+    ws, ws_bytes = _workspace(workspace, tgemm_workspace_bytes(rows, n, k, _lib.NQ_EPI_ADD_RMSNORM), x.device)
+    _lib.call("nq_tgemm_add_rmsnorm_fp8", x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), rows, n,
+              k, residual.data_ptr(), norm_weight.data_ptr(), float(eps), q.data_ptr(), q.stride(0),
+              scales.data_ptr(), scales.stride(0), ws, ws_bytes, _lib.stream(x.device))
+    return q, scales
+
+
+def tgemm_fp8_swiglu(q: torch.Tensor, scales: torch.Tensor, packed: torch.Tensor, weight_scales: torch.Tensor,
+                     out: torch.Tensor) -> torch.Tensor:
+    """The tiled prefill form of linear_fp8_swiglu (same codes, scales and interleaved weights) for any
+    number of rows."""
+
+    rows, k = q.shape
+    inter = packed.shape[0] // 2
+    if q.dtype != FP8 or packed.dtype != FP8 or packed.shape[1] != k:
+        raise TypeError("FP8 codes expected")
+    if scales.shape != (rows, k // 128) or weight_scales.shape != (2 * inter // 128, k // 128):
+        raise ValueError("FP8 scales do not match")
+    if out.shape != (rows, inter) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be bf16 [{rows}, {inter}] with unit inner stride")
+    _lib.require_device(q, scales, packed, weight_scales, out)
+    _lib.call("nq_tgemm_fp8_swiglu", q.data_ptr(), q.stride(0), scales.data_ptr(), scales.stride(0), rows,
+              packed.data_ptr(), packed.stride(0), weight_scales.data_ptr(), weight_scales.stride(0), inter, k,
+              out.data_ptr(), out.stride(0), _lib.stream(q.device))
+    return out
+
+
 def gather_sum_rows(first_ids: torch.Tensor, first_table: torch.Tensor, ids: torch.Tensor, tables: torch.Tensor,
                     out: torch.Tensor, status: torch.Tensor | None = None) -> torch.Tensor:
     """out[r] = first_table[first_ids[r]] + sum over g of tables[g][ids[g, r]], added in group order
@@ -570,6 +668,11 @@ __all__ = [
     "embed_add_rmsnorm",
     "gather_sum_rows",
     "linear_rows",
+    "tgemm",
+    "tgemm_add_rmsnorm_fp8",
+    "tgemm_fp8_swiglu",
+    "tgemm_partials",
+    "tgemm_workspace_bytes",
     "prefill_embed_rmsnorm",
     "linear_fp8_swiglu",
     "pack_fp8_swiglu",

@@ -46,6 +46,11 @@ from .layers import (
     add_rmsnorm,
     silu_mul,
     quantize_fp8_weight_blocks,
+    tgemm,
+    tgemm_add_rmsnorm_fp8,
+    tgemm_fp8_swiglu,
+    tgemm_partials,
+    tgemm_workspace_bytes,
 )
 from .errors import KVAllocationError
 from .sampling import sample_with_counter, sample_with_counter_from_planes, sample_with_uniforms
@@ -364,12 +369,14 @@ class TalkerPrefillStep:
     plus, where the codec mask is set, the codec embedding; the layer stack over every packed token
     (causal prefill attention over the paged KV, writing each token's K/V); the final-norm hidden
     state of each request's last token (``last`` indices); the codec head, the logit masks and the
-    sampler on those rows.  Every projection runs on the HIP skinny GEMM in pieces of at most 128
-    token rows (per-row epilogues, so a piece is a full result; the layer's weights stay resident
-    in the 256 MB Infinity Cache between pieces), with the decode step's fused epilogues and FP8
-    gate/up."""
+    sampler on those rows.  From TILED_FROM tokens the projections are the tiled MFMA GEMMs over
+    every token (``tgemm``: QKV as split-K planes feeding the q/k norm + RoPE + K/V write, o_proj
+    and down through the add-RMSNorm that reduces their planes; FP8 gate/up + SwiGLU as
+    ``tgemm_fp8_swiglu``); smaller buckets run the decode step's skinny GEMM with its fused
+    epilogues in pieces of at most CHUNK rows."""
 
     CHUNK = 128
+    TILED_FROM = 128
 
     def __init__(self, weights: TalkerWeights, context, rows: int, tokens: int, *,
                  workspace: torch.Tensor | None = None) -> None:
@@ -407,6 +414,8 @@ class TalkerPrefillStep:
         self.logits = torch.zeros(rows, c.vocab, **bf)
         self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
         self.fp8 = weights.fp8_gate_up
+        # the tiled prefill GEMMs from TILED_FROM tokens; below, the decode GEMM in one piece
+        self.tiled = tokens >= self.TILED_FROM
         piece = min(tokens, self.CHUNK)
         projections = (
             (c.qkv_width, c.hidden, _lib.NQ_EPI_NONE),
@@ -416,6 +425,10 @@ class TalkerPrefillStep:
         )
         need = max(16, max(linear_workspace_bytes(piece, n, k, e) for n, k, e in projections),
                    linear_workspace_bytes(rows, c.vocab, c.hidden, _lib.NQ_EPI_NONE))
+        if self.tiled:
+            need = max(need, tgemm_workspace_bytes(tokens, c.qkv_width, c.hidden, _lib.NQ_EPI_PARTIALS),
+                       tgemm_workspace_bytes(tokens, c.hidden, q_w, _lib.NQ_EPI_ADD_RMSNORM),
+                       tgemm_workspace_bytes(tokens, c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM))
         if self.fp8:
             self.act_q = torch.zeros(tokens, c.hidden, dtype=FP8, device=dev)
             self.act_scales = torch.zeros(tokens, c.hidden // 128, dtype=torch.float32, device=dev)
@@ -454,6 +467,24 @@ class TalkerPrefillStep:
         for index, layer in enumerate(self.w.layers):
             ctx.select_layer(index)
             nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
+            if self.tiled:
+                # the tiled GEMMs over every token: QKV as split-K planes feeding the q/k norm + RoPE +
+                # K/V write, o_proj and down with the add-RMSNorm reducing their planes
+                splits = tgemm_partials(self.hidden, layer.qkv, ws)
+                q = self.qkv[:, :q_w].view(t, c.num_qo_heads, c.head_dim)
+                attended = ctx.attend_partials(layer.attention, ws, splits, q).view(t, q_w)
+                if self.fp8:
+                    tgemm_add_rmsnorm_fp8(attended, layer.o, self.residual, layer.post_norm, c.rms_eps, self.act_q,
+                                          self.act_scales, ws)
+                    tgemm_fp8_swiglu(self.act_q, self.act_scales, layer.gate_up_packed, layer.gate_up_scales, self.act)
+                else:
+                    tgemm(attended, layer.o, self.hidden, _lib.NQ_EPI_ADD_RMSNORM, self.residual, layer.post_norm,
+                          c.rms_eps, ws)
+                    tgemm(self.hidden, layer.gate_up, self.act, _lib.NQ_EPI_SILU_MUL)
+                tgemm(self.act, layer.down, self.hidden, _lib.NQ_EPI_ADD_RMSNORM, self.residual, nxt, c.rms_eps, ws)
+                if trace is not None:
+                    trace[index + 1].copy_(self.residual)
+                continue
             for a, b in pieces:
                 linear(self.hidden[a:b], layer.qkv, out=self.qkv[a:b], workspace=ws)
             q = self.qkv[:, :q_w].view(t, c.num_qo_heads, c.head_dim)
