@@ -563,6 +563,31 @@ int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_
                         uint16_t *out, int64_t o_s0, void *stream);
 
 /*
+ * fp32 GEMM with fused epilogues for the codec decoder (fp32 throughout,
+ * executor/build.py:91-95), replacing torch's addmm / matmul / gelu / the
+ * residual-scale adds of model/incremental_codec.py's transformer, ConvNeXt and
+ * im2col convolutions:
+ *   out[m, n] = res[m, n] + scale[n] * act(sum_k X[r(m), k] W[n, k] + bias[n])
+ * with res / scale / bias optional (NULL), act 0 (none) or 1 (GELU, erf form),
+ * r(m) = x_rows[m] when x_rows != NULL else m; out may alias res.  fp32
+ * products on MFMA.  K % 4 == 0, N % 4 == 0, 16-byte aligned operands and row
+ * strides % 4, else NQ_ERR_UNSUPPORTED.
+ *
+ * nq_row_norm: RMSNorm (b == NULL: x * rsqrt(mean(x^2) + eps) * w) or
+ * LayerNorm ((x - mean) * rsqrt(var + eps) * w + b) of fp32 rows, width % 4 ==
+ * 0 and <= 1024.
+ *
+ * nq_codec_last_rows: rows[b] = max(off[b + 1] * u - 1, 0), the row of each
+ * stream's last fresh frame at a stage with u rows per frame.
+ */
+int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, const float *w, int64_t w_s0, int M, int N, int K,
+             const float *bias, int act, const float *res, int64_t r_s0, const float *scale, float *out, int64_t o_s0,
+             void *stream);
+int nq_row_norm(const float *x, int64_t x_s0, int rows, int width, const float *w, const float *b, float eps,
+                float *out, int64_t o_s0, void *stream);
+int nq_codec_last_rows(const int32_t *off, int B, int u, int32_t *rows, void *stream);
+
+/*
  * Incremental codec-decoder step (fp32, channels-last [T, C]).  Replaces the
  * stateful pieces of Qwen3TTSIncrementalDecoder (model/incremental_codec.py):
  * the fresh rows of B streams are concatenated; stream b owns frames

@@ -85,6 +85,9 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_fp8": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P],
     "nq_fp8_pack_swiglu": [_P, _L, _I, _I, _P, _L, _P],
     "nq_linear_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
+    "nq_sgemm": [_P, _L, _P, _P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _P, _L, _P],
+    "nq_row_norm": [_P, _L, _I, _I, _P, _P, _F, _P, _L, _P],
+    "nq_codec_last_rows": [_P, _I, _I, _P, _P],
     "nq_tgemm_splits": [_I, _I, _I],
     "nq_tgemm_workspace_bytes": [_I, _I, _I, _I],
     "nq_tgemm": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _P, _F, _P, _L, _P],

@@ -36,7 +36,6 @@ from types import SimpleNamespace
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from . import _lib
 
@@ -257,10 +256,9 @@ class IncrementalCodecDecoder:
             _lib.call("nq_codec_im2col", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u,
                       self._slots.data_ptr(), _lib.ptr(hist), c_in, k, dilation, 0, a_ptr, b_ptr, cols.data_ptr(),
                       cols.stride(0), self._stream)
-            w_col = self._derived(("conv", id(w)), lambda: w.permute(0, 2, 1).reshape(c_out, k * c_in).t().contiguous())
-            out = torch.addmm(b, cols, w_col) if b is not None else cols @ w_col
-            if residual is not None:
-                out.add_(residual)
+            # weights as [c_out, k * c_in] (column tap * c_in + ci of the gathered rows)
+            w_nk = self._derived(("conv", id(w)), lambda: w.permute(0, 2, 1).reshape(c_out, k * c_in).contiguous())
+            out = self._sgemm(cols, w_nk, bias=b, res=residual)
             if k > 1:
                 _lib.call("nq_codec_history_update", x.data_ptr(), x.stride(0), self._off.data_ptr(), self._B, u,
                           self._slots.data_ptr(), hist.data_ptr(), c_in, (k - 1) * dilation, a_ptr, b_ptr,
@@ -283,14 +281,16 @@ class IncrementalCodecDecoder:
             _lib.call("nq_codec_im2col", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u_in,
                       self._slots.data_ptr(), None, c_in, 2, 1, 1, a_ptr, b_ptr, cols.data_ptr(), cols.stride(0),
                       self._stream)
-            w_t = self._derived(("tc", id(w)), lambda: w.view(c_in, c_out, 2, s).permute(2, 0, 3, 1)
-                                .reshape(2 * c_in, s * c_out).contiguous())
+            # weights as [s * c_out, 2 * c_in]: output column j * c_out + co, input column tap * c_in + ci
+            w_nk = self._derived(("tc", id(w)), lambda: w.view(c_in, c_out, 2, s).permute(3, 1, 2, 0)
+                                 .reshape(s * c_out, 2 * c_in).contiguous())
             b_s = self._derived(("tcb", id(b)), lambda: b.repeat(s).contiguous())
-            out = torch.addmm(b_s, cols, w_t).view(x.shape[0] * s, c_out)
+            out = self._sgemm(cols, w_nk, bias=b_s).view(x.shape[0] * s, c_out)
             # new overlap: each stream's last fresh frame (activated: the first half of its
             # gathered row) through the kernel's second half
-            last = (self._off[1:].long() * u_in - 1).clamp(min=0)
-            new_ov = cols.index_select(0, last)[:, :c_in] @ w_t[c_in:]
+            last = torch.empty(self._B, dtype=torch.int32, device=self.device)
+            _lib.call("nq_codec_last_rows", self._off.data_ptr(), self._B, u_in, last.data_ptr(), self._stream)
+            new_ov = self._sgemm(cols[:, :c_in], w_nk[:, c_in:], x_rows=last)
             _lib.call("nq_codec_transconv_overlap", self._off.data_ptr(), self._B, u_in, s, self._slots.data_ptr(),
                       overlap.data_ptr(), new_ov.data_ptr(), c_out, out.data_ptr(), out.stride(0), self._stream)
             return out
@@ -300,9 +300,26 @@ class IncrementalCodecDecoder:
                   c_in, c_out, a_ptr, b_ptr, out.data_ptr(), out.stride(0), self._stream)
         return out
 
-    @staticmethod
-    def _rms(x, w, eps):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+    def _sgemm(self, x, w, *, bias=None, act=0, res=None, scale=None, x_rows=None, out=None):
+        """out = res + scale * act(x[x_rows] @ w.T + bias) on the fp32 MFMA GEMM (fp32 row-major x and
+        w [N, K] with unit inner strides; the optional pieces are left out when None)."""
+
+        rows = x.shape[0] if x_rows is None else x_rows.shape[0]
+        n, k = w.shape
+        if out is None:
+            out = torch.empty(rows, n, dtype=torch.float32, device=self.device)
+        _lib.call("nq_sgemm", x.data_ptr(), x.stride(0), _lib.ptr(x_rows), w.data_ptr(), w.stride(0), rows, n, k,
+                  _lib.ptr(bias), int(act), _lib.ptr(res), res.stride(0) if res is not None else 0, _lib.ptr(scale),
+                  out.data_ptr(), out.stride(0), self._stream)
+        return out
+
+    def _norm(self, x, w, eps, b=None):
+        """RMSNorm (b None) or LayerNorm of fp32 rows, one launch."""
+
+        out = torch.empty_like(x)
+        _lib.call("nq_row_norm", x.data_ptr(), x.stride(0), x.shape[0], x.shape[1], w.data_ptr(), _lib.ptr(b),
+                  float(eps), out.data_ptr(), out.stride(0), self._stream)
+        return out
 
     # -- the reference's call: state objects in, waveform out ---------------------------------
     def reference_keys(self) -> tuple[dict[str, str], dict[str, str]]:
@@ -504,22 +521,22 @@ class IncrementalCodecDecoder:
         # transformer (model/incremental_codec.py:193-381)
         hd = c.heads * c.head_dim
         r = c.retained_context
-        h = torch.addmm(w.in_b, x, w.in_w.t())
+        h = self._sgemm(x, w.in_w, bias=w.in_b)
         att = torch.empty(T, hd, dtype=torch.float32, device=dev)
         for li, L in enumerate(w.tf):
-            y = self._rms(h, L.ln1, c.eps)
-            qkv = y @ L.wqkv.t()
+            y = self._norm(h, L.ln1, c.eps)
+            qkv = self._sgemm(y, L.wqkv)
             q, k, v = qkv[:, :hd], qkv[:, hd: 2 * hd], qkv[:, 2 * hd:]
             _lib.call("nq_codec_window_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), qkv.stride(0), T, c.heads,
                       c.head_dim, L.qn.data_ptr(), L.kn.data_ptr(), float(c.eps), float(c.theta), self._off.data_ptr(),
                       B, self._slots.data_ptr(), pool.frame_pos.data_ptr(), pool.ctx.data_ptr(), pool.k[li].data_ptr(),
                       pool.v[li].data_ptr(), pool.k.stride(1), r, c.window, att.data_ptr(), att.stride(0), self._stream)
-            h = h + (att @ L.wo.t()) * L.ls1
-            y = self._rms(h, L.ln2, c.eps)
-            h = h + (F.gelu(y @ L.w1.t()) @ L.w2.t()) * L.ls2
+            self._sgemm(att, L.wo, scale=L.ls1, res=h, out=h)
+            y = self._norm(h, L.ln2, c.eps)
+            self._sgemm(self._sgemm(y, L.w1, act=1), L.w2, scale=L.ls2, res=h, out=h)
         _lib.call("nq_codec_advance", self._off.data_ptr(), B, self._slots.data_ptr(), pool.frame_pos.data_ptr(),
                   pool.ctx.data_ptr(), r, self._stream)
-        x = torch.addmm(w.out_b, self._rms(h, w.out_norm, c.eps), w.out_w.t())
+        x = self._sgemm(self._norm(h, w.out_norm, c.eps), w.out_w, bias=w.out_b)
 
         # upsample: causal transconv + ConvNeXt
         u = 1
@@ -527,9 +544,9 @@ class IncrementalCodecDecoder:
             x = self._transconv(x, u, s, f"up{ui}.tc", U.tc_w, U.tc_b)
             u *= s
             y = self._conv(x, u, f"up{ui}.dw", U.dw_w, U.dw_b, groups=c.dim)
-            y = F.layer_norm(y, (c.dim,), U.ln_w, U.ln_b, 1e-6)
-            y = torch.addmm(U.pw2_b, F.gelu(torch.addmm(U.pw1_b, y, U.pw1_w.t())), U.pw2_w.t())
-            x = x + U.gamma * y
+            y = self._norm(y, U.ln_w, 1e-6, U.ln_b)
+            self._sgemm(self._sgemm(y, U.pw1_w, bias=U.pw1_b, act=1), U.pw2_w, bias=U.pw2_b, scale=U.gamma, res=x,
+                        out=x)
         # decoder blocks
         x = self._conv(x, u, "dec0", w.dec0_w, w.dec0_b)
         for bi, (s, Bk) in enumerate(zip(c.dec_strides, w.blocks)):
