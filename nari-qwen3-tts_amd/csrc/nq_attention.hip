@@ -1688,18 +1688,19 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Prefill rows on MFMA (head dim 128, two query heads per kv head).  A
 // workgroup takes one 32-query tile of a row and one kv head; wave w owns 16
 // queries (w & 1) of query head 2h + (w >> 1).  Per 64-key tile the workgroup
-// stages K ([key][d]) and V transposed ([d][key]) in LDS; each wave computes
-// S = Q K^T with v_mfma_f32_16x16x32_bf16 (Q held in registers as the A
-// operand), masks bottom-right causal limits, runs the online softmax in the
+// stages K and V as they sit in the cache ([key][d], 16-byte stores); each wave
+// computes S = Q K^T with v_mfma_f32_16x16x32_bf16 (Q held in registers as the
+// A operand), masks bottom-right causal limits, runs the online softmax in the
 // exp2 domain on the MFMA output layout (a row's 16 columns sit in 16 lanes),
 // stores P as bf16 in its LDS slice and accumulates O += P V with a second
-// MFMA chain.  Keys past the tile's last query limit are never loaded.  V^T
-// rows keep their 8-key chunks XOR-swizzled by (d >> 3) & 7, which spreads the
-// transposing writes over the banks while each MFMA operand read stays one
-// contiguous 16-byte chunk.
+// MFMA chain whose V operand comes from gfx950's transposing LDS read
+// (ds_read_b64_tr_b16: four keys of one column per lane and instruction), so
+// V is never transposed on the way in.  Keys past the tile's last query limit
+// are never loaded.
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_floatx4 __attribute__((ext_vector_type(4)));
+typedef short pf_v4i16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ pf_bf16x8 pf_as_bf16x8(const uint4 &v) {
     pf_bf16x8 r;
@@ -1723,11 +1724,11 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                     int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
                     int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
                     int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
-    constexpr int KP = D + 8;        // K row pitch (bf16)
-    constexpr int VP = kPrefK + 8;   // V^T / P row pitch (bf16)
+    constexpr int KP = D + 8;        // K and V row pitch (bf16)
+    constexpr int VP = kPrefK + 8;   // P row pitch (bf16)
     constexpr int DT = D / 16;       // 16-wide output column tiles
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[D * VP];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kPrefK * KP];
     __shared__ __attribute__((aligned(16))) uint16_t pbuf[kWaves * 16 * VP];
     __shared__ int pages[kPrefPages];
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
@@ -1819,12 +1820,7 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 const int e = threadIdx.x + v * kAttnThreads;
                 const int key = e / (D / 8), c8 = e - key * (D / 8);
                 *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kr[v];
-                const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vr[v]);
-                // rows d = c8*8 + j; 8-key chunks swizzled by (d >> 3) & 7 == c8 & 7 so the lanes
-                // of one key (consecutive c8) land on different banks
-                const int pos = (((key >> 3) ^ (c8 & 7)) << 3) + (key & 7);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) vt[(c8 * 8 + j) * VP + pos] = v16[j];
+                *reinterpret_cast<uint4 *>(vs + key * KP + c8 * 8) = vr[v];
             }
             __syncthreads();
             if (kt0 + kPrefK < n_keys) issue(kt0 + kPrefK);
@@ -1871,17 +1867,26 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha[i];
-            __syncthreads();  // P visible to the whole wave (and V^T already staged)
+            __syncthreads();  // P visible to the whole wave (and V already staged)
+            // O += P V with V read in its staged [key][d] layout by transposing LDS reads: lane s of
+            // lane group kq points at key kh*32 + 8 kq + 4 half + s / 4, columns dt*16 + 4 (s % 4) .. + 3,
+            // and ds_read_b64_tr_b16 hands lane j the four keys of column dt*16 + j (the MFMA's B
+            // operand: keys 8 kq .. 8 kq + 7 of one output column)
+            const uint16_t *vrow = vs + (kq * 8 + (r16 >> 2)) * KP + 4 * (r16 & 3);
 #pragma unroll
             for (int kh = 0; kh < kPrefK / 32; ++kh) {
                 const uint4 pa = *reinterpret_cast<const uint4 *>(pw + r16 * VP + kh * 32 + kq * 8);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    const int d = dt * 16 + r16;
-                    const uint4 vb =
-                        *reinterpret_cast<const uint4 *>(vt + d * VP + (((kh * 4 + kq) ^ ((d >> 3) & 7)) << 3));
-                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(pa), pf_as_bf16x8(vb), acc[dt],
-                                                                       0, 0, 0);
+                    const uint16_t *vp = vrow + kh * 32 * KP + dt * 16;
+                    const pf_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (pf_v4i16 __attribute__((address_space(3))) *)(vp));
+                    const pf_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (pf_v4i16 __attribute__((address_space(3))) *)(vp + 4 * KP));
+                    pf_bf16x8 vb;
+                    __builtin_memcpy(&vb, &lo, 8);
+                    __builtin_memcpy(reinterpret_cast<char *>(&vb) + 8, &hi, 8);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(pa), vb, acc[dt], 0, 0, 0);
                 }
             }
         }
