@@ -54,36 +54,67 @@ class KVPublicationProposal:
     length: int
 
 
+class _ReservedRows:
+    """What one reservation decided, shared by its rows' publications (row i of each field)."""
+
+    __slots__ = ("ledger", "request_ids", "serial", "priors", "taken", "lo", "hi", "advances")
+
+    def __init__(self, ledger, request_ids, serial, priors, taken, lo, hi, advances) -> None:
+        self.ledger, self.request_ids, self.serial, self.priors = ledger, request_ids, serial, priors
+        self.taken, self.lo, self.hi, self.advances = taken, lo, hi, advances
+
+
 class PendingKVPublication:
     """One row of a reservation: publish() commits it, discard() gives its new pages back.  The
     ledger keeps this object as the request's in-flight entry; it stays live while it is that
-    entry and the request's committed state is still the one it was made against."""
+    entry and the request's committed state is still the one it was made against.  The row's
+    fields (request_id, token, prior_version, sequence_advance, page_indices) are read from the
+    reservation it belongs to."""
 
-    __slots__ = ("_ledger", "request_id", "token", "prior_version", "sequence_advance", "_prior", "_advance",
-                 "_taken", "_lo", "_hi", "_pages")
+    __slots__ = ("_rows", "_i", "_pages")
 
-    def __init__(self, ledger: "PagedKVAllocator", request_id: str, token: int, prior: RequestKVState,
-                 taken: np.ndarray, lo: int, hi: int, advance: int) -> None:
-        self._ledger = ledger
-        self.request_id = request_id
-        self.token = token
-        self.prior_version = prior.version
-        self.sequence_advance = advance
-        self._prior = prior
-        self._advance = advance
-        self._taken, self._lo, self._hi = taken, lo, hi
+    def __init__(self, rows: _ReservedRows, i: int) -> None:
+        self._rows = rows
+        self._i = i
         self._pages: tuple[int, ...] | None = None
 
     @property
+    def _ledger(self) -> "PagedKVAllocator":
+        return self._rows.ledger
+
+    @property
+    def request_id(self) -> str:
+        return self._rows.request_ids[self._i]
+
+    @property
+    def token(self) -> int:
+        return self._rows.serial + self._i + 1
+
+    @property
+    def _prior(self) -> RequestKVState:
+        return self._rows.priors[self._i]
+
+    @property
+    def prior_version(self) -> int:
+        return self._rows.priors[self._i].version
+
+    @property
+    def sequence_advance(self) -> int:
+        return self._rows.advances[self._i]
+
+    _advance = sequence_advance
+
+    @property
     def new_pages(self) -> np.ndarray:
-        return self._taken[self._lo: self._hi]
+        r = self._rows
+        return r.taken[r.lo[self._i]: r.hi[self._i]]
 
     @property
     def page_indices(self) -> tuple[int, ...]:
         """The request's pages if published: its committed pages, then the new ones."""
 
         if self._pages is None:
-            self._pages = self._prior.page_indices + tuple(self._taken[self._lo: self._hi].tolist())
+            self._pages = self._prior.page_indices + tuple(self.new_pages.tolist())
         return self._pages
 
     def proposal(self) -> KVPublicationProposal:
@@ -170,7 +201,8 @@ class PagedKVAllocator:
 
     def _take_front(self, count: int) -> np.ndarray:
         self._merge_returns()
-        taken = self._free[self._front: self._front + count]
+        # a copy: the consumed front of the array is reused when pages below it come back
+        taken = self._free[self._front: self._front + count].copy()
         self._front += count
         if count:
             self._log.append(("take", count))
@@ -188,14 +220,27 @@ class PagedKVAllocator:
         ret = self._returning[0] if len(self._returning) == 1 else np.concatenate(self._returning)
         self._returning = []
         ret = np.sort(ret.astype(np.int32, copy=False))
-        live = self._free[self._front:]
-        at = np.searchsorted(live, ret)
-        if (ret.shape[0] > 1 and np.any(ret[1:] == ret[:-1])) or (
-                live.shape[0] and np.any(live[np.minimum(at, live.shape[0] - 1)] == ret)):
+        m = ret.shape[0]
+        if m > 1 and np.any(ret[1:] == ret[:-1]):
             raise RuntimeError("a KV page was returned while already free")
-        self._free = np.insert(live, at, ret)
-        self._front = 0
+        live = self._free[self._front:]
+        if m <= self._front and (live.shape[0] == 0 or ret[-1] < live[0]):
+            # every returned page sorts below the free list (a discard of recent reservations, which
+            # took the lowest pages): they go back into the consumed front, no copy of the list
+            self._front -= m
+            self._free[self._front: self._front + m] = ret
+        else:
+            at = np.searchsorted(live, ret)
+            if live.shape[0] and np.any(live[np.minimum(at, live.shape[0] - 1)] == ret):
+                raise RuntimeError("a KV page was returned while already free")
+            self._free = np.insert(live, at, ret)
+            self._front = 0
         self._log.append(("return", ret))
+
+    def has_log(self) -> bool:
+        """Whether the free list changed since the last drain (taken pages or pending returns)."""
+
+        return bool(self._log or self._returning)
 
     def drain_log(self) -> list[tuple[str, object]]:
         """The free-list changes since the last drain, in order (for the device copy)."""
@@ -279,17 +324,21 @@ class PagedKVAllocator:
         except KeyError as missing:
             raise KeyError(f"unknown Talker KV request {missing.args[0]!r}") from None
 
-    def reserve(self, request_ids: tuple[str, ...], advances: tuple[int, ...]) -> KVReservation:
+    def reserve(self, request_ids: tuple[str, ...], advances: tuple[int, ...],
+                slots: np.ndarray | None = None) -> KVReservation:
+        """``slots``: the rows' ledger slots when the caller has already looked them up."""
+
         rows = len(request_ids)
         if not rows or rows != len(advances):
             raise ValueError("KV reservation rows must be non-empty and aligned")
         if len(set(request_ids)) != rows:
             raise ValueError("KV reservation request rows must be unique")
-        slots = self.slots(request_ids)
+        if slots is None:
+            slots = self.slots(request_ids)
         if not self._inflight.keys().isdisjoint(request_ids):
             busy = next(r for r in request_ids if r in self._inflight)
             raise SlotBusyError(f"request {busy!r} KV is already in flight")
-        if any(isinstance(a, bool) or not isinstance(a, int) or a < 1 for a in advances):
+        if not set(map(type, advances)) <= {int} or min(advances) < 1:
             raise ValueError("KV sequence advances must be positive integers")
         adv = np.asarray(advances, dtype=np.int64)
         ps = self.page_size
@@ -306,27 +355,45 @@ class PagedKVAllocator:
         hi = end.tolist()
         serial = self._serial
         self._serial += rows
-        states, inflight = self._states, self._inflight
-        publications = tuple(
-            PendingKVPublication(self, rid, serial + i + 1, states[rid], taken, lo[i], hi[i], advances[i])
-            for i, rid in enumerate(request_ids)
-        )
-        inflight.update(zip(request_ids, publications))
+        states = self._states
+        batch = _ReservedRows(self, tuple(request_ids), serial, [states[rid] for rid in request_ids], taken, lo, hi,
+                              tuple(advances))
+        publications = tuple(map(PendingKVPublication, [batch] * rows, range(rows)))
+        self._inflight.update(zip(request_ids, publications))
         return KVReservation(publications, int(end[-1]))
 
     def _live(self, publication: PendingKVPublication) -> None:
         """StaleKVPublicationError unless ``publication`` is its request's in-flight entry and the
         request's committed state is still the one the reservation was made against."""
 
-        rid = publication.request_id
-        if (
-            self._inflight.get(rid) is not publication
-            or self._states.get(rid) is not publication._prior
-            or publication.prior_version != publication._prior.version
-            or publication.sequence_advance != publication._advance
-            or publication.sequence_advance < 1
-        ):
+        rows, i = publication._rows, publication._i
+        rid = rows.request_ids[i]
+        if self._inflight.get(rid) is not publication or self._states.get(rid) is not rows.priors[i]:
             raise StaleKVPublicationError(_STALE)
+
+    def discard_all(self, publications) -> None:
+        """Discard each publication in order, as ``discard()`` on each would (a stale one raises
+        after the ones before it are discarded); the pages of consecutive rows of one reservation
+        go back in one piece."""
+
+        inflight, states = self._inflight, self._states
+        run, lo, hi = None, 0, 0
+        try:
+            for publication in publications:
+                rows, i = publication._rows, publication._i
+                rid = rows.request_ids[i]
+                if inflight.get(rid) is not publication or states.get(rid) is not rows.priors[i]:
+                    raise StaleKVPublicationError(_STALE)
+                del inflight[rid]
+                if rows is run and rows.lo[i] == hi:
+                    hi = rows.hi[i]
+                    continue
+                if run is not None and hi > lo:
+                    self._give_back(run.taken[lo:hi])
+                run, lo, hi = rows, rows.lo[i], rows.hi[i]
+        finally:
+            if run is not None and hi > lo:
+                self._give_back(run.taken[lo:hi])
 
     def _settle(self, publication: PendingKVPublication, *, commit: bool) -> None:
         self._live(publication)

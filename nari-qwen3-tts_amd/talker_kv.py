@@ -60,6 +60,10 @@ class _MetadataBuffers:
         self.write_pages = torch.zeros(tokens, **i64)
         self.write_offsets = torch.zeros(tokens, **i64)
         self.status = torch.zeros(2, **i32)
+        # device addresses of the planner outputs (the buffers live as long as the binding)
+        self.ptrs = tuple(0 if t is None else t.data_ptr() for t in (
+            self.qo_indptr, self.kv_indptr, self.kv_indices, self.last_page_len, self.position_ids, self.write_pages,
+            self.write_offsets, self.status))
 
 
 class _HipBindingBase:
@@ -150,16 +154,16 @@ class _HipBindingBase:
         if not self.prefill and metadata.qo_indptr is not None:
             raise ValueError("Talker decode cannot contain packed query metadata")
         self._stage(metadata)
-        b = self.buffers
+        bp = self.buffers.ptrs
         _lib.call(
             "nq_attention_plan",
-            _lib.ptr(b.qo_indptr),
-            _lib.ptr(b.kv_indptr),
-            _lib.ptr(b.last_page_len),
-            _lib.ptr(b.kv_indices),
-            _lib.ptr(b.position_ids),
-            _lib.ptr(b.write_pages),
-            _lib.ptr(b.write_offsets),
+            bp[0] or None,
+            bp[1],
+            bp[3],
+            bp[2],
+            bp[4],
+            bp[5],
+            bp[6],
             self.capture_batch_size,
             self.token_capacity,
             self.index_capacity,
@@ -304,23 +308,28 @@ class _PinnedRing:
     def __init__(self, shape: tuple[int, ...], device, depth: int = 4) -> None:
         self.host = [torch.zeros(shape, dtype=torch.int32, pin_memory=True) for _ in range(depth)]
         self.view = [h.numpy() for h in self.host]
-        self.events: list[torch.cuda.Event | None] = [None] * depth
+        self.events = [torch.cuda.Event() for _ in range(depth)]
+        self.used = [False] * depth
         self.next = 0
 
     def acquire(self) -> tuple[int, np.ndarray]:
         i = self.next
         self.next = (i + 1) % len(self.host)
-        if self.events[i] is not None:
+        if self.used[i]:
             self.events[i].synchronize()
         return i, self.view[i]
 
-    def send(self, i: int, dst: torch.Tensor, count: int) -> None:
-        """Copy the first ``count`` elements (along dim -1) of buffer i to ``dst``."""
+    def send(self, i: int, dst: torch.Tensor, count: int, stream: torch.cuda.Stream | None = None) -> None:
+        """Copy the first ``count`` elements (along dim -1) of buffer i to ``dst`` on the current stream
+        (``stream``, when the caller already holds it)."""
 
-        dst[..., :count].copy_(self.host[i][..., :count], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self.events[i] = ev
+        src = self.host[i]
+        if count == src.shape[-1] and dst.shape == src.shape:
+            dst.copy_(src, non_blocking=True)
+        else:
+            dst[..., :count].copy_(src[..., :count], non_blocking=True)
+        self.events[i].record(stream)
+        self.used[i] = True
 
 
 class PagedTalkerKV:
@@ -389,11 +398,15 @@ class PagedTalkerKV:
         self.allocator.resend_free_list = True
 
     # -- the device free list ---------------------------------------------------
-    def _sync_free_list(self) -> None:
-        """Bring the device free list to the ledger's: replay its log of takes and returns."""
+    def _sync_free_list(self, current: torch.cuda.Stream | None = None) -> None:
+        """Bring the device free list to the ledger's: replay its log of takes and returns (on the
+        current stream, ``current`` when the caller already holds it)."""
 
         a = self.allocator
-        stream = _lib.stream(self.device)
+        if not a.resend_free_list and not a.has_log():
+            return
+        current = current if current is not None else torch.cuda.current_stream(self.device)
+        stream = current.cuda_stream
         if a.resend_free_list:
             a.resend_free_list = False
             a.drain_log()
@@ -401,7 +414,7 @@ class PagedTalkerKV:
             i, buf = self._pages_ring.acquire()
             buf[: free.shape[0]] = free
             self._free_cur = 0
-            self._pages_ring.send(i, self._free_dev[0], free.shape[0])
+            self._pages_ring.send(i, self._free_dev[0], free.shape[0], current)
             self._free_front, self._free_len = 0, int(free.shape[0])
             return
         returned: list[np.ndarray] = []
@@ -415,7 +428,7 @@ class PagedTalkerKV:
                 i, buf = self._pages_ring.acquire()
                 m = int(pages.shape[0])
                 buf[:m] = pages
-                self._pages_ring.send(i, self._returned_dev, m)
+                self._pages_ring.send(i, self._returned_dev, m, current)
                 src = self._free_dev[self._free_cur]
                 dst = self._free_dev[1 - self._free_cur]
                 live = self._free_len - self._free_front
@@ -534,19 +547,21 @@ class PagedTalkerKV:
             raise ValueError("Talker request rows do not fit the capture")
         if sum(advances) + (0 if prefill else capture_rows - n) > token_capacity:
             raise ValueError("Talker KV metadata exceeds the captured token capacity")
-        self._sync_free_list()
+        current = torch.cuda.current_stream(self.device)
+        self._sync_free_list(current)
         a = self.allocator
         slots = a.slots(request_ids)
         if self._rows_ring is None or self._rows_ring.view[0].shape[1] < capture_rows:
             self._rows_ring = _PinnedRing((5, max(capture_rows, 64)), self.device)
             self._rows_dev = torch.zeros((5, max(capture_rows, 64)), dtype=torch.int32, device=self.device)
+            self._rows_ptrs = tuple(self._rows_dev[k].data_ptr() for k in range(5))
         # the rows' committed numbers, read before the reservation (it does not change them)
         i, rows = self._rows_ring.acquire()
         rows[0, :n] = a.length[slots]
         rows[1, :n] = a.position[slots]
         rows[3, :n] = a.page_count[slots]
         rows[4, :n] = slots
-        reservation = a.reserve(request_ids, advances)
+        reservation = a.reserve(request_ids, advances, slots)
         publications = reservation.publications
         try:
             rows[2, :n] = advances
@@ -561,21 +576,19 @@ class PagedTalkerKV:
                     device=self.device,
                 )
             staged = self._rows_dev
-            self._rows_ring.send(i, staged, staged.shape[1])  # the whole (small, contiguous) block
+            self._rows_ring.send(i, staged, staged.shape[1], current)  # the whole (small, contiguous) block
             free = self._free_dev[self._free_cur]
             # the planner takes this reservation's pages from the current front; the ledger logged
             # the take, and the next sync moves the device front past them
+            rp, bp = self._rows_ptrs, buffers.ptrs
             _lib.call(
                 "nq_plan_ragged",
-                staged[0].data_ptr(), staged[1].data_ptr(), staged[2].data_ptr(), staged[3].data_ptr(),
-                staged[4].data_ptr(), n, capture_rows, token_capacity, self.page_size,
+                rp[0], rp[1], rp[2], rp[3], rp[4], n, capture_rows, token_capacity, self.page_size,
                 int(prefill), self._table.data_ptr(), self._table.stride(0),
                 free.data_ptr() + 4 * self._free_front, self._free_len - self._free_front,
                 self._scratch_dev.data_ptr(), len(self._scratch_pages),
-                _lib.ptr(buffers.qo_indptr), buffers.kv_indptr.data_ptr(), buffers.kv_indices.data_ptr(),
-                buffers.kv_indices.numel(), buffers.last_page_len.data_ptr(),
-                buffers.position_ids.data_ptr(), buffers.write_pages.data_ptr(),
-                buffers.write_offsets.data_ptr(), buffers.status.data_ptr(), 0, _lib.stream(self.device),
+                bp[0] or None, bp[1], bp[2], buffers.kv_indices.numel(), bp[3], bp[4], bp[5], bp[6], bp[7], 0,
+                current.cuda_stream,
             )
             total_pages = int(a.page_count[slots].sum()) + reservation.pages_taken + (capture_rows - n)
             metadata = TalkerAttentionMetadata(
@@ -653,6 +666,16 @@ class PagedTalkerKV:
 
     @staticmethod
     def abort(publications) -> None:
+        """Discard every publication (in order; the ledger returns each reservation's pages in one
+        piece when its rows come together)."""
+
+        publications = tuple(publications)
+        if not publications:
+            return
+        ledger = publications[0]._ledger
+        if all(p._rows.ledger is ledger for p in publications):
+            ledger.discard_all(publications)
+            return
         for publication in publications:
             publication.discard()
 
