@@ -28,6 +28,7 @@
 // BatchPrefillWithPagedKVCacheWrapper(causal=True) (talker_kv.py:218) and the
 // short-cache kernel of model/kernels.py:408-463.
 #include <mutex>
+#include <type_traits>
 
 #include "nq_common.h"
 #include "nq_internal.h"
@@ -50,7 +51,7 @@ constexpr int kPlanGrid = 8;
 enum MetaSlot {
     kMetaChunks = 0, kMetaChunkTok = 1, kMetaStatus = 2, kMetaQueries = 3,
     kMetaDecRows = 4, kMetaBlocks = 5, kMetaPTiles = 6, kMetaPieces = 7, kMetaBinSlots = 8,
-    kMetaSplitRows = 9, kMetaCount = 16
+    kMetaSplitRows = 9, kMetaPItems = 10, kMetaCount = 16
 };
 
 // Decode bins: the fused decode kernel runs kBinWgs workgroups of kBinWaves
@@ -72,6 +73,12 @@ __host__ __device__ inline int bins_per_head(int num_kv_heads) {
 constexpr int kPrefQ = 32;
 constexpr int kPrefK = 64;
 constexpr int kPrefPages = 1024;  // page ids of one prefill item kept in LDS
+// A tile whose causal key range spans more than kPrefPieceTiles 64-key tiles is
+// cut into up to kPrefMaxPieces pieces of whole key tiles, one workgroup each;
+// the last piece to finish merges them.
+constexpr int kPrefPieceTiles = 16;
+constexpr int kPrefMaxPieces = 4;
+constexpr int kPrefDepth = 2;  // 64-key tiles whose K/V loads are in flight (1 or 2)
 
 // Prefill chunk descriptor.
 struct alignas(16) ChunkDesc {
@@ -90,8 +97,9 @@ struct alignas(16) ChunkDesc {
 
 struct PlanLayout {
     int64_t meta, chunk_indptr, desc, part_ml, part_o;
-    int64_t dec_rows, blocks, spart_ml, spart_o, ptiles, pieces, bins, piece_ml, piece_o, arrivals, total;
-    int64_t max_chunks, max_blocks, max_slots, max_ptiles, max_pieces;
+    int64_t dec_rows, blocks, spart_ml, spart_o, pitems, pieces, bins, piece_ml, piece_o, arrivals, tile_arrivals;
+    int64_t total;
+    int64_t max_chunks, max_blocks, max_slots, max_ptiles, max_pitems, max_pieces;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -105,25 +113,46 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     L.max_blocks = static_cast<int64_t>(max_pages) * (page_size > kBlockTok ? page_size / kBlockTok : 1) + T;
     L.max_slots = kStreamWaves + static_cast<int64_t>(Hkv) * T;
     L.max_ptiles = (static_cast<int64_t>(T) + kPrefQ - 1) / kPrefQ + kPlanThreads;
+    L.max_pitems = L.max_ptiles * kPrefMaxPieces;
     L.max_pieces = static_cast<int64_t>(T) + bins_per_head(Hkv);
+    // the chunk kernel's per-chunk partials, or (head dim 128, two query heads per
+    // kv head) the prefill tiles' per-(query, piece) partials, whichever is larger
+    const int64_t part_rows = L.max_chunks > static_cast<int64_t>(T) * kPrefMaxPieces
+                                  ? L.max_chunks : static_cast<int64_t>(T) * kPrefMaxPieces;
     int64_t off = 0;
     L.meta = off;         off = align256(off + kMetaCount * 4);
     L.chunk_indptr = off; off = align256(off + (static_cast<int64_t>(T) + 1) * 4);
     L.desc = off;         off = align256(off + L.max_chunks * static_cast<int64_t>(sizeof(ChunkDesc)));
-    L.part_ml = off;      off = align256(off + L.max_chunks * Hq * 2 * 4);
-    L.part_o = off;       off = align256(off + L.max_chunks * Hq * D * 4);
+    L.part_ml = off;      off = align256(off + part_rows * Hq * 2 * 4);
+    L.part_o = off;       off = align256(off + part_rows * Hq * D * 4);
     L.dec_rows = off;     off = align256(off + static_cast<int64_t>(T) * 16);
     L.blocks = off;       off = align256(off + L.max_blocks * 16);
     L.spart_ml = off;     off = align256(off + L.max_slots * G * 2 * 4);
     L.spart_o = off;      off = align256(off + L.max_slots * G * D * 4);
-    L.ptiles = off;       off = align256(off + L.max_ptiles * 16);
+    L.pitems = off;       off = align256(off + L.max_pitems * 32);
     L.pieces = off;       off = align256(off + L.max_pieces * 16);
     L.bins = off;         off = align256(off + static_cast<int64_t>(bins_per_head(Hkv)) * kBinMaxSlots * 48);
     L.piece_ml = off;     off = align256(off + L.max_pieces * Hq * 2 * 4);
     L.piece_o = off;      off = align256(off + L.max_pieces * Hq * D * 4);
     L.arrivals = off;     off = align256(off + static_cast<int64_t>(T) * Hkv * 4);
+    L.tile_arrivals = off; off = align256(off + L.max_ptiles * Hkv * 4);
     L.total = off;
     return L;
+}
+
+// Prefill tile t of a row with kv_len keys and qo_len queries covers keys
+// [0, kv_len - qo_len + 32 t + nq) (bottom-right causal); its 64-key tiles,
+// and the pieces they are cut into.
+__device__ __forceinline__ int pref_tile_keys(int kv_len, int qo_len, int t) {
+    const int nq = qo_len - t * kPrefQ < kPrefQ ? qo_len - t * kPrefQ : kPrefQ;
+    const int n_keys = kv_len - qo_len + t * kPrefQ + nq;
+    return n_keys > 0 ? n_keys : 0;
+}
+
+__device__ __forceinline__ int pref_pieces(int n_keys) {
+    const int n_kt = (n_keys + kPrefK - 1) / kPrefK;
+    const int k = (n_kt + kPrefPieceTiles - 1) / kPrefPieceTiles;
+    return k < 1 ? 1 : (k > kPrefMaxPieces ? kPrefMaxPieces : k);
 }
 
 __device__ int plan_block_scan(int v, int *tmp, int *total) {
@@ -171,7 +200,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     __shared__ int s_boff[kPlanThreads];
     __shared__ int s_dec[kPlanThreads];
     __shared__ unsigned long long s_cand[8];
-    __shared__ int s_tmp[3 * (kWave + 1)];
+    __shared__ int s_tmp[4 * (kWave + 1)];
     __shared__ __attribute__((aligned(16))) unsigned s_keys[kBinSortCap];
     __shared__ unsigned s_sorted[kBinSortCap];
     __shared__ int4 s_pa[kBinSortCap], s_pb[kBinSortCap];
@@ -220,6 +249,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             meta[kMetaPieces] = 0;
             meta[kMetaBinSlots] = 0;
             meta[kMetaSplitRows] = 0;
+            meta[kMetaPItems] = 0;
         }
     };
     if (T < 0 || T > max_queries) {
@@ -229,7 +259,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
 
     // Decode rows and their key blocks, and prefill rows' 32-query tiles, in
     // one scan.
-    int is_dec = 0, nblk = 0, nt = 0;
+    int is_dec = 0, nblk = 0, nt = 0, npc = 0;
     if (tid < n_rows) {
         const int qo_len = s_qo[tid + 1] - s_qo[tid];
         if (qo_len == 1) {
@@ -238,12 +268,13 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             nblk = nblk < 1 ? 1 : nblk;
         } else if (qo_len > 1) {
             nt = (qo_len + kPrefQ - 1) / kPrefQ;
+            for (int t = 0; t < nt; ++t) npc += pref_pieces(pref_tile_keys(s_kvlen[tid], qo_len, t));
         }
     }
-    int sc_excl[3], sc_total[3];
-    block_exclusive_scan_n<3>({is_dec, nblk, nt}, s_tmp, sc_excl, sc_total);
-    const int dec_idx = sc_excl[0], boff = sc_excl[1], t0_tiles = sc_excl[2];
-    const int n_dec = sc_total[0], n_blocks = sc_total[1], n_ptiles = sc_total[2];
+    int sc_excl[4], sc_total[4];
+    block_exclusive_scan_n<4>({is_dec, nblk, nt, npc}, s_tmp, sc_excl, sc_total);
+    const int dec_idx = sc_excl[0], boff = sc_excl[1], t0_tiles = sc_excl[2], p0_items = sc_excl[3];
+    const int n_dec = sc_total[0], n_blocks = sc_total[1], n_ptiles = sc_total[2], n_pitems = sc_total[3];
     s_dec[tid] = dec_idx;
     s_boff[tid] = boff;
     __syncthreads();
@@ -411,20 +442,38 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     }
     if (!lead) return;
 
-    // Prefill rows: 32-query tiles {first query, queries, first page offset,
-    // key limit of the first query (bottom-right causal)}.
+    // Prefill rows: 32-query tiles, each cut into pieces of whole 64-key tiles.
+    // Item = two int4: the tile {first query, queries, first page offset, key
+    // limit of the first query (bottom-right causal)} and the piece {first key,
+    // end key, (piece << 8) | pieces, tile index}.  The tiles' arrival
+    // counters (tile x kv head) start at zero.
     {
-        if (n_ptiles > L.max_ptiles) {
+        if (n_ptiles > L.max_ptiles || n_pitems > L.max_pitems) {
             fail(NQ_ERR_CAPACITY);
             return;
         }
-        int4 *ptiles = reinterpret_cast<int4 *>(ws + L.ptiles);
+        int4 *pitems = reinterpret_cast<int4 *>(ws + L.pitems);
+        int32_t *tile_arrivals = reinterpret_cast<int32_t *>(ws + L.tile_arrivals);
+        for (int i = tid; i < n_ptiles * num_kv_heads; i += blockDim.x) tile_arrivals[i] = 0;
+        const int qo_len = s_qo[tid + 1] - s_qo[tid];
+        int it = p0_items;
         for (int t = 0; t < nt; ++t) {
-            const int qo_len = s_qo[tid + 1] - s_qo[tid];
-            ptiles[t0_tiles + t] = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
-                                             s_kvlen[tid] - qo_len + t * kPrefQ + 1);
+            const int4 td = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
+                                      s_kvlen[tid] - qo_len + t * kPrefQ + 1);
+            const int n_keys = pref_tile_keys(s_kvlen[tid], qo_len, t);
+            const int n_kt = (n_keys + kPrefK - 1) / kPrefK;
+            const int k = pref_pieces(n_keys);
+            for (int p = 0; p < k; ++p, ++it) {
+                const int kb = kPrefK * (p * n_kt / k);
+                const int ke = p == k - 1 ? n_keys : kPrefK * ((p + 1) * n_kt / k);
+                pitems[2 * it] = td;
+                pitems[2 * it + 1] = make_int4(kb, ke, (p << 8) | k, t0_tiles + t);
+            }
         }
-        if (tid == 0) meta[kMetaPTiles] = n_ptiles;
+        if (tid == 0) {
+            meta[kMetaPTiles] = n_ptiles;
+            meta[kMetaPItems] = n_pitems;
+        }
     }
     if (n_ptiles == 0) {
         // no prefill rows: no query has key chunks, so every chunk offset is 0
@@ -1686,19 +1735,26 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
 // Prefill rows on MFMA (head dim 128, two query heads per kv head).  A
-// workgroup takes one 32-query tile of a row and one kv head; wave w owns 16
-// queries (w & 1) of query head 2h + (w >> 1).  Per 64-key tile the workgroup
-// stages K and V as they sit in the cache ([key][d], 16-byte stores); each wave
-// computes S = Q K^T with v_mfma_f32_16x16x32_bf16 (Q held in registers as the
-// A operand), masks bottom-right causal limits, runs the online softmax in the
-// exp2 domain on the MFMA output layout (a row's 16 columns sit in 16 lanes),
-// stores P as bf16 in its LDS slice and accumulates O += P V with a second
-// MFMA chain whose V operand comes from gfx950's transposing LDS read
-// (ds_read_b64_tr_b16: four keys of one column per lane and instruction), so
-// V is never transposed on the way in.  Keys past the tile's last query limit
-// are never loaded.
+// workgroup takes one piece (a range of whole 64-key tiles) of one 32-query
+// tile of a row and one kv head; wave w owns 16 queries (w & 1) of query head
+// 2h + (w >> 1).  Per 64-key tile the workgroup stages K and V as they sit in
+// the cache ([key][d], 16-byte stores) and each wave computes the transposed
+// scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (K from LDS as the A
+// operand, Q held in registers as the B operand), so a lane holds 16 scores
+// of ONE query (lane & 15) for keys 16 nt + 4 (lane >> 4) + e.  The online
+// softmax is then per lane (the four lanes of a query agree on the running
+// maximum through two cross-lane exchanges, and keep partial row sums that
+// are added once at the end), the probabilities are packed to bf16 in
+// registers and used directly as the B operand of O^T += V^T P^T, whose A
+// operand (V^T: 8 keys of one column per lane, in the same key order as the
+// lane's probabilities) comes from gfx950's transposing LDS read
+// (ds_read_b64_tr_b16).  P never goes through LDS.  Keys past the piece's end
+// are never loaded; the causal mask is applied only on tiles that reach a
+// query's limit.  A tile's pieces merge as described at the piece stores.
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pf_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float pf_floatx2 __attribute__((ext_vector_type(2)));
 typedef float pf_floatx4 __attribute__((ext_vector_type(4)));
 typedef short pf_v4i16 __attribute__((ext_vector_type(4)));
 
@@ -1708,197 +1764,333 @@ __device__ __forceinline__ pf_bf16x8 pf_as_bf16x8(const uint4 &v) {
     return r;
 }
 
-template <int Width>
-__device__ __forceinline__ float group_max16(float v) {
-    v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
-    v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
-    v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
-    v = fmaxf(v, dpp_f32<kDppMirror>(v));
-    return v;
+// round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pf_pack_bf16(float a, float b) {
+    const pf_bf16x2 r = __builtin_convertvector((pf_floatx2){a, b}, pf_bf16x2);
+    uint32_t u;
+    __builtin_memcpy(&u, &r, 4);
+    return u;
 }
 
 template <int D>
-__global__ void __launch_bounds__(kAttnThreads)
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4 - kPrefDepth, 4 - kPrefDepth)))
 prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                     const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
                     int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
                     int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
                     int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
     constexpr int KP = D + 8;        // K and V row pitch (bf16)
-    constexpr int VP = kPrefK + 8;   // P row pitch (bf16)
     constexpr int DT = D / 16;       // 16-wide output column tiles
     __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
     __shared__ __attribute__((aligned(16))) uint16_t vs[kPrefK * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t pbuf[kWaves * 16 * VP];
     __shared__ int pages[kPrefPages];
+    __shared__ int s_arrived;
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
     if (meta[kMetaStatus] != NQ_OK) return;
-    const int4 *ptiles = reinterpret_cast<const int4 *>(ws + L.ptiles);
-    const int64_t n_items = static_cast<int64_t>(meta[kMetaPTiles]) * num_kv_heads;
+    const int4 *pitems = reinterpret_cast<const int4 *>(ws + L.pitems);
+    float *part_ml = reinterpret_cast<float *>(ws + L.part_ml);
+    float *part_o = reinterpret_cast<float *>(ws + L.part_o);
+    int32_t *tile_arrivals = reinterpret_cast<int32_t *>(ws + L.tile_arrivals);
+    const int Hq = 2 * num_kv_heads;
+    const int64_t n_items = static_cast<int64_t>(meta[kMetaPItems]) * num_kv_heads;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int r16 = lane & 15, kq = lane >> 4;
     const int ps_mask = (1 << ps_log2) - 1;
-    uint16_t *pw = pbuf + wave * 16 * VP;
+    // V^T operand reads: lane r16 of lane group kq points at key 4 kq + r16 / 4 (+ 16, + 32 kh),
+    // columns 16 dt + 4 (r16 % 4) .. + 3; ds_read_b64_tr_b16 then hands lane j the four keys
+    // 4 kq .. 4 kq + 3 of column 16 dt + j
+    const uint16_t *vrow = vs + (kq * 4 + (r16 >> 2)) * KP + 4 * (r16 & 3);
+    const bool out_vec = (reinterpret_cast<uintptr_t>(out) & 7) == 0 && (o_s0 & 3) == 0 && (o_s1 & 3) == 0;
     bool bad = false;
     for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const int tile = static_cast<int>(item / num_kv_heads);
-        const int h = static_cast<int>(item - static_cast<int64_t>(tile) * num_kv_heads);
-        const int4 td = ptiles[tile];
+        const int pi = static_cast<int>(item / num_kv_heads);
+        const int h = static_cast<int>(item - static_cast<int64_t>(pi) * num_kv_heads);
+        const int4 td = pitems[2 * pi], pd = pitems[2 * pi + 1];
         const int q0 = td.x, nq = td.y, page_start = td.z, lim0 = td.w;
+        const int kb = pd.x, ke = pd.y, piece = pd.z >> 8, n_pieces = pd.z & 255;
         const int head = 2 * h + (wave >> 1);
         const int qsub = (wave & 1) * 16;
+        const int qj = qsub + r16;              // the lane's query within the tile
+        const int limit = lim0 + qj;            // its keys are [0, limit) (lanes past nq compute on zeros)
         uint4 qa[D / 32];
         {
-            const bool ok = qsub + r16 < nq;
-            const uint16_t *qp = q + static_cast<int64_t>(q0 + qsub + r16) * q_s0 + head * q_s1 + kq * 8;
+            const bool ok = qj < nq;
+            const uint16_t *qp = q + static_cast<int64_t>(q0 + qj) * q_s0 + head * q_s1 + kq * 8;
 #pragma unroll
             for (int kk = 0; kk < D / 32; ++kk)
                 qa[kk] = ok ? *reinterpret_cast<const uint4 *>(qp + kk * 32) : make_uint4(0, 0, 0, 0);
         }
-        float m[4], l[4];
-        pf_floatx4 acc[DT];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            m[i] = -INFINITY;
-            l[i] = 0.f;
-        }
+        float m_run = -INFINITY, l_run = 0.f;  // raw-score maximum; this lane's part of the row sum
+        pf_floatx4 acc[DT];                    // acc[dt][e] = O[query qj][16 dt + 4 kq + e] (unnormalised)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
-        const int n_keys = lim0 + nq - 1;
-        // K/V of the next 64-key tile are loaded into registers while the current tile is
-        // computed; each thread owns kStageVec (key, 8-channel) pieces of a tile.
+        // K/V of the next kPrefDepth 64-key tiles are loaded into registers (one set per tile in
+        // flight) while the current tile is computed; each thread owns kStageVec (key, 8-channel)
+        // pieces of a tile.
         constexpr int kStageVec = kPrefK * (D / 8) / kAttnThreads;
-        uint4 kr[kStageVec], vr[kStageVec];
-        // the item's page list goes to LDS once (when it fits), so a tile's K/V loads do not wait
+        uint4 kr[kPrefDepth][kStageVec], vr[kPrefDepth][kStageVec];
+        // the piece's page list goes to LDS once (when it fits), so a tile's K/V loads do not wait
         // for an index load
-        const int n_pg = n_keys > 0 ? ((n_keys - 1) >> ps_log2) + 1 : 0;
+        const int pg0 = kb >> ps_log2;
+        const int n_pg = ke > kb ? ((ke - 1) >> ps_log2) - pg0 + 1 : 0;
         const bool lds_pages = n_pg <= kPrefPages;
         __syncthreads();  // the previous item's page reads are done
         if (lds_pages) {
             for (int t = threadIdx.x; t < n_pg; t += kAttnThreads) {
-                const int at = page_start + t;
+                const int at = page_start + pg0 + t;
                 const int pg = at < index_limit ? kv_indices[at] : -1;
                 if (static_cast<unsigned>(pg) >= static_cast<unsigned>(num_pages)) bad = true;
                 pages[t] = pg;
             }
         }
         __syncthreads();
-        auto issue = [&](int kt) {
+        auto issue = [&](int kt, auto set) {
+            constexpr int S = decltype(set)::value;
             int pg[kStageVec];
 #pragma unroll
             for (int v = 0; v < kStageVec; ++v) {
                 const int e = threadIdx.x + v * kAttnThreads;
                 const int kk = kt + e / (D / 8);
                 if (lds_pages) {
-                    pg[v] = kk < n_keys ? pages[kk >> ps_log2] : -1;
+                    pg[v] = kk < ke ? pages[(kk >> ps_log2) - pg0] : -1;
                 } else {
                     const int at = page_start + (kk >> ps_log2);
-                    pg[v] = (kk < n_keys && at < index_limit) ? kv_indices[at] : -1;
-                    if (kk < n_keys && static_cast<unsigned>(pg[v]) >= static_cast<unsigned>(num_pages)) bad = true;
+                    pg[v] = (kk < ke && at < index_limit) ? kv_indices[at] : -1;
+                    if (kk < ke && static_cast<unsigned>(pg[v]) >= static_cast<unsigned>(num_pages)) bad = true;
                 }
             }
 #pragma unroll
             for (int v = 0; v < kStageVec; ++v) {
                 const int e = threadIdx.x + v * kAttnThreads;
                 const int key = e / (D / 8), c8 = e - key * (D / 8);
-                kr[v] = make_uint4(0, 0, 0, 0);
-                vr[v] = make_uint4(0, 0, 0, 0);
+                kr[S][v] = make_uint4(0, 0, 0, 0);
+                vr[S][v] = make_uint4(0, 0, 0, 0);
                 if (static_cast<unsigned>(pg[v]) < static_cast<unsigned>(num_pages)) {
                     const int64_t off = static_cast<int64_t>(pg[v]) * c_page +
                                         static_cast<int64_t>((kt + key) & ps_mask) * c_slot + h * c_head + c8 * 8;
-                    kr[v] = *reinterpret_cast<const uint4 *>(cache + off);
-                    vr[v] = *reinterpret_cast<const uint4 *>(cache + off + c_kind);
+                    kr[S][v] = *reinterpret_cast<const uint4 *>(cache + off);
+                    vr[S][v] = *reinterpret_cast<const uint4 *>(cache + off + c_kind);
                 }
             }
         };
-        if (n_keys > 0) issue(0);
-        for (int kt0 = 0; kt0 < n_keys; kt0 += kPrefK) {
+        // one 64-key tile from register set S, whose loads were issued kPrefDepth tiles ago
+        auto step = [&](int kt0, auto set) {
+            constexpr int S = decltype(set)::value;
             __syncthreads();  // the previous tile's LDS reads are done
 #pragma unroll
             for (int v = 0; v < kStageVec; ++v) {
                 const int e = threadIdx.x + v * kAttnThreads;
                 const int key = e / (D / 8), c8 = e - key * (D / 8);
-                *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kr[v];
-                *reinterpret_cast<uint4 *>(vs + key * KP + c8 * 8) = vr[v];
+                *reinterpret_cast<uint4 *>(ks + key * KP + c8 * 8) = kr[S][v];
+                *reinterpret_cast<uint4 *>(vs + key * KP + c8 * 8) = vr[S][v];
             }
             __syncthreads();
-            if (kt0 + kPrefK < n_keys) issue(kt0 + kPrefK);
-            // S = Q K^T over 4 key subtiles; lane holds S[qsub + kq*4 + i][kt0 + nt*16 + r16]
+            if (kt0 + kPrefDepth * kPrefK < ke) issue(kt0 + kPrefDepth * kPrefK, set);
+            // S^T = K Q^T over 4 key subtiles: sc[nt][e] = S[query qj][key kt0 + 16 nt + 4 kq + e]
             pf_floatx4 sc[4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
                 sc[nt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < D / 32; ++kk) {
-                    const uint4 kb = *reinterpret_cast<const uint4 *>(ks + (nt * 16 + r16) * KP + kk * 32 + kq * 8);
-                    sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(qa[kk]), pf_as_bf16x8(kb), sc[nt],
+                    const uint4 kv = *reinterpret_cast<const uint4 *>(ks + (nt * 16 + r16) * KP + kk * 32 + kq * 8);
+                    sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(kv), pf_as_bf16x8(qa[kk]), sc[nt],
                                                                       0, 0, 0);
                 }
             }
-            float alpha[4];
+            // causal mask, only where the tile reaches past the wave's first query limit
+            if (kt0 + kPrefK > lim0 + qsub) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int qj = qsub + kq * 4 + i;
-                const int limit = qj < nq ? lim0 + qj : 0;
-                float mx = -INFINITY;
+                for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const int key = kt0 + nt * 16 + r16;
-                    const float v = key < limit ? sc[nt][i] * scale_log2 : -INFINITY;
-                    sc[nt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
-                mx = group_max16<16>(mx);
-                const float mn = fmaxf(m[i], mx);
-                alpha[i] = m[i] == -INFINITY ? 0.f : exp2f(m[i] - mn);
-                float rs = 0.f;
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const float p = sc[nt][i] == -INFINITY ? 0.f : exp2f(sc[nt][i] - mn);
-                    rs += p;
-                    pw[(kq * 4 + i) * VP + nt * 16 + r16] = f32_to_bf16(p);
-                }
-                rs = group_sum<16>(rs);
-                l[i] = l[i] * alpha[i] + rs;
-                m[i] = mn;
+                    for (int e = 0; e < 4; ++e)
+                        if (kt0 + nt * 16 + kq * 4 + e >= limit) sc[nt][e] = -INFINITY;
             }
+            float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
+            for (int nt = 1; nt < 4; ++nt)
+                mx = fmaxf(mx, fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            // every tile holds a key below each lane's limit (the piece's first key is below the
+            // tile's first limit), so the new maximum is finite and m_run = -inf gives alpha = 0
+            const float mn = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - mn) * scale_log2);
+            const float nb = -mn * scale_log2;
+            uint32_t pk[8];  // bf16 probabilities: pk[2 nt + e / 2] holds keys 16 nt + 4 kq + e, e + 1
+            float rs = 0.f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha[i];
-            __syncthreads();  // P visible to the whole wave (and V already staged)
-            // O += P V with V read in its staged [key][d] layout by transposing LDS reads: lane s of
-            // lane group kq points at key kh*32 + 8 kq + 4 half + s / 4, columns dt*16 + 4 (s % 4) .. + 3,
-            // and ds_read_b64_tr_b16 hands lane j the four keys of column dt*16 + j (the MFMA's B
-            // operand: keys 8 kq .. 8 kq + 7 of one output column)
-            const uint16_t *vrow = vs + (kq * 8 + (r16 >> 2)) * KP + 4 * (r16 & 3);
+            for (int nt = 0; nt < 4; ++nt) {
+                float p[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    p[e] = __builtin_amdgcn_exp2f(fmaf(sc[nt][e], scale_log2, nb));
+                    rs += p[e];
+                }
+                pk[2 * nt] = pf_pack_bf16(p[0], p[1]);
+                pk[2 * nt + 1] = pf_pack_bf16(p[2], p[3]);
+            }
+            l_run = l_run * alpha + rs;
+            m_run = mn;
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[dt][e] *= alpha;
+            }
+            // O^T += V^T P^T: k slot s of lane group kq is key 32 kh + 16 (s / 4) + 4 kq + s % 4 in both
+            // operands
 #pragma unroll
             for (int kh = 0; kh < kPrefK / 32; ++kh) {
-                const uint4 pa = *reinterpret_cast<const uint4 *>(pw + r16 * VP + kh * 32 + kq * 8);
+                const uint4 pu = make_uint4(pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     const uint16_t *vp = vrow + kh * 32 * KP + dt * 16;
                     const pf_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (pf_v4i16 __attribute__((address_space(3))) *)(vp));
                     const pf_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (pf_v4i16 __attribute__((address_space(3))) *)(vp + 4 * KP));
-                    pf_bf16x8 vb;
-                    __builtin_memcpy(&vb, &lo, 8);
-                    __builtin_memcpy(reinterpret_cast<char *>(&vb) + 8, &hi, 8);
-                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(pa), vb, acc[dt], 0, 0, 0);
+                        (pf_v4i16 __attribute__((address_space(3))) *)(vp + 16 * KP));
+                    pf_bf16x8 va;
+                    __builtin_memcpy(&va, &lo, 8);
+                    __builtin_memcpy(reinterpret_cast<char *>(&va) + 8, &hi, 8);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf_as_bf16x8(pu), acc[dt], 0, 0, 0);
+                }
+            }
+        };
+        using Set0 = std::integral_constant<int, 0>;
+        using Set1 = std::integral_constant<int, kPrefDepth - 1>;
+        if (kb < ke) issue(kb, Set0{});
+        if constexpr (kPrefDepth == 2) {
+            if (kb + kPrefK < ke) issue(kb + kPrefK, Set1{});
+        }
+        for (int kt0 = kb; kt0 < ke; kt0 += kPrefDepth * kPrefK) {
+            step(kt0, Set0{});
+            if constexpr (kPrefDepth == 2) {
+                if (kt0 + kPrefK < ke) step(kt0 + kPrefK, Set1{});
+            }
+        }
+        float lt = l_run + __shfl_xor(l_run, 16, kWave);
+        lt += __shfl_xor(lt, 32, kWave);
+        if (n_pieces == 1) {
+            if (qj < nq) {
+                const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+                uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + head * o_s1 + 4 * kq;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const uint32_t w0 = pf_pack_bf16(acc[dt][0] * inv, acc[dt][1] * inv);
+                    const uint32_t w1 = pf_pack_bf16(acc[dt][2] * inv, acc[dt][3] * inv);
+                    if (out_vec) {
+                        *reinterpret_cast<uint2 *>(op + dt * 16) = make_uint2(w0, w1);
+                    } else {
+                        op[dt * 16] = static_cast<uint16_t>(w0);
+                        op[dt * 16 + 1] = static_cast<uint16_t>(w0 >> 16);
+                        op[dt * 16 + 2] = static_cast<uint16_t>(w1);
+                        op[dt * 16 + 3] = static_cast<uint16_t>(w1 >> 16);
+                    }
+                }
+            }
+            continue;
+        }
+        // A piece of a split tile leaves its unnormalised (m, l, acc) per (query, piece, query
+        // head), m in the exp2 domain, with agent-scope stores (coherent across the XCDs' L2s),
+        // waits for them, then counts its arrival on the (tile, kv head) counter; the piece that
+        // completes the count merges the tile's pieces in piece order.
+        if (qj < nq) {
+            const int64_t pr = (static_cast<int64_t>(q0 + qj) * kPrefMaxPieces + piece) * Hq + head;
+            float *po = part_o + pr * D + 4 * kq;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    __hip_atomic_store(po + dt * 16 + e, acc[dt][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (kq == 0) {
+                __hip_atomic_store(part_ml + pr * 2, m_run * scale_log2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(part_ml + pr * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();  // every wave's partial stores are complete
+        int32_t *counter = tile_arrivals + static_cast<int64_t>(pd.w) * num_kv_heads + h;
+        if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_arrived != n_pieces - 1) continue;
+        // merge: thread = (query, query head, quarter of D); the pieces' (m, l) first, then their
+        // partial rows two pieces at a time, weighted by 2^(m_p - max) / sum_p 2^(m_p - max) l_p
+        {
+            constexpr int kQuarter = D / 4;
+            const int pair = threadIdx.x >> 2, quarter = threadIdx.x & 3;
+            const int qj = pair >> 1, hh = 2 * h + (pair & 1);
+            if (qj < nq) {
+                const int64_t pr0 = static_cast<int64_t>(q0 + qj) * kPrefMaxPieces * Hq + hh;
+                float mk[kPrefMaxPieces], lk[kPrefMaxPieces];
+#pragma unroll
+                for (int p = 0; p < kPrefMaxPieces; ++p) {
+                    mk[p] = -INFINITY;
+                    lk[p] = 0.f;
+                    if (p < n_pieces) {
+                        mk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2);
+                        lk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2 + 1);
+                    }
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int p = 0; p < kPrefMaxPieces; ++p) mx = fmaxf(mx, mk[p]);
+                float ls = 0.f;
+#pragma unroll
+                for (int p = 0; p < kPrefMaxPieces; ++p) {
+                    mk[p] = mk[p] == -INFINITY ? 0.f : exp2f(mk[p] - mx);  // the piece's weight
+                    ls += mk[p] * lk[p];
+                }
+                const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+                uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + hh * o_s1 + quarter * kQuarter;
+                const bool vec = (reinterpret_cast<uintptr_t>(op) & 15) == 0;
+                // eight columns at a time, two pieces' loads in flight together
+#pragma unroll
+                for (int c = 0; c < kQuarter; c += 8) {
+                    float o[8];
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) o[v] = 0.f;
+#pragma unroll
+                    for (int p = 0; p < kPrefMaxPieces; p += 2) {
+                        if (p >= n_pieces) break;
+                        // the second piece of the pair is read again from piece p (weight 0) past the end
+                        const int p1 = p + 1 < n_pieces ? p + 1 : p;
+                        const float w0 = mk[p] * inv, w1 = p + 1 < n_pieces ? mk[p + 1] * inv : 0.f;
+                        const uint64_t *a0 =
+                            reinterpret_cast<const uint64_t *>(part_o + (pr0 + p * Hq) * D + quarter * kQuarter + c);
+                        const uint64_t *a1 =
+                            reinterpret_cast<const uint64_t *>(part_o + (pr0 + p1 * Hq) * D + quarter * kQuarter + c);
+                        uint64_t u0[4], u1[4];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            u0[v] = __hip_atomic_load(const_cast<uint64_t *>(a0 + v), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                            u1[v] = __hip_atomic_load(const_cast<uint64_t *>(a1 + v), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                        }
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            o[2 * v] += w0 * __uint_as_float(static_cast<uint32_t>(u0[v])) +
+                                        w1 * __uint_as_float(static_cast<uint32_t>(u1[v]));
+                            o[2 * v + 1] += w0 * __uint_as_float(static_cast<uint32_t>(u0[v] >> 32)) +
+                                            w1 * __uint_as_float(static_cast<uint32_t>(u1[v] >> 32));
+                        }
+                    }
+                    if (vec) {
+                        *reinterpret_cast<uint4 *>(op + c) =
+                            make_uint4(pf_pack_bf16(o[0], o[1]), pf_pack_bf16(o[2], o[3]), pf_pack_bf16(o[4], o[5]),
+                                       pf_pack_bf16(o[6], o[7]));
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 8; ++v) op[c + v] = f32_to_bf16(o[v]);
+                    }
                 }
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int qj = qsub + kq * 4 + i;
-            if (qj >= nq) continue;
-            const float inv = l[i] > 0.f ? 1.0f / l[i] : 0.f;
-            uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + head * o_s1 + r16;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) op[dt * 16] = f32_to_bf16(acc[dt][i] * inv);
-        }
+        if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
 }
@@ -1933,7 +2125,7 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
     }
     if (!(parts & NQ_ATTN_PREFILL)) return NQ_OK;
     if constexpr (D == 128 && G == 2) {
-        const int64_t titems = L.max_ptiles * Hkv;
+        const int64_t titems = L.max_pitems * Hkv;
         const int tgrid = static_cast<int>(titems < 4096 ? titems : 4096);
         hipLaunchKernelGGL((prefill_tile_kernel<D>), dim3(tgrid), dim3(kAttnThreads), 0, stream, q, q_s0, q_s1,
                            cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2,

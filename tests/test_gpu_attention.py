@@ -148,6 +148,9 @@ def test_mixed_prefill_and_decode_rows(nq, device):
     (16, [512, 0], [256, 255]),
     (4, [9, 0, 40], [31, 2, 70]),
     (32, [100, 31, 0], [1, 45, 96]),
+    # long causal ranges: tiles cut into the most key-range pieces, merged by the last to finish
+    (16, [3000, 1500], [40, 200]),
+    (128, [2100, 0, 700], [70, 300, 1]),
 ])
 def test_prefill_rows_match_oracle(nq, device, ps, priors, advances):
     """Causal prefill rows (MFMA tile path for 16/8 heads of 128) at tile remainders, page sizes and
