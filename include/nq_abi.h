@@ -205,6 +205,27 @@ int nq_cp_short_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const u
                           int64_t o_s1, void *stream);
 
 /*
+ * The code predictor's per-layer q/k norm + RoPE + dense K/V write and its
+ * short-cache attention in one launch: nq_qkv_partials_norm_rope_kv_write in
+ * dense mode (from the packed QKV projection's split-K planes [splits, rows,
+ * (Hq + 2 Hkv) * head_dim]; rotated q to q_out, K and V into cache position
+ * cache_position) followed by nq_cp_short_attention over valid_length =
+ * cache_position + 1, with the same bits as the two calls.  Replaces
+ * paired_qk_norm_rope_dense_cache_ (model/kernels.py:163-248, 335-405) and
+ * decode_attn_nhd_short_cache (model/kernels.py:408-463) as the code
+ * predictor's attention calls them in sequence (model/components.py:294-345).
+ * head_dim 64 or 128 with 1 or 2
+ * query heads per kv head; other shapes return NQ_ERR_UNSUPPORTED.
+ */
+int nq_cp_rope_short_attention(const float *partials, int splits, int rows, const uint16_t *q_weight,
+                               const uint16_t *k_weight, const int64_t *positions, int64_t pos_stride,
+                               float eps, float rope_theta, int round_to_input, uint16_t *q_out,
+                               int64_t q_s0, int64_t q_s1, uint16_t *cache, int64_t c_row, int64_t c_kind,
+                               int64_t c_pos, int64_t c_head, int cache_position, int num_qo_heads,
+                               int num_kv_heads, int head_dim, float sm_scale, uint16_t *out,
+                               int64_t o_s0, int64_t o_s1, void *stream);
+
+/*
  * Fused per-head RMSNorm + rotate-half RoPE of q and k (in place), with K and
  * V written into the cache.
  * Replaces paired_qk_norm_rope_paged_cache_ (model/kernels.py:15-160) and,

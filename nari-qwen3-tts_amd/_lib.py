@@ -55,6 +55,8 @@ _SIGNATURES: dict[str, list] = {
                                    _P, _L, _L, _I, _I, _I, _P, _P],
     "nq_kv_read_probe": [_P, _I, _L, _P, _I, _I, _P, _P],
     "nq_cp_short_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _L, _L, _P],
+    "nq_cp_rope_short_attention": [_P, _I, _I, _P, _P, _P, _L, _F, _F, _I, _P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I,
+                                   _F, _P, _L, _L, _P],
     "nq_qk_norm_rope_kv_write": [_P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _I, _I, _I, _I, _F,
                                  _F, _I, _P, _L, _L, _L, _L, _P, _P, _I, _P],
     "nq_qkv_partials_norm_rope_kv_write": [_P, _I, _I, _P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _I, _I, _I, _F, _F,

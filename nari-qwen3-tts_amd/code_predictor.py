@@ -38,7 +38,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .kernels import decode_attn_nhd_short_cache, qkv_partials_norm_rope_dense_cache_
+from .kernels import qkv_partials_rope_short_attention_
 from .layers import (
     embed_add_rmsnorm,
     gather_sum_rows,
@@ -176,12 +176,12 @@ class CodePredictorFrame:
             rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
         for index, L in enumerate(layers):
             cache = self.kv_cache[index]
-            # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write
-            # (the same bits as the bf16 projection followed by paired_qk_norm_rope_dense_cache_)
+            # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write and
+            # the short-cache attention, one launch (the same bits as the bf16 projection followed by
+            # paired_qk_norm_rope_dense_cache_ and decode_attn_nhd_short_cache)
             splits = linear_partials(self.x, L.qkv, ws)
-            qkv_partials_norm_rope_dense_cache_(ws, splits, self.q, L.q_norm, L.k_norm, positions, c.rms_eps,
-                                                c.rope_theta, cache[:, 0], cache[:, 1], cache_pos)
-            decode_attn_nhd_short_cache(self.q, cache[:, 0], cache[:, 1], cache_pos + 1, out=self.att)
+            qkv_partials_rope_short_attention_(ws, splits, self.q, L.q_norm, L.k_norm, positions, c.rms_eps,
+                                               c.rope_theta, cache[:, 0], cache[:, 1], cache_pos, self.att)
             linear_add_rmsnorm(self.att.view(n, q_w), L.o, self.h, L.post_norm, c.rms_eps, self.x, ws)
             linear_silu_mul(self.x, L.gate_up, out=self.act, workspace=ws)
             nxt = self.w.final_norm if index + 1 == len(layers) else layers[index + 1].input_norm

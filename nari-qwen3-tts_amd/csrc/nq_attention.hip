@@ -1731,6 +1731,87 @@ dense_short_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
     }
 }
 
+// Code-predictor layer attention with the q/k norm + RoPE + K/V write fused
+// in.  Workgroup (row, kv head h): waves 0 .. G-1 normalise and rotate query
+// heads h G + j from the packed QKV projection's split-K planes (summed in
+// plane order and rounded to bf16) and store them to q_out, wave G does the
+// same for key head h and writes it into the dense cache at cache_position,
+// wave G + 1 copies value head h there -- the arithmetic of
+// nq_qkv_partials_norm_rope_kv_write, so the same bits -- and after a barrier
+// the workgroup attends over positions [0, cache_position] exactly as
+// dense_short_kernel does.  One launch instead of two per layer.
+template <int D, int G>
+__global__ void __launch_bounds__(kAttnThreads)
+dense_rope_short_kernel(const float *__restrict__ partials, int splits, int64_t plane, int64_t prow,
+                        const uint16_t *__restrict__ q_weight, const uint16_t *__restrict__ k_weight,
+                        const int64_t *__restrict__ positions, int64_t pos_stride, float eps, float log_theta,
+                        int round_to_input, uint16_t *__restrict__ q_out, int64_t q_s0, int64_t q_s1,
+                        uint16_t *__restrict__ cache, int64_t c_row, int64_t c_kind, int64_t c_pos,
+                        int64_t c_head, int rows, int cache_position, int num_kv_heads, float scale_log2,
+                        uint16_t *__restrict__ out, int64_t o_s0, int64_t o_s1) {
+    constexpr int HALF = D / 2;
+    __shared__ Smem sm;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int Hq = num_kv_heads * G;
+    const int64_t n_items = static_cast<int64_t>(rows) * num_kv_heads;
+    bool bad = false;
+    for (int64_t w = blockIdx.x; w < n_items; w += gridDim.x) {
+        const int row = static_cast<int>(w / num_kv_heads);
+        const int h = static_cast<int>(w - static_cast<int64_t>(row) * num_kv_heads);
+        uint16_t *slot = cache + row * c_row + cache_position * c_pos + h * c_head;
+        for (int u = wave; u < G + 2; u += kWaves) {
+            const int col = (u < G ? h * G + u : u == G ? Hq + h : Hq + num_kv_heads + h) * D;
+            const float *e = partials + row * prow + col;
+            // the planes four at a time (all loads in flight together), added in plane order,
+            // rounded to bf16
+            auto load = [&](int d) {
+                float sum = 0.f;
+                for (int i0 = 0; i0 < splits; i0 += 4) {
+                    float a[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) a[v] = i0 + v < splits ? e[(i0 + v) * plane + d] : 0.f;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (i0 + v < splits) sum += a[v];
+                }
+                return bf16_to_f32(f32_to_bf16(sum));
+            };
+            if (u == G + 1) {
+                for (int d = lane; d < D; d += kWave) slot[c_kind + d] = f32_to_bf16(load(d));
+                continue;
+            }
+            const bool on = lane < HALF;
+            float x1 = 0.f, x2 = 0.f, w1 = 0.f, w2 = 0.f;
+            if (on) {
+                const uint16_t *wt = u < G ? q_weight : k_weight;
+                w1 = bf16_to_f32(wt[lane]);
+                w2 = bf16_to_f32(wt[lane + HALF]);
+                x1 = load(lane);
+                x2 = load(lane + HALF);
+            }
+            uint16_t o1 = 0, o2 = 0;
+            norm_rope_pair<D>(x1, x2, on, w1, w2, lane, eps, log_theta,
+                              static_cast<float>(positions[row * pos_stride]), round_to_input, o1, o2);
+            if (!on) continue;
+            uint16_t *dst = u < G ? q_out + row * q_s0 + (h * G + u) * q_s1 : slot;
+            dst[lane] = o1;
+            dst[lane + HALF] = o2;
+        }
+        __syncthreads();  // the rotated q and the new K/V are visible to every wave of the workgroup
+        attend_chunk<D, G>(
+            q_out + row * q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head, h, cache_position + 1, rows,
+            scale_log2, [&](int) { return row; }, [&](int rel) { return rel; }, sm, &bad);
+        for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
+            float M, Ls, O;
+            wave_combine<D>(sm, t, &M, &Ls, &O);
+            const int j = t / D, d = t % D;
+            out[row * o_s0 + (h * G + j) * o_s1 + d] = f32_to_bf16(Ls > 0.f ? O / Ls : 0.f);
+        }
+        __syncthreads();
+    }
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
@@ -2158,6 +2239,22 @@ int launch_dense(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
     return NQ_LAUNCH_STATUS();
 }
 
+template <int D, int G>
+int launch_dense_rope(const float *partials, int splits, int rows, const uint16_t *q_weight, const uint16_t *k_weight,
+                      const int64_t *positions, int64_t pos_stride, float eps, float rope_theta, int round_to_input,
+                      uint16_t *q_out, int64_t q_s0, int64_t q_s1, uint16_t *cache, int64_t c_row, int64_t c_kind,
+                      int64_t c_pos, int64_t c_head, int cache_position, int Hkv, float scale, uint16_t *out,
+                      int64_t o_s0, int64_t o_s1, hipStream_t stream) {
+    const int64_t prow = static_cast<int64_t>(Hkv * G + 2 * Hkv) * D;
+    const int64_t items = static_cast<int64_t>(rows) * Hkv;
+    const int grid = static_cast<int>(items < 8192 ? items : 8192);
+    hipLaunchKernelGGL((dense_rope_short_kernel<D, G>), dim3(grid), dim3(kAttnThreads), 0, stream, partials, splits,
+                       static_cast<int64_t>(rows) * prow, prow, q_weight, k_weight, positions, pos_stride, eps,
+                       logf(rope_theta), round_to_input, q_out, q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head,
+                       rows, cache_position, Hkv, scale * kLog2e, out, o_s0, o_s1);
+    return NQ_LAUNCH_STATUS();
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -2251,6 +2348,31 @@ extern "C" int nq_cp_short_attention(const uint16_t *q, int64_t q_s0, int64_t q_
     NQ_DENSE(128, 1) NQ_DENSE(128, 2) NQ_DENSE(128, 4) NQ_DENSE(128, 8)
     NQ_DENSE(64, 1) NQ_DENSE(64, 2) NQ_DENSE(64, 4) NQ_DENSE(64, 8)
 #undef NQ_DENSE
+    return NQ_ERR_UNSUPPORTED;
+}
+
+extern "C" int nq_cp_rope_short_attention(const float *partials, int splits, int rows, const uint16_t *q_weight,
+                                          const uint16_t *k_weight, const int64_t *positions, int64_t pos_stride,
+                                          float eps, float rope_theta, int round_to_input, uint16_t *q_out,
+                                          int64_t q_s0, int64_t q_s1, uint16_t *cache, int64_t c_row, int64_t c_kind,
+                                          int64_t c_pos, int64_t c_head, int cache_position, int num_qo_heads,
+                                          int num_kv_heads, int head_dim, float sm_scale, uint16_t *out,
+                                          int64_t o_s0, int64_t o_s1, void *stream) {
+    NQ_CHECK_ARG(partials && splits >= 1 && q_weight && k_weight && positions && q_out && cache && out);
+    NQ_CHECK_ARG(rows >= 1 && cache_position >= 0 && rope_theta > 0.f);
+    NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
+    if (!nq::aligned16(q_out) || !nq::aligned16(cache) || !nq::aligned16(out)) return NQ_ERR_UNSUPPORTED;
+    if ((q_s0 | q_s1 | c_row | c_kind | c_pos | c_head) & 7) return NQ_ERR_UNSUPPORTED;
+    const int G = num_qo_heads / num_kv_heads;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+#define NQ_DENSE_ROPE(DD, GG)                                                                                    \
+    if (head_dim == DD && G == GG)                                                                               \
+        return nq::launch_dense_rope<DD, GG>(partials, splits, rows, q_weight, k_weight, positions, pos_stride,   \
+                                             eps, rope_theta, round_to_input, q_out, q_s0, q_s1, cache, c_row,   \
+                                             c_kind, c_pos, c_head, cache_position, num_kv_heads, sm_scale, out, \
+                                             o_s0, o_s1, s);
+    NQ_DENSE_ROPE(128, 1) NQ_DENSE_ROPE(128, 2) NQ_DENSE_ROPE(64, 1) NQ_DENSE_ROPE(64, 2)
+#undef NQ_DENSE_ROPE
     return NQ_ERR_UNSUPPORTED;
 }
 

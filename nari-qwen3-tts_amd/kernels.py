@@ -180,6 +180,50 @@ def qkv_partials_norm_rope_dense_cache_(
     return q_out
 
 
+def qkv_partials_rope_short_attention_(
+    partials, splits: int, q_out, query_weight, key_weight, positions, epsilon, rope_theta, key_cache, value_cache,
+    cache_position: int, out,
+):
+    """qkv_partials_norm_rope_dense_cache_ followed by decode_attn_nhd_short_cache(q_out, key_cache,
+    value_cache, cache_position + 1, out=out), the pair the code predictor's decode layer runs
+    (model/components.py:294-345), in one launch with the same bits: q_out receives the rotated q,
+    the caches position ``cache_position``'s K and V, ``out`` [tokens, Hq, D] the attention."""
+
+    _require_bf16(q_out, query_weight, key_weight, key_cache, value_cache, out)
+    tokens, hq, d = q_out.shape
+    if key_cache.ndim != 4:
+        raise ValueError("dense CP cache shape mismatch")
+    hk = key_cache.shape[2]
+    if key_cache.shape != (tokens, key_cache.shape[1], hk, d) or value_cache.shape != key_cache.shape:
+        raise ValueError("dense CP cache shape mismatch")
+    if not isinstance(cache_position, int) or isinstance(cache_position, bool) or not 0 <= cache_position < min(
+            key_cache.shape[1], 16):
+        raise ValueError("dense CP cache position is invalid (short-cache attention covers at most 16)")
+    if key_cache.stride() != value_cache.stride() or key_cache.stride(-1) != 1 or q_out.stride(-1) != 1:
+        raise ValueError("dense CP K and V caches must share one layout")
+    if out.shape != q_out.shape or out.stride(-1) != 1:
+        raise ValueError("out must be [tokens, Hq, D] like q_out")
+    if hq % hk:
+        raise ValueError("short-cache attention requires compatible heads")
+    if positions.dtype != torch.long or positions.shape[0] != tokens:
+        raise ValueError("positions must be int64 with one entry per token")
+    if partials.numel() * partials.element_size() < splits * tokens * (hq + 2 * hk) * d * 4:
+        raise ValueError("partials hold fewer planes than splits")
+    delta = value_cache.data_ptr() - key_cache.data_ptr()
+    if delta % key_cache.element_size():
+        raise ValueError("dense CP K and V caches are misaligned")
+    _lib.require_device(partials, q_out, query_weight, key_weight, positions, key_cache, value_cache, out)
+    _lib.call(
+        "nq_cp_rope_short_attention", partials.data_ptr(), int(splits), tokens,
+        query_weight.data_ptr(), key_weight.data_ptr(), positions.data_ptr(), positions.stride(0),
+        float(epsilon), float(rope_theta), 0, q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
+        key_cache.data_ptr(), key_cache.stride(0), delta // key_cache.element_size(), key_cache.stride(1),
+        key_cache.stride(2), int(cache_position), hq, hk, d, float(d) ** -0.5,
+        out.data_ptr(), out.stride(0), out.stride(1), _lib.stream(q_out.device),
+    )
+    return out
+
+
 def decode_attn_nhd_short_cache(query, key_cache, value_cache, cache_length: int, out=None):
     """Fixed 16-position code-predictor attention (one query per row)."""
 
@@ -260,5 +304,6 @@ __all__ = [
     "paired_qk_norm_rope_",
     "paired_qk_norm_rope_dense_cache_",
     "qkv_partials_norm_rope_dense_cache_",
+    "qkv_partials_rope_short_attention_",
     "paired_qk_norm_rope_paged_cache_",
 ]

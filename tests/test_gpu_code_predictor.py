@@ -138,3 +138,43 @@ def test_bench_frame_b128_matches_oracle(nq, device):
     np.testing.assert_array_equal(to_np(frame.frames)[:, 1:], tokens.T)
     np.testing.assert_array_equal(to_np(frame.codec_sum), csum)
     np.testing.assert_allclose(to_np(frame.kv_cache), cache, atol=3e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("rows,hq,hk,d,splits,pos", [(37, 16, 8, 64, 4, 0), (128, 16, 8, 64, 4, 7),
+                                                     (9, 16, 8, 64, 3, 15), (6, 8, 8, 128, 2, 4)])
+def test_fused_rope_short_attention_equals_the_two_launches(nq, device, rows, hq, hk, d, splits, pos):
+    """One launch (q/k norm + RoPE + dense K/V write + short-cache attention from the QKV planes) gives
+    the bits of qkv_partials_norm_rope_dense_cache_ followed by decode_attn_nhd_short_cache: the rotated
+    q, the cache (every position) and the attention output."""
+
+    from nari_qwen3_tts_amd.kernels import (decode_attn_nhd_short_cache, qkv_partials_norm_rope_dense_cache_,
+                                            qkv_partials_rope_short_attention_)
+
+    print(f"case rows {rows} heads {hq}/{hk} d {d} splits {splits} pos {pos}", flush=True)
+    g = torch.Generator(device=device)
+    g.manual_seed(rows * 131 + pos)
+    width = (hq + 2 * hk) * d
+    planes = torch.randn(splits, rows, width, generator=g, device=device) * 0.7
+    qw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    positions = torch.randint(0, 4096, (rows,), generator=g, device=device, dtype=torch.long)
+    cache0 = torch.randn(rows, 2, 16, hk, d, generator=g, device=device).to(torch.bfloat16)
+    results = []
+    for fused in (False, True):
+        cache = cache0.clone()
+        q = torch.zeros(rows, hq, d, dtype=torch.bfloat16, device=device)
+        out = torch.zeros(rows, hq, d, dtype=torch.bfloat16, device=device)
+        if fused:
+            qkv_partials_rope_short_attention_(planes, splits, q, qw, kw, positions, 1e-6, 1e6, cache[:, 0],
+                                               cache[:, 1], pos, out)
+        else:
+            qkv_partials_norm_rope_dense_cache_(planes, splits, q, qw, kw, positions, 1e-6, 1e6, cache[:, 0],
+                                                cache[:, 1], pos)
+            decode_attn_nhd_short_cache(q, cache[:, 0], cache[:, 1], pos + 1, out=out)
+        torch.cuda.synchronize()
+        results.append((q, cache, out))
+    (q0, c0, o0), (q1, c1, o1) = results
+    assert torch.equal(q0, q1)
+    assert torch.equal(c0, c1)
+    assert torch.equal(o0, o1)
+    assert not torch.equal(c0, cache0)  # the position was written
