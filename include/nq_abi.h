@@ -549,6 +549,21 @@ int nq_linear_fp8(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s
  */
 int nq_fp8_pack_swiglu(const uint8_t *q, int64_t q_s0, int I, int K, uint8_t *packed, int64_t p_s0,
                        void *stream);
+
+/*
+ * bf16 gate/up with the SwiGLU fused, for the code predictor's MLP shape
+ * (K = 1024, I % 24 == 0, any row count in blocks of 64; else
+ * NQ_ERR_UNSUPPORTED and the caller uses nq_linear with NQ_EPI_SILU_MUL):
+ * out[M, I] = silu(bf16(gate)) * bf16(up) of x[M, K] . W^T (GatedMLP.forward,
+ * model/layers.py:264-270, as the code predictor's MLP runs it), whole dot
+ * products per workgroup (no split-K planes, no second kernel), summing K in
+ * four 256-wide quarters in order: the bits of nq_linear + NQ_EPI_SILU_MUL
+ * wherever that cuts K into 256-wide slices (128 rows).  `packed` holds the [gate; up] rows [2I, K]
+ * interleaved by nq_fp8_pack_swiglu applied to the bf16 rows as bytes (row
+ * length 2K bytes, strides in bytes).
+ */
+int nq_linear_swiglu(const uint16_t *x, int64_t x_s0, int M, const uint16_t *packed, int64_t w_s0, int I, int K,
+                     uint16_t *out, int64_t o_s0, void *stream);
 int nq_linear_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_t sx_s0, int M,
                          const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
                          uint16_t *out, int64_t o_s0, void *stream);

@@ -86,6 +86,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_fp8_workspace_bytes": [_I, _I, _I, _I],
     "nq_linear_fp8": [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L, _P, _L, _P],
     "nq_fp8_pack_swiglu": [_P, _L, _I, _I, _P, _L, _P],
+    "nq_linear_swiglu": [_P, _L, _I, _P, _L, _I, _I, _P, _L, _P],
     "nq_linear_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
     "nq_sgemm": [_P, _L, _P, _P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _P, _L, _P],
     "nq_row_norm": [_P, _L, _I, _I, _P, _P, _F, _P, _L, _P],

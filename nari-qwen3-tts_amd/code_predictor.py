@@ -14,11 +14,12 @@ branch (model/components.py:254-356):
   codec_embedding[g-1][token], next input = projected codec embedding.
 
 Each layer is: RMSNorm (first layer; later ones come out of the previous
-epilogue), packed QKV projection, q/k RMSNorm + RoPE with the K/V write into
-the dense 16-slot cache (no bf16 rounding before the rotation,
-model/kernels.py:335-405), short-cache attention over the valid positions,
-o_proj with the residual add + post-attention RMSNorm fused, gate_up with
-SiLU-mul fused, down with the residual add + next RMSNorm fused.  The residual
+epilogue), packed QKV projection, then one launch for the q/k RMSNorm + RoPE
+with the K/V write into the dense 16-slot cache (no bf16 rounding before the
+rotation, model/kernels.py:335-405) and the short-cache attention over the
+valid positions, o_proj with the residual add + post-attention RMSNorm fused,
+gate_up with the SwiGLU fused (one kernel over interleaved gate/up rows), down
+with the residual add + next RMSNorm fused.  The residual
 adds are the reference's plain bf16 ``residual + projection`` followed by the
 norm (components.py:331-346), which is what the fused epilogue computes.
 
@@ -45,8 +46,9 @@ from .layers import (
     linear,
     linear_add_rmsnorm,
     linear_partials,
-    linear_silu_mul,
+    linear_swiglu,
     linear_workspace_bytes,
+    pack_swiglu,
     rmsnorm,
 )
 from .sampling import sample_with_counter_from_planes, sample_with_uniforms
@@ -99,6 +101,8 @@ class CodePredictorWeights:
             )
             for _ in range(c.num_layers)
         ]
+        for L in self.layers:  # gate/up rows interleaved for the fused SwiGLU kernel
+            L.gate_up_packed = pack_swiglu(L.gate_up)
         self.final_norm = torch.ones(c.hidden, **bf)
         groups = c.num_code_groups - 1
         self.lm_head = randn(groups, c.vocab, c.hidden)
@@ -183,7 +187,7 @@ class CodePredictorFrame:
             qkv_partials_rope_short_attention_(ws, splits, self.q, L.q_norm, L.k_norm, positions, c.rms_eps,
                                                c.rope_theta, cache[:, 0], cache[:, 1], cache_pos, self.att)
             linear_add_rmsnorm(self.att.view(n, q_w), L.o, self.h, L.post_norm, c.rms_eps, self.x, ws)
-            linear_silu_mul(self.x, L.gate_up, out=self.act, workspace=ws)
+            linear_swiglu(self.x, L.gate_up_packed, self.act, weight=L.gate_up, workspace=ws)
             nxt = self.w.final_norm if index + 1 == len(layers) else layers[index + 1].input_norm
             linear_add_rmsnorm(self.act, L.down, self.h, nxt, c.rms_eps, self.x, ws)
 

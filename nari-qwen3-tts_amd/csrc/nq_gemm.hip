@@ -282,6 +282,137 @@ pack_linear_kernel(const uint16_t *__restrict__ w, int64_t w_s0, int N, int K, u
     }
 }
 
+// ---------------------------------------------------------------------------
+// Gate/up with the SwiGLU fused, bf16, for rows in blocks of 64 and K = 1024
+// (the code predictor's MLP).  The activation block [64, K] is 128 KiB, so one
+// workgroup per CU stages all of it in LDS and computes whole dot products:
+// no split-K planes and no second kernel.  The weight rows are interleaved
+// (nq_fp8_pack_swiglu on the bf16 rows): 16-row tile t holds, for q = 0..3,
+// gate rows 8t + 2q, 8t + 2q + 1 then up rows 8t + 2q, 8t + 2q + 1, so MFMA
+// lane group q ends with two gate/up pairs of the same act columns
+// 8t + 2q + {0, 1}.  A workgroup owns kBsTiles tiles of one 64-row block; its
+// kBsTiles * kBsQuarters waves each take one tile over one quarter of K, the
+// chain of each quarter runs in k order from zero (the MFMA operands and
+// order of a K slice of the split-K kernel), the quarters are summed in
+// order through LDS, and the epilogue rounds gate and up to bf16 and stores
+// bf16(silu(g) * u) -- the bits of the split-K projection with four 256-wide
+// slices (its choice at 128 rows) followed by the SiLU-mul kernel.
+
+constexpr int kBsTiles = 3;
+constexpr int kBsQuarters = 4;
+constexpr int kBsThreads = kBsTiles * kBsQuarters * kWave;
+constexpr int kBsRows = 64;
+constexpr int kBsK = 1024;
+static_assert(kBsRows / 16 == kBsQuarters, "the wave of quarter q finishes 16-row block q");
+
+template <int K>
+__global__ void __launch_bounds__(kBsThreads)
+bf16_swiglu_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w,
+                   int64_t w_s0, uint16_t *__restrict__ out, int64_t o_s0) {
+    constexpr int XP = x_pitch<K>();   // LDS row pitch (bf16)
+    constexpr int QK = K / kBsQuarters;
+    constexpr int QS = QK / 32;         // MFMA steps per quarter
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kBsRows * XP];
+    static_assert(kBsQuarters * kBsTiles * 4 * kWave * 4 * 4 <= kBsRows * XP * 2, "reduction fits the X area");
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int tl = wave % kBsTiles;
+    const int quarter = wave / kBsTiles;
+    const int tile = blockIdx.x * kBsTiles + tl;
+    const int row0 = blockIdx.y * kBsRows;
+    const int rows = M - row0 < kBsRows ? M - row0 : kBsRows;
+
+    // 1. the activation block (rows past M zero), issued first: loads complete in
+    // issue order, so the wait for them below leaves the weights in flight.  Each
+    // workgroup starts at its own rotation of the block, so the CUs of an XCD do
+    // not all ask the same L2 lines at the same moment.
+    constexpr int kVec = kBsRows * (K / 8);
+    constexpr int kPer = (kVec + kBsThreads - 1) / kBsThreads;
+    const int rot = (blockIdx.x * 258) % kVec;
+    auto rot_of = [&](int i) { return i + rot < kVec ? i + rot : i + rot - kVec; };
+    uint4 xr[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = threadIdx.x + u * kBsThreads;
+        const int v = rot_of(i);
+        const int row = v / (K / 8), c = v % (K / 8);
+        xr[u] = (i < kVec && row < rows) ? *reinterpret_cast<const uint4 *>(x + (row0 + row) * x_s0 + c * 8)
+                                         : make_uint4(0, 0, 0, 0);
+    }
+    // 2. the wave's weights: 16 packed rows over its K quarter
+    uint4 wr[QS];
+    {
+        const uint16_t *wrow = w + static_cast<int64_t>(tile * 16 + r16) * w_s0 + quarter * QK + kq * 8;
+#pragma unroll
+        for (int j = 0; j < QS; ++j) wr[j] = *reinterpret_cast<const uint4 *>(wrow + j * 32);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = threadIdx.x + u * kBsThreads;
+        const int v = rot_of(i);
+        if (i < kVec) *reinterpret_cast<uint4 *>(xs + (v / (K / 8)) * XP + (v % (K / 8)) * 8) = xr[u];
+    }
+    __syncthreads();
+
+    // 3. the quarter's MFMA chains (W as the A operand, X^T from LDS as the B operand)
+    floatx4_t acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < QS; ++j) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint4 b = *reinterpret_cast<const uint4 *>(xs + (m * 16 + r16) * XP + quarter * QK + j * 32 + kq * 8);
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wr[j]), as_bf16x8(b), acc[m], 0, 0, 0);
+        }
+    }
+
+    // 4. every quarter wave hands its sums over through the (now free) X area; the
+    // wave of quarter q then finishes 16-row block m = q of its tile, adding the
+    // quarters in order 0, 1, 2, 3
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(xs);
+    {
+        float *dst = red + ((quarter * kBsTiles + tl) * 4 * kWave + lane) * 4;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            *reinterpret_cast<float4 *>(dst + m * kWave * 4) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    }
+    __syncthreads();
+    const int m = quarter;
+    float sum[4];
+    {
+        const float4 v0 = *reinterpret_cast<const float4 *>(red + ((tl * 4 + m) * kWave + lane) * 4);
+        sum[0] = v0.x;
+        sum[1] = v0.y;
+        sum[2] = v0.z;
+        sum[3] = v0.w;
+    }
+#pragma unroll
+    for (int q = 1; q < kBsQuarters; ++q) {
+        const float4 v = *reinterpret_cast<const float4 *>(red + (((q * kBsTiles + tl) * 4 + m) * kWave + lane) * 4);
+        sum[0] += v.x;
+        sum[1] += v.y;
+        sum[2] += v.z;
+        sum[3] += v.w;
+    }
+    // 5. SwiGLU of the bf16 projection values: act columns 8t + 2kq + {0, 1}
+    const int row = m * 16 + r16;
+    if (row >= rows) return;
+    float a[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const float g = bf16_to_f32(f32_to_bf16(sum[e]));
+        const float u = bf16_to_f32(f32_to_bf16(sum[2 + e]));
+        a[e] = g / (1.0f + expf(-g)) * u;
+    }
+    *reinterpret_cast<uint32_t *>(out + (row0 + row) * o_s0 + tile * 8 + kq * 2) = pack2_bf16(a[0], a[1]);
+}
+
 }  // namespace
 
 // Bands per workgroup: the largest divisor of the band count that still
@@ -391,5 +522,19 @@ extern "C" int nq_pack_linear_weight(const uint16_t *w, int64_t w_s0, int N, int
     const int64_t blocks = (vec + 255) / 256;
     hipLaunchKernelGGL(pack_linear_kernel, dim3(static_cast<unsigned>(blocks > 8192 ? 8192 : blocks)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), w, w_s0, N, K, packed);
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_linear_swiglu(const uint16_t *x, int64_t x_s0, int M, const uint16_t *packed, int64_t w_s0, int I,
+                                int K, uint16_t *out, int64_t o_s0, void *stream) {
+    NQ_CHECK_ARG(x && packed && out && M > 0 && I > 0 && K > 0);
+    if (K != nq::kBsK || I % (8 * nq::kBsTiles) != 0) return NQ_ERR_UNSUPPORTED;
+    NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 8 == 0 && w_s0 % 8 == 0);
+    NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(packed)) % 16 == 0);
+    NQ_CHECK_ARG(o_s0 >= I && o_s0 % 2 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0);
+    const dim3 grid(static_cast<unsigned>(2 * I / (16 * nq::kBsTiles)),
+                    static_cast<unsigned>((M + nq::kBsRows - 1) / nq::kBsRows));
+    hipLaunchKernelGGL((nq::bf16_swiglu_kernel<nq::kBsK>), grid, dim3(nq::kBsThreads), 0,
+                       static_cast<hipStream_t>(stream), x, x_s0, M, packed, w_s0, out, o_s0);
     return NQ_LAUNCH_STATUS();
 }

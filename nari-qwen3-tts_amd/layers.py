@@ -634,6 +634,42 @@ def pack_fp8_swiglu(weight_q: torch.Tensor) -> torch.Tensor:
     return packed
 
 
+def pack_swiglu(weight: torch.Tensor) -> torch.Tensor:
+    """Interleave the rows of a bf16 [gate; up] matrix [2I, K] for linear_swiglu (the row permutation
+    of pack_fp8_swiglu, applied to the bf16 rows as bytes)."""
+
+    if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.shape[0] % 16 or weight.stride(1) != 1:
+        raise ValueError("bf16 gate/up rows [2I, K] with I % 8 == 0 expected")
+    _lib.require_device(weight)
+    packed = torch.empty_like(weight)
+    _lib.call("nq_fp8_pack_swiglu", weight.data_ptr(), weight.stride(0) * 2, weight.shape[0] // 2,
+              weight.shape[1] * 2, packed.data_ptr(), packed.stride(0) * 2, _lib.stream(weight.device))
+    return packed
+
+
+def linear_swiglu(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, weight: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up of the bf16 gate/up projection in one kernel where the shape allows it (K = 1024;
+    the bits of linear_silu_mul at 128 rows, where both sum K in the same four slices); else
+    linear_silu_mul on the unpacked ``weight``."""
+
+    rows, k = x.shape
+    inter = packed.shape[0] // 2
+    if out.shape != (rows, inter) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be bf16 [{rows}, {inter}] with unit inner stride")
+    if x.dtype != torch.bfloat16 or packed.dtype != torch.bfloat16 or packed.shape[1] != k or x.stride(1) != 1:
+        raise TypeError("bf16 activations and packed bf16 gate/up rows expected")
+    _lib.require_device(x, packed, out)
+    rc = _lib.load().nq_linear_swiglu(x.data_ptr(), x.stride(0), rows, packed.data_ptr(), packed.stride(0), inter,
+                                      k, out.data_ptr(), out.stride(0), _lib.stream(x.device))
+    if rc == _lib.NQ_ERR_UNSUPPORTED:
+        if weight is None:
+            raise TypeError("shape not covered by the fused SwiGLU and no unpacked weight given")
+        return linear_silu_mul(x, weight, out=out, workspace=workspace)
+    _lib.check(rc, "nq_linear_swiglu")
+    return out
+
+
 def linear_fp8_swiglu(q: torch.Tensor, scales: torch.Tensor, packed: torch.Tensor, weight_scales: torch.Tensor,
                       out: torch.Tensor, weight_q: torch.Tensor | None = None,
                       workspace: torch.Tensor | None = None) -> torch.Tensor:
@@ -663,6 +699,8 @@ def linear_fp8_swiglu(q: torch.Tensor, scales: torch.Tensor, packed: torch.Tenso
 
 
 __all__ = [
+    "linear_swiglu",
+    "pack_swiglu",
     "FP8",
     "PackedLinearWeight",
     "embed_add_rmsnorm",

@@ -224,3 +224,48 @@ def test_pack_rejects_unsupported_shapes(nq, device):
         pack_linear_weight(torch.zeros(24, 64, dtype=torch.bfloat16, device=device))
     with pytest.raises(TypeError):
         pack_linear_weight(torch.zeros(32, 48, dtype=torch.bfloat16, device=device))
+
+
+@pytest.mark.parametrize("m,inter", [(128, 3072), (64, 3072), (37, 96), (1, 96), (200, 3072)])
+def test_fused_bf16_swiglu_equals_split_k_silu_mul(nq, device, m, inter):
+    """One kernel over interleaved gate/up rows (K = 1024): at 128 rows (the code predictor's batch,
+    where the split-K projection cuts K into the same four 256-wide slices) the bits of the split-K
+    projection followed by the SiLU-mul kernel; at every row count within fp32-summation-order
+    rounding of a float32 torch reference (gate and up rounded to bf16 first)."""
+
+    from nari_qwen3_tts_amd.layers import linear_silu_mul, linear_swiglu, pack_swiglu
+
+    print(f"case m {m} inter {inter}", flush=True)
+    k = 1024
+    g = torch.Generator(device=device)
+    g.manual_seed(m * 7 + inter)
+    x = (torch.randn(m, k, generator=g, device=device) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(2 * inter, k, generator=g, device=device) * 0.05).to(torch.bfloat16)
+    packed = pack_swiglu(w)
+    out = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device=device)
+    linear_swiglu(x, packed, out)
+    torch.cuda.synchronize()
+    y = x.float() @ w.float().t()
+    gate, up = y[:, :inter].bfloat16().float(), y[:, inter:].bfloat16().float()
+    want = gate / (1.0 + torch.exp(-gate)) * up
+    err = (out.float() - want).abs()
+    # one bf16 rounding of the product plus a rare one-ulp flip of gate or up
+    assert bool((err <= want.abs() * 2.0 ** -6 + 1e-5).all()), f"max err {err.max().item():.3g}"
+    if m == 128:
+        assert torch.equal(out, linear_silu_mul(x, w))
+    # the packed rows are a permutation of the original rows
+    assert torch.equal(packed.sort(dim=0).values, w.sort(dim=0).values)
+
+
+def test_fused_bf16_swiglu_falls_back_outside_its_shape(nq, device):
+    from nari_qwen3_tts_amd.layers import linear_silu_mul, linear_swiglu, pack_swiglu
+
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    x = (torch.randn(16, 512, generator=g, device=device) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(2 * 96, 512, generator=g, device=device) * 0.05).to(torch.bfloat16)
+    out = torch.empty(16, 96, dtype=torch.bfloat16, device=device)
+    linear_swiglu(x, pack_swiglu(w), out, weight=w)
+    assert torch.equal(out, linear_silu_mul(x, w))
+    with pytest.raises(TypeError):
+        linear_swiglu(x, pack_swiglu(w), out)
