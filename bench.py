@@ -674,13 +674,17 @@ def mixed_attention(args, torch, np) -> dict:
     pre_us, _, kv2, ctx2, q2, pubs2 = build(pre_prior, pre_adv, MIXED_PREFILL)
     del kv2, ctx2, q2, pubs2
     torch.cuda.empty_cache()
+    dec_us, _, kv3, ctx3, q3, pubs3 = build(dec_prior, np.ones(MIXED_DECODE, dtype=np.int64), MIXED_DECODE)
+    del kv3, ctx3, q3, pubs3
+    torch.cuda.empty_cache()
     # algorithmic work
     kv_len = pre_prior + pre_adv
     pre_flops = float(np.sum(4.0 * cfg.num_qo_heads * cfg.head_dim * (pre_adv * pre_prior + pre_adv * (pre_adv + 1) / 2)))
     dec_bytes = float(np.sum(dec_prior + 1)) * cfg.num_kv_heads * cfg.head_dim * 4
     pre_bytes = float(np.sum(kv_len)) * cfg.num_kv_heads * cfg.head_dim * 4
     tflops = pre_flops / (pre_us / 1e6) / 1e12
-    log(f"mixed batch: {mixed_us:.1f} us/layer (prefill rows alone {pre_us:.1f} us/layer = {tflops:.1f} TFLOP/s); "
+    log(f"mixed batch: {mixed_us:.1f} us/layer (prefill rows alone {pre_us:.1f} us/layer = {tflops:.1f} TFLOP/s; "
+        f"decode rows alone {dec_us:.1f} us/layer = {dec_bytes / (dec_us / 1e6) / 1e9:.0f} GB/s); "
         f"planner {plan_us:.0f} us per decision")
     result = {
         "metric": "mixed chunked-prefill + decode attention: us per layer (16 prefill chunks + 112 decode rows)",
@@ -716,6 +720,8 @@ def mixed_attention(args, torch, np) -> dict:
         "decode_part": {
             "bytes_per_layer": dec_bytes + pre_bytes,
             "achieved_GBps_whole_launch": round((dec_bytes + pre_bytes) / (mixed_us / 1e6) / 1e9, 1),
+            "decode_rows_alone_us": round(dec_us, 2),
+            "decode_rows_alone_GBps": round(dec_bytes / (dec_us / 1e6) / 1e9, 1),
         },
         "planner_us_per_decision": round(plan_us, 1),
     }

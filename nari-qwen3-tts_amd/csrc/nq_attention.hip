@@ -62,6 +62,7 @@ constexpr int kBinWaves = 16;
 constexpr int kBinThreads = kBinWaves * kWave;
 constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
 constexpr int kBinSortCap = 2048;  // pieces the plan can sort
+constexpr bool kDecodeBins = true;  // decode rows of general batches through the bins (else stream + merge)
 
 __host__ __device__ inline int bins_per_head(int num_kv_heads) {
     const int nb = kBinWgs / num_kv_heads;
@@ -1126,6 +1127,10 @@ struct RopeSrc {
     const int64_t *positions, *write_pages, *write_offsets;
     float eps, log_theta;
     int round_to_input;
+    // bf16 query [tokens, Hq, D] already rotated (the kernel's q-input mode: no
+    // planes, no norm / RoPE, no K/V write -- the caller's rope kernel did them)
+    const uint16_t *q;
+    int64_t q_s0, q_s1;
 };
 
 template <int D, int G>
@@ -1202,7 +1207,7 @@ __device__ __forceinline__ void bin_arrive(int4 pc, int h, int num_kv_heads, int
     if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int G, bool kSmallPages>
+template <int D, int G, bool kSmallPages, bool kQIn = false>
 __global__ void __launch_bounds__(kBinThreads)
 bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
                   int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
@@ -1306,7 +1311,20 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         kw1 = bf16_to_f32(rs.k_weight[lane]);
         kw2 = bf16_to_f32(rs.k_weight[lane + HALF]);
     }
-    for (int u = wave; u < nslots * (G + 2); u += kBinWaves) {
+    if constexpr (kQIn) {
+        // q-input mode: the bin's rotated query heads into LDS, one wave per (piece, head)
+        for (int u = wave; u < nslots * G; u += kBinWaves) {
+            const int sl = u / G, j = u - sl * G;
+            const int64_t tok = s_rope[sl].x;
+            if (tok >= rs.tokens) {
+                bad = true;
+                continue;
+            }
+            const uint16_t *qh = rs.q + tok * rs.q_s0 + (h * G + j) * rs.q_s1;
+            for (int d = lane; d < D; d += kWave) s_q[(sl * G + j) * D + d] = qh[d];
+        }
+    }
+    for (int u = wave; u < (kQIn ? 0 : nslots * (G + 2)); u += kBinWaves) {
         const int sl = u / (G + 2), kind = u - sl * (G + 2);
         const int4 rp = s_rope[sl];
         const bool row_last = rp.w < 0;
@@ -1378,7 +1396,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     if (s0 < s1) {
         int sl0 = 0;
         while (sl0 + 1 < nslots && s_start[sl0 + 1] <= s0) ++sl0;
-        const bool write_block = s_rope[sl0].w < 0 && s0 == s_start[sl0 + 1] - 1;
+        const bool write_block = !kQIn && s_rope[sl0].w < 0 && s0 == s_start[sl0 + 1] - 1;
         if (!write_block) {
             ref.make(shfl_int4(dwin, 0), c_page, c_slot, num_pages, ps_log2, kv_indices, index_limit, g, &bad);
             ref.load(head_base, c_slot, kc);
@@ -2183,7 +2201,34 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
                  uint16_t *out, int64_t o_s0, int64_t o_s1, char *ws, const PlanLayout &L,
                  int max_queries, int parts, int32_t *status, hipStream_t stream) {
     const int sgrid = kStreamWaves / kWaves;
-    if (parts & NQ_ATTN_DECODE) {
+    bool decode_done = false;
+    if constexpr (D == 128 && G <= 2) {
+        // decode rows through the bins (whole rows per workgroup, split rows merged by their last
+        // piece: no merge launch), with the rotated q read from `q`; a plan holds at most
+        // kPlanThreads rows, so its bins fit kBinMaxSlots whenever this bound does
+        const int NB = bins_per_head(Hkv);
+        const int rows_bound = max_queries < kPlanThreads ? max_queries : kPlanThreads;
+        if (kDecodeBins && (parts & NQ_ATTN_DECODE) && Hkv <= kBinWgs && (rows_bound + NB - 1) / NB + 1 <= kBinMaxSlots) {
+            RopeSrc rs{};
+            rs.tokens = max_queries;
+            rs.q = q;
+            rs.q_s0 = q_s0;
+            rs.q_s1 = q_s1;
+            const dim3 grid(static_cast<unsigned>(NB * Hkv));
+            uint16_t *kv = const_cast<uint16_t *>(cache);  // q-input mode writes no K/V
+            if (ps_log2 < 4)
+                hipLaunchKernelGGL((bin_decode_kernel<D, G, true, true>), grid, dim3(kBinThreads), 0, stream, rs, kv,
+                                   c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2,
+                                   scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+            else
+                hipLaunchKernelGGL((bin_decode_kernel<D, G, false, true>), grid, dim3(kBinThreads), 0, stream, rs,
+                                   kv, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv,
+                                   ps_log2, scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+            if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+            decode_done = true;
+        }
+    }
+    if ((parts & NQ_ATTN_DECODE) && !decode_done) {
 #define NQ_LAUNCH_STREAM(KERNEL, SMALL)                                                          \
     hipLaunchKernelGGL((KERNEL<D, G, SMALL>), dim3(sgrid), dim3(kAttnThreads), 0, stream, q, q_s0, \
                        q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,         \
