@@ -39,7 +39,7 @@ SEED = 1002
 # HBM bytes one fused decode-attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE
 # counter passes in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device copy:
 # x2.0 and x1.0).
-ATTENTION_TRAFFIC_BYTES = 251_724_660
+ATTENTION_TRAFFIC_BYTES = 254_003_756
 
 
 def log(*a):
