@@ -16,6 +16,8 @@
 // A conv or transconv reads the old state, then a second small kernel writes
 // the new state (in place: each thread owns one (stream, channel) column and
 // walks it forward, so no element is overwritten before it is read).
+#include <type_traits>
+
 #include "nq_common.h"
 
 namespace nq {
@@ -151,27 +153,31 @@ conv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *
     }
 }
 
-// Narrow causal Conv1d (Cin, Cout <= 64): one thread per output row computing
-// every output channel.  The workgroup stages its 256 rows plus the `pad`
-// rows before them, activated once, in LDS (row pitch Cin + 1, so the 64 rows
-// a wave reads at one channel hit distinct banks) with the weights as
+// Narrow causal Conv1d (Cin, Cout <= 64): each thread computes every output
+// channel of R rows (rows t, t + 256, ..., of the workgroup's 256 R), so each
+// weight read from LDS feeds R rows.  The workgroup stages its 256 R rows plus
+// the `pad` rows before them, activated once, in LDS (row pitch Cin + 1, so the
+// 64 rows a wave reads at one channel hit distinct banks) with the weights as
 // [ci][k][co].  A tap whose input time is >= 0 reads the staged row (it lies in
 // the same stream); a tap before the stream's first fresh row reads the
-// stream's history from global memory.
-template <int CO>
+// stream's history from global memory.  The thread finds its first row's
+// stream by binary search and steps forward for its later rows.  Outputs (and
+// the residual) move as float4 when the row strides allow it.
+template <int CO, int R>
 __global__ void __launch_bounds__(kCodecThreads)
 conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
                   const int32_t *__restrict__ slots, const float *__restrict__ hist, const float *__restrict__ w,
                   const float *__restrict__ bias, int Cin, int Cout, int K, int dil, Act act,
                   const float *__restrict__ res, int64_t ldres, float *__restrict__ out, int64_t ldo) {
+    constexpr int ROWS = kCodecThreads * R;
     extern __shared__ float lds[];
     const int pad = (K - 1) * dil;
     const int pitch = Cin + 1;
-    float *xs = lds;                                              // [(256 + pad) * pitch]
-    float *wsm = xs + ((kCodecThreads + pad) * pitch + 3) / 4 * 4;  // [Cin * K * CO], 16-byte aligned
-    float *sa = wsm + Cin * K * CO;                   // [Cin]
-    float *sb = sa + Cin;                             // [Cin]
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kCodecThreads;
+    float *xs = lds;                                            // [(ROWS + pad) * pitch]
+    float *wsm = xs + ((ROWS + pad) * pitch + 3) / 4 * 4;       // [Cin * K * CO], 16-byte aligned
+    float *sa = wsm + Cin * K * CO;                             // [Cin]
+    float *sb = sa + Cin;                                       // [Cin]
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS;
     for (int e = threadIdx.x; e < Cin * K * CO; e += kCodecThreads) {
         const int co = e % CO;
         const int ck = e / CO;
@@ -183,7 +189,7 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
         sb[threadIdx.x] = act.inv_b_of(threadIdx.x);
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < (kCodecThreads + pad) * Cin; e += kCodecThreads) {
+    for (int e = threadIdx.x; e < (ROWS + pad) * Cin; e += kCodecThreads) {
         const int rr = e / Cin, c = e - rr * Cin;
         const int64_t g = row0 - pad + rr;
         float v = 0.f;
@@ -194,52 +200,109 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
         xs[rr * pitch + c] = v;
     }
     __syncthreads();
-    const int64_t row = row0 + threadIdx.x;
-    if (row >= T) return;
-    const int b = stream_of(off, B, row, u);
-    const int64_t local = row - static_cast<int64_t>(off[b]) * u;
-    const float *hrow = pad ? hist + static_cast<int64_t>(slots[b]) * pad * Cin : nullptr;
-    float acc[CO];
+    const int64_t first = row0 + threadIdx.x;
+    if (first >= T) return;
+    // streams of the thread's rows (non-decreasing)
+    int sb_[R];
+    int64_t local[R];
+    {
+        int b = stream_of(off, B, first, u);
 #pragma unroll
-    for (int j = 0; j < CO; ++j) acc[j] = 0.f;
-    for (int k = 0; k < K; ++k) {
-        const int back = (K - 1 - k) * dil;
-        const int64_t src = local - back;
-        const float *xr;
-        int step;
-        if (src >= 0) {
-            xr = xs + (threadIdx.x + pad - back) * pitch;
-            step = 1;
-        } else {
-            xr = hrow + (pad + src) * Cin;
-            step = 1;
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = first + static_cast<int64_t>(r) * kCodecThreads;
+            while (b + 1 < B && static_cast<int64_t>(off[b + 1]) * u <= row) ++b;
+            sb_[r] = b;
+            local[r] = row - static_cast<int64_t>(off[b]) * u;
         }
-        const float *wk = wsm + k * CO;
-        for (int ci = 0; ci < Cin; ++ci) {
-            const float xv = xr[ci * step];
-            const float4 *w4 = reinterpret_cast<const float4 *>(wk + ci * K * CO);
+    }
+    float acc[R][CO];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < CO; ++j) acc[r][j] = 0.f;
+    // taps read the staged rows through LDS addressing when every row of the wave has
+    // its whole receptive field in the stream's fresh rows (the common case), else through
+    // generic pointers that may point into the history
+    bool staged = true;
+#pragma unroll
+    for (int r = 0; r < R; ++r) staged = staged && local[r] >= pad;
+    auto taps = [&](auto lds_only) {
+        for (int k = 0; k < K; ++k) {
+            const int back = (K - 1 - k) * dil;
+            const float *xr[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int64_t src = local[r] - back;
+                if constexpr (decltype(lds_only)::value)
+                    xr[r] = xs + (threadIdx.x + r * kCodecThreads + pad - back) * pitch;
+                else
+                    xr[r] = src >= 0 ? xs + (threadIdx.x + r * kCodecThreads + pad - back) * pitch
+                                     : hist + (static_cast<int64_t>(slots[sb_[r]]) * pad + pad + src) * Cin;
+            }
+            const float *wk = wsm + k * CO;
+            for (int ci = 0; ci < Cin; ++ci) {
+                float xv[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) xv[r] = xr[r][ci];
+                const float4 *w4 = reinterpret_cast<const float4 *>(wk + ci * K * CO);
+#pragma unroll
+                for (int j = 0; j < CO / 4; ++j) {
+                    const float4 ww = w4[j];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        acc[r][4 * j] += xv[r] * ww.x;
+                        acc[r][4 * j + 1] += xv[r] * ww.y;
+                        acc[r][4 * j + 2] += xv[r] * ww.z;
+                        acc[r][4 * j + 3] += xv[r] * ww.w;
+                    }
+                }
+            }
+        }
+    };
+    if (__all(staged)) taps(std::true_type{});
+    else taps(std::false_type{});
+    const bool vec = Cout == CO && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                     (!res || ((ldres & 3) == 0 && (reinterpret_cast<uintptr_t>(res) & 15) == 0));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = first + static_cast<int64_t>(r) * kCodecThreads;
+        if (row >= T) break;
+        if (vec) {
 #pragma unroll
             for (int j = 0; j < CO / 4; ++j) {
-                const float4 ww = w4[j];
-                acc[4 * j] += xv * ww.x;
-                acc[4 * j + 1] += xv * ww.y;
-                acc[4 * j + 2] += xv * ww.z;
-                acc[4 * j + 3] += xv * ww.w;
+                float4 y = make_float4(acc[r][4 * j], acc[r][4 * j + 1], acc[r][4 * j + 2], acc[r][4 * j + 3]);
+                if (bias) {
+                    y.x += bias[4 * j];
+                    y.y += bias[4 * j + 1];
+                    y.z += bias[4 * j + 2];
+                    y.w += bias[4 * j + 3];
+                }
+                if (res) {
+                    const float4 q = *reinterpret_cast<const float4 *>(res + row * ldres + 4 * j);
+                    y.x += q.x;
+                    y.y += q.y;
+                    y.z += q.z;
+                    y.w += q.w;
+                }
+                *reinterpret_cast<float4 *>(out + row * ldo + 4 * j) = y;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CO; ++j) {
+                if (j >= Cout) break;
+                float y = acc[r][j] + (bias ? bias[j] : 0.f);
+                if (res) y += res[row * ldres + j];
+                out[row * ldo + j] = y;
             }
         }
     }
-#pragma unroll
-    for (int j = 0; j < CO; ++j) {
-        if (j >= Cout) break;
-        float y = acc[j] + (bias ? bias[j] : 0.f);
-        if (res) y += res[row * ldres + j];
-        out[row * ldo + j] = y;
-    }
 }
 
+constexpr int conv_small_rows(int CO) { return CO <= 16 ? 2 : 1; }
+
 size_t conv_small_lds(int Cin, int K, int dil, int CO) {
-    return (static_cast<size_t>(kCodecThreads + (K - 1) * dil) * (Cin + 1) + 3 + static_cast<size_t>(Cin) * K * CO +
-            2 * Cin) * sizeof(float);
+    const size_t rows = static_cast<size_t>(kCodecThreads) * conv_small_rows(CO);
+    return ((rows + (K - 1) * dil) * (Cin + 1) + 3 + static_cast<size_t>(Cin) * K * CO + 2 * Cin) * sizeof(float);
 }
 
 // depthwise causal Conv1d (groups == C): one thread per (row, channel)
@@ -602,10 +665,12 @@ extern "C" int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, cons
     const int co_pad = Cout <= 8 ? 8 : Cout <= 16 ? 16 : Cout <= 32 ? 32 : 64;
     if (groups == 1 && Cin <= 64 && Cout <= 64 && conv_small_lds(Cin, K, dilation, co_pad) <= 150 * 1024) {
         const size_t lds = conv_small_lds(Cin, K, dilation, co_pad);
-        const dim3 grid(static_cast<unsigned>((T + kCodecThreads - 1) / kCodecThreads));
+        const int64_t rows = static_cast<int64_t>(kCodecThreads) * conv_small_rows(co_pad);
+        const dim3 grid(static_cast<unsigned>((T + rows - 1) / rows));
 #define NQ_SMALL(CO)                                                                                              \
-        hipLaunchKernelGGL(conv_small_kernel<CO>, grid, dim3(kCodecThreads), lds, st, x, ldx, T, offsets, B, u, slots,  \
-                           history, w, bias, Cin, Cout, K, dilation, act, residual, ldres, out, ldo)
+        hipLaunchKernelGGL((conv_small_kernel<CO, conv_small_rows(CO)>), grid, dim3(kCodecThreads), lds, st, x, ldx, \
+                           T, offsets, B, u, slots, history, w, bias, Cin, Cout, K, dilation, act, residual, ldres,   \
+                           out, ldo)
         if (co_pad == 8) NQ_SMALL(8);
         else if (co_pad == 16) NQ_SMALL(16);
         else if (co_pad == 32) NQ_SMALL(32);
