@@ -424,6 +424,94 @@ transconv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T_out, const 
     }
 }
 
+// Narrow causal transposed Conv1d (Cout <= 16, stride s): output row r reads input
+// rows r / s and r / s - 1 (the stream's rows are aligned to s at this stage).
+// The workgroup stages the (at most 256 / s + 3) input rows its 256 output rows read,
+// activated once, in LDS (row pitch Cin + 1) with the weights as [ci][co][2s];
+// the first output rows of a stream add its carried overlap instead of an
+// earlier input row.  Outputs move as float4 when the row stride allows it.
+template <int CO>
+__global__ void __launch_bounds__(kCodecThreads)
+transconv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T_out, const int32_t *__restrict__ off,
+                       int B, int u_in, int s, const int32_t *__restrict__ slots, const float *__restrict__ overlap,
+                       const float *__restrict__ w, const float *__restrict__ bias, int Cin, int Cout, Act act,
+                       float *__restrict__ out, int64_t ldo) {
+    extern __shared__ float lds[];
+    const int ks = 2 * s;
+    const int pitch = Cin + 1;
+    const int n_max = kCodecThreads / s + 3;  // >= the staged rows for every stride
+    float *xs = lds;                                    // [n_max * pitch]
+    float *tw = xs + (n_max * pitch + 3) / 4 * 4;       // [Cin][CO][2s]
+    float *sa = tw + Cin * CO * ks;                     // [Cin]
+    float *sb = sa + Cin;                               // [Cin]
+    const int64_t T_in = T_out / s;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kCodecThreads;
+    const int64_t last = row0 + kCodecThreads - 1 < T_out ? row0 + kCodecThreads - 1 : T_out - 1;
+    const int64_t in0 = row0 / s - 1;  // staged input row 0 (may be -1)
+    const int n_in = static_cast<int>(last / s - in0 + 1);
+    for (int e = threadIdx.x; e < Cin * CO * ks; e += kCodecThreads) {
+        const int ci = e / (CO * ks);
+        const int rem = e - ci * CO * ks;
+        const int co = rem / ks, k = rem - co * ks;
+        tw[e] = co < Cout ? w[(static_cast<int64_t>(ci) * Cout + co) * ks + k] : 0.f;
+    }
+    if (act.alpha && threadIdx.x < Cin) {
+        sa[threadIdx.x] = act.a_of(threadIdx.x);
+        sb[threadIdx.x] = act.inv_b_of(threadIdx.x);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < n_in * Cin; e += kCodecThreads) {
+        const int rr = e / Cin, c = e - rr * Cin;
+        const int64_t g = in0 + rr;
+        float v = 0.f;
+        if (g >= 0 && g < T_in) {
+            v = x[g * ldx + c];
+            if (act.alpha) v = snake(v, sa[c], sb[c]);
+        }
+        xs[rr * pitch + c] = v;
+    }
+    __syncthreads();
+    const int64_t row = row0 + threadIdx.x;
+    if (row >= T_out) return;
+    const int u_out = u_in * s;
+    const int b = stream_of(off, B, row, u_out);
+    const int64_t gi = row / s;
+    const int j = static_cast<int>(row - gi * s);
+    const bool first = gi == static_cast<int64_t>(off[b]) * u_in;  // the stream's first input row
+    const float *x1 = xs + (gi - in0) * pitch;
+    const float *x0 = x1 - pitch;
+    float acc[CO];
+#pragma unroll
+    for (int q = 0; q < CO; ++q) acc[q] = 0.f;
+    for (int ci = 0; ci < Cin; ++ci) {
+        const float a1 = x1[ci], a0 = first ? 0.f : x0[ci];
+        const float *wr = tw + ci * CO * ks;
+#pragma unroll
+        for (int q = 0; q < CO; ++q) acc[q] += a1 * wr[q * ks + j] + a0 * wr[q * ks + j + s];
+    }
+    const float *ov = overlap + (static_cast<int64_t>(slots[b]) * s + j) * Cout;
+    float y[CO];
+#pragma unroll
+    for (int q = 0; q < CO; ++q) {
+        y[q] = acc[q] + (bias && q < Cout ? bias[q] : 0.f);
+        if (first && q < Cout) y[q] += ov[q];
+    }
+    if (Cout == CO && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+#pragma unroll
+        for (int q = 0; q < CO; q += 4)
+            *reinterpret_cast<float4 *>(out + row * ldo + q) = make_float4(y[q], y[q + 1], y[q + 2], y[q + 3]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < CO; ++q)
+            if (q < Cout) out[row * ldo + q] = y[q];
+    }
+}
+
+size_t transconv_small_lds(int Cin, int s, int CO) {
+    const size_t n_max = kCodecThreads / s + 3;
+    return ((n_max * (Cin + 1) + 3) / 4 * 4 + static_cast<size_t>(Cin) * CO * 2 * s + 2 * Cin) * sizeof(float);
+}
+
 // new overlap[j, co] = act(x[F - 1]) . W[:, co, s + j]; thread per (stream, j, co)
 __global__ void __launch_bounds__(kCodecThreads)
 overlap_update_kernel(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ off, int B, int u_in,
@@ -714,6 +802,22 @@ extern "C" int nq_codec_causal_transconv(const float *x, int64_t ldx, int64_t T_
     const int cg = Cout <= 16 ? 1 : Cout <= 32 ? 2 : 4;
     const int rows = kCodecThreads / cg;
     const int64_t T_out = T_in * stride_s;
+    const int co_pad = Cout <= 8 ? 8 : 16;
+    if (Cout <= 16 && transconv_small_lds(Cin, stride_s, co_pad) <= 64 * 1024) {
+        const size_t lds = transconv_small_lds(Cin, stride_s, co_pad);
+        const dim3 grid(static_cast<unsigned>((T_out + kCodecThreads - 1) / kCodecThreads));
+        if (co_pad == 8)
+            hipLaunchKernelGGL(transconv_small_kernel<8>, grid, dim3(kCodecThreads), lds, st, x, ldx, T_out, offsets, B,
+                               u_in, stride_s, slots, overlap, w, bias, Cin, Cout, act, out, ldo);
+        else
+            hipLaunchKernelGGL(transconv_small_kernel<16>, grid, dim3(kCodecThreads), lds, st, x, ldx, T_out, offsets,
+                               B, u_in, stride_s, slots, overlap, w, bias, Cin, Cout, act, out, ldo);
+        if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+        hipLaunchKernelGGL(overlap_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * stride_s * Cout)),
+                           dim3(kCodecThreads), 0, st, x, ldx, offsets, B, u_in, stride_s, slots, overlap, w, Cin, Cout,
+                           act);
+        return NQ_LAUNCH_STATUS();
+    }
     const size_t lds = static_cast<size_t>(kConvCi) * cg * 16 * 2 * stride_s * sizeof(float);
     if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
     dim3 grid(static_cast<unsigned>((T_out + rows - 1) / rows), static_cast<unsigned>((Cout + cg * 16 - 1) / (cg * 16)));
