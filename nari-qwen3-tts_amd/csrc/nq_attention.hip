@@ -1478,8 +1478,11 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     // contributors' maxima are read at once and the row maximum taken first,
     // then every (l, o) is read independently and added with its scale in
     // wave order, so the merge costs a few LDS round trips instead of one
-    // chain per contributor (and stays deterministic).
-    constexpr int EPL = G * D / kWave;
+    // chain per contributor (and stays deterministic).  The work is dealt to
+    // every wave as (piece, 64 outputs) units, one output per lane; a split
+    // piece (partial to global memory, then its arrival counted) stays one
+    // unit of a whole wave.  Each output's arithmetic is the same either way.
+    constexpr int EPL = G * D / kWave;  // outputs per lane for a whole piece; also 64-output units per piece
     constexpr int V = EPL < 4 ? EPL : 4;
     constexpr int NG = EPL / V;
     // wave span starts in registers; the wave whose span holds bin-local block b
@@ -1493,53 +1496,59 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         for (int i = 1; i < kBinWaves; ++i) w += wsp[i] <= b ? 1 : 0;
         return w;
     };
-    for (int sl = wave; sl < nslots; sl += kBinWaves) {
+    // merge VV consecutive outputs from e0 of the piece in bin-local blocks [a, b) held by waves w0..w1
+    auto merge = [&](auto vtag, int sl, int a, int w0, int w1, int e0) {
+        constexpr int VV = decltype(vtag)::value;
+        const int jj = e0 / D;
+        // wave w contributes when w0 <= w <= w1 and its span is not empty (bins
+        // of < 16 blocks); its partial of this piece is its first slot when the
+        // piece starts in its span, else its second.  Every slot read stays
+        // inside s_part; a non-contributor's value (its slot may never have
+        // been written) is dropped by a select, never multiplied in.
+        float mk[kBinWaves];
+        int base[kBinWaves];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kBinWaves; ++w) {
+            const bool on = w >= w0 && w <= w1 && wsp[w] != wsp[w + 1];
+            base[w] = (w * 2 + (a > wsp[w] ? 1 : 0)) * kPart;
+            const float m = s_part[base[w] + G * D + 2 * jj];
+            mk[w] = on ? m : -INFINITY;
+            mx = fmaxf(mx, mk[w]);
+        }
+        float ls = 0.f, os[VV];
+#pragma unroll
+        for (int v = 0; v < VV; ++v) os[v] = 0.f;
+#pragma unroll
+        for (int w = 0; w < kBinWaves; ++w) {
+            const bool on = mk[w] != -INFINITY;
+            const float sc = on ? exp2f(mk[w] - mx) : 0.f;
+            const float *pp = s_part + base[w];
+            const float lk = pp[G * D + 2 * jj + 1];
+            ls += on ? lk * sc : 0.f;
+#pragma unroll
+            for (int v = 0; v < VV; ++v) {
+                const float ov = pp[e0 + v];
+                os[v] += on ? ov * sc : 0.f;
+            }
+        }
+        bin_store<D, G, VV>(os, mx, ls, e0, s_piece[sl].w >= 0, s_pid[sl], h, s_rope[sl].x, Hq, out, o_s0, o_s1,
+                            piece_ml, piece_o);
+    };
+    for (int u = wave; u < nslots * EPL; u += kBinWaves) {
+        const int sl = u / EPL, unit = u - sl * EPL;
         const int a = s_start[sl], b = s_start[sl + 1];
         if (a == b) continue;
         const int w0 = wave_of(a), w1 = wave_of(b - 1);
         if (w0 == w1) continue;  // finished by its wave
         const int4 pc = s_piece[sl];
-        const int query = s_rope[sl].x;
-        for (int grp = 0; grp < NG; ++grp) {
-            const int e0 = (grp * kWave + lane) * V;
-            const int jj = e0 / D;
-            // wave w contributes when w0 <= w <= w1 and its span is not empty (bins
-            // of < 16 blocks); its partial of this piece is its first slot when the
-            // piece starts in its span, else its second.  Every slot read stays
-            // inside s_part; a non-contributor's value (its slot may never have
-            // been written) is dropped by a select, never multiplied in.
-            float mk[kBinWaves];
-            int base[kBinWaves];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int w = 0; w < kBinWaves; ++w) {
-                const bool on = w >= w0 && w <= w1 && wsp[w] != wsp[w + 1];
-                base[w] = (w * 2 + (a > wsp[w] ? 1 : 0)) * kPart;
-                const float m = s_part[base[w] + G * D + 2 * jj];
-                mk[w] = on ? m : -INFINITY;
-                mx = fmaxf(mx, mk[w]);
-            }
-            float ls = 0.f, os[V];
-#pragma unroll
-            for (int v = 0; v < V; ++v) os[v] = 0.f;
-#pragma unroll
-            for (int w = 0; w < kBinWaves; ++w) {
-                const bool on = mk[w] != -INFINITY;
-                const float sc = on ? exp2f(mk[w] - mx) : 0.f;
-                const float *pp = s_part + base[w];
-                const float lk = pp[G * D + 2 * jj + 1];
-                ls += on ? lk * sc : 0.f;
-#pragma unroll
-                for (int v = 0; v < V; ++v) {
-                    const float ov = pp[e0 + v];
-                    os[v] += on ? ov * sc : 0.f;
-                }
-            }
-            bin_store<D, G, V>(os, mx, ls, e0, pc.w >= 0, s_pid[sl], h, query, Hq, out, o_s0, o_s1, piece_ml,
-                               piece_o);
+        if (pc.w < 0) {
+            merge(std::integral_constant<int, 1>(), sl, a, w0, w1, unit * kWave + lane);
+            continue;
         }
-        if (pc.w >= 0)
-            bin_arrive<D, G>(pc, h, num_kv_heads, query, lane, arrivals, piece_ml, piece_o, out, o_s0, o_s1);
+        if (unit != 0) continue;
+        for (int grp = 0; grp < NG; ++grp) merge(std::integral_constant<int, V>(), sl, a, w0, w1, (grp * kWave + lane) * V);
+        bin_arrive<D, G>(pc, h, num_kv_heads, s_rope[sl].x, lane, arrivals, piece_ml, piece_o, out, o_s0, o_s1);
     }
 }
 
