@@ -419,34 +419,16 @@ int nq_silu_mul(const uint16_t *gate_up, uint16_t *out, int rows, int width, voi
  * slice order, so the result is deterministic and the same for every
  * epilogue.  Requires N % 64 == 0 and K % 512 == 0 (K % 256 when M > 64):
  * otherwise NQ_ERR_UNSUPPORTED (nq_linear_splits returns -1).  Row strides in
- * elements; x, w, out, residual, norm_weight 16-byte aligned.  w_s0 ==
- * NQ_WEIGHT_PACKED reads W in the fragment layout nq_pack_linear_weight
- * writes (same results, bit for bit).
+ * elements; x, w, out, residual, norm_weight 16-byte aligned.
  * nq_linear_workspace_bytes gives the workspace size (0 = none needed).
  */
 enum nq_epilogue { NQ_EPI_NONE = 0, NQ_EPI_ADD_RMSNORM = 1, NQ_EPI_SILU_MUL = 2, NQ_EPI_PARTIALS = 3 };
-#define NQ_WEIGHT_PACKED (-1)
 int nq_linear_splits(int M, int N, int K);
 int64_t nq_linear_workspace_bytes(int M, int N, int K, int epilogue);
 int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M, int N, int K,
               int epilogue, const uint16_t *bias, uint16_t *out, int64_t o_s0, uint16_t *residual,
               const uint16_t *norm_weight, float eps, void *workspace, int64_t workspace_bytes,
               void *stream);
-
-/*
- * Weight-load-time layout change for the projections above (no counterpart in
- * the reference, whose nn.Linear weights stay row-major): W [N, K] bf16 (row
- * stride w_s0 elements) -> packed [N / 16][K / 32][64][8] bf16, where entry
- * (g, s, lane) holds W[16 g + lane % 16][32 s + 8 (lane / 16) .. + 8], the
- * per-lane operand of one 16x16x32 MFMA step.  A projection wave then reads
- * its rows over a K slice as one contiguous run instead of 64-byte pieces of
- * 16 rows.  N % 16 == 0 and K % 32 == 0 (else NQ_ERR_UNSUPPORTED); both
- * pointers 16-byte aligned; `packed` holds N * K elements.  Currently
- * disabled: this entry point and NQ_WEIGHT_PACKED strides return
- * NQ_ERR_UNSUPPORTED (a GPU run that exercised them ended in an unexplained
- * device fault).
- */
-int nq_pack_linear_weight(const uint16_t *w, int64_t w_s0, int N, int K, uint16_t *packed, void *stream);
 
 /*
  * Decode attention with the q/k norm + RoPE + K/V write fused in, for bindings
@@ -513,8 +495,7 @@ int nq_add_rmsnorm_fp8(const uint16_t *hidden, uint16_t *residual, const uint16_
  * nq_linear with NQ_EPI_ADD_RMSNORM whose normalised output is stored as
  * nq_add_rmsnorm_fp8 stores it: the o_proj + post-attention add-RMSNorm of a
  * talker layer with FP8 gate/up.  N % 128 == 0; workspace as
- * nq_linear_workspace_bytes(M, N, K, NQ_EPI_ADD_RMSNORM); w_s0 may be
- * NQ_WEIGHT_PACKED as for nq_linear.
+ * nq_linear_workspace_bytes(M, N, K, NQ_EPI_ADD_RMSNORM).
  */
 int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const uint16_t *w, int64_t w_s0, int M,
                               int N, int K, uint16_t *residual, const uint16_t *norm_weight, float eps,

@@ -28,7 +28,6 @@ NQ_EPI_NONE = 0
 NQ_EPI_ADD_RMSNORM = 1
 NQ_EPI_SILU_MUL = 2
 NQ_EPI_PARTIALS = 3
-NQ_WEIGHT_PACKED = -1
 NQ_ATTN_DECODE = 1
 NQ_ATTN_PREFILL = 2
 NQ_NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -77,7 +76,6 @@ _SIGNATURES: dict[str, list] = {
     "nq_linear_splits": [_I, _I, _I],
     "nq_linear_workspace_bytes": [_I, _I, _I, _I],
     "nq_linear": [_P, _L, _P, _L, _I, _I, _I, _I, _P, _P, _L, _P, _P, _F, _P, _L, _P],
-    "nq_pack_linear_weight": [_P, _L, _I, _I, _P, _P],
     "nq_quantize_fp8_blocks": [_P, _L, _I, _I, _P, _L, _P, _L, _P],
     "nq_quantize_fp8_rows": [_P, _L, _I, _I, _P, _L, _P, _L, _P],
     "nq_add_rmsnorm_fp8": [_P, _P, _P, _I, _I, _F, _P, _L, _P, _L, _P],

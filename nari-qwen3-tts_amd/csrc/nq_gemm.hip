@@ -42,24 +42,14 @@ constexpr int x_pitch() {
     return KS + 16;
 }
 
-// Weights of one wave: its 16 rows over the K slice, one 32-k MFMA step per load.
-// Row-major W: lane (r16, kq) reads row n_row at k0 + 32 j + 8 kq, 64 bytes of
-// each of 16 rows per load.  Packed W (nq_pack_linear_weight): fragments
-// [N / 16][K / 32][64 lanes][8], so the wave's loads are one contiguous run of
-// 1 KB each; w_s0 then holds the fragment-row stride K * 16.
-template <int KS, bool kPacked>
+// Weights of one wave: its 16 rows over the K slice, one 32-k MFMA step per load:
+// lane (r16, kq) reads row n_row at k0 + 32 j + 8 kq, 64 bytes of each of 16 rows per load.
+template <int KS>
 __device__ __forceinline__ void gemm_load_w(uint4 (&wr)[KS / 32], const uint16_t *__restrict__ w, int64_t w_s0,
                                             int n_row, int k0, int kq) {
-    if constexpr (kPacked) {
-        const uint16_t *frag = w + static_cast<int64_t>(n_row >> 4) * w_s0 + (k0 / 32) * 512 +
-                               (kq * 16 + (n_row & 15)) * 8;
+    const uint16_t *row = w + static_cast<int64_t>(n_row) * w_s0 + k0 + kq * 8;
 #pragma unroll
-        for (int j = 0; j < KS / 32; ++j) wr[j] = *reinterpret_cast<const uint4 *>(frag + j * 512);
-    } else {
-        const uint16_t *row = w + static_cast<int64_t>(n_row) * w_s0 + k0 + kq * 8;
-#pragma unroll
-        for (int j = 0; j < KS / 32; ++j) wr[j] = *reinterpret_cast<const uint4 *>(row + j * 32);
-    }
+    for (int j = 0; j < KS / 32; ++j) wr[j] = *reinterpret_cast<const uint4 *>(row + j * 32);
 }
 
 // MFMA chain of one 16-column tile over the staged slice, then its store:
@@ -108,7 +98,7 @@ __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint
 // Workgroup (bx, by): K slice by, 64-column bands bx*nb .. bx*nb + nb - 1.
 // The X slice is staged once; wave w computes columns band*64 + w*16 + 0..15
 // of each band while the next band's weights are already in flight.
-template <int MT, int KS, bool kPacked>
+template <int MT, int KS>
 __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KS > 512 ? 1 : 2, 2)))
 gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w,
             int64_t w_s0, int N, int nb, uint16_t *__restrict__ out, int64_t o_s0,
@@ -148,7 +138,7 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
 
     // 2. the first band's weights, all in flight together
     uint4 wa[kSteps], wb[kSteps];
-    gemm_load_w<KS, kPacked>(wa, w, w_s0, band0 * 64 + wave * 16 + r16, k0, kq);
+    gemm_load_w<KS>(wa, w, w_s0, band0 * 64 + wave * 16 + r16, k0, kq);
     // keep every weight load ahead of the wait for the X block
     __builtin_amdgcn_sched_barrier(0);
 
@@ -166,10 +156,10 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     // after the barrier, and the weight stream then waits for the X block.
     for (int b = 0;; b += 2) {
         const int col_a = (band0 + b) * 64 + wave * 16;
-        if (b + 1 < nb) gemm_load_w<KS, kPacked>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
+        if (b + 1 < nb) gemm_load_w<KS>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
         gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part, bias);
         if (b + 1 >= nb) break;
-        if (b + 2 < nb) gemm_load_w<KS, kPacked>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
+        if (b + 2 < nb) gemm_load_w<KS>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
         gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part, bias);
         if (b + 2 >= nb) break;
     }
@@ -224,26 +214,14 @@ int slice_of(int M, int N, int K) {
 }
 
 
-// w_s0 == NQ_WEIGHT_PACKED selects the packed-fragment layout.  The packed
-// path is switched off (its entry points return NQ_ERR_UNSUPPORTED): the one
-// GPU run that exercised it ended in a device fault whose cause has not been
-// found, although an emulation of its index arithmetic keeps every access in
-// bounds.
-constexpr bool kPackedWeightsEnabled = false;
-
 template <int MT, int KS>
 void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
                  uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
     const int bands = N / 64, S = K / KS;
     const int nb = bands_per_wg(bands, S);
     dim3 grid(bands / nb, S);
-    if (w_s0 == NQ_WEIGHT_PACKED) {
-        hipLaunchKernelGGL((gemm_kernel<MT, KS, true>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w,
-                           static_cast<int64_t>(K) * 16, N, nb, out, o_s0, part, bias);
-    } else {
-        hipLaunchKernelGGL((gemm_kernel<MT, KS, false>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N,
-                           nb, out, o_s0, part, bias);
-    }
+    hipLaunchKernelGGL((gemm_kernel<MT, KS>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N, nb, out,
+                       o_s0, part, bias);
 }
 
 // The launch for M rows with the K slice slice_of picks.
@@ -262,24 +240,6 @@ void dispatch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, in
         default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
     }
 #undef NQ_GEMM_SLICES
-}
-
-// Packed weight fragments: vector i of the output is lane (i % 64) of fragment
-// i / 64 = (g, s), holding W[16 g + lane % 16][32 s + 8 (lane / 16) .. + 8].
-__global__ void __launch_bounds__(256)
-pack_linear_kernel(const uint16_t *__restrict__ w, int64_t w_s0, int N, int K, uint16_t *__restrict__ p) {
-    const int64_t total = static_cast<int64_t>(N) * K / 8;
-    const int steps = K / 32;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int lane = static_cast<int>(i & 63);
-        const int64_t frag = i >> 6;
-        const int64_t g = frag / steps;
-        const int s = static_cast<int>(frag - g * steps);
-        const int64_t row = g * 16 + (lane & 15);
-        const int col = s * 32 + (lane >> 4) * 8;
-        *reinterpret_cast<uint4 *>(p + i * 8) = *reinterpret_cast<const uint4 *>(w + row * w_s0 + col);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -459,8 +419,7 @@ extern "C" int nq_linear(const uint16_t *x, int64_t x_s0, const uint16_t *w, int
     NQ_CHECK_ARG(epilogue >= NQ_EPI_NONE && epilogue <= NQ_EPI_PARTIALS);
     const int S = nq_linear_splits(M, N, K);
     if (S < 0) return NQ_ERR_UNSUPPORTED;
-    if (w_s0 == NQ_WEIGHT_PACKED && !kPackedWeightsEnabled) return NQ_ERR_UNSUPPORTED;
-    NQ_CHECK_ARG(x_s0 >= K && x_s0 % 8 == 0 && (w_s0 == NQ_WEIGHT_PACKED || (w_s0 >= K && w_s0 % 8 == 0)));
+    NQ_CHECK_ARG(x_s0 >= K && x_s0 % 8 == 0 && w_s0 >= K && w_s0 % 8 == 0);
     NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0);
     const int out_width = epilogue == NQ_EPI_SILU_MUL ? N / 2 : N;
     if (epilogue != NQ_EPI_PARTIALS) {
@@ -499,8 +458,7 @@ extern "C" int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const 
     NQ_CHECK_ARG(x && w && residual && norm_weight && xq && sx && M > 0 && N > 0 && K > 0);
     const int S = nq_linear_splits(M, N, K);
     if (S < 0 || N % 128 != 0 || N > 8192) return NQ_ERR_UNSUPPORTED;
-    if (w_s0 == NQ_WEIGHT_PACKED && !kPackedWeightsEnabled) return NQ_ERR_UNSUPPORTED;
-    NQ_CHECK_ARG(x_s0 >= K && x_s0 % 8 == 0 && (w_s0 == NQ_WEIGHT_PACKED || (w_s0 >= K && w_s0 % 8 == 0)));
+    NQ_CHECK_ARG(x_s0 >= K && x_s0 % 8 == 0 && w_s0 >= K && w_s0 % 8 == 0);
     NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 == 0);
     NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(norm_weight)) % 16 == 0);
     NQ_CHECK_ARG(xq_s0 >= N && xq_s0 % 8 == 0 && reinterpret_cast<uintptr_t>(xq) % 8 == 0 && sx_s0 >= N / 128);
@@ -511,18 +469,6 @@ extern "C" int nq_linear_add_rmsnorm_fp8(const uint16_t *x, int64_t x_s0, const 
     dispatch_gemm(x, x_s0, M, w, w_s0, N, K, nullptr, 0, part, nullptr, st);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     return launch_add_rmsnorm_partials_fp8(part, S, M, N, residual, norm_weight, eps, xq, xq_s0, sx, sx_s0, st);
-}
-
-extern "C" int nq_pack_linear_weight(const uint16_t *w, int64_t w_s0, int N, int K, uint16_t *packed, void *stream) {
-    if (!kPackedWeightsEnabled) return NQ_ERR_UNSUPPORTED;
-    NQ_CHECK_ARG(w && packed && N > 0 && K > 0 && w_s0 >= K && w_s0 % 8 == 0);
-    NQ_CHECK_ARG((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(packed)) % 16 == 0);
-    if (N % 16 != 0 || K % 32 != 0) return NQ_ERR_UNSUPPORTED;
-    const int64_t vec = static_cast<int64_t>(N) * K / 8;
-    const int64_t blocks = (vec + 255) / 256;
-    hipLaunchKernelGGL(pack_linear_kernel, dim3(static_cast<unsigned>(blocks > 8192 ? 8192 : blocks)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), w, w_s0, N, K, packed);
-    return NQ_LAUNCH_STATUS();
 }
 
 extern "C" int nq_linear_swiglu(const uint16_t *x, int64_t x_s0, int M, const uint16_t *packed, int64_t w_s0, int I,

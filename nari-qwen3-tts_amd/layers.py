@@ -362,44 +362,9 @@ def linear_workspace_bytes(rows: int, out_features: int, in_features: int, epilo
     return n
 
 
-class PackedLinearWeight:
-    """A bf16 projection weight [out, in] stored in the fragment order of the HIP projection kernels
-    (nq_pack_linear_weight): each wave reads its rows over a K slice as one contiguous run.  Every
-    projection below accepts it in place of the row-major weight and gives bit-identical results."""
-
-    def __init__(self, weight: torch.Tensor) -> None:
-        if weight.dtype != torch.bfloat16:
-            raise TypeError("weight must be bf16")
-        if weight.dim() != 2 or weight.stride(1) != 1:
-            raise ValueError("a projection weight is a matrix with unit inner stride")
-        _lib.require_device(weight)
-        n, k = weight.shape
-        if n % 16 or k % 32:
-            raise TypeError(f"packed projection weights need out % 16 == 0 and in % 32 == 0, got {tuple(weight.shape)}")
-        self.shape = (n, k)
-        self.dtype = weight.dtype
-        self.device = weight.device
-        self.data = torch.empty(n * k, dtype=torch.bfloat16, device=weight.device)
-        _lib.call("nq_pack_linear_weight", weight.data_ptr(), weight.stride(0), n, k, self.data.data_ptr(),
-                  _lib.stream(weight.device))
-
-    def numel(self) -> int:
-        return self.data.numel()
-
-
-def pack_linear_weight(weight: torch.Tensor) -> PackedLinearWeight:
-    """Weight-load-time repack of a row-major bf16 projection weight (see PackedLinearWeight)."""
-
-    return PackedLinearWeight(weight)
-
-
 def _weight_arg(weight, k: int) -> tuple[int, int, int]:
-    """(pointer, row stride or NQ_WEIGHT_PACKED, out_features) of a projection weight."""
+    """(pointer, row stride, out_features) of a projection weight."""
 
-    if isinstance(weight, PackedLinearWeight):
-        if weight.shape[1] != k:
-            raise ValueError("weight in_features must match x")
-        return weight.data.data_ptr(), _lib.NQ_WEIGHT_PACKED, weight.shape[0]
     if weight.dtype != torch.bfloat16 or weight.dim() != 2 or weight.stride(1) != 1:
         raise TypeError("linear needs a bf16 2-D weight with unit inner stride")
     if weight.shape[1] != k:
@@ -415,7 +380,7 @@ def _linear(x, weight, epilogue, out, out_width, residual=None, norm_weight=None
         raise ValueError("linear needs 2-D tensors with unit inner stride")
     rows, k = x.shape
     w_ptr, w_s0, n = _weight_arg(weight, k)
-    _lib.require_device(x, weight.data if isinstance(weight, PackedLinearWeight) else weight)
+    _lib.require_device(x, weight)
     need = linear_workspace_bytes(rows, n, k, epilogue)
     out = torch.empty((rows, out_width), dtype=x.dtype, device=x.device) if out is None else out
     if out.shape != (rows, out_width) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
@@ -702,7 +667,6 @@ __all__ = [
     "linear_swiglu",
     "pack_swiglu",
     "FP8",
-    "PackedLinearWeight",
     "embed_add_rmsnorm",
     "gather_sum_rows",
     "linear_rows",
@@ -723,7 +687,6 @@ __all__ = [
     "linear_partials",
     "linear_silu_mul",
     "linear_workspace_bytes",
-    "pack_linear_weight",
     "quantize_fp8_rows",
     "quantize_fp8_weight_blocks",
     "add_rmsnorm",

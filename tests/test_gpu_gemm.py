@@ -161,7 +161,7 @@ def test_linear_bias_single_rounding(nq, device, m, n, k):
     assert bool(((y.float() - ref).abs() <= 8e-3 * ref.abs() + 2e-3).all())
 
 
-_PACKED_OFF = pytest.mark.skip(reason="packed projection weights are switched off: the GPU run that exercised them ended in a device fault whose cause is not found (index arithmetic emulated in bounds)")
+_PACKED_OFF = pytest.mark.skip(reason="the packed projection weight layout (nq_pack_linear_weight) was taken out of the library: the GPU run that exercised it ended in a device fault whose cause was not found (index arithmetic emulated in bounds); these tests of it stay, skipped")
 
 
 @_PACKED_OFF
