@@ -183,6 +183,21 @@ def attention_probe(torch, w, replays: int = 20):
     return avg_ms, kv_bytes + plane_bytes + write_bytes, tokens_per_launch
 
 
+def host_threads() -> int:
+    """Host cores the CPU baselines use: this process's CPU affinity, at most 16 (one GPU's share of
+    the host)."""
+
+    return max(1, min(len(os.sched_getaffinity(0)), 16))
+
+
+def cpu_pool(n: int):
+    """Pin the BLAS thread pool numpy uses to ``n`` threads for a CPU-baseline run."""
+
+    from threadpoolctl import threadpool_limits
+
+    return threadpool_limits(limits=n)
+
+
 def cpu_baseline(torch, np, w, budget_s: float = 10.0):
     """The oracle decode step on the host cores: all 28 layers, repeated (up to three passes) until the
     budget is spent, reported per 28-layer step."""
@@ -191,12 +206,6 @@ def cpu_baseline(torch, np, w, budget_s: float = 10.0):
     from oracle import planner as o_plan
     from oracle import talker as o_talker
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001 - threadpoolctl is optional
-        cores = 1
     kv, cfg, step, wts = w["kv"], w["cfg"], w["step"], w["weights"]
     states = [kv.state(r) for r in w["rids"]]
     # compact copy of the pages the rows own (+ one new page per row if needed)
@@ -223,6 +232,8 @@ def cpu_baseline(torch, np, w, budget_s: float = 10.0):
                 rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta)
     done = 0
     elapsed = 0.0
+    cores = host_threads()
+    pool = cpu_pool(cores)
     for step_layer in range(3 * cfg.num_layers):
         li = step_layer % cfg.num_layers
         L = wts.layers[li]
@@ -243,6 +254,7 @@ def cpu_baseline(torch, np, w, budget_s: float = 10.0):
         done += 1
         if elapsed >= budget_s and done >= cfg.num_layers:
             break
+    pool.unregister()
     step_s = elapsed / done * cfg.num_layers
     return dict(value=ROWS / step_s, unit="tok/s", cores=int(cores), kind="port",
                 sample=f"oracle decode step (numpy): {done} layer passes ({cfg.num_layers} layers per step) for {ROWS} "
@@ -444,18 +456,15 @@ def code_predictor_cpu_baseline(torch, np, weights, frame, budget_s: float = 10.
                 rope_theta=c.rope_theta, num_code_groups=c.num_code_groups)
     tokens = host(frame.tokens)
     rows, done, elapsed = 16, 0, 0.0
+    cores = host_threads()
+    pool = cpu_pool(cores)
     while elapsed < budget_s and done < CP_ROWS:
         sl = slice(done, done + rows)
         t0 = time.perf_counter()
         o_cp.whole_frame(hw, hcfg, host(frame.layer0_token)[sl], host(frame.past_hidden)[sl], tokens[:, sl])
         elapsed += time.perf_counter() - t0
         done += rows
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001 - threadpoolctl is optional
-        cores = 1
+    pool.unregister()
     return dict(value=done / elapsed, unit="frames/s", cores=int(cores), kind="port",
                 sample=f"oracle frame (numpy, teacher-forced) for {done} of {CP_ROWS} rows in {elapsed:.1f}s")
 
@@ -566,18 +575,15 @@ def codec_cpu_baseline(np, weights, cfg, budget_s: float = 10.0) -> dict:
     rng = np.random.default_rng(CODEC_SEED + 1)
     st = o_codec.empty_state(cfg.as_dict())
     done, elapsed = 0, 0.0
+    cores = host_threads()
+    pool = cpu_pool(cores)
     while elapsed < budget_s:
         codes = rng.integers(0, cfg.codebook_size, size=(12, cfg.num_quantizers))
         t0 = time.perf_counter()
         o_codec.decode_incremental(w, cfg.as_dict(), codes, st)
         elapsed += time.perf_counter() - t0
         done += 12
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001 - threadpoolctl is optional
-        cores = 1
+    pool.unregister()
     return dict(value=done * cfg.samples_per_frame / elapsed, unit="samples/s", cores=int(cores), kind="port",
                 sample=f"oracle codec (numpy) over {done} frames of one stream in 12-frame chunks, {elapsed:.1f}s")
 
