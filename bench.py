@@ -37,9 +37,9 @@ POOL_PAGES = 32768
 KV_LO, KV_HI = 64, 2048
 SEED = 1002
 # HBM bytes one fused decode-attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE
-# counter passes in profiles/paged_attention_talker_decode_b64.md (scaled by a 512 MiB device copy:
-# x2.0 and x1.0).
-ATTENTION_TRAFFIC_BYTES = 254_003_756
+# counter passes in profiles/paged_attention_talker_decode_b64.md (median over the launches of the timed
+# steps; scaled by a 512 MiB device copy: x2.0 and x1.0).
+ATTENTION_TRAFFIC_BYTES = 272_864_870
 
 
 def log(*a):
