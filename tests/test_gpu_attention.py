@@ -143,6 +143,37 @@ def test_mixed_prefill_and_decode_rows(nq, device):
     kv.abort(pubs)
 
 
+def test_mixed_batch_full_config3(nq, device):
+    """The mixed workload at full size: 16 prefill chunks (qo U{32..256} over prior context U{0..512})
+    and 112 decode rows (KV U{64..2048}), page size 16, pages drawn from a randomly permuted pool,
+    planned on the GPU; prefill tiles and decode bins run as the mixed bench leg runs them (two streams,
+    fork/join) and every output row is checked against the oracle."""
+
+    rng = np.random.default_rng(1003)
+    kv = make_kv(nq, device, pages=16384, ps=16, scratch=256)
+    g = torch.Generator(device=device)
+    g.manual_seed(1003)
+    kv.storage.copy_(torch.randn(kv.storage.shape, generator=g, device=device).to(torch.bfloat16))
+    pre_prior = rng.integers(0, 513, size=16)
+    pre_adv = rng.integers(32, 257, size=16)
+    dec_prior = rng.integers(64, 2049, size=112)
+    rids = adopt_random(kv, rng, np.concatenate([pre_prior, dec_prior]))
+    advances = tuple(int(a) for a in np.concatenate([pre_adv, np.ones(112, dtype=np.int64)]))
+    key = PrefillKey(128, sum(advances))
+    ctx = kv.create_prefill(key, slot=0)
+    pubs = kv.prepare_prefill(ctx, key, tuple(rids), advances)
+    q = torch.randn(key.token_capacity, 16, 128, generator=g, device=device).to(torch.bfloat16)
+    out = _run(nq, ctx, q)
+    n = sum(advances)
+    got, want = to_np(out)[:n], _oracle(ctx, q)[:n]
+    mx, mean = attention_error(got, want)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"max {mx:.3g} mean {mean:.3g}"
+    # the decode rows (the last 112 query tokens) on their own as well
+    mx, mean = attention_error(got[-112:], want[-112:])
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"decode rows: max {mx:.3g} mean {mean:.3g}"
+    kv.abort(pubs)
+
+
 @pytest.mark.parametrize("ps,priors,advances", [
     (16, [0, 17, 300, 5], [2, 33, 64, 100]),
     (16, [512, 0], [256, 255]),
