@@ -55,10 +55,13 @@ enum MetaSlot {
 };
 
 // Decode bins: the fused decode kernel runs kBinWgs workgroups of kBinWaves
-// waves (one workgroup per CU, the same 4096 waves as the stream kernel);
-// workgroup (bin, kv head) owns whole (decode row, kv head) items.
+// waves (one workgroup per CU); workgroup (bin, kv head) owns whole (decode
+// row, kv head) items.  Eight waves of at most 128 VGPRs (two per SIMD) measured
+// faster than 16, 12 or 4 on the batch-64 step (55.5-55.8 us against 56.3-57.7,
+// 56.8-57.3 and 58.9-59.7 per launch), and leave half of each SIMD's registers
+// to a workgroup of another kernel.
 constexpr int kBinWgs = 256;
-constexpr int kBinWaves = 16;
+constexpr int kBinWaves = 8;
 constexpr int kBinThreads = kBinWaves * kWave;
 constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
 constexpr int kBinSortCap = 2048;  // pieces the plan can sort
@@ -1100,14 +1103,14 @@ merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads,
 // ---------------------------------------------------------------------------
 // Fused decode kernel over bins, for batches of decode rows.
 //
-// Workgroup (bin b, kv head h) = blockIdx b * Hkv + h, 16 waves.  Prologue:
+// Workgroup (bin b, kv head h) = blockIdx b * Hkv + h, kBinWaves waves.  Prologue:
 // for every piece of the bin the G query heads of kv head h of its row are
 // normalised and rotated from the packed QKV projection's split-K planes into
 // LDS, and the piece holding the row's last block also writes the new token's
 // K (normalised, rotated) and V into its cache slot -- the q/k norm + RoPE +
 // KV write of nq_qkv_partials_norm_rope_kv_write, through the same
 // norm_rope_pair arithmetic.  After a barrier the bin's blocks (its pieces'
-// blocks in slot order) are cut into 16 equal spans, one per wave, and
+// blocks in slot order) are cut into kBinWaves equal spans, one per wave, and
 // streamed as in the stream kernel.  A piece wholly inside a span is finished
 // in registers; the (at most two) boundary pieces of a span leave their
 // (m, l, acc) in LDS and are merged in wave order after a second barrier.  A
@@ -1208,7 +1211,7 @@ __device__ __forceinline__ void bin_arrive(int4 pc, int h, int num_kv_heads, int
 }
 
 template <int D, int G, bool kSmallPages, bool kQIn = false>
-__global__ void __launch_bounds__(kBinThreads)
+__global__ void __launch_bounds__(kBinThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
 bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
                   int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
                   int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out, int64_t o_s0,
