@@ -54,15 +54,17 @@ enum MetaSlot {
     kMetaSplitRows = 9, kMetaPItems = 10, kMetaCount = 16
 };
 
-// Decode bins: the fused decode kernel runs kBinWgs workgroups of kBinWaves
-// waves (one workgroup per CU); workgroup (bin, kv head) owns whole (decode
-// row, kv head) items.  Eight waves of at most 128 VGPRs (two per SIMD) measured
-// faster than 16, 12 or 4 on the batch-64 step (55.5-55.8 us against 56.3-57.7,
-// 56.8-57.3 and 58.9-59.7 per launch), and leave half of each SIMD's registers
-// to a workgroup of another kernel.
+// Decode bins: the fused decode kernel runs kBinWgs workgroups (one per CU);
+// workgroup (bin, kv head) owns whole (decode row, kv head) items.  Its waves
+// (at most 128 VGPRs each) are kBinWavesSmall for launches of up to
+// kBinSmallRows rows and kBinWavesLarge above: on the batch-64 step eight
+// waves measured 55.5-55.8 us per launch against 56.3-57.7 for sixteen (12:
+// 56.8-57.3, 4: 58.9-59.7), while the 112 decode rows of the mixed batch took
+// 133.5-135.5 us with eight and 104.8-105.9 with sixteen.
 constexpr int kBinWgs = 256;
-constexpr int kBinWaves = 8;
-constexpr int kBinThreads = kBinWaves * kWave;
+constexpr int kBinWavesSmall = 8;
+constexpr int kBinWavesLarge = 16;
+constexpr int kBinSmallRows = 64;
 constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
 constexpr int kBinSortCap = 2048;  // pieces the plan can sort
 constexpr bool kDecodeBins = true;  // decode rows of general batches through the bins (else stream + merge)
@@ -1103,14 +1105,14 @@ merge_stream_kernel(const char *__restrict__ ws, PlanLayout L, int num_kv_heads,
 // ---------------------------------------------------------------------------
 // Fused decode kernel over bins, for batches of decode rows.
 //
-// Workgroup (bin b, kv head h) = blockIdx b * Hkv + h, kBinWaves waves.  Prologue:
+// Workgroup (bin b, kv head h) = blockIdx b * Hkv + h, W waves.  Prologue:
 // for every piece of the bin the G query heads of kv head h of its row are
 // normalised and rotated from the packed QKV projection's split-K planes into
 // LDS, and the piece holding the row's last block also writes the new token's
 // K (normalised, rotated) and V into its cache slot -- the q/k norm + RoPE +
 // KV write of nq_qkv_partials_norm_rope_kv_write, through the same
 // norm_rope_pair arithmetic.  After a barrier the bin's blocks (its pieces'
-// blocks in slot order) are cut into kBinWaves equal spans, one per wave, and
+// blocks in slot order) are cut into W equal spans, one per wave, and
 // streamed as in the stream kernel.  A piece wholly inside a span is finished
 // in registers; the (at most two) boundary pieces of a span leave their
 // (m, l, acc) in LDS and are merged in wave order after a second barrier.  A
@@ -1210,8 +1212,8 @@ __device__ __forceinline__ void bin_arrive(int4 pc, int h, int num_kv_heads, int
     if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int G, bool kSmallPages, bool kQIn = false>
-__global__ void __launch_bounds__(kBinThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+template <int D, int G, bool kSmallPages, bool kQIn, int W>
+__global__ void __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(4, 8)))
 bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
                   int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
                   int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out, int64_t o_s0,
@@ -1225,8 +1227,8 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     __shared__ int s_start[kBinMaxSlots + 1];
     __shared__ int s_n;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[kBinMaxSlots * G * D];
-    __shared__ __attribute__((aligned(16))) float s_part[kBinWaves * 2 * kPart];
-    __shared__ int s_wsp[kBinWaves + 1];  // wave span starts
+    __shared__ __attribute__((aligned(16))) float s_part[W * 2 * kPart];
+    __shared__ int s_wsp[W + 1];  // wave span starts
 
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
     const int NB = bins_per_head(num_kv_heads);
@@ -1281,7 +1283,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     const int nslots = s_n;
     const int NBB = s_start[nslots];
     if (NBB == 0) return;
-    if (threadIdx.x <= kBinWaves) s_wsp[threadIdx.x] = span_start(threadIdx.x, NBB, kBinWaves);
+    if (threadIdx.x <= W) s_wsp[threadIdx.x] = span_start(threadIdx.x, NBB, W);
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -1290,8 +1292,8 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     // the wave's span of the bin's blocks and its first 64 block descriptors
     // (one per lane: lane -> bin-local block -> global block), fetched now so
     // that they arrive during the RoPE work below
-    const int s0 = span_start(wave, NBB, kBinWaves);
-    const int s1 = span_start(wave + 1, NBB, kBinWaves);
+    const int s0 = span_start(wave, NBB, W);
+    const int s1 = span_start(wave + 1, NBB, W);
     auto global_block = [&](int lb) {
         int sl = 0;
         while (sl + 1 < nslots && s_start[sl + 1] <= lb) ++sl;
@@ -1316,7 +1318,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     }
     if constexpr (kQIn) {
         // q-input mode: the bin's rotated query heads into LDS, one wave per (piece, head)
-        for (int u = wave; u < nslots * G; u += kBinWaves) {
+        for (int u = wave; u < nslots * G; u += W) {
             const int sl = u / G, j = u - sl * G;
             const int64_t tok = s_rope[sl].x;
             if (tok >= rs.tokens) {
@@ -1327,7 +1329,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
             for (int d = lane; d < D; d += kWave) s_q[(sl * G + j) * D + d] = qh[d];
         }
     }
-    for (int u = wave; u < (kQIn ? 0 : nslots * (G + 2)); u += kBinWaves) {
+    for (int u = wave; u < (kQIn ? 0 : nslots * (G + 2)); u += W) {
         const int sl = u / (G + 2), kind = u - sl * (G + 2);
         const int4 rp = s_rope[sl];
         const bool row_last = rp.w < 0;
@@ -1490,13 +1492,13 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
     constexpr int NG = EPL / V;
     // wave span starts in registers; the wave whose span holds bin-local block b
     // is the number of later span starts <= b (they never decrease)
-    int wsp[kBinWaves + 1];
+    int wsp[W + 1];
 #pragma unroll
-    for (int w = 0; w <= kBinWaves; ++w) wsp[w] = s_wsp[w];
+    for (int w = 0; w <= W; ++w) wsp[w] = s_wsp[w];
     auto wave_of = [&](int b) {
         int w = 0;
 #pragma unroll
-        for (int i = 1; i < kBinWaves; ++i) w += wsp[i] <= b ? 1 : 0;
+        for (int i = 1; i < W; ++i) w += wsp[i] <= b ? 1 : 0;
         return w;
     };
     // merge VV consecutive outputs from e0 of the piece in bin-local blocks [a, b) held by waves w0..w1
@@ -1508,11 +1510,11 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         // piece starts in its span, else its second.  Every slot read stays
         // inside s_part; a non-contributor's value (its slot may never have
         // been written) is dropped by a select, never multiplied in.
-        float mk[kBinWaves];
-        int base[kBinWaves];
+        float mk[W];
+        int base[W];
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kBinWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const bool on = w >= w0 && w <= w1 && wsp[w] != wsp[w + 1];
             base[w] = (w * 2 + (a > wsp[w] ? 1 : 0)) * kPart;
             const float m = s_part[base[w] + G * D + 2 * jj];
@@ -1523,7 +1525,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
 #pragma unroll
         for (int v = 0; v < VV; ++v) os[v] = 0.f;
 #pragma unroll
-        for (int w = 0; w < kBinWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const bool on = mk[w] != -INFINITY;
             const float sc = on ? exp2f(mk[w] - mx) : 0.f;
             const float *pp = s_part + base[w];
@@ -1538,7 +1540,7 @@ bin_decode_kernel(RopeSrc rs, uint16_t *__restrict__ cache, int64_t c_page, int6
         bin_store<D, G, VV>(os, mx, ls, e0, s_piece[sl].w >= 0, s_pid[sl], h, s_rope[sl].x, Hq, out, o_s0, o_s1,
                             piece_ml, piece_o);
     };
-    for (int u = wave; u < nslots * EPL; u += kBinWaves) {
+    for (int u = wave; u < nslots * EPL; u += W) {
         const int sl = u / EPL, unit = u - sl * EPL;
         const int a = s_start[sl], b = s_start[sl + 1];
         if (a == b) continue;
@@ -2231,14 +2233,19 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
             rs.q_s1 = q_s1;
             const dim3 grid(static_cast<unsigned>(NB * Hkv));
             uint16_t *kv = const_cast<uint16_t *>(cache);  // q-input mode writes no K/V
-            if (ps_log2 < 4)
-                hipLaunchKernelGGL((bin_decode_kernel<D, G, true, true>), grid, dim3(kBinThreads), 0, stream, rs, kv,
-                                   c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2,
-                                   scale * kLog2e, out, o_s0, o_s1, ws, L, status);
-            else
-                hipLaunchKernelGGL((bin_decode_kernel<D, G, false, true>), grid, dim3(kBinThreads), 0, stream, rs,
-                                   kv, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv,
-                                   ps_log2, scale * kLog2e, out, o_s0, o_s1, ws, L, status);
+#define NQ_BIN_QIN(SMALL, W)                                                                                   \
+    hipLaunchKernelGGL((bin_decode_kernel<D, G, SMALL, true, W>), grid, dim3(W * kWave), 0, stream, rs, kv, c_page, \
+                       c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2, scale * kLog2e, out, \
+                       o_s0, o_s1, ws, L, status)
+            const bool few_rows = rows_bound <= kBinSmallRows;
+            if (ps_log2 < 4) {
+                if (few_rows) NQ_BIN_QIN(true, kBinWavesSmall);
+                else NQ_BIN_QIN(true, kBinWavesLarge);
+            } else {
+                if (few_rows) NQ_BIN_QIN(false, kBinWavesSmall);
+                else NQ_BIN_QIN(false, kBinWavesLarge);
+            }
+#undef NQ_BIN_QIN
             if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
             decode_done = true;
         }
@@ -2471,18 +2478,24 @@ extern "C" int nq_paged_decode_rope_attention(const float *partials, int splits,
     char *ws = static_cast<char *>(workspace);
     const float scale_log2 = sm_scale * nq::kLog2e;
     const dim3 grid(static_cast<unsigned>(NB * num_kv_heads));
-#define NQ_BIN(GG, SMALL)                                                                                    \
-    hipLaunchKernelGGL((nq::bin_decode_kernel<128, GG, SMALL>), grid, dim3(nq::kBinThreads), 0, st, rs, cache, \
-                       c_page, c_kind, c_slot, c_head, num_pages, kv_indices, max_pages, num_kv_heads, ps_log2,  \
+#define NQ_BIN(GG, SMALL, W)                                                                                   \
+    hipLaunchKernelGGL((nq::bin_decode_kernel<128, GG, SMALL, false, W>), grid, dim3(W * nq::kWave), 0, st, rs,   \
+                       cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices, max_pages, num_kv_heads, ps_log2, \
                        scale_log2, out, o_s0, o_s1, ws, L, status)
+#define NQ_BIN_W(GG, SMALL)                                                 \
+    do {                                                                    \
+        if (max_query_tokens <= nq::kBinSmallRows) NQ_BIN(GG, SMALL, nq::kBinWavesSmall); \
+        else NQ_BIN(GG, SMALL, nq::kBinWavesLarge);                         \
+    } while (0)
     const bool small_pages = ps_log2 < 4;
     if (G == 2) {
-        if (small_pages) NQ_BIN(2, true);
-        else NQ_BIN(2, false);
+        if (small_pages) NQ_BIN_W(2, true);
+        else NQ_BIN_W(2, false);
     } else {
-        if (small_pages) NQ_BIN(1, true);
-        else NQ_BIN(1, false);
+        if (small_pages) NQ_BIN_W(1, true);
+        else NQ_BIN_W(1, false);
     }
+#undef NQ_BIN_W
 #undef NQ_BIN
     return NQ_LAUNCH_STATUS();
 }
