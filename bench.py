@@ -39,7 +39,7 @@ SEED = 1002
 # HBM bytes one fused decode-attention launch of this workload moves, from the FETCH_SIZE / WRITE_SIZE
 # counter passes in profiles/paged_attention_talker_decode_b64.md (median over the launches of the timed
 # steps; scaled by a 512 MiB device copy: x2.0 and x1.0).
-ATTENTION_TRAFFIC_BYTES = 272_864_870
+ATTENTION_TRAFFIC_BYTES = 272_820_633
 
 
 def log(*a):
