@@ -479,15 +479,16 @@ __device__ __forceinline__ void tf8_store(const u32x4_t (&xr)[XV], const u32x4_t
 // acc += t * sx[row] * (gate scale on lane columns 0, 1 | up scale on 2, 3).
 template <int MT, int NT>
 __device__ __forceinline__ void tf8_compute(floatx4_t (&acc)[MT][NT], const uint8_t *xs, const uint8_t *ws,
-                                            const float *sxs, const float *const (&swg)[NT],
-                                            const float *const (&swu)[NT], int kb, int wm, int wn, int r16, int kq) {
+                                            const float *sxs, const float *ssw, int kb, int wm, int wn, int r16,
+                                            int kq) {
     using XL = Fp8Lds<32 * MT, 128>;
     using WL = Fp8Lds<32 * NT, 128>;
     float gs[NT], us[NT];
+    const float *sk = ssw + (kb * 2 * NT + wn * NT) * 2;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-        gs[n] = swg[n][kb];
-        us[n] = swu[n][kb];
+        gs[n] = sk[2 * n];
+        us[n] = sk[2 * n + 1];
     }
     int8v_t a[NT];
 #pragma unroll
@@ -511,6 +512,8 @@ __device__ __forceinline__ void tf8_compute(floatx4_t (&acc)[MT][NT], const uint
 }
 
 // ---------------------------------------------------------------------------
+constexpr int kTf8MaxBlocks = 32;  // 128-wide K blocks of the tiled FP8 gate/up (K <= 4096)
+
 // Tiled FP8 gate/up + SwiGLU for prefill-sized row counts (a prefill bucket's
 // packed prompt tokens, up to 640 rows).  A workgroup owns (32 MT) activation
 // rows x (32 NT) rows of the interleaved gate/up matrix (16 NT act columns);
@@ -536,6 +539,7 @@ tgemm_fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][XL::kBytes];
     __shared__ __attribute__((aligned(16))) uint8_t ws[2][WL::kBytes];
     __shared__ float sxs[2][BM];
+    __shared__ float ssw[kTf8MaxBlocks * 4 * NT];
 
     // tile of this workgroup: XCD b % 8 takes tiles (b % 8) * per .. + per - 1, m fastest
     const int per = (tiles + 7) / 8;
@@ -562,14 +566,19 @@ tgemm_fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float
         wp[q] = w + static_cast<int64_t>(p0 + (threadIdx.x + q * kFp8Threads) / 8) * w_s0 + chunk * 16;
     const int srow = m0 + static_cast<int>(threadIdx.x);
     const float *sxp = sx + static_cast<int64_t>(srow < M ? srow : M - 1) * sx_s0;
-    // gate rows 8 pt .. of packed tile pt lie in 128-row block 8 pt / 128, up rows in (I + 8 pt) / 128
-    const float *swg[NT];
-    const float *swu[NT];
+    // the weight-block scales of every K block, gate then up per 16-row packed tile t of the
+    // workgroup: gate rows 8 pt .. of packed tile pt lie in 128-row block 8 pt / 128, up rows in
+    // (I + 8 pt) / 128.  Loaded first and kept in LDS, so that no K block's MFMAs wait on a global
+    // load queued behind the register stages' loads.
+    const int blocks = K / 128;
+    constexpr int kSwPer = (kTf8MaxBlocks * 4 * NT + kFp8Threads - 1) / kFp8Threads;
+    float swr[kSwPer];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-        const int pt = (p0 + wn * 16 * NT + n * 16) / 16;
-        swg[n] = sw + static_cast<int64_t>(pt * 8 / 128) * sw_s0;
-        swu[n] = sw + static_cast<int64_t>((I + pt * 8) / 128) * sw_s0;
+    for (int q = 0; q < kSwPer; ++q) {
+        const int i = static_cast<int>(threadIdx.x) + q * kFp8Threads;  // (kb, t, gate | up)
+        const int kb = i / (4 * NT), t = (i >> 1) - kb * (2 * NT);
+        const int r = 8 * (p0 / 16 + t) + ((i & 1) ? I : 0);
+        swr[q] = kb < blocks ? sw[static_cast<int64_t>(r / 128) * sw_s0 + kb] : 0.f;
     }
 
     // two register stages: the global loads of two K blocks are in flight while the MFMAs run
@@ -584,19 +593,23 @@ tgemm_fp8_swiglu_kernel(const uint8_t *__restrict__ x, int64_t x_s0, const float
 
     // block k sits in register set k % 2 (a, b) and LDS buffer k % 2.  Step k: MFMAs on buffer
     // k % 2, block k + 1 to LDS, then the loads of block k + 3 into the set block k + 1 left free.
-    const int blocks = K / 128;
     tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, 0, BM);
+#pragma unroll
+    for (int q = 0; q < kSwPer; ++q) {
+        const int i = static_cast<int>(threadIdx.x) + q * kFp8Threads;
+        if (i < blocks * 4 * NT) ssw[i] = swr[q];
+    }
     tf8_store<BM, BN, XV, WV>(xa, wa, sa, xs[0], ws[0], sxs[0], chunk);
     if (blocks > 1) tf8_load<XV, WV>(xb, wb, sb, xp, wp, sxp, 1, BM);
     if (blocks > 2) tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, 2, BM);
     __syncthreads();
     for (int kb = 0; kb < blocks; kb += 2) {
-        tf8_compute<MT, NT>(acc, xs[0], ws[0], sxs[0], swg, swu, kb, wm, wn, r16, kq);
+        tf8_compute<MT, NT>(acc, xs[0], ws[0], sxs[0], ssw, kb, wm, wn, r16, kq);
         if (kb + 1 < blocks) tf8_store<BM, BN, XV, WV>(xb, wb, sb, xs[1], ws[1], sxs[1], chunk);
         if (kb + 3 < blocks) tf8_load<XV, WV>(xb, wb, sb, xp, wp, sxp, kb + 3, BM);
         __syncthreads();
         if (kb + 1 >= blocks) break;
-        tf8_compute<MT, NT>(acc, xs[1], ws[1], sxs[1], swg, swu, kb + 1, wm, wn, r16, kq);
+        tf8_compute<MT, NT>(acc, xs[1], ws[1], sxs[1], ssw, kb + 1, wm, wn, r16, kq);
         if (kb + 2 < blocks) tf8_store<BM, BN, XV, WV>(xa, wa, sa, xs[0], ws[0], sxs[0], chunk);
         if (kb + 4 < blocks) tf8_load<XV, WV>(xa, wa, sa, xp, wp, sxp, kb + 4, BM);
         __syncthreads();
@@ -750,14 +763,12 @@ extern "C" int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float 
                                    const uint8_t *packed, int64_t w_s0, const float *sw, int64_t sw_s0, int I, int K,
                                    uint16_t *out, int64_t o_s0, void *stream) {
     NQ_CHECK_ARG(xq && sx && packed && sw && out && M > 0 && I > 0 && K > 0);
-    if (K % 128 || I % 128) return NQ_ERR_UNSUPPORTED;
+    if (K % 128 || I % 128 || K / 128 > kTf8MaxBlocks) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && x_s0 % 16 == 0 && w_s0 % 16 == 0 && al16(xq) && al16(packed));
     NQ_CHECK_ARG(sx_s0 >= K / 128 && sw_s0 >= K / 128 && o_s0 >= I && o_s0 % 2 == 0);
     NQ_CHECK_ARG(reinterpret_cast<uintptr_t>(out) % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n128 = 2 * I / 128;
-    if ((M + 127) / 128 * n128 >= 256)
-        return launch_tgemm_fp8_swiglu<4, 4>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
     if ((M + 63) / 64 * n128 >= 256)
         return launch_tgemm_fp8_swiglu<2, 4>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
     return launch_tgemm_fp8_swiglu<2, 2>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);

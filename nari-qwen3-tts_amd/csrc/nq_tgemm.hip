@@ -232,11 +232,12 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
     }
 }
 
-constexpr int kTgMT = 4, kTgNT = 4;  // 128 x 128 tiles
+constexpr int kTgMT = 2, kTgNT = 4;  // 64 x 128 tiles
 constexpr int kTgBM = 32 * kTgMT, kTgBN = 32 * kTgNT;
+constexpr int64_t kTgRound = 512;  // two workgroups per CU (60 KB of LDS each) are resident at once
 
-// K slices of a launch.  A workgroup holds a CU (80 KB of LDS), so the units run in rounds of 256
-// and a launch costs about rounds x (slice length + a unit's fixed cost, in K columns): the slice
+// K slices of a launch.  Two workgroups fit a CU, so the units run in rounds of 512 and a launch
+// costs about rounds x (slice length + a unit's fixed cost, in K columns): the slice
 // count minimising that (each slice a multiple of 64 columns and at least 256 of them), the fewest
 // slices on a tie.
 #ifndef NQ_TG_UNIT_COST
@@ -246,10 +247,10 @@ int tgemm_splits(int M, int N, int K) {
     constexpr int64_t kUnitCost = NQ_TG_UNIT_COST;
     const int64_t tiles = static_cast<int64_t>((M + kTgBM - 1) / kTgBM) * (N / kTgBN);
     int best = 1;
-    int64_t best_cost = (tiles + 255) / 256 * (K + kUnitCost);
+    int64_t best_cost = (tiles + kTgRound - 1) / kTgRound * (K + kUnitCost);
     for (int s = 2; s <= 8; ++s) {
         if (K % (s * kTgK) || K / s < 256) continue;
-        const int64_t cost = (tiles * s + 255) / 256 * (K / s + kUnitCost);
+        const int64_t cost = (tiles * s + kTgRound - 1) / kTgRound * (K / s + kUnitCost);
         if (cost < best_cost) {
             best_cost = cost;
             best = s;
