@@ -5,8 +5,8 @@
 //
 // Unlike the decode GEMM (nq_gemm.hip: weights streamed once into registers,
 // a few activation rows, split-K planes) the prefill product has enough rows to
-// be MFMA work: each workgroup owns a (32 MT) x (32 NT) output tile, the 2 x 2
-// waves a (16 MT) x (16 NT) quarter of it, and the K loop stages 64-wide slices
+// be MFMA work: each workgroup owns a (16 MT WM) x (16 NT WN) output tile, its
+// WM x WN waves a (16 MT) x (16 NT) part of it, and the K loop stages 64-wide slices
 // of the X and W tiles through LDS, double buffered (the next slice's global
 // loads are in flight while the MFMAs run on the current one).  Both operands
 // are K-contiguous, so a lane's 16-byte LDS read is one MFMA operand: W rows as
@@ -31,7 +31,6 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));  // staging registers (a plain vector type
                                                                     // keeps them out of scratch)
 
-constexpr int kTgThreads = 256;
 constexpr int kTgK = 64;             // K elements per stage
 constexpr int kTgPitch = kTgK + 16;  // LDS row pitch in bf16 (32 bytes of padding)
 
@@ -73,23 +72,23 @@ __device__ __forceinline__ void tg_load(u32x4_t (&xr)[XV], u32x4_t (&wr)[WV], co
     for (int q = 0; q < XV; ++q) xr[q] = *reinterpret_cast<const u32x4_t *>(xp[q] + k0);
 }
 
-// A register set into LDS: vector i = threadIdx.x + 256 q is tile row i / 8, 8-element chunk i % 8.
-template <int XV, int WV>
+// A register set into LDS: vector i = threadIdx.x + T q is tile row i / 8, 8-element chunk i % 8.
+template <int XV, int WV, int T>
 __device__ __forceinline__ void tg_store(const u32x4_t (&xr)[XV], const u32x4_t (&wr)[WV], uint16_t *xbuf,
                                          uint16_t *wbuf) {
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
-        const int i = threadIdx.x + q * kTgThreads;
+        const int i = threadIdx.x + q * T;
         *reinterpret_cast<u32x4_t *>(xbuf + (i >> 3) * kTgPitch + (i & 7) * 8) = xr[q];
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
-        const int i = threadIdx.x + q * kTgThreads;
+        const int i = threadIdx.x + q * T;
         *reinterpret_cast<u32x4_t *>(wbuf + (i >> 3) * kTgPitch + (i & 7) * 8) = wr[q];
     }
 }
 
-// The MFMAs of one staged 64-wide K slice: the wave's (16 MT) x (16 NT) quarter of the tile.
+// The MFMAs of one staged 64-wide K slice: the wave's (16 MT) x (16 NT) part of the tile.
 template <int MT, int NT>
 __device__ __forceinline__ void tg_compute(floatx4_t (&acc)[MT][NT], const uint16_t *xbuf, const uint16_t *wbuf,
                                            int wm, int wn, int r16, int kq) {
@@ -110,15 +109,16 @@ __device__ __forceinline__ void tg_compute(floatx4_t (&acc)[MT][NT], const uint1
     }
 }
 
-template <int MT, int NT, int kMode>
-__global__ void __launch_bounds__(kTgThreads)
+template <int MT, int NT, int WM, int WN, int kMode>
+__global__ void __launch_bounds__(WM * WN * kWave)
 tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w, int64_t w_s0,
              int N, int k_slice, uint16_t *__restrict__ out, int64_t o_s0, float *__restrict__ part, int tiles_m,
              int tiles_n, int units) {
-    constexpr int BM = 32 * MT, BN = 32 * NT;
-    constexpr int XV = BM * (kTgK / 8) / kTgThreads;  // 16-byte vectors per thread and stage
-    constexpr int WV = BN * (kTgK / 8) / kTgThreads;
-    static_assert(XV >= 1 && WV >= 1 && XV * kTgThreads == BM * kTgK / 8 && WV * kTgThreads == BN * kTgK / 8,
+    constexpr int T = WM * WN * kWave;
+    constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
+    constexpr int XV = BM * (kTgK / 8) / T;  // 16-byte vectors per thread and stage
+    constexpr int WV = BN * (kTgK / 8) / T;
+    static_assert(XV >= 1 && WV >= 1 && XV * T == BM * kTgK / 8 && WV * T == BN * kTgK / 8,
                   "stage splits evenly over the threads");
     static_assert(kMode != kTgSwiglu || NT % 2 == 0, "SwiGLU pairs gate and up column tiles");
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * kTgPitch];
@@ -134,7 +134,7 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int r16 = lane & 15, kq = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
     // weight row of local tile row r: plain, or (SwiGLU) gate / up rows of the wave's act columns
     auto w_row = [&](int r) __attribute__((always_inline)) -> int64_t {
@@ -152,13 +152,13 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
     const uint16_t *wp[WV];
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
-        const int i = threadIdx.x + q * kTgThreads;
+        const int i = threadIdx.x + q * T;
         const int row = m0 + (i >> 3);
         xp[q] = x + static_cast<int64_t>(row < M ? row : M - 1) * x_s0 + k_begin + (i & 7) * 8;
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
-        const int i = threadIdx.x + q * kTgThreads;
+        const int i = threadIdx.x + q * T;
         wp[q] = w + w_row(i >> 3) * w_s0 + k_begin + (i & 7) * 8;
     }
     floatx4_t acc[MT][NT];
@@ -173,14 +173,14 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
     u32x4_t xa[XV], wa[WV], xb[XV], wb[WV], xc[XV], wc[WV];
     const int stages = k_slice / kTgK;
     tg_load<XV, WV>(xa, wa, xp, wp, 0);
-    tg_store<XV, WV>(xa, wa, xs[0], ws[0]);
+    tg_store<XV, WV, T>(xa, wa, xs[0], ws[0]);
     if (stages > 1) tg_load<XV, WV>(xb, wb, xp, wp, 1);
     if (stages > 2) tg_load<XV, WV>(xc, wc, xp, wp, 2);
     if (stages > 3) tg_load<XV, WV>(xa, wa, xp, wp, 3);
     __syncthreads();
 #define NQ_TG_STEP(BUF, XS, WS, K)                                                              \
     tg_compute<MT, NT>(acc, xs[BUF], ws[BUF], wm, wn, r16, kq);                                 \
-    if ((K) + 1 < stages) tg_store<XV, WV>(XS, WS, xs[(BUF) ^ 1], ws[(BUF) ^ 1]);                \
+    if ((K) + 1 < stages) tg_store<XV, WV, T>(XS, WS, xs[(BUF) ^ 1], ws[(BUF) ^ 1]);                \
     if ((K) + 4 < stages) tg_load<XV, WV>(XS, WS, xp, wp, (K) + 4);                              \
     __syncthreads();                                                                            \
     if ((K) + 1 >= stages) break;
@@ -232,11 +232,22 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
     }
 }
 
-constexpr int kTgMT = 2, kTgNT = 4;  // 64 x 128 tiles
-constexpr int kTgBM = 32 * kTgMT, kTgBN = 32 * kTgNT;
-constexpr int64_t kTgRound = 512;  // two workgroups per CU (60 KB of LDS each) are resident at once
+// 128 x 128 tiles over 4 x 4 waves of 32 x 32 (2 x 2 MFMA tiles each): 68 registers, so the
+// sixteen waves of the one workgroup a CU holds (80 KB of LDS) are resident together.  Measured on
+// the 640-token prefill captures against 64 x 128 tiles of 2 x 2 waves at two workgroups per CU:
+// 20.75 against 21.57 ms per decision (2 x 4 waves of 32 x 64 at 128 x 128: 21.06 ms).
+#ifndef NQ_TG_SHAPE
+#define NQ_TG_SHAPE 2, 2, 4, 4
+#endif
+constexpr int kTgShape[4] = {NQ_TG_SHAPE};
+constexpr int kTgMT = kTgShape[0], kTgNT = kTgShape[1], kTgWM = kTgShape[2], kTgWN = kTgShape[3];
+constexpr int kTgBM = 16 * kTgMT * kTgWM, kTgBN = 16 * kTgNT * kTgWN;
+#ifndef NQ_TG_ROUND
+#define NQ_TG_ROUND 256
+#endif
+constexpr int64_t kTgRound = NQ_TG_ROUND;  // workgroups resident at once (one per CU)
 
-// K slices of a launch.  Two workgroups fit a CU, so the units run in rounds of 512 and a launch
+// K slices of a launch.  One workgroup fits a CU, so the units run in rounds of 256 and a launch
 // costs about rounds x (slice length + a unit's fixed cost, in K columns): the slice
 // count minimising that (each slice a multiple of 64 columns and at least 256 of them), the fewest
 // slices on a tie.
@@ -264,7 +275,8 @@ int launch_tgemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int6
                  uint16_t *out, int64_t o_s0, float *part, hipStream_t st) {
     const int tiles_m = (M + kTgBM - 1) / kTgBM, tiles_n = N / kTgBN;
     const int units = tiles_m * tiles_n * S;
-    hipLaunchKernelGGL((tgemm_kernel<kTgMT, kTgNT, kMode>), dim3((units + 7) / 8 * 8), dim3(kTgThreads), 0, st, x,
+    hipLaunchKernelGGL((tgemm_kernel<kTgMT, kTgNT, kTgWM, kTgWN, kMode>), dim3((units + 7) / 8 * 8),
+                       dim3(kTgWM * kTgWN * kWave), 0, st, x,
                        x_s0, M, w, w_s0, N, K / S, out, o_s0, part, tiles_m, tiles_n, units);
     return NQ_LAUNCH_STATUS();
 }
