@@ -8,8 +8,8 @@
 // with each of res, scale, bias optional, act none or GELU (erf form, as
 // torch.nn.functional.gelu), and row(m) = m or x_rows[m] (a row gather).  The
 // products run on v_mfma_f32_16x16x4_f32 (full fp32 products and sums, no
-// reduced-precision inputs).  A workgroup owns a BM x BN tile, its 4 waves
-// (WM x WN) a (16 MT) x (16 NT) block each; 32-wide K slices of the X and W
+// reduced-precision inputs).  A workgroup owns a BM x BN tile, its WM x WN
+// waves a (16 MT) x (16 NT) block each; 32-wide K slices of the X and W
 // tiles are staged through LDS, double buffered, with two slices of global
 // loads in flight (a K tail reads as zero, columns past N are not stored).
 // Both operands are K-contiguous: a lane's 16-byte LDS read holds 4
@@ -23,7 +23,6 @@ namespace {
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kSgThreads = 256;
 constexpr int kSgK = 32;            // K floats per stage
 constexpr int kSgPitch = kSgK + 8;  // LDS row pitch in floats (32 bytes of padding)
 
@@ -44,18 +43,18 @@ __device__ __forceinline__ void sg_load(floatx4_t (&xr)[XV], floatx4_t (&wr)[WV]
         xr[q] = in ? *reinterpret_cast<const floatx4_t *>(xp[q] + k0) : floatx4_t{0.f, 0.f, 0.f, 0.f};
 }
 
-// vector i = threadIdx.x + 256 q: tile row i / 8, 4-float chunk i % 8
-template <int XV, int WV>
+// vector i = threadIdx.x + T q: tile row i / 8, 4-float chunk i % 8
+template <int XV, int WV, int T>
 __device__ __forceinline__ void sg_store(const floatx4_t (&xr)[XV], const floatx4_t (&wr)[WV], float *xbuf,
                                          float *wbuf) {
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
-        const int i = threadIdx.x + q * kSgThreads;
+        const int i = threadIdx.x + q * T;
         *reinterpret_cast<floatx4_t *>(xbuf + (i >> 3) * kSgPitch + (i & 7) * 4) = xr[q];
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
-        const int i = threadIdx.x + q * kSgThreads;
+        const int i = threadIdx.x + q * T;
         *reinterpret_cast<floatx4_t *>(wbuf + (i >> 3) * kSgPitch + (i & 7) * 4) = wr[q];
     }
 }
@@ -81,18 +80,17 @@ __device__ __forceinline__ void sg_compute(floatx4_t (&acc)[MT][NT], const float
 
 __device__ __forceinline__ float sg_gelu(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 
-template <int MT, int NT, int WM>
-__global__ void __launch_bounds__(kSgThreads)
+template <int MT, int NT, int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * kWave)
 sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restrict__ x_rows, int M,
              const float *__restrict__ w, int64_t w_s0, int N, int K, const float *__restrict__ bias, int act,
              const float *res, int64_t r_s0, const float *__restrict__ scale, float *out, int64_t o_s0, int tiles_m,
              int units) {
-    constexpr int WN = 4 / WM;
+    constexpr int T = WM * WN * kWave;
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
-    constexpr int XV = BM * (kSgK / 4) / kSgThreads;  // 16-byte vectors per thread and stage
-    constexpr int WV = BN * (kSgK / 4) / kSgThreads;
-    static_assert(WM * WN == 4 && XV >= 1 && WV >= 1 && XV * kSgThreads == BM * kSgK / 4 &&
-                      WV * kSgThreads == BN * kSgK / 4,
+    constexpr int XV = BM * (kSgK / 4) / T;  // 16-byte vectors per thread and stage
+    constexpr int WV = BN * (kSgK / 4) / T;
+    static_assert(XV >= 1 && WV >= 1 && XV * T == BM * kSgK / 4 && WV * T == BN * kSgK / 4,
                   "stage splits evenly over the threads");
     __shared__ __attribute__((aligned(16))) float xs[2][BM * kSgPitch];
     __shared__ __attribute__((aligned(16))) float ws[2][BN * kSgPitch];
@@ -112,7 +110,7 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
     const float *wp[WV];
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
-        const int i = threadIdx.x + q * kSgThreads;
+        const int i = threadIdx.x + q * T;
         int row = m0 + (i >> 3);
         row = row < M ? row : M - 1;
         if (x_rows) row = x_rows[row];
@@ -120,7 +118,7 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
-        const int i = threadIdx.x + q * kSgThreads;
+        const int i = threadIdx.x + q * T;
         const int n = n0 + (i >> 3);  // rows past N repeat row N - 1; their columns are not stored
         wp[q] = w + static_cast<int64_t>(n < N ? n : N - 1) * w_s0 + (i & 7) * 4;
     }
@@ -142,18 +140,18 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
     floatx4_t xa[XV], wa[WV], xb[XV], wb[WV];
     const int stages = (K + kSgK - 1) / kSgK;
     sg_load<XV, WV>(xa, wa, xp, wp, 0, k_left);
-    sg_store<XV, WV>(xa, wa, xs[0], ws[0]);
+    sg_store<XV, WV, T>(xa, wa, xs[0], ws[0]);
     if (stages > 1) sg_load<XV, WV>(xb, wb, xp, wp, 1, k_left);
     if (stages > 2) sg_load<XV, WV>(xa, wa, xp, wp, 2, k_left);
     __syncthreads();
     for (int k = 0;; k += 2) {
         sg_compute<MT, NT>(acc, xt0, wt0);
-        if (k + 1 < stages) sg_store<XV, WV>(xb, wb, xs[1], ws[1]);
+        if (k + 1 < stages) sg_store<XV, WV, T>(xb, wb, xs[1], ws[1]);
         if (k + 3 < stages) sg_load<XV, WV>(xb, wb, xp, wp, k + 3, k_left);
         __syncthreads();
         if (k + 1 >= stages) break;
         sg_compute<MT, NT>(acc, xt1, wt1);
-        if (k + 2 < stages) sg_store<XV, WV>(xa, wa, xs[0], ws[0]);
+        if (k + 2 < stages) sg_store<XV, WV, T>(xa, wa, xs[0], ws[0]);
         if (k + 4 < stages) sg_load<XV, WV>(xa, wa, xp, wp, k + 4, k_left);
         __syncthreads();
         if (k + 2 >= stages) break;
@@ -188,13 +186,14 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
     }
 }
 
-template <int MT, int NT, int WM>
+template <int MT, int NT, int WM, int WN>
 int launch_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, int M, const float *w, int64_t w_s0, int N,
                  int K, const float *bias, int act, const float *res, int64_t r_s0, const float *scale, float *out,
                  int64_t o_s0, hipStream_t st) {
-    constexpr int BM = 16 * MT * WM, BN = 16 * NT * (4 / WM);
+    constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
     const int tiles_m = (M + BM - 1) / BM, units = tiles_m * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL((sgemm_kernel<MT, NT, WM>), dim3((units + 7) / 8 * 8), dim3(kSgThreads), 0, st, x, x_s0,
+    hipLaunchKernelGGL((sgemm_kernel<MT, NT, WM, WN>), dim3((units + 7) / 8 * 8), dim3(WM * WN * kWave), 0, st, x,
+                       x_s0,
                        x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, tiles_m, units);
     return NQ_LAUNCH_STATUS();
 }
@@ -284,12 +283,15 @@ extern "C" int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, con
     // the largest tile that still gives every CU a workgroup (fp32 MFMA work per staged byte is high,
     // so small tiles lose little and idle CUs lose much)
     auto units = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-#define NQ_SG(MT, NT) launch_sgemm<MT, NT, 2>(x, x_s0, x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, st)
-    if (units(128, 128) >= 256) return NQ_SG(4, 4);
-    if (units(64, 128) >= 256) return NQ_SG(2, 4);
-    if (units(64, 64) >= 256) return NQ_SG(2, 2);
-    if (units(32, 64) >= 256) return NQ_SG(1, 2);
-    return NQ_SG(1, 1);
+#define NQ_SG(MT, NT, WM, WN) \
+    launch_sgemm<MT, NT, WM, WN>(x, x_s0, x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, st)
+    // 128 x 128 and 64 x 128 tiles over 16 and 8 waves of 32 x 32, 64 x 64 over 8 waves of 16 x 32: more
+    // waves per CU hide the stage latency (the codec step's GEMMs 1.30 -> 1.21 ms against 4 waves per tile)
+    if (units(128, 128) >= 256) return NQ_SG(2, 2, 4, 4);
+    if (units(64, 128) >= 256) return NQ_SG(2, 2, 2, 4);
+    if (units(64, 64) >= 256) return NQ_SG(1, 2, 4, 2);
+    if (units(32, 64) >= 256) return NQ_SG(1, 2, 2, 2);
+    return NQ_SG(1, 1, 2, 2);
 #undef NQ_SG
 }
 
