@@ -218,6 +218,11 @@ class IncrementalCodecDecoder:
         self.retained_context = self.config.retained_context
         self.pool = _StatePool(self.config, max_streams, self.device)
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        # pinned host staging for decode_ragged's offsets, slots and codes: a copy from pageable memory
+        # makes the host wait for the stream, so every call would wait for the previous step's kernels.
+        # A ring of buffers, each reused only after its last copy's event has completed.
+        self._stage_ring = [[None, None] for _ in range(4)]
+        self._stage_next = 0
         self._cache: dict = {}
         self._staging_pools: dict[int, _StatePool] = {}
         self._shape_cache: dict = {}
@@ -484,10 +489,7 @@ class IncrementalCodecDecoder:
         if off[-1] == 0:
             return [torch.empty(0, device=self.device) for _ in chunks], [
                 torch.empty(0, dtype=torch.int16, device=self.device) for _ in chunks]
-        dev = self.device
-        off_dev = torch.from_numpy(off.astype(np.int32)).to(dev, non_blocking=True)
-        slots = torch.tensor([st.slot for st in states], dtype=torch.int32, device=dev)
-        packed = torch.cat([ch.t() for ch in chunks], dim=0).to(device=dev, dtype=torch.int32).contiguous()
+        off_dev, slots, packed = self._stage_inputs(off, [st.slot for st in states], chunks)
         wav, pcm = self._run(packed, B, off_dev, off, slots, self.pool)
         r = c.retained_context
         for st, f in zip(states, frames):
@@ -495,6 +497,34 @@ class IncrementalCodecDecoder:
             st.transformer_context_length = min(r, st.transformer_context_length + f)
         bounds = off * c.samples_per_frame
         return ([wav[bounds[i]: bounds[i + 1]] for i in range(B)], [pcm[bounds[i]: bounds[i + 1]] for i in range(B)])
+
+    def _stage_inputs(self, off: np.ndarray, slots: list, chunks: list):
+        """The packed codes [frames, Q], offsets [B + 1] and slots [B] (int32) copied to the device in one
+        asynchronous copy from a pinned ring buffer."""
+        B, total, q = len(slots), int(off[-1]), self.config.num_quantizers
+        need = 2 * B + 1 + total * q
+        entry = self._stage_ring[self._stage_next]
+        self._stage_next = (self._stage_next + 1) % len(self._stage_ring)
+        buf, done = entry
+        if buf is None or buf.numel() < need:
+            buf = torch.empty(max(need, 1 << 16), dtype=torch.int32, pin_memory=True)
+        elif done is not None:
+            done.synchronize()
+        host = buf.numpy()
+        nc = total * q  # the codes first, so that their copy keeps the allocation's alignment
+        codes = host[:nc].reshape(total, q)
+        host[nc:nc + B + 1] = off
+        host[nc + B + 1:need] = slots
+        row = 0
+        for ch in chunks:
+            f = int(ch.shape[1])
+            codes[row:row + f] = ch.t().numpy() if ch.device.type == "cpu" else ch.t().cpu().numpy()
+            row += f
+        dev_buf = buf[:need].to(self.device, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        entry[0], entry[1] = buf, done
+        return dev_buf[nc:nc + B + 1], dev_buf[nc + B + 1:need], dev_buf[:nc].view(total, q)
 
     # -- the step -------------------------------------------------------------
     def _run(self, packed: torch.Tensor, B: int, off_dev: torch.Tensor, off_host: np.ndarray, slots: torch.Tensor,
