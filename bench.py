@@ -26,6 +26,7 @@ import os
 import sys
 import time
 from pathlib import Path
+from types import SimpleNamespace
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -184,10 +185,22 @@ def attention_probe(torch, w, replays: int = 20):
 
 
 def host_threads() -> int:
-    """Host cores the CPU baselines use: this process's CPU affinity, at most 16 (one GPU's share of
-    the host)."""
+    """Host cores the CPU baselines use: this process's CPU affinity (len(os.sched_getaffinity(0))),
+    limited by OMP_NUM_THREADS where the environment sets it (a GPU box sets it to its share of the
+    host's cores, whatever the affinity mask shows)."""
 
-    return max(1, min(len(os.sched_getaffinity(0)), 16))
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_fields(cores: int) -> dict:
+    """The core count a CPU baseline used and where it came from."""
+
+    return dict(cores=int(cores), affinity=len(os.sched_getaffinity(0)),
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
 
 
 def cpu_pool(n: int):
@@ -256,7 +269,7 @@ def cpu_baseline(torch, np, w, budget_s: float = 10.0):
             break
     pool.unregister()
     step_s = elapsed / done * cfg.num_layers
-    return dict(value=ROWS / step_s, unit="tok/s", cores=int(cores), kind="port",
+    return dict(value=ROWS / step_s, unit="tok/s", **cpu_fields(cores), kind="port",
                 sample=f"oracle decode step (numpy): {done} layer passes ({cfg.num_layers} layers per step) for {ROWS} "
                        f"rows in {elapsed:.1f}s, scaled to one {cfg.num_layers}-layer step")
 
@@ -465,7 +478,7 @@ def code_predictor_cpu_baseline(torch, np, weights, frame, budget_s: float = 10.
         elapsed += time.perf_counter() - t0
         done += rows
     pool.unregister()
-    return dict(value=done / elapsed, unit="frames/s", cores=int(cores), kind="port",
+    return dict(value=done / elapsed, unit="frames/s", **cpu_fields(cores), kind="port",
                 sample=f"oracle frame (numpy, teacher-forced) for {done} of {CP_ROWS} rows in {elapsed:.1f}s")
 
 
@@ -584,7 +597,7 @@ def codec_cpu_baseline(np, weights, cfg, budget_s: float = 10.0) -> dict:
         elapsed += time.perf_counter() - t0
         done += 12
     pool.unregister()
-    return dict(value=done * cfg.samples_per_frame / elapsed, unit="samples/s", cores=int(cores), kind="port",
+    return dict(value=done * cfg.samples_per_frame / elapsed, unit="samples/s", **cpu_fields(cores), kind="port",
                 sample=f"oracle codec (numpy) over {done} frames of one stream in 12-frame chunks, {elapsed:.1f}s")
 
 
@@ -675,6 +688,7 @@ def mixed_attention(args, torch, np) -> dict:
     priors = np.concatenate([pre_prior, dec_prior])
     advances = np.concatenate([pre_adv, np.ones(MIXED_DECODE, dtype=np.int64)])
     mixed_us, plan_us, kv, ctx, q, pubs = build(priors, advances, MIXED_PREFILL + MIXED_DECODE)
+    cpu = None if args.no_cpu_baseline else mixed_cpu_baseline(torch, np, kv, ctx, q)
     del kv, ctx, q, pubs
     torch.cuda.empty_cache()
     pre_us, _, kv2, ctx2, q2, pubs2 = build(pre_prior, pre_adv, MIXED_PREFILL)
@@ -731,7 +745,46 @@ def mixed_attention(args, torch, np) -> dict:
         },
         "planner_us_per_decision": round(plan_us, 1),
     }
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
     return result
+
+
+def mixed_cpu_baseline(torch, np, kv, ctx, q, budget_s: float = 10.0) -> dict:
+    """The oracle's paged attention (numpy) over the whole mixed batch -- 16 causal prefill chunks and
+    112 decode rows -- for one layer, with the metadata the GPU planner wrote; repeated until the
+    budget is spent, reported per layer."""
+
+    from oracle import attention as o_att
+    from oracle import bf16 as o_bf16
+
+    def host(t):
+        t = t.detach().cpu()
+        if t.dtype == torch.bfloat16:
+            return o_bf16.from_bits(t.contiguous().view(torch.int16).numpy().view(np.uint16))
+        return t.numpy()
+
+    b = ctx.buffers
+    indptr = b.kv_indptr.cpu().numpy()
+    rows = indptr.shape[0] - 1
+    pages = b.kv_indices[: int(indptr[-1])].cpu().numpy()
+    qo = b.qo_indptr.cpu().numpy()
+    last = b.last_page_len.cpu().numpy()
+    used, remap = np.unique(pages, return_inverse=True)
+    layer = host(kv.storage[0].index_select(0, torch.from_numpy(used.astype(np.int64)).to(q.device)))
+    qh = host(q)
+    cores = host_threads()
+    pool = cpu_pool(cores)
+    done, elapsed = 0, 0.0
+    while elapsed < budget_s or done < 1:
+        t0 = time.perf_counter()
+        o_att.paged_attention(qh, layer, indptr, remap.astype(np.int64), last, qo)
+        elapsed += time.perf_counter() - t0
+        done += 1
+    pool.unregister()
+    return dict(value=elapsed / done * 1e6, unit="us/layer", **cpu_fields(cores), kind="port",
+                sample=f"oracle paged attention (numpy) over the whole batch ({rows} rows, {int(qo[-1])} query "
+                       f"tokens, {len(used)} pages), one layer, {done} runs in {elapsed:.1f}s")
 
 
 def talker_prefill(args, torch, np) -> dict:
@@ -822,7 +875,8 @@ def talker_prefill(args, torch, np) -> dict:
     tok_s = total / (wall_ms / 1e3)
     log(f"prefill decision: {ms:.2f} ms GPU ({wall_ms:.2f} ms wall) for {total} tokens ({padded} captured) -> "
         f"{tok_s:.0f} prompt tok/s, {tflops:.1f} TFLOP/s algorithmic")
-    return {
+    cpu = None if args.no_cpu_baseline else talker_prefill_cpu_baseline(torch, np, kv, weights, rows, rids, lengths)
+    result = {
         "metric": "talker prefill: prompt tokens/s (16 chunks U{32..256} over prior U{0..512}, captured buckets)",
         "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(wall_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -835,18 +889,107 @@ def talker_prefill(args, torch, np) -> dict:
                      "frac": round(tflops / 2500.0, 4), "traffic": None, "kernel": "whole prefill decision",
                      "flops_per_step": flops, "gpu_ms_per_step": round(ms, 4)},
     }
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
+    return result
+
+
+def talker_prefill_cpu_baseline(torch, np, kv, weights, rows, rids, lengths, budget_s: float = 15.0) -> dict:
+    """The oracle talker (numpy, FP8 gate/up as the block-scaled product) over the decision's first
+    prefill part (the rows that fit 640 tokens), layer by layer until the budget is spent, scaled to
+    28 layers and reported as prompt tokens/s."""
+
+    from oracle import bf16 as o_bf16
+    from oracle import planner as o_plan
+    from oracle import talker as o_talker
+
+    def host(t):
+        t = t.detach().cpu()
+        if t.dtype == torch.bfloat16:
+            return o_bf16.from_bits(t.contiguous().view(torch.int16).numpy().view(np.uint16))
+        return t.numpy()
+
+    cfg = weights.config
+    part, tokens = [], 0
+    for rid, n in zip(rids, lengths):
+        if tokens + n > 640 or len(part) == 8:
+            break
+        part.append((rid, n))
+        tokens += n
+    free = list(kv.allocator.free_list())
+    pages_used, desc = [], []
+    for rid, n in part:
+        s = kv.state(rid)
+        need = -(-(s.sequence_length + n) // PAGE_SIZE)
+        pages = list(s.page_indices) + free[: need - len(s.page_indices)]
+        del free[: need - len(s.page_indices)]
+        desc.append((s.sequence_length, s.position_start, pages))
+        pages_used.extend(pages)
+    remap = {p: i for i, p in enumerate(pages_used)}
+    scratch_n = -(-tokens // PAGE_SIZE) + len(part)
+    scratch = list(range(len(pages_used), len(pages_used) + scratch_n))
+    meta = o_plan.metadata([(a, b, [remap[p] for p in pg]) for a, b, pg in desc], [n for _, n in part],
+                           capture_rows=len(part), token_capacity=tokens, prefill=True, page_size=PAGE_SIZE,
+                           scratch_pages=scratch)
+    idx = torch.tensor(pages_used, dtype=torch.long, device=weights.codec_head.device)
+    residual = o_talker.prefill_embedding(host(weights.text_embedding), host(weights.codec_embedding),
+                                          host(rows.text_ids[:tokens]), host(rows.codec_ids[:tokens]),
+                                          host(rows.codec_mask[:tokens]))
+    cfgd = dict(num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
+                rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta)
+    cores = host_threads()
+    pool = cpu_pool(cores)
+    done, elapsed = 0, 0.0
+    for li in range(cfg.num_layers):
+        L = weights.layers[li]
+        layer_np = dict(input_norm=host(L.input_norm), qkv=host(L.qkv), o=host(L.o), post_norm=host(L.post_norm),
+                        gate_up=host(L.gate_up), down=host(L.down), q_norm=host(L.attention.q_norm.weight),
+                        k_norm=host(L.attention.k_norm.weight), fp8_gate_up=weights.fp8_gate_up)
+        if weights.fp8_gate_up:
+            layer_np["gate_up_q"] = L.gate_up_q.view(torch.uint8).cpu().numpy()
+            layer_np["gate_up_s"] = L.gate_up_scales.cpu().numpy()
+        nxt = host(weights.final_norm) if li + 1 == cfg.num_layers else host(weights.layers[li + 1].input_norm)
+        cache = np.zeros((1, len(pages_used) + scratch_n, 2, PAGE_SIZE, cfg.num_kv_heads, cfg.head_dim), np.float32)
+        cache[0, : len(pages_used)] = host(kv.storage[li].index_select(0, idx))
+        t0 = time.perf_counter()
+        _, residual = o_talker.decode_layers([layer_np], cfgd, residual, cache, meta, range(0, 1), final_norm=nxt)
+        elapsed += time.perf_counter() - t0
+        done += 1
+        if elapsed >= budget_s:
+            break
+    pool.unregister()
+    decision_s = elapsed / done * cfg.num_layers
+    return dict(value=tokens / decision_s, unit="tok/s", **cpu_fields(cores), kind="port",
+                sample=f"oracle talker prefill (numpy) of {len(part)} chunks / {tokens} prompt tokens: {done} of "
+                       f"{cfg.num_layers} layers in {elapsed:.1f}s, scaled to {cfg.num_layers} layers")
+
+
+def measure_library():
+    """The benchmark's measurement kernels (libnq_measure.so, built next to the serving library)."""
+
+    import ctypes
+
+    from __graft_entry__ import PACKAGE_DIR
+
+    path = PACKAGE_DIR / "libnq_measure.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing; build it with __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    P, I, L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.nq_kv_read_probe.argtypes = [P, I, L, P, I, I, P, P]
+    lib.nq_kv_read_probe.restype = I
+    return lib
 
 
 def kv_read_ceiling(args, torch, np) -> dict:
     """The read ceiling of the decode attention's access pattern: the K/V pages of the batch-64 decode
     workload (64 rows, KV U[64, 2048], permuted 32768-page pool) read whole by nq_kv_read_probe, one
-    launch per layer over 28 distinct layers (no reuse from the Infinity Cache), no arithmetic."""
+    launch per layer over 28 distinct layers (no reuse from the Infinity Cache), no arithmetic; and
+    the same number of bytes read contiguously (pages 0, 1, 2, ... of each layer)."""
 
     from __graft_entry__ import load_package
 
     load_package()
-    from nari_qwen3_tts_amd import _lib
-
     dev = torch.device("cuda:0")
     layers, page_bytes = 28, 2 * PAGE_SIZE * 8 * 128 * 2
     storage = torch.empty((layers, POOL_PAGES, page_bytes // 2), dtype=torch.int16, device=dev)
@@ -855,42 +998,275 @@ def kv_read_ceiling(args, torch, np) -> dict:
     rng = np.random.default_rng(SEED)
     lengths = rng.integers(KV_LO, KV_HI + 1, size=ROWS)
     need = int(sum(-(-int(n) // PAGE_SIZE) for n in lengths))
-    pages = torch.from_numpy(rng.permutation(POOL_PAGES)[:need].astype(np.int32)).to(dev)
+    gathered = torch.from_numpy(rng.permutation(POOL_PAGES)[:need].astype(np.int32)).to(dev)
+    contiguous = torch.arange(need, dtype=torch.int32, device=dev)
     out = torch.zeros(1024, dtype=torch.int32, device=dev)
-    lib = _lib.load()
+    lib = measure_library()
     stream = torch.cuda.current_stream()
 
-    def launches():
+    def launches(pages):
         for layer in range(layers):
-            _lib.check(lib.nq_kv_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(), need,
-                                             1024, out.data_ptr(), stream.cuda_stream), "nq_kv_read_probe")
+            rc = lib.nq_kv_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(), need,
+                                      1024, out.data_ptr(), stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"nq_kv_read_probe status {rc}")
 
-    launches()
-    torch.cuda.synchronize()
+    timings = {}
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        launches()
-    end.record(stream)
-    end.synchronize()
-    us = start.elapsed_time(end) * 1e3 / (args.steps * layers)
+    for name, pages in (("gather", gathered), ("contiguous", contiguous)):
+        launches(pages)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            launches(pages)
+        end.record(stream)
+        end.synchronize()
+        timings[name] = start.elapsed_time(end) * 1e3 / (args.steps * layers)
     nbytes = need * page_bytes
-    gbs = nbytes / us / 1e3
-    log(f"KV page read ceiling: {need} pages = {nbytes / 1e6:.1f} MB per layer in {us:.1f} us -> {gbs:.0f} GB/s")
+    gbs = nbytes / timings["gather"] / 1e3
+    cgbs = nbytes / timings["contiguous"] / 1e3
+    log(f"KV page read ceiling: {need} pages = {nbytes / 1e6:.1f} MB per layer: permuted pages {timings['gather']:.1f} "
+        f"us -> {gbs:.0f} GB/s; the same bytes contiguous {timings['contiguous']:.1f} us -> {cgbs:.0f} GB/s")
     return {
         "metric": "KV page read ceiling GB/s (decode attention access pattern, no arithmetic)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 1,
-        "ms_per_step": round(us * layers / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(timings["gather"] * layers / 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random pages)",
         "config": {"workload": "K/V pages of 64 rows, KV U[64,2048], page size 16, 32768-page permuted pool, "
                                "28 distinct layers", "global_batch": ROWS, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "nq_kv_read_probe",
-                     "bytes_per_launch": nbytes, "us_per_launch": round(us, 2)},
+                     "bytes_per_launch": nbytes, "us_per_launch": round(timings["gather"], 2)},
+        "contiguous": {"us_per_launch": round(timings["contiguous"], 2), "GBps": round(cgbs, 1),
+                       "frac": round(cgbs / HBM_PEAK_GBS, 4)},
     }
 
 
-WORKLOADS = {"talker-decode": talker_decode, "kv-read-ceiling": kv_read_ceiling, "code-predictor": code_predictor, "codec": codec_step,
+SMALL_SEED = 1001
+SMALL_ROWS, SMALL_LO, SMALL_HI = 8, 16, 512
+SMALL_POOL = 4096
+SMALL_VOCAB = 3072
+# distinct K/V layers the attention timing rotates over: 64 x ~8.7 MB is more than the 256 MB
+# Infinity Cache holds, so each launch reads its pages from HBM as the first layer of a step would
+SMALL_LAYERS = 64
+
+
+def decode_sample_small(args, torch, np) -> dict:
+    """One ragged decode step of 8 rows and its draw: KV lengths U{16..512}, page size 16, 16 query /
+    8 KV heads of 128, bf16 q/k/v ~ N(0,1), every page drawn from a randomly permuted 4096-page pool.
+    A step = GPU planning (ragged page table + attention plan), q/k RMSNorm + RoPE + paged K/V write
+    + paged decode attention over one layer, then the fused sampler over 8 x 3072 fp32 logits (T 0.9,
+    top-k 50, top-p 0.95, repetition penalty 1.05 over a 64-token history, seeded fp32 uniforms, the
+    seen mask updated).  The rows' KV grows by one token per step (the publications are committed)."""
+
+    from __graft_entry__ import load_package
+
+    load_package()
+    from nari_qwen3_tts_amd.graphs import HipGraphCaptureDriver
+    from nari_qwen3_tts_amd.sampling import sample_with_uniforms
+    from nari_qwen3_tts_amd.talker_kv import PagedTalkerKV
+
+    dev = torch.device("cuda:0")
+    hq, hkv, d = 16, 8, 128
+    kv = PagedTalkerKV(num_layers=SMALL_LAYERS, num_kv_heads=hkv, num_qo_heads=hq, head_dim=d,
+                       total_pages=SMALL_POOL, page_size=PAGE_SIZE, scratch_page_count=SMALL_ROWS, workspace_bytes=0,
+                       device=dev, dtype=torch.bfloat16)
+    g = torch.Generator(device=dev)
+    g.manual_seed(SMALL_SEED)
+    for layer in range(SMALL_LAYERS):
+        kv.storage[layer].normal_(generator=g)
+    rng = np.random.default_rng(SMALL_SEED)
+    lengths = rng.integers(SMALL_LO, SMALL_HI + 1, size=SMALL_ROWS)
+    pool = rng.permutation(np.asarray(kv.allocator.free_list()))
+    rids, at = [], 0
+    for i, n in enumerate(lengths):
+        rid = f"s{i}"
+        kv.add_request(rid)
+        need = -(-int(n) // PAGE_SIZE)
+        kv.adopt_request(rid, pool[at: at + need], int(n))
+        at += need
+        rids.append(rid)
+    rids = tuple(rids)
+    gen = torch.Generator(device="cpu").manual_seed(SMALL_SEED)
+    q = torch.randn(SMALL_ROWS, hq, d, generator=gen).to(torch.bfloat16).to(dev)
+    k = torch.randn(SMALL_ROWS, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+    v = torch.randn(SMALL_ROWS, hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+    logits = torch.randn(SMALL_ROWS, SMALL_VOCAB, generator=gen).to(dev)
+    seen = torch.zeros(SMALL_ROWS, SMALL_VOCAB, dtype=torch.bool)
+    seen.scatter_(1, torch.randint(0, SMALL_VOCAB, (SMALL_ROWS, 64), generator=gen), True)
+    seen = seen.to(dev)
+    uniforms = torch.rand(SMALL_ROWS, generator=gen).to(dev)
+    temperature = torch.full((SMALL_ROWS,), 0.9, device=dev)
+    top_k = torch.full((SMALL_ROWS,), 50, dtype=torch.int32, device=dev)
+    top_p = torch.full((SMALL_ROWS,), 0.95, device=dev)
+    penalty = torch.full((SMALL_ROWS,), 1.05, device=dev)
+    tokens = torch.zeros(SMALL_ROWS, dtype=torch.long, device=dev)
+    att = SimpleNamespace(
+        q_norm=SimpleNamespace(weight=torch.ones(d, dtype=torch.bfloat16, device=dev), variance_epsilon=1e-6),
+        k_norm=SimpleNamespace(weight=torch.ones(d, dtype=torch.bfloat16, device=dev), variance_epsilon=1e-6),
+        rope_theta=1_000_000.0)
+    key = DecodeKey(SMALL_ROWS)
+    ctx = kv.create_decode(key, slot=0)
+    seen_step = seen.clone()
+
+    def device_step():
+        ctx.select_layer(0)
+        ctx.attend(att, q, k, v)
+        seen_step.copy_(seen)  # the same 64-token history every step
+        sample_with_uniforms(logits, temperature, top_k, top_p, uniforms, repetition_penalty=penalty,
+                             seen_token_mask=seen_step, update_seen=True, out=tokens)
+
+    publications = kv.prepare_capture(ctx, key)
+    driver = HipGraphCaptureDriver(device=dev)
+    call = driver.capture(device_step)
+    kv.finish_capture(ctx, publications)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        pubs = kv.prepare_decode(ctx, key, rids)
+        call.replay()
+        for p in pubs:
+            p.publish()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    kv_before = sum(kv.state(r).sequence_length for r in rids)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_us = (time.perf_counter() - t0) / args.steps * 1e6
+    if int(ctx.attention_status.item()) != 0 or int(ctx.buffers.status[0].item()) != 0:
+        raise RuntimeError("planner or attention status")
+    kv_after = sum(kv.state(r).sequence_length for r in rids)
+
+    # device time of the step's kernels after planning (q/k norm + RoPE + K/V write, attention,
+    # sampler): the captured step replayed back to back over one plan
+    pubs = kv.prepare_decode(ctx, key, rids)
+    call.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        call.replay()
+    end.record(stream)
+    end.synchronize()
+    device_us = start.elapsed_time(end) * 1e3 / args.steps
+    # planning alone: ledger + staging + the planner and attention-plan launches, then the discard
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        kv.abort(kv.prepare_decode(ctx, key, rids))
+    torch.cuda.synchronize()
+    plan_us = (time.perf_counter() - t1) / args.steps * 1e6
+
+    # the attention kernel alone: one graph of SMALL_LAYERS launches over distinct layers, replayed
+    attn_call = driver.capture(lambda: [ctx.run_attention(q, layer) for layer in range(SMALL_LAYERS)])
+    samp_call = driver.capture(lambda: [sample_with_uniforms(logits, temperature, top_k, top_p, uniforms,
+                                                             repetition_penalty=penalty, seen_token_mask=seen_step,
+                                                             out=tokens) for _ in range(SMALL_LAYERS)])
+    timings = {}
+    for name, c in (("attention", attn_call), ("sampler", samp_call)):
+        c.replay()
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(10):
+            c.replay()
+        end.record(stream)
+        end.synchronize()
+        timings[name] = start.elapsed_time(end) * 1e3 / (10 * SMALL_LAYERS)
+    kv_tokens_launch = sum(kv.state(r).sequence_length + 1 for r in rids)
+    attn_bytes = kv_tokens_launch * hkv * d * 2 * 2
+    sampler_bytes = SMALL_ROWS * SMALL_VOCAB * (4 + 1)
+    achieved = attn_bytes / (timings["attention"] / 1e6) / 1e9
+    log(f"8-row decode step: {wall_us:.1f} us per step (host planning {plan_us:.1f} us, device kernels after "
+        f"planning {device_us:.1f} us); attention {timings['attention']:.2f} us for {attn_bytes / 1e6:.2f} MB -> "
+        f"{achieved:.0f} GB/s; sampler {timings['sampler']:.2f} us")
+    result = {
+        "metric": "ragged decode step (8 rows, KV U{16..512}): paged attention + fused sampling, us per step",
+        "value": round(wall_us, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall_us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 (fp32 logits)", "data": "synthetic (N(0,1) q/k/v and KV pool, random page permutation, "
+                                              "N(0,1) logits, seeded uniforms)",
+        "config": {"workload": "8 decode rows, KV U{16..512}, page size 16, 16q/8kv heads x 128, 4096-page permuted "
+                               "pool; sampler over 8 x 3072 fp32 logits, T 0.9, top-k 50, top-p 0.95, penalty 1.05 "
+                               "over 64 seen ids", "global_batch": SMALL_ROWS, "parallelism": "single GPU"},
+        "step": "host planning (ledger, staging, planner + attention-plan launches) + one graph replay + "
+                "publication, wall clock",
+        "planning_us": round(plan_us, 1), "device_us_after_planning": round(device_us, 2),
+        "kv_tokens": [int(kv_before), int(kv_after)],
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "nq_paged_attention decode rows (bin_decode_kernel, q-input mode)",
+                     "bytes_per_launch": attn_bytes, "us_per_launch": round(timings["attention"], 2)},
+        "sampler": {"us_per_launch": round(timings["sampler"], 2), "bytes_per_launch": sampler_bytes,
+                    "GBps": round(sampler_bytes / (timings["sampler"] / 1e6) / 1e9, 1)},
+    }
+    kv.abort(pubs)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = decode_sample_small_cpu(torch, np, kv, rids, q, k, v, logits, seen, uniforms)
+    return result
+
+
+def decode_sample_small_cpu(torch, np, kv, rids, q, k, v, logits, seen, uniforms, budget_s: float = 10.0) -> dict:
+    """The oracle step on the host cores: q/k RMSNorm + RoPE, the paged K/V write, paged attention over
+    the rows' pages and the sampler, on the same inputs; repeated until the budget is spent."""
+
+    from oracle import attention as o_att
+    from oracle import bf16 as o_bf16
+    from oracle import planner as o_plan
+    from oracle import qk_rope as o_rope
+    from oracle import sampler as o_samp
+
+    def host(t):
+        t = t.detach().cpu()
+        if t.dtype == torch.bfloat16:
+            return o_bf16.from_bits(t.contiguous().view(torch.int16).numpy().view(np.uint16))
+        return t.numpy()
+
+    rows = len(rids)
+    states = [kv.state(r) for r in rids]
+    free = list(kv.allocator.free_list())
+    pages_used, desc = [], []
+    for s in states:
+        need = -(-(s.sequence_length + 1) // PAGE_SIZE)
+        pages = list(s.page_indices) + free[: need - len(s.page_indices)]
+        del free[: need - len(s.page_indices)]
+        desc.append((s.sequence_length, s.position_start, pages))
+        pages_used.extend(pages)
+    remap = {p: i for i, p in enumerate(pages_used)}
+    scratch = list(range(len(pages_used), len(pages_used) + rows))
+    meta = o_plan.metadata([(a, b, [remap[p] for p in pg]) for a, b, pg in desc], [1] * rows, capture_rows=rows,
+                           token_capacity=rows, prefill=False, page_size=PAGE_SIZE, scratch_pages=scratch)
+    idx = torch.tensor(pages_used, dtype=torch.long, device=q.device)
+    layer = np.zeros((len(pages_used) + rows, *kv.storage.shape[2:]), dtype=np.float32)
+    layer[: len(pages_used)] = host(kv.storage[0].index_select(0, idx))
+    qh, kh, vh, lh, sh, uh = host(q), host(k), host(v), host(logits), host(seen), host(uniforms)
+    w = np.ones(q.shape[-1], np.float32)
+    temp, tk, tp, pen = (np.full(rows, 0.9, np.float32), np.full(rows, 50, np.int32), np.full(rows, 0.95, np.float32),
+                         np.full(rows, 1.05, np.float32))
+    cores = host_threads()
+    pool = cpu_pool(cores)
+    done, elapsed = 0, 0.0
+    while elapsed < budget_s or done < 3:
+        t0 = time.perf_counter()
+        pos = meta["position_ids"]
+        q_rot = o_rope.norm_rope(qh, w, pos, 1e-6, 1_000_000.0, True)
+        k_rot = o_rope.norm_rope(kh, w, pos, 1e-6, 1_000_000.0, True)
+        for t in range(rows):
+            layer[int(meta["write_pages"][t]), 0, int(meta["write_offsets"][t])] = k_rot[t]
+            layer[int(meta["write_pages"][t]), 1, int(meta["write_offsets"][t])] = vh[t]
+        o_att.paged_attention(q_rot, layer, meta["kv_indptr"], meta["kv_indices"], meta["last_page_len"])
+        o_samp.sample(lh, temp, tk, tp, uh, penalty=pen, seen=sh)
+        elapsed += time.perf_counter() - t0
+        done += 1
+    pool.unregister()
+    return dict(value=elapsed / done * 1e6, unit="us/step", **cpu_fields(cores), kind="port",
+                sample=f"oracle step (numpy): q/k norm + RoPE, K/V write, paged attention over the 8 rows' pages, "
+                       f"sampler; {done} steps in {elapsed:.1f}s")
+
+
+WORKLOADS = {"talker-decode": talker_decode, "decode-sample-8": decode_sample_small, "kv-read-ceiling": kv_read_ceiling, "code-predictor": code_predictor, "codec": codec_step,
              "mixed": mixed_attention, "talker-prefill": talker_prefill}
 
 

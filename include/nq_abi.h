@@ -30,7 +30,8 @@ enum nq_status {
     NQ_ERR_INVALID_ARGUMENT = -1, /* shape / contract violation -> ValueError */
     NQ_ERR_UNSUPPORTED = -2,      /* dtype / size outside the kernels' range -> TypeError */
     NQ_ERR_LAUNCH = -3,           /* HIP launch or runtime failure -> RuntimeError */
-    NQ_ERR_CAPACITY = -4          /* too few free KV pages -> KVAllocationError */
+    NQ_ERR_CAPACITY = -4,         /* too few free KV pages -> KVAllocationError */
+    NQ_ERR_STATE = -5             /* device KV state differs from the host ledger -> RuntimeError */
 };
 
 /* dtype codes for logits and activations */
@@ -49,20 +50,22 @@ const char *nq_status_string(int status);
  * pos_start[r], advance[r] >= 1 new tokens, prior_pages[r] pages already listed
  * in page_table[table_row[r] * table_stride + 0 .. prior_pages[r]).  New pages
  * are read from free_pages[0 ..) (sorted ascending) and appended to the same
- * page_table row.  Rows n_rows .. capture_rows-1 are padding rows that use
- * scratch_pages[row].  Outputs (device):
+ * page_table row.  expect_pages (may be NULL) lists the pages the host ledger's
+ * reservation took, in row order; when the pages read from free_pages differ
+ * from it, status[0] is NQ_ERR_STATE (the metadata is still written).
+ * Rows n_rows .. capture_rows-1 are padding rows that use scratch_pages[row].  Outputs (device):
  *   qo_indptr[capture_rows+1] (only when prefill != 0; may be NULL otherwise),
  *   kv_indptr[capture_rows+1], kv_indices[kv_indices_capacity],
  *   last_page_len[capture_rows], position_ids / write_pages / write_offsets
  *   [token_capacity] (int64).
- * status[0] receives NQ_OK or NQ_ERR_CAPACITY, status[1] the number of free
- * pages consumed.  grid_blocks = 0 picks a default launch width.
+ * status[0] receives NQ_OK, NQ_ERR_CAPACITY or NQ_ERR_STATE, status[1] the
+ * number of free pages consumed.  grid_blocks = 0 picks a default launch width.
  */
 int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start, const int32_t *advance,
                    const int32_t *prior_pages, const int32_t *table_row, int n_rows,
                    int capture_rows, int token_capacity, int page_size, int prefill,
                    int32_t *page_table, int64_t table_stride, const int32_t *free_pages,
-                   int n_free, const int32_t *scratch_pages, int n_scratch,
+                   int n_free, const int32_t *expect_pages, const int32_t *scratch_pages, int n_scratch,
                    int32_t *qo_indptr, int32_t *kv_indptr, int32_t *kv_indices,
                    int64_t kv_indices_capacity, int32_t *last_page_len, int64_t *position_ids,
                    int64_t *write_pages, int64_t *write_offsets, int32_t *status,
@@ -179,17 +182,6 @@ int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_t *kv_indpt
                                int head_dim, float sm_scale, uint16_t *out, int64_t o_s0, int64_t o_s1,
                                int max_query_tokens, int max_pages, int parts, int32_t *status,
                                void *stream);
-
-/*
- * Read-bandwidth yardstick (no reference counterpart; benchmark calibration):
- * reads pages[0 .. n_pages) of a paged buffer whole (page_bytes each, a
- * multiple of 64 KiB; ids outside [0, num_pages) are skipped) with 128-bit
- * loads like the decode attention's stream and no
- * arithmetic, so its time bounds what the attention can reach on the same
- * pages.  out: >= grid uint32 words (written only for an impossible value).
- */
-int nq_kv_read_probe(const void *base, int num_pages, int64_t page_bytes, const int32_t *pages, int n_pages,
-                     int grid, uint32_t *out, void *stream);
 
 /*
  * Code-predictor short-cache attention: one query per row over the first

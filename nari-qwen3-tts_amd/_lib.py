@@ -22,6 +22,7 @@ NQ_ERR_INVALID_ARGUMENT = -1
 NQ_ERR_UNSUPPORTED = -2
 NQ_ERR_LAUNCH = -3
 NQ_ERR_CAPACITY = -4
+NQ_ERR_STATE = -5
 NQ_F32 = 0
 NQ_BF16 = 1
 NQ_EPI_NONE = 0
@@ -42,7 +43,7 @@ _F = ctypes.c_float
 _SIGNATURES: dict[str, list] = {
     "nq_abi_version": [],
     "nq_status_string": [_I],
-    "nq_plan_ragged": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P, _I, _P, _I, _P, _P, _P, _L,
+    "nq_plan_ragged": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _L, _P, _I, _P, _P, _I, _P, _P, _P, _L,
                        _P, _P, _P, _P, _P, _I, _P],
     "nq_free_list_merge": [_P, _I, _P, _I, _P, _P, _P],
     "nq_step_report": [_P, _P, _P, _P, _P, _I, _L, _L, _P, _P],
@@ -52,7 +53,6 @@ _SIGNATURES: dict[str, list] = {
                            _I, _I, _I, _P, _L, _P, _P],
     "nq_paged_attention_noalloc": [_P, _P, _P, _P, _I, _P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F,
                                    _P, _L, _L, _I, _I, _I, _P, _P],
-    "nq_kv_read_probe": [_P, _I, _L, _P, _I, _I, _P, _P],
     "nq_cp_short_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F, _P, _L, _L, _P],
     "nq_cp_rope_short_attention": [_P, _I, _I, _P, _P, _P, _L, _F, _F, _I, _P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I,
                                    _F, _P, _L, _L, _P],

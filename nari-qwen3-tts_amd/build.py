@@ -18,6 +18,7 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC = PACKAGE_DIR / "csrc"
 LIBRARY = PACKAGE_DIR / "libnq_hip.so"
+MEASURE_LIBRARY = PACKAGE_DIR / "libnq_measure.so"
 OBJ_DIR = PACKAGE_DIR / "_build"
 ARCH = "gfx950"
 
@@ -72,7 +73,25 @@ def build_library(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY} from {len(sources)} sources")
+    _build_measure(hipcc, verbose)
     return LIBRARY
+
+
+def _build_measure(hipcc: str, verbose: bool) -> None:
+    """The benchmark's measurement kernels (``csrc/measure``) as their own library,
+    ``libnq_measure.so``, outside the serving library and its ABI."""
+
+    sources = sorted((CSRC / "measure").glob("*.hip"))
+    if not sources:
+        return
+    tmp = MEASURE_LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc, *_COMMON, "-shared", "-o", str(tmp), *map(str, sources)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"measurement library build failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, MEASURE_LIBRARY)
+    if verbose:
+        print(f"built {MEASURE_LIBRARY}")
 
 
 if __name__ == "__main__":

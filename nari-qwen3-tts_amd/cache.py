@@ -138,6 +138,8 @@ class PendingKVPublication:
 class KVReservation:
     publications: tuple[PendingKVPublication, ...]
     pages_taken: int = 0
+    # the pages taken from the front of the free list, in row order (what the device planner must take)
+    taken: np.ndarray | None = None
 
 
 class PagedKVAllocator:
@@ -360,7 +362,7 @@ class PagedKVAllocator:
                               tuple(advances))
         publications = tuple(map(PendingKVPublication, [batch] * rows, range(rows)))
         self._inflight.update(zip(request_ids, publications))
-        return KVReservation(publications, int(end[-1]))
+        return KVReservation(publications, int(end[-1]), taken)
 
     def _live(self, publication: PendingKVPublication) -> None:
         """StaleKVPublicationError unless ``publication`` is its request's in-flight entry and the

@@ -243,8 +243,10 @@ class PrefillSlice:
 def lower_prefill(sequence_lengths: tuple[int, ...], keys, max_batch_size: int = PREFILL_MAX_BATCH):
     """Pack consecutive requests into prefill captures (lower_talker_prefill, planner/catalog.py:
     262-314): a part takes requests while it has fewer than ``max_batch_size`` and their tokens fit
-    the largest token capacity; it runs on the capture with the least token capacity, then the
-    fewest rows, bucketed before exact, that covers its rows and tokens."""
+    the largest token capacity; it runs on the capture that covers its rows and tokens with the
+    least token capacity, then the fewest rows, then exact before bucketed (a key's
+    ``capture_sequence_length is None`` sorts False first), then the shorter exact length -- the
+    reference's min() key (planner/catalog.py:296-303)."""
 
     if not isinstance(sequence_lengths, tuple) or not sequence_lengths:
         raise ValueError("Talker prefill sequence lengths must be a non-empty tuple")

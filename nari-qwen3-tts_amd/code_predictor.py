@@ -167,6 +167,10 @@ class CodePredictorFrame:
         )
         need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in shapes)
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        # None: the fused draw from the lm_head's split-K planes (counter RNG) or from ``uniforms``;
+        # otherwise a sampler with the reference's signature (logits, temperature, top_k, top_p, seed,
+        # offset) -> tokens, called on each group's bf16 logits (read when the forward is recorded)
+        self.sampler = None
 
     def _layers(self, cache_pos: int, normed: bool = False) -> None:
         """The 5 layers at cache position ``cache_pos``; ``normed``: self.x already holds the first
@@ -205,7 +209,11 @@ class CodePredictorFrame:
             self._layers(group, normed=True)
             logits = self.logits[group - 1]
             token = self.tokens[group - 1]
-            if self.use_counter_rng:
+            if self.sampler is not None:
+                linear(self.x, w.lm_head[group - 1], out=logits, workspace=ws)
+                token.copy_(self.sampler(logits, self.temperature, self.top_k, self.top_p, self.seed,
+                                         self.offsets[:, group - 1]))
+            elif self.use_counter_rng:
                 # the head's split-K planes summed, rounded and drawn from in the sampling launch
                 splits = linear_partials(self.x, w.lm_head[group - 1], ws)
                 planes = ws[: splits * self.rows * c.vocab * 4].view(torch.float32).view(splits, self.rows, c.vocab)

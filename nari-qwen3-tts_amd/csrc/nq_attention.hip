@@ -1180,13 +1180,12 @@ __device__ __forceinline__ void bin_arrive(int4 pc, int h, int num_kv_heads, int
                                            int32_t *__restrict__ arrivals, const float *__restrict__ piece_ml,
                                            const float *__restrict__ piece_o, uint16_t *__restrict__ out,
                                            int64_t o_s0, int64_t o_s1) {
-    // the piece's coherent stores are complete before the arrival counts
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The arrival count is an agent-scope acquire-release operation: it publishes this piece's
+    // stores (release) and, for the piece that completes the count, makes every other piece's
+    // stores visible to the merge below (acquire).
     int32_t *counter = arrivals + pc.x * num_kv_heads + h;
     int before = 0;
-    if (lane == 0) before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     before = __shfl(before, 0, kWave);
     const int p0 = pc.w >> 9, k = pc.w & 511;
     if (before != k - 1) return;
@@ -2125,12 +2124,13 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 __hip_atomic_store(part_ml + pr * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __syncthreads();  // every wave's partial stores are complete
+        // every wave's partial stores happen before thread 0's arrival count (workgroup barrier),
+        // which is an agent-scope acquire-release operation: it publishes the workgroup's stores
+        // and, for the piece that completes the count, makes the other pieces' stores visible to
+        // the merge below (the barrier after it carries that to every wave of the workgroup)
+        __syncthreads();
         int32_t *counter = tile_arrivals + static_cast<int64_t>(pd.w) * num_kv_heads + h;
-        if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (s_arrived != n_pieces - 1) continue;
         // merge: thread = (query, query head, quarter of D); the pieces' (m, l) first, then their
@@ -2568,45 +2568,4 @@ extern "C" int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_
     return nq_paged_attention(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,
                               page_size, num_qo_heads, num_kv_heads, head_dim, sm_scale, out, o_s0, o_s1,
                               max_query_tokens, max_pages, parts, ws, NQ_NOALLOC_SCRATCH_BYTES, status, stream);
-}
-
-// ---------------------------------------------------------------------------
-// Read-bandwidth yardstick for the decode attention's access pattern: every
-// page of `pages` read whole (page_bytes, a multiple of 4 KiB) and folded into
-// one xor per thread, nothing else; ids outside [0, num_pages) are skipped.  One workgroup of 256 threads per page at
-// a time, 16 x 128-bit loads per thread in flight.  `out` (>= grid words) is
-// written only for an impossible xor value, so the loads stay live.
-
-namespace nq {
-namespace {
-
-__global__ void __launch_bounds__(256)
-kv_read_probe_kernel(const uint4 *__restrict__ base, int num_pages, const int32_t *__restrict__ pages, int n_pages,
-                     int64_t page_vec, uint32_t *__restrict__ out) {
-    uint32_t acc = 0;
-    for (int p = blockIdx.x; p < n_pages; p += gridDim.x) {
-        const int page = pages[p];
-        if (static_cast<unsigned>(page) >= static_cast<unsigned>(num_pages)) continue;
-        const uint4 *src = base + static_cast<int64_t>(page) * page_vec;
-        for (int64_t at = 0; at < page_vec; at += 16 * 256) {
-            uint4 v[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = src[at + i * 256 + threadIdx.x];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
-        }
-    }
-    if (acc == 0x9e3779b9u) out[blockIdx.x] = acc;
-}
-
-}  // namespace
-}  // namespace nq
-
-extern "C" int nq_kv_read_probe(const void *base, int num_pages, int64_t page_bytes, const int32_t *pages,
-                                int n_pages, int grid, uint32_t *out, void *stream) {
-    NQ_CHECK_ARG(base && pages && out && n_pages >= 1 && num_pages >= 1 && grid >= 1);
-    if (page_bytes <= 0 || page_bytes % (16 * 16 * 256) != 0 || !nq::aligned16(base)) return NQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL(nq::kv_read_probe_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint4 *>(base), num_pages, pages, n_pages, page_bytes / 16, out);
-    return NQ_LAUNCH_STATUS();
 }

@@ -28,7 +28,8 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
                    const int32_t *__restrict__ table_row, int n_rows, int capture_rows,
                    int token_capacity, int page_size, int prefill, int32_t *__restrict__ page_table,
                    int64_t table_stride, const int32_t *__restrict__ free_pages, int n_free,
-                   const int32_t *__restrict__ scratch_pages, int32_t *__restrict__ qo_indptr,
+                   const int32_t *__restrict__ expect_pages, const int32_t *__restrict__ scratch_pages,
+                   int32_t *__restrict__ qo_indptr,
                    int32_t *__restrict__ kv_indptr, int32_t *__restrict__ kv_indices,
                    int64_t kv_indices_capacity, int32_t *__restrict__ last_page_len,
                    int64_t *__restrict__ position_ids, int64_t *__restrict__ write_pages,
@@ -74,11 +75,27 @@ plan_ragged_kernel(const int32_t *__restrict__ seq_len, const int32_t *__restric
         err = NQ_ERR_INVALID_ARGUMENT;
     else if (total_miss > n_free)
         err = NQ_ERR_CAPACITY;
-    if (blockIdx.x == 0 && r == 0) {
-        status[0] = err;
-        status[1] = err == NQ_OK ? total_miss : 0;
+    if (err != NQ_OK) {
+        if (blockIdx.x == 0 && r == 0) {
+            status[0] = err;
+            status[1] = 0;
+        }
+        return;
     }
-    if (err != NQ_OK) return;
+    if (blockIdx.x == 0) {
+        // The pages this plan takes (the front of the device free list) must be the ones the host
+        // ledger's reservation took: a difference means the two copies of the free list diverged.
+        // It is reported, not fatal here: the metadata below is still complete and consistent
+        // with the device list, and the step report fails the step on the host.
+        int differ = 0;
+        if (expect_pages)
+            for (int j = r; j < total_miss; j += kPlanThreads) differ |= free_pages[j] != expect_pages[j];
+        differ = __syncthreads_or(differ);
+        if (r == 0) {
+            status[0] = differ ? NQ_ERR_STATE : NQ_OK;
+            status[1] = total_miss;
+        }
+    }
 
     if (blockIdx.x == 0 && r < capture_rows) {
         kv_indptr[r + 1] = page_off + npages;
@@ -160,7 +177,7 @@ extern "C" int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start,
                               const int32_t *table_row, int n_rows, int capture_rows,
                               int token_capacity, int page_size, int prefill,
                               int32_t *page_table, int64_t table_stride,
-                              const int32_t *free_pages, int n_free,
+                              const int32_t *free_pages, int n_free, const int32_t *expect_pages,
                               const int32_t *scratch_pages, int n_scratch,
                               int32_t *qo_indptr, int32_t *kv_indptr, int32_t *kv_indices,
                               int64_t kv_indices_capacity, int32_t *last_page_len,
@@ -182,7 +199,7 @@ extern "C" int nq_plan_ragged(const int32_t *seq_len, const int32_t *pos_start,
     hipLaunchKernelGGL(nq::plan_ragged_kernel, dim3(grid), dim3(nq::kPlanThreads), 0,
                        static_cast<hipStream_t>(stream), seq_len, pos_start, advance,
                        prior_pages, table_row, n_rows, capture_rows, token_capacity, page_size,
-                       prefill, page_table, table_stride, free_pages, n_free, scratch_pages,
+                       prefill, page_table, table_stride, free_pages, n_free, expect_pages, scratch_pages,
                        qo_indptr, kv_indptr, kv_indices, kv_indices_capacity, last_page_len,
                        position_ids, write_pages, write_offsets, status);
     return NQ_LAUNCH_STATUS();
@@ -291,6 +308,7 @@ extern "C" const char *nq_status_string(int status) {
         case NQ_ERR_UNSUPPORTED: return "unsupported dtype or size";
         case NQ_ERR_LAUNCH: return "HIP launch failure";
         case NQ_ERR_CAPACITY: return "not enough free KV pages";
+        case NQ_ERR_STATE: return "device KV state differs from the host ledger";
         default: return "unknown status";
     }
 }

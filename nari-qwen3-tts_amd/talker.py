@@ -10,8 +10,8 @@ seen mask, temperature, top-k, top-p, draw) with the seen-mask update.
 
 The projections run on the HIP library's skinny GEMM with the following
 kernel fused in (o_proj and down with the residual add-RMSNorm, gate_up with
-SiLU-mul) whenever the bucket has at most 128 rows; larger buckets use
-torch.matmul.  With ``fp8_gate_up`` (the default, as the reference's serving
+SiLU-mul); a decode bucket holds at most 128 rows, and larger shapes are
+refused (ValueError) rather than sent to another GEMM backend.  With ``fp8_gate_up`` (the default, as the reference's serving
 build requires FP8 gate/up for every talker layer, executor/build.py:73 and
 executor/optimizations.py:22-46) the gate/up weights are held as 128 x 128
 FP8 blocks, the post-attention add-RMSNorm stores its output quantized per
@@ -30,7 +30,6 @@ import torch
 from . import _lib
 from .layers import (
     FP8,
-    add_rmsnorm_fp8,
     embed_add_rmsnorm,
     gather_sum_rows,
     linear,
@@ -43,8 +42,6 @@ from .layers import (
     linear_silu_mul,
     linear_workspace_bytes,
     prefill_embed_rmsnorm,
-    add_rmsnorm,
-    silu_mul,
     quantize_fp8_weight_blocks,
     tgemm,
     tgemm_add_rmsnorm_fp8,
@@ -143,6 +140,9 @@ def check_step_report(head) -> None:
     plan, merge, attention, embed, bad_tokens = (int(x) for x in head[:5])
     if plan == _lib.NQ_ERR_CAPACITY:
         raise KVAllocationError("the GPU planner ran out of free Talker KV pages")
+    if plan == _lib.NQ_ERR_STATE:
+        raise RuntimeError("the GPU planner took other pages than the host ledger reserved (the device free "
+                           "list diverged from the ledger)")
     if plan != _lib.NQ_OK:
         raise RuntimeError(f"GPU planner status {plan} ({_lib.status_string(plan)})")
     if merge != _lib.NQ_OK:
@@ -157,8 +157,12 @@ def check_step_report(head) -> None:
 
 class StepReport:
     """The device report of a decode step and pinned host copies of it: ``fetch`` queues one
-    device-to-host copy on the current stream, ``read`` waits for it, fails closed on the status
-    words and returns the per-row end-of-speech flags."""
+    device-to-host copy on the current stream and returns its ticket, ``read`` waits for it, fails
+    closed on the status words and returns the per-row end-of-speech flags.
+
+    The host copies form a ring of ``depth`` buffers; a ticket is the copy's serial number, and a
+    ticket whose buffer has since been reused by a later fetch is refused (RuntimeError) instead of
+    returning another step's words."""
 
     def __init__(self, rows: int, device, depth: int = 4) -> None:
         head = _lib.NQ_REPORT_HEAD
@@ -166,27 +170,38 @@ class StepReport:
         self.device = torch.zeros(head + rows, dtype=torch.int32, device=device)
         self._host = [torch.zeros(head + rows, dtype=torch.int32, pin_memory=True) for _ in range(depth)]
         self._events: list[torch.cuda.Event | None] = [None] * depth
-        self._next = 0
+        self._holder = [-1] * depth  # serial of the copy each buffer holds
+        self._serial = 0
 
     def fetch(self) -> int:
-        i = self._next
-        self._next = (i + 1) % len(self._host)
+        ticket = self._serial
+        self._serial += 1
+        i = ticket % len(self._host)
         if self._events[i] is not None:
             self._events[i].synchronize()
         self._host[i].copy_(self.device, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
         self._events[i] = ev
+        self._holder[i] = ticket
+        return ticket
+
+    def _slot(self, ticket: int) -> int:
+        i = ticket % len(self._host)
+        if ticket < 0 or self._holder[i] != ticket:
+            raise RuntimeError(f"step report {ticket} was overwritten by a later step (only the last "
+                               f"{len(self._host)} reports are kept)")
         return i
 
     def read(self, ticket: int):
-        self._events[ticket].synchronize()
-        words = self._host[ticket].numpy()
+        i = self._slot(ticket)
+        self._events[i].synchronize()
+        words = self._host[i].numpy()
         check_step_report(words[: _lib.NQ_REPORT_HEAD])
         return words[_lib.NQ_REPORT_HEAD:].astype(bool)
 
     def fence(self, ticket: int) -> "ReportFence":
-        return ReportFence(self._events[ticket])
+        return ReportFence(self._events[self._slot(ticket)])
 
 
 class ReportFence:
@@ -234,7 +249,6 @@ class TalkerDecodeStep:
         self.residual = torch.zeros(rows, c.hidden, **bf)
         self.hidden = torch.zeros(rows, c.hidden, **bf)
         self.qkv = torch.zeros(rows, c.qkv_width, **bf)
-        self.gate_up = torch.zeros(rows, 2 * c.intermediate, **bf)
         self.act = torch.zeros(rows, c.intermediate, **bf)
         self.logits = torch.zeros(rows, c.vocab, **bf)
         self.tokens = torch.zeros(rows, dtype=torch.long, device=dev)
@@ -246,11 +260,12 @@ class TalkerDecodeStep:
             (c.hidden, c.intermediate, _lib.NQ_EPI_ADD_RMSNORM),
             (c.vocab, c.hidden, _lib.NQ_EPI_PARTIALS),  # the codec head's planes feed the sampler
         )
-        self.use_hip_linear = all(_lib.load().nq_linear_splits(rows, n, k) > 0 for n, k, _ in projections)
+        declined = [(n, k) for n, k, _ in projections if _lib.load().nq_linear_splits(rows, n, k) <= 0]
+        if declined:
+            raise ValueError(f"the decode projections take buckets of at most 128 rows; {rows} rows x "
+                             f"{declined[0]} is a prefill-sized shape (TalkerPrefillStep runs those)")
         self.fp8 = weights.fp8_gate_up
-        need = 16
-        if self.use_hip_linear:
-            need = max(need, max(linear_workspace_bytes(rows, n, k, e) for n, k, e in projections))
+        need = max(16, max(linear_workspace_bytes(rows, n, k, e) for n, k, e in projections))
         if self.fp8:
             # activation codes / scales of the gate/up input
             self.act_q = torch.zeros(rows, c.hidden, dtype=FP8, device=dev)
@@ -279,46 +294,24 @@ class TalkerDecodeStep:
         if trace is not None:
             trace[0].copy_(self.residual)
         q_w = c.num_qo_heads * c.head_dim
-        kv_w = c.num_kv_heads * c.head_dim
         ws = self.linear_workspace
         for index, layer in enumerate(self.w.layers):
             ctx.select_layer(index)
             nxt = self.w.final_norm if index + 1 == len(self.w.layers) else self.w.layers[index + 1].input_norm
-            if self.use_hip_linear:
-                # the split-K planes of the QKV projection feed the q/k norm + RoPE + KV write directly
-                splits = linear_partials(self.hidden, layer.qkv, ws)
-                q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
-                attended = ctx.attend_partials(layer.attention, ws, splits, q).view(n, q_w)
-            else:
-                torch.matmul(self.hidden, layer.qkv.t(), out=self.qkv)
-                q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
-                k = self.qkv[:, q_w : q_w + kv_w].view(n, c.num_kv_heads, c.head_dim)
-                v = self.qkv[:, q_w + kv_w :].view(n, c.num_kv_heads, c.head_dim)
-                attended = ctx.attend(layer.attention, q, k, v).view(n, q_w)
+            # the split-K planes of the QKV projection feed the q/k norm + RoPE + KV write directly
+            splits = linear_partials(self.hidden, layer.qkv, ws)
+            q = self.qkv[:, :q_w].view(n, c.num_qo_heads, c.head_dim)
+            attended = ctx.attend_partials(layer.attention, ws, splits, q).view(n, q_w)
             if self.fp8:
                 # post-attention add-RMSNorm quantized per 128 columns, block-scaled FP8 gate/up + SwiGLU
-                if self.use_hip_linear:
-                    linear_add_rmsnorm_fp8(attended, layer.o, self.residual, layer.post_norm, c.rms_eps,
-                                           self.act_q, self.act_scales, ws)
-                else:
-                    torch.matmul(attended, layer.o.t(), out=self.hidden)
-                    add_rmsnorm_fp8(self.hidden, self.residual, layer.post_norm, c.rms_eps, self.act_q,
-                                    self.act_scales)
+                linear_add_rmsnorm_fp8(attended, layer.o, self.residual, layer.post_norm, c.rms_eps,
+                                       self.act_q, self.act_scales, ws)
                 linear_fp8_swiglu(self.act_q, self.act_scales, layer.gate_up_packed, layer.gate_up_scales,
                                   self.act, weight_q=layer.gate_up_q, workspace=ws)
-            elif self.use_hip_linear:
+            else:
                 linear_add_rmsnorm(attended, layer.o, self.residual, layer.post_norm, c.rms_eps, self.hidden, ws)
                 linear_silu_mul(self.hidden, layer.gate_up, out=self.act, workspace=ws)
-            else:
-                torch.matmul(attended, layer.o.t(), out=self.hidden)
-                add_rmsnorm(self.hidden, self.residual, layer.post_norm, c.rms_eps)
-                torch.matmul(self.hidden, layer.gate_up.t(), out=self.gate_up)
-                silu_mul(self.gate_up, out=self.act)
-            if self.use_hip_linear:
-                linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
-            else:
-                torch.matmul(self.act, layer.down.t(), out=self.hidden)
-                add_rmsnorm(self.hidden, self.residual, nxt, c.rms_eps)
+            linear_add_rmsnorm(self.act, layer.down, self.residual, nxt, c.rms_eps, self.hidden, ws)
             if trace is not None:
                 trace[index + 1].copy_(self.residual)
         ctx.advance_sequence_lengths()
@@ -340,7 +333,7 @@ class TalkerDecodeStep:
         ws = self.linear_workspace
         options = dict(repetition_penalty=self.penalty, seen_token_mask=self.seen, mask_from=c.codec_vocab,
                        eos_id=c.eos_id, suppress_eos=self.suppress_eos, update_seen=True, out=self.tokens)
-        if self.use_hip_linear and self.use_counter_rng:
+        if self.use_counter_rng:
             # codec head as split-K planes, summed, rounded and drawn from in the sampling launch
             # (the same logits and tokens as the projection followed by the sampler)
             splits = linear_partials(self.hidden, self.w.codec_head, ws)
@@ -348,16 +341,9 @@ class TalkerDecodeStep:
             sample_with_counter_from_planes(planes, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
                                             logits_out=self.logits, **options)
             return
-        if self.use_hip_linear:
-            linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
-        else:
-            torch.matmul(self.hidden, self.w.codec_head.t(), out=self.logits)
-        if self.use_counter_rng:
-            # the uniform comes from each row's (seed, offset) counter inside the sampling launch
-            sample_with_counter(self.logits, self.temperature, self.top_k, self.top_p, self.seed, self.offsets,
-                                **options)
-        else:
-            sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
+        # caller-supplied uniforms
+        linear(self.hidden, self.w.codec_head, out=self.logits, workspace=ws)
+        sample_with_uniforms(self.logits, self.temperature, self.top_k, self.top_p, self.uniforms, **options)
 
 
 class TalkerPrefillStep:

@@ -551,10 +551,13 @@ class PagedTalkerKV:
         self._sync_free_list(current)
         a = self.allocator
         slots = a.slots(request_ids)
-        if self._rows_ring is None or self._rows_ring.view[0].shape[1] < capture_rows:
-            self._rows_ring = _PinnedRing((5, max(capture_rows, 64)), self.device)
-            self._rows_dev = torch.zeros((5, max(capture_rows, 64)), dtype=torch.int32, device=self.device)
-            self._rows_ptrs = tuple(self._rows_dev[k].data_ptr() for k in range(5))
+        # rows 0-4: one column per request row; row 5: the pages the reservation takes (at most
+        # ceil(advance / page_size) + 1 per row), which the planner checks against the device list
+        width = max(64, capture_rows + token_capacity // self.page_size + 1)
+        if self._rows_ring is None or self._rows_ring.view[0].shape[1] < width:
+            self._rows_ring = _PinnedRing((6, width), self.device)
+            self._rows_dev = torch.zeros((6, width), dtype=torch.int32, device=self.device)
+            self._rows_ptrs = tuple(self._rows_dev[k].data_ptr() for k in range(6))
         # the rows' committed numbers, read before the reservation (it does not change them)
         i, rows = self._rows_ring.acquire()
         rows[0, :n] = a.length[slots]
@@ -565,6 +568,8 @@ class PagedTalkerKV:
         publications = reservation.publications
         try:
             rows[2, :n] = advances
+            if reservation.pages_taken:
+                rows[5, : reservation.pages_taken] = reservation.taken
             if isinstance(context, _HipBindingBase):
                 buffers = context.buffers
             else:
@@ -585,7 +590,7 @@ class PagedTalkerKV:
                 "nq_plan_ragged",
                 rp[0], rp[1], rp[2], rp[3], rp[4], n, capture_rows, token_capacity, self.page_size,
                 int(prefill), self._table.data_ptr(), self._table.stride(0),
-                free.data_ptr() + 4 * self._free_front, self._free_len - self._free_front,
+                free.data_ptr() + 4 * self._free_front, self._free_len - self._free_front, rp[5],
                 self._scratch_dev.data_ptr(), len(self._scratch_pages),
                 bp[0] or None, bp[1], bp[2], buffers.kv_indices.numel(), bp[3], bp[4], bp[5], bp[6], bp[7], 0,
                 current.cuda_stream,

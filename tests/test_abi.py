@@ -51,8 +51,8 @@ def test_argument_errors_are_caught_on_the_host(nq):
 
     lib = _lib.load()
     # capture rows above the single-workgroup limit
-    assert lib.nq_plan_ragged(*([None] * 5), 1, 2048, 1, 16, 0, None, 1, None, 0, None, 2048, None, None, None, 0,
-                              None, None, None, None, None, 0, None) == -2
+    assert lib.nq_plan_ragged(*([None] * 5), 1, 2048, 1, 16, 0, None, 1, None, 0, None, None, 2048, None, None, None,
+                              0, None, None, None, None, None, 0, None) == -2
     # vocabulary above the sampler's LDS budget
     assert lib.nq_sample(1, 0, 8192, 1, 8192, 1, 1, 1, None, None, 0, 1, 8192, -1, None, 0, 1, None) == -2
     with pytest.raises(TypeError):

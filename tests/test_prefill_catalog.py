@@ -66,6 +66,18 @@ def test_lowering_picks_the_tightest_capture_and_splits_at_caps():
         low(())
 
 
+def test_lowering_takes_the_exact_capture_at_a_tie():
+    """Equal token capacity and rows: the exact capture wins over the bucketed one, and the shorter
+    exact length over a longer one (the reference's min() key, planner/catalog.py:296-303)."""
+    c = _catalog()
+    exact, bucketed, longer = c.PrefillKey(2, 20, 10), c.PrefillKey(2, 20), c.PrefillKey(2, 20, 20)
+    assert c.lower_prefill((10, 10), {bucketed, exact})[0].key == exact
+    assert c.lower_prefill((10, 10), {bucketed, longer, exact})[0].key == exact
+    assert c.lower_prefill((10, 10), {bucketed, longer})[0].key == longer
+    # fewer rows beat the exact kind: B1 cannot hold two rows, so B2 keys only; with one row B1 wins
+    assert c.lower_prefill((9,), {exact, c.PrefillKey(1, 20)})[0].key == c.PrefillKey(1, 20)
+
+
 def test_lowering_partitions_every_surface():
     """Every row lands in exactly one part whose capture covers its rows and tokens
     (tests/scheduler/test_capture_catalog.py:70-95)."""
