@@ -1153,12 +1153,14 @@ def decode_sample_small(args, torch, np) -> dict:
     end.record(stream)
     end.synchronize()
     device_us = start.elapsed_time(end) * 1e3 / args.steps
+    kv.abort(pubs)
     # planning alone: ledger + staging + the planner and attention-plan launches, then the discard
     t1 = time.perf_counter()
     for _ in range(args.steps):
         kv.abort(kv.prepare_decode(ctx, key, rids))
     torch.cuda.synchronize()
     plan_us = (time.perf_counter() - t1) / args.steps * 1e6
+    pubs = kv.prepare_decode(ctx, key, rids)
 
     # the attention kernel alone: one graph of SMALL_LAYERS launches over distinct layers, replayed
     attn_call = driver.capture(lambda: [ctx.run_attention(q, layer) for layer in range(SMALL_LAYERS)])

@@ -167,6 +167,10 @@ class CodePredictorFrame:
         )
         need = max(linear_workspace_bytes(rows, n, k, e) for n, k, e in shapes)
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        # optional [groups, layers + 2, rows, hidden] bf16 record of each pass: the residual stream
+        # at the pass start and after every layer, then the normalised hidden state the head reads
+        # (device-to-device copies, for layer-by-layer checks)
+        self.trace: torch.Tensor | None = None
         # None: the fused draw from the lm_head's split-K planes (counter RNG) or from ``uniforms``;
         # otherwise a sampler with the reference's signature (logits, temperature, top_k, top_p, seed,
         # offset) -> tokens, called on each group's bf16 logits (read when the forward is recorded)
@@ -182,6 +186,9 @@ class CodePredictorFrame:
         layers = self.w.layers
         if not normed:
             rmsnorm(self.h, layers[0].input_norm, c.rms_eps, out=self.x)
+        trace = None if self.trace is None else self.trace[cache_pos]
+        if trace is not None:
+            trace[0].copy_(self.h)
         for index, L in enumerate(layers):
             cache = self.kv_cache[index]
             # the QKV projection's split-K planes go straight into the q/k norm + RoPE + K/V write and
@@ -194,6 +201,10 @@ class CodePredictorFrame:
             linear_swiglu(self.x, L.gate_up_packed, self.act, weight=L.gate_up, workspace=ws)
             nxt = self.w.final_norm if index + 1 == len(layers) else layers[index + 1].input_norm
             linear_add_rmsnorm(self.act, L.down, self.h, nxt, c.rms_eps, self.x, ws)
+            if trace is not None:
+                trace[index + 1].copy_(self.h)
+        if trace is not None:
+            trace[len(layers) + 1].copy_(self.x)
 
     def forward(self) -> tuple[torch.Tensor, torch.Tensor]:
         c, w, ws = self.w.config, self.w, self.workspace

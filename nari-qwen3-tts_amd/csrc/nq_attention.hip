@@ -625,8 +625,10 @@ __device__ __forceinline__ uint32_t word(const uint4 &v, int w) {
 // both products run on v_dot2_f32_bf16 with fp32 accumulation: q.k as four
 // dot2 per 8 elements, and P.V pairs two tokens per dot2 (the weights are
 // rounded to bf16 for the product and for the normaliser alike, as a bf16
-// tensor-core P.V would).
-template <int D, int G>
+// tensor-core P.V would).  With kFp32P the weights stay fp32 and P.V is fp32
+// multiply-adds on the widened V (the short-cache attention of the code
+// predictor, whose reference kernel keeps P in fp32, model/kernels.py:452-461).
+template <int D, int G, bool kFp32P = false>
 struct SoftmaxState {
     uint32_t qb[G][4];
     float scale;
@@ -688,6 +690,35 @@ struct SoftmaxState {
     __device__ __forceinline__ void accumulate(const uint4 (&vr)[Lanes<D, G>::NL],
                                                const float (&s)[Lanes<D, G>::NL][G]) {
         constexpr int NL = Lanes<D, G>::NL;
+        if constexpr (kFp32P) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                float mb = s[0][j];
+#pragma unroll
+                for (int i = 1; i < NL; ++i) mb = fmaxf(mb, s[i][j]);
+                const float mn = fmaxf(m[j], mb);
+                const bool live = mn != -INFINITY;
+                const float alpha = live ? exp2f(m[j] - mn) : 1.f;
+                m[j] = live ? mn : m[j];
+                float lsum = 0.f;
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+                for (int i = 0; i < NL; ++i) {
+                    const float pw = live && s[i][j] != -INFINITY ? exp2f(s[i][j] - mn) : 0.f;
+                    float v[8];
+                    unpack8(vr[i], v);
+                    lsum += pw;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = fmaf(pw, v[e], o[e]);
+                }
+                l[j] = l[j] * alpha + lsum;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] * alpha + o[e];
+            }
+            return;
+        }
         static_assert(NL % 2 == 0, "tokens are paired for P.V");
         // softmax of each query head first: P packed as bf16 token pairs, the old sums rescaled
         uint32_t pp[G][NL / 2];
@@ -1569,7 +1600,7 @@ struct Smem {
 
 // Attend G query heads of kv head h to `ntok` keys; key position `rel` lives in
 // page page_of(rel) at slot slot_of(rel).  Leaves per-wave states in `sm`.
-template <int D, int G, typename PageOf, typename SlotOf>
+template <int D, int G, bool kFp32P = false, typename PageOf, typename SlotOf>
 __device__ __forceinline__ void attend_chunk(const uint16_t *__restrict__ qptr, int64_t q_s1,
                                              const uint16_t *__restrict__ cache, int64_t c_page,
                                              int64_t c_kind, int64_t c_slot, int64_t c_head, int h,
@@ -1580,7 +1611,7 @@ __device__ __forceinline__ void attend_chunk(const uint16_t *__restrict__ qptr, 
     const int wave = threadIdx.x / kWave;
     const int g = lane / LN::LPT;
     const int sub = lane % LN::LPT;
-    SoftmaxState<D, G> st;
+    SoftmaxState<D, G, kFp32P> st;
     st.reset();
     st.load_q(qptr, q_s1, h, sub, scale_log2);
     const uint16_t *head_base = cache + h * c_head + sub * 8;
@@ -1749,7 +1780,7 @@ dense_short_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
     for (int64_t w = blockIdx.x; w < n_items; w += gridDim.x) {
         const int row = static_cast<int>(w / num_kv_heads);
         const int h = static_cast<int>(w - static_cast<int64_t>(row) * num_kv_heads);
-        attend_chunk<D, G>(
+        attend_chunk<D, G, true>(
             q + row * q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head, h, valid_length, rows,
             scale_log2, [&](int) { return row; }, [&](int rel) { return rel; }, sm, &bad);
         for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {
@@ -1830,7 +1861,7 @@ dense_rope_short_kernel(const float *__restrict__ partials, int splits, int64_t 
             dst[lane + HALF] = o2;
         }
         __syncthreads();  // the rotated q and the new K/V are visible to every wave of the workgroup
-        attend_chunk<D, G>(
+        attend_chunk<D, G, true>(
             q_out + row * q_s0, q_s1, cache, c_row, c_kind, c_pos, c_head, h, cache_position + 1, rows,
             scale_log2, [&](int) { return row; }, [&](int rel) { return rel; }, sm, &bad);
         for (int t = threadIdx.x; t < G * D; t += kAttnThreads) {

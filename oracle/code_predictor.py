@@ -35,33 +35,54 @@ def _mm(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None) -> np.ndarray
     return bf16.round_f32(y)
 
 
-def _layers(w: dict, cfg: dict, h: np.ndarray, cache: np.ndarray, pos: int, positions: np.ndarray) -> tuple:
+def layer(w: dict, cfg: dict, i: int, h: np.ndarray, cache: np.ndarray, pos: int, positions: np.ndarray) -> tuple:
+    """Layer i at cache position ``pos`` on the residual stream h: writes its K/V at ``pos`` of
+    cache[i] and attends over positions [0, pos]; returns (the next normalised input, h)."""
+
     hq, hkv, d = cfg["num_qo_heads"], cfg["num_kv_heads"], cfg["head_dim"]
     eps, theta = cfg["rms_eps"], cfg["rope_theta"]
     n = h.shape[0]
-    x = norms.rmsnorm(h, w["layers"][0]["input_norm"], eps)
-    for i, L in enumerate(w["layers"]):
-        qkv = _mm(x, L["qkv"])
-        q = qkv[:, : hq * d].reshape(n, hq, d)
-        k = qkv[:, hq * d : (hq + hkv) * d].reshape(n, hkv, d)
-        v = qkv[:, (hq + hkv) * d :].reshape(n, hkv, d)
-        q = qk_rope.norm_rope(q, L["q_norm"], positions, eps, theta, False)
-        k = qk_rope.norm_rope(k, L["k_norm"], positions, eps, theta, False)
-        cache[i, :, 0, pos] = k
-        cache[i, :, 1, pos] = v
-        a = bf16.round_f32(attention.short_cache_attention(q, cache[i, :, 0], cache[i, :, 1], pos + 1))
-        o = _mm(a.reshape(n, hq * d), L["o"])
-        x, h = norms.add_rmsnorm(o, h, L["post_norm"], eps)
-        act = norms.silu_mul(_mm(x, L["gate_up"]))
-        down = _mm(act, L["down"])
-        nxt = w["final_norm"] if i + 1 == len(w["layers"]) else w["layers"][i + 1]["input_norm"]
-        x, h = norms.add_rmsnorm(down, h, nxt, eps)
+    L = w["layers"][i]
+    x = norms.rmsnorm(h, L["input_norm"], eps)
+    qkv = _mm(x, L["qkv"])
+    q = qkv[:, : hq * d].reshape(n, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].reshape(n, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].reshape(n, hkv, d)
+    q = qk_rope.norm_rope(q, L["q_norm"], positions, eps, theta, False)
+    k = qk_rope.norm_rope(k, L["k_norm"], positions, eps, theta, False)
+    cache[i, :, 0, pos] = k
+    cache[i, :, 1, pos] = v
+    a = bf16.round_f32(attention.short_cache_attention(q, cache[i, :, 0], cache[i, :, 1], pos + 1))
+    o = _mm(a.reshape(n, hq * d), L["o"])
+    x, h = norms.add_rmsnorm(o, h, L["post_norm"], eps)
+    act = norms.silu_mul(_mm(x, L["gate_up"]))
+    down = _mm(act, L["down"])
+    nxt = w["final_norm"] if i + 1 == len(w["layers"]) else w["layers"][i + 1]["input_norm"]
+    return norms.add_rmsnorm(down, h, nxt, eps)
+
+
+def _layers(w: dict, cfg: dict, h: np.ndarray, cache: np.ndarray, pos: int, positions: np.ndarray) -> tuple:
+    x = None
+    for i in range(len(w["layers"])):
+        x, h = layer(w, cfg, i, h, cache, pos, positions)
     return x, h
 
 
+def logits_of(w: dict, x: np.ndarray, group: int) -> np.ndarray:
+    """Group ``group``'s logits (1-based) from the normalised hidden state x."""
+
+    return _mm(x, w["lm_head"][group - 1])
+
+
 def whole_frame(w: dict, cfg: dict, layer0_token: np.ndarray, past_hidden: np.ndarray, tokens: np.ndarray,
-                positions: np.ndarray | None = None):
-    """Teacher-forced frame: returns (logits [G-1, R, V], codec_sum [R, talker_hidden], cache)."""
+                positions: np.ndarray | None = None, forced_cache: np.ndarray | None = None):
+    """Teacher-forced frame: returns (logits [G-1, R, V], codec_sum [R, talker_hidden], cache).
+
+    ``forced_cache`` (the device's cache after the frame, [layers, R, 2, G, Hkv, D]): each pass g >= 1
+    starts from it for positions < g (pass p writes only position p, so the device's final cache
+    holds what each pass saw), so every pass is checked on its own and errors do not carry from pass
+    to pass; the returned cache still holds the oracle's own K/V at every position.
+    """
 
     groups = cfg["num_code_groups"]
     rows = layer0_token.shape[0]
@@ -73,11 +94,17 @@ def whole_frame(w: dict, cfg: dict, layer0_token: np.ndarray, past_hidden: np.nd
     codec_sum = w["layer0_embedding"][layer0_token].astype(np.float32)
     h = w["projected_layer0"][layer0_token].astype(np.float32)
     logits = np.zeros((groups - 1, rows, w["lm_head"].shape[1]), dtype=np.float32)
+    own = cache if forced_cache is None else cache.copy()
     for g in range(1, groups):
+        if forced_cache is not None:
+            own[:, :, :, g - 1] = cache[:, :, :, g - 1]  # keep the oracle's own K/V of the last pass
+            cache[:, :, :, :g] = forced_cache[:, :, :, :g]
         x, _ = _layers(w, cfg, h, cache, g, positions[:, g])
         logits[g - 1] = _mm(x, w["lm_head"][g - 1])
         tok = tokens[g - 1]
         codec_sum = bf16.round_f32(codec_sum + w["codec_embedding"][g - 1][tok])
         if g < groups - 1:
             h = w["projected_residual"][g - 1][tok].astype(np.float32)
-    return logits, codec_sum, cache
+    if forced_cache is not None:
+        own[:, :, :, groups - 1] = cache[:, :, :, groups - 1]
+    return logits, codec_sum, own

@@ -102,13 +102,23 @@ def test_frame_replays_in_a_graph(nq, device):
 
 @pytest.mark.timeout(300)
 def test_bench_frame_b128_matches_oracle(nq, device):
-    """The frame batch bench.py replays (5 layers, 128 rows, counter RNG, hipGraph) vs the oracle,
-    teacher-forced with the replay's own tokens: logits of every group within bf16 tolerance, every
-    draw bit-exact, codec_sum exact; a second replay gives the same bits."""
+    """The frame batch bench.py replays (5 layers, 128 rows, counter RNG, hipGraph) vs the oracle:
+
+    - two replays give the same bits, and an eager run of the same frame (recording the residual
+      stream of every pass and layer) gives them too;
+    - teacher-forced per layer: every layer of every pass runs in the oracle on the device's own
+      input and the device's K/V of the earlier positions; its residual update within a relative L2
+      of 1e-2 and its K/V at the pass's position within bf16 tolerance;
+    - each group's logits from the device's own final hidden state held to the bf16 bound (mean
+      2e-3, max 2e-2), every draw bit-exact on the device's logits, codec_sum exact;
+    - teacher-forced per pass (the device's cache of the earlier positions and its tokens, errors
+      then compound through the pass's 5 layers only): mean 2e-3 per group, max 3e-2 (about two bf16
+      ulps of the largest logits, |x| < 4)."""
     import bench
 
     cfg, w, frame, call = bench.build_code_predictor(torch)
     rows = frame.tokens.shape[1]
+    groups, layers = cfg.num_code_groups, cfg.num_layers
     call.replay()
     torch.cuda.synchronize()
     first = [frame.frames.clone(), frame.codec_sum.clone(), frame.logits.clone()]
@@ -116,20 +126,40 @@ def test_bench_frame_b128_matches_oracle(nq, device):
     torch.cuda.synchronize()
     assert torch.equal(first[0], frame.frames) and torch.equal(first[1], frame.codec_sum)
     assert torch.equal(first[2], frame.logits)
+    frame.trace = torch.zeros(groups, layers + 2, rows, cfg.hidden, dtype=torch.bfloat16, device=device)
+    frame.forward()
+    torch.cuda.synchronize()
+    assert torch.equal(first[0], frame.frames) and torch.equal(first[2], frame.logits)
 
     hw = _host_weights(w)
     hcfg = dict(num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
                 rms_eps=cfg.rms_eps, rope_theta=cfg.rope_theta, num_code_groups=cfg.num_code_groups)
     tokens = to_np(frame.tokens)
-    logits, csum, cache = o_cp.whole_frame(hw, hcfg, to_np(frame.layer0_token), to_np(frame.past_hidden), tokens)
     got = to_np(frame.logits)
-    # relative to the logits' RMS (about 0.64 here): the device and the oracle round the same bf16
-    # pipeline from fp32 sums taken in different orders, and each keeps its own bf16 K/V cache over
-    # the 16 passes x 5 layers, so differences of one bf16 step (0.4 % at the RMS) carry from pass
-    # to pass; a wrong position, slot or weight moves logits by the order of the RMS itself
+    trace = to_np(frame.trace)
+    device_cache = to_np(frame.kv_cache)
+    positions = to_np(frame.position_ids)
+    worst, kv_worst = 0.0, 0.0
+    for g in range(groups):
+        for i in range(layers):
+            cache = device_cache.copy()
+            _, h = o_cp.layer(hw, hcfg, i, trace[g, i], cache, g, positions[:, g])
+            want, dev = h - trace[g, i], trace[g, i + 1] - trace[g, i]
+            worst = max(worst, float(np.linalg.norm(dev - want) / np.linalg.norm(want)))
+            kv_worst = max(kv_worst, float(np.abs(cache[i, :, :, g] - device_cache[i, :, :, g]).max()))
+    print(f"per-layer rel L2 worst {worst:.2e}, K/V max err {kv_worst:.2e}", flush=True)
+    assert worst <= 1e-2 and kv_worst <= 3e-2, (worst, kv_worst)
+    head = [(float(e.mean()), float(e.max())) for e in
+            (np.abs(got[g - 1] - o_cp.logits_of(hw, trace[g, layers + 1], g)) for g in range(1, groups))]
+    print("per-group head logit error (mean, max):", ["%.1e/%.1e" % m for m in head], flush=True)
+    assert all(mean <= 2e-3 and mx <= 2e-2 for mean, mx in head), head
+
+    logits, csum, _ = o_cp.whole_frame(hw, hcfg, to_np(frame.layer0_token), to_np(frame.past_hidden), tokens,
+                                       forced_cache=device_cache)
     err = np.abs(got - logits)
-    rms = float(np.sqrt(np.mean(logits.astype(np.float64) ** 2)))
-    assert err.mean() <= 8e-3 * rms and err.max() <= 8e-2 * rms, (err.mean() / rms, err.max() / rms)
+    per_group = [(float(e.mean()), float(e.max())) for e in err]
+    print("per-pass logit error (mean, max):", ["%.1e/%.1e" % m for m in per_group], flush=True)
+    assert all(mean <= 2e-3 and mx <= 3e-2 for mean, mx in per_group), per_group
     seeds, offs = to_np(frame.seed), to_np(frame.offsets)
     for k in range(15):
         u = np.array([o_samp.uniform_from_counter(int(seeds[r]), int(offs[r, k])) for r in range(rows)], np.float32)
@@ -137,44 +167,3 @@ def test_bench_frame_b128_matches_oracle(nq, device):
         np.testing.assert_array_equal(tokens[k], want_tok)
     np.testing.assert_array_equal(to_np(frame.frames)[:, 1:], tokens.T)
     np.testing.assert_array_equal(to_np(frame.codec_sum), csum)
-    np.testing.assert_allclose(to_np(frame.kv_cache), cache, atol=3e-2, rtol=2e-2)
-
-
-@pytest.mark.parametrize("rows,hq,hk,d,splits,pos", [(37, 16, 8, 64, 4, 0), (128, 16, 8, 64, 4, 7),
-                                                     (9, 16, 8, 64, 3, 15), (6, 8, 8, 128, 2, 4)])
-def test_fused_rope_short_attention_equals_the_two_launches(nq, device, rows, hq, hk, d, splits, pos):
-    """One launch (q/k norm + RoPE + dense K/V write + short-cache attention from the QKV planes) gives
-    the bits of qkv_partials_norm_rope_dense_cache_ followed by decode_attn_nhd_short_cache: the rotated
-    q, the cache (every position) and the attention output."""
-
-    from nari_qwen3_tts_amd.kernels import (decode_attn_nhd_short_cache, qkv_partials_norm_rope_dense_cache_,
-                                            qkv_partials_rope_short_attention_)
-
-    print(f"case rows {rows} heads {hq}/{hk} d {d} splits {splits} pos {pos}", flush=True)
-    g = torch.Generator(device=device)
-    g.manual_seed(rows * 131 + pos)
-    width = (hq + 2 * hk) * d
-    planes = torch.randn(splits, rows, width, generator=g, device=device) * 0.7
-    qw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
-    kw = (torch.rand(d, generator=g, device=device) + 0.5).to(torch.bfloat16)
-    positions = torch.randint(0, 4096, (rows,), generator=g, device=device, dtype=torch.long)
-    cache0 = torch.randn(rows, 2, 16, hk, d, generator=g, device=device).to(torch.bfloat16)
-    results = []
-    for fused in (False, True):
-        cache = cache0.clone()
-        q = torch.zeros(rows, hq, d, dtype=torch.bfloat16, device=device)
-        out = torch.zeros(rows, hq, d, dtype=torch.bfloat16, device=device)
-        if fused:
-            qkv_partials_rope_short_attention_(planes, splits, q, qw, kw, positions, 1e-6, 1e6, cache[:, 0],
-                                               cache[:, 1], pos, out)
-        else:
-            qkv_partials_norm_rope_dense_cache_(planes, splits, q, qw, kw, positions, 1e-6, 1e6, cache[:, 0],
-                                                cache[:, 1], pos)
-            decode_attn_nhd_short_cache(q, cache[:, 0], cache[:, 1], pos + 1, out=out)
-        torch.cuda.synchronize()
-        results.append((q, cache, out))
-    (q0, c0, o0), (q1, c1, o1) = results
-    assert torch.equal(q0, q1)
-    assert torch.equal(c0, c1)
-    assert torch.equal(o0, o1)
-    assert not torch.equal(c0, cache0)  # the position was written
