@@ -635,6 +635,24 @@ int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, const int32_t *
                          int Cout, int K, int dilation, int groups, const float *act_alpha,
                          const float *act_beta, const float *residual, int64_t ldres, float *out,
                          int64_t ldo, void *stream);
+
+/*
+ * nq_codec_residual_unit: one decoder residual unit of C <= 32 channels in one
+ * launch (plus the history update of its K-tap convolution),
+ *   out = x + conv1x1_w2(snake_a2(causal_conv_w1(snake_a1(x), dilation) + b1)) + b2,
+ * with the same per-stream history rules as nq_codec_causal_conv for the
+ * K-tap convolution (history [slots, (K-1)*dilation, C] of snake_a1(x),
+ * advanced in place).  Replaces the residual unit of the upstream decoder block
+ * as the adapter runs it (model/incremental_codec.py:58-88 for the causal
+ * convolutions): two convolutions whose intermediate tensor never reaches
+ * memory; the result has the bits of the two nq_codec_causal_conv launches.
+ * w1 [C, C, K], w2 [C, C, 1]; out must not alias x.  C must be 8, 16 or 32.
+ */
+int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                           const int32_t *slots, float *history, int C, int K, int dilation, const float *w1,
+                           const float *b1, const float *a1_alpha, const float *a1_beta, const float *w2,
+                           const float *b2, const float *a2_alpha, const float *a2_beta, float *out, int64_t ldo,
+                           void *stream);
 int nq_codec_causal_transconv(const float *x, int64_t ldx, int64_t T_in, const int32_t *offsets, int B,
                               int u_in, int stride_s, const int32_t *slots, float *overlap, const float *w,
                               const float *bias, int Cin, int Cout, const float *act_alpha,

@@ -276,6 +276,21 @@ class IncrementalCodecDecoder:
                   out.data_ptr(), out.stride(0), self._stream)
         return out
 
+    def _res_unit(self, x, u, name, R, dilation):
+        """x + conv1x1(snake2(conv(snake1(x)) + b1)) + b2: narrow units (8, 16 or 32 channels) in one
+        launch whose intermediate never reaches memory; wider ones as the two convolutions."""
+
+        c = x.shape[1]
+        if c not in (8, 16, 32) or c * R.c1_w.shape[2] >= self.GEMM_MIN_CIN_K:
+            y = self._conv(x, u, name, R.c1_w, R.c1_b, dilation=dilation, act=(R.a1, R.b1))
+            return self._conv(y, u, None, R.c2_w, R.c2_b, act=(R.a2, R.b2), residual=x)
+        out = torch.empty_like(x)
+        _lib.call("nq_codec_residual_unit", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u,
+                  self._slots.data_ptr(), self._pool.hist[name].data_ptr(), c, R.c1_w.shape[2], dilation,
+                  R.c1_w.data_ptr(), _lib.ptr(R.c1_b), R.a1.data_ptr(), R.b1.data_ptr(), R.c2_w.data_ptr(),
+                  _lib.ptr(R.c2_b), R.a2.data_ptr(), R.b2.data_ptr(), out.data_ptr(), out.stride(0), self._stream)
+        return out
+
     def _transconv(self, x, u_in, s, name, w, b, act=None):
         c_in, c_out = w.shape[0], w.shape[1]
         a_ptr = _lib.ptr(act[0]) if act else None
@@ -583,8 +598,7 @@ class IncrementalCodecDecoder:
             x = self._transconv(x, u, s, f"dec{bi + 1}.tc", Bk.tc_w, Bk.tc_b, act=(Bk.alpha, Bk.beta))
             u *= s
             for j, (dil, R) in enumerate(zip(c.dilations, Bk.res)):
-                y = self._conv(x, u, f"dec{bi + 1}.res{j}.a", R.c1_w, R.c1_b, dilation=dil, act=(R.a1, R.b1))
-                x = self._conv(y, u, None, R.c2_w, R.c2_b, act=(R.a2, R.b2), residual=x)
+                x = self._res_unit(x, u, f"dec{bi + 1}.res{j}.a", R, dil)
         y = self._conv(x, u, "final", w.final_w, w.final_b, act=(w.final_alpha, w.final_beta))
         n = T * spf
         wav = torch.empty(n, dtype=torch.float32, device=dev)

@@ -163,12 +163,21 @@ conv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *
 // stream's history from global memory.  The thread finds its first row's
 // stream by binary search and steps forward for its later rows.  Outputs (and
 // the residual) move as float4 when the row strides allow it.
-template <int CO, int R>
+//
+// kUnit: the decoder's whole residual unit in one launch (Cin == Cout == C):
+// out = res + conv1x1(snake2(conv(snake1(x)) + bias)) + bias2, with res the
+// input x itself.  The 1x1 convolution runs in registers on the thread's
+// conv outputs (its weights [ci][co] in LDS), in the order of the separate
+// 1x1 launch, so the bits are those of the two launches; the intermediate
+// tensor never reaches memory.
+template <int CO, int R, bool kUnit = false>
 __global__ void __launch_bounds__(kCodecThreads)
 conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
                   const int32_t *__restrict__ slots, const float *__restrict__ hist, const float *__restrict__ w,
                   const float *__restrict__ bias, int Cin, int Cout, int K, int dil, Act act,
-                  const float *__restrict__ res, int64_t ldres, float *__restrict__ out, int64_t ldo) {
+                  const float *__restrict__ res, int64_t ldres, float *__restrict__ out, int64_t ldo,
+                  const float *__restrict__ w2 = nullptr, const float *__restrict__ bias2 = nullptr,
+                  Act act2 = Act{nullptr, nullptr}) {
     constexpr int ROWS = kCodecThreads * R;
     extern __shared__ float lds[];
     const int pad = (K - 1) * dil;
@@ -177,6 +186,9 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
     float *wsm = xs + ((ROWS + pad) * pitch + 3) / 4 * 4;       // [Cin * K * CO], 16-byte aligned
     float *sa = wsm + Cin * K * CO;                             // [Cin]
     float *sb = sa + Cin;                                       // [Cin]
+    float *w2s = sb + Cin + (kUnit ? (4 - (Cin * K * CO + 2 * Cin) % 4) % 4 : 0);  // [Cin][CO], 16-byte aligned
+    float *sa2 = w2s + Cin * CO;                                // [Cin]
+    float *sb2 = sa2 + Cin;                                     // [Cin]
     const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS;
     for (int e = threadIdx.x; e < Cin * K * CO; e += kCodecThreads) {
         const int co = e % CO;
@@ -187,6 +199,16 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
     if (act.alpha && threadIdx.x < Cin) {
         sa[threadIdx.x] = act.a_of(threadIdx.x);
         sb[threadIdx.x] = act.inv_b_of(threadIdx.x);
+    }
+    if constexpr (kUnit) {
+        for (int e = threadIdx.x; e < Cin * CO; e += kCodecThreads) {
+            const int co = e % CO, ci = e / CO;
+            w2s[e] = co < Cout ? w2[static_cast<int64_t>(co) * Cin + ci] : 0.f;
+        }
+        if (act2.alpha && threadIdx.x < Cin) {
+            sa2[threadIdx.x] = act2.a_of(threadIdx.x);
+            sb2[threadIdx.x] = act2.inv_b_of(threadIdx.x);
+        }
     }
     __syncthreads();
     for (int e = threadIdx.x; e < (ROWS + pad) * Cin; e += kCodecThreads) {
@@ -261,6 +283,34 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
     };
     if (__all(staged)) taps(std::true_type{});
     else taps(std::false_type{});
+    if constexpr (kUnit) {
+        // the 1x1 convolution of snake2(conv + bias), then its bias and the residual below
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float yv[CO];
+#pragma unroll
+            for (int j = 0; j < CO; ++j) {
+                const float y = acc[r][j] + (bias && j < Cout ? bias[j] : 0.f);
+                yv[j] = act2.alpha && j < Cout ? snake(y, sa2[j], sb2[j]) : y;
+                acc[r][j] = 0.f;
+            }
+#pragma unroll
+            for (int ci = 0; ci < CO; ++ci) {
+                if (ci >= Cin) break;
+                const float4 *w4 = reinterpret_cast<const float4 *>(w2s + ci * CO);
+                const float xv = yv[ci];
+#pragma unroll
+                for (int j = 0; j < CO / 4; ++j) {
+                    const float4 ww = w4[j];
+                    acc[r][4 * j] += xv * ww.x;
+                    acc[r][4 * j + 1] += xv * ww.y;
+                    acc[r][4 * j + 2] += xv * ww.z;
+                    acc[r][4 * j + 3] += xv * ww.w;
+                }
+            }
+        }
+        bias = bias2;
+    }
     const bool vec = Cout == CO && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                      (!res || ((ldres & 3) == 0 && (reinterpret_cast<uintptr_t>(res) & 15) == 0));
 #pragma unroll
@@ -300,9 +350,11 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
 
 constexpr int conv_small_rows(int CO) { return CO <= 16 ? 2 : 1; }
 
-size_t conv_small_lds(int Cin, int K, int dil, int CO) {
+size_t conv_small_lds(int Cin, int K, int dil, int CO, bool unit = false) {
     const size_t rows = static_cast<size_t>(kCodecThreads) * conv_small_rows(CO);
-    return ((rows + (K - 1) * dil) * (Cin + 1) + 3 + static_cast<size_t>(Cin) * K * CO + 2 * Cin) * sizeof(float);
+    const size_t unit_floats = unit ? 3 + static_cast<size_t>(Cin) * CO + 2 * Cin : 0;
+    return ((rows + (K - 1) * dil) * (Cin + 1) + 3 + static_cast<size_t>(Cin) * K * CO + 2 * Cin + unit_floats) *
+           sizeof(float);
 }
 
 // depthwise causal Conv1d (groups == C): one thread per (row, channel)
@@ -802,6 +854,37 @@ extern "C" int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, cons
         hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * Cin)), dim3(kCodecThreads),
                            0, st, x, ldx, offsets, B, u, slots, history, Cin, pad, groups == 1 ? act : Act{nullptr, nullptr});
     }
+    return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
+                                      const int32_t *slots, float *history, int C, int K, int dilation, const float *w1,
+                                      const float *b1, const float *a1_alpha, const float *a1_beta, const float *w2,
+                                      const float *b2, const float *a2_alpha, const float *a2_beta, float *out,
+                                      int64_t ldo, void *stream) {
+    NQ_CHECK_ARG(x && offsets && slots && history && w1 && w2 && out && B > 0 && u > 0 && T >= 0);
+    NQ_CHECK_ARG(C > 0 && K >= 2 && K <= kConvKMax && dilation >= 1 && ldx >= C && ldo >= C && out != x);
+    NQ_CHECK_ARG((a1_alpha == nullptr) == (a1_beta == nullptr) && (a2_alpha == nullptr) == (a2_beta == nullptr));
+    const int co_pad = C <= 8 ? 8 : C <= 16 ? 16 : 32;
+    if (C > 32 || C != co_pad) return NQ_ERR_UNSUPPORTED;
+    const size_t lds = conv_small_lds(C, K, dilation, co_pad, true);
+    if (lds > 150 * 1024) return NQ_ERR_UNSUPPORTED;
+    if (T == 0) return NQ_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const Act act1{a1_alpha, a1_beta}, act2{a2_alpha, a2_beta};
+    const int64_t rows = static_cast<int64_t>(kCodecThreads) * conv_small_rows(co_pad);
+    const dim3 grid(static_cast<unsigned>((T + rows - 1) / rows));
+#define NQ_UNIT(CO)                                                                                                 \
+    hipLaunchKernelGGL((conv_small_kernel<CO, conv_small_rows(CO), true>), grid, dim3(kCodecThreads), lds, st, x, ldx, \
+                       T, offsets, B, u, slots, history, w1, b1, C, C, K, dilation, act1, x, ldx, out, ldo, w2, b2,  \
+                       act2)
+    if (co_pad == 8) NQ_UNIT(8);
+    else if (co_pad == 16) NQ_UNIT(16);
+    else NQ_UNIT(32);
+#undef NQ_UNIT
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * C)), dim3(kCodecThreads), 0, st,
+                       x, ldx, offsets, B, u, slots, history, C, (K - 1) * dilation, act1);
     return NQ_LAUNCH_STATUS();
 }
 

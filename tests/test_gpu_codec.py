@@ -105,3 +105,45 @@ def test_pcm16_kernel_known_answers(nq, device):
     torch.cuda.synchronize()
     assert pcm.tolist() == [-32767, -16384, 0, 16384, 32767]
     assert wav.tolist() == [-1.0, -0.5, 0.0, 0.5, 1.0]
+
+
+@pytest.mark.parametrize("channels,dilation", [(8, 9), (16, 3), (32, 1)])
+def test_residual_unit_equals_its_two_convolutions(nq, device, channels, dilation):
+    """nq_codec_residual_unit gives the bits of its two nq_codec_causal_conv launches (the K-tap
+    convolution with its history, then the 1x1 convolution with the residual) on ragged streams,
+    including streams shorter than the receptive field, and advances the history identically."""
+    from nari_qwen3_tts_amd import _lib
+
+    g = torch.Generator(device=device)
+    g.manual_seed(channels + dilation)
+    c, k, u = channels, 7, 20
+    frames = [3, 1, 12, 0, 7]
+    off = torch.tensor(np.concatenate([[0], np.cumsum(frames)]), dtype=torch.int32, device=device)
+    B, T = len(frames), sum(frames) * u
+    slots = torch.tensor([4, 0, 2, 1, 3], dtype=torch.int32, device=device)
+    pad = (k - 1) * dilation
+
+    def r(*shape, s=1.0):
+        return torch.randn(*shape, generator=g, device=device) * s
+
+    x = r(T, c)
+    w1, b1, a1, be1 = r(c, c, k, s=0.2), r(c, s=0.1), r(c, s=0.1), r(c, s=0.1)
+    w2, b2, a2, be2 = r(c, c, 1, s=0.3), r(c, s=0.01), r(c, s=0.1), r(c, s=0.1)
+    hist0 = r(8, pad, c)
+    st = _lib.stream(device)
+    hist_a, hist_b = hist0.clone(), hist0.clone()
+    y = torch.empty_like(x)
+    want = torch.empty_like(x)
+    _lib.call("nq_codec_causal_conv", x.data_ptr(), x.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(),
+              hist_a.data_ptr(), w1.data_ptr(), b1.data_ptr(), c, c, k, dilation, 1, a1.data_ptr(), be1.data_ptr(),
+              None, 0, y.data_ptr(), y.stride(0), st)
+    _lib.call("nq_codec_causal_conv", y.data_ptr(), y.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(), None,
+              w2.data_ptr(), b2.data_ptr(), c, c, 1, 1, 1, a2.data_ptr(), be2.data_ptr(), x.data_ptr(), x.stride(0),
+              want.data_ptr(), want.stride(0), st)
+    got = torch.empty_like(x)
+    _lib.call("nq_codec_residual_unit", x.data_ptr(), x.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(),
+              hist_b.data_ptr(), c, k, dilation, w1.data_ptr(), b1.data_ptr(), a1.data_ptr(), be1.data_ptr(),
+              w2.data_ptr(), b2.data_ptr(), a2.data_ptr(), be2.data_ptr(), got.data_ptr(), got.stride(0), st)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(hist_a, hist_b)
