@@ -211,19 +211,53 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < (ROWS + pad) * Cin; e += kCodecThreads) {
-        const int rr = e / Cin, c = e - rr * Cin;
-        const int64_t g = row0 - pad + rr;
-        float v = 0.f;
-        if (g >= 0 && g < T) {
-            v = x[g * ldx + c];
-            if (act.alpha) v = snake(v, sa[c], sb[c]);
+    if ((Cin & 3) == 0 && (ldx & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        // 128-bit loads, eight per thread in flight before any is activated and stored
+        const int vpr = Cin / 4;
+        const int nvec = (ROWS + pad) * vpr;
+        for (int e0 = threadIdx.x; e0 < nvec; e0 += 8 * kCodecThreads) {
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = e0 + i * kCodecThreads;
+                const int rr = e / vpr;
+                const int64_t g = row0 - pad + rr;
+                v[i] = (e < nvec && g >= 0 && g < T)
+                           ? *reinterpret_cast<const float4 *>(x + g * ldx + (e - rr * vpr) * 4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = e0 + i * kCodecThreads;
+                if (e >= nvec) break;
+                const int rr = e / vpr, c = (e - rr * vpr) * 4;
+                const int64_t g = row0 - pad + rr;
+                float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+                if (act.alpha && g >= 0 && g < T) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) f[q] = snake(f[q], sa[c + q], sb[c + q]);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xs[rr * pitch + c + q] = f[q];
+            }
         }
-        xs[rr * pitch + c] = v;
+    } else {
+        for (int e = threadIdx.x; e < (ROWS + pad) * Cin; e += kCodecThreads) {
+            const int rr = e / Cin, c = e - rr * Cin;
+            const int64_t g = row0 - pad + rr;
+            float v = 0.f;
+            if (g >= 0 && g < T) {
+                v = x[g * ldx + c];
+                if (act.alpha) v = snake(v, sa[c], sb[c]);
+            }
+            xs[rr * pitch + c] = v;
+        }
     }
     __syncthreads();
     const int64_t first = row0 + threadIdx.x;
-    if (first >= T) return;
+    // the residual unit meets a second barrier below, so its threads past the end stay (they only
+    // skip the stores)
+    if (!kUnit && first >= T) return;
     // streams of the thread's rows (non-decreasing)
     int sb_[R];
     int64_t local[R];
@@ -248,6 +282,27 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
     bool staged = true;
 #pragma unroll
     for (int r = 0; r < R; ++r) staged = staged && local[r] >= pad;
+    // one tap's multiply-adds over the input channels: the rows' inputs xr[r][ci], the weights at wk
+    // ([ci][k][co] with row pitch kw floats)
+    auto channel_loop = [&](const float *const (&xr)[R], const float *wk, int kw, int cin) {
+        for (int ci = 0; ci < cin; ++ci) {
+            float xv[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) xv[r] = xr[r][ci];
+            const float4 *w4 = reinterpret_cast<const float4 *>(wk + ci * kw);
+#pragma unroll
+            for (int j = 0; j < CO / 4; ++j) {
+                const float4 ww = w4[j];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    acc[r][4 * j] += xv[r] * ww.x;
+                    acc[r][4 * j + 1] += xv[r] * ww.y;
+                    acc[r][4 * j + 2] += xv[r] * ww.z;
+                    acc[r][4 * j + 3] += xv[r] * ww.w;
+                }
+            }
+        }
+    };
     auto taps = [&](auto lds_only) {
         for (int k = 0; k < K; ++k) {
             const int back = (K - 1 - k) * dil;
@@ -261,54 +316,28 @@ conv_small_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int
                     xr[r] = src >= 0 ? xs + (threadIdx.x + r * kCodecThreads + pad - back) * pitch
                                      : hist + (static_cast<int64_t>(slots[sb_[r]]) * pad + pad + src) * Cin;
             }
-            const float *wk = wsm + k * CO;
-            for (int ci = 0; ci < Cin; ++ci) {
-                float xv[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) xv[r] = xr[r][ci];
-                const float4 *w4 = reinterpret_cast<const float4 *>(wk + ci * K * CO);
-#pragma unroll
-                for (int j = 0; j < CO / 4; ++j) {
-                    const float4 ww = w4[j];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        acc[r][4 * j] += xv[r] * ww.x;
-                        acc[r][4 * j + 1] += xv[r] * ww.y;
-                        acc[r][4 * j + 2] += xv[r] * ww.z;
-                        acc[r][4 * j + 3] += xv[r] * ww.w;
-                    }
-                }
-            }
+            channel_loop(xr, wsm + k * CO, K * CO, Cin);
         }
     };
     if (__all(staged)) taps(std::true_type{});
     else taps(std::false_type{});
     if constexpr (kUnit) {
-        // the 1x1 convolution of snake2(conv + bias), then its bias and the residual below
+        // the 1x1 convolution of snake2(conv + bias): each thread parks its rows' activated conv
+        // outputs in its own rows of the (now free) staging area and reads them back per channel
+        __syncthreads();
+        const float *yr[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float yv[CO];
+            float *yw = xs + (threadIdx.x + r * kCodecThreads) * pitch;
 #pragma unroll
             for (int j = 0; j < CO; ++j) {
-                const float y = acc[r][j] + (bias && j < Cout ? bias[j] : 0.f);
-                yv[j] = act2.alpha && j < Cout ? snake(y, sa2[j], sb2[j]) : y;
+                const float y = acc[r][j] + (bias ? bias[j] : 0.f);
+                yw[j] = act2.alpha ? snake(y, sa2[j], sb2[j]) : y;
                 acc[r][j] = 0.f;
             }
-#pragma unroll
-            for (int ci = 0; ci < CO; ++ci) {
-                if (ci >= Cin) break;
-                const float4 *w4 = reinterpret_cast<const float4 *>(w2s + ci * CO);
-                const float xv = yv[ci];
-#pragma unroll
-                for (int j = 0; j < CO / 4; ++j) {
-                    const float4 ww = w4[j];
-                    acc[r][4 * j] += xv * ww.x;
-                    acc[r][4 * j + 1] += xv * ww.y;
-                    acc[r][4 * j + 2] += xv * ww.z;
-                    acc[r][4 * j + 3] += xv * ww.w;
-                }
-            }
+            yr[r] = yw;
         }
+        channel_loop(yr, w2s, CO, Cin);
         bias = bias2;
     }
     const bool vec = Cout == CO && (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
@@ -864,6 +893,7 @@ extern "C" int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, co
                                       int64_t ldo, void *stream) {
     NQ_CHECK_ARG(x && offsets && slots && history && w1 && w2 && out && B > 0 && u > 0 && T >= 0);
     NQ_CHECK_ARG(C > 0 && K >= 2 && K <= kConvKMax && dilation >= 1 && ldx >= C && ldo >= C && out != x);
+    if (K != kConvKMax) return NQ_ERR_UNSUPPORTED;  // the fused kernel is built for 7 taps
     NQ_CHECK_ARG((a1_alpha == nullptr) == (a1_beta == nullptr) && (a2_alpha == nullptr) == (a2_beta == nullptr));
     const int co_pad = C <= 8 ? 8 : C <= 16 ? 16 : 32;
     if (C > 32 || C != co_pad) return NQ_ERR_UNSUPPORTED;
