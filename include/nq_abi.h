@@ -612,7 +612,9 @@ int nq_codec_last_rows(const int32_t *off, int B, int u, int32_t *rows, void *st
  *   (depthwise), history [slots, (K-1)*dilation, Cin] holding post-activation
  *   inputs.  Optional SnakeBeta on the input (act_alpha/act_beta: log-scale
  *   per-channel parameters, x + sin(e^a x)^2 / e^b) and a residual added to the
- *   output.  The history is advanced in place after the convolution.
+ *   output.  The history is advanced in place after the convolution; histories
+ *   of more than 4096 values per stream ((K-1)*dilation*Cin) are refused
+ *   (NQ_ERR_UNSUPPORTED) before any launch.
  * nq_codec_causal_transconv: causal ConvTranspose1d with kernel 2*stride and
  *   a stride-long bias-free overlap carry (_causal_transconv, :90-138):
  *   w [Cin, Cout, 2*stride], overlap [slots, stride, Cout]; optional SnakeBeta

@@ -24,6 +24,7 @@ namespace nq {
 namespace {
 
 constexpr int kCodecThreads = 256;
+constexpr int kHistoryPerThread = 16;  // history_update_kernel covers pad * C <= 256 * 16
 
 // stream of stage row t: the largest b with off[b] * u <= t
 __device__ __forceinline__ int stream_of(const int32_t *__restrict__ off, int B, int64_t t, int u) {
@@ -411,23 +412,36 @@ dwconv_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t
     }
 }
 
-// new history = last pad rows of [history ; act(x)] per stream; thread per (stream, channel)
+// new history = last pad rows of [history ; act(x)] per stream
 __global__ void __launch_bounds__(kCodecThreads)
 history_update_kernel(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ off, int B, int u,
                       const int32_t *__restrict__ slots, float *__restrict__ hist, int C, int pad, Act act) {
-    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
-    if (i >= static_cast<int64_t>(B) * C) return;
-    const int b = static_cast<int>(i / C);
-    const int c = static_cast<int>(i - static_cast<int64_t>(b) * C);
+    // one workgroup per stream: every (j, c) of its [pad, C] history is read first (the entries that
+    // shift down and the fresh tail rows, activated), then all are written after a barrier, so no
+    // entry is overwritten before it is read
+    constexpr int kPer = kHistoryPerThread;
+    const int b = blockIdx.x;
     const int64_t base = static_cast<int64_t>(off[b]) * u;
     const int64_t F = static_cast<int64_t>(off[b + 1]) * u - base;
-    float *h = hist + static_cast<int64_t>(slots[b]) * pad * C + c;
-    for (int j = 0; j < pad; ++j) {
-        float v;
-        if (j + F < pad) v = h[(j + F) * C];
-        else v = act.apply(x[(base + F - pad + j) * ldx + c], c);
-        h[static_cast<int64_t>(j) * C] = v;
+    float *h = hist + static_cast<int64_t>(slots[b]) * pad * C;
+    const int n = pad * C;
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = threadIdx.x + i * kCodecThreads;
+        v[i] = 0.f;
+        if (e < n) {
+            const int j = e / C, c = e - j * C;
+            v[i] = j + F < pad ? h[(j + F) * C + c] : act.apply(x[(base + F - pad + j) * ldx + c], c);
+        }
     }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = threadIdx.x + i * kCodecThreads;
+        if (e < n) h[e] = v[i];
+    }
+}
 }
 
 // ---------------------------------------------------------------------------
@@ -844,6 +858,7 @@ extern "C" int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, cons
     NQ_CHECK_ARG(ldx >= Cin && ldo >= Cout && (!residual || ldres >= Cout));
     const int pad = (K - 1) * dilation;
     NQ_CHECK_ARG(pad == 0 || history);
+    if (pad * Cin > kCodecThreads * kHistoryPerThread) return NQ_ERR_UNSUPPORTED;
     if (T == 0) return NQ_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const Act act{act_alpha, act_beta};
@@ -880,7 +895,7 @@ extern "C" int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, cons
     }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     if (pad > 0) {
-        hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * Cin)), dim3(kCodecThreads),
+        hipLaunchKernelGGL(history_update_kernel, dim3(B), dim3(kCodecThreads),
                            0, st, x, ldx, offsets, B, u, slots, history, Cin, pad, groups == 1 ? act : Act{nullptr, nullptr});
     }
     return NQ_LAUNCH_STATUS();
@@ -894,6 +909,7 @@ extern "C" int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, co
     NQ_CHECK_ARG(x && offsets && slots && history && w1 && w2 && out && B > 0 && u > 0 && T >= 0);
     NQ_CHECK_ARG(C > 0 && K >= 2 && K <= kConvKMax && dilation >= 1 && ldx >= C && ldo >= C && out != x);
     if (K != kConvKMax) return NQ_ERR_UNSUPPORTED;  // the fused kernel is built for 7 taps
+    if ((K - 1) * dilation * C > kCodecThreads * kHistoryPerThread) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG((a1_alpha == nullptr) == (a1_beta == nullptr) && (a2_alpha == nullptr) == (a2_beta == nullptr));
     const int co_pad = C <= 8 ? 8 : C <= 16 ? 16 : 32;
     if (C > 32 || C != co_pad) return NQ_ERR_UNSUPPORTED;
@@ -913,7 +929,7 @@ extern "C" int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, co
     else NQ_UNIT(32);
 #undef NQ_UNIT
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
-    hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * C)), dim3(kCodecThreads), 0, st,
+    hipLaunchKernelGGL(history_update_kernel, dim3(B), dim3(kCodecThreads), 0, st,
                        x, ldx, offsets, B, u, slots, history, C, (K - 1) * dilation, act1);
     return NQ_LAUNCH_STATUS();
 }
@@ -1030,7 +1046,8 @@ extern "C" int nq_codec_history_update(const float *x, int64_t ldx, const int32_
                                        const float *act_beta, void *stream) {
     NQ_CHECK_ARG(x && offsets && slots && history && B > 0 && u > 0 && C > 0 && pad > 0 && ldx >= C);
     NQ_CHECK_ARG((act_alpha == nullptr) == (act_beta == nullptr));
-    hipLaunchKernelGGL(history_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * C)), dim3(kCodecThreads), 0,
+    if (pad * C > nq::kCodecThreads * nq::kHistoryPerThread) return NQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(history_update_kernel, dim3(B), dim3(kCodecThreads), 0,
                        static_cast<hipStream_t>(stream), x, ldx, offsets, B, u, slots, history, C, pad,
                        Act{act_alpha, act_beta});
     return NQ_LAUNCH_STATUS();
