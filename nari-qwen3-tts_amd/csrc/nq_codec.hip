@@ -442,7 +442,6 @@ history_update_kernel(const float *__restrict__ x, int64_t ldx, const int32_t *_
         if (e < n) h[e] = v[i];
     }
 }
-}
 
 // ---------------------------------------------------------------------------
 // causal ConvTranspose1d, kernel 2s, stride s, overlap s.  Output row p of a
