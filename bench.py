@@ -519,7 +519,7 @@ def codec_step(args, torch, np) -> dict:
     dev = torch.device("cuda:0")
     cfg = CodecConfig()
     weights = CodecWeights(cfg, dev, seed=CODEC_SEED)
-    dec = IncrementalCodecDecoder(weights, max_streams=CODEC_STREAMS)
+    dec = IncrementalCodecDecoder(weights, max_streams=CODEC_STREAMS, matmul_precision=args.matmul_precision)
     rng = np.random.default_rng(CODEC_SEED)
     states = [dec.new_state() for _ in range(CODEC_STREAMS)]
 
@@ -562,6 +562,7 @@ def codec_step(args, torch, np) -> dict:
                         "8 sliding-window layers, transconv+ConvNeXt x4, decoder blocks x500 -> 24 kHz fp32 PCM",
             "global_batch": CODEC_STREAMS,
             "parallelism": "single GPU",
+            "matmul_precision": dec.matmul_precision,
         },
         "roofline": {
             "bound": "mfma",
@@ -570,7 +571,8 @@ def codec_step(args, torch, np) -> dict:
             "unit": "TFLOP/s",
             "frac": round(achieved / 157.3, 4),
             "traffic": None,
-            "kernel": "whole step (fp32 convolutions, transconvs, window attention, projections)",
+            "kernel": "whole step (fp32 convolutions, transconvs, window attention, projections; the GEMMs' "
+                      "products at the matmul precision, 'high' = bf16x3 splits with fp32 sums)",
             "flops_per_step": flops,
         },
     }
@@ -1280,6 +1282,9 @@ def main() -> int:
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="talker-decode",
                     help="talker-decode is the serving metric; the others measure the neighbouring hot-path rows")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--matmul-precision", choices=["high", "highest"], default="high",
+                    help="codec GEMM products: torch's float32 matmul precision by name (the reference serves "
+                         "with 'high')")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()

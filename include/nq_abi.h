@@ -578,9 +578,16 @@ int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_
  * im2col convolutions:
  *   out[m, n] = res[m, n] + scale[n] * act(sum_k X[r(m), k] W[n, k] + bias[n])
  * with res / scale / bias optional (NULL), act 0 (none) or 1 (GELU, erf form),
- * r(m) = x_rows[m] when x_rows != NULL else m; out may alias res.  fp32
- * products on MFMA.  K % 4 == 0, N % 4 == 0, 16-byte aligned operands and row
- * strides % 4, else NQ_ERR_UNSUPPORTED.
+ * r(m) = x_rows[m] when x_rows != NULL else m; out may alias res.  K % 4 == 0,
+ * N % 4 == 0, 16-byte aligned operands and row strides % 4, else
+ * NQ_ERR_UNSUPPORTED.
+ *
+ * precision names torch's float32 matmul precisions: NQ_MATMUL_HIGHEST, fp32
+ * products on MFMA; NQ_MATMUL_HIGH, the reference's serving policy
+ * (model/checkpoint.py:46-49 sets torch.set_float32_matmul_precision("high")):
+ * each operand as the sum of two bf16 (hi = bf16(v), lo = bf16(v - hi)) and
+ * each product as hi*hi + hi*lo + lo*hi on bf16 MFMA with fp32 sums, within
+ * 3 * 2^-16 of the fp32 product.
  *
  * nq_row_norm: RMSNorm (b == NULL: x * rsqrt(mean(x^2) + eps) * w) or
  * LayerNorm ((x - mean) * rsqrt(var + eps) * w + b) of fp32 rows, width % 4 ==
@@ -589,9 +596,10 @@ int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float *sx, int64_
  * nq_codec_last_rows: rows[b] = max(off[b + 1] * u - 1, 0), the row of each
  * stream's last fresh frame at a stage with u rows per frame.
  */
+enum nq_matmul_precision { NQ_MATMUL_HIGHEST = 0, NQ_MATMUL_HIGH = 1 };
 int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, const float *w, int64_t w_s0, int M, int N, int K,
              const float *bias, int act, const float *res, int64_t r_s0, const float *scale, float *out, int64_t o_s0,
-             void *stream);
+             int precision, void *stream);
 int nq_row_norm(const float *x, int64_t x_s0, int rows, int width, const float *w, const float *b, float eps,
                 float *out, int64_t o_s0, void *stream);
 int nq_codec_last_rows(const int32_t *off, int B, int u, int32_t *rows, void *stream);

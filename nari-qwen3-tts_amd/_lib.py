@@ -29,6 +29,8 @@ NQ_EPI_NONE = 0
 NQ_EPI_ADD_RMSNORM = 1
 NQ_EPI_SILU_MUL = 2
 NQ_EPI_PARTIALS = 3
+NQ_MATMUL_HIGHEST = 0
+NQ_MATMUL_HIGH = 1
 NQ_ATTN_DECODE = 1
 NQ_ATTN_PREFILL = 2
 NQ_NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -86,7 +88,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_fp8_pack_swiglu": [_P, _L, _I, _I, _P, _L, _P],
     "nq_linear_swiglu": [_P, _L, _I, _P, _L, _I, _I, _P, _L, _P],
     "nq_linear_fp8_swiglu": [_P, _L, _P, _L, _I, _P, _L, _P, _L, _I, _I, _P, _L, _P],
-    "nq_sgemm": [_P, _L, _P, _P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _P, _L, _P],
+    "nq_sgemm": [_P, _L, _P, _P, _L, _I, _I, _I, _P, _I, _P, _L, _P, _P, _L, _I, _P],
     "nq_row_norm": [_P, _L, _I, _I, _P, _P, _F, _P, _L, _P],
     "nq_codec_last_rows": [_P, _I, _I, _P, _P],
     "nq_tgemm_splits": [_I, _I, _I],

@@ -24,8 +24,13 @@ causal conv: 2000 samples per 12 Hz frame, 24 kHz fp32 PCM, clamped.
 State lives in device slot arrays (one slot per stream): conv histories,
 transconv overlaps, retained K/V, frame position and valid context count.
 The stateful operators are HIP kernels (``nq_codec_*``); the transformer and
-ConvNeXt projections are plain fp32 GEMMs (torch/hipBLASLt) and the norms and
-GELU in between are torch element-wise ops.
+ConvNeXt projections and the wide convolutions (im2col) run on the library's
+fp32 GEMM with its fused epilogues (``nq_sgemm``), and the norms on
+``nq_row_norm``.  Its products follow torch's float32 matmul precision by name:
+"high" by default, the reference's serving policy
+(model/checkpoint.py:46-49: ``torch.set_float32_matmul_precision("high")``),
+computed as bf16x3 split products with fp32 sums; "highest" keeps full fp32
+products.
 """
 
 from __future__ import annotations
@@ -210,7 +215,13 @@ class _StatePool:
 class IncrementalCodecDecoder:
     """``decoder(codes, states) -> (wav, pcm16)`` over ragged chunks of many streams."""
 
-    def __init__(self, weights: CodecWeights, max_streams: int = 64) -> None:
+    MATMUL_PRECISIONS = {"highest": _lib.NQ_MATMUL_HIGHEST, "high": _lib.NQ_MATMUL_HIGH}
+
+    def __init__(self, weights: CodecWeights, max_streams: int = 64, *, matmul_precision: str = "high") -> None:
+        if matmul_precision not in self.MATMUL_PRECISIONS:
+            raise ValueError(f"matmul_precision must be one of {sorted(self.MATMUL_PRECISIONS)}")
+        self.matmul_precision = matmul_precision
+        self._precision = self.MATMUL_PRECISIONS[matmul_precision]
         self.w = weights
         self.config = weights.config
         self.device = weights.codebooks.device
@@ -321,8 +332,9 @@ class IncrementalCodecDecoder:
         return out
 
     def _sgemm(self, x, w, *, bias=None, act=0, res=None, scale=None, x_rows=None, out=None):
-        """out = res + scale * act(x[x_rows] @ w.T + bias) on the fp32 MFMA GEMM (fp32 row-major x and
-        w [N, K] with unit inner strides; the optional pieces are left out when None)."""
+        """out = res + scale * act(x[x_rows] @ w.T + bias) on the fp32 MFMA GEMM at the decoder's matmul
+        precision (fp32 row-major x and w [N, K] with unit inner strides; the optional pieces are left
+        out when None)."""
 
         rows = x.shape[0] if x_rows is None else x_rows.shape[0]
         n, k = w.shape
@@ -330,7 +342,7 @@ class IncrementalCodecDecoder:
             out = torch.empty(rows, n, dtype=torch.float32, device=self.device)
         _lib.call("nq_sgemm", x.data_ptr(), x.stride(0), _lib.ptr(x_rows), w.data_ptr(), w.stride(0), rows, n, k,
                   _lib.ptr(bias), int(act), _lib.ptr(res), res.stride(0) if res is not None else 0, _lib.ptr(scale),
-                  out.data_ptr(), out.stride(0), self._stream)
+                  out.data_ptr(), out.stride(0), self._precision, self._stream)
         return out
 
     def _norm(self, x, w, eps, b=None):

@@ -6,15 +6,29 @@
 //   out[m, n] = res[m, n] + scale[n] * act(sum_k X[row(m), k] W[n, k] + bias[n])
 //
 // with each of res, scale, bias optional, act none or GELU (erf form, as
-// torch.nn.functional.gelu), and row(m) = m or x_rows[m] (a row gather).  The
-// products run on v_mfma_f32_16x16x4_f32 (full fp32 products and sums, no
-// reduced-precision inputs).  A workgroup owns a BM x BN tile, its WM x WN
-// waves a (16 MT) x (16 NT) block each; 32-wide K slices of the X and W
-// tiles are staged through LDS, double buffered, with two slices of global
-// loads in flight (a K tail reads as zero, columns past N are not stored).
-// Both operands are K-contiguous: a lane's 16-byte LDS read holds 4
-// consecutive k of one row, which feed the 4 MFMAs of a 16-k group
-// (MFMA t sums k = 4 q + t over the lane groups q), so A and B take the same k.
+// torch.nn.functional.gelu), and row(m) = m or x_rows[m] (a row gather).
+//
+// Two product precisions, torch's float32 matmul precisions by name:
+// - "highest": v_mfma_f32_16x16x4_f32, full fp32 products and sums.
+// - "high" (the reference's serving policy, model/checkpoint.py:46-49 sets
+//   torch.set_float32_matmul_precision("high")): each fp32 operand is the sum
+//   of two bf16, v = hi + lo + e with hi = bf16(v), lo = bf16(v - hi) and
+//   |e| <= 2^-16 |v|, and a product is hi*hi + hi*lo + lo*hi on
+//   v_mfma_f32_16x16x32_bf16 (each bf16 product exact in fp32, fp32 sums), so
+//   each product is within 3 * 2^-16 of x*w -- the "sum of two bfloat16"
+//   form torch documents for that precision.  The three MFMAs of a 32-k step
+//   cost about a fifth of the eight fp32 MFMAs of the same step.
+//
+// A workgroup owns a BM x BN tile, its WM x WN waves a (16 MT) x (16 NT) block
+// each; 32-wide K slices of the X and W tiles are staged through LDS, double
+// buffered, with two slices of global loads in flight (a K tail reads as zero,
+// columns past N are not stored).  Both operands are K-contiguous.  fp32
+// stages: a lane's 16-byte LDS read holds 4 consecutive k of one row, which
+// feed the 4 MFMAs of a 16-k group (MFMA t sums k = 4 q + t over the lane
+// groups q), so A and B take the same k.  Split stages: the fp32 slice is
+// split while it is written to LDS, a row holding its 32 hi then its 32 lo
+// values, and a lane's 16-byte read is the 8 consecutive k of one 32-k MFMA
+// operand.
 #include "nq_common.h"
 #include "nq_internal.h"
 
@@ -23,17 +37,25 @@ namespace {
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kSgK = 32;            // K floats per stage
-constexpr int kSgPitch = kSgK + 8;  // LDS row pitch in floats (32 bytes of padding)
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
+
+// LDS row of a stage of KS k: KS fp32, or KS hi then KS lo bf16, then 32 bytes of padding (a row offset of
+// 32 bytes modulo 128 spreads a 16-byte read of 16 rows over the banks)
+template <int KS>
+constexpr int sg_row_bytes() {
+    return KS * 4 + 32;
+}
 
 bool sg_al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // The thread's vectors of one stage: every vector of a thread has the same 4-float chunk of its row,
 // so one test covers the K tail (chunks at or past K read as zero; K % 4 == 0).
-template <int XV, int WV>
+template <int KS, int XV, int WV>
 __device__ __forceinline__ void sg_load(floatx4_t (&xr)[XV], floatx4_t (&wr)[WV], const float *const (&xp)[XV],
                                         const float *const (&wp)[WV], int stage, int k_left) {
-    const int k0 = stage * kSgK;
+    const int k0 = stage * KS;
     const bool in = k0 < k_left;
 #pragma unroll
     for (int q = 0; q < WV; ++q)
@@ -43,44 +65,93 @@ __device__ __forceinline__ void sg_load(floatx4_t (&xr)[XV], floatx4_t (&wr)[WV]
         xr[q] = in ? *reinterpret_cast<const floatx4_t *>(xp[q] + k0) : floatx4_t{0.f, 0.f, 0.f, 0.f};
 }
 
-// vector i = threadIdx.x + T q: tile row i / 8, 4-float chunk i % 8
-template <int XV, int WV, int T>
-__device__ __forceinline__ void sg_store(const floatx4_t (&xr)[XV], const floatx4_t (&wr)[WV], float *xbuf,
-                                         float *wbuf) {
+// v = hi + lo + e: hi = bf16(v), lo = bf16(v - hi) (round to nearest even, v_cvt_pk_bf16_f32; v - hi is
+// exact in fp32), |e| <= 2^-16 |v|
+__device__ __forceinline__ uint32_t sg_pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((floatx2_t){a, b}, bf16x2_t));
+}
+__device__ __forceinline__ void sg_split(const floatx4_t &v, uint2 &hi, uint2 &lo) {
+    hi.x = sg_pack(v[0], v[1]);
+    hi.y = sg_pack(v[2], v[3]);
+    lo.x = sg_pack(v[0] - __uint_as_float(hi.x << 16), v[1] - __uint_as_float(hi.x & 0xffff0000u));
+    lo.y = sg_pack(v[2] - __uint_as_float(hi.y << 16), v[3] - __uint_as_float(hi.y & 0xffff0000u));
+}
+
+// One register set into LDS.  Vector i = threadIdx.x + T q: tile row i / (KS / 4), 4-float chunk
+// c = i % (KS / 4) (k = 4c .. 4c + 3 of the stage): fp32 at byte 16 c of the row, or split, hi at byte
+// 8 c and lo at byte 2 KS + 8 c.
+template <int KS, int V, int T, bool kSplit>
+__device__ __forceinline__ void sg_store_rows(const floatx4_t (&r)[V], char *buf) {
+    constexpr int C = KS / 4;
 #pragma unroll
-    for (int q = 0; q < XV; ++q) {
+    for (int q = 0; q < V; ++q) {
         const int i = threadIdx.x + q * T;
-        *reinterpret_cast<floatx4_t *>(xbuf + (i >> 3) * kSgPitch + (i & 7) * 4) = xr[q];
-    }
-#pragma unroll
-    for (int q = 0; q < WV; ++q) {
-        const int i = threadIdx.x + q * T;
-        *reinterpret_cast<floatx4_t *>(wbuf + (i >> 3) * kSgPitch + (i & 7) * 4) = wr[q];
+        char *row = buf + (i / C) * sg_row_bytes<KS>();
+        if constexpr (kSplit) {
+            uint2 hi, lo;
+            sg_split(r[q], hi, lo);
+            *reinterpret_cast<uint2 *>(row + (i % C) * 8) = hi;
+            *reinterpret_cast<uint2 *>(row + 2 * KS + (i % C) * 8) = lo;
+        } else {
+            *reinterpret_cast<floatx4_t *>(row + (i % C) * 16) = r[q];
+        }
     }
 }
 
-template <int MT, int NT>
-__device__ __forceinline__ void sg_compute(floatx4_t (&acc)[MT][NT], const float *xt, const float *wt) {
+// The MFMAs of one staged slice on the wave's (16 MT) x (16 NT) block; xt / wt point at the lane's row
+// (r16) of the wave's first tile, plus 16 kq bytes.
+template <int MT, int NT, int KS, bool kSplit>
+__device__ __forceinline__ void sg_compute(floatx4_t (&acc)[MT][NT], const char *xt, const char *wt) {
+    constexpr int RB = sg_row_bytes<KS>();
+    if constexpr (kSplit) {
+        // lane (r16, kq): k = 32 j + 8 kq .. + 7 of 32-k step j, the same k in A (W rows) and B (X rows)
 #pragma unroll
-    for (int g = 0; g < kSgK / 16; ++g) {
-        floatx4_t a[NT], b[MT];
+        for (int j = 0; j < KS / 32; ++j) {
+            bf16x8_t ah[NT], al[NT], bh[MT], bl[MT];
 #pragma unroll
-        for (int n = 0; n < NT; ++n) a[n] = *reinterpret_cast<const floatx4_t *>(wt + n * 16 * kSgPitch + g * 16);
+            for (int n = 0; n < NT; ++n) {
+                ah[n] = *reinterpret_cast<const bf16x8_t *>(wt + n * 16 * RB + j * 64);
+                al[n] = *reinterpret_cast<const bf16x8_t *>(wt + n * 16 * RB + 2 * KS + j * 64);
+            }
 #pragma unroll
-        for (int m = 0; m < MT; ++m) b[m] = *reinterpret_cast<const floatx4_t *>(xt + m * 16 * kSgPitch + g * 16);
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
+            for (int m = 0; m < MT; ++m) {
+                bh[m] = *reinterpret_cast<const bf16x8_t *>(xt + m * 16 * RB + j * 64);
+                bl[m] = *reinterpret_cast<const bf16x8_t *>(xt + m * 16 * RB + 2 * KS + j * 64);
+            }
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[n][t], b[m][t], acc[m][n], 0, 0, 0);
+                for (int n = 0; n < NT; ++n) {
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[n], bh[m], acc[m][n], 0, 0, 0);
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[n], bl[m], acc[m][n], 0, 0, 0);
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[n], bh[m], acc[m][n], 0, 0, 0);
+                }
+        }
+    } else {
+        // lane (r16, kq): k = 16 g + 4 kq + t feeds MFMA t of 16-k group g
+#pragma unroll
+        for (int g = 0; g < KS / 16; ++g) {
+            floatx4_t a[NT], b[MT];
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                a[n] = *reinterpret_cast<const floatx4_t *>(wt + n * 16 * RB + g * 64);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                b[m] = *reinterpret_cast<const floatx4_t *>(xt + m * 16 * RB + g * 64);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int n = 0; n < NT; ++n)
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[n][t], b[m][t], acc[m][n], 0, 0, 0);
+        }
     }
 }
 
 __device__ __forceinline__ float sg_gelu(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 
-template <int MT, int NT, int WM, int WN>
+template <int MT, int NT, int WM, int WN, int KS, bool kSplit>
 __global__ void __launch_bounds__(WM * WN * kWave)
 sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restrict__ x_rows, int M,
              const float *__restrict__ w, int64_t w_s0, int N, int K, const float *__restrict__ bias, int act,
@@ -88,12 +159,14 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
              int units) {
     constexpr int T = WM * WN * kWave;
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
-    constexpr int XV = BM * (kSgK / 4) / T;  // 16-byte vectors per thread and stage
-    constexpr int WV = BN * (kSgK / 4) / T;
-    static_assert(XV >= 1 && WV >= 1 && XV * T == BM * kSgK / 4 && WV * T == BN * kSgK / 4,
-                  "stage splits evenly over the threads");
-    __shared__ __attribute__((aligned(16))) float xs[2][BM * kSgPitch];
-    __shared__ __attribute__((aligned(16))) float ws[2][BN * kSgPitch];
+    constexpr int C = KS / 4;  // 16-byte chunks per row and stage
+    constexpr int RB = sg_row_bytes<KS>();
+    constexpr int XV = BM * C / T;  // 16-byte vectors per thread and stage
+    constexpr int WV = BN * C / T;
+    static_assert(XV >= 1 && WV >= 1 && XV * T == BM * C && WV * T == BN * C && T % C == 0,
+                  "stage splits evenly over the threads, one chunk column per thread");
+    __shared__ __attribute__((aligned(16))) char xs[2][BM * RB];
+    __shared__ __attribute__((aligned(16))) char ws[2][BN * RB];
 
     // tile of this workgroup: XCD b % 8 takes tiles (b % 8) * per .. + per - 1, m fastest
     const int per = (units + 7) / 8;
@@ -111,18 +184,18 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
         const int i = threadIdx.x + q * T;
-        int row = m0 + (i >> 3);
+        int row = m0 + i / C;
         row = row < M ? row : M - 1;
         if (x_rows) row = x_rows[row];
-        xp[q] = x + static_cast<int64_t>(row) * x_s0 + (i & 7) * 4;
+        xp[q] = x + static_cast<int64_t>(row) * x_s0 + (i % C) * 4;
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
         const int i = threadIdx.x + q * T;
-        const int n = n0 + (i >> 3);  // rows past N repeat row N - 1; their columns are not stored
-        wp[q] = w + static_cast<int64_t>(n < N ? n : N - 1) * w_s0 + (i & 7) * 4;
+        const int n = n0 + i / C;  // rows past N repeat row N - 1; their columns are not stored
+        wp[q] = w + static_cast<int64_t>(n < N ? n : N - 1) * w_s0 + (i % C) * 4;
     }
-    const int k_left = K - (threadIdx.x & 7) * 4;  // stage k0 is inside K for this thread while k0 < k_left
+    const int k_left = K - (threadIdx.x % C) * 4;  // stage k0 is inside K for this thread while k0 < k_left
 
     floatx4_t acc[MT][NT];
 #pragma unroll
@@ -130,29 +203,31 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[m][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-    const float *xt0 = xs[0] + (wm * 16 * MT + r16) * kSgPitch + kq * 4;
-    const float *wt0 = ws[0] + (wn * 16 * NT + r16) * kSgPitch + kq * 4;
-    const float *xt1 = xs[1] + (wm * 16 * MT + r16) * kSgPitch + kq * 4;
-    const float *wt1 = ws[1] + (wn * 16 * NT + r16) * kSgPitch + kq * 4;
+    const int x_off = (wm * 16 * MT + r16) * RB + kq * 16;
+    const int w_off = (wn * 16 * NT + r16) * RB + kq * 16;
+    auto store = [&](const floatx4_t (&xr)[XV], const floatx4_t (&wr)[WV], int buf) __attribute__((always_inline)) {
+        sg_store_rows<KS, XV, T, kSplit>(xr, xs[buf]);
+        sg_store_rows<KS, WV, T, kSplit>(wr, ws[buf]);
+    };
 
     // stage j sits in register set j % 2 (a, b) and LDS buffer j % 2.  Step k: MFMAs on buffer
     // k % 2, stage k + 1 to LDS, then the loads of stage k + 3 into the set stage k + 1 left free.
     floatx4_t xa[XV], wa[WV], xb[XV], wb[WV];
-    const int stages = (K + kSgK - 1) / kSgK;
-    sg_load<XV, WV>(xa, wa, xp, wp, 0, k_left);
-    sg_store<XV, WV, T>(xa, wa, xs[0], ws[0]);
-    if (stages > 1) sg_load<XV, WV>(xb, wb, xp, wp, 1, k_left);
-    if (stages > 2) sg_load<XV, WV>(xa, wa, xp, wp, 2, k_left);
+    const int stages = (K + KS - 1) / KS;
+    sg_load<KS, XV, WV>(xa, wa, xp, wp, 0, k_left);
+    store(xa, wa, 0);
+    if (stages > 1) sg_load<KS, XV, WV>(xb, wb, xp, wp, 1, k_left);
+    if (stages > 2) sg_load<KS, XV, WV>(xa, wa, xp, wp, 2, k_left);
     __syncthreads();
     for (int k = 0;; k += 2) {
-        sg_compute<MT, NT>(acc, xt0, wt0);
-        if (k + 1 < stages) sg_store<XV, WV, T>(xb, wb, xs[1], ws[1]);
-        if (k + 3 < stages) sg_load<XV, WV>(xb, wb, xp, wp, k + 3, k_left);
+        sg_compute<MT, NT, KS, kSplit>(acc, xs[0] + x_off, ws[0] + w_off);
+        if (k + 1 < stages) store(xb, wb, 1);
+        if (k + 3 < stages) sg_load<KS, XV, WV>(xb, wb, xp, wp, k + 3, k_left);
         __syncthreads();
         if (k + 1 >= stages) break;
-        sg_compute<MT, NT>(acc, xt1, wt1);
-        if (k + 2 < stages) sg_store<XV, WV, T>(xa, wa, xs[0], ws[0]);
-        if (k + 4 < stages) sg_load<XV, WV>(xa, wa, xp, wp, k + 4, k_left);
+        sg_compute<MT, NT, KS, kSplit>(acc, xs[1] + x_off, ws[1] + w_off);
+        if (k + 2 < stages) store(xa, wa, 0);
+        if (k + 4 < stages) sg_load<KS, XV, WV>(xa, wa, xp, wp, k + 4, k_left);
         __syncthreads();
         if (k + 2 >= stages) break;
     }
@@ -186,15 +261,14 @@ sgemm_kernel(const float *__restrict__ x, int64_t x_s0, const int32_t *__restric
     }
 }
 
-template <int MT, int NT, int WM, int WN>
+template <int MT, int NT, int WM, int WN, int KS, bool kSplit>
 int launch_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, int M, const float *w, int64_t w_s0, int N,
                  int K, const float *bias, int act, const float *res, int64_t r_s0, const float *scale, float *out,
                  int64_t o_s0, hipStream_t st) {
     constexpr int BM = 16 * MT * WM, BN = 16 * NT * WN;
     const int tiles_m = (M + BM - 1) / BM, units = tiles_m * ((N + BN - 1) / BN);
-    hipLaunchKernelGGL((sgemm_kernel<MT, NT, WM, WN>), dim3((units + 7) / 8 * 8), dim3(WM * WN * kWave), 0, st, x,
-                       x_s0,
-                       x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, tiles_m, units);
+    hipLaunchKernelGGL((sgemm_kernel<MT, NT, WM, WN, KS, kSplit>), dim3((units + 7) / 8 * 8), dim3(WM * WN * kWave), 0,
+                       st, x, x_s0, x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, tiles_m, units);
     return NQ_LAUNCH_STATUS();
 }
 
@@ -269,10 +343,24 @@ __global__ void last_rows_kernel(const int32_t *__restrict__ off, int B, int u, 
 
 using namespace nq;
 
+#ifndef NQ_SG_KS_64x128
+#define NQ_SG_KS_64x128 32
+#endif
+#ifndef NQ_SG_KS_64x64
+#define NQ_SG_KS_64x64 64
+#endif
+#ifndef NQ_SG_KS_32x64
+#define NQ_SG_KS_32x64 64
+#endif
+#ifndef NQ_SG_KS_32x32
+#define NQ_SG_KS_32x32 128
+#endif
+
 extern "C" int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, const float *w, int64_t w_s0, int M,
                         int N, int K, const float *bias, int act, const float *res, int64_t r_s0, const float *scale,
-                        float *out, int64_t o_s0, void *stream) {
+                        float *out, int64_t o_s0, int precision, void *stream) {
     NQ_CHECK_ARG(x && w && out && M >= 0 && N > 0 && K > 0 && (act == 0 || act == 1));
+    NQ_CHECK_ARG(precision == NQ_MATMUL_HIGHEST || precision == NQ_MATMUL_HIGH);
     NQ_CHECK_ARG(x_s0 >= K && w_s0 >= K && o_s0 >= N && (!res || r_s0 >= N));
     if (K % 4 || N % 4 || x_s0 % 4 || w_s0 % 4 || o_s0 % 4 || (res && r_s0 % 4) || !sg_al16(x) ||
         !sg_al16(w) || !sg_al16(out) || (res && !sg_al16(res)) || (bias && !sg_al16(bias)) ||
@@ -280,18 +368,26 @@ extern "C" int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, con
         return NQ_ERR_UNSUPPORTED;
     if (M == 0) return NQ_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // the largest tile that still gives every CU a workgroup (fp32 MFMA work per staged byte is high,
-    // so small tiles lose little and idle CUs lose much)
+    // the largest tile that still gives every CU a workgroup (MFMA work per staged byte is high, so
+    // small tiles lose little and idle CUs lose much)
     auto units = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-#define NQ_SG(MT, NT, WM, WN) \
-    launch_sgemm<MT, NT, WM, WN>(x, x_s0, x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, o_s0, st)
+#define NQ_SG(MT, NT, WM, WN, KS, SPLIT)                                                                          \
+    launch_sgemm<MT, NT, WM, WN, KS, SPLIT>(x, x_s0, x_rows, M, w, w_s0, N, K, bias, act, res, r_s0, scale, out, \
+                                            o_s0, st)
     // 128 x 128 and 64 x 128 tiles over 16 and 8 waves of 32 x 32, 64 x 64 over 8 waves of 16 x 32: more
-    // waves per CU hide the stage latency (the codec step's GEMMs 1.30 -> 1.21 ms against 4 waves per tile)
-    if (units(128, 128) >= 256) return NQ_SG(2, 2, 4, 4);
-    if (units(64, 128) >= 256) return NQ_SG(2, 2, 2, 4);
-    if (units(64, 64) >= 256) return NQ_SG(1, 2, 4, 2);
-    if (units(32, 64) >= 256) return NQ_SG(1, 2, 2, 2);
-    return NQ_SG(1, 1, 2, 2);
+    // waves per CU hide the stage latency (the codec step's fp32 GEMMs 1.30 -> 1.21 ms against 4 waves per
+    // tile).  The smaller tiles take more k per stage (fewer barriers and more bytes in flight per wave).
+#define NQ_SG_PICK(SPLIT)                                                                \
+    if (units(128, 128) >= 256) return NQ_SG(2, 2, 4, 4, 32, SPLIT);                    \
+    if (units(64, 128) >= 256) return NQ_SG(2, 2, 2, 4, NQ_SG_KS_64x128, SPLIT);        \
+    if (units(64, 64) >= 256) return NQ_SG(1, 2, 4, 2, NQ_SG_KS_64x64, SPLIT);          \
+    if (units(32, 64) >= 256) return NQ_SG(1, 2, 2, 2, NQ_SG_KS_32x64, SPLIT);          \
+    return NQ_SG(1, 1, 2, 2, NQ_SG_KS_32x32, SPLIT);
+    if (precision == NQ_MATMUL_HIGH) {
+        NQ_SG_PICK(true)
+    }
+    NQ_SG_PICK(false)
+#undef NQ_SG_PICK
 #undef NQ_SG
 }
 
