@@ -69,6 +69,14 @@ constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
 constexpr int kBinSortCap = 2048;  // pieces the plan can sort
 constexpr bool kDecodeBins = true;  // decode rows of general batches through the bins (else stream + merge)
 
+// Shortest piece a decode row is cut into, in 16-token blocks: a bin's average load below this (a
+// small batch) would cut every row into pieces that each wave of a bin covers in under a block and
+// that then pay the cross-workgroup merge.  8 rows with KV U{16..512}: 19.5 us per launch cutting
+// to the average load, 14.7 with 16-block pieces, 13.9 with 32 or 64 (whole rows).  Batches whose
+// average bin load is longer (more than 32 x 16 tokens x 32 bins of decode tokens at 8 KV heads, the
+// batch-64 step among them) are dealt as before.
+constexpr int kBinMinPieceBlocks = 32;
+
 __host__ __device__ inline int bins_per_head(int num_kv_heads) {
     const int nb = kBinWgs / num_kv_heads;
     return nb < 1 ? 1 : nb;
@@ -290,8 +298,8 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     }
     if (lead && is_dec) dec_rows[dec_idx] = make_int4(tid, s_qo[tid], boff, nblk);
 
-    // Decode bins (lead workgroup): rows longer than a bin's average load C are
-    // cut into k = ceil(blocks / C) near-equal pieces; pieces are sorted by size
+    // Decode bins (lead workgroup): rows longer than a bin's average load C (at
+    // least kBinMinPieceBlocks) are cut into k = ceil(blocks / C) near-equal pieces; pieces are sorted by size
     // (descending, then piece id) and dealt to the bins in snake order
     // (0, 1, .., NB-1, NB-1, .., 0, ..), which evens the bins' loads.  Piece
     // descriptor: {decode row, first block, block count, (first piece << 9) | k
@@ -305,7 +313,8 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     // (decode row x kv head) start at zero.
     if (lead) {
         const int NB = bins_per_head(num_kv_heads);
-        const int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
+        int C = n_blocks > 0 ? (n_blocks + NB - 1) / NB : 1;
+        C = C < kBinMinPieceBlocks ? kBinMinPieceBlocks : C;
         const int k = is_dec ? (nblk + C - 1) / C : 0;
         int pc_excl[2], pc_total[2];
         block_exclusive_scan_n<2>({k, k > 1 ? 1 : 0}, s_tmp, pc_excl, pc_total);
