@@ -101,8 +101,6 @@ class CodePredictorWeights:
             )
             for _ in range(c.num_layers)
         ]
-        for L in self.layers:  # gate/up rows interleaved for the fused SwiGLU kernel
-            L.gate_up_packed = pack_swiglu(L.gate_up)
         self.final_norm = torch.ones(c.hidden, **bf)
         groups = c.num_code_groups - 1
         self.lm_head = randn(groups, c.vocab, c.hidden)
@@ -110,11 +108,74 @@ class CodePredictorWeights:
         self.proj_b = randn(c.hidden)
         self.layer0_embedding = randn(c.talker_vocab, c.talker_hidden, scale=1.0)
         self.codec_embedding = randn(groups, c.vocab, c.talker_hidden, scale=1.0)
-        # derived once, as the executor does (torch GEMM with bias; not on the per-frame path)
+        self._derive()
+
+    def _derive(self) -> None:
+        for L in self.layers:  # gate/up rows interleaved for the fused SwiGLU kernel
+            L.gate_up_packed = pack_swiglu(L.gate_up)
+        groups = self.config.num_code_groups - 1
+        # derived once, as the executor does (executor/code_predictor.py:72-88: torch GEMM with bias,
+        # not on the per-frame path)
         self.projected_layer0 = F.linear(self.layer0_embedding, self.proj_w, self.proj_b).contiguous()
         self.projected_residual = torch.stack(
             [F.linear(self.codec_embedding[i], self.proj_w, self.proj_b) for i in range(groups - 1)]
         ).contiguous()
+
+    @classmethod
+    def from_reference_model(cls, model, layer0_embedding, config) -> "CodePredictorWeights":
+        """The parameters of a loaded reference code predictor: ``model`` a ``Qwen3TTSCodePredictor``
+        (model/components.py:132-200), ``layer0_embedding`` the talker's codec embedding the executor
+        is given (executor/build.py:74-76) and ``config`` the reference's ``Qwen3TTSConfig``
+        (model/config.py:66-118).  Every tensor is the model's own, as contiguous bf16 on its device:
+        per layer the norms, the packed QKV and o projections, the q/k norms and the packed [gate; up]
+        and down projections; the final norm, the 15 heads, the small-to-MTP projection with its bias
+        and the codec embeddings; the projected embedding tables are derived as the executor derives
+        them."""
+
+        t = config.talker
+        p = t.code_predictor
+        c = CodePredictorConfig(num_layers=int(p.num_hidden_layers), hidden=int(p.hidden_size),
+                                num_qo_heads=int(p.num_attention_heads), num_kv_heads=int(p.num_key_value_heads),
+                                head_dim=int(p.head_dim), intermediate=int(p.intermediate_size),
+                                vocab=int(p.vocab_size), talker_hidden=int(t.hidden_size),
+                                talker_vocab=int(t.vocab_size), num_code_groups=int(t.num_code_groups),
+                                rms_eps=float(p.rms_norm_eps), rope_theta=float(p.rope_theta))
+        inner = model.model
+        groups = c.num_code_groups - 1
+        if len(inner.layers) != c.num_layers or len(model.lm_head) != groups or len(inner.codec_embedding) != groups:
+            raise ValueError("the code predictor's layer, head or embedding count does not match the config")
+
+        def bf(x, shape):
+            x = x.detach()
+            if tuple(x.shape) != tuple(shape):
+                raise ValueError(f"reference weight of shape {tuple(x.shape)} where {tuple(shape)} was expected")
+            return x.to(torch.bfloat16).contiguous()
+
+        self = cls.__new__(cls)
+        self.config = c
+        self.layers = []
+        for L in inner.layers:
+            a, mlp = L.self_attn, L.mlp
+            self.layers.append(SimpleNamespace(
+                input_norm=bf(L.input_layernorm.weight, (c.hidden,)),
+                qkv=bf(a.qkv_proj.weight, (c.qkv_width, c.hidden)),
+                o=bf(a.o_proj.weight, (c.hidden, c.num_qo_heads * c.head_dim)),
+                post_norm=bf(L.post_attention_layernorm.weight, (c.hidden,)),
+                gate_up=bf(mlp.gate_up_proj.weight, (2 * c.intermediate, c.hidden)),
+                down=bf(mlp.down_proj.weight, (c.hidden, c.intermediate)),
+                q_norm=bf(a.q_norm.weight, (c.head_dim,)),
+                k_norm=bf(a.k_norm.weight, (c.head_dim,)),
+            ))
+        self.final_norm = bf(inner.norm.weight, (c.hidden,))
+        self.lm_head = torch.stack([bf(h.weight, (c.vocab, c.hidden)) for h in model.lm_head]).contiguous()
+        proj = model.small_to_mtp_projection
+        self.proj_w = bf(proj.weight, (c.hidden, c.talker_hidden))
+        self.proj_b = bf(proj.bias, (c.hidden,))
+        self.layer0_embedding = bf(layer0_embedding.weight, (c.talker_vocab, c.talker_hidden))
+        self.codec_embedding = torch.stack(
+            [bf(e.weight, (c.vocab, c.talker_hidden)) for e in inner.codec_embedding]).contiguous()
+        self._derive()
+        return self
 
     def weight_bytes_per_pass(self) -> int:
         c = self.config

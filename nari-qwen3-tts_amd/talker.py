@@ -111,12 +111,71 @@ class TalkerWeights:
         self.text_embedding = randn(c.text_vocab, c.hidden)
         # codec token embeddings (Qwen3TTSTalkerInnerModel.codec_embedding, model/components.py:71)
         self.codec_embedding = randn(c.vocab, c.hidden)
+        self._derive(fp8_gate_up)
+
+    def _derive(self, fp8_gate_up: bool) -> None:
         self.fp8_gate_up = fp8_gate_up
         for layer in self.layers:
             layer.gate_up_q, layer.gate_up_scales = (
                 quantize_fp8_weight_blocks(layer.gate_up) if fp8_gate_up else (None, None))
             # the same codes with gate/up rows interleaved for the fused SwiGLU kernel
             layer.gate_up_packed = pack_fp8_swiglu(layer.gate_up_q) if fp8_gate_up else None
+
+    @classmethod
+    def from_reference_model(cls, model, config, *, fp8_gate_up: bool = True) -> "TalkerWeights":
+        """The parameters of a loaded reference talker: ``model`` a ``Qwen3TTSTalkerModel``
+        (model/components.py:93-130; its projected text-embedding cache initialised, as
+        ``initialize_projected_text_embedding_cache`` does at load) and ``config`` the reference's
+        ``Qwen3TTSConfig`` (model/config.py:66-118).  Every tensor is the model's own, as contiguous
+        bf16 on the model's device: per layer the input / post-attention norms, the packed QKV and
+        o projections, the q/k norms and the packed [gate; up] and down projections; the final norm,
+        the codec head, the projected text embedding and the codec embedding.  The FP8 gate/up blocks
+        are made from the bf16 weights as GatedMLP.initialize_fp8_gate_up_weight makes them
+        (model/layers.py:226-239)."""
+
+        t = config.talker
+        c = TalkerConfig(num_layers=int(t.num_hidden_layers), hidden=int(t.hidden_size),
+                         num_qo_heads=int(t.num_attention_heads), num_kv_heads=int(t.num_key_value_heads),
+                         head_dim=int(t.head_dim), intermediate=int(t.intermediate_size), vocab=int(t.vocab_size),
+                         text_vocab=int(t.text_vocab_size), codec_vocab=int(t.code_predictor.vocab_size),
+                         eos_id=int(t.codec_eos_token_id), rms_eps=float(t.rms_norm_eps),
+                         rope_theta=float(t.rope_theta))
+        inner = model.model
+        if len(inner.layers) != c.num_layers:
+            raise ValueError(f"the model has {len(inner.layers)} layers, the config {c.num_layers}")
+
+        def bf(x, shape):
+            x = x.detach()
+            if tuple(x.shape) != tuple(shape):
+                raise ValueError(f"reference weight of shape {tuple(x.shape)} where {tuple(shape)} was expected")
+            return x.to(torch.bfloat16).contiguous()
+
+        self = cls.__new__(cls)
+        self.config = c
+        self.layers = []
+        for L in inner.layers:
+            a, mlp = L.self_attn, L.mlp
+            self.layers.append(SimpleNamespace(
+                input_norm=bf(L.input_layernorm.weight, (c.hidden,)),
+                qkv=bf(a.qkv_proj.weight, (c.qkv_width, c.hidden)),
+                o=bf(a.o_proj.weight, (c.hidden, c.num_qo_heads * c.head_dim)),
+                post_norm=bf(L.post_attention_layernorm.weight, (c.hidden,)),
+                gate_up=bf(mlp.gate_up_proj.weight, (2 * c.intermediate, c.hidden)),
+                down=bf(mlp.down_proj.weight, (c.hidden, c.intermediate)),
+                attention=SimpleNamespace(
+                    q_norm=SimpleNamespace(weight=bf(a.q_norm.weight, (c.head_dim,)),
+                                           variance_epsilon=float(a.q_norm.variance_epsilon)),
+                    k_norm=SimpleNamespace(weight=bf(a.k_norm.weight, (c.head_dim,)),
+                                           variance_epsilon=float(a.k_norm.variance_epsilon)),
+                    rope_theta=float(a.rope_theta),
+                ),
+            ))
+        self.final_norm = bf(inner.norm.weight, (c.hidden,))
+        self.codec_head = bf(model.codec_head.weight, (c.vocab, c.hidden))
+        self.text_embedding = bf(model.get_projected_text_embedding_cache(), (c.text_vocab, c.hidden))
+        self.codec_embedding = bf(inner.codec_embedding.weight, (c.vocab, c.hidden))
+        self._derive(fp8_gate_up)
+        return self
 
     def weight_bytes(self) -> int:
         """Bytes of weights one decode step reads (FP8 codes + scales for gate/up when enabled)."""
