@@ -632,7 +632,10 @@ int nq_codec_last_rows(const int32_t *off, int B, int u, int32_t *rows, void *st
  *   and the fresh frames inside the sliding window, with retained slot j
  *   valid when j >= R - ctx_len[slot]; then the retained K/V
  *   ([slots, R, H, D] per layer, slot stride state_slot_stride) advance in
- *   place (_pre_transformer, :193-381).  q, k, v rows share stride ld.
+ *   place (_pre_transformer, :193-381).  q, k, v rows share stride ld; the
+ *   fresh k rows are left rotated (q is only read).  One launch, one workgroup
+ *   per (stream, head); D must be 16, 32 or 64, window <= 32, and the
+ *   operands 16-byte aligned with strides % 4 == 0, else NQ_ERR_UNSUPPORTED.
  * nq_codec_advance: frame_pos[slot] += F; ctx_len[slot] = min(R, ctx + F)
  *   (:375-380), once per step after the last layer.
  * nq_codec_pcm16: wav = clamp(x, -1, 1); pcm = round-half-even(wav * 32767)

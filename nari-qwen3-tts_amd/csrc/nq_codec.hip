@@ -686,123 +686,225 @@ overlap_fixup_kernel(const int32_t *__restrict__ off, int B, int u_in, int s, co
 }
 
 // ---------------------------------------------------------------------------
-// transformer: per-head RMSNorm + RoPE of q and k (in place), positions =
-// frame_position[slot] + local frame.  One wave per (token, head); lane i
-// holds the pair (i, i + D/2) for D <= 128.
+// transformer attention of one (stream, head): per-head RMSNorm + RoPE of q
+// and of the fresh k (positions = frame_position[slot] + fresh index), the
+// sliding-window attention over [retained R frames ; fresh frames], and the
+// retained K/V advance, in one workgroup (_pre_transformer, :193-381).
+//
+// Query i of the stream (position P0 + i) sees the positions P0 + i - R ..
+// P0 + i: retained slot j (position P0 - R + j) when j >= R - ctx and j >= i,
+// fresh frame f when i - R <= f <= i.  The fresh queries go in blocks of 64;
+// for block i0 the key rows are the positions P0 + i0 - R + kappa, kappa in
+// [0, R + nq): a retained slot (already rotated in the state) while
+// i0 - R + kappa < 0, else fresh frame f = i0 - R + kappa, rotated here (and
+// written back in place, so a later block reads it rotated) unless an earlier
+// block already did.  K, V and the rotated q of a block are staged in LDS
+// (rows of D + 4 floats); query lane j then reads key row j + s for window
+// step s, so the 64 lanes read 64 consecutive rows and a 16-byte read covers
+// every bank once.  The four waves split the channels: wave w forms partial
+// scores over its D/4 channels, the partials meet in LDS, every wave finishes
+// the softmax of its lanes and accumulates P V over its own channels.  After
+// the last block the new retained rows (the last R positions) are written from
+// LDS: the state is read (staged) before this workgroup overwrites it, and no
+// other workgroup touches this (stream, head).
 
-__global__ void __launch_bounds__(kCodecThreads)
-codec_qk_rope_kernel(float *__restrict__ q, float *__restrict__ k, int64_t ld, int T, int H, int D,
-                     const float *__restrict__ qn, const float *__restrict__ kn, float eps, float log_theta,
-                     const int32_t *__restrict__ off, int B, const int32_t *__restrict__ slots,
-                     const int64_t *__restrict__ frame_pos) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t item = blockIdx.x * static_cast<int64_t>(kCodecThreads / kWave) + threadIdx.x / kWave;
-    if (item >= static_cast<int64_t>(T) * H * 2) return;
-    const int which = static_cast<int>(item & 1);
-    const int64_t th = item >> 1;
-    const int t = static_cast<int>(th / H), h = static_cast<int>(th - static_cast<int64_t>(t) * H);
-    const int b = stream_of(off, B, t, 1);
-    const float pos = static_cast<float>(frame_pos[slots[b]] + (t - off[b]));
-    float *v = (which ? k : q) + static_cast<int64_t>(t) * ld + h * D;
-    const float *wn = which ? kn : qn;
-    const int half = D / 2;
-    const bool on = lane < half;
-    const float x1 = on ? v[lane] : 0.f, x2 = on ? v[lane + half] : 0.f;
-    float ss = x1 * x1 + x2 * x2;
-    for (int m = 1; m < kWave; m <<= 1) ss += __shfl_xor(ss, m, kWave);
-    if (!on) return;
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-    const float f = x1 * inv * wn[lane], s2 = x2 * inv * wn[lane + half];
-    const float inv_freq = expf(-log_theta * (2.0f * static_cast<float>(lane) / static_cast<float>(D)));
-    float sn, cs;
-    sincosf(pos * inv_freq, &sn, &cs);
-    v[lane] = f * cs - s2 * sn;
-    v[lane + half] = s2 * cs + f * sn;
-}
+constexpr int kWinThreads = 256;
+constexpr int kWinWaves = kWinThreads / kWave;
+constexpr int kWinQ = 64;     // queries per block (one per lane)
+constexpr int kWinMax = 32;   // window (R + 1) the kernel takes
 
-// sliding-window attention over [retained R frames ; fresh frames]: query i of
-// a stream (position P0 + i) sees retained slot j (position P0 - R + j) when
-// j >= R - ctx and j >= i, and fresh frame i' when i - window < i' <= i.
-// One wave per (token, head); lane = channel (D <= 64).
+template <int D>
+__global__ void __launch_bounds__(kWinThreads)
+window_block_kernel(const float *__restrict__ q, float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+                    int H, const float *__restrict__ qn, const float *__restrict__ kn, float eps, float log_theta,
+                    const int32_t *__restrict__ off, const int32_t *__restrict__ slots,
+                    const int64_t *__restrict__ frame_pos, const int32_t *__restrict__ ctx_len, float *state_k,
+                    float *state_v, int64_t state_slot_stride, int R, float scale, float *__restrict__ out,
+                    int64_t ldo) {
+    static_assert(D % 16 == 0 && D <= 64, "four waves of D / 4 channels, 4-channel chunks");
+    constexpr int P = D + 4;                // LDS row pitch (floats)
+    constexpr int LPR = D / 4;              // lanes (4-channel chunks) per row
+    constexpr int RPP = kWinThreads / LPR;  // rows staged per pass
+    constexpr int DW = D / kWinWaves;       // channels per wave
+    constexpr int CW = DW / 4;              // chunks per wave
+    __shared__ __attribute__((aligned(16))) float ks[(kWinMax - 1 + kWinQ) * P];
+    __shared__ __attribute__((aligned(16))) float vs[(kWinMax - 1 + kWinQ) * P];
+    __shared__ __attribute__((aligned(16))) float qs[kWinQ * P];
+    __shared__ float ps[kWinWaves * kWinMax * kWinQ];
 
-__global__ void __launch_bounds__(kCodecThreads)
-window_attention_kernel(const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-                        int64_t ld, int T, int H, int D, const int32_t *__restrict__ off, int B,
-                        const int32_t *__restrict__ slots, const float *__restrict__ state_k,
-                        const float *__restrict__ state_v, int64_t state_slot_stride, int R, int window,
-                        const int32_t *__restrict__ ctx_len, float scale, float *__restrict__ out, int64_t ldo) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t item = blockIdx.x * static_cast<int64_t>(kCodecThreads / kWave) + threadIdx.x / kWave;
-    if (item >= static_cast<int64_t>(T) * H) return;
-    const int t = static_cast<int>(item / H), h = static_cast<int>(item - static_cast<int64_t>(t) * H);
-    const int b = stream_of(off, B, t, 1);
-    const int i = t - off[b];
+    const int b = blockIdx.x / H, h = blockIdx.x - (blockIdx.x / H) * H;
+    const int64_t t0 = off[b];
+    const int F = off[b + 1] - off[b];
+    if (F <= 0) return;  // no fresh frames: nothing attends and the state stays as it is
     const int slot = slots[b];
     const int ctx = ctx_len[slot];
-    const bool on = lane < D;
-    const float qv = on ? q[static_cast<int64_t>(t) * ld + h * D + lane] * scale : 0.f;
-    float m = -INFINITY, l = 0.f, acc = 0.f;
-    auto visit = [&](const float *kp, const float *vp) {
-        float sdot = on ? qv * kp[lane] : 0.f;
-        for (int s = 1; s < kWave; s <<= 1) sdot += __shfl_xor(sdot, s, kWave);
-        const float mn = fmaxf(m, sdot);
-        const float a = expf(m - mn), p = expf(sdot - mn);
-        l = l * a + p;
-        acc = acc * a + (on ? p * vp[lane] : 0.f);
-        m = mn;
-    };
-    const float *sk = state_k + static_cast<int64_t>(slot) * state_slot_stride;
-    const float *sv = state_v + static_cast<int64_t>(slot) * state_slot_stride;
-    const int j0 = max(R - ctx, i - window + 1 + R);  // retained slot j has position P0 - R + j
-    for (int j = max(j0, 0); j < R; ++j) visit(sk + (static_cast<int64_t>(j) * H + h) * D, sv + (static_cast<int64_t>(j) * H + h) * D);
-    for (int f = max(0, i - window + 1); f <= i; ++f) {
-        const int64_t tr = off[b] + f;
-        visit(k + tr * ld + h * D, v + tr * ld + h * D);
-    }
-    if (on) out[static_cast<int64_t>(t) * ldo + h * D + lane] = acc / l;
-}
+    const int64_t P0 = frame_pos[slot];
+    const int W = R + 1;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int c = threadIdx.x % LPR;  // the thread's 4-channel chunk when staging
+    float *sk = state_k + static_cast<int64_t>(slot) * state_slot_stride + h * D;
+    float *sv = state_v + static_cast<int64_t>(slot) * state_slot_stride + h * D;
+    const int64_t srow = static_cast<int64_t>(H) * D;  // state row stride
 
-// retained K/V <- last R frames of [retained ; fresh]; thread per (stream, head, channel)
-__global__ void __launch_bounds__(kCodecThreads)
-kv_update_kernel(const float *__restrict__ k, const float *__restrict__ v, int64_t ld, int H, int D,
-                 const int32_t *__restrict__ off, int B, const int32_t *__restrict__ slots, float *__restrict__ state_k,
-                 float *__restrict__ state_v, int64_t state_slot_stride, int R) {
-    const int64_t i = blockIdx.x * static_cast<int64_t>(kCodecThreads) + threadIdx.x;
-    if (i >= static_cast<int64_t>(B) * H * D) return;
-    const int b = static_cast<int>(i / (static_cast<int64_t>(H) * D));
-    const int hd = static_cast<int>(i - static_cast<int64_t>(b) * H * D);
-    const int F = off[b + 1] - off[b];
-    float *sk = state_k + static_cast<int64_t>(slots[b]) * state_slot_stride + hd;
-    float *sv = state_v + static_cast<int64_t>(slots[b]) * state_slot_stride + hd;
-    const int64_t stride = static_cast<int64_t>(H) * D;
-    // New row j is old row j + F or fresh row F - R + j.  Rows go in chunks of kChunk whose reads are
-    // all issued before their writes: an old row a chunk reads (at or past j0 + F) is never one an
-    // earlier chunk wrote, and one it also writes is read first, as in a row-by-row walk; the chunk's
-    // loads are in flight together (10.9 -> 7.9 us per launch at 32 streams; 32-row chunks measured
-    // no better).
-    constexpr int kChunk = 8;
-    for (int j0 = 0; j0 < R; j0 += kChunk) {
-        float kv[kChunk], vv[kChunk];
+    // RMSNorm (weight wn) + rotate-half RoPE of a row held as one 4-channel chunk per lane of its
+    // LPR-lane group: the group sums the squares, and chunk c pairs with chunk c ^ (LPR / 2)
+    // (channels d and d + D / 2, inv_freq of pair d = theta^(-2d/D)), as the reference rotates them
+    const bool first = c < LPR / 2;
+    float inv_freq[4];
 #pragma unroll
-        for (int e = 0; e < kChunk; ++e) {
-            const int j = j0 + e;
-            kv[e] = vv[e] = 0.f;
-            if (j >= R) continue;
-            if (j + F < R) {
-                kv[e] = sk[(j + F) * stride];
-                vv[e] = sv[(j + F) * stride];
-            } else {
-                const int64_t tr = off[b] + F - R + j;
-                kv[e] = k[tr * ld + hd];
-                vv[e] = v[tr * ld + hd];
+    for (int e = 0; e < 4; ++e) {
+        const int d = 4 * (first ? c : c - LPR / 2) + e;  // the pair's first channel
+        inv_freq[e] = expf(-log_theta * (2.0f * static_cast<float>(d) / static_cast<float>(D)));
+    }
+    auto norm_rope = [&](float4 x, const float *wn, float pos) {
+        float ssq = x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+#pragma unroll
+        for (int m = 1; m < LPR; m <<= 1) ssq += __shfl_xor(ssq, m, kWave);
+        const float inv = 1.0f / sqrtf(ssq / static_cast<float>(D) + eps);
+        const float4 w4 = *reinterpret_cast<const float4 *>(wn + 4 * c);
+        const float y[4] = {x.x * inv * w4.x, x.y * inv * w4.y, x.z * inv * w4.z, x.w * inv * w4.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float partner = __shfl_xor(y[e], LPR / 2, kWave);
+            float sn, cs;
+            sincosf(pos * inv_freq[e], &sn, &cs);
+            o[e] = first ? y[e] * cs - partner * sn : y[e] * cs + partner * sn;
+        }
+        return make_float4(o[0], o[1], o[2], o[3]);
+    };
+
+    int last_i0 = 0;
+    for (int i0 = 0; i0 < F; i0 += kWinQ) {
+        last_i0 = i0;
+        const int nq = F - i0 < kWinQ ? F - i0 : kWinQ;
+        const int rows = R + nq;
+        // stage K and V rows kappa (position P0 + i0 - R + kappa) and the block's rotated q; a group
+        // of LPR lanes owns one row per pass (every lane of a group takes the same branch).  Every
+        // load of the block is issued before the first is used, so the passes share one round trip.
+        constexpr int KVP = (kWinMax - 1 + kWinQ + RPP - 1) / RPP;  // K/V passes at most
+        constexpr int QP = (kWinQ + RPP - 1) / RPP;                 // q passes at most
+        float4 kreg[KVP], vreg[KVP], qreg[QP];
+#pragma unroll
+        for (int pp = 0; pp < KVP; ++pp) {
+            const int kappa = pp * RPP + threadIdx.x / LPR;
+            const int fi = i0 - R + kappa;
+            kreg[pp] = vreg[pp] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kappa < rows) {
+                if (fi < 0) {  // retained slot i0 + kappa, rotated when it was stored
+                    kreg[pp] = *reinterpret_cast<const float4 *>(sk + (i0 + kappa) * srow + 4 * c);
+                    vreg[pp] = *reinterpret_cast<const float4 *>(sv + (i0 + kappa) * srow + 4 * c);
+                } else {
+                    kreg[pp] = *reinterpret_cast<const float4 *>(k + (t0 + fi) * ld + h * D + 4 * c);
+                    vreg[pp] = *reinterpret_cast<const float4 *>(v + (t0 + fi) * ld + h * D + 4 * c);
+                }
             }
         }
 #pragma unroll
-        for (int e = 0; e < kChunk; ++e) {
-            if (j0 + e >= R) continue;
-            sk[(j0 + e) * stride] = kv[e];
-            sv[(j0 + e) * stride] = vv[e];
+        for (int pp = 0; pp < QP; ++pp) {
+            const int jq = pp * RPP + threadIdx.x / LPR;
+            qreg[pp] = jq < nq ? *reinterpret_cast<const float4 *>(q + (t0 + i0 + jq) * ld + h * D + 4 * c)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+#pragma unroll
+        for (int pp = 0; pp < KVP; ++pp) {
+            const int kappa = pp * RPP + threadIdx.x / LPR;
+            const int fi = i0 - R + kappa;
+            if (kappa < rows) {
+                float4 kv = kreg[pp];
+                if (fi >= i0) {  // this block's own frame: rotate it, and keep it rotated in place
+                    kv = norm_rope(kv, kn, static_cast<float>(P0 + fi));
+                    *reinterpret_cast<float4 *>(k + (t0 + fi) * ld + h * D + 4 * c) = kv;
+                }
+                *reinterpret_cast<float4 *>(ks + kappa * P + 4 * c) = kv;
+                *reinterpret_cast<float4 *>(vs + kappa * P + 4 * c) = vreg[pp];
+            }
+        }
+#pragma unroll
+        for (int pp = 0; pp < QP; ++pp) {
+            const int jq = pp * RPP + threadIdx.x / LPR;
+            if (jq < nq)
+                *reinterpret_cast<float4 *>(qs + jq * P + 4 * c) =
+                    norm_rope(qreg[pp], qn, static_cast<float>(P0 + i0 + jq));
+        }
+        __syncthreads();
+
+        // partial scores over wave w's channels: lane j = query i0 + j, window step s = key row j + s
+        const int j = lane;
+        const bool live = j < nq;
+        float4 qv[CW];
+#pragma unroll
+        for (int u = 0; u < CW; ++u)
+            qv[u] = live ? *reinterpret_cast<const float4 *>(qs + j * P + wave * DW + 4 * u) : make_float4(0, 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < kWinMax; ++s) {
+            if (s >= W) break;
+            float dot = 0.f;
+            if (live) {
+                const float *kr = ks + (j + s) * P + wave * DW;
+#pragma unroll
+                for (int u = 0; u < CW; ++u) {
+                    const float4 kk = *reinterpret_cast<const float4 *>(kr + 4 * u);
+                    dot += qv[u].x * kk.x + qv[u].y * kk.y + qv[u].z * kk.z + qv[u].w * kk.w;
+                }
+            }
+            ps[(wave * kWinMax + s) * kWinQ + j] = dot;
+        }
+        __syncthreads();
+
+        // softmax of the lane's window (in every wave, for its own channels of P V)
+        float sc[kWinMax];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kWinMax; ++s) {
+            sc[s] = -INFINITY;
+            const int fi = i0 + j - R + s;  // the key's fresh index (< 0: retained slot R + fi)
+            if (s < W && live && (fi >= 0 || R + fi >= R - ctx)) {
+                float full = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWinWaves; ++w) full += ps[(w * kWinMax + s) * kWinQ + j];
+                sc[s] = full * scale;
+                mx = fmaxf(mx, sc[s]);
+            }
+        }
+        float l = 0.f;
+        float acc[DW];
+#pragma unroll
+        for (int d = 0; d < DW; ++d) acc[d] = 0.f;
+#pragma unroll
+        for (int s = 0; s < kWinMax; ++s) {
+            if (sc[s] != -INFINITY) {
+                const float pr = expf(sc[s] - mx);
+                l += pr;
+                const float *vr = vs + (j + s) * P + wave * DW;
+#pragma unroll
+                for (int u = 0; u < CW; ++u) {
+                    const float4 vv = *reinterpret_cast<const float4 *>(vr + 4 * u);
+                    acc[4 * u] += pr * vv.x;
+                    acc[4 * u + 1] += pr * vv.y;
+                    acc[4 * u + 2] += pr * vv.z;
+                    acc[4 * u + 3] += pr * vv.w;
+                }
+            }
+        }
+        if (live) {
+            float *op = out + (t0 + i0 + j) * ldo + h * D + wave * DW;
+            const float il = 1.0f / l;
+#pragma unroll
+            for (int u = 0; u < CW; ++u)
+                *reinterpret_cast<float4 *>(op + 4 * u) =
+                    make_float4(acc[4 * u] * il, acc[4 * u + 1] * il, acc[4 * u + 2] * il, acc[4 * u + 3] * il);
+        }
+        if (i0 + kWinQ < F) __syncthreads();  // the block's LDS rows are read before the next block restages them
+    }
+    // retained rows jr = 0 .. R-1 <- positions P0 + F - R + jr: row kappa = jr + F - last_i0 of the last
+    // block's staged K/V (a retained slot or a rotated fresh frame); staged before the first block's
+    // barrier, so every read of the old state precedes these stores
+    for (int e = threadIdx.x; e < R * LPR; e += kWinThreads) {
+        const int jr = e / LPR, cc = e % LPR;
+        const int kappa = jr + F - last_i0;
+        *reinterpret_cast<float4 *>(sk + jr * srow + 4 * cc) = *reinterpret_cast<const float4 *>(ks + kappa * P + 4 * cc);
+        *reinterpret_cast<float4 *>(sv + jr * srow + 4 * cc) = *reinterpret_cast<const float4 *>(vs + kappa * P + 4 * cc);
     }
 }
 
@@ -987,21 +1089,28 @@ extern "C" int nq_codec_window_attention(float *q, float *k, const float *v, int
                                          int64_t state_slot_stride, int R, int window, float *out, int64_t ldo,
                                          void *stream) {
     NQ_CHECK_ARG(q && k && v && q_norm && k_norm && offsets && slots && frame_pos && ctx_len && out);
-    NQ_CHECK_ARG(state_k && state_v && T >= 0 && B > 0 && H > 0 && D >= 2 && D <= kWave && D % 2 == 0);
-    NQ_CHECK_ARG(R >= 0 && window == R + 1 && state_slot_stride >= static_cast<int64_t>(R) * H * D);
+    NQ_CHECK_ARG(state_k && state_v && T >= 0 && B > 0 && H > 0 && R >= 0 && window == R + 1);
+    NQ_CHECK_ARG(state_slot_stride >= static_cast<int64_t>(R) * H * D);
     NQ_CHECK_ARG(ld >= static_cast<int64_t>(H) * D && ldo >= static_cast<int64_t>(H) * D && rope_theta > 0.f);
+    if (D != 16 && D != 32 && D != 64) return NQ_ERR_UNSUPPORTED;
+    if (window > nq::kWinMax) return NQ_ERR_UNSUPPORTED;
+    if (ld % 4 || ldo % 4 || state_slot_stride % 4 ||
+        ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+          reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(state_k) |
+          reinterpret_cast<uintptr_t>(state_v) | reinterpret_cast<uintptr_t>(q_norm) |
+          reinterpret_cast<uintptr_t>(k_norm)) & 15))
+        return NQ_ERR_UNSUPPORTED;
     if (T == 0) return NQ_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int wpb = kCodecThreads / kWave;
-    hipLaunchKernelGGL(codec_qk_rope_kernel, dim3(static_cast<unsigned>((static_cast<int64_t>(T) * H * 2 + wpb - 1) / wpb)),
-                       dim3(kCodecThreads), 0, st, q, k, ld, T, H, D, q_norm, k_norm, eps, logf(rope_theta), offsets, B,
-                       slots, frame_pos);
-    hipLaunchKernelGGL(window_attention_kernel, dim3(static_cast<unsigned>((static_cast<int64_t>(T) * H + wpb - 1) / wpb)),
-                       dim3(kCodecThreads), 0, st, q, k, v, ld, T, H, D, offsets, B, slots, state_k, state_v,
-                       state_slot_stride, R, window, ctx_len, 1.0f / sqrtf(static_cast<float>(D)), out, ldo);
-    if (R > 0)
-        hipLaunchKernelGGL(kv_update_kernel, dim3(grid_for(static_cast<int64_t>(B) * H * D)), dim3(kCodecThreads), 0, st,
-                           k, v, ld, H, D, offsets, B, slots, state_k, state_v, state_slot_stride, R);
+    const float lt = logf(rope_theta), scale = 1.0f / sqrtf(static_cast<float>(D));
+#define NQ_WIN(DD)                                                                                                \
+    hipLaunchKernelGGL(nq::window_block_kernel<DD>, dim3(static_cast<unsigned>(B) * H), dim3(nq::kWinThreads), 0, \
+                       st, q, k, v, ld, H, q_norm, k_norm, eps, lt, offsets, slots, frame_pos, ctx_len, state_k,    \
+                       state_v, state_slot_stride, R, scale, out, ldo)
+    if (D == 64) NQ_WIN(64);
+    else if (D == 32) NQ_WIN(32);
+    else NQ_WIN(16);
+#undef NQ_WIN
     return NQ_LAUNCH_STATUS();
 }
 
