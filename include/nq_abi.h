@@ -658,14 +658,20 @@ int nq_codec_causal_conv(const float *x, int64_t ldx, int64_t T, const int32_t *
  * advanced in place).  Replaces the residual unit of the upstream decoder block
  * as the adapter runs it (model/incremental_codec.py:58-88 for the causal
  * convolutions): two convolutions whose intermediate tensor never reaches
- * memory; the result has the bits of the two nq_codec_causal_conv launches.
+ * memory.  precision NQ_MATMUL_HIGHEST: fp32 products on the vector ALUs, the
+ * bits of the two nq_codec_causal_conv launches.  NQ_MATMUL_HIGH (the
+ * decoder's default, as the reference's convolutions run under cuDNN's TF32
+ * default): for C = 16 and 32 both convolutions as implicit GEMMs on bf16 MFMA
+ * with the split products of nq_sgemm's NQ_MATMUL_HIGH (each product within
+ * 3 * 2^-16 of fp32, fp32 sums; x, out and history 16-byte aligned with ldx,
+ * ldo % 4 == 0); C = 8 keeps the fp32 products.
  * w1 [C, C, K], w2 [C, C, 1]; out must not alias x.  C must be 8, 16 or 32.
  */
 int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, const int32_t *offsets, int B, int u,
                            const int32_t *slots, float *history, int C, int K, int dilation, const float *w1,
                            const float *b1, const float *a1_alpha, const float *a1_beta, const float *w2,
                            const float *b2, const float *a2_alpha, const float *a2_beta, float *out, int64_t ldo,
-                           void *stream);
+                           int precision, void *stream);
 int nq_codec_causal_transconv(const float *x, int64_t ldx, int64_t T_in, const int32_t *offsets, int B,
                               int u_in, int stride_s, const int32_t *slots, float *overlap, const float *w,
                               const float *bias, int Cin, int Cout, const float *act_alpha,

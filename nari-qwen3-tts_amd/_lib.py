@@ -99,7 +99,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_codec_embed_sum": [_P, _I, _I, _P, _I, _I, _P, _P, _P],
     "nq_codec_causal_conv": [_P, _L, _L, _P, _I, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _L, _P, _L, _P],
     "nq_codec_residual_unit": [_P, _L, _L, _P, _I, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
-                               _P],
+                               _I, _P],
     "nq_codec_causal_transconv": [_P, _L, _L, _P, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _P, _P, _L, _P],
     "nq_codec_window_attention": [_P, _P, _P, _L, _I, _I, _I, _P, _P, _F, _F, _P, _I, _P, _P, _P, _P, _P, _L, _I,
                                   _I, _P, _L, _P],

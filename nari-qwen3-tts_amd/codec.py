@@ -299,7 +299,8 @@ class IncrementalCodecDecoder:
         _lib.call("nq_codec_residual_unit", x.data_ptr(), x.stride(0), x.shape[0], self._off.data_ptr(), self._B, u,
                   self._slots.data_ptr(), self._pool.hist[name].data_ptr(), c, R.c1_w.shape[2], dilation,
                   R.c1_w.data_ptr(), _lib.ptr(R.c1_b), R.a1.data_ptr(), R.b1.data_ptr(), R.c2_w.data_ptr(),
-                  _lib.ptr(R.c2_b), R.a2.data_ptr(), R.b2.data_ptr(), out.data_ptr(), out.stride(0), self._stream)
+                  _lib.ptr(R.c2_b), R.a2.data_ptr(), R.b2.data_ptr(), out.data_ptr(), out.stride(0), self._precision,
+                  self._stream)
         return out
 
     def _transconv(self, x, u_in, s, name, w, b, act=None):

@@ -928,6 +928,313 @@ pcm16_kernel(const float *__restrict__ x, int64_t n, float *__restrict__ wav, in
     }
 }
 
+// ---------------------------------------------------------------------------
+// A decoder residual unit of C = 8, 16 or 32 channels on MFMA, for the decoder's
+// "high" float32 matmul precision (the reference's convolutions run on cuDNN with
+// its TF32 default): out = x + conv1x1(snake2(conv7(snake1(x)) + b1)) + b2 as two
+// implicit GEMMs with bf16x3 split products and fp32 sums, each operand v = hi +
+// lo + e with hi = bf16(v), lo = bf16(v - hi), |e| <= 2^-16 |v|, a product
+// hi*hi + hi*lo + lo*hi.  The 7-tap convolution is D[co][t] = sum_k W[co][k]
+// X[k][t] with k = tap * C + ci (zero weights past the seventh tap), X[k][t] =
+// snake1(x)[t - (6 - tap) dil][ci]: the weights are the A operand of
+// v_mfma_f32_16x16x32_bf16 (split once per workgroup into an LDS fragment table,
+// one 16-byte read per lane), the activated input rows the B operand (a lane's 8
+// consecutive k are 8 consecutive channels of one input row, staged split in LDS
+// as [row][C hi | C lo] with a 16-byte row pad, 8 rows of a lane group then
+// cover distinct banks), so a lane ends with 4 consecutive output channels of
+// one row.  Rows within (K-1) dil of their stream's start take those taps from
+// the stream's history (the wave takes that path only when one of its rows
+// needs it).  The activated 7-tap outputs go split, one 16-row tile at a time,
+// through the wave's own LDS rows into the B operand of the 1x1 convolution.  A
+// workgroup of 4 waves owns 4 x 16 x unit_tiles<C>() output rows.
+
+typedef __bf16 cu_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 cu_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float cu_floatx2 __attribute__((ext_vector_type(2)));
+typedef float cu_floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kUnitThreads = 256;
+constexpr int kUnitTaps = 7;
+
+// 16-row tiles per wave (256 output rows per workgroup): 8 and 16 tiles for 8 and 16 channels measured
+// 130 / 48 us against 85 / 39 us per launch, the workgroup's chain being latency-bound
+constexpr int kUnitStreamsLds = 1024;  // stream offsets searched in LDS (more streams: in global memory)
+template <int C>
+constexpr int unit_tiles() {
+    return 4;
+}
+template <int C>
+constexpr int unit_rows() {
+    return kUnitThreads / kWave * unit_tiles<C>() * 16;  // output rows per workgroup
+}
+
+__device__ __forceinline__ uint32_t cu_pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((cu_floatx2){a, b}, cu_bf16x2));
+}
+
+// hi / lo bf16 words of the pair (a, b); a - bf16(a) is exact in fp32
+__device__ __forceinline__ void cu_split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = cu_pack(a, b);
+    lo = cu_pack(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
+__device__ __forceinline__ cu_bf16x8 cu_frag(const uint4 &v) { return __builtin_bit_cast(cu_bf16x8, v); }
+
+template <int C>
+constexpr int unit_ksteps() {
+    return (kUnitTaps * C + 31) / 32;
+}
+
+template <int C>
+size_t unit_mfma_lds(int pad) {
+    constexpr int NT = C <= 16 ? 1 : 2;
+    constexpr int RB = 4 * C + 16;
+    return static_cast<size_t>(unit_ksteps<C>() * NT * 2 * kWave + NT * 2 * kWave) * 16 +
+           static_cast<size_t>(unit_rows<C>() + pad) * RB + static_cast<size_t>(kUnitThreads / kWave) * 16 * RB;
+}
+
+template <int C>
+__global__ void __launch_bounds__(kUnitThreads)
+unit_mfma_kernel(const float *__restrict__ x, int64_t ldx, int64_t T, const int32_t *__restrict__ off, int B, int u,
+                 const int32_t *__restrict__ slots, const float *__restrict__ hist, int dil,
+                 const float *__restrict__ w1, const float *__restrict__ b1, Act act1,
+                 const float *__restrict__ w2, const float *__restrict__ b2, Act act2,
+                 float *__restrict__ out, int64_t ldo) {
+    static_assert(C == 8 || C == 16 || C == 32, "8, 16 or 32 channels");
+    constexpr int NT = C <= 16 ? 1 : 2;     // 16-wide output-channel tiles
+    constexpr int KS = unit_ksteps<C>();     // 32-k steps of the 7-tap convolution
+    constexpr int RB = 4 * C + 16;           // LDS row bytes
+    constexpr int VPR = C / 4;               // float4 per input row
+    constexpr int MT = unit_tiles<C>();      // 16-row tiles per wave
+    constexpr int ROWS = unit_rows<C>();     // output rows per workgroup
+    extern __shared__ __attribute__((aligned(16))) char ulds[];
+    __shared__ float sp[4][32];              // snake1 a, 1/b; snake2 a, 1/b
+    __shared__ int32_t soff[kUnitStreamsLds + 1];
+    uint4 *wf1 = reinterpret_cast<uint4 *>(ulds);      // [KS][NT][hi, lo][64 lanes]
+    uint4 *wf2 = wf1 + KS * NT * 2 * kWave;            // [NT][hi, lo][64 lanes]
+    char *xs = reinterpret_cast<char *>(wf2 + NT * 2 * kWave);
+    const int pad = (kUnitTaps - 1) * dil;
+    char *ys = xs + (ROWS + pad) * RB;                 // [wave][16 rows][RB]
+    const int tid = threadIdx.x;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS;
+
+    // 1. the input rows row0 - pad .. row0 + ROWS - 1, activated and split (rows outside [0, T) zero), in
+    // batches of eight 128-bit loads per thread; the first batch is issued before the weight table is
+    // built, so that its round trip overlaps the table's
+    const int nvec = (ROWS + pad) * VPR;
+    auto load_batch = [&](int e0, float4 (&v)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + i * kUnitThreads;
+            const int rr = e / VPR;
+            const int64_t g = row0 - pad + rr;
+            v[i] = (e < nvec && g >= 0 && g < T)
+                       ? *reinterpret_cast<const float4 *>(x + g * ldx + (e - rr * VPR) * 4)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_batch = [&](int e0, const float4 (&v)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = e0 + i * kUnitThreads;
+            if (e >= nvec) break;
+            const int rr = e / VPR, c4 = (e - rr * VPR) * 4;
+            const int64_t g = row0 - pad + rr;
+            float f[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            if (act1.alpha && g >= 0 && g < T) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) f[q] = snake(f[q], sp[0][c4 + q], sp[1][c4 + q]);
+            }
+            uint32_t h0, l0, h1, l1;
+            cu_split2(f[0], f[1], h0, l0);
+            cu_split2(f[2], f[3], h1, l1);
+            *reinterpret_cast<uint2 *>(xs + rr * RB + 2 * c4) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(xs + rr * RB + 2 * C + 2 * c4) = make_uint2(l0, l1);
+        }
+    };
+    float4 vb[8];
+    load_batch(tid, vb);
+
+    // 2. the weights as split MFMA A fragments: lane (r16, kq) of step j holds W[co = 16 nt + r16][k = 32 j + 8 kq .. + 7]
+    for (int e = tid; e < KS * NT * kWave; e += kUnitThreads) {
+        const int ln = e % kWave, nt = (e / kWave) % NT, j = e / (kWave * NT);
+        const int co = nt * 16 + (ln & 15), k0 = 32 * j + 8 * (ln >> 4);
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float v2[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int kk = k0 + 2 * p + q, tap = kk / C, ci = kk - (kk / C) * C;
+                v2[q] = (co < C && tap < kUnitTaps) ? w1[(static_cast<int64_t>(co) * C + ci) * kUnitTaps + tap] : 0.f;
+            }
+            cu_split2(v2[0], v2[1], hi[p], lo[p]);
+        }
+        wf1[((j * NT + nt) * 2) * kWave + ln] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        wf1[((j * NT + nt) * 2 + 1) * kWave + ln] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+    for (int e = tid; e < NT * kWave; e += kUnitThreads) {
+        const int ln = e % kWave, nt = e / kWave;
+        const int co = nt * 16 + (ln & 15), ci0 = 8 * (ln >> 4);
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int ci = ci0 + 2 * p;
+            const float a = (co < C && ci < C) ? w2[co * C + ci] : 0.f;
+            const float b = (co < C && ci + 1 < C) ? w2[co * C + ci + 1] : 0.f;
+            cu_split2(a, b, hi[p], lo[p]);
+        }
+        wf2[(nt * 2) * kWave + ln] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        wf2[(nt * 2 + 1) * kWave + ln] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+    const bool off_lds = B <= kUnitStreamsLds;
+    if (off_lds)
+        for (int i = tid; i <= B; i += kUnitThreads) soff[i] = off[i];
+    if (tid < C) {
+        sp[0][tid] = act1.alpha ? act1.a_of(tid) : 0.f;
+        sp[1][tid] = act1.alpha ? act1.inv_b_of(tid) : 0.f;
+        sp[2][tid] = act2.alpha ? act2.a_of(tid) : 0.f;
+        sp[3][tid] = act2.alpha ? act2.inv_b_of(tid) : 0.f;
+    }
+
+    __syncthreads();  // the snake parameters and stream offsets
+    store_batch(tid, vb);
+    for (int e0 = tid + 8 * kUnitThreads; e0 < nvec; e0 += 8 * kUnitThreads) {
+        load_batch(e0, vb);
+        store_batch(e0, vb);
+    }
+    __syncthreads();
+
+    // 3. the 7-tap convolution: wave w owns rows row0 + (MT w + m) 16 + r16, m < MT
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, kq = lane >> 4;
+    // the lane's row of tile m is row0 + (MT w + m) 16 + r16; its offset from its stream's first row
+    // (pad when far enough: the rows of a workgroup lie in few streams, so the search runs once per tile)
+    const int32_t *offs = off_lds ? soff : off;
+    int local[MT];
+    bool near_start = false;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int64_t t = row0 + (wave * MT + m) * 16 + r16;
+        local[m] = pad;
+        if (t < T) {
+            const int b = stream_of(offs, B, t, u);
+            const int64_t l = t - static_cast<int64_t>(offs[b]) * u;
+            local[m] = l < pad ? static_cast<int>(l) : pad;
+            near_start = near_start || l < pad;
+        }
+    }
+    // the residual rows of the epilogue, loaded now so that their round trip overlaps the MFMAs
+    float4 xres[MT][NT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int64_t t = row0 + (wave * MT + m) * 16 + r16;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int co = nt * 16 + 4 * kq;
+            xres[m][nt] = (co < C && t < T) ? *reinterpret_cast<const float4 *>(x + t * ldx + co)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const bool slow = __any(near_start);
+    cu_floatx4 acc[MT][NT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[m][nt] = cu_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+        cu_bf16x8 ah[NT], al[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            ah[nt] = cu_frag(wf1[((j * NT + nt) * 2) * kWave + lane]);
+            al[nt] = cu_frag(wf1[((j * NT + nt) * 2 + 1) * kWave + lane]);
+        }
+        const int k0 = 32 * j + 8 * kq, tap = k0 / C, cb = k0 - (k0 / C) * C;
+        const int back = tap < kUnitTaps ? (kUnitTaps - 1 - tap) * dil : 0;  // past the 7th tap: zero weights
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const char *rp = xs + ((wave * MT + m) * 16 + r16 + pad - back) * RB + 2 * cb;
+            uint4 bh = *reinterpret_cast<const uint4 *>(rp);
+            uint4 bl = *reinterpret_cast<const uint4 *>(rp + 2 * C);
+            if (slow && tap < kUnitTaps && local[m] - back < 0) {
+                // a row within pad of its stream's start: this tap reads the stream's history
+                const int b = stream_of(offs, B, row0 + (wave * MT + m) * 16 + r16, u);
+                const float *hp =
+                    hist + (static_cast<int64_t>(slots[b]) * pad + pad + local[m] - back) * C + cb;
+                const float4 h0 = *reinterpret_cast<const float4 *>(hp);
+                const float4 h1 = *reinterpret_cast<const float4 *>(hp + 4);
+                cu_split2(h0.x, h0.y, bh.x, bl.x);
+                cu_split2(h0.z, h0.w, bh.y, bl.y);
+                cu_split2(h1.x, h1.y, bh.z, bl.z);
+                cu_split2(h1.z, h1.w, bh.w, bl.w);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[nt], cu_frag(bh), acc[m][nt], 0, 0, 0);
+                acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[nt], cu_frag(bl), acc[m][nt], 0, 0, 0);
+                acc[m][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[nt], cu_frag(bh), acc[m][nt], 0, 0, 0);
+            }
+        }
+    }
+
+    // 4. per tile: y = snake2(conv + b1), split into the wave's own 16 LDS rows (lane (r16, kq) holds
+    // y[row r16][co = 16 nt + 4 kq .. + 3]), read back as the B operand of the 1x1 convolution (lane
+    // (r16, kq) = y[row r16][ci = 8 kq .. + 7]), then the residual
+    char *yw = ys + wave * 16 * RB;
+    cu_bf16x8 a2h[NT], a2l[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        a2h[nt] = cu_frag(wf2[(nt * 2) * kWave + lane]);
+        a2l[nt] = cu_frag(wf2[(nt * 2 + 1) * kWave + lane]);
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int co = nt * 16 + 4 * kq;
+            if (co >= C) continue;
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[e] = acc[m][nt][e] + (b1 ? b1[co + e] : 0.f);
+                if (act2.alpha) y[e] = snake(y[e], sp[2][co + e], sp[3][co + e]);
+            }
+            uint32_t h0, l0, h1, l1;
+            cu_split2(y[0], y[1], h0, l0);
+            cu_split2(y[2], y[3], h1, l1);
+            char *rp = yw + r16 * RB + 2 * co;
+            *reinterpret_cast<uint2 *>(rp) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(rp + 2 * C) = make_uint2(l0, l1);
+        }
+        __builtin_amdgcn_wave_barrier();  // the wave reads back what its own lanes wrote (LDS keeps its order)
+        uint4 bh = make_uint4(0, 0, 0, 0), bl = make_uint4(0, 0, 0, 0);
+        if (8 * kq < C) {
+            const char *rp = yw + r16 * RB + 16 * kq;
+            bh = *reinterpret_cast<const uint4 *>(rp);
+            bl = *reinterpret_cast<const uint4 *>(rp + 2 * C);
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane has read the tile before the next one is written
+        const int64_t t = row0 + (wave * MT + m) * 16 + r16;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            cu_floatx4 d = cu_floatx4{0.f, 0.f, 0.f, 0.f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2l[nt], cu_frag(bh), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2h[nt], cu_frag(bl), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2h[nt], cu_frag(bh), d, 0, 0, 0);
+            const int co = nt * 16 + 4 * kq;
+            if (co >= C || t >= T) continue;
+            const float4 xr = xres[m][nt];
+            float4 o;
+            o.x = xr.x + d[0] + (b2 ? b2[co] : 0.f);
+            o.y = xr.y + d[1] + (b2 ? b2[co + 1] : 0.f);
+            o.z = xr.z + d[2] + (b2 ? b2[co + 2] : 0.f);
+            o.w = xr.w + d[3] + (b2 ? b2[co + 3] : 0.f);
+            *reinterpret_cast<float4 *>(out + t * ldo + co) = o;
+        }
+    }
+}
+
 int grid_for(int64_t n) {
     const int64_t g = (n + kCodecThreads - 1) / kCodecThreads;
     return static_cast<int>(g < 1 ? 1 : g > 8192 ? 8192 : g);
@@ -1006,29 +1313,51 @@ extern "C" int nq_codec_residual_unit(const float *x, int64_t ldx, int64_t T, co
                                       const int32_t *slots, float *history, int C, int K, int dilation, const float *w1,
                                       const float *b1, const float *a1_alpha, const float *a1_beta, const float *w2,
                                       const float *b2, const float *a2_alpha, const float *a2_beta, float *out,
-                                      int64_t ldo, void *stream) {
+                                      int64_t ldo, int precision, void *stream) {
     NQ_CHECK_ARG(x && offsets && slots && history && w1 && w2 && out && B > 0 && u > 0 && T >= 0);
     NQ_CHECK_ARG(C > 0 && K >= 2 && K <= kConvKMax && dilation >= 1 && ldx >= C && ldo >= C && out != x);
-    if (K != kConvKMax) return NQ_ERR_UNSUPPORTED;  // the fused kernel is built for 7 taps
+    NQ_CHECK_ARG(precision == NQ_MATMUL_HIGHEST || precision == NQ_MATMUL_HIGH);
+    if (K != kConvKMax) return NQ_ERR_UNSUPPORTED;  // the fused kernels are built for 7 taps
     if ((K - 1) * dilation * C > kCodecThreads * kHistoryPerThread) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG((a1_alpha == nullptr) == (a1_beta == nullptr) && (a2_alpha == nullptr) == (a2_beta == nullptr));
     const int co_pad = C <= 8 ? 8 : C <= 16 ? 16 : 32;
     if (C > 32 || C != co_pad) return NQ_ERR_UNSUPPORTED;
-    const size_t lds = conv_small_lds(C, K, dilation, co_pad, true);
+    // the split-product MFMA kernel for 16 and 32 channels; 8 channels keep the fp32 direct kernel at
+    // either precision (at 1.98 M rows: 58 us against 84 us for the MFMA kernel, whose workgroups are
+    // latency-bound at that width)
+    const bool split = precision == NQ_MATMUL_HIGH && C >= 16;
+    const int pad = (K - 1) * dilation;
+    if (split && (ldx % 4 || ldo % 4 || ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                                          reinterpret_cast<uintptr_t>(history)) & 15)))
+        return NQ_ERR_UNSUPPORTED;
+    const size_t lds = split ? (C == 8 ? unit_mfma_lds<8>(pad) : C == 16 ? unit_mfma_lds<16>(pad)
+                                                                          : unit_mfma_lds<32>(pad))
+                             : conv_small_lds(C, K, dilation, co_pad, true);
     if (lds > 150 * 1024) return NQ_ERR_UNSUPPORTED;
     if (T == 0) return NQ_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const Act act1{a1_alpha, a1_beta}, act2{a2_alpha, a2_beta};
-    const int64_t rows = static_cast<int64_t>(kCodecThreads) * conv_small_rows(co_pad);
-    const dim3 grid(static_cast<unsigned>((T + rows - 1) / rows));
-#define NQ_UNIT(CO)                                                                                                 \
-    hipLaunchKernelGGL((conv_small_kernel<CO, conv_small_rows(CO), true>), grid, dim3(kCodecThreads), lds, st, x, ldx, \
-                       T, offsets, B, u, slots, history, w1, b1, C, C, K, dilation, act1, x, ldx, out, ldo, w2, b2,  \
-                       act2)
-    if (co_pad == 8) NQ_UNIT(8);
-    else if (co_pad == 16) NQ_UNIT(16);
-    else NQ_UNIT(32);
+    if (split) {
+#define NQ_UNIT(CC)                                                                                                  \
+        hipLaunchKernelGGL(unit_mfma_kernel<CC>, dim3(static_cast<unsigned>((T + unit_rows<CC>() - 1) / unit_rows<CC>())), \
+                           dim3(kUnitThreads), lds, st, x, ldx, T, offsets, B, u, slots, history, dilation, w1, b1,     \
+                           act1, w2, b2, act2, out, ldo)
+        if (C == 8) NQ_UNIT(8);
+        else if (C == 16) NQ_UNIT(16);
+        else NQ_UNIT(32);
 #undef NQ_UNIT
+    } else {
+        const int64_t rows = static_cast<int64_t>(kCodecThreads) * conv_small_rows(co_pad);
+        const dim3 grid(static_cast<unsigned>((T + rows - 1) / rows));
+#define NQ_UNIT(CO)                                                                                                 \
+        hipLaunchKernelGGL((conv_small_kernel<CO, conv_small_rows(CO), true>), grid, dim3(kCodecThreads), lds, st, x, \
+                           ldx, T, offsets, B, u, slots, history, w1, b1, C, C, K, dilation, act1, x, ldx, out, ldo, \
+                           w2, b2, act2)
+        if (co_pad == 8) NQ_UNIT(8);
+        else if (co_pad == 16) NQ_UNIT(16);
+        else NQ_UNIT(32);
+#undef NQ_UNIT
+    }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     hipLaunchKernelGGL(history_update_kernel, dim3(B), dim3(kCodecThreads), 0, st,
                        x, ldx, offsets, B, u, slots, history, C, (K - 1) * dilation, act1);

@@ -24,6 +24,45 @@ def test_header_and_binding_agree(nq):
     assert _declared() == set(_lib.EXPORTED)
 
 
+def _declared_parameters() -> dict[str, list[str]]:
+    """name -> the C types of its parameters, as include/nq_abi.h declares them."""
+
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"\b(nq_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = [q.strip() for q in m.group(2).replace("\n", " ").split(",") if q.strip()]
+        if params == ["void"]:
+            params = []
+        # drop the parameter name: the type is everything before it
+        out[m.group(1)] = [re.sub(r"\s*\b[a-zA-Z_][a-zA-Z0-9_]*$", "", q) if not q.endswith("*") else q
+                           for q in params]
+    return out
+
+
+def _ctype_of(c_type: str):
+    c_type = c_type.replace("const ", "").strip()
+    if "*" in c_type:
+        return ctypes.c_void_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}[c_type]
+
+
+def test_binding_argument_types_match_the_header(nq):
+    """Every ctypes signature has the header's arity and argument kinds (pointer / int / int64 /
+    float), so a parameter added to one side but not the other fails here, on the CPU, instead of
+    passing a shifted argument list to the library."""
+    from nari_qwen3_tts_amd import _lib
+
+    declared = _declared_parameters()
+    assert set(declared) == set(_lib.EXPORTED)
+    for name, params in declared.items():
+        want = [_ctype_of(t) for t in params]
+        got = _lib._SIGNATURES[name]
+        assert len(got) == len(want), (name, len(got), len(want))
+        assert got == want, (name, [t.__name__ for t in got], [t.__name__ for t in want])
+
+
 def test_library_exports_every_declared_symbol(nq):
     from nari_qwen3_tts_amd import _lib
 

@@ -113,15 +113,13 @@ def test_pcm16_kernel_known_answers(nq, device):
     assert wav.tolist() == [-1.0, -0.5, 0.0, 0.5, 1.0]
 
 
-@pytest.mark.parametrize("channels,dilation", [(8, 9), (16, 3), (32, 1)])
-def test_residual_unit_equals_its_two_convolutions(nq, device, channels, dilation):
-    """nq_codec_residual_unit gives the bits of its two nq_codec_causal_conv launches (the K-tap
-    convolution with its history, then the 1x1 convolution with the residual) on ragged streams,
-    including streams shorter than the receptive field, and advances the history identically."""
-    from nari_qwen3_tts_amd import _lib
+def _unit_case(device, channels, dilation, integer: bool):
+    """Ragged streams at 20 rows per frame (incl. streams shorter than the receptive field and an empty
+    one) and the operands of one residual unit: random floats with both SnakeBeta activations, or small
+    integers with none (every product and sum exact in fp32 and every value its own two-bf16 split)."""
 
     g = torch.Generator(device=device)
-    g.manual_seed(channels + dilation)
+    g.manual_seed(channels + dilation + (1000 if integer else 0))
     c, k, u = channels, 7, 20
     frames = [3, 1, 12, 0, 7]
     off = torch.tensor(np.concatenate([[0], np.cumsum(frames)]), dtype=torch.int32, device=device)
@@ -129,27 +127,98 @@ def test_residual_unit_equals_its_two_convolutions(nq, device, channels, dilatio
     slots = torch.tensor([4, 0, 2, 1, 3], dtype=torch.int32, device=device)
     pad = (k - 1) * dilation
 
-    def r(*shape, s=1.0):
+    def r(*shape, s=1.0, lim=4):
+        if integer:
+            return torch.randint(-lim, lim + 1, shape, generator=g, device=device).float()
         return torch.randn(*shape, generator=g, device=device) * s
 
     x = r(T, c)
-    w1, b1, a1, be1 = r(c, c, k, s=0.2), r(c, s=0.1), r(c, s=0.1), r(c, s=0.1)
-    w2, b2, a2, be2 = r(c, c, 1, s=0.3), r(c, s=0.01), r(c, s=0.1), r(c, s=0.1)
+    w1, b1, w2, b2 = r(c, c, k, s=0.2, lim=2), r(c, s=0.1), r(c, c, 1, s=0.3, lim=2), r(c, s=0.01)
+    acts = (None, None, None, None) if integer else (r(c, s=0.1), r(c, s=0.1), r(c, s=0.1), r(c, s=0.1))
     hist0 = r(8, pad, c)
+    return dict(c=c, k=k, u=u, off=off, B=B, T=T, slots=slots, x=x, w1=w1, b1=b1, w2=w2, b2=b2, acts=acts,
+                hist0=hist0, dilation=dilation)
+
+
+def _two_convolutions(case, device):
+    from nari_qwen3_tts_amd import _lib
+
+    c, k, T, x = case["c"], case["k"], case["T"], case["x"]
+    a1, be1, a2, be2 = case["acts"]
     st = _lib.stream(device)
-    hist_a, hist_b = hist0.clone(), hist0.clone()
+    hist = case["hist0"].clone()
     y = torch.empty_like(x)
     want = torch.empty_like(x)
-    _lib.call("nq_codec_causal_conv", x.data_ptr(), x.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(),
-              hist_a.data_ptr(), w1.data_ptr(), b1.data_ptr(), c, c, k, dilation, 1, a1.data_ptr(), be1.data_ptr(),
-              None, 0, y.data_ptr(), y.stride(0), st)
-    _lib.call("nq_codec_causal_conv", y.data_ptr(), y.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(), None,
-              w2.data_ptr(), b2.data_ptr(), c, c, 1, 1, 1, a2.data_ptr(), be2.data_ptr(), x.data_ptr(), x.stride(0),
-              want.data_ptr(), want.stride(0), st)
+    _lib.call("nq_codec_causal_conv", x.data_ptr(), x.stride(0), T, case["off"].data_ptr(), case["B"], case["u"],
+              case["slots"].data_ptr(), hist.data_ptr(), case["w1"].data_ptr(), case["b1"].data_ptr(), c, c, k,
+              case["dilation"], 1, _lib.ptr(a1), _lib.ptr(be1), None, 0, y.data_ptr(), y.stride(0), st)
+    _lib.call("nq_codec_causal_conv", y.data_ptr(), y.stride(0), T, case["off"].data_ptr(), case["B"], case["u"],
+              case["slots"].data_ptr(), None, case["w2"].data_ptr(), case["b2"].data_ptr(), c, c, 1, 1, 1,
+              _lib.ptr(a2), _lib.ptr(be2), x.data_ptr(), x.stride(0), want.data_ptr(), want.stride(0), st)
+    return want, hist
+
+
+def _unit(case, device, precision):
+    from nari_qwen3_tts_amd import _lib
+
+    c, x = case["c"], case["x"]
+    a1, be1, a2, be2 = case["acts"]
+    hist = case["hist0"].clone()
     got = torch.empty_like(x)
-    _lib.call("nq_codec_residual_unit", x.data_ptr(), x.stride(0), T, off.data_ptr(), B, u, slots.data_ptr(),
-              hist_b.data_ptr(), c, k, dilation, w1.data_ptr(), b1.data_ptr(), a1.data_ptr(), be1.data_ptr(),
-              w2.data_ptr(), b2.data_ptr(), a2.data_ptr(), be2.data_ptr(), got.data_ptr(), got.stride(0), st)
+    _lib.call("nq_codec_residual_unit", x.data_ptr(), x.stride(0), case["T"], case["off"].data_ptr(), case["B"],
+              case["u"], case["slots"].data_ptr(), hist.data_ptr(), c, case["k"], case["dilation"],
+              case["w1"].data_ptr(), case["b1"].data_ptr(), _lib.ptr(a1), _lib.ptr(be1), case["w2"].data_ptr(),
+              case["b2"].data_ptr(), _lib.ptr(a2), _lib.ptr(be2), got.data_ptr(), got.stride(0), precision,
+              _lib.stream(device))
+    return got, hist
+
+
+UNIT_SHAPES = [(8, 9), (16, 3), (32, 1), (32, 9)]
+
+
+@pytest.mark.parametrize("channels,dilation", UNIT_SHAPES)
+def test_residual_unit_equals_its_two_convolutions(nq, device, channels, dilation):
+    """nq_codec_residual_unit at fp32 products ("highest") gives the bits of its two
+    nq_codec_causal_conv launches (the K-tap convolution with its history, then the 1x1 convolution
+    with the residual) on ragged streams, including streams shorter than the receptive field, and
+    advances the history identically."""
+    case = _unit_case(device, channels, dilation, integer=False)
+    want, hist_a = _two_convolutions(case, device)
+    got, hist_b = _unit(case, device, 0)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+    assert torch.equal(hist_a, hist_b)
+
+
+@pytest.mark.parametrize("channels,dilation", UNIT_SHAPES)
+def test_split_residual_unit_is_exact_on_integer_operands(nq, device, channels, dilation):
+    """At the "high" precision (two implicit GEMMs on bf16 MFMA with split products) and integer
+    operands without activations, every split is exact (v = hi + lo, the weights' low parts zero) and
+    every sum exact in fp32, so the MFMA unit equals the fp32 two-convolution path bit for bit: the
+    taps, channels, history rows of each stream start, the 1x1 convolution and the residual are all
+    pinned."""
+    case = _unit_case(device, channels, dilation, integer=True)
+    want, hist_a = _two_convolutions(case, device)
+    got, hist_b = _unit(case, device, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(hist_a, hist_b)
+
+
+@pytest.mark.parametrize("channels,dilation", UNIT_SHAPES)
+def test_split_residual_unit_near_fp32(nq, device, channels, dilation):
+    """At the "high" precision on random operands with both SnakeBeta activations: within 1e-3
+    absolute (mean 1e-4) of the fp32 path, whose outputs here are of order 1-10 (each split product is
+    within 3 * 2^-16 of the fp32 one), and for 16 and 32 channels not bit-equal to it (the split
+    products did run); 8 channels keep the fp32 products, so there the bits are the fp32 path's."""
+    case = _unit_case(device, channels, dilation, integer=False)
+    want, hist_a = _two_convolutions(case, device)
+    got, hist_b = _unit(case, device, 1)
+    torch.cuda.synchronize()
+    err = (got - want).abs()
+    assert float(err.max()) <= 1e-3 and float(err.mean()) <= 1e-4, (float(err.max()), float(err.mean()))
+    if channels >= 16:
+        assert not torch.equal(got, want)
+    else:
+        assert torch.equal(got, want)
     assert torch.equal(hist_a, hist_b)
