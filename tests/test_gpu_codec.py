@@ -222,3 +222,83 @@ def test_split_residual_unit_near_fp32(nq, device, channels, dilation):
     else:
         assert torch.equal(got, want)
     assert torch.equal(hist_a, hist_b)
+
+
+# (head dim, heads, window): the codec's 64 x 8 with its 26-frame window, and the other head widths the
+# kernel takes, up to its largest window
+WINDOW_SHAPES = [(64, 8, 26), (32, 4, 32), (16, 4, 8)]
+
+
+@pytest.mark.parametrize("D,H,window", WINDOW_SHAPES)
+def test_window_attention_kernel_against_the_oracle(nq, device, D, H, window):
+    """nq_codec_window_attention over ragged streams on permuted slots, one launch: fresh chunks of 1 to
+    130 frames (chunks past 64 frames take several query blocks, each reading keys the block before it
+    rotated in place), an empty chunk, retained windows empty, partly and wholly valid (the invalid
+    slots hold large values that must stay masked).  Against the oracle's per-head RMSNorm + RoPE and
+    sliding-window attention (model/incremental_codec.py:227-262,318-326): the output, the fresh keys
+    rotated in place, the untouched queries and values, the valid rows of the advanced retained K/V
+    (the last R positions), an unused slot and the empty stream's slot left as they were."""
+    from nari_qwen3_tts_amd import _lib
+
+    R = window - 1
+    eps, theta = 1e-6, 10000.0
+    frames = [1, 7, 40, 0, 70, 130]
+    ctx = [0, 3, R, 5, R, min(R, 10)]
+    pos0 = [0, 3, 200, 5, 57, 10]
+    slots = [5, 0, 3, 1, 4, 2]
+    n_slots = 7  # slot 6 is never named
+    B, T, HD = len(frames), sum(frames), H * D
+    rng = np.random.default_rng(D + window)
+    qkv = rng.standard_normal((T, 3 * HD)).astype(np.float32)
+    qn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    state_k = rng.standard_normal((n_slots, R, H, D)).astype(np.float32)
+    state_v = rng.standard_normal((n_slots, R, H, D)).astype(np.float32)
+    for b, s in enumerate(slots):  # slots outside the valid context: values no softmax could absorb
+        state_k[s, : R - ctx[b]] = 1e3
+        state_v[s, : R - ctx[b]] = -1e3
+    off = np.concatenate([[0], np.cumsum(frames)]).astype(np.int32)
+
+    t = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dt)  # noqa: E731
+    d_qkv, d_qn, d_kn = t(qkv), t(qn), t(kn)
+    d_sk, d_sv = t(state_k), t(state_v)
+    d_off, d_slots = t(off), t(np.array(slots, dtype=np.int32))
+    d_pos = t(np.array([0] * n_slots, dtype=np.int64))
+    d_ctx = t(np.array([0] * n_slots, dtype=np.int32))
+    for b, s in enumerate(slots):
+        d_pos[s], d_ctx[s] = pos0[b], ctx[b]
+    out = torch.full((T, HD), float("nan"), device=device)
+    q, k, v = d_qkv[:, :HD], d_qkv[:, HD : 2 * HD], d_qkv[:, 2 * HD :]
+    _lib.call("nq_codec_window_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), d_qkv.stride(0), T, H, D,
+              d_qn.data_ptr(), d_kn.data_ptr(), eps, theta, d_off.data_ptr(), B, d_slots.data_ptr(),
+              d_pos.data_ptr(), d_ctx.data_ptr(), d_sk.data_ptr(), d_sv.data_ptr(), d_sk.stride(0), R, window,
+              out.data_ptr(), out.stride(0), _lib.stream(device))
+    torch.cuda.synchronize()
+    got_out, got_qkv = out.cpu().numpy(), d_qkv.cpu().numpy()
+    got_sk, got_sv = d_sk.cpu().numpy(), d_sv.cpu().numpy()
+
+    np.testing.assert_array_equal(got_qkv[:, :HD], qkv[:, :HD])           # q is only read
+    np.testing.assert_array_equal(got_qkv[:, 2 * HD :], qkv[:, 2 * HD :])  # v is only read
+    np.testing.assert_array_equal(got_sk[6], state_k[6])                   # a slot no stream names
+    np.testing.assert_array_equal(got_sv[6], state_v[6])
+    for b, (f, s) in enumerate(zip(frames, slots)):
+        rows = slice(off[b], off[b + 1])
+        if f == 0:
+            np.testing.assert_array_equal(got_sk[s], state_k[s])
+            np.testing.assert_array_equal(got_sv[s], state_v[s])
+            continue
+        pos = pos0[b] + np.arange(f)
+        qr = o_codec.rope(o_codec.rmsnorm(qkv[rows, :HD].reshape(f, H, D), qn, eps), pos, theta)
+        kr = o_codec.rope(o_codec.rmsnorm(qkv[rows, HD : 2 * HD].reshape(f, H, D), kn, eps), pos, theta)
+        vr = qkv[rows, 2 * HD :].reshape(f, H, D)
+        keys = np.concatenate([state_k[s], kr])
+        vals = np.concatenate([state_v[s], vr])
+        att = o_codec.window_attention(qr, keys, vals, pos0[b], ctx[b], window)
+        np.testing.assert_allclose(got_out[rows].reshape(f, H, D), att, atol=1e-4, rtol=1e-4,
+                                   err_msg=f"attention output, stream {b}")
+        np.testing.assert_allclose(got_qkv[rows, HD : 2 * HD].reshape(f, H, D), kr, atol=1e-4, rtol=1e-4,
+                                   err_msg=f"keys rotated in place, stream {b}")
+        valid = R - min(R, ctx[b] + f)  # first retained row the advanced context covers
+        np.testing.assert_allclose(got_sk[s, valid:], keys[len(keys) - R :][valid:], atol=1e-4, rtol=1e-4,
+                                   err_msg=f"retained keys, stream {b}")
+        np.testing.assert_array_equal(got_sv[s, valid:], vals[len(vals) - R :][valid:])
