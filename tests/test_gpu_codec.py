@@ -173,7 +173,8 @@ def _unit(case, device, precision):
     return got, hist
 
 
-UNIT_SHAPES = [(8, 9), (16, 3), (32, 1), (32, 9)]
+# every (channels, dilation) of the decoder's residual units on this kernel
+UNIT_SHAPES = [(c, d) for c in (8, 16, 32) for d in (1, 3, 9)]
 
 
 @pytest.mark.parametrize("channels,dilation", UNIT_SHAPES)
