@@ -56,8 +56,8 @@ __device__ __forceinline__ void gemm_load_w(uint4 (&wr)[KS / 32], const uint16_t
 // the lane holds Y[m*16 + r16][col + kq*4 + 0..3].
 template <int MT, int KS>
 __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint16_t *xs, int r16, int kq, int M,
-                                          int N, int col, int slice, uint16_t *__restrict__ out, int64_t o_s0,
-                                          float *__restrict__ part, const uint16_t *__restrict__ bias) {
+                                          int row0, int mr, int N, int col, int slice, uint16_t *__restrict__ out,
+                                          int64_t o_s0, float *__restrict__ part, const uint16_t *__restrict__ bias) {
     floatx4_t acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -81,8 +81,9 @@ __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const int row = m * 16 + r16;
-        if (row >= M) continue;
+        const int lr = m * 16 + r16;  // row within the block
+        if (lr >= mr) continue;
+        const int row = row0 + lr;
         if (part) {
             float *p = part + (static_cast<int64_t>(slice) * M + row) * N + col;
             *reinterpret_cast<float4 *>(p) = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
@@ -90,14 +91,17 @@ __device__ __forceinline__ void gemm_tile(const uint4 (&wr)[KS / 32], const uint
             uint2 o;
             o.x = pack2_bf16(acc[m][0] + b4[0], acc[m][1] + b4[1]);
             o.y = pack2_bf16(acc[m][2] + b4[2], acc[m][3] + b4[3]);
-            *reinterpret_cast<uint2 *>(out + row * o_s0 + col) = o;
+            *reinterpret_cast<uint2 *>(out + static_cast<int64_t>(row) * o_s0 + col) = o;
         }
     }
 }
 
-// Workgroup (bx, by): K slice by, 64-column bands bx*nb .. bx*nb + nb - 1.
-// The X slice is staged once; wave w computes columns band*64 + w*16 + 0..15
-// of each band while the next band's weights are already in flight.
+// Workgroup (bx, by, bz): K slice by, 64-column bands bx*nb .. bx*nb + nb - 1,
+// rows bz*16*MT .. (a row block; more than 64 rows run as several blocks, so
+// that twice the workgroups share the weights through L2 instead of one
+// workgroup staging 128 rows).  The X slice is staged once; wave w computes
+// columns band*64 + w*16 + 0..15 of each band while the next band's weights
+// are already in flight.
 template <int MT, int KS>
 __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(KS > 512 ? 1 : 2, 2)))
 gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t *__restrict__ w,
@@ -113,6 +117,9 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     const int kq = lane >> 4;  // which 8-wide k group of the 32-k step
     const int band0 = blockIdx.x * nb;
     const int k0 = blockIdx.y * KS;
+    const int row0 = blockIdx.z * kRows;
+    const int mr = M - row0 < kRows ? M - row0 : kRows;  // rows of this block
+    x += static_cast<int64_t>(row0) * x_s0;
 
     // 1. X[:, k0 : k0 + KS] into registers (rows >= M are zero): issued first,
     // so that waiting for them does not wait for the weights
@@ -129,11 +136,11 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     for (int q = 0; q < kXVec; ++q) {
         const int v = rot_of(threadIdx.x + q * kGemmThreads);
         const int row = v / kVecPerRow, col = v % kVecPerRow;
-        // unconditional load (rows past M read row 0, M >= 1) so that no branch
-        // splits the prologue: the weight loads below must stay ahead of the
-        // barrier, and the compiler only keeps them there in straight-line code
-        const uint4 t = *reinterpret_cast<const uint4 *>(x + (row < M ? row : 0) * x_s0 + k0 + col * 8);
-        xr[q] = row < M ? t : make_uint4(0, 0, 0, 0);
+        // unconditional load (rows past the block read its row 0, mr >= 1) so that
+        // no branch splits the prologue: the weight loads below must stay ahead of
+        // the barrier, and the compiler only keeps them there in straight-line code
+        const uint4 t = *reinterpret_cast<const uint4 *>(x + (row < mr ? row : 0) * x_s0 + k0 + col * 8);
+        xr[q] = row < mr ? t : make_uint4(0, 0, 0, 0);
     }
 
     // 2. the first band's weights, all in flight together
@@ -157,10 +164,10 @@ gemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t 
     for (int b = 0;; b += 2) {
         const int col_a = (band0 + b) * 64 + wave * 16;
         if (b + 1 < nb) gemm_load_w<KS>(wb, w, w_s0, col_a + 64 + r16, k0, kq);
-        gemm_tile<MT, KS>(wa, xs, r16, kq, M, N, col_a, blockIdx.y, out, o_s0, part, bias);
+        gemm_tile<MT, KS>(wa, xs, r16, kq, M, row0, mr, N, col_a, blockIdx.y, out, o_s0, part, bias);
         if (b + 1 >= nb) break;
         if (b + 2 < nb) gemm_load_w<KS>(wa, w, w_s0, col_a + 128 + r16, k0, kq);
-        gemm_tile<MT, KS>(wb, xs, r16, kq, M, N, col_a + 64, blockIdx.y, out, o_s0, part, bias);
+        gemm_tile<MT, KS>(wb, xs, r16, kq, M, row0, mr, N, col_a + 64, blockIdx.y, out, o_s0, part, bias);
         if (b + 2 >= nb) break;
     }
 }
@@ -193,9 +200,9 @@ gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t
     }
 }
 
-// K slice per workgroup: 512 columns of K (256 when the X block has 128 rows,
-// which keeps the staged block inside 64 KiB of LDS).  Every slice is one
-// fp32 partial plane.
+// K slice per workgroup: 512 columns of K (256 above 64 rows, where a band and
+// slice run as 64-row blocks: the slices, planes and sums of one 128-row
+// block, twice the workgroups).  Every slice is one fp32 partial plane.
 int slice_of(int M, int N, int K) {
     // 512 K columns per workgroup for up to 64 rows (256 above); a projection
     // whose grid would still fit one workgroup per CU with 256-column slices
@@ -218,8 +225,9 @@ template <int MT, int KS>
 void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
                  uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
     const int bands = N / 64, S = K / KS;
-    const int nb = bands_per_wg(bands, S);
-    dim3 grid(bands / nb, S);
+    const int blocks = (M + 16 * MT - 1) / (16 * MT);  // row blocks
+    const int nb = bands_per_wg(bands, S * blocks);
+    dim3 grid(bands / nb, S, blocks);
     hipLaunchKernelGGL((gemm_kernel<MT, KS>), grid, dim3(kGemmThreads), 0, st, x, x_s0, M, w, w_s0, N, nb, out,
                        o_s0, part, bias);
 }
@@ -227,8 +235,11 @@ void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int6
 // The launch for M rows with the K slice slice_of picks.
 void dispatch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
                    uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
     const int ks = slice_of(M, N, K);
+    // more than 64 rows run as row blocks: of 64 rows, or of 32 where 64-row blocks would leave
+    // CUs without a workgroup (the code predictor's 128-row o projection: 128 -> 256 workgroups)
+    int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+    if (M > 64 && (N / 64) * (K / ks) * ((M + 63) / 64) < 256) mt = 2;
 #define NQ_GEMM_SLICES(MT)                                                                   \
     ks == 256   ? launch_gemm<MT, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st) \
     : ks == 768 ? launch_gemm<MT, 768>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st) \
@@ -236,8 +247,7 @@ void dispatch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, in
     switch (mt) {
         case 1: NQ_GEMM_SLICES(1); break;
         case 2: NQ_GEMM_SLICES(2); break;
-        case 4: NQ_GEMM_SLICES(4); break;
-        default: launch_gemm<8, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st); break;
+        default: NQ_GEMM_SLICES(4); break;
     }
 #undef NQ_GEMM_SLICES
 }
