@@ -200,11 +200,28 @@ gemm_reduce_kernel(const float *__restrict__ part, int S, int M, int N, uint16_t
     }
 }
 
-// K slice per workgroup: 512 columns of K (256 above 64 rows, where a band and
-// slice run as 64-row blocks: the slices, planes and sums of one 128-row
-// block, twice the workgroups).  Every slice is one fp32 partial plane.
+// More than 64 rows: 768-column K slices (a third of the planes) where K allows
+// them and the grid still has a workgroup for every CU, else the 256-column
+// slices of a 128-row block (whose sums the fused bf16 gate/up + SwiGLU kernel
+// reproduces), in row blocks of 64, else of 32 (32-row blocks of 256-column
+// slices when neither fills the CUs).
+struct RowsPlan {
+    int ks, rows;
+};
+RowsPlan rows_plan(int M, int N, int K) {
+    const int bands = N / 64;
+    for (const int ks : {768, 256}) {
+        if (K % ks) continue;
+        for (const int rb : {64, 32})
+            if (static_cast<int64_t>(bands) * (K / ks) * ((M + rb - 1) / rb) >= 256) return {ks, rb};
+    }
+    return {256, 32};
+}
+
+// K slice per workgroup (rows_plan above 64 rows).  Every slice is one fp32
+// partial plane.
 int slice_of(int M, int N, int K) {
-    // 512 K columns per workgroup for up to 64 rows (256 above); a projection
+    // 512 K columns per workgroup for up to 64 rows; a projection
     // whose grid would still fit one workgroup per CU with 256-column slices
     // (bands x slices <= 256) takes those, so that every CU streams weights.
     // 768-column slices where they make the grid whole multiples of 256
@@ -212,7 +229,7 @@ int slice_of(int M, int N, int K) {
     // workgroups, so half the CUs stream twice the weights of the others
     // (measured 10.8 us against 10.2 us for 256 even workgroups, which also
     // leave 8 partial planes instead of 12).
-    if (M > 64) return 256;
+    if (M > 64) return rows_plan(M, N, K).ks;
     if (N % 64 != 0) return 512;
     const int bands = N / 64;
     if (K % 256 == 0 && bands * (K / 256) <= 256) return 256;
@@ -236,10 +253,10 @@ void launch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int6
 void dispatch_gemm(const uint16_t *x, int64_t x_s0, int M, const uint16_t *w, int64_t w_s0, int N, int K,
                    uint16_t *out, int64_t o_s0, float *part, const uint16_t *bias, hipStream_t st) {
     const int ks = slice_of(M, N, K);
-    // more than 64 rows run as row blocks: of 64 rows, or of 32 where 64-row blocks would leave
-    // CUs without a workgroup (the code predictor's 128-row o projection: 128 -> 256 workgroups)
+    // more than 64 rows run as the row blocks rows_plan picks (the code predictor's 128-row o
+    // projection: 32-row blocks, 256 workgroups instead of 64 for one 128-row block)
     int mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-    if (M > 64 && (N / 64) * (K / ks) * ((M + 63) / 64) < 256) mt = 2;
+    if (M > 64 && N % 64 == 0) mt = rows_plan(M, N, K).rows / 16;
 #define NQ_GEMM_SLICES(MT)                                                                   \
     ks == 256   ? launch_gemm<MT, 256>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st) \
     : ks == 768 ? launch_gemm<MT, 768>(x, x_s0, M, w, w_s0, N, K, out, o_s0, part, bias, st) \
