@@ -25,6 +25,14 @@ SHAPES = [
     (37, 192, 1024),
     (16, 128, 512),
     (100, 320, 768),
+    # more than 64 rows, as row blocks: 768-column slices in 32-row blocks (the code predictor's down),
+    # in 64-row blocks with a 36-row last block; 256-column slices in 32-row blocks (its o projection),
+    # in 64-row blocks with a 26-row and with a one-row last block
+    (128, 1024, 3072),
+    (100, 2048, 6144),
+    (128, 1024, 1024),
+    (90, 1024, 3072),
+    (65, 2048, 2048),
 ]
 
 
