@@ -991,14 +991,23 @@ def measure_library():
     P, I, L = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     lib.nq_kv_read_probe.argtypes = [P, I, L, P, I, I, P, P]
     lib.nq_kv_read_probe.restype = I
+    lib.nq_kv_head_read_probe.argtypes = [P, I, L, P, I, I, I, I, P, P]
+    lib.nq_kv_head_read_probe.restype = I
     return lib
+
+
+# launch shapes of the per-head read probe: (workgroups per kv head, pages in flight per thread) --
+# the decode attention's 256 workgroups at about its bytes in flight per CU, and twice the workgroups
+HEAD_PROBE_SHAPES = {"per_head": (32, 8), "per_head_2x": (64, 8)}
 
 
 def kv_read_ceiling(args, torch, np) -> dict:
     """The read ceiling of the decode attention's access pattern: the K/V pages of the batch-64 decode
     workload (64 rows, KV U[64, 2048], permuted 32768-page pool) read whole by nq_kv_read_probe, one
-    launch per layer over 28 distinct layers (no reuse from the Infinity Cache), no arithmetic; and
-    the same number of bytes read contiguously (pages 0, 1, 2, ... of each layer)."""
+    launch per layer over 28 distinct layers (no reuse from the Infinity Cache), no arithmetic; the
+    same number of bytes read contiguously (pages 0, 1, 2, ... of each layer); and the same pages read
+    the way the attention reads them (nq_kv_head_read_probe: 32 x 8 workgroups, each reading one kv
+    head's 256-byte K and V rows of its pages, 16 lanes per row)."""
 
     from __graft_entry__ import load_package
 
@@ -1017,29 +1026,40 @@ def kv_read_ceiling(args, torch, np) -> dict:
     lib = measure_library()
     stream = torch.cuda.current_stream()
 
-    def launches(pages):
+    def launches(pages, per_head=None):
         for layer in range(layers):
-            rc = lib.nq_kv_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(), need,
-                                      1024, out.data_ptr(), stream.cuda_stream)
+            if per_head:
+                groups, depth = HEAD_PROBE_SHAPES[per_head]
+                rc = lib.nq_kv_head_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(),
+                                               need, 8, groups, depth, out.data_ptr(), stream.cuda_stream)
+            else:
+                rc = lib.nq_kv_read_probe(storage[layer].data_ptr(), POOL_PAGES, page_bytes, pages.data_ptr(), need,
+                                          1024, out.data_ptr(), stream.cuda_stream)
             if rc != 0:
-                raise RuntimeError(f"nq_kv_read_probe status {rc}")
+                raise RuntimeError(f"read probe status {rc}")
 
     timings = {}
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for name, pages in (("gather", gathered), ("contiguous", contiguous)):
-        launches(pages)
+    for name, pages, per_head in (("gather", gathered, None), ("contiguous", contiguous, None),
+                                  ("per_head", gathered, "per_head"), ("per_head_2x", gathered, "per_head_2x")):
+        launches(pages, per_head)
         torch.cuda.synchronize()
         start.record(stream)
         for _ in range(args.steps):
-            launches(pages)
+            launches(pages, per_head)
         end.record(stream)
         end.synchronize()
         timings[name] = start.elapsed_time(end) * 1e3 / (args.steps * layers)
     nbytes = need * page_bytes
     gbs = nbytes / timings["gather"] / 1e3
     cgbs = nbytes / timings["contiguous"] / 1e3
+    hgbs = nbytes / timings["per_head"] / 1e3
+    h2gbs = nbytes / timings["per_head_2x"] / 1e3
     log(f"KV page read ceiling: {need} pages = {nbytes / 1e6:.1f} MB per layer: permuted pages {timings['gather']:.1f} "
-        f"us -> {gbs:.0f} GB/s; the same bytes contiguous {timings['contiguous']:.1f} us -> {cgbs:.0f} GB/s")
+        f"us -> {gbs:.0f} GB/s; the same bytes contiguous {timings['contiguous']:.1f} us -> {cgbs:.0f} GB/s; "
+        f"the permuted pages read per kv head as the attention reads them, 256 workgroups "
+        f"{timings['per_head']:.1f} us -> {hgbs:.0f} GB/s, 512 workgroups {timings['per_head_2x']:.1f} us -> "
+        f"{h2gbs:.0f} GB/s")
     return {
         "metric": "KV page read ceiling GB/s (decode attention access pattern, no arithmetic)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 1,
@@ -1052,6 +1072,10 @@ def kv_read_ceiling(args, torch, np) -> dict:
                      "bytes_per_launch": nbytes, "us_per_launch": round(timings["gather"], 2)},
         "contiguous": {"us_per_launch": round(timings["contiguous"], 2), "GBps": round(cgbs, 1),
                        "frac": round(cgbs / HBM_PEAK_GBS, 4)},
+        "per_head": {"us_per_launch": round(timings["per_head"], 2), "GBps": round(hgbs, 1),
+                     "frac": round(hgbs / HBM_PEAK_GBS, 4), "kernel": "nq_kv_head_read_probe", "workgroups": 256},
+        "per_head_2x": {"us_per_launch": round(timings["per_head_2x"], 2), "GBps": round(h2gbs, 1),
+                        "frac": round(h2gbs / HBM_PEAK_GBS, 4), "kernel": "nq_kv_head_read_probe", "workgroups": 512},
     }
 
 
