@@ -648,14 +648,21 @@ int launch_tgemm_fp8_swiglu(const uint8_t *x, int64_t x_s0, const float *sx, int
     return NQ_LAUNCH_STATUS();
 }
 
-// 128 x 128 tiles over 4 x 4 waves of 32 x 32 (101 registers, sixteen waves in the one workgroup a CU
-// holds).  Measured on the 640-token prefill captures: 20.1 ms per decision against 20.8 for 64 x 128
-// tiles of 2 x 2 waves (two workgroups per CU), 20.3 for 64 x 128 of 2 x 4 waves and 20.4 for 128 x 128
-// of 4 x 2 waves.
-#ifndef NQ_TF8_SHAPE
-#define NQ_TF8_SHAPE 2, 2, 4, 4
-#endif
-constexpr int kTf8Shape[4] = {NQ_TF8_SHAPE};
+// Tile shapes of the tiled FP8 gate/up.  Square: 128 x 128 tiles over 4 x 4 waves of 32 x 32 (101
+// registers, sixteen waves in the one workgroup a CU holds; on the 640-token prefill captures 20.1 ms per
+// decision against 20.8 for 64 x 128 tiles of 2 x 2 waves, 20.3 for 64 x 128 of 2 x 4 waves and 20.4
+// for 128 x 128 of 4 x 2 waves).  Wide: 128 x 256 tiles over 2 x 4 waves of 64 x 64 (256 registers,
+// 149 KB of LDS): a 64 x 64 wave tile reads half the LDS bytes per MFMA of a 32 x 32 one, and the
+// 32 x 32 tiles' LDS reads (128 KB per CU per K block) outlast their MFMAs.  A round of either shape
+// (every CU one workgroup) costs about the same whatever the row count: 19.5 us square, 31 us wide
+// (I = 6144, K = 2048: e.g. 640 rows, 2 square rounds 39.1-39.5 us against 1 wide round 33.9-34.5 us;
+// 768 rows, 3 square rounds 53.8-54.4 us against 2 wide 60.1-60.4 us), so the launch takes the shape
+// with the smaller rounds x round cost.  Fewer than 256 square tiles run the 64 x 64 tiles of 2 x 2
+// waves, which fill more CUs.
+constexpr int kTf8Square[4] = {2, 2, 4, 4};
+constexpr int kTf8Wide[4] = {4, 4, 2, 4};
+constexpr int kTf8SquareRound = 39;  // round costs in half microseconds
+constexpr int kTf8WideRound = 62;
 
 constexpr int kFp8Slice = 1024;  // K bytes per workgroup slice (M <= 64)
 
@@ -779,9 +786,16 @@ extern "C" int nq_tgemm_fp8_swiglu(const uint8_t *xq, int64_t x_s0, const float 
     NQ_CHECK_ARG(sx_s0 >= K / 128 && sw_s0 >= K / 128 && o_s0 >= I && o_s0 % 2 == 0);
     NQ_CHECK_ARG(reinterpret_cast<uintptr_t>(out) % 4 == 0);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    constexpr int bm = 16 * kTf8Shape[0] * kTf8Shape[2], bn = 16 * kTf8Shape[1] * kTf8Shape[3];
-    if ((M + bm - 1) / bm * (2 * I / bn) >= 256)
-        return launch_tgemm_fp8_swiglu<kTf8Shape[0], kTf8Shape[1], kTf8Shape[2], kTf8Shape[3]>(
+    constexpr int bm = 16 * kTf8Square[0] * kTf8Square[2], bn = 16 * kTf8Square[1] * kTf8Square[3];
+    constexpr int wbm = 16 * kTf8Wide[0] * kTf8Wide[2], wbn = 16 * kTf8Wide[1] * kTf8Wide[3];
+    const int square = (M + bm - 1) / bm * (2 * I / bn);
+    if (square < 256)
+        return launch_tgemm_fp8_swiglu<2, 2, 2, 2>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0,
+                                                   st);
+    const int wide = (2 * I) % wbn == 0 ? (M + wbm - 1) / wbm * (2 * I / wbn) : 0;
+    if (wide > 0 && kTf8WideRound * ((wide + 255) / 256) < kTf8SquareRound * ((square + 255) / 256))
+        return launch_tgemm_fp8_swiglu<kTf8Wide[0], kTf8Wide[1], kTf8Wide[2], kTf8Wide[3]>(
             xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
-    return launch_tgemm_fp8_swiglu<2, 2, 2, 2>(xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
+    return launch_tgemm_fp8_swiglu<kTf8Square[0], kTf8Square[1], kTf8Square[2], kTf8Square[3]>(
+        xq, x_s0, sx, sx_s0, M, packed, w_s0, sw, sw_s0, I, K, out, o_s0, st);
 }

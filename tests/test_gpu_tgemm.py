@@ -105,7 +105,9 @@ def _fp8_integer_case(device, m, n, k, seed):
                               t(sw, torch.float32))
 
 
-@pytest.mark.parametrize("m", [640, 300, 37])
+# 640 and 300 rows run the 128 x 256 tiles, 768 the 128 x 128 ones (fewer rounds), 1280 two rounds of
+# 128 x 256 tiles, 37 the 64 x 64 tiles
+@pytest.mark.parametrize("m", [640, 300, 37, 768, 1280])
 def test_tgemm_fp8_swiglu_exact_on_integer_codes(nq, device, m):
     from nari_qwen3_tts_amd.layers import pack_fp8_swiglu, tgemm_fp8_swiglu
 
