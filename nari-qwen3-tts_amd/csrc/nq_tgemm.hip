@@ -32,6 +32,7 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));  // staging re
                                                                     // keeps them out of scratch)
 
 constexpr int kTgK = 64;             // K elements per stage
+constexpr int kTgC = kTgK / 8;       // 16-byte chunks of a staged row
 constexpr int kTgPitch = kTgK + 16;  // LDS row pitch in bf16 (32 bytes of padding)
 
 bool tg_al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -72,23 +73,23 @@ __device__ __forceinline__ void tg_load(u32x4_t (&xr)[XV], u32x4_t (&wr)[WV], co
     for (int q = 0; q < XV; ++q) xr[q] = *reinterpret_cast<const u32x4_t *>(xp[q] + k0);
 }
 
-// A register set into LDS: vector i = threadIdx.x + T q is tile row i / 8, 8-element chunk i % 8.
+// A register set into LDS: vector i = threadIdx.x + T q is tile row i / kTgC, 8-element chunk i % kTgC.
 template <int XV, int WV, int T>
 __device__ __forceinline__ void tg_store(const u32x4_t (&xr)[XV], const u32x4_t (&wr)[WV], uint16_t *xbuf,
                                          uint16_t *wbuf) {
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
         const int i = threadIdx.x + q * T;
-        *reinterpret_cast<u32x4_t *>(xbuf + (i >> 3) * kTgPitch + (i & 7) * 8) = xr[q];
+        *reinterpret_cast<u32x4_t *>(xbuf + (i / kTgC) * kTgPitch + (i % kTgC) * 8) = xr[q];
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
         const int i = threadIdx.x + q * T;
-        *reinterpret_cast<u32x4_t *>(wbuf + (i >> 3) * kTgPitch + (i & 7) * 8) = wr[q];
+        *reinterpret_cast<u32x4_t *>(wbuf + (i / kTgC) * kTgPitch + (i % kTgC) * 8) = wr[q];
     }
 }
 
-// The MFMAs of one staged 64-wide K slice: the wave's (16 MT) x (16 NT) part of the tile.
+// The MFMAs of one staged kTgK-wide K slice: the wave's (16 MT) x (16 NT) part of the tile.
 template <int MT, int NT>
 __device__ __forceinline__ void tg_compute(floatx4_t (&acc)[MT][NT], const uint16_t *xbuf, const uint16_t *wbuf,
                                            int wm, int wn, int r16, int kq) {
@@ -147,19 +148,19 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
             return static_cast<int64_t>(tn) * BN + r;
         }
     };
-    // staging vector i = threadIdx.x + q * 256: tile row i / 8, 8-element chunk i % 8
+    // staging vector i = threadIdx.x + q * T: tile row i / kTgC, 8-element chunk i % kTgC
     const uint16_t *xp[XV];
     const uint16_t *wp[WV];
 #pragma unroll
     for (int q = 0; q < XV; ++q) {
         const int i = threadIdx.x + q * T;
-        const int row = m0 + (i >> 3);
-        xp[q] = x + static_cast<int64_t>(row < M ? row : M - 1) * x_s0 + k_begin + (i & 7) * 8;
+        const int row = m0 + i / kTgC;
+        xp[q] = x + static_cast<int64_t>(row < M ? row : M - 1) * x_s0 + k_begin + (i % kTgC) * 8;
     }
 #pragma unroll
     for (int q = 0; q < WV; ++q) {
         const int i = threadIdx.x + q * T;
-        wp[q] = w + w_row(i >> 3) * w_s0 + k_begin + (i & 7) * 8;
+        wp[q] = w + w_row(i / kTgC) * w_s0 + k_begin + (i % kTgC) * 8;
     }
     floatx4_t acc[MT][NT];
 #pragma unroll
