@@ -343,18 +343,8 @@ __global__ void last_rows_kernel(const int32_t *__restrict__ off, int B, int u, 
 
 using namespace nq;
 
-#ifndef NQ_SG_KS_64x128
-#define NQ_SG_KS_64x128 32
-#endif
-#ifndef NQ_SG_KS_64x64
-#define NQ_SG_KS_64x64 64
-#endif
-#ifndef NQ_SG_KS_32x64
-#define NQ_SG_KS_32x64 64
-#endif
-#ifndef NQ_SG_KS_32x32
-#define NQ_SG_KS_32x32 128
-#endif
+// K columns per stage of each tile shape (smaller tiles take deeper stages)
+constexpr int kSgKs64x128 = 32, kSgKs64x64 = 64, kSgKs32x64 = 64, kSgKs32x32 = 128;
 
 extern "C" int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, const float *w, int64_t w_s0, int M,
                         int N, int K, const float *bias, int act, const float *res, int64_t r_s0, const float *scale,
@@ -379,10 +369,10 @@ extern "C" int nq_sgemm(const float *x, int64_t x_s0, const int32_t *x_rows, con
     // tile).  The smaller tiles take more k per stage (fewer barriers and more bytes in flight per wave).
 #define NQ_SG_PICK(SPLIT)                                                                \
     if (units(128, 128) >= 256) return NQ_SG(2, 2, 4, 4, 32, SPLIT);                    \
-    if (units(64, 128) >= 256) return NQ_SG(2, 2, 2, 4, NQ_SG_KS_64x128, SPLIT);        \
-    if (units(64, 64) >= 256) return NQ_SG(1, 2, 4, 2, NQ_SG_KS_64x64, SPLIT);          \
-    if (units(32, 64) >= 256) return NQ_SG(1, 2, 2, 2, NQ_SG_KS_32x64, SPLIT);          \
-    return NQ_SG(1, 1, 2, 2, NQ_SG_KS_32x32, SPLIT);
+    if (units(64, 128) >= 256) return NQ_SG(2, 2, 2, 4, kSgKs64x128, SPLIT);        \
+    if (units(64, 64) >= 256) return NQ_SG(1, 2, 4, 2, kSgKs64x64, SPLIT);          \
+    if (units(32, 64) >= 256) return NQ_SG(1, 2, 2, 2, kSgKs32x64, SPLIT);          \
+    return NQ_SG(1, 1, 2, 2, kSgKs32x32, SPLIT);
     if (precision == NQ_MATMUL_HIGH) {
         NQ_SG_PICK(true)
     }

@@ -237,26 +237,17 @@ tgemm_kernel(const uint16_t *__restrict__ x, int64_t x_s0, int M, const uint16_t
 // sixteen waves of the one workgroup a CU holds (80 KB of LDS) are resident together.  Measured on
 // the 640-token prefill captures against 64 x 128 tiles of 2 x 2 waves at two workgroups per CU:
 // 20.75 against 21.57 ms per decision (2 x 4 waves of 32 x 64 at 128 x 128: 21.06 ms).
-#ifndef NQ_TG_SHAPE
-#define NQ_TG_SHAPE 2, 2, 4, 4
-#endif
-constexpr int kTgShape[4] = {NQ_TG_SHAPE};
+constexpr int kTgShape[4] = {2, 2, 4, 4};
 constexpr int kTgMT = kTgShape[0], kTgNT = kTgShape[1], kTgWM = kTgShape[2], kTgWN = kTgShape[3];
 constexpr int kTgBM = 16 * kTgMT * kTgWM, kTgBN = 16 * kTgNT * kTgWN;
-#ifndef NQ_TG_ROUND
-#define NQ_TG_ROUND 256
-#endif
-constexpr int64_t kTgRound = NQ_TG_ROUND;  // workgroups resident at once (one per CU)
+constexpr int64_t kTgRound = 256;  // workgroups resident at once (one per CU)
 
 // K slices of a launch.  One workgroup fits a CU, so the units run in rounds of 256 and a launch
 // costs about rounds x (slice length + a unit's fixed cost, in K columns): the slice
 // count minimising that (each slice a multiple of 64 columns and at least 256 of them), the fewest
 // slices on a tie.
-#ifndef NQ_TG_UNIT_COST
-#define NQ_TG_UNIT_COST 512
-#endif
 int tgemm_splits(int M, int N, int K) {
-    constexpr int64_t kUnitCost = NQ_TG_UNIT_COST;
+    constexpr int64_t kUnitCost = 512;
     const int64_t tiles = static_cast<int64_t>((M + kTgBM - 1) / kTgBM) * (N / kTgBN);
     int best = 1;
     int64_t best_cost = (tiles + kTgRound - 1) / kTgRound * (K + kUnitCost);
