@@ -146,11 +146,16 @@ int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
  * NQ_ATTN_PREFILL (rows with several queries), or both.  The two parts read
  * the same plan and write disjoint output rows, so a caller may issue them on
  * two streams to run them concurrently; NQ_ATTN_DECODE alone promises the plan
- * holds no row with more than one query.  status (device int32, may be NULL)
- * is set to NQ_ERR_INVALID_ARGUMENT when a page id outside [0, num_pages) is
- * met (that page is skipped).
+ * holds no row with more than one query.  NQ_ATTN_BESIDE_PREFILL (with
+ * NQ_ATTN_DECODE) says the prefill part runs concurrently on another stream:
+ * decode launches of more than 64 rows then take twelve-wave workgroups
+ * instead of sixteen, which leaves each CU room that the prefill tiles use
+ * (the K/V span split follows the workgroup size, so results agree with a
+ * launch without the flag to rounding, not bit for bit).  status (device int32, may be NULL) is set to
+ * NQ_ERR_INVALID_ARGUMENT when a page id outside [0, num_pages) is met (that
+ * page is skipped).
  */
-enum nq_attention_parts { NQ_ATTN_DECODE = 1, NQ_ATTN_PREFILL = 2 };
+enum nq_attention_parts { NQ_ATTN_DECODE = 1, NQ_ATTN_PREFILL = 2, NQ_ATTN_BESIDE_PREFILL = 4 };
 int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *cache,
                        int64_t c_page, int64_t c_kind, int64_t c_slot, int64_t c_head,
                        int num_pages, const int32_t *kv_indices, int page_size, int num_qo_heads,

@@ -33,6 +33,7 @@ NQ_MATMUL_HIGHEST = 0
 NQ_MATMUL_HIGH = 1
 NQ_ATTN_DECODE = 1
 NQ_ATTN_PREFILL = 2
+NQ_ATTN_BESIDE_PREFILL = 4
 NQ_NOALLOC_SCRATCH_BYTES = 32 << 20
 NQ_REPORT_HEAD = 8
 

@@ -60,10 +60,15 @@ enum MetaSlot {
 // kBinSmallRows rows and kBinWavesLarge above: on the batch-64 step eight
 // waves measured 55.5-55.8 us per launch against 56.3-57.7 for sixteen (12:
 // 56.8-57.3, 4: 58.9-59.7), while the 112 decode rows of the mixed batch took
-// 133.5-135.5 us with eight and 104.8-105.9 with sixteen.
+// 133.5-135.5 us with eight and 104.8-105.9 with sixteen.  A launch that runs
+// beside the prefill part of its batch (NQ_ATTN_BESIDE_PREFILL) takes
+// kBinWavesShared above kBinSmallRows: with twelve waves the mixed batch's layer
+// took 128.1-128.9 us against 132.7-135.3 with sixteen (its decode rows alone
+// 104.4-105.3 against 103.7-103.8).
 constexpr int kBinWgs = 256;
 constexpr int kBinWavesSmall = 8;
 constexpr int kBinWavesLarge = 16;
+constexpr int kBinWavesShared = 12;
 constexpr int kBinSmallRows = 64;
 constexpr int kBinMaxSlots = 40;   // pieces per bin (LDS q capacity)
 constexpr int kBinSortCap = 2048;  // pieces the plan can sort
@@ -2278,11 +2283,14 @@ int launch_paged(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint16_t *
                        c_kind, c_slot, c_head, num_pages, kv_indices, index_limit, Hkv, ps_log2, scale * kLog2e, out, \
                        o_s0, o_s1, ws, L, status)
             const bool few_rows = rows_bound <= kBinSmallRows;
+            const bool beside = (parts & NQ_ATTN_BESIDE_PREFILL) != 0;
             if (ps_log2 < 4) {
                 if (few_rows) NQ_BIN_QIN(true, kBinWavesSmall);
+                else if (beside) NQ_BIN_QIN(true, kBinWavesShared);
                 else NQ_BIN_QIN(true, kBinWavesLarge);
             } else {
                 if (few_rows) NQ_BIN_QIN(false, kBinWavesSmall);
+                else if (beside) NQ_BIN_QIN(false, kBinWavesShared);
                 else NQ_BIN_QIN(false, kBinWavesLarge);
             }
 #undef NQ_BIN_QIN
@@ -2410,7 +2418,9 @@ extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,
                                   int parts, void *workspace, int64_t workspace_bytes,
                                   int32_t *status, void *stream) {
     NQ_CHECK_ARG(q && cache && kv_indices && out && workspace);
-    NQ_CHECK_ARG(parts >= 1 && parts <= (NQ_ATTN_DECODE | NQ_ATTN_PREFILL));
+    NQ_CHECK_ARG((parts & (NQ_ATTN_DECODE | NQ_ATTN_PREFILL)) != 0 &&
+                 (parts & ~(NQ_ATTN_DECODE | NQ_ATTN_PREFILL | NQ_ATTN_BESIDE_PREFILL)) == 0);
+    NQ_CHECK_ARG(!(parts & NQ_ATTN_BESIDE_PREFILL) || (parts & NQ_ATTN_DECODE));
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1);
     NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
     NQ_CHECK_ARG(max_query_tokens >= 1 && max_pages >= 1);
@@ -2588,7 +2598,9 @@ extern "C" int nq_paged_attention_noalloc(const int32_t *qo_indptr, const int32_
     if (n_rows > nq::kPlanThreads) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG(q && cache && kv_indptr && last_page_len && kv_indices && out);
     NQ_CHECK_ARG(qo_indptr || n_rows <= max_query_tokens);
-    NQ_CHECK_ARG(parts >= 1 && parts <= (NQ_ATTN_DECODE | NQ_ATTN_PREFILL));
+    NQ_CHECK_ARG((parts & (NQ_ATTN_DECODE | NQ_ATTN_PREFILL)) != 0 &&
+                 (parts & ~(NQ_ATTN_DECODE | NQ_ATTN_PREFILL | NQ_ATTN_BESIDE_PREFILL)) == 0);
+    NQ_CHECK_ARG(!(parts & NQ_ATTN_BESIDE_PREFILL) || (parts & NQ_ATTN_DECODE));
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0 && num_pages >= 1);
     NQ_CHECK_ARG(num_kv_heads >= 1 && num_qo_heads % num_kv_heads == 0);
     if (!nq::aligned16(q) || !nq::aligned16(cache) || !nq::aligned16(out)) return NQ_ERR_UNSUPPORTED;

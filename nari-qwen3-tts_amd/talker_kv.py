@@ -267,7 +267,8 @@ class _HipBindingBase:
         self._fork.record(main)
         self._side.wait_event(self._fork)
         self._attention_call(query, layer_index, _lib.NQ_ATTN_PREFILL, self._side.cuda_stream)
-        out = self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE, main.cuda_stream)
+        out = self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_BESIDE_PREFILL,
+                                   main.cuda_stream)
         self._join.record(self._side)
         main.wait_event(self._join)
         return out

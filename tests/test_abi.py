@@ -102,3 +102,29 @@ def test_argument_errors_are_caught_on_the_host(nq):
 
     with pytest.raises(KVAllocationError):
         _lib.check(-4, "x")
+
+
+def test_attention_parts_flags(nq):
+    """The attention part flags agree with the header, and flag sets without a part to run, with an
+    unknown bit, or with the beside-prefill bit but no decode part are refused on the host."""
+
+    from nari_qwen3_tts_amd import _lib
+
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"enum nq_attention_parts \{([^}]*)\}", text).group(1)
+    declared = {k.strip(): int(v) for k, v in (e.split("=") for e in body.split(",") if e.strip())}
+    assert declared == {"NQ_ATTN_DECODE": _lib.NQ_ATTN_DECODE, "NQ_ATTN_PREFILL": _lib.NQ_ATTN_PREFILL,
+                        "NQ_ATTN_BESIDE_PREFILL": _lib.NQ_ATTN_BESIDE_PREFILL}
+    lib = _lib.load()
+
+    def call(parts):
+        # placeholder pointers: the argument checks run before any device access
+        return lib.nq_paged_attention(1, 2048, 128, 1, 65536, 32768, 2048, 128, 64, 1, 16, 16, 8, 128, 0.088, 1,
+                                      2048, 128, 64, 1024, parts, 1, 1 << 40, None, None)
+
+    for parts in (0, _lib.NQ_ATTN_BESIDE_PREFILL, _lib.NQ_ATTN_PREFILL | _lib.NQ_ATTN_BESIDE_PREFILL, 8):
+        assert call(parts) == -1, parts
+    # accepted flag sets pass on to the next check, which refuses the misaligned placeholder pointers
+    for parts in (_lib.NQ_ATTN_DECODE, _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_BESIDE_PREFILL,
+                  _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_PREFILL):
+        assert call(parts) == -2, parts

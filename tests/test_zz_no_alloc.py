@@ -40,6 +40,7 @@ def _mixed_case(nq, device, seed, pre_prior, pre_adv, dec_prior, pages):
 
 
 def test_noalloc_attention_equals_the_workspace_path(nq, device):
+    from nari_qwen3_tts_amd import _lib
     from nari_qwen3_tts_amd.kernels import paged_attention_noalloc
 
     cases = [
@@ -55,7 +56,11 @@ def test_noalloc_attention_equals_the_workspace_path(nq, device):
         want = ctx.run_attention(q, 0).clone()
         status = torch.zeros(1, dtype=torch.int32, device=device)
         got = torch.full_like(q, 7.0)
-        paged_attention_noalloc(q, kv.storage[0], ctx.metadata, max_pages=ctx.index_capacity, status=status, out=got)
+        # the workspace path issues a mixed batch's decode rows with NQ_ATTN_BESIDE_PREFILL (their workgroup
+        # size, hence their K/V span split, depends on it), so the comparison takes the same parts
+        parts = _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_PREFILL | (_lib.NQ_ATTN_BESIDE_PREFILL if pre_prior else 0)
+        paged_attention_noalloc(q, kv.storage[0], ctx.metadata, max_pages=ctx.index_capacity, parts=parts,
+                                status=status, out=got)
         torch.cuda.synchronize()
         assert int(status.item()) == 0 and int(ctx.attention_status.item()) == 0
         assert torch.equal(got[:n], want[:n]), f"seed {seed}: no-allocation output differs from the workspace path"
