@@ -51,7 +51,7 @@ constexpr int kPlanGrid = 8;
 enum MetaSlot {
     kMetaChunks = 0, kMetaChunkTok = 1, kMetaStatus = 2, kMetaQueries = 3,
     kMetaDecRows = 4, kMetaBlocks = 5, kMetaPTiles = 6, kMetaPieces = 7, kMetaBinSlots = 8,
-    kMetaSplitRows = 9, kMetaPItems = 10, kMetaCount = 16
+    kMetaSplitRows = 9, kMetaPItems = 10, kMetaPWide = 11, kMetaCount = 16
 };
 
 // Decode bins: the fused decode kernel runs kBinWgs workgroups (one per CU);
@@ -87,17 +87,30 @@ __host__ __device__ inline int bins_per_head(int num_kv_heads) {
     return nb < 1 ? 1 : nb;
 }
 
-// Prefill MFMA tiles: 32 queries of one row (x 2 query heads = 64 score rows)
-// against 64-key tiles.
+// Prefill MFMA tiles against 64-key tiles, in one of two shapes chosen per
+// batch by the plan: narrow tiles of kPrefQ queries of one row (a wave: 16
+// queries of one query head, two register sets of K/V in flight) when the
+// batch has prefill rows only, wide tiles of kPrefQWide queries (a wave: 16
+// queries in both query heads of the kv head, each K/V operand read feeding
+// two MFMAs; one register set in flight) when it also has decode rows, whose
+// launch then runs beside it.  On the mixed batch of 16 prompt chunks and 112
+// decode rows the wide tiles took the layer to 124.3-126.8 us against
+// 128.9-132.3 with narrow ones (four alternations on one box: 328 instead of
+// 608 tile workgroups share the CUs with the decode bins), while the prefill
+// rows alone took 38.0-38.1 us against 35.2-35.3 with narrow tiles (a longer
+// chain per key tile on the longest tiles' critical path).
 constexpr int kPrefQ = 32;
+constexpr int kPrefQWide = 64;
 constexpr int kPrefK = 64;
 constexpr int kPrefPages = 1024;  // page ids of one prefill item kept in LDS
 // A tile whose causal key range spans more than kPrefPieceTiles 64-key tiles is
 // cut into up to kPrefMaxPieces pieces of whole key tiles, one workgroup each;
-// the last piece to finish merges them.
+// the last piece to finish merges them.  Cutting shorter tiles measured slower:
+// with the mixed batch's wide tiles cut to fill the 512 resident workgroups
+// (pieces of at most 5 key tiles) the prefill rows took 74.5-74.8 us (58.8 with
+// a relaxed arrival count in a timing copy), against 38 us uncut.
 constexpr int kPrefPieceTiles = 16;
 constexpr int kPrefMaxPieces = 4;
-constexpr int kPrefDepth = 2;  // 64-key tiles whose K/V loads are in flight (1 or 2)
 
 // Prefill chunk descriptor.
 struct alignas(16) ChunkDesc {
@@ -159,18 +172,23 @@ __host__ __device__ inline PlanLayout plan_layout(int T, int max_pages, int page
     return L;
 }
 
-// Prefill tile t of a row with kv_len keys and qo_len queries covers keys
-// [0, kv_len - qo_len + 32 t + nq) (bottom-right causal); its 64-key tiles,
-// and the pieces they are cut into.
-__device__ __forceinline__ int pref_tile_keys(int kv_len, int qo_len, int t) {
-    const int nq = qo_len - t * kPrefQ < kPrefQ ? qo_len - t * kPrefQ : kPrefQ;
-    const int n_keys = kv_len - qo_len + t * kPrefQ + nq;
+// Prefill tile t (of qt queries) of a row with kv_len keys and qo_len queries
+// covers keys [0, kv_len - qo_len + qt t + nq) (bottom-right causal); its
+// 64-key tiles, and the pieces they are cut into.
+__device__ __forceinline__ int pref_tile_keys(int kv_len, int qo_len, int t, int qt) {
+    const int nq = qo_len - t * qt < qt ? qo_len - t * qt : qt;
+    const int n_keys = kv_len - qo_len + t * qt + nq;
     return n_keys > 0 ? n_keys : 0;
 }
 
+// Pieces of a tile over n_keys keys.  Every piece spans at least two key
+// tiles, so the first key of the last piece lies below the tile's first query
+// limit (the limits of a tile's queries lie within 64 keys of each other):
+// each piece's first key tile holds a key every query attends to.
 __device__ __forceinline__ int pref_pieces(int n_keys) {
     const int n_kt = (n_keys + kPrefK - 1) / kPrefK;
-    const int k = (n_kt + kPrefPieceTiles - 1) / kPrefPieceTiles;
+    int k = (n_kt + kPrefPieceTiles - 1) / kPrefPieceTiles;
+    k = k > n_kt / 2 ? n_kt / 2 : k;
     return k < 1 ? 1 : (k > kPrefMaxPieces ? kPrefMaxPieces : k);
 }
 
@@ -219,7 +237,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     __shared__ int s_boff[kPlanThreads];
     __shared__ int s_dec[kPlanThreads];
     __shared__ unsigned long long s_cand[8];
-    __shared__ int s_tmp[4 * (kWave + 1)];
+    __shared__ int s_tmp[6 * (kWave + 1)];
     __shared__ __attribute__((aligned(16))) unsigned s_keys[kBinSortCap];
     __shared__ unsigned s_sorted[kBinSortCap];
     __shared__ int4 s_pa[kBinSortCap], s_pb[kBinSortCap];
@@ -276,9 +294,10 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         return;
     }
 
-    // Decode rows and their key blocks, and prefill rows' 32-query tiles, in
-    // one scan.
-    int is_dec = 0, nblk = 0, nt = 0, npc = 0;
+    // Decode rows and their key blocks, and prefill rows' tiles and pieces in
+    // both tile shapes, in one scan; the shape follows whether the batch has
+    // decode rows.
+    int is_dec = 0, nblk = 0, nt_n = 0, np_n = 0, nt_w = 0, np_w = 0;
     if (tid < n_rows) {
         const int qo_len = s_qo[tid + 1] - s_qo[tid];
         if (qo_len == 1) {
@@ -286,14 +305,21 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
             nblk = (s_kvlen[tid] + kBlockTok - 1) / kBlockTok;
             nblk = nblk < 1 ? 1 : nblk;
         } else if (qo_len > 1) {
-            nt = (qo_len + kPrefQ - 1) / kPrefQ;
-            for (int t = 0; t < nt; ++t) npc += pref_pieces(pref_tile_keys(s_kvlen[tid], qo_len, t));
+            nt_n = (qo_len + kPrefQ - 1) / kPrefQ;
+            for (int t = 0; t < nt_n; ++t) np_n += pref_pieces(pref_tile_keys(s_kvlen[tid], qo_len, t, kPrefQ));
+            nt_w = (qo_len + kPrefQWide - 1) / kPrefQWide;
+            for (int t = 0; t < nt_w; ++t) np_w += pref_pieces(pref_tile_keys(s_kvlen[tid], qo_len, t, kPrefQWide));
         }
     }
-    int sc_excl[4], sc_total[4];
-    block_exclusive_scan_n<4>({is_dec, nblk, nt, npc}, s_tmp, sc_excl, sc_total);
-    const int dec_idx = sc_excl[0], boff = sc_excl[1], t0_tiles = sc_excl[2], p0_items = sc_excl[3];
-    const int n_dec = sc_total[0], n_blocks = sc_total[1], n_ptiles = sc_total[2], n_pitems = sc_total[3];
+    int sc_excl[6], sc_total[6];
+    block_exclusive_scan_n<6>({is_dec, nblk, nt_n, np_n, nt_w, np_w}, s_tmp, sc_excl, sc_total);
+    const int dec_idx = sc_excl[0], boff = sc_excl[1];
+    const int n_dec = sc_total[0], n_blocks = sc_total[1];
+    const bool wide = n_dec > 0;
+    const int qt = wide ? kPrefQWide : kPrefQ;
+    const int nt = wide ? nt_w : nt_n;
+    const int t0_tiles = wide ? sc_excl[4] : sc_excl[2], p0_items = wide ? sc_excl[5] : sc_excl[3];
+    const int n_ptiles = wide ? sc_total[4] : sc_total[2], n_pitems = wide ? sc_total[5] : sc_total[3];
     s_dec[tid] = dec_idx;
     s_boff[tid] = boff;
     __syncthreads();
@@ -462,7 +488,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
     }
     if (!lead) return;
 
-    // Prefill rows: 32-query tiles, each cut into pieces of whole 64-key tiles.
+    // Prefill rows: tiles of qt queries, each cut into pieces of whole 64-key tiles.
     // Item = two int4: the tile {first query, queries, first page offset, key
     // limit of the first query (bottom-right causal)} and the piece {first key,
     // end key, (piece << 8) | pieces, tile index}.  The tiles' arrival
@@ -478,9 +504,9 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         const int qo_len = s_qo[tid + 1] - s_qo[tid];
         int it = p0_items;
         for (int t = 0; t < nt; ++t) {
-            const int4 td = make_int4(s_qo[tid] + t * kPrefQ, min(kPrefQ, qo_len - t * kPrefQ), s_base[tid],
-                                      s_kvlen[tid] - qo_len + t * kPrefQ + 1);
-            const int n_keys = pref_tile_keys(s_kvlen[tid], qo_len, t);
+            const int4 td = make_int4(s_qo[tid] + t * qt, min(qt, qo_len - t * qt), s_base[tid],
+                                      s_kvlen[tid] - qo_len + t * qt + 1);
+            const int n_keys = pref_tile_keys(s_kvlen[tid], qo_len, t, qt);
             const int n_kt = (n_keys + kPrefK - 1) / kPrefK;
             const int k = pref_pieces(n_keys);
             for (int p = 0; p < k; ++p, ++it) {
@@ -493,6 +519,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         if (tid == 0) {
             meta[kMetaPTiles] = n_ptiles;
             meta[kMetaPItems] = n_pitems;
+            meta[kMetaPWide] = wide ? 1 : 0;
         }
     }
     if (n_ptiles == 0) {
@@ -1892,16 +1919,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
 // Prefill rows on MFMA (head dim 128, two query heads per kv head).  A
-// workgroup takes one piece (a range of whole 64-key tiles) of one 32-query
-// tile of a row and one kv head; wave w owns 16 queries (w & 1) of query head
-// 2h + (w >> 1).  Per 64-key tile the workgroup stages K and V as they sit in
-// the cache ([key][d], 16-byte stores) and each wave computes the transposed
-// scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (K from LDS as the A
-// operand, Q held in registers as the B operand), so a lane holds 16 scores
-// of ONE query (lane & 15) for keys 16 nt + 4 (lane >> 4) + e.  The online
-// softmax is then per lane (the four lanes of a query agree on the running
-// maximum through two cross-lane exchanges, and keep partial row sums that
-// are added once at the end), the probabilities are packed to bf16 in
+// workgroup takes one piece (a range of whole 64-key tiles) of one 64-query
+// tile of a row and one kv head h; wave w owns queries 16 w .. 16 w + 15 in
+// both query heads 2h and 2h + 1, so every K and V operand it reads from LDS
+// feeds two MFMAs.  Per 64-key tile the workgroup stages K and V as they sit
+// in the cache ([key][d], 16-byte stores) and each wave computes the
+// transposed scores S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (K from LDS as
+// the A operand, Q held in registers as the B operand), so a lane holds 16
+// scores of ONE query (lane & 15) per head for keys 16 nt + 4 (lane >> 4) + e.
+// The online softmax is then per lane (the four lanes of a query agree on the
+// running maximum through two cross-lane exchanges, and keep partial row sums
+// that are added once at the end), the probabilities are packed to bf16 in
 // registers and used directly as the B operand of O^T += V^T P^T, whose A
 // operand (V^T: 8 keys of one column per lane, in the same key order as the
 // lane's probabilities) comes from gfx950's transposing LDS read
@@ -1929,24 +1957,24 @@ __device__ __forceinline__ uint32_t pf_pack_bf16(float a, float b) {
     return u;
 }
 
-template <int D>
-__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4 - kPrefDepth, 4 - kPrefDepth)))
-prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
-                    const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
-                    int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
-                    int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
-                    int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
+// One workgroup's prefill items in the tile shape kWide (see kPrefQ); ks, vs
+// and pages are the launch's LDS arrays, s_arrived its arrival flag.
+template <int D, bool kWide>
+__device__ __forceinline__ void prefill_tiles(
+    const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1, const uint16_t *__restrict__ cache, int64_t c_page,
+    int64_t c_kind, int64_t c_slot, int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices,
+    int index_limit, int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out, int64_t o_s0,
+    int64_t o_s1, char *__restrict__ ws, const PlanLayout &L, int32_t *status, uint16_t *ks, uint16_t *vs,
+    int *pages, int *s_arrived) {
     // K and V row pitch (bf16): rows 288 bytes apart, the 32-byte row offset at which gfx950 serves
     // 16-byte LDS reads of consecutive rows without bank conflicts (272-byte rows measured 0.6 us
     // slower per layer of the mixed batch)
     constexpr int KP = D + 16;
-    constexpr int DT = D / 16;       // 16-wide output column tiles
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[kPrefK * KP];
-    __shared__ int pages[kPrefPages];
-    __shared__ int s_arrived;
+    constexpr int DT = D / 16;         // 16-wide output column tiles
+    constexpr int KK = D / 32;         // 32-deep k steps of S^T
+    constexpr int NH = kWide ? 2 : 1;  // query heads per wave
+    constexpr int kDepth = kWide ? 1 : 2;  // 64-key tiles whose K/V loads are in flight
     const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
-    if (meta[kMetaStatus] != NQ_OK) return;
     const int4 *pitems = reinterpret_cast<const int4 *>(ws + L.pitems);
     float *part_ml = reinterpret_cast<float *>(ws + L.part_ml);
     float *part_o = reinterpret_cast<float *>(ws + L.part_o);
@@ -1962,6 +1990,10 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
     // 4 kq .. 4 kq + 3 of column 16 dt + j
     const uint16_t *vrow = vs + (kq * 4 + (r16 >> 2)) * KP + 4 * (r16 & 3);
     const bool out_vec = (reinterpret_cast<uintptr_t>(out) & 7) == 0 && (o_s0 & 3) == 0 && (o_s1 & 3) == 0;
+    // the wave's queries within a tile, and its query head a of kv head h: wide waves take 16
+    // queries each in both heads, narrow ones 16 queries (wave & 1) of head 2h + (wave >> 1)
+    const int qsub = kWide ? wave * 16 : (wave & 1) * 16;
+    auto head_of = [&](int h, int a) { return kWide ? 2 * h + a : 2 * h + (wave >> 1); };
     bool bad = false;
     for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
         const int pi = static_cast<int>(item / num_kv_heads);
@@ -1969,27 +2001,34 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
         const int4 td = pitems[2 * pi], pd = pitems[2 * pi + 1];
         const int q0 = td.x, nq = td.y, page_start = td.z, lim0 = td.w;
         const int kb = pd.x, ke = pd.y, piece = pd.z >> 8, n_pieces = pd.z & 255;
-        const int head = 2 * h + (wave >> 1);
-        const int qsub = (wave & 1) * 16;
         const int qj = qsub + r16;              // the lane's query within the tile
         const int limit = lim0 + qj;            // its keys are [0, limit) (lanes past nq compute on zeros)
-        uint4 qa[D / 32];
+        uint4 qa[NH][KK];
         {
             const bool ok = qj < nq;
-            const uint16_t *qp = q + static_cast<int64_t>(q0 + qj) * q_s0 + head * q_s1 + kq * 8;
 #pragma unroll
-            for (int kk = 0; kk < D / 32; ++kk)
-                qa[kk] = ok ? *reinterpret_cast<const uint4 *>(qp + kk * 32) : make_uint4(0, 0, 0, 0);
+            for (int a = 0; a < NH; ++a) {
+                const uint16_t *qp = q + static_cast<int64_t>(q0 + qj) * q_s0 + head_of(h, a) * q_s1 + kq * 8;
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk)
+                    qa[a][kk] = ok ? *reinterpret_cast<const uint4 *>(qp + kk * 32) : make_uint4(0, 0, 0, 0);
+            }
         }
-        float m_run = -INFINITY, l_run = 0.f;  // raw-score maximum; this lane's part of the row sum
-        pf_floatx4 acc[DT];                    // acc[dt][e] = O[query qj][16 dt + 4 kq + e] (unnormalised)
+        // per head: raw-score maximum, this lane's part of the row sum
+        float m_run[NH], l_run[NH];
+        pf_floatx4 acc[NH][DT];  // acc[a][dt][e] = O[query qj][head a][16 dt + 4 kq + e] (unnormalised)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
-        // K/V of the next kPrefDepth 64-key tiles are loaded into registers (one set per tile in
+        for (int a = 0; a < NH; ++a) {
+            m_run[a] = -INFINITY;
+            l_run[a] = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[a][dt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+        // K/V of the next kDepth 64-key tiles are loaded into registers (one set per tile in
         // flight) while the current tile is computed; each thread owns kStageVec (key, 8-channel)
         // pieces of a tile.
         constexpr int kStageVec = kPrefK * (D / 8) / kAttnThreads;
-        uint4 kr[kPrefDepth][kStageVec], vr[kPrefDepth][kStageVec];
+        uint4 kr[kDepth][kStageVec], vr[kDepth][kStageVec];
         // the piece's page list goes to LDS once (when it fits), so a tile's K/V loads do not wait
         // for an index load
         const int pg0 = kb >> ps_log2;
@@ -2034,7 +2073,7 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 }
             }
         };
-        // one 64-key tile from register set S, whose loads were issued kPrefDepth tiles ago
+        // one 64-key tile from register set S, whose loads were issued kDepth tiles ago
         auto step = [&](int kt0, auto set) {
             constexpr int S = decltype(set)::value;
             __syncthreads();  // the previous tile's LDS reads are done
@@ -2046,17 +2085,21 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 *reinterpret_cast<uint4 *>(vs + key * KP + c8 * 8) = vr[S][v];
             }
             __syncthreads();
-            if (kt0 + kPrefDepth * kPrefK < ke) issue(kt0 + kPrefDepth * kPrefK, set);
-            // S^T = K Q^T over 4 key subtiles: sc[nt][e] = S[query qj][key kt0 + 16 nt + 4 kq + e]
-            pf_floatx4 sc[4];
+            if (kt0 + kDepth * kPrefK < ke) issue(kt0 + kDepth * kPrefK, set);
+            // S^T = K Q^T over 4 key subtiles, each K operand read once for the wave's heads:
+            // sc[a][nt][e] = S[head a][query qj][key kt0 + 16 nt + 4 kq + e]
+            pf_floatx4 sc[NH][4];
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
-                sc[nt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int kk = 0; kk < D / 32; ++kk) {
+                for (int a = 0; a < NH; ++a) sc[a][nt] = pf_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
                     const uint4 kv = *reinterpret_cast<const uint4 *>(ks + (nt * 16 + r16) * KP + kk * 32 + kq * 8);
-                    sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(kv), pf_as_bf16x8(qa[kk]), sc[nt],
-                                                                      0, 0, 0);
+#pragma unroll
+                    for (int a = 0; a < NH; ++a)
+                        sc[a][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(kv), pf_as_bf16x8(qa[a][kk]),
+                                                                             sc[a][nt], 0, 0, 0);
                 }
             }
             // causal mask, only where the tile reaches past the wave's first query limit
@@ -2065,45 +2108,60 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                 for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (kt0 + nt * 16 + kq * 4 + e >= limit) sc[nt][e] = -INFINITY;
+                        if (kt0 + nt * 16 + kq * 4 + e >= limit) {
+#pragma unroll
+                            for (int a = 0; a < NH; ++a) sc[a][nt][e] = -INFINITY;
+                        }
             }
-            float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+            // every piece's first tile holds a key below each lane's limit (the piece's first key is
+            // below the tile's first limit), so the new maximum is finite and m_run = -inf gives
+            // alpha = 0
+            uint32_t pk[NH][8];  // bf16 probabilities: pk[a][2 nt + e / 2] holds keys 16 nt + 4 kq + e, e + 1
+            bool rescale = false;
+            float alpha[NH];
 #pragma unroll
-            for (int nt = 1; nt < 4; ++nt)
-                mx = fmaxf(mx, fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            // every tile holds a key below each lane's limit (the piece's first key is below the
-            // tile's first limit), so the new maximum is finite and m_run = -inf gives alpha = 0
-            const float mn = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - mn) * scale_log2);
-            const float nb = -mn * scale_log2;
-            uint32_t pk[8];  // bf16 probabilities: pk[2 nt + e / 2] holds keys 16 nt + 4 kq + e, e + 1
-            float rs = 0.f;
+            for (int a = 0; a < NH; ++a) {
+                float mx = fmaxf(fmaxf(sc[a][0][0], sc[a][0][1]), fmaxf(sc[a][0][2], sc[a][0][3]));
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                float p[4];
+                for (int nt = 1; nt < 4; ++nt)
+                    mx = fmaxf(mx, fmaxf(fmaxf(sc[a][nt][0], sc[a][nt][1]), fmaxf(sc[a][nt][2], sc[a][nt][3])));
+                mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+                const float mn = fmaxf(m_run[a], mx);
+                alpha[a] = __builtin_amdgcn_exp2f((m_run[a] - mn) * scale_log2);
+                rescale = rescale || alpha[a] != 1.f;
+                const float nb = -mn * scale_log2;
+                float rs = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    p[e] = __builtin_amdgcn_exp2f(fmaf(sc[nt][e], scale_log2, nb));
-                    rs += p[e];
+                for (int nt = 0; nt < 4; ++nt) {
+                    float p[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        p[e] = __builtin_amdgcn_exp2f(fmaf(sc[a][nt][e], scale_log2, nb));
+                        rs += p[e];
+                    }
+                    pk[a][2 * nt] = pf_pack_bf16(p[0], p[1]);
+                    pk[a][2 * nt + 1] = pf_pack_bf16(p[2], p[3]);
                 }
-                pk[2 * nt] = pf_pack_bf16(p[0], p[1]);
-                pk[2 * nt + 1] = pf_pack_bf16(p[2], p[3]);
+                l_run[a] = l_run[a] * alpha[a] + rs;
+                m_run[a] = mn;
             }
-            l_run = l_run * alpha + rs;
-            m_run = mn;
-            if (__any(alpha != 1.f)) {
+            if (__any(rescale)) {
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
+                for (int a = 0; a < NH; ++a)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[dt][e] *= alpha;
+                    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[a][dt][e] *= alpha[a];
             }
-            // O^T += V^T P^T: k slot s of lane group kq is key 32 kh + 16 (s / 4) + 4 kq + s % 4 in both
-            // operands
+            // O^T += V^T P^T, each V^T operand read once for the wave's heads: k slot s of lane group
+            // kq is key 32 kh + 16 (s / 4) + 4 kq + s % 4 in both operands
 #pragma unroll
             for (int kh = 0; kh < kPrefK / 32; ++kh) {
-                const uint4 pu = make_uint4(pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]);
+                uint4 pu[NH];
+#pragma unroll
+                for (int a = 0; a < NH; ++a)
+                    pu[a] = make_uint4(pk[a][4 * kh], pk[a][4 * kh + 1], pk[a][4 * kh + 2], pk[a][4 * kh + 3]);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     const uint16_t *vp = vrow + kh * 32 * KP + dt * 16;
@@ -2114,39 +2172,48 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
                     pf_bf16x8 va;
                     __builtin_memcpy(&va, &lo, 8);
                     __builtin_memcpy(reinterpret_cast<char *>(&va) + 8, &hi, 8);
-                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf_as_bf16x8(pu), acc[dt], 0, 0, 0);
+#pragma unroll
+                    for (int a = 0; a < NH; ++a)
+                        acc[a][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf_as_bf16x8(pu[a]), acc[a][dt], 0, 0, 0);
                 }
             }
         };
         using Set0 = std::integral_constant<int, 0>;
-        using Set1 = std::integral_constant<int, kPrefDepth - 1>;
+        using Set1 = std::integral_constant<int, kDepth - 1>;
         if (kb < ke) issue(kb, Set0{});
-        if constexpr (kPrefDepth == 2) {
+        if constexpr (kDepth == 2) {
             if (kb + kPrefK < ke) issue(kb + kPrefK, Set1{});
         }
-        for (int kt0 = kb; kt0 < ke; kt0 += kPrefDepth * kPrefK) {
+        for (int kt0 = kb; kt0 < ke; kt0 += kDepth * kPrefK) {
             step(kt0, Set0{});
-            if constexpr (kPrefDepth == 2) {
+            if constexpr (kDepth == 2) {
                 if (kt0 + kPrefK < ke) step(kt0 + kPrefK, Set1{});
             }
         }
-        float lt = l_run + __shfl_xor(l_run, 16, kWave);
-        lt += __shfl_xor(lt, 32, kWave);
+        float lt[NH];
+#pragma unroll
+        for (int a = 0; a < NH; ++a) {
+            lt[a] = l_run[a] + __shfl_xor(l_run[a], 16, kWave);
+            lt[a] += __shfl_xor(lt[a], 32, kWave);
+        }
         if (n_pieces == 1) {
             if (qj < nq) {
-                const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-                uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + head * o_s1 + 4 * kq;
 #pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const uint32_t w0 = pf_pack_bf16(acc[dt][0] * inv, acc[dt][1] * inv);
-                    const uint32_t w1 = pf_pack_bf16(acc[dt][2] * inv, acc[dt][3] * inv);
-                    if (out_vec) {
-                        *reinterpret_cast<uint2 *>(op + dt * 16) = make_uint2(w0, w1);
-                    } else {
-                        op[dt * 16] = static_cast<uint16_t>(w0);
-                        op[dt * 16 + 1] = static_cast<uint16_t>(w0 >> 16);
-                        op[dt * 16 + 2] = static_cast<uint16_t>(w1);
-                        op[dt * 16 + 3] = static_cast<uint16_t>(w1 >> 16);
+                for (int a = 0; a < NH; ++a) {
+                    const float inv = lt[a] > 0.f ? 1.0f / lt[a] : 0.f;
+                    uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + head_of(h, a) * o_s1 + 4 * kq;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        const uint32_t w0 = pf_pack_bf16(acc[a][dt][0] * inv, acc[a][dt][1] * inv);
+                        const uint32_t w1 = pf_pack_bf16(acc[a][dt][2] * inv, acc[a][dt][3] * inv);
+                        if (out_vec) {
+                            *reinterpret_cast<uint2 *>(op + dt * 16) = make_uint2(w0, w1);
+                        } else {
+                            op[dt * 16] = static_cast<uint16_t>(w0);
+                            op[dt * 16 + 1] = static_cast<uint16_t>(w0 >> 16);
+                            op[dt * 16 + 2] = static_cast<uint16_t>(w1);
+                            op[dt * 16 + 3] = static_cast<uint16_t>(w1 >> 16);
+                        }
                     }
                 }
             }
@@ -2157,16 +2224,25 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
         // waits for them, then counts its arrival on the (tile, kv head) counter; the piece that
         // completes the count merges the tile's pieces in piece order.
         if (qj < nq) {
-            const int64_t pr = (static_cast<int64_t>(q0 + qj) * kPrefMaxPieces + piece) * Hq + head;
-            float *po = part_o + pr * D + 4 * kq;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
+            for (int a = 0; a < NH; ++a) {
+                const int64_t pr = (static_cast<int64_t>(q0 + qj) * kPrefMaxPieces + piece) * Hq + head_of(h, a);
+                // columns 16 dt + 4 kq + e as pairs (e = 0, 1 and 2, 3): 8-byte words 8 dt and 8 dt + 1
+                uint64_t *po = reinterpret_cast<uint64_t *>(part_o + pr * D + 4 * kq);
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    __hip_atomic_store(po + dt * 16 + e, acc[dt][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (kq == 0) {
-                __hip_atomic_store(part_ml + pr * 2, m_run * scale_log2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(part_ml + pr * 2 + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        const uint64_t w = static_cast<uint64_t>(__float_as_uint(acc[a][dt][e])) |
+                                           (static_cast<uint64_t>(__float_as_uint(acc[a][dt][e + 1])) << 32);
+                        __hip_atomic_store(po + dt * 8 + e / 2, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                if (kq == 0) {
+                    __hip_atomic_store(part_ml + pr * 2, m_run[a] * scale_log2, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(part_ml + pr * 2 + 1, lt[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
         // every wave's partial stores happen before thread 0's arrival count (workgroup barrier),
@@ -2175,78 +2251,90 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
         // the merge below (the barrier after it carries that to every wave of the workgroup)
         __syncthreads();
         int32_t *counter = tile_arrivals + static_cast<int64_t>(pd.w) * num_kv_heads + h;
-        if (threadIdx.x == 0) s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) *s_arrived = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
-        if (s_arrived != n_pieces - 1) continue;
-        // merge: thread = (query, query head, quarter of D); the pieces' (m, l) first, then their
-        // partial rows two pieces at a time, weighted by 2^(m_p - max) / sum_p 2^(m_p - max) l_p
+        if (*s_arrived != n_pieces - 1) continue;
+        // merge: thread = (row, quarter of D), a row being (query, query head): wide tiles give a
+        // thread one query in both heads, narrow ones one (query, head) pair.  A row's (m, l) and
+        // its first two pieces' partial rows are loaded together (one memory round trip), then
+        // pieces are added two at a time, weighted by 2^(m_p - max) / sum_p 2^(m_p - max) l_p
         {
-            constexpr int kQuarter = D / 4;
-            const int pair = threadIdx.x >> 2, quarter = threadIdx.x & 3;
-            const int qj = pair >> 1, hh = 2 * h + (pair & 1);
-            if (qj < nq) {
-                const int64_t pr0 = static_cast<int64_t>(q0 + qj) * kPrefMaxPieces * Hq + hh;
-                float mk[kPrefMaxPieces], lk[kPrefMaxPieces];
+            constexpr int kQuarter = D / 4;   // columns per thread and row
+            constexpr int kWords = kQuarter / 2;
+            const int quarter = threadIdx.x & 3;
+            const int mq = kWide ? threadIdx.x >> 2 : threadIdx.x >> 3;
+            if (mq < nq) {
 #pragma unroll
-                for (int p = 0; p < kPrefMaxPieces; ++p) {
-                    mk[p] = -INFINITY;
-                    lk[p] = 0.f;
-                    if (p < n_pieces) {
-                        mk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2);
-                        lk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2 + 1);
+                for (int a = 0; a < NH; ++a) {
+                    const int hh = kWide ? 2 * h + a : 2 * h + ((threadIdx.x >> 2) & 1);
+                    // row of (query, piece p, head hh): pr0 + p Hq
+                    const int64_t pr0 = static_cast<int64_t>(q0 + mq) * kPrefMaxPieces * Hq + hh;
+                    float mk[kPrefMaxPieces], lk[kPrefMaxPieces];
+#pragma unroll
+                    for (int p = 0; p < kPrefMaxPieces; ++p) {
+                        mk[p] = -INFINITY;
+                        lk[p] = 0.f;
+                        if (p < n_pieces) {
+                            mk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2);
+                            lk[p] = coherent_load(part_ml + (pr0 + p * Hq) * 2 + 1);
+                        }
                     }
-                }
-                float mx = -INFINITY;
+                    // u[s][w]: columns 2w, 2w + 1 of the quarter, piece p + s (the last piece again,
+                    // with weight 0, past the end)
+                    uint64_t u[2][kWords];
+                    auto load_pair = [&](int p) {
 #pragma unroll
-                for (int p = 0; p < kPrefMaxPieces; ++p) mx = fmaxf(mx, mk[p]);
-                float ls = 0.f;
+                        for (int s = 0; s < 2; ++s) {
+                            const int pp = p + s < n_pieces ? p + s : p;
+                            uint64_t *src =
+                                reinterpret_cast<uint64_t *>(part_o + (pr0 + pp * Hq) * D + quarter * kQuarter);
 #pragma unroll
-                for (int p = 0; p < kPrefMaxPieces; ++p) {
-                    mk[p] = mk[p] == -INFINITY ? 0.f : exp2f(mk[p] - mx);  // the piece's weight
-                    ls += mk[p] * lk[p];
-                }
-                const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-                uint16_t *op = out + static_cast<int64_t>(q0 + qj) * o_s0 + hh * o_s1 + quarter * kQuarter;
-                const bool vec = (reinterpret_cast<uintptr_t>(op) & 15) == 0;
-                // eight columns at a time, two pieces' loads in flight together
+                            for (int w = 0; w < kWords; ++w)
+                                u[s][w] = __hip_atomic_load(src + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    };
+                    load_pair(0);
+                    float wt[kPrefMaxPieces];
+                    float mx = -INFINITY;
 #pragma unroll
-                for (int c = 0; c < kQuarter; c += 8) {
-                    float o[8];
+                    for (int p = 0; p < kPrefMaxPieces; ++p) mx = fmaxf(mx, mk[p]);
+                    float ls = 0.f;
 #pragma unroll
-                    for (int v = 0; v < 8; ++v) o[v] = 0.f;
+                    for (int p = 0; p < kPrefMaxPieces; ++p) {
+                        wt[p] = mk[p] == -INFINITY ? 0.f : exp2f(mk[p] - mx);  // the piece's weight
+                        ls += wt[p] * lk[p];
+                    }
+                    const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+#pragma unroll
+                    for (int p = 0; p < kPrefMaxPieces; ++p) wt[p] = p < n_pieces ? wt[p] * inv : 0.f;
+                    float o[kQuarter];
+#pragma unroll
+                    for (int c = 0; c < kQuarter; ++c) o[c] = 0.f;
 #pragma unroll
                     for (int p = 0; p < kPrefMaxPieces; p += 2) {
                         if (p >= n_pieces) break;
-                        // the second piece of the pair is read again from piece p (weight 0) past the end
-                        const int p1 = p + 1 < n_pieces ? p + 1 : p;
-                        const float w0 = mk[p] * inv, w1 = p + 1 < n_pieces ? mk[p + 1] * inv : 0.f;
-                        const uint64_t *a0 =
-                            reinterpret_cast<const uint64_t *>(part_o + (pr0 + p * Hq) * D + quarter * kQuarter + c);
-                        const uint64_t *a1 =
-                            reinterpret_cast<const uint64_t *>(part_o + (pr0 + p1 * Hq) * D + quarter * kQuarter + c);
-                        uint64_t u0[4], u1[4];
+                        if (p > 0) load_pair(p);
+                        const float w0 = wt[p], w1 = wt[p + 1];
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            u0[v] = __hip_atomic_load(const_cast<uint64_t *>(a0 + v), __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                            u1[v] = __hip_atomic_load(const_cast<uint64_t *>(a1 + v), __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                        }
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            o[2 * v] += w0 * __uint_as_float(static_cast<uint32_t>(u0[v])) +
-                                        w1 * __uint_as_float(static_cast<uint32_t>(u1[v]));
-                            o[2 * v + 1] += w0 * __uint_as_float(static_cast<uint32_t>(u0[v] >> 32)) +
-                                            w1 * __uint_as_float(static_cast<uint32_t>(u1[v] >> 32));
+                        for (int w = 0; w < kWords; ++w) {
+                            o[2 * w] += w0 * __uint_as_float(static_cast<uint32_t>(u[0][w])) +
+                                        w1 * __uint_as_float(static_cast<uint32_t>(u[1][w]));
+                            o[2 * w + 1] += w0 * __uint_as_float(static_cast<uint32_t>(u[0][w] >> 32)) +
+                                            w1 * __uint_as_float(static_cast<uint32_t>(u[1][w] >> 32));
                         }
                     }
-                    if (vec) {
-                        *reinterpret_cast<uint4 *>(op + c) =
-                            make_uint4(pf_pack_bf16(o[0], o[1]), pf_pack_bf16(o[2], o[3]), pf_pack_bf16(o[4], o[5]),
-                                       pf_pack_bf16(o[6], o[7]));
-                    } else {
+                    uint16_t *op = out + static_cast<int64_t>(q0 + mq) * o_s0 + hh * o_s1 + quarter * kQuarter;
+                    const bool vec = (reinterpret_cast<uintptr_t>(op) & 15) == 0;
 #pragma unroll
-                        for (int v = 0; v < 8; ++v) op[c + v] = f32_to_bf16(o[v]);
+                    for (int c = 0; c < kQuarter; c += 8) {
+                        if (vec) {
+                            *reinterpret_cast<uint4 *>(op + c) =
+                                make_uint4(pf_pack_bf16(o[c], o[c + 1]), pf_pack_bf16(o[c + 2], o[c + 3]),
+                                           pf_pack_bf16(o[c + 4], o[c + 5]), pf_pack_bf16(o[c + 6], o[c + 7]));
+                        } else {
+#pragma unroll
+                            for (int v = 0; v < 8; ++v) op[c + v] = f32_to_bf16(o[c + v]);
+                        }
                     }
                 }
             }
@@ -2254,6 +2342,32 @@ prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (bad && status) atomicExch(status, NQ_ERR_INVALID_ARGUMENT);
+}
+
+// Two waves per SIMD: the narrow shape keeps two register sets of K/V in flight, the wide shape
+// one set and both heads' scores and accumulators (at most 256 VGPRs either way).
+template <int D>
+__global__ void __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+prefill_tile_kernel(const uint16_t *__restrict__ q, int64_t q_s0, int64_t q_s1,
+                    const uint16_t *__restrict__ cache, int64_t c_page, int64_t c_kind, int64_t c_slot,
+                    int64_t c_head, int num_pages, const int32_t *__restrict__ kv_indices, int index_limit,
+                    int num_kv_heads, int ps_log2, float scale_log2, uint16_t *__restrict__ out,
+                    int64_t o_s0, int64_t o_s1, char *__restrict__ ws, PlanLayout L, int32_t *status) {
+    constexpr int KP = D + 16;
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefK * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t vs[kPrefK * KP];
+    __shared__ int pages[kPrefPages];
+    __shared__ int s_arrived;
+    const int32_t *meta = reinterpret_cast<const int32_t *>(ws + L.meta);
+    if (meta[kMetaStatus] != NQ_OK) return;
+    if (meta[kMetaPWide])
+        prefill_tiles<D, true>(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,
+                               index_limit, num_kv_heads, ps_log2, scale_log2, out, o_s0, o_s1, ws, L, status, ks, vs,
+                               pages, &s_arrived);
+    else
+        prefill_tiles<D, false>(q, q_s0, q_s1, cache, c_page, c_kind, c_slot, c_head, num_pages, kv_indices,
+                                index_limit, num_kv_heads, ps_log2, scale_log2, out, o_s0, o_s1, ws, L, status, ks,
+                                vs, pages, &s_arrived);
 }
 
 template <int D, int G>
