@@ -179,9 +179,13 @@ def test_mixed_batch_full_config3(nq, device):
     (16, [512, 0], [256, 255]),
     (4, [9, 0, 40], [31, 2, 70]),
     (32, [100, 31, 0], [1, 45, 96]),
-    # long causal ranges: tiles cut into the most key-range pieces, merged by the last to finish
+    # long causal ranges: tiles cut into key-range pieces, merged by the last to finish (a decode row
+    # in the batch makes the plan use the wide 64-query tiles)
     (16, [3000, 1500], [40, 200]),
     (128, [2100, 0, 700], [70, 300, 1]),
+    # four pieces (more than 48 key tiles), the merge's second pair: narrow tiles, then wide ones
+    (16, [3200, 8], [64, 33]),
+    (16, [3100, 40, 900], [100, 1, 64]),
 ])
 def test_prefill_rows_match_oracle(nq, device, ps, priors, advances):
     """Causal prefill rows (MFMA tile path for 16/8 heads of 128) at tile remainders, page sizes and
