@@ -161,8 +161,16 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(message)
 
 
+_functions: dict[str, object] = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(load(), name)(*args), name)
+    fn = _functions.get(name)
+    if fn is None:
+        fn = _functions[name] = getattr(load(), name)
+    status = fn(*args)
+    if status != NQ_OK:
+        check(status, name)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
@@ -170,7 +178,12 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream(device: torch.device | None = None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The hipStream_t of torch's current stream on ``device`` (the current device when it names none):
+    the handle ``torch.cuda.current_stream(device).cuda_stream`` gives, without building the Stream
+    object (this runs before every launch)."""
+
+    index = device.index if device is not None and device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def require_device(*tensors: torch.Tensor) -> None:

@@ -32,6 +32,8 @@ import numpy as np
 from .errors import KVAllocationError, SlotBusyError, StaleKVPublicationError
 
 _STALE = "Talker KV publication is stale or no longer pending"
+# reservations of at most this many rows count their pages in plain integers, larger ones in numpy
+_SMALL_RESERVATION = 32
 
 
 @dataclass(frozen=True, slots=True)
@@ -114,7 +116,10 @@ class PendingKVPublication:
         """The request's pages if published: its committed pages, then the new ones."""
 
         if self._pages is None:
-            self._pages = self._prior.page_indices + tuple(self.new_pages.tolist())
+            r, i = self._rows, self._i
+            lo, hi = r.lo[i], r.hi[i]
+            prior = r.priors[i].page_indices
+            self._pages = prior if lo == hi else prior + tuple(r.taken[lo:hi].tolist())
         return self._pages
 
     def proposal(self) -> KVPublicationProposal:
@@ -342,19 +347,29 @@ class PagedKVAllocator:
             raise SlotBusyError(f"request {busy!r} KV is already in flight")
         if not set(map(type, advances)) <= {int} or min(advances) < 1:
             raise ValueError("KV sequence advances must be positive integers")
-        adv = np.asarray(advances, dtype=np.int64)
         ps = self.page_size
-        need = (self.length[slots] + adv + ps - 1) // ps - self.page_count[slots]
-        np.maximum(need, 0, out=need)
-        end = np.cumsum(need)
         available = self.free_pages
-        if end[-1] > available:
-            k = int(np.argmax(end > available))
-            left = available - int(end[k] - need[k])
-            raise KVAllocationError(f"Talker KV needs {int(need[k])} pages for {request_ids[k]!r}, only {left} remain")
-        taken = self._take_front(int(end[-1]))
-        lo = (end - need).tolist()
-        hi = end.tolist()
+        if rows <= _SMALL_RESERVATION:
+            # per-row page counts in plain integers (for a few rows numpy's per-call cost dominates)
+            lo, hi, total = [], [], 0
+            for length, count, a in zip(self.length[slots].tolist(), self.page_count[slots].tolist(), advances):
+                lo.append(total)
+                n = (length + a + ps - 1) // ps - count
+                if n > 0:
+                    total += n
+                hi.append(total)
+            end_total = total
+        else:
+            adv = np.asarray(advances, dtype=np.int64)
+            need = (self.length[slots] + adv + ps - 1) // ps - self.page_count[slots]
+            np.maximum(need, 0, out=need)
+            end = np.cumsum(need)
+            lo, hi, end_total = (end - need).tolist(), end.tolist(), int(end[-1])
+        if end_total > available:
+            k = next(r for r in range(rows) if hi[r] > available)
+            raise KVAllocationError(f"Talker KV needs {hi[k] - lo[k]} pages for {request_ids[k]!r}, only "
+                                    f"{available - lo[k]} remain")
+        taken = self._take_front(end_total)
         serial = self._serial
         self._serial += rows
         states = self._states
@@ -362,7 +377,7 @@ class PagedKVAllocator:
                               tuple(advances))
         publications = tuple(map(PendingKVPublication, [batch] * rows, range(rows)))
         self._inflight.update(zip(request_ids, publications))
-        return KVReservation(publications, int(end[-1]), taken)
+        return KVReservation(publications, end_total, taken)
 
     def _live(self, publication: PendingKVPublication) -> None:
         """StaleKVPublicationError unless ``publication`` is its request's in-flight entry and the
@@ -398,20 +413,28 @@ class PagedKVAllocator:
                 self._give_back(run.taken[lo:hi])
 
     def _settle(self, publication: PendingKVPublication, *, commit: bool) -> None:
-        self._live(publication)
-        rid = publication.request_id
-        del self._inflight[rid]
+        # the row's fields read straight from its reservation (the properties' values): this runs
+        # once per row of every decode step
+        rows, i = publication._rows, publication._i
+        rid, prior = rows.request_ids[i], rows.priors[i]
+        inflight = self._inflight
+        if inflight.get(rid) is not publication or self._states.get(rid) is not prior:
+            raise StaleKVPublicationError(_STALE)
+        del inflight[rid]
+        lo, hi = rows.lo[i], rows.hi[i]
         if not commit:
-            self._give_back(publication.new_pages)
+            self._give_back(rows.taken[lo:hi])
             return
-        prior, advance = publication._prior, publication._advance
+        pages = publication._pages
+        if pages is None:
+            pages = prior.page_indices if lo == hi else prior.page_indices + tuple(rows.taken[lo:hi].tolist())
+        advance = rows.advances[i]
+        length, position = prior.sequence_length + advance, prior.position_start + advance
         slot = self._slot_of[rid]
-        pages = publication.page_indices
-        self.length[slot] = prior.sequence_length + advance
-        self.position[slot] = prior.position_start + advance
+        self.length[slot] = length
+        self.position[slot] = position
         self.page_count[slot] = len(pages)
-        self._states[rid] = RequestKVState(rid, pages, prior.sequence_length + advance, prior.position_start + advance,
-                                           prior.version + 1)
+        self._states[rid] = RequestKVState(rid, pages, length, position, prior.version + 1)
 
 
 __all__ = [

@@ -561,9 +561,9 @@ class PagedTalkerKV:
             self._rows_ptrs = tuple(self._rows_dev[k].data_ptr() for k in range(6))
         # the rows' committed numbers, read before the reservation (it does not change them)
         i, rows = self._rows_ring.acquire()
-        rows[0, :n] = a.length[slots]
-        rows[1, :n] = a.position[slots]
-        rows[3, :n] = a.page_count[slots]
+        np.take(a.length, slots, out=rows[0, :n])
+        np.take(a.position, slots, out=rows[1, :n])
+        np.take(a.page_count, slots, out=rows[3, :n])
         rows[4, :n] = slots
         reservation = a.reserve(request_ids, advances, slots)
         publications = reservation.publications
@@ -596,7 +596,8 @@ class PagedTalkerKV:
                 bp[0] or None, bp[1], bp[2], buffers.kv_indices.numel(), bp[3], bp[4], bp[5], bp[6], bp[7], 0,
                 current.cuda_stream,
             )
-            total_pages = int(a.page_count[slots].sum()) + reservation.pages_taken + (capture_rows - n)
+            # the rows' committed page counts (row 3, unchanged by the reservation) and the new pages
+            total_pages = int(rows[3, :n].sum()) + reservation.pages_taken + (capture_rows - n)
             metadata = TalkerAttentionMetadata(
                 qo_indptr=buffers.qo_indptr,
                 paged_kv_indptr=buffers.kv_indptr,

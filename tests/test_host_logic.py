@@ -200,3 +200,39 @@ def test_slot_leases_fail_closed(nq):
     leases.release(second)
     with pytest.raises(SlotBusyError):
         leases.release(second)
+
+
+@pytest.mark.parametrize("rows", [3, 40])
+def test_reservation_counts_pages_alike_for_few_and_many_rows(nq, monkeypatch, rows):
+    """Reservations of a few rows count their new pages in plain integers, larger ones in numpy:
+    both give the same pages per row, the same committed states and the same error message."""
+
+    import numpy as np
+
+    from nari_qwen3_tts_amd import cache
+    from nari_qwen3_tts_amd.errors import KVAllocationError
+
+    rng = np.random.default_rng(rows)
+    prior = rng.integers(0, 70, size=rows).tolist()
+    advances = tuple(int(x) for x in rng.integers(1, 40, size=rows))
+
+    def run(small: int):
+        monkeypatch.setattr(cache, "_SMALL_RESERVATION", small)
+        a = cache.PagedKVAllocator(total_pages=4096, page_size=16)
+        rids = tuple(f"r{i}" for i in range(rows))
+        for rid, n in zip(rids, prior):
+            a.add_request(rid)
+            if n:
+                a.reserve((rid,), (n,)).publications[0].publish()
+        res = a.reserve(rids, advances)
+        pages = [tuple(p.new_pages.tolist()) for p in res.publications]
+        for p in res.publications:
+            p.publish()
+        states = [a.state(rid) for rid in rids]
+        with pytest.raises(KVAllocationError) as err:
+            a.reserve(rids, tuple(16 * a.free_pages for _ in rids))  # every free page per row, or more
+        return res.pages_taken, pages, states, str(err.value)
+
+    plain, numeric = run(10**6), run(0)
+    assert plain == numeric
+    assert plain[0] == sum(len(p) for p in plain[1]) > 0
