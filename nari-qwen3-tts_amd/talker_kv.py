@@ -266,11 +266,13 @@ class _HipBindingBase:
             self._fork, self._join = torch.cuda.Event(), torch.cuda.Event()
         self._fork.record(main)
         self._side.wait_event(self._fork)
-        # the decode launch is issued first: its bins take the CUs before the prefill tiles (the mixed
-        # layer 124.7-127.2 us against 124.5-128.1 the other way round, medians 124.9 and 127.2)
+        # the prefill launch is issued first.  The other order helps a batch that has decode rows (its
+        # bins take the CUs first: mixed layer median 124.9 against 127.2 us) but costs a batch of
+        # prompt chunks alone, whose empty decode launch then goes ahead of the tiles, 6 % of a
+        # prefill decision (21.09 against 19.89 ms)
+        self._attention_call(query, layer_index, _lib.NQ_ATTN_PREFILL, self._side.cuda_stream)
         out = self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_BESIDE_PREFILL,
                                    main.cuda_stream)
-        self._attention_call(query, layer_index, _lib.NQ_ATTN_PREFILL, self._side.cuda_stream)
         self._join.record(self._side)
         main.wait_event(self._join)
         return out
