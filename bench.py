@@ -645,7 +645,7 @@ def mixed_attention(args, torch, np) -> dict:
     dec_prior = rng.integers(64, 2049, size=MIXED_DECODE)
     tokens = int(pre_adv.sum()) + MIXED_DECODE
 
-    def build(priors, advances, rows):
+    def build(priors, advances, rows, decode_rows):
         kv = PagedTalkerKV(num_layers=layers, num_kv_heads=cfg.num_kv_heads, num_qo_heads=cfg.num_qo_heads,
                            head_dim=cfg.head_dim, total_pages=POOL_PAGES, page_size=PAGE_SIZE,
                            scratch_page_count=max(rows, -(-int(sum(advances)) // PAGE_SIZE) + 8), workspace_bytes=0,
@@ -665,7 +665,8 @@ def mixed_attention(args, torch, np) -> dict:
             at += need
             rids.append(rid)
         key = PrefillKey(rows, int(sum(advances)))
-        ctx = kv.create_prefill(key, slot=0)
+        # the mixed batch's one-query rows through the decode launch beside the prefill launch
+        ctx = kv.create_prefill(key, slot=0, decode_rows=decode_rows)
         rows_t, adv_t = tuple(rids), tuple(int(a) for a in advances)
         for _ in range(5):  # first calls allocate the pinned staging rings
             kv.abort(kv.prepare_prefill(ctx, key, rows_t, adv_t))
@@ -700,14 +701,14 @@ def mixed_attention(args, torch, np) -> dict:
 
     priors = np.concatenate([pre_prior, dec_prior])
     advances = np.concatenate([pre_adv, np.ones(MIXED_DECODE, dtype=np.int64)])
-    mixed_us, plan_us, kv, ctx, q, pubs = build(priors, advances, MIXED_PREFILL + MIXED_DECODE)
+    mixed_us, plan_us, kv, ctx, q, pubs = build(priors, advances, MIXED_PREFILL + MIXED_DECODE, True)
     cpu = None if args.no_cpu_baseline else mixed_cpu_baseline(torch, np, kv, ctx, q)
     del kv, ctx, q, pubs
     torch.cuda.empty_cache()
-    pre_us, _, kv2, ctx2, q2, pubs2 = build(pre_prior, pre_adv, MIXED_PREFILL)
+    pre_us, _, kv2, ctx2, q2, pubs2 = build(pre_prior, pre_adv, MIXED_PREFILL, False)
     del kv2, ctx2, q2, pubs2
     torch.cuda.empty_cache()
-    dec_us, _, kv3, ctx3, q3, pubs3 = build(dec_prior, np.ones(MIXED_DECODE, dtype=np.int64), MIXED_DECODE)
+    dec_us, _, kv3, ctx3, q3, pubs3 = build(dec_prior, np.ones(MIXED_DECODE, dtype=np.int64), MIXED_DECODE, True)
     del kv3, ctx3, q3, pubs3
     torch.cuda.empty_cache()
     # algorithmic work

@@ -164,6 +164,24 @@ int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1, const uint
                        void *workspace, int64_t workspace_bytes, int32_t *status, void *stream);
 
 /*
+ * nq_attention_plan for attention launches that run only `parts` (the
+ * nq_attention_parts flags nq_paged_attention takes).  Without NQ_ATTN_DECODE
+ * the rows of one query are planned into the prefill part as well, so a
+ * single NQ_ATTN_PREFILL launch serves the whole batch and no decode launch
+ * is needed; with it the plan is nq_attention_plan's.  No counterpart in the
+ * reference, whose prefill and decode batches go to separate FlashInfer
+ * wrappers (P/executor/talker_kv.py:140-306): it lets a prefill binding skip
+ * the decode launch that only a batch mixing both kinds of row needs.
+ */
+int nq_attention_plan_parts(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                            const int32_t *last_page_len, const int32_t *kv_indices,
+                            const int64_t *position_ids, const int64_t *write_pages,
+                            const int64_t *write_offsets, int n_rows, int max_query_tokens,
+                            int max_pages, int page_size, int num_qo_heads, int num_kv_heads,
+                            int head_dim, int parts, void *workspace, int64_t workspace_bytes,
+                            void *stream);
+
+/*
  * nq_attention_plan followed by nq_paged_attention (positions and write slots
  * not planned, so not usable before nq_paged_decode_rope_attention), with the
  * plan and partials in the library's own static device scratch instead of a

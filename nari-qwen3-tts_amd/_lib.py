@@ -52,6 +52,7 @@ _SIGNATURES: dict[str, list] = {
     "nq_step_report": [_P, _P, _P, _P, _P, _I, _L, _L, _P, _P],
     "nq_attention_workspace_bytes": [_I, _I, _I, _I, _I, _I],
     "nq_attention_plan": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P],
+    "nq_attention_plan_parts": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P],
     "nq_paged_attention": [_P, _L, _L, _P, _L, _L, _L, _L, _I, _P, _I, _I, _I, _I, _F, _P, _L, _L,
                            _I, _I, _I, _P, _L, _P, _P],
     "nq_paged_attention_noalloc": [_P, _P, _P, _P, _I, _P, _L, _L, _P, _L, _L, _L, _L, _I, _I, _I, _I, _I, _F,

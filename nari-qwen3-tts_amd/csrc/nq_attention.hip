@@ -230,7 +230,7 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
                       const int32_t *__restrict__ kv_indices, const int64_t *__restrict__ position_ids,
                       const int64_t *__restrict__ write_pages, const int64_t *__restrict__ write_offsets,
                       int n_rows, int max_queries, int index_limit, int page_size, int num_kv_heads,
-                      char *__restrict__ ws, PlanLayout L) {
+                      char *__restrict__ ws, PlanLayout L, int decode_as_prefill) {
     __shared__ int s_qo[kPlanThreads + 1];
     __shared__ int s_kvlen[kPlanThreads];
     __shared__ int s_base[kPlanThreads];
@@ -296,15 +296,16 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
 
     // Decode rows and their key blocks, and prefill rows' tiles and pieces in
     // both tile shapes, in one scan; the shape follows whether the batch has
-    // decode rows.
+    // decode rows.  With decode_as_prefill (no decode launch will run) a
+    // one-query row is planned as a prefill row.
     int is_dec = 0, nblk = 0, nt_n = 0, np_n = 0, nt_w = 0, np_w = 0;
     if (tid < n_rows) {
         const int qo_len = s_qo[tid + 1] - s_qo[tid];
-        if (qo_len == 1) {
+        if (qo_len == 1 && !decode_as_prefill) {
             is_dec = 1;
             nblk = (s_kvlen[tid] + kBlockTok - 1) / kBlockTok;
             nblk = nblk < 1 ? 1 : nblk;
-        } else if (qo_len > 1) {
+        } else if (qo_len >= 1) {
             nt_n = (qo_len + kPrefQ - 1) / kPrefQ;
             for (int t = 0; t < nt_n; ++t) np_n += pref_pieces(pref_tile_keys(s_kvlen[tid], qo_len, t, kPrefQ));
             nt_w = (qo_len + kPrefQWide - 1) / kPrefQWide;
@@ -545,7 +546,8 @@ attention_plan_kernel(const int32_t *__restrict__ qo_indptr, const int32_t *__re
         int kvlen = s_kvlen[lo] - qo_len + (q - s_qo[lo]) + 1;
         kvlen = kvlen < 0 ? 0 : (kvlen > s_kvlen[lo] ? s_kvlen[lo] : kvlen);
         *row_out = lo;
-        return qo_len > 1 ? kvlen : -1;  // -1: a decode query, served by the stream kernel
+        // -1: a decode query, served by the stream kernel
+        return qo_len > 1 || (qo_len == 1 && decode_as_prefill) ? kvlen : -1;
     };
     const int n_cand = 5;  // 64 .. 1024 tokens
     unsigned long long cand[n_cand];
@@ -2500,13 +2502,16 @@ extern "C" int64_t nq_attention_workspace_bytes(int max_query_tokens, int max_pa
         .total;
 }
 
-extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
-                                 const int32_t *last_page_len, const int32_t *kv_indices,
-                                 const int64_t *position_ids, const int64_t *write_pages,
-                                 const int64_t *write_offsets,
-                                 int n_rows, int max_query_tokens, int max_pages, int page_size,
-                                 int num_qo_heads, int num_kv_heads, int head_dim, void *workspace,
-                                 int64_t workspace_bytes, void *stream) {
+extern "C" int nq_attention_plan_parts(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                                       const int32_t *last_page_len, const int32_t *kv_indices,
+                                       const int64_t *position_ids, const int64_t *write_pages,
+                                       const int64_t *write_offsets, int n_rows, int max_query_tokens,
+                                       int max_pages, int page_size, int num_qo_heads, int num_kv_heads,
+                                       int head_dim, int parts, void *workspace, int64_t workspace_bytes,
+                                       void *stream) {
+    NQ_CHECK_ARG((parts & (NQ_ATTN_DECODE | NQ_ATTN_PREFILL)) != 0 &&
+                 (parts & ~(NQ_ATTN_DECODE | NQ_ATTN_PREFILL | NQ_ATTN_BESIDE_PREFILL)) == 0);
+    NQ_CHECK_ARG(!(parts & NQ_ATTN_BESIDE_PREFILL) || (parts & NQ_ATTN_DECODE));
     NQ_CHECK_ARG(n_rows >= 1 && max_query_tokens >= 1 && max_pages >= 1);
     if (n_rows > nq::kPlanThreads) return NQ_ERR_UNSUPPORTED;
     NQ_CHECK_ARG(page_size >= 1 && (page_size & (page_size - 1)) == 0);
@@ -2519,8 +2524,22 @@ extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_ind
     hipLaunchKernelGGL(nq::attention_plan_kernel, dim3(nq::kPlanGrid), dim3(nq::kPlanThreads), 0,
                        static_cast<hipStream_t>(stream), qo_indptr, kv_indptr, last_page_len,
                        kv_indices, position_ids, write_pages, write_offsets, n_rows, max_query_tokens,
-                       max_pages, page_size, num_kv_heads, static_cast<char *>(workspace), L);
+                       max_pages, page_size, num_kv_heads, static_cast<char *>(workspace), L,
+                       (parts & NQ_ATTN_DECODE) ? 0 : 1);
     return NQ_LAUNCH_STATUS();
+}
+
+extern "C" int nq_attention_plan(const int32_t *qo_indptr, const int32_t *kv_indptr,
+                                 const int32_t *last_page_len, const int32_t *kv_indices,
+                                 const int64_t *position_ids, const int64_t *write_pages,
+                                 const int64_t *write_offsets,
+                                 int n_rows, int max_query_tokens, int max_pages, int page_size,
+                                 int num_qo_heads, int num_kv_heads, int head_dim, void *workspace,
+                                 int64_t workspace_bytes, void *stream) {
+    return nq_attention_plan_parts(qo_indptr, kv_indptr, last_page_len, kv_indices, position_ids, write_pages,
+                                   write_offsets, n_rows, max_query_tokens, max_pages, page_size, num_qo_heads,
+                                   num_kv_heads, head_dim, NQ_ATTN_DECODE | NQ_ATTN_PREFILL, workspace,
+                                   workspace_bytes, stream);
 }
 
 extern "C" int nq_paged_attention(const uint16_t *q, int64_t q_s0, int64_t q_s1,

@@ -127,6 +127,9 @@ class _HipBindingBase:
         self.fused_decode = True
         self._side: torch.cuda.Stream | None = None
         self.free_list_status: torch.Tensor | None = None
+        # whether a prefill binding's attention runs a decode launch for its one-query rows (beside
+        # the prefill launch, on two streams) or plans them into the prefill launch (one launch)
+        self.decode_rows = not self.prefill
 
     # -- planning ---------------------------------------------------------
     def _stage(self, metadata: TalkerAttentionMetadata) -> None:
@@ -156,7 +159,7 @@ class _HipBindingBase:
         self._stage(metadata)
         bp = self.buffers.ptrs
         _lib.call(
-            "nq_attention_plan",
+            "nq_attention_plan_parts",
             bp[0] or None,
             bp[1],
             bp[3],
@@ -171,6 +174,7 @@ class _HipBindingBase:
             self.num_qo_heads,
             self.num_kv_heads,
             self.head_dim,
+            self._parts(),
             _lib.ptr(self.workspace),
             self.workspace.numel(),
             _lib.stream(self.device),
@@ -251,15 +255,24 @@ class _HipBindingBase:
         )
         return self.run_attention(query_out, self._layer_index)
 
+    def _parts(self) -> int:
+        """The attention launches this binding runs (and its plan is made for)."""
+
+        if not self.prefill:
+            return _lib.NQ_ATTN_DECODE
+        return _lib.NQ_ATTN_DECODE | _lib.NQ_ATTN_PREFILL if self.decode_rows else _lib.NQ_ATTN_PREFILL
+
     def run_attention(self, query: torch.Tensor, layer_index: int, stream: int | None = None) -> torch.Tensor:
         """Paged attention of ``query`` over one layer with the planned metadata (no q/k transform).
 
-        Prefill bindings run the prefill rows on a side stream while the decode rows run on the
-        caller's stream (fork/join through events, so the pair is graph-capturable)."""
+        A prefill binding with ``decode_rows`` runs the prefill rows on a side stream while the
+        decode rows run on the caller's stream (fork/join through events, so the pair is
+        graph-capturable); without it the plan put its one-query rows into the prefill part too,
+        and one launch serves the batch."""
 
-        if not self.prefill or stream is not None:
-            return self._attention_call(query, layer_index, _lib.NQ_ATTN_DECODE | (
-                _lib.NQ_ATTN_PREFILL if self.prefill else 0), _lib.stream(self.device) if stream is None else stream)
+        if not self.prefill or not self.decode_rows or stream is not None:
+            return self._attention_call(query, layer_index, self._parts(),
+                                        _lib.stream(self.device) if stream is None else stream)
         main = torch.cuda.current_stream(self.device)
         if self._side is None:
             self._side = torch.cuda.Stream(self.device)
@@ -516,8 +529,17 @@ class PagedTalkerKV:
             self._workspaces[slot] = ws
         return ws
 
-    def create_prefill(self, key, *, slot: int):
-        return self._binding(key, slot)
+    def create_prefill(self, key, *, slot: int, decode_rows: bool = False):
+        """The prefill binding of ``key`` in capture slot ``slot``.  ``decode_rows``: batches of this
+        capture may hold many one-query (decode) rows beside the prompt chunks; their attention then
+        runs as a decode launch beside the prefill launch, on two streams.  Without it (the
+        reference's prefill batches, prompt chunks only) a one-query row is attended in the prefill
+        launch, and the empty decode launch and the fork/join it needs are saved."""
+
+        binding = self._binding(key, slot)
+        if isinstance(binding, _HipBindingBase):
+            binding.decode_rows = bool(decode_rows)
+        return binding
 
     def create_decode(self, key, *, slot: int):
         return self._binding(key, slot)

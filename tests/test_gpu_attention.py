@@ -133,7 +133,7 @@ def test_mixed_prefill_and_decode_rows(nq, device):
     rids = adopt_random(kv, rng, np.concatenate([pre_prior, dec_prior]))
     advances = tuple(int(a) for a in np.concatenate([pre_adv, np.ones(12, dtype=np.int64)]))
     key = PrefillKey(16, sum(advances) + 3)
-    ctx = kv.create_prefill(key, slot=0)
+    ctx = kv.create_prefill(key, slot=0, decode_rows=True)
     pubs = kv.prepare_prefill(ctx, key, tuple(rids), advances)
     q = torch.randn(key.token_capacity, 16, 128, generator=g, device=device).to(torch.bfloat16)
     out = _run(nq, ctx, q)
@@ -160,7 +160,7 @@ def test_mixed_batch_full_config3(nq, device):
     rids = adopt_random(kv, rng, np.concatenate([pre_prior, dec_prior]))
     advances = tuple(int(a) for a in np.concatenate([pre_adv, np.ones(112, dtype=np.int64)]))
     key = PrefillKey(128, sum(advances))
-    ctx = kv.create_prefill(key, slot=0)
+    ctx = kv.create_prefill(key, slot=0, decode_rows=True)
     pubs = kv.prepare_prefill(ctx, key, tuple(rids), advances)
     q = torch.randn(key.token_capacity, 16, 128, generator=g, device=device).to(torch.bfloat16)
     out = _run(nq, ctx, q)
@@ -180,16 +180,19 @@ def test_mixed_batch_full_config3(nq, device):
     (4, [9, 0, 40], [31, 2, 70]),
     (32, [100, 31, 0], [1, 45, 96]),
     # long causal ranges: tiles cut into key-range pieces, merged by the last to finish (a decode row
-    # in the batch makes the plan use the wide 64-query tiles)
+    # with decode_rows makes the plan use the wide 64-query tiles)
     (16, [3000, 1500], [40, 200]),
     (128, [2100, 0, 700], [70, 300, 1]),
     # four pieces (more than 48 key tiles), the merge's second pair: narrow tiles, then wide ones
     (16, [3200, 8], [64, 33]),
     (16, [3100, 40, 900], [100, 1, 64]),
 ])
-def test_prefill_rows_match_oracle(nq, device, ps, priors, advances):
+@pytest.mark.parametrize("decode_rows", [False, True])
+def test_prefill_rows_match_oracle(nq, device, ps, priors, advances, decode_rows):
     """Causal prefill rows (MFMA tile path for 16/8 heads of 128) at tile remainders, page sizes and
-    prior lengths that straddle pages, with a decode row mixed in where an advance is 1."""
+    prior lengths that straddle pages, with a decode row mixed in where an advance is 1: attended in
+    the prefill launch as a one-query row, or (decode_rows) by a decode launch beside it, which
+    makes the plan use the wide tiles."""
 
     rng = np.random.default_rng(sum(advances) + ps)
     scratch = max(32, -(-(sum(advances) + 5) // ps) + 4)  # padding tokens live in scratch slots
@@ -199,7 +202,7 @@ def test_prefill_rows_match_oracle(nq, device, ps, priors, advances):
     kv.storage.copy_(torch.randn(kv.storage.shape, generator=g, device=device).to(torch.bfloat16))
     rids = adopt_random(kv, rng, np.asarray(priors))
     key = PrefillKey(len(priors) + 2, sum(advances) + 5)
-    ctx = kv.create_prefill(key, slot=0)
+    ctx = kv.create_prefill(key, slot=0, decode_rows=decode_rows)
     pubs = kv.prepare_prefill(ctx, key, tuple(rids), tuple(advances))
     q = torch.randn(key.token_capacity, 16, 128, generator=g, device=device).to(torch.bfloat16)
     out = _run(nq, ctx, q)

@@ -27,7 +27,7 @@ def _mixed_case(nq, device, seed, pre_prior, pre_adv, dec_prior, pages):
     advances = tuple(int(a) for a in np.concatenate([pre_adv, np.ones(len(dec_prior), dtype=np.int64)]))
     if len(pre_prior):
         key = PrefillKey(rows, sum(advances) + 3)
-        ctx = kv.create_prefill(key, slot=0)
+        ctx = kv.create_prefill(key, slot=0, decode_rows=True)  # decode rows through the decode launch
         pubs = kv.prepare_prefill(ctx, key, tuple(rids), advances)
         tokens = key.token_capacity
     else:
